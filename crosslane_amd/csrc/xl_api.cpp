@@ -1,0 +1,615 @@
+// C ABI of the MI355X routed-expert lane: context, resident bank and the lane
+// entry points. Host side of the drop-in boundary declared in include/crosslane.h.
+//
+// Reference interfaces replaced (engine/strata/...):
+//   warm/runtime.hpp:10-16                 WarmRedirect (contains / compute / compute_many)
+//   sycl/stage/wiring/hip_resident_bank.hpp HipResidentBank (load :38-142, expert :143-166,
+//                                          enqueue_layer :170-236)
+//   warm/runtime.cpp:180-188               fixed-order combine
+//   sycl/stage/wiring/hip_q8k.hpp:6-10     q8k::{quantize, mv}
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <new>
+#include <set>
+#include <stdexcept>
+#include <string>
+#include <vector>
+
+#include "../../include/crosslane.h"
+#include "xl_format.hpp"
+#include "xl_internal.hpp"
+
+namespace {
+
+struct Failure : std::runtime_error {
+    int32_t code;
+    Failure(int32_t c, const std::string& m) : std::runtime_error(m), code(c) {}
+};
+
+[[noreturn]] void fail(int32_t code, const char* fmt, ...) {
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    std::vsnprintf(buf, sizeof buf, fmt, ap);
+    va_end(ap);
+    throw Failure(code, buf);
+}
+void need(bool ok, int32_t code, const char* what) {
+    if (!ok) fail(code, "%s", what);
+}
+void hip_check(hipError_t e, const char* what) {
+    if (e != hipSuccess) fail(XL_E_HIP, "%s: %s", what, hipGetErrorString(e));
+}
+
+#include "xl_codebooks.inc"
+
+uint64_t expand_codes(unsigned short code, bool iq1) {
+    static const uint8_t mag[3] = {8, 25, 43};
+    static const uint8_t tri[3] = {0xff, 0x00, 0x01};
+    uint64_t v = 0;
+    for (int j = 0; j < 8; ++j) {
+        const unsigned s = (code >> (2 * j)) & 3u;
+        if (s > 2) throw Failure(XL_E_STATE, "corrupt codebook symbol");
+        v |= uint64_t(iq1 ? tri[s] : mag[s]) << (8 * j);
+    }
+    return v;
+}
+uint8_t ksigns(int i) { return uint8_t(i | ((__builtin_popcount(unsigned(i)) & 1) << 7)); }
+
+// Device table rows: IQ2_XXS grid, IQ2_XS grid, IQ1 grid, 128 sign masks.
+std::vector<uint64_t> device_tables() {
+    std::vector<uint64_t> t;
+    t.reserve(2944);
+    for (int i = 0; i < 256; ++i) t.push_back(expand_codes(kIq2xxsCodes[i], false));
+    for (int i = 0; i < 512; ++i) t.push_back(expand_codes(kIq2xsCodes[i], false));
+    for (int i = 0; i < 2048; ++i) t.push_back(expand_codes(kIq1sCodes[i], true));
+    for (int i = 0; i < 128; ++i) {
+        const uint8_t s = ksigns(i);
+        uint64_t m = 0;
+        for (int j = 0; j < 8; ++j)
+            if (s & (1u << j)) m |= uint64_t(0xff) << (8 * j);
+        t.push_back(m);
+    }
+    return t;
+}
+
+int env_int(const char* name, int fallback) {
+    const char* s = std::getenv(name);
+    if (!s || !*s) return fallback;
+    char* end = nullptr;
+    const long v = std::strtol(s, &end, 10);
+    if (*end || v < 1 || v > 1 << 20) fail(XL_E_ARG, "%s must be a positive integer", name);
+    return int(v);
+}
+
+uint64_t matrix_blocks(int n, int k) { return uint64_t(n) * uint64_t(k / 256); }
+
+}  // namespace
+
+struct xl_context {
+    xl_config cfg{};
+    int cus = 0;
+    hipStream_t stream = nullptr;
+    bool poisoned = false;
+    xl_error last{};
+    // workspace (one allocation, carved)
+    void* ws = nullptr;
+    uint64_t ws_bytes = 0;
+    uint2* tables = nullptr;
+    int* err_flag = nullptr;
+    float *x = nullptr, *xd = nullptr, *h = nullptr, *hd = nullptr, *g = nullptr, *u = nullptr, *y = nullptr;
+    float *out = nullptr, *shared = nullptr, *w = nullptr, *mv_x = nullptr;
+    int8_t *xq = nullptr, *hq = nullptr;
+    int32_t* ids = nullptr;
+    uint8_t* q8std = nullptr;
+    int act_max = 0;  // longest vector the activation workspace holds
+    // bank
+    bool bank_ready = false, generated = false;
+    std::vector<int32_t> types;
+    std::vector<uint8_t*> slabs;
+    std::vector<xl::ExpertDesc> descs;
+    xl::ExpertDesc* d_descs = nullptr;
+    uint64_t payload = 0, allocated = 0;
+    int grid_gu = 0, grid_down = 0;
+};
+
+namespace {
+
+void set_error(xl_context* ctx, xl_error* err, int32_t code, const char* msg) {
+    xl_error e{};
+    e.code = code;
+    std::snprintf(e.message, sizeof e.message, "%s", msg);
+    if (ctx) ctx->last = e;
+    if (err) *err = e;
+}
+
+template <class F>
+int32_t guarded(xl_context* ctx, xl_error* err, F&& f) {
+    try {
+        if (err) { err->code = XL_OK; err->message[0] = 0; }
+        f();
+        return XL_OK;
+    } catch (const Failure& e) {
+        if (ctx && (e.code == XL_E_HIP || e.code == XL_E_DEVICE)) {
+            // Poison: drain whatever is queued, refuse further compute.
+            ctx->poisoned = true;
+            if (ctx->stream) (void)hipStreamSynchronize(ctx->stream);
+        }
+        set_error(ctx, err, e.code, e.what());
+        return e.code;
+    } catch (const std::bad_alloc&) {
+        set_error(ctx, err, XL_E_MEMORY, "host allocation failed");
+        return XL_E_MEMORY;
+    } catch (const std::exception& e) {
+        set_error(ctx, err, XL_E_STATE, e.what());
+        return XL_E_STATE;
+    } catch (...) {
+        set_error(ctx, err, XL_E_STATE, "unknown exception");
+        return XL_E_STATE;
+    }
+}
+
+void ready(const xl_context* ctx, bool need_bank) {
+    need(ctx != nullptr, XL_E_ARG, "null context");
+    need(!ctx->poisoned, XL_E_STATE, "context poisoned by an earlier device error; close it");
+    if (need_bank) need(ctx->bank_ready, XL_E_STATE, "bank not created");
+    hip_check(hipSetDevice(ctx->cfg.device), "hipSetDevice");
+}
+
+hipStream_t pick_stream(const xl_context* ctx, void* s) { return s ? static_cast<hipStream_t>(s) : ctx->stream; }
+
+// Reads and checks the device error flag after draining the stream.
+void drain(xl_context* ctx, hipStream_t s) {
+    hip_check(hipStreamSynchronize(s), "stream synchronize");
+    int flag = 0;
+    hip_check(hipMemcpy(&flag, ctx->err_flag, sizeof flag, hipMemcpyDeviceToHost), "error flag read");
+    if (flag) {
+        fail(XL_E_DEVICE, "device error flag 0x%x (%s%s%s)", flag, (flag & xl::kDevErrExpertId) ? "expert id out of range " : "",
+             (flag & xl::kDevErrNonFinite) ? "non-finite activation " : "", (flag & xl::kDevErrType) ? "bad block type" : "");
+    }
+}
+
+void check_ids(const xl_context* ctx, const int32_t* ids, int32_t k) {
+    need(ids != nullptr, XL_E_ARG, "null ids");
+    need(k >= 1 && k <= ctx->cfg.max_picks, XL_E_ARG, "pick count outside 1..max_picks");
+    std::set<int32_t> seen;
+    for (int i = 0; i < k; ++i) {
+        need(ids[i] >= 0 && ids[i] < ctx->cfg.n_experts, XL_E_ARG, "expert id out of range");
+        need(seen.insert(ids[i]).second, XL_E_ARG, "duplicate expert id");
+    }
+}
+void check_finite(const float* v, size_t n, const char* what) {
+    need(v != nullptr, XL_E_ARG, what);
+    for (size_t i = 0; i < n; ++i)
+        if (!std::isfinite(v[i])) fail(XL_E_ARG, "%s: non-finite value at %zu", what, i);
+}
+void check_layer(const xl_context* ctx, int32_t layer) {
+    need(layer >= 0 && layer < ctx->cfg.n_layers, XL_E_ARG, "layer out of range");
+}
+
+// Enqueues the routed-expert layer on stream s: Q8_K(x), gate/up + SwiGLU,
+// Q8_K(h), down, fixed-order combine. All pointers are device pointers.
+void enqueue_layer(xl_context* ctx, int32_t layer, const int32_t* d_ids, const float* d_w, int32_t k, const float* d_x,
+                   const float* d_shared, float* d_out, hipStream_t s, float* g_dbg = nullptr,
+                   float* u_dbg = nullptr) {
+    const int dim = ctx->cfg.dim, ff = ctx->cfg.ff, E = ctx->cfg.n_experts;
+    const xl::ExpertDesc* descs = ctx->d_descs + size_t(layer) * E;
+    hip_check(xl::dev::launch_q8k(d_x, dim / 256, ctx->xq, ctx->xd, nullptr, ctx->err_flag, s), "Q8_K(x) launch");
+    hip_check(xl::dev::launch_gate_up(descs, d_ids, k, E, dim, ff, ctx->xq, ctx->xd, ctx->tables, ctx->h, g_dbg, u_dbg,
+                                      ctx->err_flag, ctx->grid_gu, s),
+              "gate/up launch");
+    hip_check(xl::dev::launch_q8k(ctx->h, k * ff / 256, ctx->hq, ctx->hd, nullptr, ctx->err_flag, s), "Q8_K(h) launch");
+    hip_check(xl::dev::launch_down(descs, d_ids, k, E, dim, ff, ctx->hq, ctx->hd, ctx->tables, ctx->y, ctx->err_flag,
+                                   ctx->grid_down, s),
+              "down launch");
+    if (d_out)
+        hip_check(xl::dev::launch_combine(d_ids, d_w, k, ctx->y, dim, d_shared, d_out, s), "combine launch");
+}
+
+}  // namespace
+
+extern "C" {
+
+uint32_t xl_abi_version(void) { return XL_ABI_VERSION; }
+
+int32_t xl_open(uint32_t abi_version, const xl_config* cfg, xl_context** out, xl_error* err) {
+    xl_context* ctx = nullptr;
+    const int32_t rc = guarded(nullptr, err, [&] {
+        need(out != nullptr, XL_E_ARG, "null output pointer");
+        *out = nullptr;
+        need(abi_version == XL_ABI_VERSION, XL_E_VERSION, "ABI version mismatch");
+        need(cfg != nullptr, XL_E_ARG, "null config");
+        need(cfg->struct_bytes == sizeof(xl_config), XL_E_VERSION, "xl_config size mismatch");
+        int lpr, ppl;
+        need(xl::row_shape(cfg->dim, lpr, ppl), XL_E_ARG, "dim not supported (256..4096, see row_shape)");
+        need(xl::row_shape(cfg->ff, lpr, ppl), XL_E_ARG, "ff not supported (256..4096, see row_shape)");
+        need(cfg->n_layers >= 1 && cfg->n_layers <= 4096, XL_E_ARG, "n_layers outside 1..4096");
+        need(cfg->n_experts >= 1 && cfg->n_experts <= 65536, XL_E_ARG, "n_experts outside 1..65536");
+        need(cfg->max_picks >= 1 && cfg->max_picks <= 16, XL_E_ARG, "max_picks outside 1..16");
+        need(cfg->max_tokens >= 0 && cfg->max_tokens <= 65536, XL_E_ARG, "max_tokens outside 0..65536");
+        int ndev = 0;
+        hip_check(hipGetDeviceCount(&ndev), "hipGetDeviceCount");
+        need(cfg->device >= 0 && cfg->device < ndev, XL_E_ARG, "device ordinal out of range");
+        ctx = new xl_context();
+        ctx->cfg = *cfg;
+        hip_check(hipSetDevice(cfg->device), "hipSetDevice");
+        hipDeviceProp_t prop{};
+        hip_check(hipGetDeviceProperties(&prop, cfg->device), "hipGetDeviceProperties");
+        ctx->cus = prop.multiProcessorCount;
+        hip_check(hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking), "hipStreamCreate");
+        ctx->grid_gu = env_int("XL_GRID_GATE_UP", 2 * ctx->cus);
+        ctx->grid_down = env_int("XL_GRID_DOWN", 2 * ctx->cus);
+
+        const int P = cfg->max_picks, dim = cfg->dim, ff = cfg->ff;
+        ctx->act_max = std::max({dim, ff, 4096});
+        struct Part { void** p; uint64_t bytes; };
+        const uint64_t tab_bytes = 2944 * 8;
+        std::vector<Part> parts = {
+            {reinterpret_cast<void**>(&ctx->tables), tab_bytes},
+            {reinterpret_cast<void**>(&ctx->err_flag), 256},
+            {reinterpret_cast<void**>(&ctx->x), uint64_t(dim) * 4},
+            {reinterpret_cast<void**>(&ctx->xq), uint64_t(ctx->act_max)},
+            {reinterpret_cast<void**>(&ctx->xd), uint64_t(ctx->act_max / 256) * 4},
+            {reinterpret_cast<void**>(&ctx->mv_x), uint64_t(ctx->act_max) * 4},
+            {reinterpret_cast<void**>(&ctx->h), uint64_t(P) * ff * 4},
+            {reinterpret_cast<void**>(&ctx->hq), uint64_t(P) * ff},
+            {reinterpret_cast<void**>(&ctx->hd), uint64_t(P) * (ff / 256) * 4},
+            {reinterpret_cast<void**>(&ctx->g), uint64_t(P) * ff * 4},
+            {reinterpret_cast<void**>(&ctx->u), uint64_t(P) * ff * 4},
+            {reinterpret_cast<void**>(&ctx->y), uint64_t(P) * dim * 4},
+            {reinterpret_cast<void**>(&ctx->out), uint64_t(dim) * 4},
+            {reinterpret_cast<void**>(&ctx->shared), uint64_t(dim) * 4},
+            {reinterpret_cast<void**>(&ctx->w), 64 * 4},
+            {reinterpret_cast<void**>(&ctx->ids), 64 * 4},
+            {reinterpret_cast<void**>(&ctx->q8std), uint64_t(P) * (std::max(dim, ff) / 256) * 292},
+        };
+        uint64_t total = 0;
+        for (auto& p : parts) total += xl::align256(p.bytes);
+        hip_check(hipMalloc(&ctx->ws, total), "workspace hipMalloc");
+        ctx->ws_bytes = total;
+        uint64_t at = 0;
+        for (auto& p : parts) {
+            *p.p = static_cast<uint8_t*>(ctx->ws) + at;
+            at += xl::align256(p.bytes);
+        }
+        const auto t = device_tables();
+        hip_check(hipMemcpy(ctx->tables, t.data(), tab_bytes, hipMemcpyHostToDevice), "table upload");
+        hip_check(hipMemset(ctx->err_flag, 0, 256), "error flag clear");
+        *out = ctx;
+    });
+    if (rc != XL_OK && ctx) xl_close(ctx);
+    return rc;
+}
+
+void xl_close(xl_context* ctx) {
+    if (!ctx) return;
+    (void)hipSetDevice(ctx->cfg.device);
+    if (ctx->stream) (void)hipStreamSynchronize(ctx->stream);
+    for (auto* s : ctx->slabs) (void)hipFree(s);
+    if (ctx->d_descs) (void)hipFree(ctx->d_descs);
+    if (ctx->ws) (void)hipFree(ctx->ws);
+    if (ctx->stream) (void)hipStreamDestroy(ctx->stream);
+    delete ctx;
+}
+
+int32_t xl_last_error(const xl_context* ctx, xl_error* err) {
+    if (!ctx || !err) return XL_E_ARG;
+    *err = ctx->last;
+    return XL_OK;
+}
+
+int32_t xl_bank_create(xl_context* ctx, const int32_t* types, xl_error* err) {
+    return guarded(ctx, err, [&] {
+        ready(ctx, false);
+        need(!ctx->bank_ready, XL_E_STATE, "bank already created");
+        need(types != nullptr, XL_E_ARG, "null type map");
+        const int L = ctx->cfg.n_layers, E = ctx->cfg.n_experts, dim = ctx->cfg.dim, ff = ctx->cfg.ff;
+        const size_t n = size_t(L) * E * 3;
+        for (size_t i = 0; i < n; ++i) need(xl::supported_type(types[i]), XL_E_ARG, "unsupported block type");
+        for (size_t e = 0; e < size_t(L) * E; ++e)
+            need(types[3 * e] == types[3 * e + 1], XL_E_ARG, "gate and up must share a block type");
+        ctx->types.assign(types, types + n);
+        ctx->descs.assign(size_t(L) * E, xl::ExpertDesc{});
+        // One slab per layer, experts contiguous, each matrix's planes 256-B aligned.
+        for (int l = 0; l < L; ++l) {
+            uint64_t bytes = 0;
+            for (int e = 0; e < E; ++e)
+                for (int r = 0; r < 3; ++r) {
+                    const int t = types[(size_t(l) * E + e) * 3 + r];
+                    const int nr = r < 2 ? ff : dim, kk = r < 2 ? dim : ff;
+                    bytes += xl::plane_layout(t, matrix_blocks(nr, kk)).bytes;
+                    ctx->payload += matrix_blocks(nr, kk) * uint64_t(xl::block_bytes(t));
+                }
+            uint8_t* slab = nullptr;
+            const hipError_t e = hipMalloc(&slab, bytes);
+            if (e != hipSuccess) fail(XL_E_MEMORY, "bank slab %d (%llu bytes): %s", l, (unsigned long long)bytes, hipGetErrorString(e));
+            ctx->slabs.push_back(slab);
+            ctx->allocated += bytes;
+            uint64_t at = 0;
+            for (int e2 = 0; e2 < E; ++e2)
+                for (int r = 0; r < 3; ++r) {
+                    const int t = types[(size_t(l) * E + e2) * 3 + r];
+                    const int nr = r < 2 ? ff : dim, kk = r < 2 ? dim : ff;
+                    const auto P = xl::plane_layout(t, matrix_blocks(nr, kk));
+                    xl::MatRef& m = ctx->descs[size_t(l) * E + e2].m[r];
+                    m.base = slab + at;
+                    m.off1 = P.off[1];
+                    m.off2 = P.off[2];
+                    m.type = t;
+                    m.nb = kk / 256;
+                    at += P.bytes;
+                }
+        }
+        hip_check(hipMalloc(&ctx->d_descs, ctx->descs.size() * sizeof(xl::ExpertDesc)), "descriptor hipMalloc");
+        hip_check(hipMemcpy(ctx->d_descs, ctx->descs.data(), ctx->descs.size() * sizeof(xl::ExpertDesc),
+                            hipMemcpyHostToDevice),
+                  "descriptor upload");
+        ctx->bank_ready = true;
+    });
+}
+
+int32_t xl_bank_generate(xl_context* ctx, uint64_t seed, xl_error* err) {
+    return guarded(ctx, err, [&] {
+        ready(ctx, true);
+        const int L = ctx->cfg.n_layers, E = ctx->cfg.n_experts, dim = ctx->cfg.dim, ff = ctx->cfg.ff;
+        for (int l = 0; l < L; ++l)
+            for (int e = 0; e < E; ++e)
+                for (int r = 0; r < 3; ++r) {
+                    const xl::MatRef& m = ctx->descs[size_t(l) * E + e].m[r];
+                    const int nr = r < 2 ? ff : dim, kk = r < 2 ? dim : ff;
+                    hip_check(xl::dev::launch_generate(const_cast<uint8_t*>(m.base), m.type, nr, kk, seed, uint32_t(l),
+                                                       uint32_t(e), uint32_t(r), ctx->stream),
+                              "generate launch");
+                }
+        drain(ctx, ctx->stream);
+        ctx->generated = true;
+    });
+}
+
+int32_t xl_bank_upload(xl_context* ctx, int32_t layer, int32_t expert, int32_t role, const void* aos, uint64_t bytes,
+                       xl_error* err) {
+    return guarded(ctx, err, [&] {
+        ready(ctx, true);
+        check_layer(ctx, layer);
+        need(expert >= 0 && expert < ctx->cfg.n_experts && role >= 0 && role < 3, XL_E_ARG, "expert/role out of range");
+        need(aos != nullptr, XL_E_ARG, "null weights");
+        const xl::MatRef& m = ctx->descs[size_t(layer) * ctx->cfg.n_experts + expert].m[role];
+        const int nr = role < 2 ? ctx->cfg.ff : ctx->cfg.dim, kk = role < 2 ? ctx->cfg.dim : ctx->cfg.ff;
+        const uint64_t nblk = matrix_blocks(nr, kk);
+        need(bytes == nblk * uint64_t(xl::block_bytes(m.type)), XL_E_ARG, "weight byte extent differs from shape");
+        const auto P = xl::plane_layout(m.type, nblk);
+        std::vector<uint8_t> planar(P.bytes, 0);
+        const auto* src = static_cast<const uint8_t*>(aos);
+        for (uint64_t b = 0; b < nblk; ++b)
+            xl::block_to_planes(m.type, src + b * xl::block_bytes(m.type), planar.data(), P, b);
+        hip_check(hipMemcpyAsync(const_cast<uint8_t*>(m.base), planar.data(), P.bytes, hipMemcpyHostToDevice, ctx->stream),
+                  "weight upload");
+        hip_check(hipStreamSynchronize(ctx->stream), "weight upload drain");
+    });
+}
+
+int32_t xl_bank_download(xl_context* ctx, int32_t layer, int32_t expert, int32_t role, void* aos, uint64_t bytes,
+                         xl_error* err) {
+    return guarded(ctx, err, [&] {
+        ready(ctx, true);
+        check_layer(ctx, layer);
+        need(expert >= 0 && expert < ctx->cfg.n_experts && role >= 0 && role < 3, XL_E_ARG, "expert/role out of range");
+        need(aos != nullptr, XL_E_ARG, "null output");
+        const xl::MatRef& m = ctx->descs[size_t(layer) * ctx->cfg.n_experts + expert].m[role];
+        const int nr = role < 2 ? ctx->cfg.ff : ctx->cfg.dim, kk = role < 2 ? ctx->cfg.dim : ctx->cfg.ff;
+        const uint64_t nblk = matrix_blocks(nr, kk);
+        need(bytes == nblk * uint64_t(xl::block_bytes(m.type)), XL_E_ARG, "output byte extent differs from shape");
+        const auto P = xl::plane_layout(m.type, nblk);
+        std::vector<uint8_t> planar(P.bytes);
+        hip_check(hipMemcpyAsync(planar.data(), m.base, P.bytes, hipMemcpyDeviceToHost, ctx->stream), "weight download");
+        hip_check(hipStreamSynchronize(ctx->stream), "weight download drain");
+        auto* dst = static_cast<uint8_t*>(aos);
+        for (uint64_t b = 0; b < nblk; ++b) xl::planes_to_block(m.type, planar.data(), P, b, dst + b * xl::block_bytes(m.type));
+    });
+}
+
+int32_t xl_bank_info_get(const xl_context* ctx, xl_bank_info* out) {
+    if (!ctx || !out) return XL_E_ARG;
+    std::memset(out, 0, sizeof *out);
+    out->payload_bytes = ctx->payload;
+    out->allocated_bytes = ctx->allocated;
+    out->workspace_bytes = ctx->ws_bytes;
+    out->n_layers = ctx->cfg.n_layers;
+    out->n_experts = ctx->cfg.n_experts;
+    out->generated = ctx->generated ? 1 : 0;
+    return XL_OK;
+}
+
+int32_t xl_contains(const xl_context* ctx, int32_t layer, int32_t expert) {
+    return ctx && ctx->bank_ready && layer >= 0 && layer < ctx->cfg.n_layers && expert >= 0 &&
+           expert < ctx->cfg.n_experts;
+}
+
+int32_t xl_experts_forward(xl_context* ctx, int32_t layer, const int32_t* ids, int32_t k, const float* x, float* ys,
+                           xl_error* err) {
+    return guarded(ctx, err, [&] {
+        ready(ctx, true);
+        check_layer(ctx, layer);
+        check_ids(ctx, ids, k);
+        check_finite(x, size_t(ctx->cfg.dim), "input vector");
+        need(ys != nullptr, XL_E_ARG, "null output");
+        hipStream_t s = ctx->stream;
+        hip_check(hipMemcpyAsync(ctx->ids, ids, sizeof(int32_t) * k, hipMemcpyHostToDevice, s), "ids upload");
+        hip_check(hipMemcpyAsync(ctx->x, x, sizeof(float) * ctx->cfg.dim, hipMemcpyHostToDevice, s), "x upload");
+        enqueue_layer(ctx, layer, ctx->ids, nullptr, k, ctx->x, nullptr, nullptr, s);
+        hip_check(hipMemcpyAsync(ys, ctx->y, sizeof(float) * size_t(k) * ctx->cfg.dim, hipMemcpyDeviceToHost, s),
+                  "output download");
+        drain(ctx, s);
+        for (size_t i = 0; i < size_t(k) * ctx->cfg.dim; ++i)
+            if (!std::isfinite(ys[i])) fail(XL_E_DEVICE, "non-finite expert output");
+    });
+}
+
+int32_t xl_expert_forward(xl_context* ctx, int32_t layer, int32_t expert, const float* x, float* y, xl_error* err) {
+    const int32_t id = expert;
+    return xl_experts_forward(ctx, layer, &id, 1, x, y, err);
+}
+
+int32_t xl_layer_forward(xl_context* ctx, int32_t layer, const int32_t* ids, const float* w, int32_t k, const float* x,
+                         const float* shared_or_null, float* out, xl_error* err) {
+    return guarded(ctx, err, [&] {
+        ready(ctx, true);
+        check_layer(ctx, layer);
+        check_ids(ctx, ids, k);
+        check_finite(w, size_t(k), "route weights");
+        check_finite(x, size_t(ctx->cfg.dim), "input vector");
+        if (shared_or_null) check_finite(shared_or_null, size_t(ctx->cfg.dim), "shared vector");
+        need(out != nullptr, XL_E_ARG, "null output");
+        hipStream_t s = ctx->stream;
+        const int dim = ctx->cfg.dim;
+        hip_check(hipMemcpyAsync(ctx->ids, ids, sizeof(int32_t) * k, hipMemcpyHostToDevice, s), "ids upload");
+        hip_check(hipMemcpyAsync(ctx->w, w, sizeof(float) * k, hipMemcpyHostToDevice, s), "weights upload");
+        hip_check(hipMemcpyAsync(ctx->x, x, sizeof(float) * dim, hipMemcpyHostToDevice, s), "x upload");
+        if (shared_or_null)
+            hip_check(hipMemcpyAsync(ctx->shared, shared_or_null, sizeof(float) * dim, hipMemcpyHostToDevice, s),
+                      "shared upload");
+        enqueue_layer(ctx, layer, ctx->ids, ctx->w, k, ctx->x, shared_or_null ? ctx->shared : nullptr, ctx->out, s);
+        hip_check(hipMemcpyAsync(out, ctx->out, sizeof(float) * dim, hipMemcpyDeviceToHost, s), "output download");
+        drain(ctx, s);
+    });
+}
+
+int32_t xl_expert_trace(xl_context* ctx, int32_t layer, int32_t expert, const float* x, float* g, float* u, float* h,
+                        void* q8h, float* y, xl_error* err) {
+    return guarded(ctx, err, [&] {
+        ready(ctx, true);
+        check_layer(ctx, layer);
+        const int32_t id = expert;
+        check_ids(ctx, &id, 1);
+        check_finite(x, size_t(ctx->cfg.dim), "input vector");
+        hipStream_t s = ctx->stream;
+        const int dim = ctx->cfg.dim, ff = ctx->cfg.ff;
+        hip_check(hipMemcpyAsync(ctx->ids, &id, sizeof id, hipMemcpyHostToDevice, s), "ids upload");
+        hip_check(hipMemcpyAsync(ctx->x, x, sizeof(float) * dim, hipMemcpyHostToDevice, s), "x upload");
+        enqueue_layer(ctx, layer, ctx->ids, nullptr, 1, ctx->x, nullptr, nullptr, s, ctx->g, ctx->u);
+        // Standard 292-byte Q8_K blocks of h, same kernel as the hot path.
+        hip_check(xl::dev::launch_q8k(ctx->h, ff / 256, ctx->hq, ctx->hd, ctx->q8std, ctx->err_flag, s), "Q8_K(h) launch");
+        if (g) hip_check(hipMemcpyAsync(g, ctx->g, sizeof(float) * ff, hipMemcpyDeviceToHost, s), "g download");
+        if (u) hip_check(hipMemcpyAsync(u, ctx->u, sizeof(float) * ff, hipMemcpyDeviceToHost, s), "u download");
+        if (h) hip_check(hipMemcpyAsync(h, ctx->h, sizeof(float) * ff, hipMemcpyDeviceToHost, s), "h download");
+        if (q8h) hip_check(hipMemcpyAsync(q8h, ctx->q8std, size_t(ff / 256) * 292, hipMemcpyDeviceToHost, s), "q8h download");
+        if (y) hip_check(hipMemcpyAsync(y, ctx->y, sizeof(float) * dim, hipMemcpyDeviceToHost, s), "y download");
+        drain(ctx, s);
+    });
+}
+
+int32_t xl_layer_forward_async(xl_context* ctx, int32_t layer, const int32_t* d_ids, const float* d_w, int32_t k,
+                               const float* d_x, const float* d_shared_or_null, float* d_out, void* stream,
+                               xl_error* err) {
+    return guarded(ctx, err, [&] {
+        ready(ctx, true);
+        check_layer(ctx, layer);
+        need(k >= 1 && k <= ctx->cfg.max_picks, XL_E_ARG, "pick count outside 1..max_picks");
+        need(d_ids && d_w && d_x && d_out, XL_E_ARG, "null device pointer");
+        enqueue_layer(ctx, layer, d_ids, d_w, k, d_x, d_shared_or_null, d_out, pick_stream(ctx, stream));
+    });
+}
+
+int32_t xl_sync(xl_context* ctx, void* stream, xl_error* err) {
+    return guarded(ctx, err, [&] {
+        need(ctx != nullptr, XL_E_ARG, "null context");
+        hip_check(hipSetDevice(ctx->cfg.device), "hipSetDevice");
+        drain(ctx, pick_stream(ctx, stream));
+    });
+}
+
+int32_t xl_quantize_q8k_async(xl_context* ctx, const float* d_x, int32_t rows, int32_t k, void* d_q8k, void* stream,
+                              xl_error* err) {
+    return guarded(ctx, err, [&] {
+        ready(ctx, false);
+        need(d_x && d_q8k, XL_E_ARG, "null device pointer");
+        need(rows >= 1 && k >= 256 && k % 256 == 0, XL_E_ARG, "rows >= 1 and k a positive multiple of 256");
+        const uint64_t nblocks = uint64_t(rows) * uint64_t(k / 256);
+        need(nblocks <= uint64_t(ctx->act_max / 256), XL_E_ARG, "more blocks than the activation workspace holds");
+        hip_check(xl::dev::launch_q8k(d_x, int(nblocks), ctx->xq, ctx->xd, static_cast<uint8_t*>(d_q8k), ctx->err_flag,
+                                      pick_stream(ctx, stream)),
+                  "Q8_K launch");
+    });
+}
+
+int32_t xl_matvec_async(xl_context* ctx, int32_t type, const void* d_planar, int32_t n, int32_t k, const float* d_x,
+                        float* d_y, int32_t* d_partials, void* stream, xl_error* err) {
+    return guarded(ctx, err, [&] {
+        ready(ctx, false);
+        need(xl::supported_type(type), XL_E_ARG, "unsupported block type");
+        need(d_planar && d_x && d_y, XL_E_ARG, "null device pointer");
+        int lpr, ppl;
+        need(n >= 1 && xl::row_shape(k, lpr, ppl), XL_E_ARG, "unsupported matvec shape");
+        need(k <= ctx->act_max, XL_E_ARG, "k exceeds the activation workspace");
+        hipStream_t s = pick_stream(ctx, stream);
+        hip_check(xl::dev::launch_q8k(d_x, k / 256, ctx->xq, ctx->xd, nullptr, ctx->err_flag, s), "Q8_K launch");
+        const auto P = xl::plane_layout(type, matrix_blocks(n, k));
+        xl::MatRef m{};
+        m.base = static_cast<const uint8_t*>(d_planar);
+        m.off1 = P.off[1];
+        m.off2 = P.off[2];
+        m.type = type;
+        m.nb = k / 256;
+        hip_check(xl::dev::launch_matvec(m, n, k, ctx->xq, ctx->xd, ctx->tables, d_y, d_partials, ctx->err_flag, s),
+                  "matvec launch");
+    });
+}
+
+uint64_t xl_planar_bytes(int32_t type, int32_t n, int32_t k) {
+    if (!xl::supported_type(type) || n <= 0 || k <= 0 || k % 256) return 0;
+    return xl::plane_layout(type, matrix_blocks(n, k)).bytes;
+}
+
+int32_t xl_repack(int32_t type, int32_t n, int32_t k, const void* aos, void* planar) {
+    if (!xl::supported_type(type) || n <= 0 || k <= 0 || k % 256 || !aos || !planar) return XL_E_ARG;
+    const uint64_t nblk = matrix_blocks(n, k);
+    const auto P = xl::plane_layout(type, nblk);
+    std::memset(planar, 0, P.bytes);
+    for (uint64_t b = 0; b < nblk; ++b)
+        xl::block_to_planes(type, static_cast<const uint8_t*>(aos) + b * xl::block_bytes(type),
+                            static_cast<uint8_t*>(planar), P, b);
+    return XL_OK;
+}
+
+int32_t xl_restore(int32_t type, int32_t n, int32_t k, const void* planar, void* aos) {
+    if (!xl::supported_type(type) || n <= 0 || k <= 0 || k % 256 || !aos || !planar) return XL_E_ARG;
+    const uint64_t nblk = matrix_blocks(n, k);
+    const auto P = xl::plane_layout(type, nblk);
+    for (uint64_t b = 0; b < nblk; ++b)
+        xl::planes_to_block(type, static_cast<const uint8_t*>(planar), P, b,
+                            static_cast<uint8_t*>(aos) + b * xl::block_bytes(type));
+    return XL_OK;
+}
+
+int32_t xl_generate_host(int32_t type, uint64_t seed, int32_t layer, int32_t expert, int32_t role, int32_t n, int32_t k,
+                         void* aos) {
+    if (!xl::supported_type(type) || n <= 0 || k <= 0 || k % 256 || !aos || layer < 0 || expert < 0 || role < 0 ||
+        role > 2)
+        return XL_E_ARG;
+    const uint64_t key = xl::gen_key(seed, uint32_t(layer), uint32_t(expert), uint32_t(role));
+    const uint64_t nblk = matrix_blocks(n, k);
+    for (uint64_t b = 0; b < nblk; ++b) xl::gen_block(type, key, b, static_cast<uint8_t*>(aos) + b * xl::block_bytes(type));
+    return XL_OK;
+}
+
+int32_t xl_codebook(int32_t which, uint64_t* out) {
+    if (!out || which < 0 || which > 3) return XL_E_ARG;
+    try {
+        const auto t = device_tables();
+        if (which == 0) std::copy(t.begin(), t.begin() + 256, out);
+        else if (which == 1) std::copy(t.begin() + 256, t.begin() + 768, out);
+        else if (which == 2) std::copy(t.begin() + 768, t.begin() + 2816, out);
+        else for (int i = 0; i < 128; ++i) out[i] = ksigns(i);
+        return XL_OK;
+    } catch (...) {
+        return XL_E_STATE;
+    }
+}
+
+}  // extern "C"

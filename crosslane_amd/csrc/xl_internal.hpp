@@ -1,0 +1,63 @@
+// Internal types shared by the host API (xl_api.cpp) and the kernels
+// (xl_kernels.hip). Not part of the C ABI.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <cstdint>
+
+namespace xl {
+
+// Device-side error bits (OR-ed into the context's flag word by kernels).
+enum : int {
+    kDevErrExpertId = 1,     // an id outside [0, n_experts)
+    kDevErrNonFinite = 2,    // non-finite activation seen by a quantizer
+    kDevErrType = 4,         // a matrix with an unsupported block type
+};
+
+// One planar matrix (see plane_layout in xl_format.hpp).
+struct MatRef {
+    const uint8_t* base;
+    uint64_t off1, off2;     // byte offsets of planes 1 and 2
+    int32_t type;            // ggml type id 16 / 17 / 29
+    int32_t nb;              // blocks per row (k / 256)
+};
+
+// Per (layer, expert) descriptor: gate (w1), up (w3), down (w2).
+struct ExpertDesc {
+    MatRef m[3];
+};
+
+// Shapes accepted by the specialized row kernels: K (the contraction length)
+// maps to lanes-per-row LPR and pairs-per-lane PPL with LPR * PPL * 64 == K.
+inline bool row_shape(int k, int& lpr, int& ppl) {
+    if (k <= 0 || k % 256) return false;
+    const int pairs = k / 64;
+    int l = 64;
+    while (l > 4 && pairs % l) l >>= 1;
+    lpr = l;
+    ppl = pairs / l;
+    switch (k) {
+        case 256: case 512: case 768: case 1024: case 2048: case 3072: case 4096: return true;
+        default: return false;
+    }
+}
+
+namespace dev {
+hipError_t launch_q8k(const float* x, int nblocks, int8_t* qs, float* d, uint8_t* std_out, int* err, hipStream_t s);
+hipError_t launch_matvec(const MatRef& m, int n, int k, const int8_t* aq, const float* ad, const uint2* tables,
+                         float* y, int32_t* partials, int* err, hipStream_t s);
+// Gate/up + SwiGLU for k picks: h[i*ff + r] = silu(gate_i . x) * (up_i . x).
+hipError_t launch_gate_up(const ExpertDesc* descs, const int32_t* ids, int k, int n_experts, int dim, int ff,
+                          const int8_t* xq, const float* xd, const uint2* tables, float* h, float* g_dbg,
+                          float* u_dbg, int* err, int grid, hipStream_t s);
+// Down for k picks: y[i*dim + r] = down_i . Q8_K(h_i).
+hipError_t launch_down(const ExpertDesc* descs, const int32_t* ids, int k, int n_experts, int dim, int ff,
+                       const int8_t* hq, const float* hd, const uint2* tables, float* y, int* err, int grid,
+                       hipStream_t s);
+// Fixed-order combine: ascending id, out = fma(w, y, out), then + shared.
+hipError_t launch_combine(const int32_t* ids, const float* w, int k, const float* y, int dim, const float* shared,
+                          float* out, hipStream_t s);
+// Seeded generation of one planar matrix (role 0 gate, 1 up, 2 down).
+hipError_t launch_generate(uint8_t* base, int type, int n, int k, uint64_t seed, uint32_t layer, uint32_t expert,
+                           uint32_t role, hipStream_t s);
+}  // namespace dev
+}  // namespace xl

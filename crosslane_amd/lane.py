@@ -1,0 +1,267 @@
+"""ctypes binding of libcrosslane.so and the `Lane` class.
+
+`Lane` keeps the reference lane's method names and meaning
+(engine/strata/warm/runtime.hpp:10-16):
+
+    warm_contains(layer, e)            -> bool
+    warm_grouped()                     -> True (layer batches run in one call)
+    warm_compute(layer, e, x)          -> y            (one expert)
+    warm_compute_many(layer, ids, x)   -> [y_i ...]    (ids order)
+
+plus `layer_forward`, which adds the caller's fixed-order combine
+(warm_execute, engine/strata/warm/runtime.cpp:180-188), and device-resident
+variants taking torch CUDA tensors. Errors raise `XLError`, as the reference
+raises std::runtime_error from `require`.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+from typing import Optional, Sequence
+
+import numpy as np
+
+IQ2_XXS, IQ2_XS, IQ1_M = 16, 17, 29
+BLOCK_BYTES = {IQ2_XXS: 66, IQ2_XS: 74, IQ1_M: 56}
+ABI_VERSION = 1
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "libcrosslane.so")
+
+
+class XLError(RuntimeError):
+    def __init__(self, code: int, message: str):
+        super().__init__(f"[xl {code}] {message}")
+        self.code = code
+
+
+class _Err(C.Structure):
+    _fields_ = [("code", C.c_int32), ("message", C.c_char * 512)]
+
+
+class _Config(C.Structure):
+    _fields_ = [("struct_bytes", C.c_uint32), ("device", C.c_int32), ("dim", C.c_int32), ("ff", C.c_int32),
+                ("n_layers", C.c_int32), ("n_experts", C.c_int32), ("max_picks", C.c_int32),
+                ("max_tokens", C.c_int32)]
+
+
+class _BankInfo(C.Structure):
+    _fields_ = [("payload_bytes", C.c_uint64), ("allocated_bytes", C.c_uint64), ("workspace_bytes", C.c_uint64),
+                ("n_layers", C.c_int32), ("n_experts", C.c_int32), ("generated", C.c_int32),
+                ("reserved", C.c_int32)]
+
+
+_P = C.c_void_p
+_I32 = C.c_int32
+_f32p = np.ctypeslib.ndpointer(np.float32, flags="C_CONTIGUOUS")
+_i32p = np.ctypeslib.ndpointer(np.int32, flags="C_CONTIGUOUS")
+_u64p = np.ctypeslib.ndpointer(np.uint64, flags="C_CONTIGUOUS")
+_ErrP = C.POINTER(_Err)
+
+_SIGNATURES = {
+    "xl_abi_version": (C.c_uint32, []),
+    "xl_open": (_I32, [C.c_uint32, C.POINTER(_Config), C.POINTER(_P), _ErrP]),
+    "xl_close": (None, [_P]),
+    "xl_last_error": (_I32, [_P, _ErrP]),
+    "xl_bank_create": (_I32, [_P, _i32p, _ErrP]),
+    "xl_bank_generate": (_I32, [_P, C.c_uint64, _ErrP]),
+    "xl_bank_upload": (_I32, [_P, _I32, _I32, _I32, _P, C.c_uint64, _ErrP]),
+    "xl_bank_download": (_I32, [_P, _I32, _I32, _I32, _P, C.c_uint64, _ErrP]),
+    "xl_bank_info_get": (_I32, [_P, C.POINTER(_BankInfo)]),
+    "xl_contains": (_I32, [_P, _I32, _I32]),
+    "xl_expert_forward": (_I32, [_P, _I32, _I32, _f32p, _f32p, _ErrP]),
+    "xl_experts_forward": (_I32, [_P, _I32, _i32p, _I32, _f32p, _f32p, _ErrP]),
+    "xl_layer_forward": (_I32, [_P, _I32, _i32p, _f32p, _I32, _f32p, _P, _f32p, _ErrP]),
+    "xl_expert_trace": (_I32, [_P, _I32, _I32, _f32p, _P, _P, _P, _P, _P, _ErrP]),
+    "xl_layer_forward_async": (_I32, [_P, _I32, _P, _P, _I32, _P, _P, _P, _P, _ErrP]),
+    "xl_sync": (_I32, [_P, _P, _ErrP]),
+    "xl_quantize_q8k_async": (_I32, [_P, _P, _I32, _I32, _P, _P, _ErrP]),
+    "xl_matvec_async": (_I32, [_P, _I32, _P, _I32, _I32, _P, _P, _P, _P, _ErrP]),
+    "xl_planar_bytes": (C.c_uint64, [_I32, _I32, _I32]),
+    "xl_repack": (_I32, [_I32, _I32, _I32, _P, _P]),
+    "xl_restore": (_I32, [_I32, _I32, _I32, _P, _P]),
+    "xl_generate_host": (_I32, [_I32, C.c_uint64, _I32, _I32, _I32, _I32, _I32, _P]),
+    "xl_codebook": (_I32, [_I32, _u64p]),
+}
+
+_lib: Optional[C.CDLL] = None
+
+
+def lib() -> C.CDLL:
+    """Loads libcrosslane.so from the package directory. No fallback."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise ImportError(f"{LIB_PATH} is missing: build it with `python -m crosslane_amd._build` "
+                              "(or __graft_entry__.build()); there is no CPU fallback")
+        L = C.CDLL(LIB_PATH)
+        for name, (res, args) in _SIGNATURES.items():
+            f = getattr(L, name)
+            f.restype = res
+            f.argtypes = args
+        if L.xl_abi_version() != ABI_VERSION:
+            raise ImportError("libcrosslane.so ABI version differs from this binding")
+        _lib = L
+    return _lib
+
+
+def _check(rc: int, err: _Err) -> None:
+    if rc != 0:
+        raise XLError(int(err.code or rc), err.message.decode(errors="replace"))
+
+
+def _ptr(t) -> Optional[int]:
+    if t is None:
+        return None
+    return int(t.data_ptr())
+
+
+# ---- host utilities (no GPU) -------------------------------------------------
+def planar_bytes(t: int, n: int, k: int) -> int:
+    return int(lib().xl_planar_bytes(t, n, k))
+
+
+def repack(t: int, n: int, k: int, aos: np.ndarray) -> np.ndarray:
+    aos = np.ascontiguousarray(aos, dtype=np.uint8)
+    assert aos.size == n * (k // 256) * BLOCK_BYTES[t]
+    out = np.zeros(planar_bytes(t, n, k), dtype=np.uint8)
+    rc = lib().xl_repack(t, n, k, aos.ctypes.data, out.ctypes.data)
+    if rc:
+        raise XLError(rc, "repack rejected its arguments")
+    return out
+
+
+def restore(t: int, n: int, k: int, planar: np.ndarray) -> np.ndarray:
+    planar = np.ascontiguousarray(planar, dtype=np.uint8)
+    out = np.zeros(n * (k // 256) * BLOCK_BYTES[t], dtype=np.uint8)
+    rc = lib().xl_restore(t, n, k, planar.ctypes.data, out.ctypes.data)
+    if rc:
+        raise XLError(rc, "restore rejected its arguments")
+    return out
+
+
+def generate_host(t: int, seed: int, layer: int, expert: int, role: int, n: int, k: int) -> np.ndarray:
+    out = np.zeros(n * (k // 256) * BLOCK_BYTES[t], dtype=np.uint8)
+    rc = lib().xl_generate_host(t, seed, layer, expert, role, n, k, out.ctypes.data)
+    if rc:
+        raise XLError(rc, "generate_host rejected its arguments")
+    return out
+
+
+def codebook(which: int) -> np.ndarray:
+    out = np.zeros((256, 512, 2048, 128)[which], dtype=np.uint64)
+    rc = lib().xl_codebook(which, out)
+    if rc:
+        raise XLError(rc, "codebook index")
+    return out
+
+
+# ---- the lane ------------------------------------------------------------------
+class Lane:
+    """One context: a resident bank of n_layers x n_experts experts on one GPU."""
+
+    def __init__(self, dim: int, ff: int, n_layers: int, n_experts: int, types: np.ndarray,
+                 max_picks: int = 8, max_tokens: int = 0, device: int = 0):
+        L = lib()
+        cfg = _Config(C.sizeof(_Config), device, dim, ff, n_layers, n_experts, max_picks, max_tokens)
+        ctx = _P()
+        err = _Err()
+        _check(L.xl_open(ABI_VERSION, C.byref(cfg), C.byref(ctx), C.byref(err)), err)
+        self._ctx = ctx
+        self.dim, self.ff, self.n_layers, self.n_experts, self.max_picks = dim, ff, n_layers, n_experts, max_picks
+        types = np.ascontiguousarray(types, dtype=np.int32).reshape(n_layers, n_experts, 3)
+        self.types = types
+        self._call("xl_bank_create", types.reshape(-1))
+
+    # -- plumbing
+    def _call(self, name: str, *args) -> None:
+        err = _Err()
+        _check(getattr(lib(), name)(self._ctx, *args, C.byref(err)), err)
+
+    def close(self) -> None:
+        if getattr(self, "_ctx", None):
+            lib().xl_close(self._ctx)
+            self._ctx = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    # -- bank
+    def generate(self, seed: int) -> None:
+        self._call("xl_bank_generate", C.c_uint64(seed))
+
+    def upload(self, layer: int, expert: int, role: int, aos: np.ndarray) -> None:
+        aos = np.ascontiguousarray(aos, dtype=np.uint8)
+        self._call("xl_bank_upload", layer, expert, role, aos.ctypes.data, C.c_uint64(aos.size))
+
+    def download(self, layer: int, expert: int, role: int) -> np.ndarray:
+        t = int(self.types[layer, expert, role])
+        n, k = (self.ff, self.dim) if role < 2 else (self.dim, self.ff)
+        out = np.zeros(n * (k // 256) * BLOCK_BYTES[t], dtype=np.uint8)
+        self._call("xl_bank_download", layer, expert, role, out.ctypes.data, C.c_uint64(out.size))
+        return out
+
+    def info(self) -> dict:
+        bi = _BankInfo()
+        lib().xl_bank_info_get(self._ctx, C.byref(bi))
+        return {f: getattr(bi, f) for f, _ in _BankInfo._fields_}
+
+    # -- WarmRedirect surface
+    def warm_contains(self, layer: int, e: int) -> bool:
+        return bool(lib().xl_contains(self._ctx, layer, e))
+
+    def warm_grouped(self) -> bool:
+        return True
+
+    def warm_compute(self, layer: int, e: int, x: np.ndarray) -> np.ndarray:
+        y = np.zeros(self.dim, dtype=np.float32)
+        self._call("xl_expert_forward", layer, e, np.ascontiguousarray(x, dtype=np.float32), y)
+        return y
+
+    def warm_compute_many(self, layer: int, ids: Sequence[int], x: np.ndarray) -> list:
+        ids = np.ascontiguousarray(ids, dtype=np.int32)
+        ys = np.zeros((ids.size, self.dim), dtype=np.float32)
+        self._call("xl_experts_forward", layer, ids, ids.size, np.ascontiguousarray(x, dtype=np.float32),
+                   ys.reshape(-1))
+        return [ys[i] for i in range(ids.size)]
+
+    def layer_forward(self, layer: int, ids: Sequence[int], weights: Sequence[float], x: np.ndarray,
+                      shared: Optional[np.ndarray] = None) -> np.ndarray:
+        ids = np.ascontiguousarray(ids, dtype=np.int32)
+        w = np.ascontiguousarray(weights, dtype=np.float32)
+        out = np.zeros(self.dim, dtype=np.float32)
+        sh = None if shared is None else np.ascontiguousarray(shared, dtype=np.float32)
+        self._call("xl_layer_forward", layer, ids, w, ids.size, np.ascontiguousarray(x, dtype=np.float32),
+                   None if sh is None else sh.ctypes.data, out)
+        return out
+
+    def expert_trace(self, layer: int, e: int, x: np.ndarray) -> dict:
+        ff, dim = self.ff, self.dim
+        g = np.zeros(ff, np.float32); u = np.zeros(ff, np.float32); h = np.zeros(ff, np.float32)
+        q8h = np.zeros((ff // 256) * 292, np.uint8); y = np.zeros(dim, np.float32)
+        self._call("xl_expert_trace", layer, e, np.ascontiguousarray(x, dtype=np.float32), g.ctypes.data,
+                   u.ctypes.data, h.ctypes.data, q8h.ctypes.data, y.ctypes.data)
+        return {"g": g, "u": u, "h": h, "q8h": q8h, "y": y}
+
+    # -- device-resident (torch CUDA tensors)
+    def layer_forward_async(self, layer: int, ids, w, x, out, shared=None, stream=None) -> None:
+        self._call("xl_layer_forward_async", layer, _ptr(ids), _ptr(w), int(ids.numel()), _ptr(x), _ptr(shared),
+                   _ptr(out), None if stream is None else int(stream))
+
+    def sync(self, stream=None) -> None:
+        self._call("xl_sync", None if stream is None else int(stream))
+
+    def quantize_q8k_async(self, x, rows: int, k: int, q8k_out, stream=None) -> None:
+        self._call("xl_quantize_q8k_async", _ptr(x), rows, k, _ptr(q8k_out), None if stream is None else int(stream))
+
+    def matvec_async(self, t: int, planar, n: int, k: int, x, y, partials=None, stream=None) -> None:
+        self._call("xl_matvec_async", t, _ptr(planar), n, k, _ptr(x), _ptr(y), _ptr(partials),
+                   None if stream is None else int(stream))

@@ -1,0 +1,148 @@
+/* crosslane MI355X routed-expert lane: C ABI.
+ *
+ * One resident expert bank on one GPU; per token and layer, "compute these
+ * top-k experts for this vector, then join them in a fixed order". Plain
+ * pointers and sizes only. Every call returns int32 status (XL_OK = 0) and,
+ * when `err` is non-null, fills it; the context also keeps the last error.
+ * A context is driven by one caller thread at a time (the reference drives its
+ * HIP lane from one dedicated worker thread, engine/strata/warm/worker.hpp:9-18).
+ * No call allocates device memory after xl_bank_create (the workspace is sized
+ * at xl_open, like the reference's arena reservation,
+ * engine/strata/sycl/stage/wiring/hip_resident_bank.hpp:63-94).
+ *
+ * Conventions mirror the reference's DSO ABI (engine/strata/sycl/stage/wiring/
+ * abi_v2.h:28-68, abi_backend_plugin.cpp:31-39): a version + struct-size check
+ * before anything is written, an int32 code plus a 512-byte message, every
+ * exception caught at the boundary, and a context poisoned by a device error
+ * (all later compute calls fail until xl_close).
+ */
+#ifndef CROSSLANE_H
+#define CROSSLANE_H
+#include <stdint.h>
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define XL_ABI_VERSION 1u
+
+enum {
+    XL_OK = 0,
+    XL_E_ARG = 1,        /* invalid argument (shape, id, pointer, finiteness) */
+    XL_E_STATE = 2,      /* wrong call order, or a poisoned context */
+    XL_E_HIP = 3,        /* HIP runtime error */
+    XL_E_DEVICE = 4,     /* a kernel reported an error flag (bad id, non-finite) */
+    XL_E_VERSION = 5,    /* ABI version or struct size mismatch */
+    XL_E_MEMORY = 6      /* device or host allocation failed */
+};
+
+/* ggml block type ids accepted for expert matrices */
+enum { XL_IQ2_XXS = 16, XL_IQ2_XS = 17, XL_IQ1_M = 29 };
+
+typedef struct xl_error {
+    int32_t code;
+    char message[512];
+} xl_error;
+
+typedef struct xl_config {
+    uint32_t struct_bytes; /* sizeof(xl_config) */
+    int32_t device;        /* HIP device ordinal */
+    int32_t dim;           /* d_model: 256..4096, a multiple of 256 */
+    int32_t ff;            /* d_ff:    256..4096, a multiple of 256 */
+    int32_t n_layers;      /* layers in the bank */
+    int32_t n_experts;     /* routed experts per layer */
+    int32_t max_picks;     /* top-k bound, 1..16 (reference kPicks = 8, model_meta.hpp:18) */
+    int32_t max_tokens;    /* grouped-path token bound (0 = grouped path unused) */
+} xl_config;
+
+typedef struct xl_bank_info {
+    uint64_t payload_bytes;    /* ggml bytes of every resident matrix */
+    uint64_t allocated_bytes;  /* device bytes held by the bank (256-B aligned planes) */
+    uint64_t workspace_bytes;  /* device bytes of the per-call workspace */
+    int32_t n_layers, n_experts;
+    int32_t generated;         /* 1 after xl_bank_generate */
+    int32_t reserved;
+} xl_bank_info;
+
+typedef struct xl_context xl_context;
+
+uint32_t xl_abi_version(void);
+
+/* Opens a context on cfg->device and sizes its workspace. */
+int32_t xl_open(uint32_t abi_version, const xl_config* cfg, xl_context** out, xl_error* err);
+/* Drains the context stream, then frees every device allocation. */
+void xl_close(xl_context* ctx);
+int32_t xl_last_error(const xl_context* ctx, xl_error* err);
+
+/* ---- bank ---------------------------------------------------------------
+ * types: n_layers * n_experts * 3 ggml type ids, roles (gate w1, up w3,
+ * down w2) fastest; gate and up must share a type (the reference requires the
+ * same, hip_resident.hpp:114). Replaces HipResidentBank::load's slab sizing
+ * (hip_resident_bank.hpp:38-142, hip_resident.hpp:54-97). */
+int32_t xl_bank_create(xl_context* ctx, const int32_t* types, xl_error* err);
+/* Fills every matrix on the device from the seeded generator. */
+int32_t xl_bank_generate(xl_context* ctx, uint64_t seed, xl_error* err);
+/* Uploads / downloads one matrix as raw ggml AoS blocks (host memory); the
+ * bank stores it repacked into planes. role: 0 gate, 1 up, 2 down. */
+int32_t xl_bank_upload(xl_context* ctx, int32_t layer, int32_t expert, int32_t role, const void* aos, uint64_t bytes,
+                       xl_error* err);
+int32_t xl_bank_download(xl_context* ctx, int32_t layer, int32_t expert, int32_t role, void* aos, uint64_t bytes,
+                         xl_error* err);
+int32_t xl_bank_info_get(const xl_context* ctx, xl_bank_info* out);
+/* 1 when (layer, expert) is resident (WarmRedirect::warm_contains,
+ * engine/strata/warm/runtime.hpp:14). */
+int32_t xl_contains(const xl_context* ctx, int32_t layer, int32_t expert);
+
+/* ---- lane calls, host memory, synchronous --------------------------------
+ * xl_expert_forward   = WarmRedirect::warm_compute        (runtime.hpp:15)
+ * xl_experts_forward  = WarmRedirect::warm_compute_many   (runtime.hpp:13):
+ *                       ys is k rows of dim floats in `ids` order
+ * xl_layer_forward    = the lane plus the caller's fixed-order combine
+ *                       (warm_execute, runtime.cpp:180-188): ascending id,
+ *                       out = fma(w, y, out), then out += shared when given.
+ * ids must be unique and in [0, n_experts); k in 1..max_picks; x finite. */
+int32_t xl_expert_forward(xl_context* ctx, int32_t layer, int32_t expert, const float* x, float* y, xl_error* err);
+int32_t xl_experts_forward(xl_context* ctx, int32_t layer, const int32_t* ids, int32_t k, const float* x, float* ys,
+                           xl_error* err);
+int32_t xl_layer_forward(xl_context* ctx, int32_t layer, const int32_t* ids, const float* w, int32_t k, const float* x,
+                         const float* shared_or_null, float* out, xl_error* err);
+/* Expert chain with its intermediates (the reference's probe snapshot,
+ * parity/hip_resident_check.cpp:56-62,93-104); any output may be null.
+ * q8h receives ff/256 Q8_K blocks of 292 bytes. */
+int32_t xl_expert_trace(xl_context* ctx, int32_t layer, int32_t expert, const float* x, float* g, float* u, float* h,
+                        void* q8h, float* y, xl_error* err);
+
+/* ---- device-resident calls (device pointers, ordered on `stream`; a null
+ * stream means the context stream). Results are valid after the stream
+ * drains; xl_sync drains and reports kernel error flags. ids are checked on
+ * the device: a bad id sets the flag and that pick contributes nothing. */
+int32_t xl_layer_forward_async(xl_context* ctx, int32_t layer, const int32_t* d_ids, const float* d_w, int32_t k,
+                               const float* d_x, const float* d_shared_or_null, float* d_out, void* stream,
+                               xl_error* err);
+int32_t xl_sync(xl_context* ctx, void* stream, xl_error* err);
+
+/* ---- primitives (device pointers) -----------------------------------------
+ * q8k_* : Q8_K quantization of rows x k floats (k a multiple of 256) into
+ * rows*k/256 blocks of 292 bytes (q8k_core.hpp:13-38, hip_q8k.hpp:9). */
+int32_t xl_quantize_q8k_async(xl_context* ctx, const float* d_x, int32_t rows, int32_t k, void* d_q8k, void* stream,
+                              xl_error* err);
+/* One planar matrix (n x k) times Q8_K(x): y[n] and, when non-null, the
+ * per-block int32 partials (n*k/256 ints; IQ1_M: (main, delta) pairs).
+ * Replaces q8k::mv (hip_q8k.hpp:10). d_x is the f32 input vector. */
+int32_t xl_matvec_async(xl_context* ctx, int32_t type, const void* d_planar, int32_t n, int32_t k, const float* d_x,
+                        float* d_y, int32_t* d_partials, void* stream, xl_error* err);
+
+/* ---- host utilities (no device needed) ------------------------------------ */
+uint64_t xl_planar_bytes(int32_t type, int32_t n, int32_t k);
+int32_t xl_repack(int32_t type, int32_t n, int32_t k, const void* aos, void* planar);
+int32_t xl_restore(int32_t type, int32_t n, int32_t k, const void* planar, void* aos);
+/* The generator's AoS bytes of matrix (layer, expert, role), host-side. */
+int32_t xl_generate_host(int32_t type, uint64_t seed, int32_t layer, int32_t expert, int32_t role, int32_t n, int32_t k,
+                         void* aos);
+/* Expanded codebooks: 0 IQ2_XXS grid (256 u64), 1 IQ2_XS grid (512),
+ * 2 IQ1 grid (2048), 3 ksigns (128 values widened to u64). */
+int32_t xl_codebook(int32_t which, uint64_t* out);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,63 @@
+// Thin extern "C" wrapper that compiles the reference's own CPU arithmetic from
+// its sources under /root/reference (include paths set by oracle/Makefile) into
+// oracle/_ref/libxlref.so. TEST INFRASTRUCTURE ONLY: it lets the tests compare
+// the oracle restatement with the reference code itself, and serves as the
+// "reference" CPU baseline. Nothing here is copied; the headers are included
+// where they lie.
+//   sycl/stage/wiring/q8k_core.hpp (+ q8k_tables.inc): Q8_K quant and IQ dots
+//   sycl/moe/core.hpp (+ format.hpp, tables.hpp):     per-32 decoder
+//   warm/other_combine.hpp:                             fixed-order combine
+#include <array>
+#include <atomic>
+#include <cstring>
+#include <span>
+#include <thread>
+#include <utility>
+#include <vector>
+#include "q8k_core.hpp"
+#include "core.hpp"
+#include "other_combine.hpp"
+
+namespace q = strata::wiring::q8k;
+namespace m = strata::ds4::moe;
+
+extern "C" {
+void ref_quant_block(const float* x, void* out) { q::quant_block(x, *static_cast<q::Block*>(out)); }
+float ref_dot(int t, const uint8_t* w, const void* a, int nb) { return q::dot(t, w, static_cast<const q::Block*>(a), nb); }
+void ref_integer_lane(int t, const uint8_t* w, const void* a, int lane, int* main_out, int* delta_out) {
+    const auto v = q::integer_lane(t, w, *static_cast<const q::Block*>(a), lane);
+    *main_out = v.main; *delta_out = v.delta;
+}
+float ref_swiglu(float g, float u, float lim) { return q::swiglu(g, u, lim); }
+float ref_half(uint16_t h) { return q::half(h); }
+int ref_nearest(float x) { return q::nearest(x); }
+void ref_table(int which, uint64_t* out) {
+    if (which == 0) std::memcpy(out, q::iq2xxs_grid, sizeof q::iq2xxs_grid);
+    else if (which == 1) std::memcpy(out, q::iq2xs_grid, sizeof q::iq2xs_grid);
+    else if (which == 2) std::memcpy(out, q::iq1s_grid, sizeof q::iq1s_grid);
+    else for (int i = 0; i < 128; ++i) out[i] = q::ksigns_iq2xs[i];
+}
+// Per-32 decode of sub-block kb of one row (types: 16, 17, 29).
+void ref_decode(int t, const uint8_t* row, int kb, int* q32, int* s2, float* d) {
+    const m::Type ty = t == 16 ? m::Type::iq2_xxs : t == 17 ? m::Type::iq2_xs : m::Type::iq1_m;
+    const auto s = m::decode(ty, row, kb);
+    for (int j = 0; j < 32; ++j) q32[j] = s.q[j];
+    s2[0] = s.s[0]; s2[1] = s.s[1]; *d = s.d;
+}
+// Matvec over threads with the reference's dot, rows split in 64-row jobs.
+void ref_matvec(int t, const uint8_t* w, int n, int k, const void* a, float* y, int threads) {
+    const int nb = k / 256; const size_t rb = size_t(nb) * q::block_bytes(t);
+    const auto* act = static_cast<const q::Block*>(a);
+    std::atomic<int> next{0};
+    auto run = [&] { for (int j; (j = next.fetch_add(1)) * 64 < n;) for (int r = j * 64; r < n && r < j * 64 + 64; ++r) y[r] = q::dot(t, w + size_t(r) * rb, act, nb); };
+    std::vector<std::thread> pool; for (int i = 1; i < threads; ++i) pool.emplace_back(run);
+    run(); for (auto& th : pool) th.join();
+}
+void ref_combine(const int* ids, const float* w, int k, const float* rows, int dim, const float* shared, float* out) {
+    std::array<std::vector<std::pair<size_t, std::vector<float>>>, 1> results;
+    for (int i = 0; i < k; ++i) results[0].emplace_back(size_t(i), std::vector<float>(rows + size_t(i) * dim, rows + size_t(i + 1) * dim));
+    auto y = strata::wiring::other_combine(std::span<const int>(ids, size_t(k)), std::span<const float>(w, size_t(k)),
+                                           std::span<const float>(shared, size_t(dim)), results, strata::wiring::OtherOptions{});
+    std::memcpy(out, y.data(), sizeof(float) * size_t(dim));
+}
+}

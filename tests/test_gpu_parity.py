@@ -1,0 +1,220 @@
+"""GPU parity of the HIP path against the CPU oracle, through the C ABI.
+
+Bars: Q8_K bytes and per-block int32 partials bit-exact;
+f32 outputs within max relative error 1e-3 (max-norm, tests.conftest.max_rel);
+runs bit-identical run to run. The hidden-state quantization is compared by
+feeding the device's own SwiGLU output to the oracle quantizer (host and device
+exp differ by ulps; the reference does the same, warm/expert_check.cpp:86-88).
+"""
+from __future__ import annotations
+
+import os
+import sys
+
+import numpy as np
+import pytest
+
+import crosslane_amd as xl
+from oracle.oracle import BLOCK_BYTES
+from tests.conftest import max_rel
+
+pytestmark = pytest.mark.gpu
+TOL = 1e-3
+
+torch = pytest.importorskip("torch")
+
+
+def step(msg):
+    print(f"[gpu-step] {msg}", flush=True)
+    sys.stdout.flush()
+
+
+def dev(a):
+    return torch.from_numpy(np.ascontiguousarray(a)).to("cuda")
+
+
+def types_map(L, E, gu, dn):
+    t = np.zeros((L, E, 3), np.int32)
+    t[..., 0] = gu; t[..., 1] = gu; t[..., 2] = dn
+    return t
+
+
+@pytest.fixture(scope="module")
+def probe():
+    """A context used only for primitives (quantize / matvec)."""
+    lane = xl.Lane(4096, 4096, 1, 1, types_map(1, 1, 16, 16), max_picks=1)
+    yield lane
+    lane.close()
+
+
+# ---- Q8_K -----------------------------------------------------------------------
+def test_q8k_bit_exact(probe, orc, rng):
+    gold = np.load(os.path.join(os.path.dirname(__file__), "golden", "reference_vectors.npz"))
+    cases = [gold["q8k_x"].reshape(-1)]
+    for scale in (1e-3, 1.0, 1e3):
+        cases.append((rng.standard_normal(4096) * scale).astype(np.float32))
+    for x in cases:
+        step(f"q8k blocks={x.size // 256}")
+        dx = dev(x.astype(np.float32))
+        out = torch.zeros(x.size // 256 * 292, dtype=torch.uint8, device="cuda")
+        probe.quantize_q8k_async(dx, 1, x.size, out)
+        probe.sync()
+        assert np.array_equal(out.cpu().numpy(), orc.quantize(x).view(np.uint8))
+
+
+# ---- matvec + per-block partials -------------------------------------------------
+@pytest.mark.parametrize("t", [16, 17, 29])
+@pytest.mark.parametrize("n,k", [(64, 256), (96, 512), (40, 768), (128, 1024), (64, 2048), (256, 3072), (256, 4096)])
+def test_matvec_partials_exact(probe, orc, t, n, k):
+    step(f"matvec type={t} n={n} k={k}")
+    aos = orc.gen_matrix(t, 1234 + k, 0, t, 0, n, k)
+    planar = dev(xl.repack(t, n, k, aos))
+    x = np.random.default_rng(n * k + t).standard_normal(k).astype(np.float32)
+    y = torch.zeros(n, dtype=torch.float32, device="cuda")
+    nb = k // 256
+    parts = torch.zeros(n * nb * (2 if t == 29 else 1), dtype=torch.int32, device="cuda")
+    probe.matvec_async(t, planar, n, k, dev(x), y, parts)
+    probe.sync()
+    act = orc.quantize(x)
+    rb = nb * BLOCK_BYTES[t]
+    want_parts = np.concatenate([orc.block_partials(t, aos[r * rb:(r + 1) * rb], act) for r in range(n)])
+    assert np.array_equal(parts.cpu().numpy(), want_parts)
+    want_y = orc.matvec(t, aos, n, k, act)
+    assert max_rel(y.cpu().numpy(), want_y) < TOL
+
+
+# ---- one expert, stage by stage ---------------------------------------------------
+@pytest.mark.parametrize("dim,ff,sig", [(512, 256, (16, 16, 17)), (256, 768, (29, 29, 29)),
+                                        (1024, 512, (17, 17, 16)), (4096, 3072, (16, 16, 17))])
+def test_expert_stages(orc, dim, ff, sig):
+    step(f"expert stages dim={dim} ff={ff} sig={sig}")
+    E = 4
+    lane = xl.Lane(dim, ff, 1, E, types_map(1, E, sig[0], sig[2]), max_picks=6)
+    try:
+        lane.generate(seed=0xABC)
+        x = np.random.default_rng(dim + ff).standard_normal(dim).astype(np.float32)
+        e = 2
+        tr = lane.expert_trace(0, e, x)
+        gate, up, down = orc.gen_expert(sig, 0xABC, 0, e, dim, ff)
+        yo, go, uo, ho = orc.expert(sig, gate, up, down, dim, ff, x, intermediates=True)
+        assert max_rel(tr["g"], go) < TOL and max_rel(tr["u"], uo) < TOL
+        assert max_rel(tr["h"], ho) < TOL
+        # Q8_K(h) bit-exact given the device's own h
+        assert np.array_equal(tr["q8h"], orc.quantize(tr["h"]).view(np.uint8))
+        # down from the device's h: partial-exact path, float within tolerance
+        assert max_rel(tr["y"], orc.down_from_hidden(sig[2], down, dim, ff, tr["h"])) < TOL
+        assert max_rel(tr["y"], yo) < TOL
+    finally:
+        lane.close()
+
+
+# ---- generator -------------------------------------------------------------------
+def test_device_generator_matches_oracle(orc):
+    step("device generator")
+    types = np.array([[[16, 16, 17], [29, 29, 29], [17, 17, 16]]], np.int32)
+    lane = xl.Lane(512, 768, 1, 3, types, max_picks=3)
+    try:
+        lane.generate(seed=987654321)
+        for e in range(3):
+            for r in range(3):
+                t = int(types[0, e, r])
+                n, k = (768, 512) if r < 2 else (512, 768)
+                assert np.array_equal(lane.download(0, e, r), orc.gen_matrix(t, 987654321, 0, e, r, n, k)), (e, r)
+    finally:
+        lane.close()
+
+
+def test_upload_download_roundtrip(orc):
+    step("upload/download")
+    lane = xl.Lane(256, 256, 2, 2, types_map(2, 2, 29, 17), max_picks=2)
+    try:
+        aos = orc.gen_matrix(17, 5, 9, 9, 2, 256, 256)
+        lane.upload(1, 1, 2, aos)
+        assert np.array_equal(lane.download(1, 1, 2), aos)
+    finally:
+        lane.close()
+
+
+# ---- layer: config-1 shapes --------------------------------------------------------
+@pytest.fixture(scope="module")
+def layer_lane():
+    step("layer lane: 4096x3072, 384 experts, IQ2_XXS gate/up + IQ2_XS down")
+    lane = xl.Lane(4096, 3072, 1, 384, types_map(1, 384, 16, 17), max_picks=8)
+    lane.generate(seed=0x1A7E5)
+    yield lane
+    lane.close()
+
+
+def route(logits, k=6):
+    p = np.exp(logits - logits.max()); p /= p.sum()
+    ids = np.argsort(-p, kind="stable")[:k]
+    w = p[ids] / p[ids].sum()
+    return ids.astype(np.int32), w.astype(np.float32)
+
+
+def test_layer_vs_oracle(layer_lane, orc):
+    rng = np.random.default_rng(11)
+    for trial in range(2):
+        ids, w = route(rng.standard_normal(384).astype(np.float32))
+        x = rng.standard_normal(4096).astype(np.float32)
+        shared = rng.standard_normal(4096).astype(np.float32) if trial else None
+        step(f"layer trial={trial} ids={ids.tolist()}")
+        got = layer_lane.layer_forward(0, ids, w, x, shared)
+        rows = np.stack([orc.expert((16, 16, 17), *orc.gen_expert((16, 16, 17), 0x1A7E5, 0, int(e), 4096, 3072),
+                                    4096, 3072, x) for e in ids])
+        want = orc.combine(ids, w, rows, shared)
+        assert max_rel(got, want) < TOL
+
+
+def test_layer_deterministic_and_batch_equals_serial(layer_lane):
+    rng = np.random.default_rng(12)
+    ids, w = route(rng.standard_normal(384).astype(np.float32))
+    x = rng.standard_normal(4096).astype(np.float32)
+    step("layer determinism")
+    a = layer_lane.layer_forward(0, ids, w, x)
+    for _ in range(3):
+        assert np.array_equal(a.view(np.uint32), layer_lane.layer_forward(0, ids, w, x).view(np.uint32))
+    many = layer_lane.warm_compute_many(0, ids, x)
+    for i, e in enumerate(ids):
+        single = layer_lane.warm_compute(0, int(e), x)
+        assert np.array_equal(single.view(np.uint32), many[i].view(np.uint32))
+
+
+def test_layer_async_matches_sync(layer_lane):
+    rng = np.random.default_rng(13)
+    ids, w = route(rng.standard_normal(384).astype(np.float32))
+    x = rng.standard_normal(4096).astype(np.float32)
+    step("layer async")
+    want = layer_lane.layer_forward(0, ids, w, x)
+    out = torch.zeros(4096, dtype=torch.float32, device="cuda")
+    layer_lane.layer_forward_async(0, dev(ids), dev(w), dev(x), out)
+    layer_lane.sync()
+    assert np.array_equal(out.cpu().numpy().view(np.uint32), want.view(np.uint32))
+
+
+def test_host_rejects_bad_routes(layer_lane):
+    x = np.zeros(4096, np.float32)
+    with pytest.raises(xl.XLError):
+        layer_lane.layer_forward(0, [1, 1], [0.5, 0.5], x)
+    with pytest.raises(xl.XLError):
+        layer_lane.layer_forward(0, [384], [1.0], x)
+    with pytest.raises(xl.XLError):
+        layer_lane.layer_forward(0, [3], [1.0], np.full(4096, np.nan, np.float32))
+
+
+def test_device_rejects_bad_id_and_poisons():
+    # An out-of-range id reaches the kernels only through the device path; the
+    # kernels bounds-check it, skip the pick and raise the error flag.
+    step("device bad id")
+    lane = xl.Lane(256, 256, 1, 4, types_map(1, 4, 16, 16), max_picks=2)
+    try:
+        lane.generate(1)
+        out = torch.zeros(256, dtype=torch.float32, device="cuda")
+        lane.layer_forward_async(0, dev(np.array([1, 99], np.int32)), dev(np.array([0.5, 0.5], np.float32)),
+                                 dev(np.ones(256, np.float32)), out)
+        with pytest.raises(xl.XLError, match="expert id"):
+            lane.sync()
+        with pytest.raises(xl.XLError, match="poisoned"):
+            lane.layer_forward(0, [1], [1.0], np.ones(256, np.float32))
+    finally:
+        lane.close()

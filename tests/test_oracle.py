@@ -1,0 +1,212 @@
+"""CPU: pins the oracle (oracle/xl_oracle.c) before anything is compared with it.
+
+Each function is checked against (a) the golden vectors written from the
+reference's own q8k_core.hpp / other_combine.hpp (tests/golden), (b) the same
+reference code compiled in oracle/_ref when present, and (c) what the
+mathematics fixes: exact fp16 decode, closed-form Q8_K blocks, round-half-even
+ties, a brute-force dequantize-and-multiply integer dot, and the reference's
+independent per-32 decoder (sycl/moe/core.hpp:78-105).
+"""
+from __future__ import annotations
+
+import os
+
+import numpy as np
+import pytest
+
+from oracle.oracle import BLOCK_BYTES, Q8K_DTYPE
+
+GOLD = np.load(os.path.join(os.path.dirname(__file__), "golden", "reference_vectors.npz"))
+
+
+def f32bits(a):
+    return np.asarray(a, dtype=np.float32).view(np.uint32)
+
+
+# ---- scalars ------------------------------------------------------------------
+def test_half_decode_exhaustive(orc):
+    # q8k_core.hpp:17-24: every fp16 -> f32 exactly; numpy's float16 widening is exact.
+    h = np.arange(65536, dtype=np.uint32).astype(np.uint16)
+    want = h.view(np.float16).astype(np.float32)
+    got = np.array([orc.lib.orc_half(int(v)) for v in h], dtype=np.float32)
+    finite = np.isfinite(want)
+    assert np.array_equal(f32bits(got[finite]), f32bits(want[finite]))
+    assert np.all(np.isnan(got[np.isnan(want)]))
+    assert np.array_equal(got[np.isinf(want)], want[np.isinf(want)])
+
+
+def test_nearest_round_half_even(orc):
+    # ggml nearest_int: round half to even for |x| < 2^22.
+    for x, want in [(0.5, 0), (1.5, 2), (2.5, 2), (-0.5, 0), (-1.5, -2), (-2.5, -2), (126.5, 126), (127.49, 127),
+                    (-127.0, -127), (3.0, 3)]:
+        assert orc.lib.orc_nearest(x) == want, x
+
+
+# ---- Q8_K -----------------------------------------------------------------------
+def test_q8k_golden(orc):
+    got = orc.quantize(GOLD["q8k_x"].reshape(-1)).view(np.uint8).reshape(-1, 292)
+    assert np.array_equal(got, GOLD["q8k_bytes"])
+
+
+def test_q8k_closed_forms(orc):
+    z = orc.quantize(np.zeros(256, np.float32))[0]
+    assert z["d"] == 0 and not z["qs"].any() and not z["bsums"].any()
+    for c, j in [(3.5, 17), (-2.0, 0), (1e-20, 255)]:
+        x = np.zeros(256, np.float32); x[j] = c
+        b = orc.quantize(x)[0]
+        # is = -127/c, so qs[j] = -127 and d = 1/is = -c/127 (rounded twice).
+        assert b["qs"][j] == -127 and np.count_nonzero(b["qs"]) == 1
+        assert b["d"] == np.float32(1.0) / (np.float32(-127.0) / np.float32(c))
+        assert b["bsums"][j // 16] == -127
+    # |max| tie: the FIRST value of largest magnitude sets the sign (strict '>').
+    x = np.zeros(256, np.float32); x[5] = -4.0; x[9] = 4.0
+    b = orc.quantize(x)[0]
+    assert b["qs"][5] == -127 and b["qs"][9] == 127
+
+
+def test_q8k_vs_reference_random(orc, ref, rng):
+    for scale in (1e-3, 1.0, 1e3):
+        x = (rng.standard_normal(256 * 64) * scale).astype(np.float32)
+        assert orc.quantize(x).tobytes() == ref.quantize(x).tobytes()
+
+
+def test_q8k_bsums_and_range(orc, rng):
+    x = rng.standard_normal(256 * 32).astype(np.float32)
+    q = orc.quantize(x)
+    assert np.all(q["qs"] >= -127) and np.all(q["qs"] <= 127)
+    assert np.array_equal(q["bsums"], q["qs"].reshape(-1, 16, 16).astype(np.int32).sum(-1))
+    # dequantized values within half a quantum of the input
+    deq = q["qs"].astype(np.float64) * q["d"][:, None].astype(np.float64)
+    err = np.abs(deq - x.reshape(-1, 256)) / np.abs(q["d"][:, None])
+    assert err.max() <= 0.5 + 1e-3
+
+
+# ---- IQ x Q8_K dot --------------------------------------------------------------
+@pytest.mark.parametrize("t", [16, 17, 29])
+def test_dot_golden(orc, t):
+    act = orc.quantize(GOLD["dot_act_x"])
+    rows = GOLD[f"dot{t}_rows"]
+    got = np.array([orc.dot(t, rows[r], act) for r in range(rows.shape[0])], np.float32)
+    assert np.array_equal(f32bits(got), f32bits(GOLD[f"dot{t}_y"]))
+    bb = BLOCK_BYTES[t]
+    for r in range(rows.shape[0]):
+        for b in range(2):
+            for l in range(8):
+                assert orc.integer_lane(t, rows[r, b * bb:(b + 1) * bb], act[b:b + 1], l) == tuple(
+                    GOLD[f"dot{t}_lanes"][r, b, l])
+
+
+@pytest.mark.parametrize("t", [16, 17, 29])
+def test_dot_vs_reference_generated(orc, ref, t):
+    act = orc.quantize(np.random.default_rng(t).standard_normal(1024).astype(np.float32))
+    w = orc.gen_matrix(t, 99, 3, 7, 1, 64, 1024)
+    rb = 4 * BLOCK_BYTES[t]
+    for r in range(64):
+        row = w[r * rb:(r + 1) * rb]
+        assert np.float32(orc.dot(t, row, act)).view(np.uint32) == np.float32(ref.dot(t, row, act)).view(np.uint32)
+
+
+@pytest.mark.parametrize("t", [16, 17, 29])
+def test_block_partials_brute_force(orc, t, rng):
+    # The per-block integer is order-independent: a plain dequantize-and-multiply
+    # pins it. IQ1_M's brute force is 8*main + delta (values 8*grid + delta).
+    act = orc.quantize(rng.standard_normal(256 * 4).astype(np.float32))
+    w = orc.gen_matrix(t, 5, 0, 1, 2, 16, 1024)
+    bb = BLOCK_BYTES[t]
+    for r in range(16):
+        row = w[r * 4 * bb:(r + 1) * 4 * bb]
+        parts = orc.block_partials(t, row, act)
+        for b in range(4):
+            brute = orc.brute_block(t, row[b * bb:(b + 1) * bb], act[b:b + 1])
+            if t == 29:
+                assert brute == 8 * parts[2 * b] + parts[2 * b + 1]
+            else:
+                assert brute == parts[b]
+
+
+@pytest.mark.parametrize("t", [16, 17, 29])
+def test_brute_force_vs_reference_decoder(orc, ref, t, rng):
+    # Reference per-32 decoder (sycl/moe/core.hpp): values and odd sub-scales.
+    w = orc.gen_matrix(t, 11, 1, 2, 0, 4, 256)
+    bb = BLOCK_BYTES[t]
+    x = rng.integers(-127, 128, size=256).astype(np.int8)
+    act = np.zeros(1, dtype=Q8K_DTYPE); act["qs"][0] = x; act["d"] = 1.0
+    for r in range(4):
+        blk = w[r * bb:(r + 1) * bb]
+        total = 0
+        for kb in range(8):
+            q, s, _ = ref.decode(t, blk, kb)
+            total += int(s[0]) * int(np.dot(q[:16], x[32 * kb:32 * kb + 16].astype(np.int64)))
+            total += int(s[1]) * int(np.dot(q[16:], x[32 * kb + 16:32 * kb + 32].astype(np.int64)))
+        assert orc.brute_block(t, blk, act) == total
+
+
+def test_dot_mutation_fails(orc):
+    # A changed sign index must change the integer (a pin that can fail).
+    act = orc.quantize(GOLD["dot_act_x"])
+    rows = GOLD["dot16_rows"].copy()
+    base = orc.block_partials(16, rows[1], act)
+    rows[1, 2 + 4] ^= 0x01       # flip one sign bit of sub-block 0, group 0
+    assert not np.array_equal(base, orc.block_partials(16, rows[1], act))
+
+
+# ---- SwiGLU and combine -----------------------------------------------------------
+def test_swiglu_golden(orc):
+    g, u = GOLD["swiglu_gu"]
+    for lim, key in ((0.0, "swiglu_y0"), (7.0, "swiglu_y7")):
+        got = np.array([orc.swiglu(a, b, lim) for a, b in zip(g, u)], np.float32)
+        assert np.array_equal(f32bits(got), f32bits(GOLD[key]))
+
+
+def test_combine_golden(orc):
+    i = 0
+    while f"comb{i}_ids" in GOLD:
+        got = orc.combine(GOLD[f"comb{i}_ids"], GOLD[f"comb{i}_w"], GOLD[f"comb{i}_rows"], GOLD[f"comb{i}_shared"])
+        assert np.array_equal(f32bits(got), f32bits(GOLD[f"comb{i}_out"])), i
+        i += 1
+    assert i >= 5
+
+
+def test_combine_order_matters(orc):
+    # Ascending-id order is observable: a reordering that keeps ids fixed gives
+    # identical bits, a different id order generally does not.
+    rng = np.random.default_rng(3)
+    rows = rng.standard_normal((6, 512)).astype(np.float32) * 1e3
+    w = rng.random(6).astype(np.float32)
+    ids = np.array([40, 3, 17, 200, 9, 100], np.int32)
+    a = orc.combine(ids, w, rows)
+    p = rng.permutation(6)
+    assert np.array_equal(f32bits(a), f32bits(orc.combine(ids[p], w[p], rows[p])))
+    sequential = np.zeros(512, np.float64)
+    out = np.zeros(512, np.float32)
+    for i in np.argsort(ids):
+        out = (w[i].astype(np.float64) * rows[i].astype(np.float64) + out.astype(np.float64)).astype(np.float32)
+    # float64 products of two floats are exact, so this is fma then one rounding.
+    assert np.array_equal(f32bits(a), f32bits(out))
+
+
+# ---- generator --------------------------------------------------------------------
+def test_generator_fields(orc):
+    for t in (16, 17, 29):
+        w = orc.gen_matrix(t, 2026, 4, 9, 0, 64, 1024).reshape(-1, BLOCK_BYTES[t])
+        if t == 29:
+            sc = w[:, 48:56].view(np.uint16)
+            d = ((sc[:, 0] >> 12) | ((sc[:, 1] >> 8) & 0xF0) | ((sc[:, 2] >> 4) & 0xF00) | (sc[:, 3] & 0xF000))
+        else:
+            d = w[:, 0:2].view(np.uint16)[:, 0]
+        dv = d.astype(np.uint16).view(np.float16).astype(np.float64)
+        assert dv.min() >= 1e-3 * (1 - 1e-3) and dv.max() <= 1e-2 * (1 + 1e-3)
+        assert 0.4 < (dv.mean() - 1e-3) / 9e-3 < 0.6
+        assert orc.gen_matrix(t, 2026, 4, 9, 0, 64, 1024).tobytes() == w.tobytes()  # pure function
+        assert orc.gen_matrix(t, 2027, 4, 9, 0, 64, 1024).tobytes() != w.tobytes()
+
+
+def test_codebook_self_consistency(orc):
+    for which, vals in ((0, (8, 25, 43)), (1, (8, 25, 43)), (2, (0xFF, 0x00, 0x01))):
+        cb = orc.codebook(which)
+        b = cb.view(np.uint8)
+        assert set(np.unique(b).tolist()) == set(vals)
+        assert len(np.unique(cb)) == cb.size   # distinct rows
+    ks = orc.ksigns()
+    for i in range(128):
+        assert ks[i] & 0x7F == i and bin(int(ks[i])).count("1") % 2 == 0

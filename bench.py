@@ -1,0 +1,178 @@
+#!/usr/bin/env python3
+"""Routed-expert benchmark on one MI355X.
+
+Workload: one MoE layer at decode batch 1, d_model 4096,
+d_ff 3072, 384 resident experts (gate/up IQ2_XXS, down IQ2_XS), top-6 of a
+softmax over seeded N(0,1) router logits with renormalized weights, fixed-order
+combine into a 4096-wide f32 output. A step is one layer call through the C ABI
+(xl_layer_forward_async) with routes, inputs and the bank already resident in
+HBM; every step uses a fresh seeded route so consecutive steps touch different
+experts (the bank is ~3.9 GB, far beyond the 256 MB MALL).
+
+Prints one JSON line: value = achieved algorithmic HBM GB/s of the layer
+(selected experts' weight bytes + x in + out, 60,784,640 B per layer), plus
+us_per_layer, the roofline of the dominant kernel (HIP events recorded inside
+the library around each kernel of the timed steps) and the CPU baseline (the
+reference's own q8k_core.hpp chain, compiled from the reference sources into
+oracle/_ref, timed on a bounded sample on the host cores).
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+DIM, FF, E, K = 4096, 3072, 384, 6
+GATE_T, DOWN_T = 16, 17
+BYTES = {16: 66, 17: 74, 29: 56}
+W_GU = FF * (DIM // 256) * BYTES[GATE_T]          # 3,244,032 B per gate/up matrix
+W_DN = DIM * (FF // 256) * BYTES[DOWN_T]          # 3,637,248 B per down matrix
+LAYER_BYTES = K * (2 * W_GU + W_DN) + 2 * DIM * 4  # 60,784,640 B
+# Algorithmic bytes of each kernel of the layer (weights + activations in/out).
+KERNEL_BYTES = {
+    "layer": LAYER_BYTES,   # the fused single-launch layer kernel
+    "q8k_x": DIM * 4 + DIM + DIM // 256 * 4,
+    "gate_up": 2 * K * W_GU + DIM + DIM // 256 * 4 + K * FF * 4,
+    "q8k_h": K * FF * 4 + K * FF + K * FF // 256 * 4,
+    "down": K * W_DN + K * FF + K * FF // 256 * 4 + K * DIM * 4,
+    "combine": K * DIM * 4 + 2 * K * 4 + DIM * 4,
+}
+HBM_PEAK_GBS = 8000.0
+SEED = 0x1A7E5
+
+
+def routes(n, seed):
+    rng = np.random.default_rng(seed)
+    ids = np.zeros((n, K), np.int32)
+    w = np.zeros((n, K), np.float32)
+    for i in range(n):
+        logits = rng.standard_normal(E).astype(np.float32)
+        p = np.exp(logits - logits.max()).astype(np.float64)
+        p /= p.sum()
+        top = np.argsort(-p, kind="stable")[:K]
+        ids[i] = top
+        w[i] = (p[top] / p[top].sum()).astype(np.float32)
+    x = rng.standard_normal((n, DIM)).astype(np.float32)
+    return ids, w, x
+
+
+def cpu_baseline(layers: int, threads: int):
+    """The reference's own CPU chain (oracle/_ref) on `layers` routed layers."""
+    from oracle.oracle import Oracle, Reference   # checker/baseline only
+    orc = Oracle()
+    kind = "reference" if Reference.available() else "port"
+    impl = Reference() if kind == "reference" else orc
+    ids, w, x = routes(layers, SEED + 1)
+    types = (GATE_T, GATE_T, DOWN_T)
+    elapsed = 0.0
+    for l in range(layers):
+        mats = [orc.gen_expert(types, SEED, 0, int(e), DIM, FF) for e in ids[l]]   # not timed
+        t0 = time.perf_counter()
+        rows = np.stack([impl.expert(types, *m, DIM, FF, x[l], threads=threads) for m in mats])
+        impl.combine(ids[l], w[l], rows, np.zeros(DIM, np.float32)) if kind == "reference" else \
+            orc.combine(ids[l], w[l], rows)
+        elapsed += time.perf_counter() - t0
+    us = elapsed / layers * 1e6
+    return {
+        "value": round(LAYER_BYTES / (us * 1e-6) / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": kind,
+        "us_per_layer": round(us, 1),
+        "sample": f"{layers} config-1 layers (6 experts + combine each), "
+                  f"{'reference q8k_core.hpp chain from oracle/_ref' if kind == 'reference' else 'oracle port'}, "
+                  f"{threads} threads, 64-row jobs",
+    }
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=2000)
+    ap.add_argument("--warmup", type=int, default=100)
+    ap.add_argument("--routes", type=int, default=512)
+    ap.add_argument("--cpu-layers", type=int, default=16)
+    ap.add_argument("--cpu-threads", type=int, default=0)
+    ap.add_argument("--no-cpu", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: this build measures one GPU only (asked for --gpus {args.gpus}); "
+              "the routed-expert path runs on a single MI355X holding the whole bank", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    import crosslane_amd as xl
+
+    types = np.zeros((1, E, 3), np.int32)
+    types[..., 0] = GATE_T; types[..., 1] = GATE_T; types[..., 2] = DOWN_T
+    lane = xl.Lane(DIM, FF, 1, E, types, max_picks=8)
+    lane.generate(SEED)
+    ids, w, x = routes(args.routes, SEED)
+    d_ids = torch.from_numpy(ids).cuda()
+    d_w = torch.from_numpy(w).cuda()
+    d_x = torch.from_numpy(x).cuda()
+    d_out = torch.zeros((args.routes, DIM), dtype=torch.float32, device="cuda")
+    stream = torch.cuda.current_stream()
+    sp = stream.cuda_stream
+
+    def step(i):
+        r = i % args.routes
+        lane.layer_forward_async(0, d_ids[r], d_w[r], d_x[r], d_out[r], stream=sp)
+
+    for i in range(args.warmup):
+        step(i)
+    torch.cuda.synchronize()
+    lane.profile_begin(args.steps)
+    t0 = torch.cuda.Event(enable_timing=True)
+    t1 = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    t0.record(stream)
+    wall0 = time.perf_counter()
+    for i in range(args.steps):
+        step(args.warmup + i)
+    t1.record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - wall0
+    prof = lane.profile_end()
+    lane.sync(sp)
+    ms = t0.elapsed_time(t1)
+    us_layer = ms * 1e3 / args.steps
+    gbs = LAYER_BYTES / (us_layer * 1e-6) / 1e9
+
+    stages = {k: v / prof["calls"] for k, v in prof["stages"].items()}   # ms per call
+    dom = max(stages, key=stages.get)
+    dom_us = stages[dom] * 1e3
+    achieved = KERNEL_BYTES[dom] / (dom_us * 1e-6) / 1e9
+
+    cpu = None
+    if not args.no_cpu:
+        threads = args.cpu_threads or min(16, os.cpu_count() or 1)
+        cpu = cpu_baseline(args.cpu_layers, threads)
+
+    line = {
+        "metric": "routed-expert µs/layer (top-6, batch 1) + achieved HBM GB/s vs MI355X peak",
+        "value": round(gbs, 2), "unit": "GB/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round(ms / args.steps, 6), "us_per_layer": round(us_layer, 3),
+        "hbm_frac": round(gbs / HBM_PEAK_GBS, 4),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "int8",
+        "data": "synthetic (seeded IQ blocks generated on device, N(0,1) activations and router logits)",
+        "config": {"workload": "config1: MoE layer, decode batch 1, top-6 of 384 resident experts, d_model 4096, "
+                               "d_ff 3072, gate/up IQ2_XXS + down IQ2_XS, fixed-order combine",
+                   "layer_bytes": LAYER_BYTES, "routes": args.routes},
+        "stages_us": {k: round(v * 1e3, 3) for k, v in stages.items()},
+        "roofline": {"bound": "hbm", "kernel": dom, "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "bytes_per_launch": KERNEL_BYTES[dom], "us_per_launch": round(dom_us, 3)},
+        "cpu_baseline": cpu,
+        "host_wall_us_per_step": round(wall * 1e6 / args.steps, 3),
+    }
+    print(json.dumps(line), flush=True)
+    lane.close()
+
+
+if __name__ == "__main__":
+    main()

@@ -84,7 +84,7 @@ int env_int(const char* name, int fallback) {
     if (!s || !*s) return fallback;
     char* end = nullptr;
     const long v = std::strtol(s, &end, 10);
-    if (*end || v < 1 || v > 1 << 20) fail(XL_E_ARG, "%s must be a positive integer", name);
+    if (*end || v < 0 || v > 1 << 20) fail(XL_E_ARG, "%s must be a non-negative integer", name);
     return int(v);
 }
 
@@ -101,7 +101,7 @@ struct xl_context {
     // workspace (one allocation, carved)
     void* ws = nullptr;
     uint64_t ws_bytes = 0;
-    uint2* tables = nullptr;
+    uint16_t* codes = nullptr;   // compact codebooks (2-bit symbols), expanded into LDS by the kernels
     int* err_flag = nullptr;
     float *x = nullptr, *xd = nullptr, *h = nullptr, *hd = nullptr, *g = nullptr, *u = nullptr, *y = nullptr;
     float *out = nullptr, *shared = nullptr, *w = nullptr, *mv_x = nullptr;
@@ -114,12 +114,42 @@ struct xl_context {
     std::vector<int32_t> types;
     std::vector<uint8_t*> slabs;
     std::vector<xl::ExpertDesc> descs;
+    std::vector<int> gu_mask, dn_mask;   // per layer: block types among gate/up and among down matrices
     xl::ExpertDesc* d_descs = nullptr;
     uint64_t payload = 0, allocated = 0;
     int grid_gu = 0, grid_down = 0;
+    bool fused = true;          // one cooperative launch per layer (XL_FUSED=0 selects separate launches)
+    uint32_t* sync = nullptr;   // counters of the fused layer kernel
+    // stage profiling (xl_profile_begin / xl_profile_end): events recorded
+    // around every kernel of the layer calls, on the stream they run on.
+    struct Prof {
+        bool on = false;
+        int max_calls = 0, calls = 0, stages = 0;
+        std::vector<hipEvent_t> ev;      // max_calls * (kMaxStages + 1)
+        std::vector<std::string> names;
+    } prof;
 };
 
 namespace {
+
+constexpr int kMaxStages = 8;
+
+// Stage marks: call mark(ctx, s, i) before stage i (i = 0) and after it.
+struct Marks {
+    xl_context* ctx;
+    hipStream_t s;
+    int slot = -1, n = 0;
+    Marks(xl_context* c, hipStream_t st) : ctx(c), s(st) {
+        if (ctx->prof.on && ctx->prof.calls < ctx->prof.max_calls) slot = ctx->prof.calls++;
+    }
+    void operator()(const char* name) {
+        if (slot < 0) return;
+        if (n > 0 && int(ctx->prof.names.size()) < n) ctx->prof.names.emplace_back(name);
+        if (n <= kMaxStages) hip_check(hipEventRecord(ctx->prof.ev[size_t(slot) * (kMaxStages + 1) + n], s), "event record");
+        if (n > ctx->prof.stages) ctx->prof.stages = n;
+        ++n;
+    }
+};
 
 void set_error(xl_context* ctx, xl_error* err, int32_t code, const char* msg) {
     xl_error e{};
@@ -170,8 +200,8 @@ void drain(xl_context* ctx, hipStream_t s) {
     int flag = 0;
     hip_check(hipMemcpy(&flag, ctx->err_flag, sizeof flag, hipMemcpyDeviceToHost), "error flag read");
     if (flag) {
-        fail(XL_E_DEVICE, "device error flag 0x%x (%s%s%s)", flag, (flag & xl::kDevErrExpertId) ? "expert id out of range " : "",
-             (flag & xl::kDevErrNonFinite) ? "non-finite activation " : "", (flag & xl::kDevErrType) ? "bad block type" : "");
+        fail(XL_E_DEVICE, "device error flag 0x%x (%s%s%s%s)", flag, (flag & xl::kDevErrExpertId) ? "expert id out of range " : "",
+             (flag & xl::kDevErrNonFinite) ? "non-finite activation " : "", (flag & xl::kDevErrType) ? "bad block type " : "", (flag & xl::kDevErrTimeout) ? "layer wait timeout" : "");
     }
 }
 
@@ -200,16 +230,39 @@ void enqueue_layer(xl_context* ctx, int32_t layer, const int32_t* d_ids, const f
                    float* u_dbg = nullptr) {
     const int dim = ctx->cfg.dim, ff = ctx->cfg.ff, E = ctx->cfg.n_experts;
     const xl::ExpertDesc* descs = ctx->d_descs + size_t(layer) * E;
+    const int gu_mask = ctx->gu_mask[size_t(layer)], dn_mask = ctx->dn_mask[size_t(layer)];
+    Marks mark(ctx, s);
+    mark("");
+    if (ctx->fused && !g_dbg && !u_dbg) {
+        xl::LayerArgs a{};
+        a.descs = descs; a.ids = d_ids; a.w = d_w; a.x = d_x; a.shared = d_shared; a.out = d_out;
+        a.k = k; a.n_experts = E; a.dim = dim; a.ff = ff;
+        a.xq = ctx->xq; a.xd = ctx->xd; a.h = ctx->h; a.hq = ctx->hq; a.hd = ctx->hd; a.y = ctx->y;
+        a.sync = ctx->sync; a.err = ctx->err_flag; a.codes = ctx->codes;
+        const hipError_t e = xl::dev::launch_layer_fused(a, gu_mask | dn_mask, ctx->cus, s);
+        if (e == hipSuccess) {
+            mark("layer");
+            return;
+        }
+        if (e != hipErrorNotSupported) hip_check(e, "fused layer launch");
+        (void)hipGetLastError();   // shape without a fused instance: separate launches below
+    }
     hip_check(xl::dev::launch_q8k(d_x, dim / 256, ctx->xq, ctx->xd, nullptr, ctx->err_flag, s), "Q8_K(x) launch");
-    hip_check(xl::dev::launch_gate_up(descs, d_ids, k, E, dim, ff, ctx->xq, ctx->xd, ctx->tables, ctx->h, g_dbg, u_dbg,
-                                      ctx->err_flag, ctx->grid_gu, s),
+    mark("q8k_x");
+    hip_check(xl::dev::launch_gate_up(descs, d_ids, k, E, dim, ff, ctx->xq, ctx->xd, ctx->codes, ctx->h, g_dbg, u_dbg,
+                                      ctx->err_flag, ctx->grid_gu, gu_mask, s),
               "gate/up launch");
+    mark("gate_up");
     hip_check(xl::dev::launch_q8k(ctx->h, k * ff / 256, ctx->hq, ctx->hd, nullptr, ctx->err_flag, s), "Q8_K(h) launch");
-    hip_check(xl::dev::launch_down(descs, d_ids, k, E, dim, ff, ctx->hq, ctx->hd, ctx->tables, ctx->y, ctx->err_flag,
-                                   ctx->grid_down, s),
+    mark("q8k_h");
+    hip_check(xl::dev::launch_down(descs, d_ids, k, E, dim, ff, ctx->hq, ctx->hd, ctx->codes, ctx->y, ctx->err_flag,
+                                   ctx->grid_down, dn_mask, s),
               "down launch");
-    if (d_out)
+    mark("down");
+    if (d_out) {
         hip_check(xl::dev::launch_combine(d_ids, d_w, k, ctx->y, dim, d_shared, d_out, s), "combine launch");
+        mark("combine");
+    }
 }
 
 }  // namespace
@@ -243,16 +296,17 @@ int32_t xl_open(uint32_t abi_version, const xl_config* cfg, xl_context** out, xl
         hip_check(hipGetDeviceProperties(&prop, cfg->device), "hipGetDeviceProperties");
         ctx->cus = prop.multiProcessorCount;
         hip_check(hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking), "hipStreamCreate");
-        ctx->grid_gu = env_int("XL_GRID_GATE_UP", 2 * ctx->cus);
-        ctx->grid_down = env_int("XL_GRID_DOWN", 2 * ctx->cus);
+        ctx->grid_gu = env_int("XL_WGS_GATE_UP", 4 * ctx->cus);
+        ctx->grid_down = env_int("XL_WGS_DOWN", 4 * ctx->cus);
 
         const int P = cfg->max_picks, dim = cfg->dim, ff = cfg->ff;
         ctx->act_max = std::max({dim, ff, 4096});
         struct Part { void** p; uint64_t bytes; };
-        const uint64_t tab_bytes = 2944 * 8;
+        const uint64_t code_bytes = (256 + 512 + 2048) * 2;
         std::vector<Part> parts = {
-            {reinterpret_cast<void**>(&ctx->tables), tab_bytes},
+            {reinterpret_cast<void**>(&ctx->codes), code_bytes},
             {reinterpret_cast<void**>(&ctx->err_flag), 256},
+            {reinterpret_cast<void**>(&ctx->sync), uint64_t(xl::kSyncWords) * 4},
             {reinterpret_cast<void**>(&ctx->x), uint64_t(dim) * 4},
             {reinterpret_cast<void**>(&ctx->xq), uint64_t(ctx->act_max)},
             {reinterpret_cast<void**>(&ctx->xd), uint64_t(ctx->act_max / 256) * 4},
@@ -278,9 +332,15 @@ int32_t xl_open(uint32_t abi_version, const xl_config* cfg, xl_context** out, xl
             *p.p = static_cast<uint8_t*>(ctx->ws) + at;
             at += xl::align256(p.bytes);
         }
-        const auto t = device_tables();
-        hip_check(hipMemcpy(ctx->tables, t.data(), tab_bytes, hipMemcpyHostToDevice), "table upload");
+        std::vector<uint16_t> codes;
+        codes.insert(codes.end(), kIq2xxsCodes, kIq2xxsCodes + 256);
+        codes.insert(codes.end(), kIq2xsCodes, kIq2xsCodes + 512);
+        codes.insert(codes.end(), kIq1sCodes, kIq1sCodes + 2048);
+        for (int i = 0; i < 256 + 512; ++i) (void)expand_codes(codes[size_t(i)], false);   // rejects a corrupt symbol
+        hip_check(hipMemcpy(ctx->codes, codes.data(), code_bytes, hipMemcpyHostToDevice), "codebook upload");
         hip_check(hipMemset(ctx->err_flag, 0, 256), "error flag clear");
+        hip_check(hipMemset(ctx->sync, 0, size_t(xl::kSyncWords) * 4), "counter clear");
+        ctx->fused = env_int("XL_FUSED", 0) != 0;   // cooperative single-launch layer: opt-in
         *out = ctx;
     });
     if (rc != XL_OK && ctx) xl_close(ctx);
@@ -315,6 +375,13 @@ int32_t xl_bank_create(xl_context* ctx, const int32_t* types, xl_error* err) {
         for (size_t e = 0; e < size_t(L) * E; ++e)
             need(types[3 * e] == types[3 * e + 1], XL_E_ARG, "gate and up must share a block type");
         ctx->types.assign(types, types + n);
+        ctx->gu_mask.assign(size_t(L), 0);
+        ctx->dn_mask.assign(size_t(L), 0);
+        for (int l = 0; l < L; ++l)
+            for (int e = 0; e < E; ++e) {
+                ctx->gu_mask[size_t(l)] |= xl::dev::type_bit(types[(size_t(l) * E + e) * 3]);
+                ctx->dn_mask[size_t(l)] |= xl::dev::type_bit(types[(size_t(l) * E + e) * 3 + 2]);
+            }
         ctx->descs.assign(size_t(L) * E, xl::ExpertDesc{});
         // One slab per layer, experts contiguous, each matrix's planes 256-B aligned.
         for (int l = 0; l < L; ++l) {
@@ -556,8 +623,53 @@ int32_t xl_matvec_async(xl_context* ctx, int32_t type, const void* d_planar, int
         m.off2 = P.off[2];
         m.type = type;
         m.nb = k / 256;
-        hip_check(xl::dev::launch_matvec(m, n, k, ctx->xq, ctx->xd, ctx->tables, d_y, d_partials, ctx->err_flag, s),
+        hip_check(xl::dev::launch_matvec(m, n, k, ctx->xq, ctx->xd, ctx->codes, d_y, d_partials, ctx->err_flag, s),
                   "matvec launch");
+    });
+}
+
+int32_t xl_profile_begin(xl_context* ctx, int32_t max_calls, xl_error* err) {
+    return guarded(ctx, err, [&] {
+        ready(ctx, false);
+        need(!ctx->prof.on, XL_E_STATE, "profiling already active");
+        need(max_calls >= 1 && max_calls <= 1 << 16, XL_E_ARG, "max_calls outside 1..65536");
+        auto& P = ctx->prof;
+        P = xl_context::Prof{};
+        P.ev.resize(size_t(max_calls) * (kMaxStages + 1), nullptr);
+        for (auto& e : P.ev) hip_check(hipEventCreate(&e), "hipEventCreate");
+        P.max_calls = max_calls;
+        P.on = true;
+    });
+}
+
+int32_t xl_profile_end(xl_context* ctx, float* stage_ms, int32_t max_stages, int32_t* n_stages, int32_t* n_calls,
+                       char* names, int32_t names_bytes, xl_error* err) {
+    return guarded(ctx, err, [&] {
+        need(ctx != nullptr && ctx->prof.on, XL_E_STATE, "profiling not active");
+        auto& P = ctx->prof;
+        struct Free {
+            xl_context::Prof& p;
+            ~Free() { for (auto& e : p.ev) if (e) (void)hipEventDestroy(e); p = xl_context::Prof{}; }
+        } release{P};
+        hip_check(hipSetDevice(ctx->cfg.device), "hipSetDevice");
+        const int S = std::min(P.stages, std::max(0, int(max_stages)));
+        for (int i = 0; i < S; ++i) stage_ms[i] = 0.0f;
+        for (int c = 0; c < P.calls; ++c) {
+            hip_check(hipEventSynchronize(P.ev[size_t(c) * (kMaxStages + 1) + S]), "event synchronize");
+            for (int i = 0; i < S; ++i) {
+                float ms = 0.0f;
+                hip_check(hipEventElapsedTime(&ms, P.ev[size_t(c) * (kMaxStages + 1) + i],
+                                              P.ev[size_t(c) * (kMaxStages + 1) + i + 1]), "event elapsed");
+                stage_ms[i] += ms;
+            }
+        }
+        if (n_stages) *n_stages = S;
+        if (n_calls) *n_calls = P.calls;
+        if (names && names_bytes > 0) {
+            std::string all;
+            for (int i = 0; i < S && i < int(P.names.size()); ++i) { if (i) all += ','; all += P.names[i]; }
+            std::snprintf(names, size_t(names_bytes), "%s", all.c_str());
+        }
     });
 }
 

@@ -85,9 +85,9 @@ XL_HD uint16_t iq1m_scale_bits(const uint8_t* sc8) {
 //
 // A matrix of n rows x k columns holds NB = n*(k/256) blocks. The AoS ggml
 // bytes are split into field planes, each row-major over [row][block]:
-//   IQ2_XXS: Q = 8 sub-blocks x 8 B (4 grid indices + u32 signs/scale)  64 B
+//   IQ2_XXS: Q = 8 sub-blocks x 8 B (4 grid indices + 4 sign/scale bytes) 64 B
 //            D = fp16 scale                                               2 B
-//   IQ2_XS : Q = 32 u16 codes (9-bit grid | 7-bit sign index)            64 B
+//   IQ2_XS : Q = 32 u16 codes (7-bit sign index | 9-bit grid << 7)      64 B
 //            S = 8 scale bytes                                            8 B
 //            D = fp16 scale                                               2 B
 //   IQ1_M  : Q = 32 low index bytes                                      32 B
@@ -120,16 +120,44 @@ XL_HD PlaneLayout plane_layout(int type, uint64_t nblocks) {
     return L;
 }
 
+// Field re-encodings applied by the repack (lossless, same byte count). They
+// put every codebook index of a group where one SDWA byte select reaches it:
+//   IQ2_XXS aux word: AoS {sign0..3 at bits 7g..7g+6, scale at 28..31} becomes
+//     four bytes, byte g = sign_g | (bit g of scale) << 7.
+//   IQ2_XS code u16: AoS {grid9 | sign7 << 9} becomes {sign7 | grid9 << 7}.
+// IQ1_M is stored as in ggml.
+XL_HD uint32_t xxs_aux_to_planar(uint32_t aux) {
+    uint32_t out = 0;
+    for (int g = 0; g < 4; ++g)
+        out |= (((aux >> (7 * g)) & 127u) | (((aux >> (28 + g)) & 1u) << 7)) << (8 * g);
+    return out;
+}
+XL_HD uint32_t xxs_aux_from_planar(uint32_t v) {
+    uint32_t out = 0;
+    for (int g = 0; g < 4; ++g) {
+        const uint32_t b = (v >> (8 * g)) & 255u;
+        out |= ((b & 127u) << (7 * g)) | ((b >> 7) << (28 + g));
+    }
+    return out;
+}
+XL_HD uint16_t xs_code_to_planar(uint16_t c) { return uint16_t((c >> 9) | ((c & 511u) << 7)); }
+XL_HD uint16_t xs_code_from_planar(uint16_t c) { return uint16_t(((c >> 7) & 511u) | ((c & 127u) << 9)); }
+XL_HD uint32_t rd32(const uint8_t* p) { return uint32_t(rd16(p)) | (uint32_t(rd16(p + 2)) << 16); }
+XL_HD void wr32(uint8_t* p, uint32_t v) { wr16(p, uint16_t(v)); wr16(p + 2, uint16_t(v >> 16)); }
+
 // Scatter one AoS block (index blk of the matrix) into the planes at base.
 XL_HD void block_to_planes(int type, const uint8_t* aos, uint8_t* base, const PlaneLayout& L, uint64_t blk) {
     uint8_t* q = base + L.off[0] + L.width[0] * blk;
     uint8_t* p1 = base + L.off[1] + L.width[1] * blk;
     uint8_t* p2 = base + L.off[2] + L.width[2] * blk;
     if (type == kIQ2_XXS) {
-        for (int i = 0; i < 64; ++i) q[i] = aos[2 + i];
+        for (int c = 0; c < 8; ++c) {
+            for (int i = 0; i < 4; ++i) q[8 * c + i] = aos[2 + 8 * c + i];
+            wr32(q + 8 * c + 4, xxs_aux_to_planar(rd32(aos + 6 + 8 * c)));
+        }
         p1[0] = aos[0]; p1[1] = aos[1];
     } else if (type == kIQ2_XS) {
-        for (int i = 0; i < 64; ++i) q[i] = aos[2 + i];
+        for (int i = 0; i < 32; ++i) wr16(q + 2 * i, xs_code_to_planar(rd16(aos + 2 + 2 * i)));
         for (int i = 0; i < 8; ++i) p1[i] = aos[66 + i];
         p2[0] = aos[0]; p2[1] = aos[1];
     } else {
@@ -145,10 +173,13 @@ XL_HD void planes_to_block(int type, const uint8_t* base, const PlaneLayout& L, 
     const uint8_t* p2 = base + L.off[2] + L.width[2] * blk;
     if (type == kIQ2_XXS) {
         aos[0] = p1[0]; aos[1] = p1[1];
-        for (int i = 0; i < 64; ++i) aos[2 + i] = q[i];
+        for (int c = 0; c < 8; ++c) {
+            for (int i = 0; i < 4; ++i) aos[2 + 8 * c + i] = q[8 * c + i];
+            wr32(aos + 6 + 8 * c, xxs_aux_from_planar(rd32(q + 8 * c + 4)));
+        }
     } else if (type == kIQ2_XS) {
         aos[0] = p2[0]; aos[1] = p2[1];
-        for (int i = 0; i < 64; ++i) aos[2 + i] = q[i];
+        for (int i = 0; i < 32; ++i) wr16(aos + 2 + 2 * i, xs_code_from_planar(rd16(q + 2 * i)));
         for (int i = 0; i < 8; ++i) aos[66 + i] = p1[i];
     } else {
         for (int i = 0; i < 32; ++i) aos[i] = q[i];

@@ -11,6 +11,7 @@ enum : int {
     kDevErrExpertId = 1,     // an id outside [0, n_experts)
     kDevErrNonFinite = 2,    // non-finite activation seen by a quantizer
     kDevErrType = 4,         // a matrix with an unsupported block type
+    kDevErrTimeout = 8,      // a bounded wait of the fused layer kernel expired
 };
 
 // One planar matrix (see plane_layout in xl_format.hpp).
@@ -41,18 +42,47 @@ inline bool row_shape(int k, int& lpr, int& ppl) {
     }
 }
 
+// Arguments of the fused layer kernel (device pointers).
+struct LayerArgs {
+    const ExpertDesc* descs;    // this layer's n_experts descriptors
+    const int32_t* ids;
+    const float* w;
+    const float* x;
+    const float* shared;        // may be null
+    float* out;
+    int k, n_experts, dim, ff;
+    int8_t* xq; float* xd;      // Q8_K(x), split form (qs, d)
+    float* h;                   // k * ff
+    int8_t* hq; float* hd;      // Q8_K(h), split form
+    float* y;                   // k * dim
+    uint32_t* sync;             // kSyncWords zeroed counters; the kernel re-zeroes them on exit
+    int* err;
+    const uint16_t* codes;
+    int need;                   // codebooks to expand (filled in by the launcher)
+    int per_g, per_d;           // row slots per wave (filled in by the launcher)
+};
+constexpr int kSyncWords = 256;
+
 namespace dev {
+// Fused layer: returns hipErrorNotSupported when (dim, ff) has no fused
+// instance or the device cannot hold the cooperative grid.
+hipError_t launch_layer_fused(const LayerArgs& args, int type_mask, int cus, hipStream_t s);
 hipError_t launch_q8k(const float* x, int nblocks, int8_t* qs, float* d, uint8_t* std_out, int* err, hipStream_t s);
-hipError_t launch_matvec(const MatRef& m, int n, int k, const int8_t* aq, const float* ad, const uint2* tables,
+// `codes` is the compact codebook buffer (2-bit symbols, see xl_rows.hpp);
+// `target_wgs` is the workgroup count the row launches aim for.
+hipError_t launch_matvec(const MatRef& m, int n, int k, const int8_t* aq, const float* ad, const uint16_t* codes,
                          float* y, int32_t* partials, int* err, hipStream_t s);
 // Gate/up + SwiGLU for k picks: h[i*ff + r] = silu(gate_i . x) * (up_i . x).
 hipError_t launch_gate_up(const ExpertDesc* descs, const int32_t* ids, int k, int n_experts, int dim, int ff,
-                          const int8_t* xq, const float* xd, const uint2* tables, float* h, float* g_dbg,
-                          float* u_dbg, int* err, int grid, hipStream_t s);
+                          const int8_t* xq, const float* xd, const uint16_t* codes, float* h, float* g_dbg,
+                          float* u_dbg, int* err, int target_wgs, int type_mask, hipStream_t s);
 // Down for k picks: y[i*dim + r] = down_i . Q8_K(h_i).
 hipError_t launch_down(const ExpertDesc* descs, const int32_t* ids, int k, int n_experts, int dim, int ff,
-                       const int8_t* hq, const float* hd, const uint2* tables, float* y, int* err, int grid,
-                       hipStream_t s);
+                       const int8_t* hq, const float* hd, const uint16_t* codes, float* y, int* err, int target_wgs,
+                       int type_mask, hipStream_t s);
+// type_mask bits (1 IQ2_XXS, 2 IQ2_XS, 4 IQ1_M): block types present among the
+// launch's matrices; sizes the LDS codebook region.
+int type_bit(int type);
 // Fixed-order combine: ascending id, out = fma(w, y, out), then + shared.
 hipError_t launch_combine(const int32_t* ids, const float* w, int k, const float* y, int dim, const float* shared,
                           float* out, hipStream_t s);

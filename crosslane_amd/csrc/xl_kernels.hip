@@ -1,50 +1,63 @@
 // CDNA4 (gfx950) kernels of the routed-expert lane.
 //
+//   layer_kernel    the whole routed-expert layer in one cooperative launch:
+//                   Q8_K(x), gate/up + SwiGLU of every pick, Q8_K(h), down,
+//                   fixed-order combine (the hot path)
 //   q8k_kernel      Q8_K activation quantization, bit-exact to the reference's
 //                   quant_block (engine/strata/sycl/stage/wiring/q8k_core.hpp:30-38)
 //   matvec_kernel   one IQ matrix x Q8_K vector (+ optional per-block int32
-//                   partials); the parity probe for the row core
-//   gate_up_kernel  gate and up rows of all picks + SwiGLU, one launch
-//   down_kernel     down rows of all picks, one launch
-//   combine_kernel  fixed-order weighted combine (engine/strata/warm/runtime.cpp:183-188)
+//                   partials); the parity probe for the row engine
+//   gate_up_kernel, down_kernel, combine_kernel
+//                   the same layer as separate launches (probe / fallback path)
 //   generate_kernel seeded planar bank fill
-//
-// Row core: a wave covers RPW = 64 / LPR rows at a time; lane l of a row group
-// owns pairs {l + LPR*j : j < PPL} (a pair = 2 sub-blocks = 64 weights = one
-// 16-byte load of the Q plane for IQ2 types). Its 64-byte activation slices stay
-// in VGPRs for every row the wave visits. Per-block integers are completed by a
-// quad DPP sum (the 4 pairs of a block sit in one quad), converted to float once,
-// scaled by fp16(d_w) * d_x and summed over the row group by DPP/swizzle.
-// Codebooks and sign masks live in LDS.
 //
 // Build with -ffp-contract=off: the quantizer and the combine rely on separately
 // rounded IEEE operations (explicit __f*_rn below as well).
 #include <hip/hip_runtime.h>
 
-#include "xl_decode.hpp"
 #include "xl_format.hpp"
 #include "xl_internal.hpp"
+#include "xl_rows.hpp"
 
 namespace xl::dev {
 
+int type_bit(int type) { return type == kIQ2_XXS ? 1 : type == kIQ2_XS ? 2 : type == kIQ1_M ? 4 : 0; }
+
 // ---------------------------------------------------------------------------
-// Q8_K quantization. One wave per 256-value block, lane l owns values 4l..4l+3.
-// The block maximum is the first value of largest magnitude (the reference's
-// strict '>' scan), found by an argmax that breaks ties toward the lower index.
+// Q8_K of one 256-value block by one wave (lane l owns values 4l..4l+3). The
+// block maximum is the first value of largest magnitude (the reference's strict
+// '>' scan), found by an argmax that breaks ties toward the lower index.
+// Writes the split form (qs, d) and optionally the 292-byte block.
 // ---------------------------------------------------------------------------
 __device__ __forceinline__ int nearest_i(float x) {
     const float v = __fadd_rn(x, 12582912.0f);   // q8k_core.hpp:25-29
     return int(__float_as_uint(v) & 0x007fffffu) - 0x00400000;
 }
 
-__global__ __launch_bounds__(256) void q8k_kernel(const float* __restrict__ x, int nblocks, int8_t* __restrict__ qs,
-                                                  float* __restrict__ dq, uint8_t* __restrict__ std_out,
-                                                  int* __restrict__ err) {
-    const int lane = threadIdx.x & 63;
-    const int b = blockIdx.x * 4 + (threadIdx.x >> 6);
-    if (b >= nblocks) return;
-    const float4 v4 = reinterpret_cast<const float4*>(x + size_t(b) * 256)[lane];
-    const float v[4] = {v4.x, v4.y, v4.z, v4.w};
+// Device-coherent 32-bit accesses for data exchanged between workgroups of one
+// launch (possibly on different XCDs): agent-scope relaxed atomics reach memory
+// past the XCD-private L2, so no cache writeback / invalidate is needed; an
+// s_waitcnt before the counter update orders them.
+__device__ __forceinline__ uint32_t coh_ld(const void* p) {
+    return __hip_atomic_load(reinterpret_cast<const uint32_t*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void coh_st(void* p, uint32_t v) {
+    __hip_atomic_store(reinterpret_cast<uint32_t*>(p), v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void coh_stf(float* p, float v) { coh_st(p, __float_as_uint(v)); }
+__device__ __forceinline__ void drain_memory() { __builtin_amdgcn_s_waitcnt(0); }
+
+template <bool COH = false>
+__device__ __forceinline__ void q8k_block(const float* __restrict__ x, int8_t* __restrict__ qs, float* __restrict__ dq,
+                                          uint8_t* __restrict__ std_out, int* __restrict__ err, int lane) {
+    float v[4];
+    if constexpr (COH) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) v[j] = __uint_as_float(coh_ld(x + 4 * lane + j));
+    } else {
+        const float4 v4 = reinterpret_cast<const float4*>(x)[lane];
+        v[0] = v4.x; v[1] = v4.y; v[2] = v4.z; v[3] = v4.w;
+    }
     float am = 0.0f, mx = 0.0f;
     int idx = 1 << 30;
     bool finite = true;
@@ -77,240 +90,159 @@ __global__ __launch_bounds__(256) void q8k_kernel(const float* __restrict__ x, i
         d = __fdiv_rn(1.0f, is);
     }
     bsum = quad_sum(bsum);
-    reinterpret_cast<uint32_t*>(qs + size_t(b) * 256)[lane] = packed;
-    if (lane == 0) dq[b] = d;
-    if (std_out) {
-        uint8_t* o = std_out + size_t(b) * 292;
-        if (lane == 0) *reinterpret_cast<float*>(o) = d;
-        reinterpret_cast<uint32_t*>(o + 4)[lane] = packed;
-        if ((lane & 3) == 0) reinterpret_cast<int16_t*>(o + 260)[lane >> 2] = int16_t(bsum);
-    }
-}
-
-// ---------------------------------------------------------------------------
-// Row core
-// ---------------------------------------------------------------------------
-template <int PPL>
-struct Act {
-    uint32_t a[PPL][16];   // 64 Q8_K bytes of each owned pair
-    float d[PPL];          // Q8_K scale of the pair's block
-    int s8[PPL][8];        // per-8 activation sums (IQ1_M delta term)
-};
-
-template <int LPR, int PPL>
-__device__ __forceinline__ void load_act(Act<PPL>& A, const int8_t* __restrict__ qs, const float* __restrict__ dq, int l) {
-#pragma unroll
-    for (int j = 0; j < PPL; ++j) {
-        const int p = l + LPR * j;
-        const uint4* src = reinterpret_cast<const uint4*>(qs + 64 * p);
-#pragma unroll
-        for (int c = 0; c < 4; ++c) {
-            const uint4 t = src[c];
-            A.a[j][4 * c + 0] = t.x; A.a[j][4 * c + 1] = t.y;
-            A.a[j][4 * c + 2] = t.z; A.a[j][4 * c + 3] = t.w;
-        }
-        A.d[j] = dq[p >> 2];
-#pragma unroll
-        for (int g = 0; g < 8; ++g) A.s8[j][g] = group_sum(A.a[j][2 * g], A.a[j][2 * g + 1]);
-    }
-}
-
-__device__ __forceinline__ uint4 ld16(const uint8_t* p) { return *reinterpret_cast<const uint4*>(p); }
-__device__ __forceinline__ uint2 ld8(const uint8_t* p) { return *reinterpret_cast<const uint2*>(p); }
-__device__ __forceinline__ uint32_t ld4(const uint8_t* p) { return *reinterpret_cast<const uint32_t*>(p); }
-__device__ __forceinline__ uint32_t ld2(const uint8_t* p) { return *reinterpret_cast<const uint16_t*>(p); }
-
-// Dot of one row against the activation slices. Returns the row value in every
-// lane of the row group. With PART, lane 4q of the group writes the per-block
-// integer(s) of its quad's block (IQ1_M: main, delta).
-template <int TYPE, int LPR, int PPL, bool PART>
-__device__ __forceinline__ float row_dot(const MatRef& m, int row, bool valid, int l, const Act<PPL>& A,
-                                         const uint2* tab, int32_t* __restrict__ partials) {
-    float acc = 0.0f, accd = 0.0f;
-#pragma unroll
-    for (int j = 0; j < PPL; ++j) {
-        const int p = l + LPR * j;
-        const uint64_t blk = uint64_t(row) * uint64_t(m.nb) + uint64_t(p >> 2);
-        const int pp = p & 3;
-        if constexpr (TYPE == kIQ2_XXS) {
-            uint4 w = make_uint4(0, 0, 0, 0);
-            uint32_t d16 = 0;
-            if (valid) { w = ld16(m.base + blk * 64 + pp * 16); d16 = ld2(m.base + m.off1 + blk * 2); }
-            const int I = quad_sum(pair_iq2xxs(tab, w, A.a[j]));
-            const float db = __fmul_rn(half_to_float(uint16_t(d16)), A.d[j]);
-            acc = fmaf(db, float(I), acc);
-            if constexpr (PART) if (valid && (l & 3) == 0) partials[blk] = I;
-        } else if constexpr (TYPE == kIQ2_XS) {
-            uint4 w = make_uint4(0, 0, 0, 0);
-            uint32_t sc = 0, d16 = 0;
-            if (valid) {
-                w = ld16(m.base + blk * 64 + pp * 16);
-                sc = ld2(m.base + m.off1 + blk * 8 + pp * 2);
-                d16 = ld2(m.base + m.off2 + blk * 2);
-            }
-            const int I = quad_sum(pair_iq2xs(tab, w, sc, A.a[j]));
-            const float db = __fmul_rn(half_to_float(uint16_t(d16)), A.d[j]);
-            acc = fmaf(db, float(I), acc);
-            if constexpr (PART) if (valid && (l & 3) == 0) partials[blk] = I;
-        } else {
-            uint2 q = make_uint2(0, 0), sw = make_uint2(0, 0);
-            uint32_t h = 0;
-            if (valid) {
-                q = ld8(m.base + blk * 32 + pp * 8);
-                h = ld4(m.base + m.off1 + blk * 16 + pp * 4);
-                sw = ld8(m.base + m.off2 + blk * 8);
-            }
-            const uint32_t scw = ((pp & 2) ? sw.y : sw.x) >> (16 * (pp & 1));
-            const int2 r = pair_iq1m(tab, q, h, scw, A.a[j], A.s8[j]);
-            const int im = quad_sum(r.x), id = quad_sum(r.y);
-            const uint16_t dh = uint16_t((sw.x >> 12) & 0xfu) | uint16_t((sw.x >> 24) & 0xf0u) |
-                                uint16_t((sw.y >> 4) & 0xf00u) | uint16_t((sw.y >> 16) & 0xf000u);
-            const float db = __fmul_rn(half_to_float(dh), A.d[j]);
-            acc = fmaf(db, float(im), acc);
-            accd = fmaf(db, float(id), accd);
-            if constexpr (PART) if (valid && (l & 3) == 0) { partials[2 * blk] = im; partials[2 * blk + 1] = id; }
-        }
-    }
-    const float tm = group_sum_quads<LPR>(acc);
-    if constexpr (TYPE == kIQ1_M) {
-        const float td = group_sum_quads<LPR>(accd);
-        return __fadd_rn(tm, __fmul_rn(0.125f, td));
+    if constexpr (COH) {
+        coh_st(qs + 4 * lane, packed);
+        if (lane == 0) coh_stf(dq, d);
     } else {
-        return __fmul_rn(0.125f, tm);
+        reinterpret_cast<uint32_t*>(qs)[lane] = packed;
+        if (lane == 0) *dq = d;
+    }
+    if (std_out) {
+        if (lane == 0) *reinterpret_cast<float*>(std_out) = d;
+        reinterpret_cast<uint32_t*>(std_out + 4)[lane] = packed;
+        if ((lane & 3) == 0) reinterpret_cast<int16_t*>(std_out + 260)[lane >> 2] = int16_t(bsum);
     }
 }
 
-template <int LPR, int PPL, bool PART>
-__device__ __forceinline__ float row_dot_any(const MatRef& m, int row, bool valid, int l, const Act<PPL>& A,
-                                             const uint2* tab, int32_t* partials, int* err) {
-    switch (m.type) {
-        case kIQ2_XXS: return row_dot<kIQ2_XXS, LPR, PPL, PART>(m, row, valid, l, A, tab, partials);
-        case kIQ2_XS: return row_dot<kIQ2_XS, LPR, PPL, PART>(m, row, valid, l, A, tab, partials);
-        case kIQ1_M: return row_dot<kIQ1_M, LPR, PPL, PART>(m, row, valid, l, A, tab, partials);
-        default:
-            if (l == 0) atomicOr(err, kDevErrType);
-            return 0.0f;
-    }
+__global__ __launch_bounds__(256) void q8k_kernel(const float* __restrict__ x, int nblocks, int8_t* __restrict__ qs,
+                                                  float* __restrict__ dq, uint8_t* __restrict__ std_out,
+                                                  int* __restrict__ err) {
+    const int b = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (b >= nblocks) return;   // wave-uniform
+    q8k_block<false>(x + size_t(b) * 256, qs + size_t(b) * 256, dq + b, std_out ? std_out + size_t(b) * 292 : nullptr, err,
+              threadIdx.x & 63);
 }
 
-__device__ __forceinline__ void load_tables(uint2* tab, const uint2* __restrict__ g) {
-    for (int i = threadIdx.x; i < kTabRows; i += blockDim.x) tab[i] = g[i];
-    __syncthreads();
-}
-
-// ---------------------------------------------------------------------------
-// Debug/probe matvec: one matrix, one Q8_K vector.
-// ---------------------------------------------------------------------------
-template <int LPR, int PPL, bool PART>
-__global__ __launch_bounds__(256) void matvec_kernel(MatRef m, int n, const int8_t* __restrict__ aq,
-                                                     const float* __restrict__ ad, const uint2* __restrict__ tables,
-                                                     float* __restrict__ y, int32_t* __restrict__ partials, int* err) {
-    __shared__ uint2 tab[kTabRows];
-    load_tables(tab, tables);
-    constexpr int RPW = 64 / LPR;
-    const int lane = threadIdx.x & 63, grp = lane / LPR, l = lane % LPR;
-    Act<PPL> A;
-    load_act<LPR, PPL>(A, aq, ad, l);
-    const int waves = gridDim.x * 4;
-    for (int s = blockIdx.x * 4 + (threadIdx.x >> 6); s * RPW < n; s += waves) {
-        const int row = s * RPW + grp;
-        const bool valid = row < n;
-        const float v = row_dot_any<LPR, PPL, PART>(m, row, valid, l, A, tab, partials, err);
-        if (valid && l == 0) y[row] = v;
-    }
-}
-
-// ---------------------------------------------------------------------------
-// Gate/up + SwiGLU for all picks in one launch. Work = k*ff rows flattened
-// (pick-major), split into contiguous per-wave ranges of row slots.
-// ---------------------------------------------------------------------------
 __device__ __forceinline__ float silu_mul(float g, float u) {
     // q8k_core.hpp:92-95 with limit 0: (g / (1 + exp(-g))) * u
     const float e = expf(-g);
     return __fmul_rn(__fdiv_rn(g, __fadd_rn(1.0f, e)), u);
 }
 
-template <int LPR, int PPL>
-__global__ __launch_bounds__(256) void gate_up_kernel(const ExpertDesc* __restrict__ descs,
-                                                      const int32_t* __restrict__ ids, int k, int n_experts, int ff,
-                                                      const int8_t* __restrict__ xq, const float* __restrict__ xd,
-                                                      const uint2* __restrict__ tables, float* __restrict__ h,
-                                                      float* __restrict__ g_dbg, float* __restrict__ u_dbg,
-                                                      int* __restrict__ err) {
-    __shared__ uint2 tab[kTabRows];
-    load_tables(tab, tables);
+// ---------------------------------------------------------------------------
+// Probe matvec: one matrix, one Q8_K vector, optional per-block partials.
+// ---------------------------------------------------------------------------
+template <int LPR, int PPL, bool PART>
+__global__ __launch_bounds__(256) void matvec_kernel(MatRef m, int n, const int8_t* __restrict__ aq,
+                                                     const float* __restrict__ ad, const uint16_t* __restrict__ codes,
+                                                     int need, float* __restrict__ y, int32_t* __restrict__ partials) {
+    extern __shared__ uint8_t lds[];
     constexpr int RPW = 64 / LPR;
     const int lane = threadIdx.x & 63, grp = lane / LPR, l = lane % LPR;
+    CodeRegs cr;
+    codes_prefetch(cr, codes, need, threadIdx.x);
+    Act<PPL> A;
+    load_act<LPR, PPL>(A, aq, ad, l);
+    codes_fill(lds, cr, need, threadIdx.x);
+    __syncthreads();
+    const int waves = gridDim.x * 4;
+    for (int s = blockIdx.x * 4 + (threadIdx.x >> 6); s * RPW < n; s += waves) {
+        const int row = s * RPW + grp;
+        const bool valid = row < n;
+        Raw<PPL> r;
+        if (valid) load_raw<LPR, PPL>(r, m.type, m, row, l); else zero_raw(r);
+        const float v = dot_raw<LPR, PPL, PART>(r, m.type, row, m.nb, l, A, lds, partials, valid);
+        if (valid && l == 0) y[row] = v;
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Separate-launch layer path: gate/up + SwiGLU, down, combine. Workgroup b
+// serves pick b / wgpp; each wave loads all of its (at most U) row slots before
+// the LDS codebook fill.
+// ---------------------------------------------------------------------------
+template <int LPR, int PPL, int U>
+__global__ __launch_bounds__(256) void gate_up_kernel(const ExpertDesc* __restrict__ descs,
+                                                      const int32_t* __restrict__ ids, int n_experts, int ff, int wgpp,
+                                                      const int8_t* __restrict__ xq, const float* __restrict__ xd,
+                                                      const uint16_t* __restrict__ codes, int need,
+                                                      float* __restrict__ h, float* __restrict__ g_dbg,
+                                                      float* __restrict__ u_dbg, int* __restrict__ err) {
+    extern __shared__ uint8_t lds[];
+    constexpr int RPW = 64 / LPR;
+    const int lane = threadIdx.x & 63, grp = lane / LPR, l = lane % LPR;
+    const int i = blockIdx.x / wgpp;
+    const int jw = (blockIdx.x - i * wgpp) * 4 + (threadIdx.x >> 6);
+    const int id = ids[i];
+    if (id < 0 || id >= n_experts) {   // workgroup-uniform: no barrier is skipped by part of the group
+        if (threadIdx.x == 0) atomicOr(err, kDevErrExpertId);
+        return;
+    }
+    const ExpertDesc& D = descs[id];
+    const int type = D.m[0].type;
+    const int slots = ff / RPW, per = (slots + 4 * wgpp - 1) / (4 * wgpp);
+    const int slot0 = jw * per, nslots = max(0, min(per, slots - slot0));
+    CodeRegs cr;
+    codes_prefetch(cr, codes, need, threadIdx.x);
     Act<PPL> A;
     load_act<LPR, PPL>(A, xq, xd, l);
-    const int slots_per_pick = ff / RPW, total = k * slots_per_pick;
-    const int waves = gridDim.x * 4, gw = blockIdx.x * 4 + (threadIdx.x >> 6);
-    const int per = (total + waves - 1) / waves;
-    const int first = gw * per, last = min(total, first + per);
-    for (int s = first; s < last; ++s) {
-        const int i = s / slots_per_pick;
-        const int row = (s - i * slots_per_pick) * RPW + grp;
-        const int id = ids[i];
-        if (id < 0 || id >= n_experts) {
-            if (lane == 0) atomicOr(err, kDevErrExpertId);
-            continue;
+    Raw<PPL> rg[U], ru[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+        if (u < nslots) {
+            load_raw<LPR, PPL>(rg[u], type, D.m[0], (slot0 + u) * RPW + grp, l);
+            load_raw<LPR, PPL>(ru[u], type, D.m[1], (slot0 + u) * RPW + grp, l);
         }
-        const ExpertDesc& D = descs[id];
-        const float g = row_dot_any<LPR, PPL, false>(D.m[0], row, true, l, A, tab, nullptr, err);
-        const float u = row_dot_any<LPR, PPL, false>(D.m[1], row, true, l, A, tab, nullptr, err);
-        if (l == 0) {
-            h[size_t(i) * ff + row] = silu_mul(g, u);
-            if (g_dbg) g_dbg[size_t(i) * ff + row] = g;
-            if (u_dbg) u_dbg[size_t(i) * ff + row] = u;
+    codes_fill(lds, cr, need, threadIdx.x);
+    __syncthreads();
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+        if (u < nslots) {
+            const int row = (slot0 + u) * RPW + grp;
+            const float g = dot_raw<LPR, PPL, false>(rg[u], type, row, D.m[0].nb, l, A, lds, nullptr, true);
+            const float v = dot_raw<LPR, PPL, false>(ru[u], type, row, D.m[1].nb, l, A, lds, nullptr, true);
+            if (l == 0) {
+                h[size_t(i) * ff + row] = silu_mul(g, v);
+                if (g_dbg) g_dbg[size_t(i) * ff + row] = g;
+                if (u_dbg) u_dbg[size_t(i) * ff + row] = v;
+            }
         }
-    }
 }
 
-// ---------------------------------------------------------------------------
-// Down rows of all picks in one launch; activation slices reload when the
-// wave's range crosses into the next pick.
-// ---------------------------------------------------------------------------
-template <int LPR, int PPL>
+template <int LPR, int PPL, int U>
 __global__ __launch_bounds__(256) void down_kernel(const ExpertDesc* __restrict__ descs, const int32_t* __restrict__ ids,
-                                                   int k, int n_experts, int dim, int ff, const int8_t* __restrict__ hq,
-                                                   const float* __restrict__ hd, const uint2* __restrict__ tables,
-                                                   float* __restrict__ y, int* __restrict__ err) {
-    __shared__ uint2 tab[kTabRows];
-    load_tables(tab, tables);
+                                                   int n_experts, int dim, int ff, int wgpp,
+                                                   const int8_t* __restrict__ hq, const float* __restrict__ hd,
+                                                   const uint16_t* __restrict__ codes, int need, float* __restrict__ y,
+                                                   int* __restrict__ err) {
+    extern __shared__ uint8_t lds[];
     constexpr int RPW = 64 / LPR;
     const int lane = threadIdx.x & 63, grp = lane / LPR, l = lane % LPR;
-    Act<PPL> A;
-    const int slots_per_pick = dim / RPW, total = k * slots_per_pick;
-    const int waves = gridDim.x * 4, gw = blockIdx.x * 4 + (threadIdx.x >> 6);
-    const int per = (total + waves - 1) / waves;
-    const int first = gw * per, last = min(total, first + per);
-    int cur = -1;
-    for (int s = first; s < last; ++s) {
-        const int i = s / slots_per_pick;
-        const int row = (s - i * slots_per_pick) * RPW + grp;
-        const int id = ids[i];
-        if (id < 0 || id >= n_experts) {
-            if (lane == 0) atomicOr(err, kDevErrExpertId);
-            continue;
-        }
-        if (i != cur) {
-            load_act<LPR, PPL>(A, hq + size_t(i) * ff, hd + size_t(i) * (ff / 256), l);
-            cur = i;
-        }
-        const float v = row_dot_any<LPR, PPL, false>(descs[id].m[2], row, true, l, A, tab, nullptr, err);
-        if (l == 0) y[size_t(i) * dim + row] = v;
+    const int i = blockIdx.x / wgpp;
+    const int jw = (blockIdx.x - i * wgpp) * 4 + (threadIdx.x >> 6);
+    const int id = ids[i];
+    if (id < 0 || id >= n_experts) {
+        if (threadIdx.x == 0) atomicOr(err, kDevErrExpertId);
+        return;
     }
+    const MatRef& M = descs[id].m[2];
+    const int type = M.type;
+    const int slots = dim / RPW, per = (slots + 4 * wgpp - 1) / (4 * wgpp);
+    const int slot0 = jw * per, nslots = max(0, min(per, slots - slot0));
+    CodeRegs cr;
+    codes_prefetch(cr, codes, need, threadIdx.x);
+    Act<PPL> A;
+    load_act<LPR, PPL>(A, hq + size_t(i) * ff, hd + size_t(i) * (ff / 256), l);
+    Raw<PPL> r[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+        if (u < nslots) load_raw<LPR, PPL>(r[u], type, M, (slot0 + u) * RPW + grp, l);
+    codes_fill(lds, cr, need, threadIdx.x);
+    __syncthreads();
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+        if (u < nslots) {
+            const int row = (slot0 + u) * RPW + grp;
+            const float v = dot_raw<LPR, PPL, false>(r[u], type, row, M.nb, l, A, lds, nullptr, true);
+            if (l == 0) y[size_t(i) * dim + row] = v;
+        }
 }
 
-// ---------------------------------------------------------------------------
-// Fixed-order combine (runtime.cpp:183-188): ascending expert id, sequential
-// fma starting from +0, then + shared. One thread per output coordinate.
-// ---------------------------------------------------------------------------
-__global__ __launch_bounds__(256) void combine_kernel(const int32_t* __restrict__ ids, const float* __restrict__ w,
-                                                      int k, const float* __restrict__ y, int dim,
-                                                      const float* __restrict__ shared, float* __restrict__ out) {
-    const int c = blockIdx.x * 256 + threadIdx.x;
-    if (c >= dim) return;
+// Fixed-order combine (runtime.cpp:183-188) of one output coordinate: ascending
+// expert id, out = fma(w, y, out) from +0, then + shared.
+template <bool COH = false>
+__device__ __forceinline__ float combine_one(const int32_t* ids, const float* w, int k, const float* y, int dim, int c,
+                                             const float* shared) {
     int order[16];
     for (int i = 0; i < k; ++i) order[i] = i;
     for (int i = 1; i < k; ++i)
@@ -318,9 +250,228 @@ __global__ __launch_bounds__(256) void combine_kernel(const int32_t* __restrict_
             const int t = order[j]; order[j] = order[j - 1]; order[j - 1] = t;
         }
     float acc = 0.0f;
-    for (int t = 0; t < k; ++t) acc = fmaf(w[order[t]], y[size_t(order[t]) * dim + c], acc);
+    for (int t = 0; t < k; ++t) {
+        const float* p = y + size_t(order[t]) * dim + c;
+        acc = fmaf(w[order[t]], COH ? __uint_as_float(coh_ld(p)) : *p, acc);
+    }
     if (shared) acc = __fadd_rn(acc, shared[c]);
-    out[c] = acc;
+    return acc;
+}
+
+__global__ __launch_bounds__(256) void combine_kernel(const int32_t* __restrict__ ids, const float* __restrict__ w,
+                                                      int k, const float* __restrict__ y, int dim,
+                                                      const float* __restrict__ shared, float* __restrict__ out) {
+    const int c = blockIdx.x * 256 + threadIdx.x;
+    if (c < dim) out[c] = combine_one<false>(ids, w, k, y, dim, c, shared);
+}
+
+// ---------------------------------------------------------------------------
+// The fused layer kernel.
+//
+// Every wave owns a contiguous range of gate/up row slots (pick-major over
+// k * ff rows) and of down row slots (over k * dim rows). It issues the loads
+// of its first batch of each before anything waits, fills the LDS codebooks,
+// then works through the dependency chain:
+//   x ready    workgroup 0 quantizes x into (xq, xd) and raises sync[kSyncX]
+//   gate/up    rows -> h (f32); each wave adds its row count to sync[kSyncGu + i]
+//   Q8_K(h)    wave q < k*ff/256 quantizes block q once pick i's gate/up rows
+//              are all in, then adds 1 to sync[kSyncHq + i]
+//   down       rows of pick i once all its h blocks are in -> y (f32)
+//   combine    the wave whose row count completes a 64-row chunk (all picks)
+//              combines that chunk into out
+//   exit       the last workgroup zeroes every counter for the next launch
+// Waits only point backwards in this chain and the launch is cooperative (all
+// workgroups resident), so it cannot deadlock; every spin is bounded and raises
+// kDevErrTimeout instead of hanging. Device-scope fences order the data
+// written before a counter add against the reads after the matching wait.
+// ---------------------------------------------------------------------------
+constexpr int kSyncX = 0, kSyncExit = 1, kSyncGu = 2, kSyncHq = 18, kSyncChunk = 34;
+constexpr uint32_t kSpinLimit = 1u << 20;   // polls of ~1 us: about a second, far beyond any legal wait
+
+__device__ __forceinline__ uint32_t ld_relaxed(const uint32_t* p) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ uint32_t add_relaxed(uint32_t* p, uint32_t v) {
+    return __hip_atomic_fetch_add(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+// Wave-uniform bounded wait for *p >= target. The data it guards is read with
+// coh_ld after the wait, so no cache invalidation is needed.
+__device__ bool wait_geq(const uint32_t* p, uint32_t target, int* err) {
+    uint32_t spins = 0;
+    while (ld_relaxed(p) < target) {
+        __builtin_amdgcn_s_sleep(1);
+        if (++spins > kSpinLimit) {
+            if ((threadIdx.x & 63) == 0) atomicOr(err, kDevErrTimeout);
+            return false;
+        }
+    }
+    return true;
+}
+
+template <int LG, int PG, int UG, int LD, int PD, int UD>
+__global__ __launch_bounds__(256) void layer_kernel(LayerArgs a) {
+    extern __shared__ uint8_t lds[];
+    constexpr int RG = 64 / LG, RD = 64 / LD;
+    const int t = threadIdx.x, lane = t & 63, wv = t >> 6;
+    const int gw = blockIdx.x * 4 + wv;
+    const int grpG = lane / LG, lG = lane % LG, grpD = lane / LD, lD = lane % LD;
+
+    CodeRegs cr;
+    codes_prefetch(cr, a.codes, a.need, t);
+
+    // ---- gate/up slots of this wave; the first batch is loaded now
+    const int sppG = a.ff / RG, SG = a.k * sppG;
+    const int g0 = gw * a.per_g, gn = max(0, min(a.per_g, SG - g0));
+    Raw<PG> rg[UG], ru[UG];
+    auto g_slot = [&](int s, int& i, int& row, const ExpertDesc*& D) -> bool {
+        i = s / sppG;
+        row = (s - i * sppG) * RG + grpG;
+        const int id = a.ids[i];
+        if (id < 0 || id >= a.n_experts) return false;
+        D = a.descs + id;
+        return true;
+    };
+    auto g_load = [&](int first) {
+#pragma unroll
+        for (int u = 0; u < UG; ++u)
+            if (first + u < gn) {
+                int i, row;
+                const ExpertDesc* D;
+                if (g_slot(g0 + first + u, i, row, D)) {
+                    load_raw<LG, PG>(rg[u], D->m[0].type, D->m[0], row, lG);
+                    load_raw<LG, PG>(ru[u], D->m[1].type, D->m[1], row, lG);
+                }
+            }
+    };
+    g_load(0);
+
+    // ---- down slots; the first batch is loaded now
+    const int sppD = a.dim / RD, SD = a.k * sppD;
+    const int d0 = gw * a.per_d, dn = max(0, min(a.per_d, SD - d0));
+    Raw<PD> rd[UD];
+    auto d_slot = [&](int s, int& i, int& row, const ExpertDesc*& D) -> bool {
+        i = s / sppD;
+        row = (s - i * sppD) * RD + grpD;
+        const int id = a.ids[i];
+        if (id < 0 || id >= a.n_experts) return false;
+        D = a.descs + id;
+        return true;
+    };
+    auto d_load = [&](int first) {
+#pragma unroll
+        for (int u = 0; u < UD; ++u)
+            if (first + u < dn) {
+                int i, row;
+                const ExpertDesc* D;
+                if (d_slot(d0 + first + u, i, row, D)) load_raw<LD, PD>(rd[u], D->m[2].type, D->m[2], row, lD);
+            }
+    };
+    d_load(0);
+
+    codes_fill(lds, cr, a.need, t);
+    __syncthreads();
+
+    // ---- Q8_K(x) by workgroup 0
+    if (blockIdx.x == 0) {
+        for (int b = wv; b < a.dim / 256; b += 4)
+            q8k_block<true>(a.x + 256 * b, a.xq + 256 * b, a.xd + b, nullptr, a.err, lane);
+        drain_memory();
+        __syncthreads();
+        if (t == 0) add_relaxed(a.sync + kSyncX, 1);
+    }
+    if (gw < a.k && lane == 0) {   // every bad id is reported once
+        const int id = a.ids[gw];
+        if (id < 0 || id >= a.n_experts) atomicOr(a.err, kDevErrExpertId);
+    }
+
+    // ---- gate/up + SwiGLU
+    if (gn > 0) {
+        wait_geq(a.sync + kSyncX, 1, a.err);
+        Act<PG> A;
+        load_act<LG, PG, true>(A, a.xq, a.xd, lG);
+        for (int first = 0; first < gn; first += UG) {
+            if (first > 0) g_load(first);
+#pragma unroll
+            for (int u = 0; u < UG; ++u)
+                if (first + u < gn) {
+                    int i, row;
+                    const ExpertDesc* D;
+                    if (!g_slot(g0 + first + u, i, row, D)) continue;
+                    const int type = D->m[0].type;
+                    const float g = dot_raw<LG, PG, false>(rg[u], type, row, D->m[0].nb, lG, A, lds, nullptr, true);
+                    const float v = dot_raw<LG, PG, false>(ru[u], type, row, D->m[1].nb, lG, A, lds, nullptr, true);
+                    if (lG == 0) coh_stf(a.h + size_t(i) * a.ff + row, silu_mul(g, v));
+                }
+        }
+        // publish rows per pick (a wave's range spans at most a few picks)
+        drain_memory();
+        if (lane == 0) {
+            int s = g0;
+            while (s < g0 + gn) {
+                const int i = s / sppG;
+                const int end = min(g0 + gn, (i + 1) * sppG);
+                add_relaxed(a.sync + kSyncGu + i, uint32_t((end - s) * RG));
+                s = end;
+            }
+        }
+    }
+
+    // ---- Q8_K(h): one block per wave for the first k*ff/256 waves
+    const int hblocks = a.ff / 256;
+    if (gw < a.k * hblocks) {
+        const int i = gw / hblocks, b = gw - i * hblocks;
+        wait_geq(a.sync + kSyncGu + i, uint32_t(a.ff), a.err);
+        const size_t o = size_t(i) * a.ff + 256 * b;
+        q8k_block<true>(a.h + o, a.hq + o, a.hd + size_t(i) * hblocks + b, nullptr, a.err, lane);
+        drain_memory();
+        if (lane == 0) add_relaxed(a.sync + kSyncHq + i, 1);
+    }
+
+    // ---- down
+    if (dn > 0) {
+        Act<PD> B;
+        int cur = -1;
+        for (int first = 0; first < dn; first += UD) {
+            if (first > 0) d_load(first);
+#pragma unroll
+            for (int u = 0; u < UD; ++u)
+                if (first + u < dn) {
+                    int i, row;
+                    const ExpertDesc* D;
+                    if (!d_slot(d0 + first + u, i, row, D)) continue;
+                    if (i != cur) {
+                        wait_geq(a.sync + kSyncHq + i, uint32_t(hblocks), a.err);
+                        load_act<LD, PD, true>(B, a.hq + size_t(i) * a.ff, a.hd + size_t(i) * hblocks, lD);
+                        cur = i;
+                    }
+                    const float v =
+                        dot_raw<LD, PD, false>(rd[u], D->m[2].type, row, D->m[2].nb, lD, B, lds, nullptr, true);
+                    if (lD == 0) coh_stf(a.y + size_t(i) * a.dim + row, v);
+                }
+        }
+        // publish per 64-row chunk; the wave completing a chunk combines it
+        drain_memory();
+        for (int u = 0; u < dn; ++u) {
+            const int s = d0 + u, i = s / sppD, row0 = (s - i * sppD) * RD, c = row0 >> 6;
+            uint32_t old = 0;
+            if (lane == 0) old = add_relaxed(a.sync + kSyncChunk + c, uint32_t(RD));
+            old = __shfl(old, 0);
+            if (old + uint32_t(RD) == uint32_t(a.k * 64)) {
+                const int r = 64 * c + lane;
+                if (a.out) a.out[r] = combine_one<true>(a.ids, a.w, a.k, a.y, a.dim, r, a.shared);
+            }
+        }
+    }
+
+    // ---- exit: the last workgroup zeroes the counters for the next launch
+    __syncthreads();
+    if (t == 0) {
+        const uint32_t old = add_relaxed(a.sync + kSyncExit, 1);
+        if (old == gridDim.x - 1) {   // every other workgroup has finished with the counters
+            const int n = kSyncChunk + a.dim / 64;
+            for (int j = 0; j < n; ++j) __hip_atomic_store(a.sync + j, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+    }
 }
 
 // ---------------------------------------------------------------------------
@@ -339,7 +490,18 @@ __global__ __launch_bounds__(256) void generate_kernel(uint8_t* __restrict__ bas
     if (type == kIQ2_XXS || type == kIQ2_XS) {
         uint64_t* q = reinterpret_cast<uint64_t*>(base + blk * 64);
 #pragma unroll
-        for (int j = 0; j < 8; ++j) q[j] = shift_pair(w[j], w[j + 1]);
+        for (int j = 0; j < 8; ++j) {
+            const uint64_t v = shift_pair(w[j], w[j + 1]);   // AoS bytes 2+8j .. 9+8j
+            uint64_t o;
+            if (type == kIQ2_XXS) {
+                o = (v & 0xffffffffull) | (uint64_t(xxs_aux_to_planar(uint32_t(v >> 32))) << 32);
+            } else {
+                o = 0;
+#pragma unroll
+                for (int c = 0; c < 4; ++c) o |= uint64_t(xs_code_to_planar(uint16_t(v >> (16 * c)))) << (16 * c);
+            }
+            q[j] = o;
+        }
         if (type == kIQ2_XXS) {
             *reinterpret_cast<uint16_t*>(base + off1 + blk * 2) = d;
         } else {
@@ -365,26 +527,33 @@ __global__ __launch_bounds__(256) void generate_kernel(uint8_t* __restrict__ bas
 // ---------------------------------------------------------------------------
 #define XL_SHAPES(X) X(4, 1) X(8, 1) X(4, 3) X(16, 1) X(32, 1) X(16, 3) X(64, 1)
 
+static int need_of(int type_mask) {
+    return ((type_mask & 1) ? kNeedXXS : 0) | ((type_mask & 2) ? kNeedXS : 0) | ((type_mask & 4) ? kNeedIQ1 : 0);
+}
+
 hipError_t launch_q8k(const float* x, int nblocks, int8_t* qs, float* d, uint8_t* std_out, int* err, hipStream_t s) {
     if (nblocks <= 0) return hipSuccess;
     hipLaunchKernelGGL(q8k_kernel, dim3((nblocks + 3) / 4), dim3(256), 0, s, x, nblocks, qs, d, std_out, err);
     return hipGetLastError();
 }
 
-hipError_t launch_matvec(const MatRef& m, int n, int k, const int8_t* aq, const float* ad, const uint2* tables,
+hipError_t launch_matvec(const MatRef& m, int n, int k, const int8_t* aq, const float* ad, const uint16_t* codes,
                          float* y, int32_t* partials, int* err, hipStream_t s) {
+    (void)err;
     int lpr, ppl;
-    if (!row_shape(k, lpr, ppl) || n <= 0) return hipErrorInvalidValue;
+    if (!row_shape(k, lpr, ppl) || n <= 0 || !supported_type(m.type)) return hipErrorInvalidValue;
     const int rpw = 64 / lpr, slots = (n + rpw - 1) / rpw;
     const int grid = (slots + 3) / 4 < 1024 ? (slots + 3) / 4 : 1024;
+    const int need = need_of(type_bit(m.type)) | (partials && m.type == kIQ1_M ? kNeedPlain : 0);
+    const size_t lds = size_t(lds_bytes_for(need));
 #define XL_MV(L, P)                                                                                                   \
     if (lpr == L && ppl == P) {                                                                                       \
         if (partials)                                                                                                 \
-            hipLaunchKernelGGL((matvec_kernel<L, P, true>), dim3(grid), dim3(256), 0, s, m, n, aq, ad, tables, y,     \
-                               partials, err);                                                                        \
+            hipLaunchKernelGGL((matvec_kernel<L, P, true>), dim3(grid), dim3(256), lds, s, m, n, aq, ad, codes, need, \
+                               y, partials);                                                                          \
         else                                                                                                          \
-            hipLaunchKernelGGL((matvec_kernel<L, P, false>), dim3(grid), dim3(256), 0, s, m, n, aq, ad, tables, y,    \
-                               partials, err);                                                                        \
+            hipLaunchKernelGGL((matvec_kernel<L, P, false>), dim3(grid), dim3(256), lds, s, m, n, aq, ad, codes,      \
+                               need, y, partials);                                                                    \
         return hipGetLastError();                                                                                     \
     }
     XL_SHAPES(XL_MV)
@@ -392,15 +561,29 @@ hipError_t launch_matvec(const MatRef& m, int n, int k, const int8_t* aq, const 
     return hipErrorInvalidValue;
 }
 
+// Workgroups per pick: enough that no wave owns more than U row slots, and at
+// least target_wgs / k so the launch fills the device.
+static int wg_per_pick(int slots, int umax, int k, int target_wgs) {
+    const int need = (slots + 4 * umax - 1) / (4 * umax);
+    const int fill = (target_wgs + k - 1) / k;
+    const int cap = (slots + 3) / 4;
+    int w = need > fill ? need : fill;
+    return w < cap ? w : (need > cap ? need : cap);
+}
+
 hipError_t launch_gate_up(const ExpertDesc* descs, const int32_t* ids, int k, int n_experts, int dim, int ff,
-                          const int8_t* xq, const float* xd, const uint2* tables, float* h, float* g_dbg, float* u_dbg,
-                          int* err, int grid, hipStream_t s) {
+                          const int8_t* xq, const float* xd, const uint16_t* codes, float* h, float* g_dbg,
+                          float* u_dbg, int* err, int target_wgs, int type_mask, hipStream_t s) {
     int lpr, ppl;
-    if (!row_shape(dim, lpr, ppl)) return hipErrorInvalidValue;
+    if (!row_shape(dim, lpr, ppl) || k <= 0) return hipErrorInvalidValue;
+    constexpr int U = 4;
+    const int wgpp = wg_per_pick(ff / (64 / lpr), U, k, target_wgs);
+    const int need = need_of(type_mask);
+    const size_t lds = size_t(lds_bytes_for(need));
 #define XL_GU(L, P)                                                                                                   \
     if (lpr == L && ppl == P) {                                                                                       \
-        hipLaunchKernelGGL((gate_up_kernel<L, P>), dim3(grid), dim3(256), 0, s, descs, ids, k, n_experts, ff, xq, xd, \
-                           tables, h, g_dbg, u_dbg, err);                                                             \
+        hipLaunchKernelGGL((gate_up_kernel<L, P, U>), dim3(k * wgpp), dim3(256), lds, s, descs, ids, n_experts, ff,   \
+                           wgpp, xq, xd, codes, need, h, g_dbg, u_dbg, err);                                          \
         return hipGetLastError();                                                                                     \
     }
     XL_SHAPES(XL_GU)
@@ -409,14 +592,18 @@ hipError_t launch_gate_up(const ExpertDesc* descs, const int32_t* ids, int k, in
 }
 
 hipError_t launch_down(const ExpertDesc* descs, const int32_t* ids, int k, int n_experts, int dim, int ff,
-                       const int8_t* hq, const float* hd, const uint2* tables, float* y, int* err, int grid,
-                       hipStream_t s) {
+                       const int8_t* hq, const float* hd, const uint16_t* codes, float* y, int* err, int target_wgs,
+                       int type_mask, hipStream_t s) {
     int lpr, ppl;
-    if (!row_shape(ff, lpr, ppl)) return hipErrorInvalidValue;
+    if (!row_shape(ff, lpr, ppl) || k <= 0) return hipErrorInvalidValue;
+    constexpr int U = 2;
+    const int wgpp = wg_per_pick(dim / (64 / lpr), U, k, target_wgs);
+    const int need = need_of(type_mask);
+    const size_t lds = size_t(lds_bytes_for(need));
 #define XL_DN(L, P)                                                                                                   \
     if (lpr == L && ppl == P) {                                                                                       \
-        hipLaunchKernelGGL((down_kernel<L, P>), dim3(grid), dim3(256), 0, s, descs, ids, k, n_experts, dim, ff, hq,   \
-                           hd, tables, y, err);                                                                       \
+        hipLaunchKernelGGL((down_kernel<L, P, U>), dim3(k * wgpp), dim3(256), lds, s, descs, ids, n_experts, dim, ff, \
+                           wgpp, hq, hd, codes, need, y, err);                                                        \
         return hipGetLastError();                                                                                     \
     }
     XL_SHAPES(XL_DN)
@@ -440,6 +627,41 @@ hipError_t launch_generate(uint8_t* base, int type, int n, int k, uint64_t seed,
     hipLaunchKernelGGL(generate_kernel, dim3(unsigned(grid)), dim3(256), 0, s, base, type, nblocks, L.off[1], L.off[2],
                        key);
     return hipGetLastError();
+}
+
+// One cooperative launch of the fused layer: the grid is every workgroup the
+// device holds at once (occupancy x CUs), so all of them are resident.
+template <int LG, int PG, int UG, int LD, int PD, int UD>
+static hipError_t fused_launch(const LayerArgs& args, int cus, hipStream_t s) {
+    auto kern = layer_kernel<LG, PG, UG, LD, PD, UD>;
+    const size_t lds = size_t(lds_bytes_for(args.need));
+    int per_cu = 0;
+    hipError_t e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kern, 256, lds);
+    if (e != hipSuccess) return e;
+    if (per_cu < 1) return hipErrorNotSupported;
+    LayerArgs a = args;
+    const int grid = cus * per_cu, waves = grid * 4;
+    const int SG = a.k * (a.ff / (64 / LG)), SD = a.k * (a.dim / (64 / LD));
+    a.per_g = (SG + waves - 1) / waves;
+    a.per_d = (SD + waves - 1) / waves;
+    if (a.k * (a.ff / 256) > waves || a.k < 1 || a.k > 16 || a.dim / 64 + 34 > kSyncWords) return hipErrorNotSupported;
+    void* params[] = {&a};
+    e = hipLaunchCooperativeKernel(reinterpret_cast<const void*>(kern), dim3(grid), dim3(256), params,
+                                   static_cast<unsigned int>(lds), s);
+    return e;
+}
+
+hipError_t launch_layer_fused(const LayerArgs& args, int type_mask, int cus, hipStream_t s) {
+    LayerArgs a = args;
+    a.need = need_of(type_mask);
+    int lg, pg, ld, pd;
+    if (!row_shape(a.dim, lg, pg) || !row_shape(a.ff, ld, pd)) return hipErrorNotSupported;
+    if (lg == 64 && pg == 1 && ld == 16 && pd == 3) return fused_launch<64, 1, 4, 16, 3, 1>(a, cus, s);   // 4096 x 3072
+    if (lg == 4 && pg == 1 && ld == 4 && pd == 1) return fused_launch<4, 1, 4, 4, 1, 2>(a, cus, s);       // 256 x 256
+    if (lg == 8 && pg == 1 && ld == 4 && pd == 1) return fused_launch<8, 1, 4, 4, 1, 2>(a, cus, s);       // 512 x 256
+    if (lg == 4 && pg == 1 && ld == 4 && pd == 3) return fused_launch<4, 1, 4, 4, 3, 2>(a, cus, s);       // 256 x 768
+    if (lg == 16 && pg == 1 && ld == 8 && pd == 1) return fused_launch<16, 1, 4, 8, 1, 2>(a, cus, s);     // 1024 x 512
+    return hipErrorNotSupported;
 }
 
 }  // namespace xl::dev

@@ -76,6 +76,8 @@ _SIGNATURES = {
     "xl_sync": (_I32, [_P, _P, _ErrP]),
     "xl_quantize_q8k_async": (_I32, [_P, _P, _I32, _I32, _P, _P, _ErrP]),
     "xl_matvec_async": (_I32, [_P, _I32, _P, _I32, _I32, _P, _P, _P, _P, _ErrP]),
+    "xl_profile_begin": (_I32, [_P, _I32, _ErrP]),
+    "xl_profile_end": (_I32, [_P, _f32p, _I32, C.POINTER(_I32), C.POINTER(_I32), C.c_char_p, _I32, _ErrP]),
     "xl_planar_bytes": (C.c_uint64, [_I32, _I32, _I32]),
     "xl_repack": (_I32, [_I32, _I32, _I32, _P, _P]),
     "xl_restore": (_I32, [_I32, _I32, _I32, _P, _P]),
@@ -258,6 +260,18 @@ class Lane:
 
     def sync(self, stream=None) -> None:
         self._call("xl_sync", None if stream is None else int(stream))
+
+    def profile_begin(self, max_calls: int) -> None:
+        self._call("xl_profile_begin", max_calls)
+
+    def profile_end(self) -> dict:
+        """Per-stage total milliseconds over the profiled calls: {name: ms}, calls."""
+        ms = np.zeros(8, np.float32)
+        ns, nc = _I32(), _I32()
+        names = C.create_string_buffer(256)
+        self._call("xl_profile_end", ms, 8, C.byref(ns), C.byref(nc), names, 256)
+        keys = names.value.decode().split(",") if ns.value else []
+        return {"calls": nc.value, "stages": {k: float(ms[i]) for i, k in enumerate(keys)}}
 
     def quantize_q8k_async(self, x, rows: int, k: int, q8k_out, stream=None) -> None:
         self._call("xl_quantize_q8k_async", _ptr(x), rows, k, _ptr(q8k_out), None if stream is None else int(stream))

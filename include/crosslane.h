@@ -131,6 +131,16 @@ int32_t xl_quantize_q8k_async(xl_context* ctx, const float* d_x, int32_t rows, i
 int32_t xl_matvec_async(xl_context* ctx, int32_t type, const void* d_planar, int32_t n, int32_t k, const float* d_x,
                         float* d_y, int32_t* d_partials, void* stream, xl_error* err);
 
+/* ---- stage profiling --------------------------------------------------------
+ * Between xl_profile_begin and xl_profile_end, the first max_calls layer calls
+ * record a HIP event before and after each kernel on the stream it runs on
+ * (the reference's phase marks, hip_experts.hpp:13-20). xl_profile_end drains
+ * and returns per-stage totals in ms, the stage and call counts and the stage
+ * names (comma separated). Event creation happens in xl_profile_begin. */
+int32_t xl_profile_begin(xl_context* ctx, int32_t max_calls, xl_error* err);
+int32_t xl_profile_end(xl_context* ctx, float* stage_ms, int32_t max_stages, int32_t* n_stages, int32_t* n_calls,
+                       char* names, int32_t names_bytes, xl_error* err);
+
 /* ---- host utilities (no device needed) ------------------------------------ */
 uint64_t xl_planar_bytes(int32_t type, int32_t n, int32_t k);
 int32_t xl_repack(int32_t type, int32_t n, int32_t k, const void* aos, void* planar);

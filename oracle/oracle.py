@@ -170,6 +170,7 @@ class Reference:
         L.ref_decode.argtypes = [C.c_int, _u8p, C.c_int, _i32p, _i32p, C.POINTER(C.c_float)]
         L.ref_matvec.argtypes = [C.c_int, _u8p, C.c_int, C.c_int, _P, _f32p, C.c_int]
         L.ref_combine.argtypes = [_i32p, _f32p, C.c_int, _f32p, C.c_int, _f32p, _f32p]
+        L.ref_expert.argtypes = [_i32p, _u8p, _u8p, _u8p, C.c_int, C.c_int, _f32p, _f32p, C.c_int]
 
     @staticmethod
     def available() -> bool:
@@ -207,6 +208,12 @@ class Reference:
         q = np.zeros(32, dtype=np.int32); s = np.zeros(2, dtype=np.int32); d = C.c_float()
         self.lib.ref_decode(t, np.ascontiguousarray(row), kb, q, s, C.byref(d))
         return q, s, d.value
+
+    def expert(self, types, gate, up, down, dim, ff, x, threads=8):
+        y = np.zeros(dim, dtype=np.float32)
+        self.lib.ref_expert(np.asarray(types, dtype=np.int32), gate.reshape(-1), up.reshape(-1), down.reshape(-1),
+                            dim, ff, np.ascontiguousarray(x, dtype=np.float32), y, threads)
+        return y
 
     def combine(self, ids, w, rows, shared):
         rows = np.ascontiguousarray(rows, dtype=np.float32)

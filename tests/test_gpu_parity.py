@@ -218,3 +218,70 @@ def test_device_rejects_bad_id_and_poisons():
             lane.layer_forward(0, [1], [1.0], np.ones(256, np.float32))
     finally:
         lane.close()
+
+
+@pytest.mark.parametrize("t", [16, 17, 29])
+def test_matvec_any_fp16_scale(probe, orc, t):
+    # Super-block scales over all finite fp16 classes: subnormal, negative, zero,
+    # large. The device converts with the hardware f16->f32 instruction.
+    n, k = 128, 1024
+    step(f"matvec fp16 scales type={t}")
+    rng = np.random.default_rng(t + 7)
+    aos = orc.gen_matrix(t, 31, 0, 0, 0, n, k).reshape(-1, BLOCK_BYTES[t])
+    h = rng.integers(0, 0x10000, size=aos.shape[0]).astype(np.uint16)
+    h[(h & 0x7C00) == 0x7C00] &= 0xBFFF          # no inf/nan
+    h[:16] = [0x0000, 0x8000, 0x0001, 0x8001, 0x03FF, 0x0400, 0x7BFF, 0xFBFF, 0x3C00, 0xBC00, 0x0200, 0x83FF,
+              0x1000, 0x9000, 0x2E66, 0x5555]
+    if t == 29:
+        for q in range(4):
+            w = aos[:, 48 + 2 * q].astype(np.uint16) | (aos[:, 49 + 2 * q].astype(np.uint16) << 8)
+            w = (w & 0x0FFF) | (((h >> (4 * q)) & 15) << 12)
+            aos[:, 48 + 2 * q] = w & 0xFF; aos[:, 49 + 2 * q] = w >> 8
+    else:
+        aos[:, 0] = h & 0xFF; aos[:, 1] = h >> 8
+    aos = aos.reshape(-1)
+    x = rng.standard_normal(k).astype(np.float32)
+    y = torch.zeros(n, dtype=torch.float32, device="cuda")
+    probe.matvec_async(t, dev(xl.repack(t, n, k, aos)), n, k, dev(x), y)
+    probe.sync()
+    want = orc.matvec(t, aos, n, k, orc.quantize(x))
+    got = y.cpu().numpy()
+    assert np.all(np.isfinite(got))
+    assert max_rel(got, want) < TOL
+
+
+@pytest.mark.parametrize("dim,ff,sig", [(4096, 3072, None), (1024, 512, (17, 17, 16)), (256, 768, (29, 29, 17)),
+                                        (512, 256, (16, 16, 29))])
+def test_fused_layer_equals_separate_launches(orc, dim, ff, sig, monkeypatch):
+    # The fused cooperative kernel and the separate launches share the row
+    # engine and the quantizer, so their outputs must agree bit for bit; the
+    # oracle checks the fused result to the tolerance.
+    step(f"fused vs separate dim={dim} ff={ff} sig={sig}")
+    E, k = 24, 6
+    rng = np.random.default_rng(dim * 7 + ff)
+    if sig is None:   # config-3 style mix: per-expert types over the three formats
+        t = rng.choice([16, 17, 29], size=E, p=[0.19, 0.17, 0.64]).astype(np.int32)
+        types = np.stack([t, t, t], axis=-1)[None]
+    else:
+        types = types_map(1, E, sig[0], sig[2])
+    lanes = {}
+    for fused in ("1", "0"):
+        monkeypatch.setenv("XL_FUSED", fused)
+        lanes[fused] = xl.Lane(dim, ff, 1, E, types, max_picks=8)
+        lanes[fused].generate(seed=77)
+    try:
+        for trial in range(3):
+            ids, w = route(rng.standard_normal(E).astype(np.float32), k)
+            x = rng.standard_normal(dim).astype(np.float32)
+            shared = rng.standard_normal(dim).astype(np.float32) if trial == 1 else None
+            a = lanes["1"].layer_forward(0, ids, w, x, shared)
+            b = lanes["0"].layer_forward(0, ids, w, x, shared)
+            assert np.array_equal(a.view(np.uint32), b.view(np.uint32)), trial
+            rows = []
+            for e in ids:
+                tt = tuple(int(v) for v in types[0, e])
+                rows.append(orc.expert(tt, *orc.gen_expert(tt, 77, 0, int(e), dim, ff), dim, ff, x))
+            assert max_rel(a, orc.combine(ids, w, np.stack(rows), shared)) < TOL
+    finally:
+        for lane in lanes.values():
+            lane.close()

@@ -60,16 +60,21 @@ def test_repack_restore_lossless(orc, t, nk):
     assert np.array_equal(xl.restore(t, n, k, planar), aos)
 
 
-def test_repack_exhaustive_fields(orc):
-    # Every byte position of a block lands in exactly one plane position.
+def test_repack_is_a_bit_permutation():
+    # The repack moves and re-encodes fields but only permutes bits: every
+    # single set bit of a block lands on exactly one planar bit, and back.
     for t in (16, 17, 29):
         bb = L.BLOCK_BYTES[t]
-        for pos in range(bb):
+        seen = set()
+        for bit in range(8 * bb):
             aos = np.zeros(4 * bb, np.uint8)
-            aos[bb + pos] = 0xA5                     # block 1
+            aos[bb + bit // 8] = 1 << (bit % 8)                # block 1 of 4
             planar = xl.repack(t, 1, 1024, aos)
-            assert np.count_nonzero(planar) == 1
+            ones = np.flatnonzero(np.unpackbits(planar))
+            assert ones.size == 1
+            seen.add(int(ones[0]))
             assert np.array_equal(xl.restore(t, 1, 1024, planar), aos)
+        assert len(seen) == 8 * bb
 
 
 @pytest.mark.parametrize("t", [16, 17, 29])

@@ -112,12 +112,16 @@ def main():
     lane = xl.Lane(DIM, FF, 1, E, types, max_picks=8)
     lane.generate(SEED)
     ids, w, x = routes(args.routes, SEED)
-    d_ids = torch.from_numpy(ids).cuda()
-    d_w = torch.from_numpy(w).cuda()
-    d_x = torch.from_numpy(x).cuda()
-    d_out = torch.zeros((args.routes, DIM), dtype=torch.float32, device="cuda")
-    stream = torch.cuda.current_stream()
+    # A dedicated (non-default) stream: the library launches on it and the
+    # timing events are recorded on it.
+    stream = torch.cuda.Stream()
     sp = stream.cuda_stream
+    with torch.cuda.stream(stream):
+        d_ids = torch.from_numpy(ids).cuda()
+        d_w = torch.from_numpy(w).cuda()
+        d_x = torch.from_numpy(x).cuda()
+        d_out = torch.zeros((args.routes, DIM), dtype=torch.float32, device="cuda")
+    torch.cuda.synchronize()
 
     def step(i):
         r = i % args.routes
@@ -126,10 +130,8 @@ def main():
     for i in range(args.warmup):
         step(i)
     torch.cuda.synchronize()
-    lane.profile_begin(args.steps)
     t0 = torch.cuda.Event(enable_timing=True)
     t1 = torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize()
     t0.record(stream)
     wall0 = time.perf_counter()
     for i in range(args.steps):
@@ -137,12 +139,20 @@ def main():
     t1.record(stream)
     torch.cuda.synchronize()
     wall = time.perf_counter() - wall0
-    prof = lane.profile_end()
     lane.sync(sp)
     ms = t0.elapsed_time(t1)
     us_layer = ms * 1e3 / args.steps
     gbs = LAYER_BYTES / (us_layer * 1e-6) / 1e9
 
+    # Per-kernel durations: a separate pass with HIP events recorded by the
+    # library around each kernel on the same stream (not part of the timed run).
+    n_prof = min(args.steps, 200)
+    lane.profile_begin(n_prof)
+    for i in range(n_prof):
+        step(i)
+    torch.cuda.synchronize()
+    prof = lane.profile_end()
+    lane.sync(sp)
     stages = {k: v / prof["calls"] for k, v in prof["stages"].items()}   # ms per call
     dom = max(stages, key=stages.get)
     dom_us = stages[dom] * 1e3

@@ -8,8 +8,8 @@ import sys
 PKG = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(PKG, "csrc")
 LIB = os.path.join(PKG, "libcrosslane.so")
-SOURCES = ["xl_kernels.hip", "xl_api.cpp"]
-HEADERS = ["xl_format.hpp", "xl_decode.hpp", "xl_internal.hpp", "xl_codebooks.inc", "exports.map"]
+SOURCES = ["xl_kernels.hip", "xl_layer.hip", "xl_api.cpp"]
+HEADERS = ["xl_format.hpp", "xl_rows.hpp", "xl_internal.hpp", "xl_codebooks.inc", "exports.map"]
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = os.environ.get("XL_OFFLOAD_ARCH", "gfx950")
@@ -19,6 +19,9 @@ FLAGS = [
     "-ffp-contract=off", "-fno-fast-math",
     # Packed-FP32 VALU forms are kept out of the generated code.
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # Keep single-lane atomics as issued: the atomic optimizer rewrites them to
+    # broadcast their result at once, which stalls on the return value.
+    "-mllvm", "-amdgpu-atomic-optimizer-strategy=None",
     "-Wall", "-Wno-unused-function", "-Wno-unknown-pragmas",
     f"-Wl,--version-script={os.path.join(CSRC, 'exports.map')}",
 ]

@@ -79,6 +79,27 @@ std::vector<uint64_t> device_tables() {
     return t;
 }
 
+// Expanded codebooks of the single-launch kernel (byte layout kG_* in
+// xl_layer.hip), one copy each: sign rows {M, M & 0x01..01} where M has 0xff in
+// the bytes of negative weights, then the IQ2_XXS, IQ2_XS and IQ1 grids.
+std::vector<uint64_t> layer_tables() {
+    std::vector<uint64_t> t;
+    t.reserve(xl::kLayer3TableBytes / 8);
+    for (int i = 0; i < 128; ++i) {
+        const uint8_t sg = ksigns(i);
+        uint64_t m = 0;
+        for (int j = 0; j < 8; ++j)
+            if (sg & (1u << j)) m |= uint64_t(0xff) << (8 * j);
+        t.push_back(m);
+        t.push_back(m & 0x0101010101010101ull);
+    }
+    for (int i = 0; i < 256; ++i) t.push_back(expand_codes(kIq2xxsCodes[i], false));
+    for (int i = 0; i < 512; ++i) t.push_back(expand_codes(kIq2xsCodes[i], false));
+    for (int i = 0; i < 2048; ++i) t.push_back(expand_codes(kIq1sCodes[i], true));
+    if (t.size() * 8 != size_t(xl::kLayer3TableBytes)) throw Failure(XL_E_STATE, "expanded table size");
+    return t;
+}
+
 int env_int(const char* name, int fallback) {
     const char* s = std::getenv(name);
     if (!s || !*s) return fallback;
@@ -91,6 +112,14 @@ int env_int(const char* name, int fallback) {
 uint64_t matrix_blocks(int n, int k) { return uint64_t(n) * uint64_t(k / 256); }
 
 }  // namespace
+
+// A layer whose experts all share one type triple has every expert's three
+// matrices at slab + id * estride + roff[role].
+struct LayerShape {
+    bool regular = false;
+    uint64_t estride = 0, roff[3] = {0, 0, 0};
+    int rtype[3] = {0, 0, 0};
+};
 
 struct xl_context {
     xl_config cfg{};
@@ -115,11 +144,22 @@ struct xl_context {
     std::vector<uint8_t*> slabs;
     std::vector<xl::ExpertDesc> descs;
     std::vector<int> gu_mask, dn_mask;   // per layer: block types among gate/up and among down matrices
+    std::vector<LayerShape> layer_shape; // per layer: regular-layout addressing (see Layer3Args)
     xl::ExpertDesc* d_descs = nullptr;
     uint64_t payload = 0, allocated = 0;
     int grid_gu = 0, grid_down = 0;
-    bool fused = true;          // one cooperative launch per layer (XL_FUSED=0 selects separate launches)
-    uint32_t* sync = nullptr;   // counters of the fused layer kernel
+    // Layer path: 1 = single launch (xl_layer.hip, default), 2 = cooperative
+    // fused kernel, 0 = separate launches. XL_LAYER_PATH selects; shapes
+    // without a single-launch instance use separate launches.
+    int path = 1;
+    uint32_t* sync = nullptr;   // counters of the cooperative fused kernel
+    uint64_t* htag = nullptr;   // single-launch handoff buffers (Layer3Args)
+    uint64_t* hqtag = nullptr;
+    uint64_t* hdtag = nullptr;
+    uint32_t* ctl = nullptr;
+    uint64_t* tables = nullptr;
+    uint64_t* timeline = nullptr;   // per-wave timestamps of the last profiled single launch
+    uint64_t timeline_words = 0;
     // stage profiling (xl_profile_begin / xl_profile_end): events recorded
     // around every kernel of the layer calls, on the stream they run on.
     struct Prof {
@@ -233,7 +273,34 @@ void enqueue_layer(xl_context* ctx, int32_t layer, const int32_t* d_ids, const f
     const int gu_mask = ctx->gu_mask[size_t(layer)], dn_mask = ctx->dn_mask[size_t(layer)];
     Marks mark(ctx, s);
     mark("");
-    if (ctx->fused && !g_dbg && !u_dbg) {
+    if (ctx->path == 1 && !g_dbg && !u_dbg) {
+        xl::Layer3Args a{};
+        a.descs = descs; a.ids = d_ids; a.w = d_w; a.x = d_x; a.shared = d_shared; a.out = d_out;
+        a.k = k; a.n_experts = E; a.dim = dim; a.ff = ff;
+        a.htag = ctx->htag; a.hqtag = ctx->hqtag; a.hdtag = ctx->hdtag; a.ctl = ctx->ctl; a.err = ctx->err_flag;
+        a.tables = ctx->tables;
+        if (ctx->prof.on && ctx->prof.calls <= ctx->prof.max_calls) {
+            a.trace = ctx->timeline;
+            hip_check(hipMemsetAsync(ctx->timeline, 0, size_t(ctx->cus) * 16 * 32 * 8, s), "timeline clear");
+        }
+        const LayerShape& ls = ctx->layer_shape[size_t(layer)];
+        if (ls.regular) {
+            a.slab = ctx->slabs[size_t(layer)];
+            a.estride = ls.estride;
+            for (int r = 0; r < 3; ++r) { a.roff[r] = ls.roff[r]; a.rtype[r] = ls.rtype[r]; }
+        }
+        if (d_out) {
+            const hipError_t e = xl::dev::launch_layer3(a, gu_mask, dn_mask, ctx->cus, s);
+            if (e == hipSuccess) {
+                if (a.trace) ctx->timeline_words = uint64_t(ctx->cus) * 16 * 32;
+                mark("layer");
+                return;
+            }
+            if (e != hipErrorNotSupported) hip_check(e, "single-launch layer");
+            (void)hipGetLastError();   // no instance for this shape: separate launches below
+        }
+    }
+    if (ctx->path == 2 && !g_dbg && !u_dbg) {
         xl::LayerArgs a{};
         a.descs = descs; a.ids = d_ids; a.w = d_w; a.x = d_x; a.shared = d_shared; a.out = d_out;
         a.k = k; a.n_experts = E; a.dim = dim; a.ff = ff;
@@ -322,6 +389,12 @@ int32_t xl_open(uint32_t abi_version, const xl_config* cfg, xl_context** out, xl
             {reinterpret_cast<void**>(&ctx->w), 64 * 4},
             {reinterpret_cast<void**>(&ctx->ids), 64 * 4},
             {reinterpret_cast<void**>(&ctx->q8std), uint64_t(P) * (std::max(dim, ff) / 256) * 292},
+            {reinterpret_cast<void**>(&ctx->htag), uint64_t(P) * ff * 8},
+            {reinterpret_cast<void**>(&ctx->hqtag), uint64_t(P) * ff * 2},
+            {reinterpret_cast<void**>(&ctx->hdtag), uint64_t(P) * (ff / 256) * 8},
+            {reinterpret_cast<void**>(&ctx->ctl), 256},
+            {reinterpret_cast<void**>(&ctx->tables), uint64_t(xl::kLayer3TableBytes)},
+            {reinterpret_cast<void**>(&ctx->timeline), uint64_t(ctx->cus) * 16 * 32 * 8},
         };
         uint64_t total = 0;
         for (auto& p : parts) total += xl::align256(p.bytes);
@@ -340,7 +413,14 @@ int32_t xl_open(uint32_t abi_version, const xl_config* cfg, xl_context** out, xl
         hip_check(hipMemcpy(ctx->codes, codes.data(), code_bytes, hipMemcpyHostToDevice), "codebook upload");
         hip_check(hipMemset(ctx->err_flag, 0, 256), "error flag clear");
         hip_check(hipMemset(ctx->sync, 0, size_t(xl::kSyncWords) * 4), "counter clear");
-        ctx->fused = env_int("XL_FUSED", 0) != 0;   // cooperative single-launch layer: opt-in
+        hip_check(hipMemset(ctx->htag, 0, size_t(P) * ff * 8), "tag clear");
+        hip_check(hipMemset(ctx->hdtag, 0, size_t(P) * (ff / 256) * 8), "tag clear");
+        hip_check(hipMemset(ctx->hqtag, 0, size_t(P) * ff * 2), "tag clear");
+        hip_check(hipMemset(ctx->ctl, 0, 256), "epoch clear");
+        const std::vector<uint64_t> tab = layer_tables();
+        hip_check(hipMemcpy(ctx->tables, tab.data(), tab.size() * 8, hipMemcpyHostToDevice), "table upload");
+        ctx->path = env_int("XL_LAYER_PATH", 1);
+        need(ctx->path >= 0 && ctx->path <= 2, XL_E_ARG, "XL_LAYER_PATH must be 0, 1 or 2");
         *out = ctx;
     });
     if (rc != XL_OK && ctx) xl_close(ctx);
@@ -412,6 +492,27 @@ int32_t xl_bank_create(xl_context* ctx, const int32_t* types, xl_error* err) {
                     m.nb = kk / 256;
                     at += P.bytes;
                 }
+        }
+        ctx->layer_shape.assign(size_t(L), LayerShape{});
+        for (int l = 0; l < L; ++l) {
+            LayerShape& ls = ctx->layer_shape[size_t(l)];
+            const int32_t* t0 = types + size_t(l) * E * 3;
+            bool same = true;
+            for (int e = 1; e < E && same; ++e)
+                for (int r = 0; r < 3; ++r) same = same && t0[3 * e + r] == t0[r];
+            if (!same) continue;
+            const uint8_t* b0 = ctx->descs[size_t(l) * E].m[0].base;
+            uint64_t at = 0;
+            for (int r = 0; r < 3; ++r) {
+                ls.roff[r] = uint64_t(ctx->descs[size_t(l) * E].m[r].base - b0);
+                ls.rtype[r] = t0[r];
+                at += xl::plane_layout(t0[r], r < 2 ? matrix_blocks(ff, dim) : matrix_blocks(dim, ff)).bytes;
+            }
+            ls.estride = at;
+            ls.regular = true;
+            for (int e = 0; e < E && ls.regular; ++e)
+                for (int r = 0; r < 3; ++r)
+                    ls.regular = ls.regular && ctx->descs[size_t(l) * E + e].m[r].base == b0 + uint64_t(e) * at + ls.roff[r];
         }
         hip_check(hipMalloc(&ctx->d_descs, ctx->descs.size() * sizeof(xl::ExpertDesc)), "descriptor hipMalloc");
         hip_check(hipMemcpy(ctx->d_descs, ctx->descs.data(), ctx->descs.size() * sizeof(xl::ExpertDesc),
@@ -670,6 +771,18 @@ int32_t xl_profile_end(xl_context* ctx, float* stage_ms, int32_t max_stages, int
             for (int i = 0; i < S && i < int(P.names.size()); ++i) { if (i) all += ','; all += P.names[i]; }
             std::snprintf(names, size_t(names_bytes), "%s", all.c_str());
         }
+    });
+}
+
+int32_t xl_profile_timeline(xl_context* ctx, uint64_t* out, int32_t max_words, int32_t* n_words, xl_error* err) {
+    return guarded(ctx, err, [&] {
+        ready(ctx, false);
+        need(out != nullptr && n_words != nullptr && max_words >= 0, XL_E_ARG, "null output");
+        const uint64_t n = std::min<uint64_t>(ctx->timeline_words, uint64_t(max_words));
+        hip_check(hipStreamSynchronize(ctx->stream), "stream synchronize");
+        hip_check(hipDeviceSynchronize(), "device synchronize");
+        if (n) hip_check(hipMemcpy(out, ctx->timeline, n * 8, hipMemcpyDeviceToHost), "timeline download");
+        *n_words = int32_t(n);
     });
 }
 

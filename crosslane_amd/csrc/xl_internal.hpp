@@ -63,7 +63,38 @@ struct LayerArgs {
 };
 constexpr int kSyncWords = 256;
 
+// Arguments of the single-launch layer kernel (xl_layer.hip); device pointers.
+struct Layer3Args {
+    const ExpertDesc* descs;    // this layer's n_experts descriptors
+    const int32_t* ids;
+    const float* w;
+    const float* x;
+    const float* shared;        // may be null
+    float* out;
+    int k, n_experts, dim, ff;
+    uint64_t* htag;             // k * ff words: (h value bits, epoch << 32)
+    uint64_t* hqtag;            // k * ff/4 words: (4 Q8_K(h) quants, epoch << 32)
+    uint64_t* hdtag;            // k * ff/256 words: (Q8_K(h) block scale bits, epoch << 32)
+    uint32_t* ctl;              // [0] epoch of the last launch, [1] arrival counter (zero between launches)
+    int* err;
+    const uint64_t* tables;     // expanded codebooks (kLayer3TableBytes), see kG_* in xl_layer.hip
+    // Regular layers (all experts with the same three block types, each
+    // expert's matrices consecutive in the layer slab): matrix (id, role)
+    // starts at slab + id * estride + roff[role] and no descriptor is read.
+    // slab == nullptr: read the descriptors.
+    const uint8_t* slab;
+    uint64_t estride;
+    uint64_t roff[3];
+    int rtype[3];
+    uint64_t* trace;            // null, or 8 timestamps (s_memrealtime) per wave of the grid
+};
+constexpr int kLayer3TableBytes = 24576;   // expanded codebooks of the single-launch kernel
+
 namespace dev {
+// Single-launch layer: hipErrorNotSupported when (dim, ff, k) has no instance.
+// gu_types / dn_types: block types among the layer's gate/up / down matrices
+// (bits 1 IQ2_XXS, 2 IQ2_XS, 4 IQ1_M) select the kernel instance.
+hipError_t launch_layer3(const Layer3Args& args, int gu_types, int dn_types, int cus, hipStream_t s);
 // Fused layer: returns hipErrorNotSupported when (dim, ff) has no fused
 // instance or the device cannot hold the cooperative grid.
 hipError_t launch_layer_fused(const LayerArgs& args, int type_mask, int cus, hipStream_t s);

@@ -1,0 +1,865 @@
+// The routed-expert layer in one launch (gfx950).
+//
+// One workgroup of NW waves per CU, one launch per layer. The layer's weight
+// bytes move as one steady stream (about two items in flight per wave, the
+// point where gfx950 HBM reads run fastest), in the order the work needs them:
+//
+//   prologue  one copy of each codebook and x are loaded first (they need no
+//             ids); the first gate/up slots follow; the codebooks are then
+//             replicated inside LDS (bank-interleaved copies, see Lay) and x
+//             quantized to Q8_K in LDS by every workgroup
+//   gate/up   slot s of the k*ff gate/up rows (pick-major) belongs to wave
+//             s mod W of the grid; h = silu(gate.x) * (up.x) is published per
+//             row as a 64-bit (value, epoch) word
+//   Q8_K(h)   block (i, b) is quantized by one designated wave once all of its
+//             256 tagged h words carry this launch's epoch, and published as
+//             tagged words (4 quants, epoch) plus a tagged scale
+//   down      workgroup g owns output row groups {g, g+G, ...} of every pick.
+//             Its passes (row group, pick) are dealt to its waves round robin
+//             in pick order, so every wave streams early picks first and the
+//             last pick's rows arrive last, while that pick's h is still being
+//             quantized. The wave holding a workgroup's first pass of a pick
+//             stages the pick's Q8_K(h) in LDS; the results go to LDS, and the
+//             fixed-order combine (ascending expert id, sequential fma, then
+//             + shared; engine/strata/warm/runtime.cpp:183-188) needs nothing
+//             from other workgroups
+//
+// Waits only point backwards (gate/up never waits; quantizers wait on gate/up;
+// down waits on quantizers), so the grid drains whether or not all workgroups
+// are resident at once. Every wait is bounded: on expiry the kernel raises
+// kDevErrTimeout and finishes.
+//
+// Epoch: each launch reads the device word E and tags its data E + 1; the last
+// workgroup to arrive (an arrival counter) stores E + 1 for the next launch.
+// The tag never comes from the host, so a captured launch can be replayed.
+//
+// Cross-workgroup data moves through agent-scope (sc1) atomic loads and stores,
+// which are coherent across the XCDs' L2 caches; every published word carries
+// its own tag, so no store ordering wait is needed.
+#include <hip/hip_runtime.h>
+
+#include "xl_format.hpp"
+#include "xl_internal.hpp"
+
+namespace xl::dev {
+
+// ---- LDS layout ------------------------------------------------------------------------
+// Codebooks are replicated in C bank-interleaved copies: entry e of copy c sits
+// at (e * C + c) * row_bytes and lane l reads copy l % C. Random lookups by the
+// 16 (b128) or 32 (b64) lanes an LDS cycle serves then fall into distinct banks
+// far more often than with one copy (measured on gfx950: random b128 lookups
+// from one copy take 2.2x the conflict-free time, from 16 interleaved copies
+// 1.0x; random b64 from one copy 1.7x, from 16 copies 1.5x).
+constexpr int kYStage = 1024;                 // floats of y staging for the combine
+constexpr int kLdsBytes = 160 * 1024 - 512;   // the kernel's LDS array (the rest: small shared words)
+// Byte offsets for an instance whose matrices use the block types in TM (bits
+// 1 IQ2_XXS, 2 IQ2_XS, 4 IQ1_M): only those codebooks are held. HQ: Q8_K(h)
+// of the picks staged once per workgroup (per pick ff quants then 16 scales);
+// before the codebooks are replicated it holds their single copies.
+template <int TM>
+struct Lay {
+    static constexpr int CS = 16;                       // sign-row copies (16-byte rows)
+    static constexpr int CXXS = 16;                     // IQ2_XXS grid copies (8-byte rows)
+    static constexpr int CXS = (TM & 4) ? 8 : 16;       // IQ2_XS grid copies
+    static constexpr int SGN = 0;                                            // 128 rows {M.lo, M.hi, M1.lo, M1.hi}
+    static constexpr int XXS = SGN + ((TM & 3) ? 128 * CS * 16 : 0);         // 256 rows of 8 magnitudes
+    static constexpr int XS = XXS + ((TM & 1) ? 256 * CXXS * 8 : 0);         // 512 rows of 8 magnitudes
+    static constexpr int IQ1 = XS + ((TM & 2) ? 512 * CXS * 8 : 0);          // 2048 rows of 8 values (one copy)
+    static constexpr int XQ = IQ1 + ((TM & 4) ? 2048 * 8 : 0);               // Q8_K(x) quants (dim <= 4096)
+    static constexpr int XD = XQ + 4096;                                     // Q8_K(x) scales (16)
+    static constexpr int Y = XD + 64;                                        // y staging
+    static constexpr int HQ = Y + kYStage * 4;
+    static_assert(HQ + 8192 <= kLdsBytes, "LDS budget");
+};
+// Global codebooks (uploaded once per context), one copy each, byte offsets:
+// sign rows {M.lo, M.hi, M1.lo, M1.hi} x 128 (M: 0xff in the bytes of negative
+// weights), IQ2_XXS rows x 256, IQ2_XS rows x 512, IQ1 rows x 2048 (8 B each).
+constexpr int kG_SGN = 0, kG_XXS = 2048, kG_XS = 4096, kG_IQ1 = 8192, kG_Bytes = 24576;
+static_assert(kG_Bytes == kLayer3TableBytes, "table layout");
+
+typedef const __attribute__((address_space(1))) uint8_t* g8;
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+
+// Agent-scope (device-coherent) accesses for data exchanged inside one launch.
+__device__ __forceinline__ uint64_t coh_ld64(const uint64_t* p) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void coh_st64(uint64_t* p, uint64_t v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ uint32_t coh_ld32(const uint32_t* p) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void coh_st32(uint32_t* p, uint32_t v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ uint64_t tag_word(uint32_t bits, uint32_t epoch) { return uint64_t(bits) | (uint64_t(epoch) << 32); }
+
+__device__ __forceinline__ int sdot4(uint32_t a, uint32_t b, int c) { return __builtin_amdgcn_sdot4(int(a), int(b), c, false); }
+__device__ __forceinline__ uint32_t xad(uint32_t a, uint32_t b, uint32_t c) { return (a ^ b) + c; }   // v_xad_u32
+__device__ __forceinline__ float h2f(uint32_t h) { return float(__builtin_bit_cast(_Float16, uint16_t(h))); }
+
+template <int CTRL>
+__device__ __forceinline__ float dppf(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+// Sum over aligned groups of G lanes (G in 4..64) by DPP adds only (no LDS
+// traffic); the group's sum lands in the group's last lane (for G <= 16 in
+// every lane of the group). A fixed data movement, so run-to-run identical.
+template <int G>
+__device__ __forceinline__ float gsum(float v) {
+    v += dppf<0xB1>(v);                                            // quad_perm [1,0,3,2]
+    v += dppf<0x4E>(v);                                            // quad_perm [2,3,0,1]
+    if constexpr (G >= 8) v += dppf<0x141>(v);                     // row_half_mirror
+    if constexpr (G >= 16) v += dppf<0x140>(v);                    // row_mirror
+    if constexpr (G >= 32)                                         // row_bcast:15 into rows 1 and 3
+        v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x142, 0xA, 0xF, false));
+    if constexpr (G >= 64)                                         // row_bcast:31 into rows 2 and 3
+        v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x143, 0xC, 0xF, false));
+    return v;
+}
+
+// s_waitcnt immediate for "vector memory counter <= n" (gfx9 encoding; the
+// export and LDS/scalar counters are left unconstrained).
+constexpr int vmcnt_imm(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8); }
+
+// ---- Q8_K of one 256-value block by one wave (lane l owns values 4l..4l+3).
+// Bit-exact restatement of engine/strata/sycl/stage/wiring/q8k_core.hpp:30-38:
+// mx is the first value of largest magnitude (strict '>' scan), is = -127/mx,
+// q = min(127, nearest(is * v)), d = 1/is; an all-zero block gives d = 0, q = 0.
+struct Q8Lane {
+    uint32_t packed;   // this lane's 4 quants
+    float d;
+    bool finite;
+};
+__device__ __forceinline__ int nearest_rn(float x) {
+    const float v = __fadd_rn(x, 12582912.0f);   // q8k_core.hpp:25-29
+    return int(__float_as_uint(v) & 0x007fffffu) - 0x00400000;
+}
+// The block's (value, index) of largest magnitude, lowest index on ties: the
+// combine is associative and commutative, so the DPP tree gives the same
+// winner as the reference's sequential scan.
+__device__ __forceinline__ void amax_pick(float& m, int& i, float m2, int i2) {
+    const float a = fabsf(m), a2 = fabsf(m2);
+    if (a2 > a || (a2 == a && i2 < i)) { m = m2; i = i2; }
+}
+template <int CTRL>
+__device__ __forceinline__ void amax_step(float& m, int& i) {
+    amax_pick(m, i, dppf<CTRL>(m), __builtin_amdgcn_update_dpp(0, i, CTRL, 0xF, 0xF, false));
+}
+__device__ __forceinline__ Q8Lane q8k_lane(const float v[4], int lane) {
+    float mx = 0.0f;
+    int idx = 4 * lane;
+    bool finite = true;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        finite = finite && (fabsf(v[j]) <= 3.402823466e38f);
+        if (fabsf(v[j]) > fabsf(mx)) { mx = v[j]; idx = 4 * lane + j; }
+    }
+    amax_step<0xB1>(mx, idx);
+    amax_step<0x4E>(mx, idx);
+    amax_step<0x141>(mx, idx);
+    amax_step<0x140>(mx, idx);   // every lane of a 16-lane row holds the row's pick
+#pragma unroll
+    for (int r = 1; r < 4; ++r)
+        amax_pick(mx, idx, __int_as_float(__builtin_amdgcn_readlane(__float_as_int(mx), 16 * r)),
+                  __builtin_amdgcn_readlane(idx, 16 * r));
+    mx = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(mx)));   // row 0's lanes now hold the block's pick
+    Q8Lane r{0u, 0.0f, !__any(!finite)};
+    if (mx != 0.0f) {
+        const float is = __fdiv_rn(-127.0f, mx);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            int q = nearest_rn(__fmul_rn(is, v[j]));
+            q = q < 127 ? q : 127;
+            r.packed |= uint32_t(uint8_t(int8_t(q))) << (8 * j);
+        }
+        r.d = __fdiv_rn(1.0f, is);
+    }
+    return r;
+}
+
+__device__ __forceinline__ float silu_mul3(float g, float u) {
+    // q8k_core.hpp:92-95 with limit 0: (g / (1 + exp(-g))) * u
+    const float e = expf(-g);
+    return __fmul_rn(__fdiv_rn(g, __fadd_rn(1.0f, e)), u);
+}
+
+// ---- row engine --------------------------------------------------------------------------
+struct Lut {
+    uint32_t sgn, xxs, xs, iq1;   // per-lane LDS byte address of this lane's copy of each table
+};
+template <int TM>
+__device__ __forceinline__ Lut make_lut(int lane) {
+    using LY = Lay<TM>;
+    Lut L;
+    L.sgn = LY::SGN + uint32_t(lane % LY::CS) * 16;
+    L.xxs = LY::XXS + uint32_t(lane % LY::CXXS) * 8;
+    L.xs = LY::XS + uint32_t(lane % LY::CXS) * 8;
+    L.iq1 = LY::IQ1;
+    return L;
+}
+
+// Activations of the pairs a lane owns: 64 Q8_K bytes per pair and the pair's block scale.
+template <int P>
+struct Act3 {
+    uint32_t a[P][16];
+    float d[P];
+};
+
+// Raw words of one pair (64 weights) of one row, meaning by type:
+//   IQ2_XXS: w0..3 = 16 B of Q (2 sub-blocks x {4 grid bytes, 4 sign|scale-bit bytes}), w4 = d16
+//   IQ2_XS : w0..3 = 8 codes {sign7 | grid9 << 7}, w4 = the pair's two scale bytes, w5 = d16
+//   IQ1_M  : w0..1 = 8 low index bytes, w2 = 8 nibbles (3 index bits + delta sign), w3..4 = block scale words
+struct Raw3 {
+    uint32_t w[6];
+};
+// Plane offsets of a matrix of NB blocks (plane_layout in xl_format.hpp).
+__device__ __forceinline__ void plane_offs(int type, uint64_t NB, uint32_t& o1, uint32_t& o2) {
+    const uint64_t w0 = type == kIQ1_M ? 32 : 64;
+    const uint64_t w1 = type == kIQ2_XXS ? 2 : type == kIQ2_XS ? 8 : 16;
+    const uint64_t a1 = align256(w0 * NB);
+    o1 = uint32_t(a1);
+    o2 = uint32_t(align256(a1 + w1 * NB));
+}
+// A matrix as the kernel addresses it: planes at base, base + o1, base + o2
+// (one matrix is far below 4 GB, so plane and row offsets are 32-bit).
+struct MRef {
+    const uint8_t* base;
+    uint32_t o1, o2;
+    int type, nb;
+};
+// Lane-constant byte offsets of pair p of the lane's row (rG rows below the row
+// group's first row) in each plane: weight loads are buffer loads whose
+// per-lane offset never changes and whose row-group offset is scalar, so a
+// load costs no vector address arithmetic.
+struct PairOff {
+    uint32_t q, a, b;
+};
+__device__ __forceinline__ PairOff pair_off(int type, int nb, int rG, int p) {
+    const uint32_t e = uint32_t(rG * nb * 4 + p), blk = uint32_t(rG * nb + (p >> 2));
+    PairOff o;
+    if (type == kIQ1_M) { o.q = e * 8; o.a = e * 4; o.b = blk * 8; }
+    else if (type == kIQ2_XS) { o.q = e * 16; o.a = e * 2; o.b = blk * 2; }
+    else { o.q = e * 16; o.a = blk * 2; o.b = 0; }
+    return o;
+}
+// VMEM instructions one pair load issues, per type (-1: not fixed at compile time).
+template <int TM>
+constexpr int loads_per_pair() { return TM == 1 ? 2 : (TM == 2 || TM == 4) ? 3 : -1; }
+
+typedef uint32_t v4u32 __attribute__((ext_vector_type(4)));
+typedef uint32_t v2u32 __attribute__((ext_vector_type(2)));
+constexpr int kNT = 2;   // cache policy: non-temporal (streamed once)
+// Pair p of row row0 + rG of matrix m (row0 wave-uniform).
+__device__ __forceinline__ void load_pair(Raw3& r, int type, const MRef& m, int row0, const PairOff& po) {
+    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc((void*)m.base, (short)0, -1, 0x00020000);
+    const uint32_t rb = uint32_t(row0) * uint32_t(m.nb);   // blocks before the row group
+    if (type == kIQ1_M) {
+        const v2u32 q = __builtin_amdgcn_raw_buffer_load_b64(rs, po.q, rb * 32, kNT);
+        r.w[2] = __builtin_amdgcn_raw_buffer_load_b32(rs, po.a, m.o1 + rb * 16, kNT);
+        const v2u32 sw = __builtin_amdgcn_raw_buffer_load_b64(rs, po.b, m.o2 + rb * 8, kNT);
+        r.w[0] = q.x; r.w[1] = q.y;
+        r.w[3] = sw.x; r.w[4] = sw.y; r.w[5] = 0;
+    } else {
+        const v4u32 q = __builtin_amdgcn_raw_buffer_load_b128(rs, po.q, rb * 64, kNT);
+        r.w[0] = q.x; r.w[1] = q.y; r.w[2] = q.z; r.w[3] = q.w;
+        if (type == kIQ2_XXS) {
+            r.w[4] = __builtin_amdgcn_raw_buffer_load_b16(rs, po.a, m.o1 + rb * 2, kNT);
+            r.w[5] = 0;
+        } else {
+            r.w[4] = __builtin_amdgcn_raw_buffer_load_b16(rs, po.a, m.o1 + rb * 8, kNT);
+            r.w[5] = __builtin_amdgcn_raw_buffer_load_b16(rs, po.b, m.o2 + rb * 2, kNT);
+        }
+    }
+}
+template <int TM>
+__device__ __forceinline__ void load_pair_t(Raw3& r, const MRef& m, int row0, int rG, int p) {
+    if constexpr (TM == 1) load_pair(r, kIQ2_XXS, m, row0, pair_off(kIQ2_XXS, m.nb, rG, p));
+    else if constexpr (TM == 2) load_pair(r, kIQ2_XS, m, row0, pair_off(kIQ2_XS, m.nb, rG, p));
+    else if constexpr (TM == 4) load_pair(r, kIQ1_M, m, row0, pair_off(kIQ1_M, m.nb, rG, p));
+    else load_pair(r, m.type, m, row0, pair_off(m.type, m.nb, rG, p));
+}
+
+// 2s+1 from the four scale bits stored in bit 7 of each sign byte.
+__device__ __forceinline__ int xxs_sc(uint32_t signs) {
+    return int(__builtin_amdgcn_udot4((signs >> 7) & 0x01010101u, 0x10080402u, 1u, false));
+}
+// The pair decoders issue every codebook lookup of the pair before using any:
+// 16 LDS reads in flight per lane hide the LDS latency.
+template <int TM>
+__device__ __forceinline__ int pair_xxs3(const uint8_t* lds, const Lut& L, const uint32_t* w, const uint32_t* a) {
+    constexpr int SX = Lay<TM>::CXXS * 8, SS = Lay<TM>::CS * 16;   // entry strides
+    uint2 g[8];
+    uint4 m[8];
+#pragma unroll
+    for (int s = 0; s < 2; ++s)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            g[4 * s + q] = *reinterpret_cast<const uint2*>(lds + L.xxs + ((w[2 * s] >> (8 * q)) & 255u) * SX);
+            m[4 * s + q] = *reinterpret_cast<const uint4*>(lds + L.sgn + ((w[2 * s + 1] >> (8 * q)) & 127u) * SS);
+        }
+    int acc[2] = {0, 0};
+#pragma unroll
+    for (int s = 0; s < 2; ++s)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const int e = 4 * s + q;
+            acc[s] = sdot4(xad(g[e].x, m[e].x, m[e].z), a[8 * s + 2 * q], acc[s]);
+            acc[s] = sdot4(xad(g[e].y, m[e].y, m[e].w), a[8 * s + 2 * q + 1], acc[s]);
+        }
+    return __mul24(acc[0], xxs_sc(w[1])) + __mul24(acc[1], xxs_sc(w[3]));
+}
+template <int TM>
+__device__ __forceinline__ int pair_xs3(const uint8_t* lds, const Lut& L, const uint32_t* w, const uint32_t* a) {
+    constexpr int SX = Lay<TM>::CXS * 8, SS = Lay<TM>::CS * 16;
+    uint2 g[8];
+    uint4 m[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+        const uint32_t c = (w[e / 2] >> (16 * (e & 1))) & 0xffffu;
+        g[e] = *reinterpret_cast<const uint2*>(lds + L.xs + (c >> 7) * SX);
+        m[e] = *reinterpret_cast<const uint4*>(lds + L.sgn + (c & 127u) * SS);
+    }
+    int total = 0;
+#pragma unroll
+    for (int s = 0; s < 2; ++s) {
+        int lo = 0, hi = 0;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const int e = 4 * s + q;
+            int& acc = q < 2 ? lo : hi;
+            acc = sdot4(xad(g[e].x, m[e].x, m[e].z), a[8 * s + 2 * q], acc);
+            acc = sdot4(xad(g[e].y, m[e].y, m[e].w), a[8 * s + 2 * q + 1], acc);
+        }
+        const uint32_t byte = (w[4] >> (8 * s)) & 255u;
+        total += __mul24(lo, int(2u * (byte & 15u) + 1u)) + __mul24(hi, int(2u * (byte >> 4) + 1u));
+    }
+    return total;
+}
+// IQ1_M pair as the single integer sum over its 64 weights of (2s+1)*(8*grid + delta)*q;
+// the delta part uses the group sums of the quants.
+__device__ __forceinline__ int pair_iq13(const uint8_t* lds, const Lut& L, const uint32_t* w, uint32_t scw, const uint32_t* a) {
+    uint2 gr[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+        const int s = e / 4, g = e % 4;
+        const uint32_t nib = (w[2] >> (16 * s + 4 * g)) & 15u;
+        const uint32_t idx = ((w[s] >> (8 * g)) & 255u) | ((nib & 7u) << 8);
+        gr[e] = *reinterpret_cast<const uint2*>(lds + L.iq1 + (idx << 3));
+    }
+    int total = 0;
+#pragma unroll
+    for (int s = 0; s < 2; ++s) {
+        int m0 = 0, m1 = 0, d0 = 0, d1 = 0;
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+            const int e = 4 * s + g;
+            const uint32_t nib = (w[2] >> (16 * s + 4 * g)) & 15u;
+            const uint32_t a0 = a[8 * s + 2 * g], a1 = a[8 * s + 2 * g + 1];
+            const int m = sdot4(gr[e].y, a1, sdot4(gr[e].x, a0, 0));
+            const int sg = sdot4(0x01010101u, a1, sdot4(0x01010101u, a0, 0));
+            const int dl = (nib & 8u) ? -sg : sg;
+            if (g < 2) { m0 += m; d0 += dl; } else { m1 += m; d1 += dl; }
+        }
+        const int c0 = int(2u * ((scw >> (6 * s)) & 7u) + 1u), c1 = int(2u * ((scw >> (6 * s + 3)) & 7u) + 1u);
+        total += c0 * (8 * m0 + d0) + c1 * (8 * m1 + d1);
+    }
+    return total;
+}
+
+// One pair's contribution fma(fp16(d_w) * d_x, I, acc); the row is then summed
+// over its lanes and scaled by 1/8 (q8k_core.hpp:87-91 regrouped: the integers
+// per block are exact, the float order is this kernel's own).
+template <int T, int TM>
+__device__ __forceinline__ float pair_term(const uint8_t* lds, const Lut& L, const Raw3& r, int p, const uint32_t* a,
+                                           float dx, float acc) {
+    int I;
+    uint32_t d16;
+    if constexpr (T == kIQ2_XXS) {
+        I = pair_xxs3<TM>(lds, L, r.w, a);
+        d16 = r.w[4];
+    } else if constexpr (T == kIQ2_XS) {
+        I = pair_xs3<TM>(lds, L, r.w, a);
+        d16 = r.w[5];
+    } else {
+        const uint32_t scw = ((p & 2) ? r.w[4] : r.w[3]) >> (16 * (p & 1));
+        I = pair_iq13(lds, L, r.w, scw, a);
+        d16 = ((r.w[3] >> 12) & 0xfu) | ((r.w[3] >> 24) & 0xf0u) | ((r.w[4] >> 4) & 0xf00u) | ((r.w[4] >> 16) & 0xf000u);
+    }
+    return fmaf(__fmul_rn(h2f(d16), dx), float(I), acc);
+}
+template <int T, int TM>
+__device__ __forceinline__ bool has_type() {
+    return (T == kIQ2_XXS && (TM & 1)) || (T == kIQ2_XS && (TM & 2)) || (T == kIQ1_M && (TM & 4));
+}
+// Lane partial of one row (TM: types possible for this row; LT: types held in LDS).
+template <int TM, int LT, int P>
+__device__ __forceinline__ float row_sum(const uint8_t* lds, const Lut& L, int type, const Raw3* r, const Act3<P>& A, int l,
+                                         int LPR) {
+    float acc = 0.0f;
+    if constexpr (TM == 1 || TM == 2 || TM == 4) {
+        constexpr int T = TM == 1 ? kIQ2_XXS : TM == 2 ? kIQ2_XS : kIQ1_M;
+#pragma unroll
+        for (int j = 0; j < P; ++j) acc = pair_term<T, LT>(lds, L, r[j], l + LPR * j, A.a[j], A.d[j], acc);
+    } else {
+        if (has_type<kIQ2_XXS, TM>() && type == kIQ2_XXS) {
+#pragma unroll
+            for (int j = 0; j < P; ++j) acc = pair_term<kIQ2_XXS, LT>(lds, L, r[j], l + LPR * j, A.a[j], A.d[j], acc);
+        } else if (has_type<kIQ2_XS, TM>() && type == kIQ2_XS) {
+#pragma unroll
+            for (int j = 0; j < P; ++j) acc = pair_term<kIQ2_XS, LT>(lds, L, r[j], l + LPR * j, A.a[j], A.d[j], acc);
+        } else if (has_type<kIQ1_M, TM>()) {
+#pragma unroll
+            for (int j = 0; j < P; ++j) acc = pair_term<kIQ1_M, LT>(lds, L, r[j], l + LPR * j, A.a[j], A.d[j], acc);
+        }
+    }
+    return acc;
+}
+
+// Matrix (id, role) of a layer: by arithmetic for regular layers, else from
+// the descriptor. Rows x nb blocks give the plane offsets.
+template <int TM>
+__device__ __forceinline__ MRef mref(const Layer3Args& a, int id, int role, int rows, int nb) {
+    MRef m;
+    if (a.slab) {
+        m.base = a.slab + uint64_t(id) * a.estride + a.roff[role];
+        m.type = a.rtype[role];
+    } else {
+        const MatRef& d = a.descs[id].m[role];
+        m.base = d.base;
+        m.type = d.type;
+    }
+    if constexpr (TM == 1) m.type = kIQ2_XXS;
+    else if constexpr (TM == 2) m.type = kIQ2_XS;
+    else if constexpr (TM == 4) m.type = kIQ1_M;
+    m.nb = nb;
+    plane_offs(m.type, uint64_t(rows) * uint64_t(nb), m.o1, m.o2);
+    return m;
+}
+
+// ---- codebooks into LDS -------------------------------------------------------------------
+// Direct-to-LDS load of `bytes` (a multiple of 1 KB) from global src to LDS
+// dst; wave w issues the 1-KB groups w, w + NW, ...
+template <int NW>
+__device__ __forceinline__ void lds_dma(uint8_t* lds, int dst, const uint8_t* src, int bytes, int wv, int lane) {
+    for (int g = wv; g * 1024 < bytes; g += NW)
+        __builtin_amdgcn_global_load_lds((const void*)(src + 1024 * g + 16 * lane),
+                                         (__attribute__((address_space(3))) void*)(lds + dst + 1024 * g), 16, 0, 0);
+}
+// Replicates `rows` rows of rb bytes (8 or 16) held once at LDS src into C
+// interleaved copies at dst: consecutive threads write consecutive 16-B chunks.
+template <int NT>
+__device__ __forceinline__ void lds_replicate(uint8_t* lds, int dst, int src, int rows, int rb, int C, int t) {
+    const int chunks = rows * C * rb / 16;
+    const int per_row = C * rb / 16;
+    for (int c = t; c < chunks; c += NT) {
+        const int e = c / per_row;
+        uint4 v;
+        if (rb == 16) {
+            v = *reinterpret_cast<const uint4*>(lds + src + 16 * e);
+        } else {
+            const uint2 h = *reinterpret_cast<const uint2*>(lds + src + 8 * e);
+            v = make_uint4(h.x, h.y, h.x, h.y);
+        }
+        *reinterpret_cast<uint4*>(lds + dst + 16 * c) = v;
+    }
+}
+
+// Workgroup barrier for LDS data: the wave's LDS accesses complete, then the
+// barrier. Unlike __syncthreads it does not wait for the wave's outstanding
+// global loads (a workgroup fence would, as it cannot tell them from
+// direct-to-LDS loads). The empty asm statements keep the compiler from moving
+// memory accesses across it.
+constexpr int kLgkm0 = 15 | (3 << 14) | (7 << 4);   // s_waitcnt lgkmcnt(0) only
+__device__ __forceinline__ void lds_barrier() {
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_waitcnt(kLgkm0);
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+}
+
+// ---- bounded waits -------------------------------------------------------------------------
+constexpr uint32_t kPollLimit = 1u << 21;   // polls (each a device-memory round trip): about a second
+
+__device__ __forceinline__ void set_err(int* err, int bit) { atomicOr(err, bit); }
+
+// ---- the kernel --------------------------------------------------------------------------------
+// NW waves per workgroup. LG x PG: lanes per gate/up row and pairs per lane
+// (LG * PG * 64 == dim); LD x PD: the same for down rows (LD * PD * 64 == ff).
+// GUT / DNT: block types among the gate/up / down matrices (bits 1 IQ2_XXS,
+// 2 IQ2_XS, 4 IQ1_M). MG / MD: most gate/up slots / down passes one wave
+// holds; WIN: gate/up slots in flight per wave; WIND: down passes in flight.
+template <int NW, int LG, int PG, int LD, int PD, int MG, int MD, int WIN, int WIND, int GUT, int DNT>
+__global__ __launch_bounds__(NW * 64, 1) void layer3_kernel(Layer3Args a) {
+    __shared__ __attribute__((aligned(16))) uint8_t lds[kLdsBytes];
+    __shared__ uint32_t s_epoch;
+    __shared__ int s_ids[16];
+    __shared__ float s_w[16];
+    __shared__ uint32_t s_hq_ready[16];   // epoch once pick i's Q8_K(h) is staged in LDS
+    constexpr int TM = GUT | DNT;
+    using LY = Lay<TM>;
+    constexpr int RG = 64 / LG, RD = 64 / LD;
+    const int t = threadIdx.x, lane = t & 63;
+    const int wv = __builtin_amdgcn_readfirstlane(t >> 6);   // wave-uniform: keeps slot/pick/matrix math scalar
+    const int G = gridDim.x, W = G * NW, gw = blockIdx.x * NW + wv;
+    const int k = a.k, ff = a.ff, dim = a.dim;
+    const int lG = lane % LG, rG = lane / LG, lD = lane % LD, rD = lane / LD;
+    const int nbx = dim / 256, nbh = ff / 256;
+    auto mark = [&](int n) {   // optional per-wave timeline (s_memrealtime, 100 MHz)
+        if (a.trace && lane == 0) a.trace[size_t(gw) * 32 + n] = __builtin_amdgcn_s_memrealtime();
+    };
+
+    // ---- ids and matrix references of this wave's work, read before the
+    // kernel's first global store so that they come through the scalar unit.
+    // Slots past the wave's last repeat it and bad ids read expert 0, so every
+    // path issues the same loads (the waits on them stay exact); gid < 0 marks
+    // a slot whose result is not used. Passes likewise.
+    const int sppG = ff / RG, SG = k * sppG;
+    const int ng = SG > gw ? min(MG, (SG - gw + W - 1) / W) : 0;
+    const int quads = dim / RD;
+    const int nq_wg = quads > int(blockIdx.x) ? (quads - int(blockIdx.x) + G - 1) / G : 0;
+    const int P = k * nq_wg;
+    const int nd = P > wv ? min(MD, (P - wv + NW - 1) / NW) : 0;   // passes p = wv + NW*j, pick-major
+    // pick indices first, then every id load, then the references: one wait
+    int gslot[MG], gpick[MG], dpick[MD], drow[MD], gidr[MG], didr[MD];
+#pragma unroll
+    for (int j = 0; j < MG; ++j) {
+        gslot[j] = gw + W * (j < ng ? j : ng - 1);
+        gpick[j] = ng > 0 ? gslot[j] / sppG : 0;
+    }
+#pragma unroll
+    for (int j = 0; j < MD; ++j) {
+        const int p = wv + NW * (j < nd ? j : nd - 1);
+        dpick[j] = nd > 0 ? p / nq_wg : 0;
+        drow[j] = nd > 0 ? (int(blockIdx.x) + G * (p - dpick[j] * nq_wg)) * RD + rD : rD;
+    }
+    // lane i holds ids[i] (one load); a wave reads the ids it needs by readlane
+    const int idv = lane < k ? a.ids[lane] : -1;
+#pragma unroll
+    for (int j = 0; j < MG; ++j) gidr[j] = __builtin_amdgcn_readlane(idv, gpick[j]);
+#pragma unroll
+    for (int j = 0; j < MD; ++j) didr[j] = __builtin_amdgcn_readlane(idv, dpick[j]);
+    MRef gm[MG], um[MG], dm[MD];
+    int gid[MG], did[MD];
+#pragma unroll
+    for (int j = 0; j < MG; ++j) {
+        const bool ok = ng > 0 && gidr[j] >= 0 && gidr[j] < a.n_experts;
+        gid[j] = (j < ng && ok) ? gidr[j] : -1;
+        gm[j] = mref<GUT>(a, ok ? gidr[j] : 0, 0, ff, nbx);
+        um[j] = mref<GUT>(a, ok ? gidr[j] : 0, 1, ff, nbx);
+    }
+#pragma unroll
+    for (int j = 0; j < MD; ++j) {
+        const bool ok = nd > 0 && didr[j] >= 0 && didr[j] < a.n_experts;
+        did[j] = (j < nd && ok) ? didr[j] : -1;
+        dm[j] = mref<DNT>(a, ok ? didr[j] : 0, 2, dim, nbh);
+    }
+    // ---- codebook single copies and x (issued ahead of the weight loads)
+    {
+        const uint8_t* gt = reinterpret_cast<const uint8_t*>(a.tables);
+        if constexpr (TM & 3) lds_dma<NW>(lds, LY::HQ, gt + kG_SGN, 2048, wv, lane);
+        if constexpr (TM & 1) lds_dma<NW>(lds, LY::HQ + 2048, gt + kG_XXS, 2048, wv, lane);
+        if constexpr (TM & 2) lds_dma<NW>(lds, LY::HQ + 4096, gt + kG_XS, 4096, wv, lane);
+        if constexpr (TM & 4) lds_dma<NW>(lds, LY::IQ1, gt + kG_IQ1, 16384, wv, lane);
+    }
+    constexpr int UX = (16 + NW - 1) / NW;
+    float4 xv[UX];
+#pragma unroll
+    for (int u = 0; u < UX; ++u) {
+        const int b = wv + NW * u;
+        if (b < nbx) xv[u] = reinterpret_cast<const float4*>(a.x + 256 * b)[lane];
+    }
+
+    // ids and weights for the combine, and the epoch word: loaded now, used later
+    const int cid = idv;
+    float cw = 0.0f;
+    if (wv == 0 && lane < k) cw = a.w[lane];
+    uint32_t* ctl = a.ctl;   // [0] epoch of the last launch, [1] arrivals
+    const uint32_t e_prev = coh_ld32(ctl);
+
+    // ---- the first WIN gate/up slots
+    Raw3 rg[WIN][PG], ru[WIN][PG];
+    auto load_slot = [&](int j, int b) {
+        const int row0 = (gslot[j] % sppG) * RG;
+#pragma unroll
+        for (int q = 0; q < PG; ++q) {
+            load_pair_t<GUT>(rg[b][q], gm[j], row0, rG, lG + LG * q);
+            load_pair_t<GUT>(ru[b][q], um[j], row0, rG, lG + LG * q);
+        }
+    };
+    if (ng > 0) {
+#pragma unroll
+        for (int j = 0; j < WIN; ++j) load_slot(j, j);
+    }
+    mark(0);
+
+    // ---- codebooks replicated, x quantized (LDS), epoch
+    constexpr int LPP = loads_per_pair<GUT>();
+    if constexpr (LPP > 0) __builtin_amdgcn_s_waitcnt(vmcnt_imm(WIN * PG * 2 * LPP));   // all but the slot loads
+    else __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+    lds_barrier();   // every wave's codebook chunks are in
+    mark(1);
+    if constexpr (TM & 3) lds_replicate<NW * 64>(lds, LY::SGN, LY::HQ, 128, 16, LY::CS, t);
+    if constexpr (TM & 1) lds_replicate<NW * 64>(lds, LY::XXS, LY::HQ + 2048, 256, 8, LY::CXXS, t);
+    if constexpr (TM & 2) lds_replicate<NW * 64>(lds, LY::XS, LY::HQ + 4096, 512, 8, LY::CXS, t);
+#pragma unroll
+    for (int u = 0; u < UX; ++u) {
+        const int b = wv + NW * u;
+        if (b < nbx) {
+            const float v[4] = {xv[u].x, xv[u].y, xv[u].z, xv[u].w};
+            const Q8Lane q = q8k_lane(v, lane);
+            if (!q.finite && lane == 0) set_err(a.err, kDevErrNonFinite);
+            reinterpret_cast<uint32_t*>(lds + LY::XQ + 256 * b)[lane] = q.packed;
+            if (lane == 0) reinterpret_cast<float*>(lds + LY::XD)[b] = q.d;
+        }
+    }
+    if (wv == 0 && lane < k) {
+        s_ids[lane] = cid;
+        s_w[lane] = cw;
+    }
+    if (t < 16) s_hq_ready[t] = 0u;
+    if (t == 0) s_epoch = e_prev + 1u;
+    lds_barrier();
+    const uint32_t epoch = s_epoch;
+    // Arrival: this workgroup has read the epoch word. Whoever arrives last
+    // advances it, at the end of the kernel (the count is not awaited before).
+    uint32_t arrived = 0;
+    if (t == 0) arrived = __hip_atomic_fetch_add(ctl + 1, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (gw < k && lane == 0) {   // each bad id is reported once
+        const int id = s_ids[gw];
+        if (id < 0 || id >= a.n_experts) set_err(a.err, kDevErrExpertId);
+    }
+    mark(2);
+
+    const Lut L = make_lut<TM>(lane);
+    Raw3 rd[WIND + 1][PD];   // ring of down passes in flight
+    auto load_pass = [&](int j) {
+#pragma unroll
+        for (int q = 0; q < PD; ++q) load_pair_t<DNT>(rd[j % (WIND + 1)][q], dm[j], drow[j] - rD, rD, lD + LD * q);
+    };
+    int issued = 0;   // down passes issued so far (wave-uniform)
+
+    // ---- gate/up; its last WIND iterations start the down stream
+    {
+        Act3<PG> A;
+#pragma unroll
+        for (int q = 0; q < PG; ++q) {
+            const int p = lG + LG * q;
+            const uint4* src = reinterpret_cast<const uint4*>(lds + LY::XQ + 64 * p);
+#pragma unroll
+            for (int c = 0; c < 4; ++c) {
+                const uint4 v = src[c];
+                A.a[q][4 * c] = v.x; A.a[q][4 * c + 1] = v.y; A.a[q][4 * c + 2] = v.z; A.a[q][4 * c + 3] = v.w;
+            }
+            A.d[q] = reinterpret_cast<const float*>(lds + LY::XD)[p >> 2];
+        }
+        // Fully unrolled (no break): the per-slot references stay in registers.
+#pragma unroll
+        for (int j = 0; j < MG; ++j) {
+            if (j < ng) {
+                if (j >= 1 && j + WIN - 1 < MG) load_slot(j + WIN - 1, (j + WIN - 1) % WIN);
+                if (j >= MG - WIND && nd > 0) {   // static position for the common case ng == MG
+                    load_pass(j - (MG - WIND));
+                    issued = j - (MG - WIND) + 1;
+                }
+                const int s = gslot[j];
+                const int i = s / sppG, row = (s - i * sppG) * RG + rG;
+                float hv = 0.0f;
+                if (gid[j] >= 0) {
+                    const float g = gsum<LG>(row_sum<GUT, TM, PG>(lds, L, gm[j].type, rg[j % WIN], A, lG, LG));
+                    const float u = gsum<LG>(row_sum<GUT, TM, PG>(lds, L, gm[j].type, ru[j % WIN], A, lG, LG));
+                    hv = silu_mul3(__fmul_rn(0.125f, g), __fmul_rn(0.125f, u));
+                }
+                if (lG == LG - 1) coh_st64(a.htag + size_t(i) * ff + row, tag_word(__float_as_uint(hv), epoch));
+                mark(8 + j);
+            }
+        }
+    }
+    mark(3);
+    // waves with fewer slots start their down stream here
+#pragma unroll
+    for (int j = 0; j < WIND; ++j)
+        if (j < MD && j >= issued && nd > 0) load_pass(j);
+
+    // ---- Q8_K(h): block q of the k*ff/256 blocks belongs to wave q*stride
+    const int nqb = k * nbh;
+    const int stride = W / nqb;
+    if (stride >= 1 && gw % stride == 0 && gw / stride < nqb) {
+        const int qb = gw / stride, i = qb / nbh, bb = qb - i * nbh;
+        const uint64_t* src = a.htag + size_t(i) * ff + 256 * bb + 4 * lane;
+        uint64_t v[4];
+        uint32_t polls = 0;
+        for (;;) {
+#pragma unroll
+            for (int j = 0; j < 4; ++j) v[j] = coh_ld64(src + j);
+            bool ok = true;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) ok = ok && uint32_t(v[j] >> 32) == epoch;
+            if (__all(ok)) break;
+            if (++polls > kPollLimit) {
+                if (lane == 0) set_err(a.err, kDevErrTimeout);
+                break;
+            }
+            __builtin_amdgcn_s_sleep(2);
+        }
+        const float hv[4] = {__uint_as_float(uint32_t(v[0])), __uint_as_float(uint32_t(v[1])),
+                             __uint_as_float(uint32_t(v[2])), __uint_as_float(uint32_t(v[3]))};
+        const Q8Lane q = q8k_lane(hv, lane);
+        if (!q.finite && lane == 0) set_err(a.err, kDevErrNonFinite);
+        coh_st64(a.hqtag + size_t(i) * (ff / 4) + 64 * bb + lane, tag_word(q.packed, epoch));
+        if (lane == 0) coh_st64(a.hdtag + qb, tag_word(__float_as_uint(q.d), epoch));
+    }
+    mark(4);
+
+    // ---- down passes, pick by pick, into LDS
+    float* ys = reinterpret_cast<float*>(lds + LY::Y);
+    const int hq_stride = ff + 64;
+    {
+        int cur = -1;
+        Act3<PD> B;
+#pragma unroll
+        for (int j = 0; j < MD; ++j) {
+            if (j < nd) {
+                if (j + WIND < MD && j + WIND < nd) load_pass(j + WIND);
+                const int i = dpick[j];
+                float y = 0.0f;
+                if (did[j] >= 0) {
+                    if (i != cur) {
+                        uint8_t* hq = lds + LY::HQ + i * hq_stride;
+                        if ((i * nq_wg) % NW == wv) {
+                            // this wave holds the workgroup's first pass of pick i: stage the
+                            // pick's Q8_K(h) once all its tagged words are in
+                            const int per = ff / 256;   // tagged words per lane (ff <= 4096: at most 16)
+                            const uint64_t* src = a.hqtag + size_t(i) * (ff / 4) + per * lane;
+                            uint64_t w16[16];
+                            uint64_t dw = 0;
+                            uint32_t polls = 0;
+                            for (;;) {
+#pragma unroll
+                                for (int c = 0; c < 16; ++c)
+                                    if (c < per) w16[c] = coh_ld64(src + c);
+                                if (lane < nbh) dw = coh_ld64(a.hdtag + size_t(i) * nbh + lane);
+                                bool ok = lane >= nbh || uint32_t(dw >> 32) == epoch;
+#pragma unroll
+                                for (int c = 0; c < 16; ++c)
+                                    if (c < per) ok = ok && uint32_t(w16[c] >> 32) == epoch;
+                                if (__all(ok)) break;
+                                if (++polls > kPollLimit) {
+                                    if (lane == 0) set_err(a.err, kDevErrTimeout);
+                                    break;
+                                }
+                                __builtin_amdgcn_s_sleep(2);
+                            }
+#pragma unroll
+                            for (int c = 0; c < 16; ++c)
+                                if (c < per) reinterpret_cast<uint32_t*>(hq)[per * lane + c] = uint32_t(w16[c]);
+                            if (lane < nbh) reinterpret_cast<uint32_t*>(hq + ff)[lane] = uint32_t(dw);
+                            // LDS writes of one wave land in order: the flag goes last
+                            if (lane == 0) __hip_atomic_store(&s_hq_ready[i], epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+                        } else {
+                            uint32_t polls = 0;
+                            while (__hip_atomic_load(&s_hq_ready[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) != epoch) {
+                                if (++polls > kPollLimit) {
+                                    if (lane == 0) set_err(a.err, kDevErrTimeout);
+                                    break;
+                                }
+                                __builtin_amdgcn_s_sleep(1);
+                            }
+                        }
+#pragma unroll
+                        for (int q = 0; q < PD; ++q) {
+                            const int p = lD + LD * q;
+                            const uint4* srcl = reinterpret_cast<const uint4*>(hq + 64 * p);
+#pragma unroll
+                            for (int c = 0; c < 4; ++c) {
+                                const uint4 v = srcl[c];
+                                B.a[q][4 * c] = v.x; B.a[q][4 * c + 1] = v.y; B.a[q][4 * c + 2] = v.z; B.a[q][4 * c + 3] = v.w;
+                            }
+                            B.d[q] = reinterpret_cast<const float*>(hq + ff)[p >> 2];
+                        }
+                        cur = i;
+                    }
+                    y = __fmul_rn(0.125f, gsum<LD>(row_sum<DNT, TM, PD>(lds, L, dm[j].type, rd[j % (WIND + 1)], B, lD, LD)));
+                }
+                if (lD == LD - 1) ys[(wv + NW * j) * RD + rD] = y;
+                if (j == 0) mark(5);
+            }
+        }
+    }
+    mark(6);
+    lds_barrier();
+
+    // ---- fixed-order combine of this workgroup's rows
+    const int nrows = nq_wg * RD;
+    for (int r = t; r < nrows; r += NW * 64) {
+        const int qq = r / RD, rr = r - qq * RD;
+        const int orow = (int(blockIdx.x) + G * qq) * RD + rr;
+        int order[16];
+        for (int i = 0; i < k; ++i) order[i] = i;
+        for (int i = 1; i < k; ++i)
+            for (int j = i; j > 0 && s_ids[order[j]] < s_ids[order[j - 1]]; --j) {
+                const int tmp = order[j]; order[j] = order[j - 1]; order[j - 1] = tmp;
+            }
+        float acc = 0.0f;
+        for (int s2 = 0; s2 < k; ++s2) {
+            const int i = order[s2];
+            acc = fmaf(s_w[i], ys[(i * nq_wg + qq) * RD + rr], acc);
+        }
+        if (a.shared) acc = __fadd_rn(acc, a.shared[orow]);
+        a.out[orow] = acc;
+    }
+    mark(7);
+    if (t == 0 && arrived == uint32_t(G) - 1u) {   // every workgroup has read the epoch word
+        coh_st32(ctl, epoch);
+        coh_st32(ctl + 1, 0u);
+    }
+}
+
+// ---- launcher ------------------------------------------------------------------------------
+template <int NW, int LG, int PG, int LD, int PD, int MG, int MD, int WIN, int WIND, int GUT, int DNT>
+static hipError_t launch3(const Layer3Args& args, int grid, hipStream_t s) {
+    constexpr int RG = 64 / LG, RD = 64 / LD;
+    const int W = grid * NW;
+    const int SG = args.k * (args.ff / RG);
+    const int quads = args.dim / RD;
+    const int nq_wg = (quads + grid - 1) / grid;
+    const int P = args.k * nq_wg;
+    const int nqb = args.k * (args.ff / 256);
+    if ((SG + W - 1) / W > MG || (P + NW - 1) / NW > MD || nqb > W || P * RD > kYStage || grid > quads ||
+        args.ff > 4096 || Lay<GUT | DNT>::HQ + args.k * (args.ff + 64) > kLdsBytes)
+        return hipErrorNotSupported;
+    hipLaunchKernelGGL((layer3_kernel<NW, LG, PG, LD, PD, MG, MD, WIN, WIND, GUT, DNT>), dim3(grid), dim3(NW * 64), 0, s,
+                       args);
+    return hipGetLastError();
+}
+
+// Instances by block-type set: (gate/up types, down types) exactly ({IQ2_XXS},
+// {IQ2_XS}) has its own instance; anything else takes the all-types one.
+template <int NW, int LG, int PG, int LD, int PD, int MG, int MD, int WIN, int WIND>
+static hipError_t launch3_types(const Layer3Args& args, int gu_types, int dn_types, int grid, hipStream_t s) {
+    if (gu_types == 1 && dn_types == 2) return launch3<NW, LG, PG, LD, PD, MG, MD, WIN, WIND, 1, 2>(args, grid, s);
+    return launch3<NW, LG, PG, LD, PD, MG, MD, WIN, WIND, 7, 7>(args, grid, s);
+}
+
+hipError_t launch_layer3(const Layer3Args& args, int gu_types, int dn_types, int cus, hipStream_t s) {
+    if (args.k < 1 || args.k > 16 || args.dim > 4096) return hipErrorNotSupported;
+    int lg, pg, ld, pd;
+    if (!row_shape(args.dim, lg, pg) || !row_shape(args.ff, ld, pd)) return hipErrorNotSupported;
+    const int RD = 64 / ld;
+    const int grid = std::min(cus, args.dim / RD);
+    if (lg == 64 && pg == 1 && ld == 16 && pd == 3)   // 4096 x 3072
+        return launch3_types<8, 64, 1, 16, 3, 9, 3, 3, 1>(args, gu_types, dn_types, grid, s);
+    if (lg == 16 && pg == 1 && ld == 8 && pd == 1)    // 1024 x 512
+        return launch3<8, 16, 1, 8, 1, 6, 2, 3, 1, 7, 7>(args, grid, s);
+    if (lg == 4 && pg == 1 && ld == 4 && pd == 3)     // 256 x 768
+        return launch3<8, 4, 1, 4, 3, 6, 2, 3, 1, 7, 7>(args, grid, s);
+    if (lg == 8 && pg == 1 && ld == 4 && pd == 1)     // 512 x 256
+        return launch3<8, 8, 1, 4, 1, 6, 2, 3, 1, 7, 7>(args, grid, s);
+    if (lg == 4 && pg == 1 && ld == 4 && pd == 1)     // 256 x 256
+        return launch3<8, 4, 1, 4, 1, 6, 2, 3, 1, 7, 7>(args, grid, s);
+    return hipErrorNotSupported;
+}
+
+}  // namespace xl::dev

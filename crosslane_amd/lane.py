@@ -78,6 +78,7 @@ _SIGNATURES = {
     "xl_matvec_async": (_I32, [_P, _I32, _P, _I32, _I32, _P, _P, _P, _P, _ErrP]),
     "xl_profile_begin": (_I32, [_P, _I32, _ErrP]),
     "xl_profile_end": (_I32, [_P, _f32p, _I32, C.POINTER(_I32), C.POINTER(_I32), C.c_char_p, _I32, _ErrP]),
+    "xl_profile_timeline": (_I32, [_P, _u64p, _I32, C.POINTER(_I32), _ErrP]),
     "xl_planar_bytes": (C.c_uint64, [_I32, _I32, _I32]),
     "xl_repack": (_I32, [_I32, _I32, _I32, _P, _P]),
     "xl_restore": (_I32, [_I32, _I32, _I32, _P, _P]),
@@ -272,6 +273,13 @@ class Lane:
         self._call("xl_profile_end", ms, 8, C.byref(ns), C.byref(nc), names, 256)
         keys = names.value.decode().split(",") if ns.value else []
         return {"calls": nc.value, "stages": {k: float(ms[i]) for i, k in enumerate(keys)}}
+
+    def profile_timeline(self) -> np.ndarray:
+        """Per-wave phase stamps (100 MHz) of the last profiled single-launch call: [waves, 32]."""
+        out = np.zeros(1 << 16, np.uint64)
+        n = _I32()
+        self._call("xl_profile_timeline", out, out.size, C.byref(n))
+        return out[: n.value].reshape(-1, 32)
 
     def quantize_q8k_async(self, x, rows: int, k: int, q8k_out, stream=None) -> None:
         self._call("xl_quantize_q8k_async", _ptr(x), rows, k, _ptr(q8k_out), None if stream is None else int(stream))

@@ -141,6 +141,14 @@ int32_t xl_profile_begin(xl_context* ctx, int32_t max_calls, xl_error* err);
 int32_t xl_profile_end(xl_context* ctx, float* stage_ms, int32_t max_stages, int32_t* n_stages, int32_t* n_calls,
                        char* names, int32_t names_bytes, xl_error* err);
 
+/* Per-wave timeline of the last single-launch layer call made while profiling
+ * was active: 8 s_memrealtime stamps (100 MHz) per wave, wave-major over the
+ * grid (zero where a wave did not reach a phase). Phases: 0 prologue loads
+ * issued, 1 loads in, 2 x quantized (barrier), 3 gate/up done, 4 quantizer
+ * duty done, 5 first down pass done, 6 all down passes done, 7 combine done.
+ * A diagnostic aid: it has no counterpart in the reference. */
+int32_t xl_profile_timeline(xl_context* ctx, uint64_t* out, int32_t max_words, int32_t* n_words, xl_error* err);
+
 /* ---- host utilities (no device needed) ------------------------------------ */
 uint64_t xl_planar_bytes(int32_t type, int32_t n, int32_t k);
 int32_t xl_repack(int32_t type, int32_t n, int32_t k, const void* aos, void* planar);

@@ -250,13 +250,14 @@ def test_matvec_any_fp16_scale(probe, orc, t):
     assert max_rel(got, want) < TOL
 
 
-@pytest.mark.parametrize("dim,ff,sig", [(4096, 3072, None), (1024, 512, (17, 17, 16)), (256, 768, (29, 29, 17)),
-                                        (512, 256, (16, 16, 29))])
-def test_fused_layer_equals_separate_launches(orc, dim, ff, sig, monkeypatch):
-    # The fused cooperative kernel and the separate launches share the row
-    # engine and the quantizer, so their outputs must agree bit for bit; the
-    # oracle checks the fused result to the tolerance.
-    step(f"fused vs separate dim={dim} ff={ff} sig={sig}")
+@pytest.mark.parametrize("dim,ff,sig", [(4096, 3072, None), (4096, 3072, (16, 16, 17)), (1024, 512, (17, 17, 16)),
+                                        (256, 768, (29, 29, 17)), (512, 256, (16, 16, 29)), (256, 256, (17, 17, 17))])
+def test_layer_paths_agree(orc, dim, ff, sig, monkeypatch):
+    # The single-launch kernel (path 1), the separate launches (path 0) and the
+    # cooperative kernel (path 2) share the row arithmetic per block but sum
+    # lanes in their own orders, so they agree to the tolerance, and each is
+    # bit-identical run to run; the oracle checks every path.
+    step(f"layer paths dim={dim} ff={ff} sig={sig}")
     E, k = 24, 6
     rng = np.random.default_rng(dim * 7 + ff)
     if sig is None:   # config-3 style mix: per-expert types over the three formats
@@ -265,23 +266,25 @@ def test_fused_layer_equals_separate_launches(orc, dim, ff, sig, monkeypatch):
     else:
         types = types_map(1, E, sig[0], sig[2])
     lanes = {}
-    for fused in ("1", "0"):
-        monkeypatch.setenv("XL_FUSED", fused)
-        lanes[fused] = xl.Lane(dim, ff, 1, E, types, max_picks=8)
-        lanes[fused].generate(seed=77)
+    for path in ("1", "0", "2"):
+        monkeypatch.setenv("XL_LAYER_PATH", path)
+        lanes[path] = xl.Lane(dim, ff, 1, E, types, max_picks=8)
+        lanes[path].generate(seed=77)
     try:
         for trial in range(3):
             ids, w = route(rng.standard_normal(E).astype(np.float32), k)
             x = rng.standard_normal(dim).astype(np.float32)
             shared = rng.standard_normal(dim).astype(np.float32) if trial == 1 else None
-            a = lanes["1"].layer_forward(0, ids, w, x, shared)
-            b = lanes["0"].layer_forward(0, ids, w, x, shared)
-            assert np.array_equal(a.view(np.uint32), b.view(np.uint32)), trial
             rows = []
             for e in ids:
                 tt = tuple(int(v) for v in types[0, e])
                 rows.append(orc.expert(tt, *orc.gen_expert(tt, 77, 0, int(e), dim, ff), dim, ff, x))
-            assert max_rel(a, orc.combine(ids, w, np.stack(rows), shared)) < TOL
+            want = orc.combine(ids, w, np.stack(rows), shared)
+            for path, lane in lanes.items():
+                got = lane.layer_forward(0, ids, w, x, shared)
+                again = lane.layer_forward(0, ids, w, x, shared)
+                assert np.array_equal(got.view(np.uint32), again.view(np.uint32)), (path, trial)
+                assert max_rel(got, want) < TOL, (path, trial, max_rel(got, want))
     finally:
         for lane in lanes.values():
             lane.close()

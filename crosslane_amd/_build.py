@@ -8,8 +8,8 @@ import sys
 PKG = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(PKG, "csrc")
 LIB = os.path.join(PKG, "libcrosslane.so")
-SOURCES = ["xl_kernels.hip", "xl_layer.hip", "xl_api.cpp"]
-HEADERS = ["xl_format.hpp", "xl_rows.hpp", "xl_internal.hpp", "xl_codebooks.inc", "exports.map"]
+SOURCES = ["xl_kernels.hip", "xl_layer.hip", "xl_stream.hip", "xl_api.cpp"]
+HEADERS = ["xl_format.hpp", "xl_rows.hpp", "xl_internal.hpp", "xl_dev.hpp", "xl_codebooks.inc", "exports.map"]
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = os.environ.get("XL_OFFLOAD_ARCH", "gfx950")

@@ -148,10 +148,13 @@ struct xl_context {
     xl::ExpertDesc* d_descs = nullptr;
     uint64_t payload = 0, allocated = 0;
     int grid_gu = 0, grid_down = 0;
-    // Layer path: 1 = single launch (xl_layer.hip, default), 2 = cooperative
-    // fused kernel, 0 = separate launches. XL_LAYER_PATH selects; shapes
-    // without a single-launch instance use separate launches.
+    // Layer path: 1 = single launch (default: the streaming kernel of
+    // xl_stream.hip for IQ2_XXS gate/up + IQ2_XS down layers, else the
+    // all-types kernel of xl_layer.hip), 3 = the all-types single launch only,
+    // 2 = cooperative fused kernel, 0 = separate launches. XL_LAYER_PATH
+    // selects; shapes without a single-launch instance use separate launches.
     int path = 1;
+    float* hbuf = nullptr;      // streaming kernel's h exchange (2 x kHBufWords, sentinel-filled)
     uint32_t* sync = nullptr;   // counters of the cooperative fused kernel
     uint64_t* htag = nullptr;   // single-launch handoff buffers (Layer3Args)
     uint64_t* hqtag = nullptr;
@@ -273,12 +276,13 @@ void enqueue_layer(xl_context* ctx, int32_t layer, const int32_t* d_ids, const f
     const int gu_mask = ctx->gu_mask[size_t(layer)], dn_mask = ctx->dn_mask[size_t(layer)];
     Marks mark(ctx, s);
     mark("");
-    if (ctx->path == 1 && !g_dbg && !u_dbg) {
+    if ((ctx->path == 1 || ctx->path == 3) && !g_dbg && !u_dbg) {
         xl::Layer3Args a{};
         a.descs = descs; a.ids = d_ids; a.w = d_w; a.x = d_x; a.shared = d_shared; a.out = d_out;
         a.k = k; a.n_experts = E; a.dim = dim; a.ff = ff;
         a.htag = ctx->htag; a.hqtag = ctx->hqtag; a.hdtag = ctx->hdtag; a.ctl = ctx->ctl; a.err = ctx->err_flag;
         a.tables = ctx->tables;
+        a.hbuf = ctx->hbuf;
         if (ctx->prof.on && ctx->prof.calls <= ctx->prof.max_calls) {
             a.trace = ctx->timeline;
             hip_check(hipMemsetAsync(ctx->timeline, 0, size_t(ctx->cus) * 16 * 32 * 8, s), "timeline clear");
@@ -290,7 +294,13 @@ void enqueue_layer(xl_context* ctx, int32_t layer, const int32_t* d_ids, const f
             for (int r = 0; r < 3; ++r) { a.roff[r] = ls.roff[r]; a.rtype[r] = ls.rtype[r]; }
         }
         if (d_out) {
-            const hipError_t e = xl::dev::launch_layer3(a, gu_mask, dn_mask, ctx->cus, s);
+            hipError_t e = hipErrorNotSupported;
+            if (ctx->path == 1 && gu_mask == 1 && dn_mask == 2) {
+                e = xl::dev::launch_stream(a, ctx->cus, s);
+                if (e != hipSuccess && e != hipErrorNotSupported) hip_check(e, "streaming layer");
+                (void)hipGetLastError();
+            }
+            if (e == hipErrorNotSupported) e = xl::dev::launch_layer3(a, gu_mask, dn_mask, ctx->cus, s);
             if (e == hipSuccess) {
                 if (a.trace) ctx->timeline_words = uint64_t(ctx->cus) * 16 * 32;
                 mark("layer");
@@ -393,6 +403,7 @@ int32_t xl_open(uint32_t abi_version, const xl_config* cfg, xl_context** out, xl
             {reinterpret_cast<void**>(&ctx->hqtag), uint64_t(P) * ff * 2},
             {reinterpret_cast<void**>(&ctx->hdtag), uint64_t(P) * (ff / 256) * 8},
             {reinterpret_cast<void**>(&ctx->ctl), 256},
+            {reinterpret_cast<void**>(&ctx->hbuf), uint64_t(2) * xl::kHBufWords * 4},
             {reinterpret_cast<void**>(&ctx->tables), uint64_t(xl::kLayer3TableBytes)},
             {reinterpret_cast<void**>(&ctx->timeline), uint64_t(ctx->cus) * 16 * 32 * 8},
         };
@@ -417,10 +428,11 @@ int32_t xl_open(uint32_t abi_version, const xl_config* cfg, xl_context** out, xl
         hip_check(hipMemset(ctx->hdtag, 0, size_t(P) * (ff / 256) * 8), "tag clear");
         hip_check(hipMemset(ctx->hqtag, 0, size_t(P) * ff * 2), "tag clear");
         hip_check(hipMemset(ctx->ctl, 0, 256), "epoch clear");
+        hip_check(hipMemset(ctx->hbuf, 0xff, size_t(2) * xl::kHBufWords * 4), "h exchange fill");
         const std::vector<uint64_t> tab = layer_tables();
         hip_check(hipMemcpy(ctx->tables, tab.data(), tab.size() * 8, hipMemcpyHostToDevice), "table upload");
         ctx->path = env_int("XL_LAYER_PATH", 1);
-        need(ctx->path >= 0 && ctx->path <= 2, XL_E_ARG, "XL_LAYER_PATH must be 0, 1 or 2");
+        need(ctx->path >= 0 && ctx->path <= 3, XL_E_ARG, "XL_LAYER_PATH must be 0, 1, 2 or 3");
         *out = ctx;
     });
     if (rc != XL_OK && ctx) xl_close(ctx);

@@ -86,8 +86,10 @@ struct Layer3Args {
     uint64_t estride;
     uint64_t roff[3];
     int rtype[3];
-    uint64_t* trace;            // null, or 8 timestamps (s_memrealtime) per wave of the grid
+    uint64_t* trace;            // null, or 32 timestamps (s_memrealtime) per wave of the grid
+    float* hbuf;                // streaming kernel: 2 x kHBufWords h words, sentinel-filled (see xl_stream.hip)
 };
+constexpr int kHBufWords = 16 * 4096;      // k_max * ff_max
 constexpr int kLayer3TableBytes = 24576;   // expanded codebooks of the single-launch kernel
 
 namespace dev {
@@ -95,6 +97,9 @@ namespace dev {
 // gu_types / dn_types: block types among the layer's gate/up / down matrices
 // (bits 1 IQ2_XXS, 2 IQ2_XS, 4 IQ1_M) select the kernel instance.
 hipError_t launch_layer3(const Layer3Args& args, int gu_types, int dn_types, int cus, hipStream_t s);
+// Streaming layer for IQ2_XXS gate/up + IQ2_XS down: hipErrorNotSupported when
+// (dim, ff, k) has no instance.
+hipError_t launch_stream(const Layer3Args& args, int cus, hipStream_t s);
 // Fused layer: returns hipErrorNotSupported when (dim, ff) has no fused
 // instance or the device cannot hold the cooperative grid.
 hipError_t launch_layer_fused(const LayerArgs& args, int type_mask, int cus, hipStream_t s);

@@ -1,0 +1,675 @@
+// The routed-expert layer in one streaming launch, for layers whose gate/up
+// matrices are all IQ2_XXS and whose down matrices are all IQ2_XS (gfx950).
+//
+// One workgroup of NW waves per CU. The decode work per 8-weight group is one
+// grid lookup, one sign lookup, two v_xad and two v_dot4; everything else is
+// laid out so that nothing more is needed:
+//
+//   codebooks  bank-interleaved copies whose row stride is 256 bytes, so a
+//              lookup address is one v_perm_b32 of the index byte and the
+//              lane's copy offset: IQ2_XXS grid 32 copies (conflict-free b64),
+//              sign rows 16 copies (conflict-free b128). The sign table has 256
+//              rows, indexed by the whole byte (bit 7 is ignored: it carries a
+//              scale bit for IQ2_XXS and a grid bit for IQ2_XS).
+//   gate/up    slot s of the k*ff rows (pick-major) belongs to wave s mod W;
+//              the rows' SiLU runs once per batch of kBatch slots, one lane
+//              per slot, and h goes out as plain 32-bit words.
+//   h exchange two buffers of k_max*ff_max floats, used by alternate launches
+//              of this kernel. A buffer holds the sentinel 0xffffffff (a NaN no
+//              arithmetic produces; a computed h with those bits is stored as
+//              the canonical NaN) in every word before its launch: each launch
+//              refills the other buffer, which the previous launch used.
+//              Readers poll for non-sentinel words, so no fence is needed.
+//   down       workgroup g owns output row groups {g, g+G, ...} of every pick;
+//              its passes (row group, pick) are dealt to its waves in pick
+//              order, one pass per wave per step. Before step j the workgroup
+//              quantizes the h of the picks that step needs (Q8_K, one block
+//              per wave at a time) into LDS, from loads issued one step ahead:
+//              early steps need early picks, whose h is complete while later
+//              picks are still being produced.
+//   combine    fixed order (ascending expert id, sequential fma, then + shared;
+//              engine/strata/warm/runtime.cpp:183-188), per workgroup.
+//
+// Waits only point backwards (down waits on gate/up, which waits on nothing)
+// and the grid is at most one workgroup per CU, so every workgroup runs once
+// the CUs are free and the grid drains. Every wait is bounded: on expiry the
+// kernel raises kDevErrTimeout and finishes.
+//
+// The launch parity comes from a device word advanced by the last workgroup to
+// arrive (an arrival counter), never from the host, so a captured launch can
+// be replayed.
+#include <hip/hip_runtime.h>
+
+#include <utility>
+
+#include "xl_dev.hpp"
+
+namespace xl::dev {
+namespace {
+
+// f.template operator()<J>() for J = 0 .. N-1: the index is a constant in the
+// body, so ring slots indexed by it stay in registers (a runtime loop index,
+// even of a loop unrolled later, leaves them to memory).
+template <int N, class F>
+__device__ __forceinline__ void static_for(F&& f) {
+    [&]<int... Js>(std::integer_sequence<int, Js...>) { (f.template operator()<Js>(), ...); }(std::make_integer_sequence<int, N>{});
+}
+
+// ---- LDS map (bytes) -------------------------------------------------------------------------
+constexpr int kS_SGN = 0;          // sign masks: 256 rows x 32 copies x 8 B {M.lo, M.hi}
+constexpr int kS_XXS = 65536;      // IQ2_XXS grid: 256 x 32 copies x 8 B (gate/up phase)
+constexpr int kS_HQ = 65536;       // Q8_K(h) of the picks (down phase): pick i at kS_HQ + i * (ff + 64)
+constexpr int kS_HQBytes = 65536;
+constexpr int kS_XS = 131072;      // IQ2_XS grid: 512 x 4 copies x 8 B
+constexpr int kS_XQ = 147456;      // Q8_K(x): dim quants, then 16 block scales (gate/up phase)
+constexpr int kS_Y = 147456;       // y staging, kS_YFloats floats (down phase)
+constexpr int kS_YFloats = 1024;
+constexpr int kS_Bytes = 151616;
+static_assert(kS_XQ + 4096 + 64 <= kS_Bytes && kS_Y + 4 * kS_YFloats <= kS_Bytes, "LDS map");
+
+// Global codebooks (one copy each; see layer_tables in xl_api.cpp).
+constexpr int kG_XXS = 2048, kG_XS = 4096;
+
+struct Smem {
+    uint8_t b[kS_Bytes];   // first, so that its LDS address is 0 and table bases fold into offsets
+    int ids[16];
+    float w[16];
+    int order[16];         // picks by ascending expert id (stable: equal ids keep pick order)
+    uint32_t parity;
+};
+
+// Lane constants of the lookups: byte 0 is the lane's copy offset, byte 2 the
+// table base in 64-KB units; v_perm_b32 puts the index byte in byte 1.
+__device__ __forceinline__ uint32_t perm(uint32_t idx_word, uint32_t lane_word, uint32_t sel) {
+    return __builtin_amdgcn_perm(idx_word, lane_word, sel);
+}
+// selector: byte0 <- lane_word.byte0, byte1 <- idx_word.byte(q), byte2 <- lane_word.byte2, byte3 <- 0
+__device__ __forceinline__ constexpr uint32_t sel_b(int q) { return 0x0C020400u + (uint32_t(q) << 8); }
+
+constexpr uint32_t kSentinel = 0xffffffffu;
+constexpr uint32_t kQNaN = 0x7fc00000u;
+
+// Sign row r: M has 0xff in the bytes of negative weights (7 sign bits of r
+// plus their parity, as ksigns_iq2xs). Two ways to apply it, one op per dword:
+// select between a and -a (v_bfi_b32: the activation takes the sign), or
+// (g ^ M) + (M & 0x01010101), which negates exactly those bytes of g (grid
+// bytes are 1..127, so no carry crosses a byte).
+__device__ __forceinline__ uint2 sign_row(uint32_t r) {
+    const uint32_t s7 = r & 127u;
+    const uint32_t s8 = s7 | ((__builtin_popcount(s7) & 1u) << 7);
+    const uint32_t clo = ((s8 & 15u) * 0x00204081u) & 0x01010101u;
+    const uint32_t chi = ((s8 >> 4) * 0x00204081u) & 0x01010101u;
+    return make_uint2(clo * 255u, chi * 255u);
+}
+__device__ __forceinline__ uint32_t bfi(uint32_t m, uint32_t x, uint32_t y) { return (m & x) | (~m & y); }   // v_bfi_b32
+// Bytewise two's-complement negation: (~x + 1) per byte = (x ^ 0xff..) + 0x01.. with no
+// carry across bytes except for a 0x00 byte, whose carry is masked off byte by byte.
+__device__ __forceinline__ uint32_t neg_bytes(uint32_t x) {
+    const uint32_t lo = ((x & 0x00ff00ffu) ^ 0x00ff00ffu) + 0x00010001u;   // bytes 0, 2 (a carry lands in 1, 3)
+    const uint32_t hi = ((x & 0xff00ff00u) ^ 0xff00ff00u) + 0x01000100u;   // bytes 1, 3
+    return (lo & 0x00ff00ffu) | (hi & 0xff00ff00u);
+}
+
+// h = silu(g) * u with the hardware exp2 and reciprocal (about 1 ulp each): h
+// only feeds Q8_K(h), and the layer output is held to a relative 1e-3, not to
+// the bits of the reference's expf. g -> -inf gives -0, g -> +inf gives g * u.
+__device__ __forceinline__ float silu_fast(float g, float u) {
+    const float e = __builtin_amdgcn_exp2f(__fmul_rn(g, -1.4426950408889634f));
+    return __fmul_rn(__fmul_rn(g, __builtin_amdgcn_rcpf(__fadd_rn(1.0f, e))), u);
+}
+
+// ---- pair decoders -------------------------------------------------------------------------
+// Codebook rows of one pair: 8 grid rows and 8 sign masks. The decoders are
+// split into lookups and arithmetic so that a slot issues both of its rows'
+// lookups before either row's arithmetic waits on them.
+struct Looks {
+    uint2 g[8], m[8];
+};
+// IQ2_XXS pair (w0..3: two sub-blocks of {4 grid bytes, 4 sign|scale-bit bytes}).
+__device__ __forceinline__ Looks look_xxs(const uint8_t* lds, uint32_t lo_g, uint32_t lo_s, const uint32_t* w) {
+    Looks L;
+#pragma unroll
+    for (int s = 0; s < 2; ++s)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            L.g[4 * s + q] = *reinterpret_cast<const uint2*>(lds + perm(w[2 * s], lo_g, sel_b(q)));
+            L.m[4 * s + q] = *reinterpret_cast<const uint2*>(lds + perm(w[2 * s + 1], lo_s, sel_b(q)));
+        }
+    return L;
+}
+// Against 64 Q8_K quants a (and their negations na): the exact integer sum of
+// (2s+1) * grid * sign * q over the pair (q8k_core.hpp:96-114 regrouped per
+// sub-block; the sign is applied to q).
+__device__ __forceinline__ int sum_xxs(const Looks& L, const uint32_t* w, const uint32_t* a, const uint32_t* na) {
+    int acc[2] = {0, 0};
+#pragma unroll
+    for (int s = 0; s < 2; ++s)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const int e = 4 * s + q, k0 = 8 * s + 2 * q;
+            acc[s] = sdot4(L.g[e].x, bfi(L.m[e].x, na[k0], a[k0]), acc[s]);
+            acc[s] = sdot4(L.g[e].y, bfi(L.m[e].y, na[k0 + 1], a[k0 + 1]), acc[s]);
+        }
+    return __mul24(acc[0], xxs_sc(w[1])) + __mul24(acc[1], xxs_sc(w[3]));
+}
+// IQ2_XS pair (w0..3: 8 codes {sign7 | grid9 << 7}, sc: the pair's two scale
+// bytes): the exact integer sum with the 16-weight scales (q8k_core.hpp:116-140).
+__device__ __forceinline__ int pair_xs(const uint8_t* lds, uint32_t lo_x, uint32_t lo_s, const uint32_t* w, uint32_t sc,
+                                       const uint32_t* a) {
+    uint2 g[8];
+    uint2 m[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+        const uint32_t h = e & 1;
+        // grid row * 32 = (code >> 7) << 5: one shift and one v_and_or_b32 with the lane's copy
+        const uint32_t sh = h ? (w[e >> 1] >> 18) : (w[e >> 1] >> 2);
+        g[e] = *reinterpret_cast<const uint2*>(lds + ((sh & 0x3fe0u) | lo_x));
+        m[e] = *reinterpret_cast<const uint2*>(lds + perm(w[e >> 1], lo_s, sel_b(2 * h)));
+    }
+    int total = 0;
+#pragma unroll
+    for (int s = 0; s < 2; ++s) {
+        int lo = 0, hi = 0;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const int e = 4 * s + q;
+            int& acc = q < 2 ? lo : hi;
+            acc = sdot4(xad(g[e].x, m[e].x, m[e].x & 0x01010101u), a[8 * s + 2 * q], acc);
+            acc = sdot4(xad(g[e].y, m[e].y, m[e].y & 0x01010101u), a[8 * s + 2 * q + 1], acc);
+        }
+        const uint32_t byte = (sc >> (8 * s)) & 255u;
+        total += __mul24(lo, int(2u * (byte & 15u) + 1u)) + __mul24(hi, int(2u * (byte >> 4) + 1u));
+    }
+    return total;
+}
+
+template <int P>
+struct Act {
+    uint32_t a[P][16];
+    float d[P];
+};
+// Activations of pairs lp, lp + L, ... from a Q8_K vector in LDS (quants at
+// base, block scales at base + scl).
+template <int P>
+__device__ __forceinline__ void load_act(Act<P>& A, const uint8_t* lds, int base, int scl, int lp, int L) {
+#pragma unroll
+    for (int q = 0; q < P; ++q) {
+        const int p = lp + L * q;
+        const uint4* src = reinterpret_cast<const uint4*>(lds + base + 64 * p);
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+            const uint4 v = src[c];
+            A.a[q][4 * c] = v.x; A.a[q][4 * c + 1] = v.y; A.a[q][4 * c + 2] = v.z; A.a[q][4 * c + 3] = v.w;
+        }
+        A.d[q] = reinterpret_cast<const float*>(lds + base + scl)[p >> 2];
+    }
+}
+
+// Coherent (sc1) 16-byte load of 4 h words; a sentinel word means "not yet".
+__device__ __forceinline__ uint4 h_load(const float* hb, uint32_t word) {
+    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc((void*)hb, (short)0, -1, 0x00020000);
+    const v4u32 v = __builtin_amdgcn_raw_buffer_load_b128(rs, word * 4, 0, 16);   // per-lane offset: voffset
+    return make_uint4(v.x, v.y, v.z, v.w);
+}
+__device__ __forceinline__ bool h_ready(const uint4& v) {
+    return (v.x != kSentinel) & (v.y != kSentinel) & (v.z != kSentinel) & (v.w != kSentinel);
+}
+
+// ---- Q8_K of NB blocks at once ---------------------------------------------------------------
+// Block m is held by the wave as v[m] (lane l owns values 4l..4l+3). Bit-exact
+// with q8k_core.hpp:30-38: mx is the first value of largest magnitude (found
+// as the wave's largest magnitude, then the lowest position holding it), is =
+// -127/mx, q = min(127, nearest(is * v)), d = 1/is; an all-zero block gives
+// d = 0 and q = 0. The two divisions run once for all NB blocks (lane m
+// divides for block m); nearest is v_rndne (exact for |is * v| < 2^22) and
+// the quants are packed as q + 128 bytes by v_cvt_pk_u8_f32 (exact integers).
+template <int CTRL>
+__device__ __forceinline__ uint32_t umax_dpp(uint32_t a) {   // lanes the pattern leaves out keep a
+    return max(a, uint32_t(__builtin_amdgcn_update_dpp(int(a), int(a), CTRL, 0xF, 0xF, false)));
+}
+// The wave's largest magnitude as a bit pattern: magnitudes of floats order as
+// their bits do, so integer max needs no NaN canonicalization (a NaN or an
+// infinity wins and is caught by the finiteness test on the result).
+__device__ __forceinline__ uint32_t wave_umax(uint32_t a) {
+    a = umax_dpp<0xB1>(a);
+    a = umax_dpp<0x4E>(a);
+    a = umax_dpp<0x141>(a);
+    a = umax_dpp<0x140>(a);    // every lane: its row's max
+    a = max(a, uint32_t(__builtin_amdgcn_update_dpp(0, int(a), 0x142, 0xA, 0xF, false)));   // rows 1, 3
+    a = max(a, uint32_t(__builtin_amdgcn_update_dpp(0, int(a), 0x143, 0xC, 0xF, false)));   // rows 2, 3
+    return uint32_t(__builtin_amdgcn_readlane(int(a), 63));
+}
+// Returns false if a value of blocks 0..nvalid-1 is not finite (the others may hold anything).
+// |is * v| <= 127 (1 + 2^-24)^2 < 127.5 for every v of the block, so nearest(is * v)
+// never exceeds 127 and the reference's min(127, .) never applies.
+template <int NB>
+__device__ __forceinline__ bool q8k_blocks(const uint4 (&hv)[NB], int nvalid, int lane, uint32_t (&packed)[NB],
+                                           float (&d)[NB]) {
+    bool fin = true;
+    uint32_t am[NB];
+    float mxv = 0.0f;
+#pragma unroll
+    for (int m = 0; m < NB; ++m) {
+        // opaque copies: a select chain over the block's words would otherwise be
+        // turned into an indexed load from a stack copy of the block
+        uint32_t x0 = hv[m].x, x1 = hv[m].y, x2 = hv[m].z, x3 = hv[m].w;
+        asm volatile("" : "+v"(x0), "+v"(x1), "+v"(x2), "+v"(x3));
+        const uint32_t a0 = x0 & 0x7fffffffu, a1 = x1 & 0x7fffffffu;
+        const uint32_t a2 = x2 & 0x7fffffffu, a3 = x3 & 0x7fffffffu;
+        am[m] = wave_umax(max(max(a0, a1), max(a2, a3)));
+        fin = fin & ((m >= nvalid) | (am[m] <= 0x7f7fffffu));
+        const bool e0 = a0 == am[m], e1 = a1 == am[m], e2 = a2 == am[m];
+        const uint32_t sel = e0 ? x0 : e1 ? x1 : e2 ? x2 : x3;
+        const uint64_t hit = __builtin_amdgcn_ballot_w64(e0 | e1 | e2 | (a3 == am[m]));
+        const int first = int(__builtin_ctzll(hit | (uint64_t(1) << 63)));
+        const float mx = __uint_as_float(uint32_t(__builtin_amdgcn_readlane(int(sel), first)));
+        mxv = lane == m ? mx : mxv;
+    }
+    const float isv = __fdiv_rn(-127.0f, mxv);
+    const float dv = __fdiv_rn(1.0f, isv);
+#pragma unroll
+    for (int m = 0; m < NB; ++m) {
+        const float is = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(isv), m));
+        const uint32_t vb[4] = {hv[m].x, hv[m].y, hv[m].z, hv[m].w};
+        uint32_t p = 0;
+#pragma unroll
+        for (int j = 0; j < 4; ++j)   // q + 128 in 1..255, an exact integer: the byte conversion is exact
+            p = __builtin_amdgcn_cvt_pk_u8_f32(__fadd_rn(__builtin_rintf(__fmul_rn(is, __uint_as_float(vb[j]))), 128.0f), j, p);
+        const bool zero = am[m] == 0u;
+        packed[m] = zero ? 0u : p ^ 0x80808080u;
+        d[m] = zero ? 0.0f : __int_as_float(__builtin_amdgcn_readlane(__float_as_int(dv), m));
+    }
+    return fin;
+}
+
+// ---- the kernel ----------------------------------------------------------------------------
+// LG x PG: lanes per gate/up row and pairs per lane (LG * PG * 64 == dim);
+// LD x PD: the same for down rows (LD * PD * 64 == ff). MG / MD: most gate/up
+// slots / down passes per wave; WIN: gate/up slots in flight per wave; WIND:
+// down passes in flight; MQ: most Q8_K(h) blocks one wave quantizes per step.
+constexpr int kBatch = 3;   // gate/up slots per SiLU batch
+template <int NW, int LG, int PG, int LD, int PD, int MG, int MD, int WIN, int WIND, int MQ>
+__global__ __launch_bounds__(NW * 64, 1) void stream_kernel(Layer3Args a) {
+    static_assert(WIN <= MG && WIND <= MD && WIND <= MG && MG <= 32 && MD <= 32, "prefetch depths, metadata lanes");
+    __shared__ __attribute__((aligned(16))) Smem sm;
+    uint8_t* const lds = sm.b;
+    constexpr int RG = 64 / LG, RD = 64 / LD;
+    const int t = threadIdx.x, lane = t & 63;
+    const int wv = __builtin_amdgcn_readfirstlane(t >> 6);
+    const int G = gridDim.x, W = G * NW, gw = blockIdx.x * NW + wv;
+    const int k = a.k, ff = a.ff, dim = a.dim;
+    const int lG = lane % LG, rG = lane / LG, lD = lane % LD, rD = lane / LD;
+    const int nbx = dim / 256, nbh = ff / 256;
+    auto mark = [&](int n) {
+        if (a.trace && lane == 0) a.trace[size_t(gw) * 32 + n] = __builtin_amdgcn_s_memrealtime();
+    };
+
+    // ---- this wave's work: gate/up slots gw + W*j, down passes wv + NW*j (pick-major)
+    const int sppG = ff / RG, SG = k * sppG;
+    const int ng = SG > gw ? min(MG, (SG - gw + W - 1) / W) : 0;
+    const int quads = dim / RD;
+    const int nq_wg = quads > int(blockIdx.x) ? (quads - int(blockIdx.x) + G - 1) / G : 0;
+    const int P = k * nq_wg;
+    const int nd = P > wv ? min(MD, (P - wv + NW - 1) / NW) : 0;
+    // Slot and pass metadata, computed lane-parallel and kept in one register:
+    // lane j < 32 holds gate/up slot j, lane 32 + j down pass j, packed as
+    // expert << 16 | pick << 12 | first row (bad ids read expert 0 and are
+    // masked out). A use reads its lane back (v_readlane), so the scalar
+    // registers stay free for the loads' addresses.
+    const int idl = a.ids[lane < k ? lane : k - 1];   // unconditional loads keep the wait counts exact
+    const int idv = lane < k ? idl : -1;
+    uint32_t meta;
+    uint64_t okmask;   // bit j: slot j is this wave's with a valid id; bit 32 + j: pass j likewise
+    {
+        const bool isd = lane >= 32;
+        const int j = lane & 31;
+        const int n = isd ? nd : ng;
+        const int jj = j < n ? j : n > 0 ? n - 1 : 0;   // past the last: repeat a valid row
+        const int unit = isd ? wv + NW * jj : gw + W * jj;
+        const int per = isd ? nq_wg : sppG;
+        const int pick = n > 0 ? unit / per : 0;
+        const int row = isd ? (n > 0 ? (int(blockIdx.x) + G * (unit - pick * nq_wg)) * RD : 0)
+                            : (unit - pick * sppG) * RG;
+        const int id = __shfl(idv, min(pick, 15));
+        const bool ok = n > 0 && id >= 0 && id < a.n_experts;
+        meta = (uint32_t(ok ? id : 0) << 16) | (uint32_t(min(pick, 15)) << 12) | uint32_t(row);
+        okmask = __builtin_amdgcn_ballot_w64(ok && j < n);
+    }
+    auto gsl = [&](int j) { return uint32_t(__builtin_amdgcn_readlane(int(meta), j)); };
+    auto dsl = [&](int j) { return uint32_t(__builtin_amdgcn_readlane(int(meta), 32 + j)); };
+    auto dpick = [&](int j) { return int((dsl(j) >> 12) & 15u); };
+    const uint32_t gok = uint32_t(okmask), dok = uint32_t(okmask >> 32);
+    // h word of slot j's first row (pick * ff + row = slot * RG), or -2^30 when the
+    // slot is not this wave's
+    auto hrow = [&](int j) { return j < ng ? (gw + W * j) * RG : -(1 << 30); };
+    // regular layer: matrix (e, role) at slab + e * estride + roff[role]; plane offsets shared
+    uint32_t go1, go2, do1, do2;
+    plane_offs(kIQ2_XXS, uint64_t(ff) * uint64_t(nbx), go1, go2);
+    plane_offs(kIQ2_XS, uint64_t(dim) * uint64_t(nbh), do1, do2);
+    auto matrix = [&](int e, int role, uint32_t o1, uint32_t o2, int type, int nb) {
+        return MRef{a.slab + uint64_t(e) * a.estride + a.roff[role], o1, o2, type, nb};
+    };
+
+    // ---- codebook rows and x first (they need no ids), then the first slots. The
+    // rows come into registers (plain loads: waiting for them does not wait for
+    // the slot loads issued after them).
+    constexpr int NT = NW * 64;
+    constexpr int NX = (4096 + NT - 1) / NT, NS = (1024 + NT - 1) / NT;   // 16-byte chunks per thread: XXS, XS
+    uint2 vx[NX], vs[NS];
+    {
+        const uint2* gx = reinterpret_cast<const uint2*>(reinterpret_cast<const uint8_t*>(a.tables) + kG_XXS);
+        const uint2* gs = reinterpret_cast<const uint2*>(reinterpret_cast<const uint8_t*>(a.tables) + kG_XS);
+#pragma unroll
+        for (int i = 0; i < NX; ++i) vx[i] = gx[min(t + NT * i, 4095) >> 4];   // chunk c: row c / 16, copies 2(c % 16), +1
+#pragma unroll
+        for (int i = 0; i < NS; ++i) vs[i] = gs[min(t + NT * i, 1023) >> 1];   // chunk c: row c / 2, copies 2(c % 2), +1
+    }
+    constexpr int UX = (16 + NW - 1) / NW;
+    float4 xv[UX];
+#pragma unroll
+    for (int u = 0; u < UX; ++u) {
+        const int b = wv + NW * u;
+        xv[u] = reinterpret_cast<const float4*>(a.x + 256 * (b < nbx ? b : 0))[lane];
+    }
+    const float cw = a.w[lane < k ? lane : k - 1];
+    uint32_t* ctl = a.ctl + 2;   // [0] parity source: launches of this kernel so far, [1] arrivals
+    const uint32_t e_prev = coh_ld32(ctl);
+
+    Raw3 rg[WIN][PG], ru[WIN][PG];
+    auto load_slot = [&]<int j>() {
+        constexpr int b = j % WIN;
+        const uint32_t m = gsl(j);
+        const int row0 = int(m & 0xfffu), e = int(m >> 16);
+#pragma unroll
+        for (int q = 0; q < PG; ++q) {
+            load_pair_t<1>(rg[b][q], matrix(e, 0, go1, go2, kIQ2_XXS, nbx), row0, rG, lG + LG * q);
+            load_pair_t<1>(ru[b][q], matrix(e, 1, go1, go2, kIQ2_XXS, nbx), row0, rG, lG + LG * q);
+        }
+    };
+    // Every wave issues the same loads whatever its share (idle slots and passes
+    // re-read valid rows and are discarded), so every wait count is exact.
+    static_for<WIN>([&]<int j>() { load_slot.template operator()<j>(); });
+    mark(0);
+
+    // ---- sign rows (computed), grid copies, Q8_K(x): LDS writes, one barrier
+#pragma unroll
+    for (int i = 0; i < NX; ++i) {
+        const int c = t + NT * i;   // 16-byte chunk: row c / 16, copy c % 16
+        if (c < 4096) {   // chunk c: sign row c / 16, copies 2(c % 16), +1
+            const uint2 r = sign_row(uint32_t(c) >> 4);
+            *reinterpret_cast<uint4*>(lds + kS_SGN + 16 * c) = make_uint4(r.x, r.y, r.x, r.y);
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < NX; ++i)
+        if (t + NT * i < 4096)
+            *reinterpret_cast<uint4*>(lds + kS_XXS + 16 * (t + NT * i)) = make_uint4(vx[i].x, vx[i].y, vx[i].x, vx[i].y);
+#pragma unroll
+    for (int i = 0; i < NS; ++i)
+        if (t + NT * i < 1024)
+            *reinterpret_cast<uint4*>(lds + kS_XS + 16 * (t + NT * i)) = make_uint4(vs[i].x, vs[i].y, vs[i].x, vs[i].y);
+    mark(1);
+    {
+        uint4 xb[UX];
+        uint32_t xp[UX];
+        float xd[UX];
+#pragma unroll
+        for (int u = 0; u < UX; ++u)
+            xb[u] = make_uint4(__float_as_uint(xv[u].x), __float_as_uint(xv[u].y), __float_as_uint(xv[u].z),
+                               __float_as_uint(xv[u].w));
+        const bool fin = q8k_blocks<UX>(xb, nbx > wv ? (nbx - wv + NW - 1) / NW : 0, lane, xp, xd);
+        if (!fin && lane == 0) set_err(a.err, kDevErrNonFinite);
+#pragma unroll
+        for (int u = 0; u < UX; ++u) {
+            const int b = wv + NW * u;
+            if (b < nbx) {
+                reinterpret_cast<uint32_t*>(lds + kS_XQ + 256 * b)[lane] = xp[u];
+                if (lane == 0) reinterpret_cast<float*>(lds + kS_XQ + 4096)[b] = xd[u];
+            }
+        }
+    }
+    if (wv == 0) {
+        int rank = 0;   // the combine order (engine/strata/warm/runtime.cpp:183-188)
+        for (int j = 0; j < k; ++j) {
+            const int idj = __builtin_amdgcn_readlane(idv, j);
+            rank += (idj < idv) | ((idj == idv) & (j < lane));
+        }
+        if (lane < k) {
+            sm.ids[lane] = idv;
+            sm.w[lane] = cw;
+            sm.order[rank] = lane;
+        }
+    }
+    if (t == 0) sm.parity = (e_prev + 1u) & 1u;
+    lds_barrier();
+    const uint32_t parity = __builtin_amdgcn_readfirstlane(sm.parity);   // uniform: keeps buffer bases scalar
+    float* const hcur = a.hbuf + size_t(parity) * kHBufWords;
+    // Arrival: the last workgroup to arrive advances the launch count at its end.
+    uint32_t arrived = 0;
+    if (t == 0) arrived = __hip_atomic_fetch_add(ctl + 1, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (gw < k && lane == 0) {
+        const int id = sm.ids[gw];
+        if (id < 0 || id >= a.n_experts) set_err(a.err, kDevErrExpertId);
+    }
+    // The other buffer (used by the previous launch) back to the sentinel for the next one.
+    {
+        float* const hnext = a.hbuf + size_t(parity ^ 1u) * kHBufWords;
+        const uint4 s4 = make_uint4(kSentinel, kSentinel, kSentinel, kSentinel);
+        for (int c = int(blockIdx.x) * NW * 64 + t; c < kHBufWords / 4; c += G * NW * 64)
+            reinterpret_cast<uint4*>(hnext)[c] = s4;
+    }
+    mark(2);
+
+    const uint32_t lo_g = (uint32_t(lane & 31) * 8u) | 0x00010000u;   // kS_XXS = 1 << 16
+    const uint32_t lo_s = uint32_t(lane & 31) * 8u;                     // kS_SGN = 0
+    uint32_t lo_x = uint32_t(kS_XS) + uint32_t(lane & 3) * 8u;
+    asm volatile("" : "+v"(lo_x));   // opaque: keeps (x & mask) | lo_x one v_and_or_b32
+
+    Raw3 rd[WIND + 1][PD];
+    auto load_pass = [&]<int j>() {
+#pragma unroll
+        for (int q = 0; q < PD; ++q)
+            load_pair_t<2>(rd[j % (WIND + 1)][q], matrix(int(dsl(j) >> 16), 2, do1, do2, kIQ2_XS, nbh),
+                           int(dsl(j) & 0xfffu), rD, lD + LD * q);
+    };
+
+    // ---- gate/up
+    {
+        Act<PG> A;
+        load_act<PG>(A, lds, kS_XQ, 4096, lG, LG);
+        uint32_t NA[PG][16];   // -q bytewise (q in -127..127, so no overflow)
+#pragma unroll
+        for (int q = 0; q < PG; ++q)
+#pragma unroll
+            for (int c = 0; c < 16; ++c) NA[q][c] = neg_bytes(A.a[q][c]);
+        float bg = 0.0f, bu = 0.0f;   // lane LG-1-b of each row group: slot b of the batch
+        int hidx = 0;                 // that slot's h word (pick * ff + row)
+        static_for<MG>([&]<int j>() {
+            if constexpr (j >= 1 && j + WIN - 1 < MG) load_slot.template operator()<j + WIN - 1>();
+            if constexpr (j >= MG - WIND) load_pass.template operator()<j - (MG - WIND)>();   // the down stream starts under the last slots
+            float fg = 0.0f, fu = 0.0f;
+#pragma unroll
+            for (int q = 0; q < PG; ++q) {
+                const Raw3& G0 = rg[j % WIN][q];
+                const Raw3& U0 = ru[j % WIN][q];
+                const Looks Lg = look_xxs(lds, lo_g, lo_s, G0.w);
+                const Looks Lu = look_xxs(lds, lo_g, lo_s, U0.w);
+                const int Ig = sum_xxs(Lg, G0.w, A.a[q], NA[q]);
+                const int Iu = sum_xxs(Lu, U0.w, A.a[q], NA[q]);
+                fg = fmaf(__fmul_rn(h2f(G0.h[0]), A.d[q]), float(Ig), fg);
+                fu = fmaf(__fmul_rn(h2f(U0.h[0]), A.d[q]), float(Iu), fu);
+            }
+            // A bad id read expert 0's rows: its h is published as 0 so that readers
+            // finish. The mask is applied by an opaque multiply: a select would let the
+            // compiler sink each row's whole decode into its own branch, serializing the
+            // gate and up rows.
+            float okf = ((gok >> j) & 1u) ? 1.0f : 0.0f;
+            asm volatile("" : "+v"(okf));
+            const float g = gsum<LG>(fg) * okf, u = gsum<LG>(fu) * okf;
+            const int b = j % kBatch;
+            const bool mine = lG == LG - 1 - b;
+            bg = mine ? g : bg;
+            bu = mine ? u : bu;
+            hidx = mine ? hrow(j) + rG : hidx;
+            if (b == kBatch - 1 || j == MG - 1) {
+                const float hv = silu_fast(__fmul_rn(0.125f, bg), __fmul_rn(0.125f, bu));
+                const uint32_t hb = __float_as_uint(hv) == kSentinel ? kQNaN : __float_as_uint(hv);
+                if (lG >= LG - 1 - b && hidx >= 0)
+                    __hip_atomic_store(reinterpret_cast<uint32_t*>(hcur) + hidx, hb, __ATOMIC_RELAXED,
+                                       __HIP_MEMORY_SCOPE_AGENT);
+            }
+            mark(8 + j);
+        });
+    }
+    mark(3);
+
+    // ---- down: step j quantizes the h of the picks it needs, then every wave runs pass j
+    float* ys = reinterpret_cast<float*>(lds + kS_Y);
+    const int hq_stride = ff + 64;
+    // picks [pk_lo(j), pk_hi(j)) are first needed at step j
+    auto pk_lo = [&](int j) { return min(k, (NW * j + nq_wg - 1) / nq_wg); };
+    auto pk_hi = [&](int j) { return min(k, (NW * j + NW + nq_wg - 1) / nq_wg); };
+    uint4 hv[2][MQ];   // h loads of steps j and j + 1 (issued two steps ahead)
+    auto h_issue = [&]<int j>() {   // loads of step j's blocks owned by this wave
+        const int b0 = pk_lo(j) * nbh, nb = pk_hi(j) * nbh - b0;
+#pragma unroll
+        for (int m = 0; m < MQ; ++m) {
+            const int bq = wv + NW * m;
+            const int blk = bq < nb ? b0 + bq : 0;   // unused slots re-read block 0
+            const int i = blk / nbh, bb = blk - i * nbh;
+            hv[j & 1][m] = h_load(hcur, uint32_t(i * ff + 256 * bb + 4 * lane));
+        }
+    };
+    h_issue.template operator()<0>();
+    if constexpr (MD > 1) h_issue.template operator()<1>();
+    lds_barrier();   // Q8_K(h) is staged over the IQ2_XXS grid: every wave is past gate/up
+    {
+        Act<PD> B;
+        static_for<MD>([&]<int j>() {
+            {   // steps past nsteps stage nothing and compute a discarded pass
+                // wait until this step's blocks are complete (all re-polled together), then
+                // quantize them into LDS
+                const int b0 = pk_lo(j) * nbh, nb = pk_hi(j) * nbh - b0;
+                auto all_ready = [&]() {
+                    bool ok = true;
+#pragma unroll
+                    for (int m = 0; m < MQ; ++m) ok = ok & ((wv + NW * m >= nb) | h_ready(hv[j & 1][m]));
+                    return __all(ok);
+                };
+                uint32_t polls = 0;
+                if (!all_ready()) {   // the common case never enters the retry loop
+                    do {
+                        if (++polls > kPollLimit) {
+                            if (lane == 0) set_err(a.err, kDevErrTimeout);
+                            break;
+                        }
+                        __builtin_amdgcn_s_sleep(2);
+                        h_issue.template operator()<j>();
+                    } while (!all_ready());
+                }
+                if (a.trace && lane == 0 && j < 4) a.trace[size_t(gw) * 32 + 20 + j] = polls;
+                mark(24 + 2 * j);
+                {
+                    uint32_t hp[MQ];
+                    float hd[MQ];
+                    const bool fin = q8k_blocks<MQ>(hv[j & 1], nb > wv ? (nb - wv + NW - 1) / NW : 0, lane, hp, hd);
+                    if (!fin && lane == 0) set_err(a.err, kDevErrNonFinite);
+#pragma unroll
+                    for (int m = 0; m < MQ; ++m) {
+                        const int bq = wv + NW * m;
+                        if (bq < nb) {
+                            const int blk = b0 + bq, i = blk / nbh, bb = blk - i * nbh;
+                            uint8_t* hq = lds + kS_HQ + i * hq_stride;
+                            reinterpret_cast<uint32_t*>(hq + 256 * bb)[lane] = hp[m];
+                            if (lane == 0) reinterpret_cast<float*>(hq + ff)[bb] = hd[m];
+                        }
+                    }
+                }
+                lds_barrier();
+                mark(25 + 2 * j);
+                if constexpr (j + 2 < MD) h_issue.template operator()<j + 2>();
+                {
+                    if constexpr (j + WIND < MD) load_pass.template operator()<j + WIND>();
+                    const int i = dpick(j);
+                    if (j == 0 || i != dpick(j > 0 ? j - 1 : 0)) load_act<PD>(B, lds, kS_HQ + i * hq_stride, ff, lD, LD);
+                    float f = 0.0f;
+#pragma unroll
+                    for (int q = 0; q < PD; ++q) {
+                        const Raw3& D0 = rd[j % (WIND + 1)][q];
+                        const int I = pair_xs(lds, lo_x, lo_s, D0.w, D0.h[0], B.a[q]);
+                        f = fmaf(__fmul_rn(h2f(D0.h[1]), B.d[q]), float(I), f);
+                    }
+                    float okf = ((dok >> j) & 1u) ? 0.125f : 0.0f;   // opaque, as in gate/up
+                    asm volatile("" : "+v"(okf));
+                    const float y = __fmul_rn(okf, gsum<LD>(f));
+                    if (j < nd && lD == LD - 1) ys[(wv + NW * j) * RD + rD] = y;
+                }
+                if (j == 0) mark(5);
+            }
+        });
+    }
+    mark(6);
+    lds_barrier();
+
+    // ---- fixed-order combine of this workgroup's rows
+    const int nrows = nq_wg * RD;
+    for (int r = t; r < nrows; r += NW * 64) {
+        const int qq = r / RD, rr = r - qq * RD;
+        const int orow = (int(blockIdx.x) + G * qq) * RD + rr;
+        float acc = 0.0f;
+        for (int s2 = 0; s2 < k; ++s2) {
+            const int i = sm.order[s2];
+            acc = fmaf(sm.w[i], ys[(i * nq_wg + qq) * RD + rr], acc);
+        }
+        if (a.shared) acc = __fadd_rn(acc, a.shared[orow]);
+        a.out[orow] = acc;
+    }
+    mark(7);
+    if (t == 0 && arrived == uint32_t(G) - 1u) {   // every workgroup has read the launch count
+        coh_st32(ctl, e_prev + 1u);
+        coh_st32(ctl + 1, 0u);
+    }
+}
+
+template <int NW, int LG, int PG, int LD, int PD, int MG, int MD, int WIN, int WIND, int MQ>
+hipError_t launch_stream_t(const Layer3Args& args, int grid, hipStream_t s) {
+    constexpr int RG = 64 / LG, RD = 64 / LD;
+    const int W = grid * NW;
+    const int SG = args.k * (args.ff / RG);
+    const int quads = args.dim / RD;
+    const int nq_wg = (quads + grid - 1) / grid;
+    const int P = args.k * nq_wg;
+    const int nbh = args.ff / 256;
+    // most blocks one step needs: the picks first needed by NW consecutive passes
+    int most = 0;
+    for (int j = 0; j * NW < P; ++j) {
+        const int lo = std::min(args.k, (NW * j + nq_wg - 1) / nq_wg);
+        const int hi = std::min(args.k, (NW * j + NW + nq_wg - 1) / nq_wg);
+        most = std::max(most, (hi - lo) * nbh);
+    }
+    if ((SG + W - 1) / W > MG || args.n_experts > 65536 || args.dim > 4096 || args.ff > 4096 || (P + NW - 1) / NW > MD || (most + NW - 1) / NW > MQ || P * RD > kS_YFloats ||
+        grid > quads || args.k * (args.ff + 64) > kS_HQBytes || args.k * args.ff > kHBufWords || !args.hbuf ||
+        !args.slab)   // regular layers only: every matrix is found from its expert id
+        return hipErrorNotSupported;
+    hipLaunchKernelGGL((stream_kernel<NW, LG, PG, LD, PD, MG, MD, WIN, WIND, MQ>), dim3(grid), dim3(NW * 64), 0, s, args);
+    return hipGetLastError();
+}
+
+}  // namespace
+
+hipError_t launch_stream(const Layer3Args& args, int cus, hipStream_t s) {
+    if (args.k < 1 || args.k > 16 || args.dim > 4096 || args.ff > 4096) return hipErrorNotSupported;
+    int lg, pg, ld, pd;
+    if (!row_shape(args.dim, lg, pg) || !row_shape(args.ff, ld, pd)) return hipErrorNotSupported;
+    const int RD = 64 / ld;
+    const int grid = std::min(cus, args.dim / RD);
+    if (lg == 64 && pg == 1 && ld == 16 && pd == 3)   // 4096 x 3072
+        return launch_stream_t<8, 64, 1, 16, 3, 9, 3, 3, 3, 3>(args, grid, s);
+    if (lg == 16 && pg == 1 && ld == 8 && pd == 1)    // 1024 x 512
+        return launch_stream_t<8, 16, 1, 8, 1, 6, 2, 3, 1, 2>(args, grid, s);
+    if (lg == 4 && pg == 1 && ld == 4 && pd == 3)     // 256 x 768
+        return launch_stream_t<8, 4, 1, 4, 3, 6, 2, 3, 1, 2>(args, grid, s);
+    return hipErrorNotSupported;
+}
+
+}  // namespace xl::dev

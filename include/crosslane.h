@@ -142,11 +142,14 @@ int32_t xl_profile_end(xl_context* ctx, float* stage_ms, int32_t max_stages, int
                        char* names, int32_t names_bytes, xl_error* err);
 
 /* Per-wave timeline of the last single-launch layer call made while profiling
- * was active: 8 s_memrealtime stamps (100 MHz) per wave, wave-major over the
- * grid (zero where a wave did not reach a phase). Phases: 0 prologue loads
- * issued, 1 loads in, 2 x quantized (barrier), 3 gate/up done, 4 quantizer
- * duty done, 5 first down pass done, 6 all down passes done, 7 combine done.
- * A diagnostic aid: it has no counterpart in the reference. */
+ * was active: 32 words per wave, wave-major over the grid, holding
+ * s_memrealtime stamps (100 MHz; zero where a wave did not reach a phase).
+ * Words: 0 prologue loads issued, 1 codebooks written, 2 x quantized
+ * (barrier), 3 gate/up done, 4 quantizer duty done (all-types kernel),
+ * 5 first down pass done, 6 all down passes done, 7 combine done, 8 + j
+ * gate/up slot j done; streaming kernel only: 20 + j re-polls of down step j
+ * (a count, not a stamp), 24 + 2j step j's h complete, 25 + 2j step j's
+ * Q8_K(h) staged. A diagnostic aid: it has no counterpart in the reference. */
 int32_t xl_profile_timeline(xl_context* ctx, uint64_t* out, int32_t max_words, int32_t* n_words, xl_error* err);
 
 /* ---- host utilities (no device needed) ------------------------------------ */

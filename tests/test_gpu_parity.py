@@ -202,20 +202,22 @@ def test_host_rejects_bad_routes(layer_lane):
         layer_lane.layer_forward(0, [3], [1.0], np.full(4096, np.nan, np.float32))
 
 
-def test_device_rejects_bad_id_and_poisons():
+@pytest.mark.parametrize("dim,ff,gu,dn", [(256, 256, 16, 16), (1024, 512, 16, 17)])
+def test_device_rejects_bad_id_and_poisons(dim, ff, gu, dn):
     # An out-of-range id reaches the kernels only through the device path; the
-    # kernels bounds-check it, skip the pick and raise the error flag.
-    step("device bad id")
-    lane = xl.Lane(256, 256, 1, 4, types_map(1, 4, 16, 16), max_picks=2)
+    # kernels bounds-check it, skip the pick and raise the error flag (the
+    # second case runs the streaming kernel, whose readers must still finish).
+    step(f"device bad id dim={dim} ff={ff} types=({gu},{dn})")
+    lane = xl.Lane(dim, ff, 1, 4, types_map(1, 4, gu, dn), max_picks=2)
     try:
         lane.generate(1)
-        out = torch.zeros(256, dtype=torch.float32, device="cuda")
+        out = torch.zeros(dim, dtype=torch.float32, device="cuda")
         lane.layer_forward_async(0, dev(np.array([1, 99], np.int32)), dev(np.array([0.5, 0.5], np.float32)),
-                                 dev(np.ones(256, np.float32)), out)
+                                 dev(np.ones(dim, np.float32)), out)
         with pytest.raises(xl.XLError, match="expert id"):
             lane.sync()
         with pytest.raises(xl.XLError, match="poisoned"):
-            lane.layer_forward(0, [1], [1.0], np.ones(256, np.float32))
+            lane.layer_forward(0, [1], [1.0], np.ones(dim, np.float32))
     finally:
         lane.close()
 
@@ -251,12 +253,15 @@ def test_matvec_any_fp16_scale(probe, orc, t):
 
 
 @pytest.mark.parametrize("dim,ff,sig", [(4096, 3072, None), (4096, 3072, (16, 16, 17)), (1024, 512, (17, 17, 16)),
+                                        (1024, 512, (16, 16, 17)), (256, 768, (16, 16, 17)),
                                         (256, 768, (29, 29, 17)), (512, 256, (16, 16, 29)), (256, 256, (17, 17, 17))])
 def test_layer_paths_agree(orc, dim, ff, sig, monkeypatch):
-    # The single-launch kernel (path 1), the separate launches (path 0) and the
-    # cooperative kernel (path 2) share the row arithmetic per block but sum
-    # lanes in their own orders, so they agree to the tolerance, and each is
-    # bit-identical run to run; the oracle checks every path.
+    # The single-launch kernels (path 1: the streaming kernel where the types
+    # are IQ2_XXS gate/up + IQ2_XS down, else the all-types one; path 3: the
+    # all-types one only), the separate launches (path 0) and the cooperative
+    # kernel (path 2) share the row arithmetic per block but sum lanes in their
+    # own orders, so they agree to the tolerance, and each is bit-identical run
+    # to run; the oracle checks every path.
     step(f"layer paths dim={dim} ff={ff} sig={sig}")
     E, k = 24, 6
     rng = np.random.default_rng(dim * 7 + ff)
@@ -266,7 +271,7 @@ def test_layer_paths_agree(orc, dim, ff, sig, monkeypatch):
     else:
         types = types_map(1, E, sig[0], sig[2])
     lanes = {}
-    for path in ("1", "0", "2"):
+    for path in ("1", "3", "0", "2"):
         monkeypatch.setenv("XL_LAYER_PATH", path)
         lanes[path] = xl.Lane(dim, ff, 1, E, types, max_picks=8)
         lanes[path].generate(seed=77)

@@ -1,22 +1,32 @@
 #!/usr/bin/env python3
 """Routed-expert benchmark on one MI355X.
 
-Workload: one MoE layer at decode batch 1, d_model 4096,
-d_ff 3072, 384 resident experts (gate/up IQ2_XXS, down IQ2_XS), top-6 of a
-softmax over seeded N(0,1) router logits with renormalized weights, fixed-order
-combine into a 4096-wide f32 output. A step is one layer call through the C ABI
-(xl_layer_forward_async) with routes, inputs and the bank already resident in
-HBM; every step uses a fresh seeded route so consecutive steps touch different
-experts (the bank is ~3.9 GB, far beyond the 256 MB MALL).
+Default workload: one MoE layer at decode batch 1, d_model
+4096, d_ff 3072, 384 resident experts (gate/up IQ2_XXS, down IQ2_XS), top-6 of
+a softmax over seeded N(0,1) router logits with renormalized weights,
+fixed-order combine into a 4096-wide f32 output. A step is one layer call
+through the C ABI (xl_layer_forward_async) with routes, inputs and the bank
+already resident in HBM; every step uses a fresh seeded route so consecutive
+steps touch different experts (the bank is ~3.9 GB, far beyond the 256 MB MALL).
 
-Prints one JSON line: value = achieved algorithmic HBM GB/s of the layer
-(selected experts' weight bytes + x in + out, 60,784,640 B per layer), plus
-us_per_layer; the roofline of the layer kernel (one launch per step, so its
-average duration is the timed region's HIP-event time on the launching stream
-divided by the steps; HBM traffic per launch from the committed rocprofv3
-FETCH_SIZE / WRITE_SIZE summary in profiles/); and the CPU baseline (the
-reference's own q8k_core.hpp chain, compiled from the reference sources into
-oracle/_ref, timed on a bounded sample on the host cores).
+--config selects the other single-GPU workloads of the same metric:
+  0  one config-1 expert per step (k = 1, w = 1), fresh expert each step;
+  2  all-IQ1_M bank, 6 distinct experts drawn with p ~ rank^-1.1 over a seeded
+     permutation (Zipf: hot experts recur, so the MALL can serve part of it);
+  3  a 40-layer pass per step: 40 x 384 experts whose whole-expert type is
+     drawn 17 % IQ2_XS / 19 % IQ2_XXS / 64 % IQ1_M, top-6 per layer, the
+     hidden carried layer to layer through an RMS normalization (torch ops on
+     the same stream, inside the timed region: the model's RMSNorm stand-in,
+     without which the quadratic SwiGLU overflows f32 within a few layers).
+
+Prints one JSON line: value = achieved algorithmic HBM GB/s (selected experts'
+weight bytes + x in + out per layer), plus us_per_layer; the roofline of the
+layer kernel (one launch per layer, so its average duration is the timed
+region's HIP-event time on the launching stream divided by the launches; HBM
+traffic per launch from the committed rocprofv3 FETCH_SIZE / WRITE_SIZE
+summary in profiles/, config 1); and the CPU baseline (the reference's own
+q8k_core.hpp chain, compiled from the reference sources into oracle/_ref, timed
+on a bounded sample on the host cores).
 """
 from __future__ import annotations
 
@@ -40,6 +50,13 @@ LAYER_BYTES = K * (2 * W_GU + W_DN) + 2 * DIM * 4  # 60,784,640 B
 HBM_PEAK_GBS = 8000.0
 SEED = 0x1A7E5
 PMC_SUMMARY = os.path.join(ROOT, "profiles", "stream_kernel_config1_hbm_traffic.md")
+N_LAYERS_3 = 40
+MIX_3 = ((17, 0.17), (16, 0.19), (29, 0.64))   # whole-expert type draw of config 3
+
+
+def expert_bytes(t3) -> int:
+    """Weight bytes of one expert with (gate, up, down) types t3."""
+    return FF * (DIM // 256) * (BYTES[t3[0]] + BYTES[t3[1]]) + DIM * (FF // 256) * BYTES[t3[2]]
 
 
 def measured_traffic():
@@ -68,33 +85,70 @@ def routes(n, seed):
     return ids, w, x
 
 
-def cpu_baseline(layers: int, threads: int, pool: int = 48):
-    """The reference's own CPU chain (oracle/_ref) on `layers` routed layers.
+def zipf_routes(n, seed, s=1.1):
+    """Config 2: K distinct experts drawn without replacement with p ~ rank^-s
+    over a seeded permutation of the experts; weights = renormalized p."""
+    rng = np.random.default_rng(seed)
+    perm = rng.permutation(E)
+    p_rank = np.arange(1, E + 1, dtype=np.float64) ** -s
+    p = np.zeros(E)
+    p[perm] = p_rank / p_rank.sum()
+    ids = np.zeros((n, K), np.int32)
+    w = np.zeros((n, K), np.float32)
+    for i in range(n):
+        pick = rng.choice(E, size=K, replace=False, p=p)
+        ids[i] = pick
+        w[i] = (p[pick] / p[pick].sum()).astype(np.float32)
+    x = rng.standard_normal((n, DIM)).astype(np.float32)
+    return ids, w, x
 
-    The picks are drawn from a pool of `pool` generated experts (48 x 9.6 MB,
-    beyond the host caches); generation is not timed."""
+
+def mixed_types(n_layers, seed):
+    """Config 3: per (layer, expert) one type for all three matrices."""
+    rng = np.random.default_rng(seed)
+    tv = np.array([t for t, _ in MIX_3], np.int32)
+    t = rng.choice(tv, size=(n_layers, E), p=[p for _, p in MIX_3])
+    return np.repeat(t[..., None], 3, axis=-1).astype(np.int32)
+
+
+def cpu_baseline(layers: int, threads: int, pool: int = 48, config: int = 1):
+    """The reference's own CPU chain (oracle/_ref) on `layers` routed layers of
+    the config's shape.
+
+    The picks are drawn from a pool of `pool` generated experts (48 x ~9 MB,
+    beyond the host caches) whose types follow the config; generation is not
+    timed."""
     from oracle.oracle import Oracle, Reference   # checker/baseline only
     orc = Oracle()
     kind = "reference" if Reference.available() else "port"
     impl = Reference() if kind == "reference" else orc
-    types = (GATE_T, GATE_T, DOWN_T)
-    mats = [orc.gen_expert(types, SEED, 0, e, DIM, FF) for e in range(pool)]   # not timed
     rng = np.random.default_rng(SEED + 1)
+    if config == 2:
+        ptypes = [(29, 29, 29)] * pool
+    elif config == 3:
+        tv = rng.choice([t for t, _ in MIX_3], size=pool, p=[p for _, p in MIX_3])
+        ptypes = [(int(t),) * 3 for t in tv]
+    else:
+        ptypes = [(GATE_T, GATE_T, DOWN_T)] * pool
+    k = 1 if config == 0 else K
+    mats = [orc.gen_expert(ptypes[e], SEED, 0, e, DIM, FF) for e in range(pool)]   # not timed
     elapsed = 0.0
-    for l in range(layers):
-        ids = rng.choice(pool, size=K, replace=False).astype(np.int32)
-        w = rng.random(K).astype(np.float32)
+    nbytes = 0
+    for _ in range(layers):
+        ids = rng.choice(pool, size=k, replace=False).astype(np.int32)
+        w = rng.random(k).astype(np.float32)
         x = rng.standard_normal(DIM).astype(np.float32)
         t0 = time.perf_counter()
-        rows = np.stack([impl.expert(types, *mats[e], DIM, FF, x, threads=threads) for e in ids])
+        rows = np.stack([impl.expert(ptypes[e], *mats[e], DIM, FF, x, threads=threads) for e in ids])
         impl.combine(ids, w, rows, np.zeros(DIM, np.float32)) if kind == "reference" else orc.combine(ids, w, rows)
         elapsed += time.perf_counter() - t0
+        nbytes += sum(expert_bytes(ptypes[e]) for e in ids) + 2 * DIM * 4
     us = elapsed / layers * 1e6
     return {
-        "value": round(LAYER_BYTES / (us * 1e-6) / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": kind,
+        "value": round(nbytes / elapsed / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": kind,
         "us_per_layer": round(us, 1),
-        "sample": f"{layers} config-1 layers (6 experts + combine each, drawn from {pool} generated experts), "
-                  f"{'reference q8k_core.hpp chain from oracle/_ref' if kind == 'reference' else 'oracle port'}, "
+        "sample": f"{layers} config-{config} layers ({k} expert(s) + combine each, drawn from {pool} generated "
+                  f"experts), {'reference q8k_core.hpp chain from oracle/_ref' if kind == 'reference' else 'oracle port'}, "
                   f"{threads} threads, {elapsed:.1f} s timed",
     }
 
@@ -102,10 +156,11 @@ def cpu_baseline(layers: int, threads: int, pool: int = 48):
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=2000)
-    ap.add_argument("--warmup", type=int, default=100)
+    ap.add_argument("--steps", type=int, default=0, help="timed steps (default: 2000 layers' worth)")
+    ap.add_argument("--warmup", type=int, default=-1)
+    ap.add_argument("--config", type=int, default=1, choices=(0, 1, 2, 3))
     ap.add_argument("--routes", type=int, default=512)
-    ap.add_argument("--cpu-layers", type=int, default=500)
+    ap.add_argument("--cpu-layers", type=int, default=0)
     ap.add_argument("--cpu-threads", type=int, default=0)
     ap.add_argument("--no-cpu", action="store_true")
     args = ap.parse_args()
@@ -113,15 +168,48 @@ def main():
         print(f"bench.py: this build measures one GPU only (asked for --gpus {args.gpus}); "
               "the routed-expert path runs on a single MI355X holding the whole bank", file=sys.stderr)
         sys.exit(2)
+    cfg = args.config
+    L = N_LAYERS_3 if cfg == 3 else 1
+    steps = args.steps or (50 if cfg == 3 else 2000)
+    warmup = args.warmup if args.warmup >= 0 else (5 if cfg == 3 else 100)
 
     import torch
     import crosslane_amd as xl
 
-    types = np.zeros((1, E, 3), np.int32)
-    types[..., 0] = GATE_T; types[..., 1] = GATE_T; types[..., 2] = DOWN_T
-    lane = xl.Lane(DIM, FF, 1, E, types, max_picks=8)
+    # ---- bank and routes
+    if cfg == 3:
+        types = mixed_types(L, SEED + 3)
+    else:
+        types = np.zeros((1, E, 3), np.int32)
+        t3 = (29, 29, 29) if cfg == 2 else (GATE_T, GATE_T, DOWN_T)
+        types[..., 0], types[..., 1], types[..., 2] = t3
+    lane = xl.Lane(DIM, FF, L, E, types, max_picks=8)
     lane.generate(SEED)
-    ids, w, x = routes(args.routes, SEED)
+    n_r = args.routes
+    if cfg == 0:
+        rng = np.random.default_rng(SEED)
+        ids = rng.integers(0, E, size=(n_r, 1, 1)).astype(np.int32)
+        w = np.ones((n_r, 1, 1), np.float32)
+        x = rng.standard_normal((n_r, DIM)).astype(np.float32)
+    elif cfg == 2:
+        ids, w, x = zipf_routes(n_r, SEED)
+        ids, w = ids[:, None, :], w[:, None, :]
+    elif cfg == 3:
+        n_r = min(n_r, 64)
+        per = [routes(n_r, SEED + 100 + l) for l in range(L)]
+        ids = np.stack([p[0] for p in per], axis=1)
+        w = np.stack([p[1] for p in per], axis=1)
+        x = per[0][2]
+    else:
+        ids, w, x = routes(n_r, SEED)
+        ids, w = ids[:, None, :], w[:, None, :]
+    k = ids.shape[2]
+    # algorithmic bytes per step, averaged over the routes the timed steps use
+    used = [(warmup + i) % n_r for i in range(steps)]
+    step_bytes = np.array([sum(expert_bytes(types[l, e]) for l in range(L) for e in ids[r, l]) + L * 2 * DIM * 4
+                           for r in range(n_r)], np.float64)
+    bytes_per_step = float(step_bytes[used].mean())
+
     # A dedicated (non-default) stream: the library launches on it and the
     # timing events are recorded on it.
     stream = torch.cuda.Stream()
@@ -130,57 +218,81 @@ def main():
         d_ids = torch.from_numpy(ids).cuda()
         d_w = torch.from_numpy(w).cuda()
         d_x = torch.from_numpy(x).cuda()
-        d_out = torch.zeros((args.routes, DIM), dtype=torch.float32, device="cuda")
+        d_h = torch.zeros((L + 1, DIM), dtype=torch.float32, device="cuda")   # config 3: the carried hidden
+        d_out = torch.zeros((n_r, DIM), dtype=torch.float32, device="cuda")
     torch.cuda.synchronize()
 
     def step(i):
-        r = i % args.routes
-        lane.layer_forward_async(0, d_ids[r], d_w[r], d_x[r], d_out[r], stream=sp)
+        r = i % n_r
+        if cfg != 3:
+            lane.layer_forward_async(0, d_ids[r, 0], d_w[r, 0], d_x[r], d_out[r], stream=sp)
+            return
+        with torch.cuda.stream(stream):
+            d_h[0].copy_(d_x[r])
+            for l in range(L):
+                lane.layer_forward_async(l, d_ids[r, l], d_w[r, l], d_h[l], d_h[l + 1], stream=sp)
+                y = d_h[l + 1]
+                y.mul_(torch.rsqrt(y.square().mean() + 1e-6))   # RMS-normalized hidden for the next layer
 
-    for i in range(args.warmup):
+    for i in range(warmup):
         step(i)
     torch.cuda.synchronize()
     t0 = torch.cuda.Event(enable_timing=True)
     t1 = torch.cuda.Event(enable_timing=True)
     t0.record(stream)
     wall0 = time.perf_counter()
-    for i in range(args.steps):
-        step(args.warmup + i)
+    for i in range(steps):
+        step(warmup + i)
     t1.record(stream)
     torch.cuda.synchronize()
     wall = time.perf_counter() - wall0
     lane.sync(sp)
+    if cfg == 3:
+        assert bool(torch.isfinite(d_h).all()), "non-finite hidden in the 40-layer pass"
     ms = t0.elapsed_time(t1)
-    us_layer = ms * 1e3 / args.steps
-    gbs = LAYER_BYTES / (us_layer * 1e-6) / 1e9
+    us_step = ms * 1e3 / steps
+    us_layer = us_step / L
+    gbs = bytes_per_step / (us_step * 1e-6) / 1e9
 
-    # One kernel launch per step: the layer kernel's average duration is the
-    # timed region's event time over the steps (rocprofv3 --kernel-trace of the
-    # same command agrees; see profiles/).
-    achieved = LAYER_BYTES / (us_layer * 1e-6) / 1e9
-    traffic = measured_traffic()
+    # One kernel launch per layer: the layer kernel's average duration is the
+    # timed region's event time over the launches (rocprofv3 --kernel-trace of
+    # the same command agrees; see profiles/). Config 3's figure also holds the
+    # normalization between layers, so it bounds the kernel from below.
+    kernel = ("xl::dev::stream_kernel (single-launch layer)" if cfg in (0, 1)
+              else "xl::dev::layer3_kernel (all-types single-launch layer)")
+    traffic = measured_traffic() if cfg == 1 else None
 
     cpu = None
     if not args.no_cpu:
         threads = args.cpu_threads or min(16, os.cpu_count() or 1)
-        cpu = cpu_baseline(args.cpu_layers, threads)
+        cpu_layers = args.cpu_layers or {0: 1500, 1: 500, 2: 500, 3: 500}[cfg]
+        cpu = cpu_baseline(cpu_layers, threads, config=cfg)
 
+    workloads = {
+        0: "config0: one expert per step (k=1, w=1) of 384 resident, d_model 4096, d_ff 3072, "
+           "gate/up IQ2_XXS + down IQ2_XS",
+        1: "config1: MoE layer, decode batch 1, top-6 of 384 resident experts, d_model 4096, "
+           "d_ff 3072, gate/up IQ2_XXS + down IQ2_XS, fixed-order combine",
+        2: "config2: MoE layer, decode batch 1, all-IQ1_M bank of 384, 6 distinct experts ~ rank^-1.1 (Zipf), "
+           "fixed-order combine",
+        3: "config3: 40-layer pass per token, 40 x 384 experts typed 17% IQ2_XS / 19% IQ2_XXS / 64% IQ1_M, "
+           "top-6 per layer, hidden carried through RMS normalization",
+    }
     line = {
         "metric": "routed-expert µs/layer (top-6, batch 1) + achieved HBM GB/s vs MI355X peak",
-        "value": round(gbs, 2), "unit": "GB/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
-        "ms_per_step": round(ms / args.steps, 6), "us_per_layer": round(us_layer, 3),
+        "value": round(gbs, 2), "unit": "GB/s", "n_gpus": 1, "steps": steps, "warmup": warmup,
+        "ms_per_step": round(ms / steps, 6), "us_per_layer": round(us_layer, 3),
         "hbm_frac": round(gbs / HBM_PEAK_GBS, 4),
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "int8",
         "data": "synthetic (seeded IQ blocks generated on device, N(0,1) activations and router logits)",
-        "config": {"workload": "config1: MoE layer, decode batch 1, top-6 of 384 resident experts, d_model 4096, "
-                               "d_ff 3072, gate/up IQ2_XXS + down IQ2_XS, fixed-order combine",
-                   "layer_bytes": LAYER_BYTES, "routes": args.routes},
-        "roofline": {"bound": "hbm", "kernel": "xl::dev::stream_kernel (single-launch layer)",
-                     "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
-                     "bytes_per_launch": LAYER_BYTES, "us_per_launch": round(us_layer, 3)},
+        "config": {"workload": workloads[cfg], "layers_per_step": L, "bytes_per_step": int(round(bytes_per_step)),
+                   "routes": n_r},
+        "roofline": {"bound": "hbm", "kernel": kernel,
+                     "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": traffic,
+                     "bytes_per_launch": int(round(bytes_per_step / L)), "us_per_launch": round(us_layer, 3)},
         "cpu_baseline": cpu,
-        "host_wall_us_per_step": round(wall * 1e6 / args.steps, 3),
+        "host_wall_us_per_step": round(wall * 1e6 / steps, 3),
     }
     print(json.dumps(line), flush=True)
     lane.close()

@@ -151,8 +151,9 @@ struct xl_context {
     // Layer path: 1 = single launch (default: the streaming kernel of
     // xl_stream.hip for IQ2_XXS gate/up + IQ2_XS down layers, else the
     // all-types kernel of xl_layer.hip), 3 = the all-types single launch only,
-    // 2 = cooperative fused kernel, 0 = separate launches. XL_LAYER_PATH
-    // selects; shapes without a single-launch instance use separate launches.
+    // 2 = cooperative fused kernel, 0 = separate launches, 4 = the streaming
+    // kernel only (a layer it cannot run is an error). XL_LAYER_PATH selects;
+    // shapes without a single-launch instance use separate launches.
     int path = 1;
     float* hbuf = nullptr;      // streaming kernel's h exchange (2 x kHBufWords, sentinel-filled)
     uint32_t* sync = nullptr;   // counters of the cooperative fused kernel
@@ -276,7 +277,7 @@ void enqueue_layer(xl_context* ctx, int32_t layer, const int32_t* d_ids, const f
     const int gu_mask = ctx->gu_mask[size_t(layer)], dn_mask = ctx->dn_mask[size_t(layer)];
     Marks mark(ctx, s);
     mark("");
-    if ((ctx->path == 1 || ctx->path == 3) && !g_dbg && !u_dbg) {
+    if ((ctx->path == 1 || ctx->path == 3 || ctx->path == 4) && !g_dbg && !u_dbg) {
         xl::Layer3Args a{};
         a.descs = descs; a.ids = d_ids; a.w = d_w; a.x = d_x; a.shared = d_shared; a.out = d_out;
         a.k = k; a.n_experts = E; a.dim = dim; a.ff = ff;
@@ -295,11 +296,12 @@ void enqueue_layer(xl_context* ctx, int32_t layer, const int32_t* d_ids, const f
         }
         if (d_out) {
             hipError_t e = hipErrorNotSupported;
-            if (ctx->path == 1 && gu_mask == 1 && dn_mask == 2) {
+            if ((ctx->path == 1 || ctx->path == 4) && gu_mask == 1 && dn_mask == 2) {
                 e = xl::dev::launch_stream(a, ctx->cus, s);
                 if (e != hipSuccess && e != hipErrorNotSupported) hip_check(e, "streaming layer");
                 (void)hipGetLastError();
             }
+            need(ctx->path != 4 || e == hipSuccess, XL_E_ARG, "XL_LAYER_PATH=4: no streaming-kernel instance for this layer");
             if (e == hipErrorNotSupported) e = xl::dev::launch_layer3(a, gu_mask, dn_mask, ctx->cus, s);
             if (e == hipSuccess) {
                 if (a.trace) ctx->timeline_words = uint64_t(ctx->cus) * 16 * 32;
@@ -432,7 +434,7 @@ int32_t xl_open(uint32_t abi_version, const xl_config* cfg, xl_context** out, xl
         const std::vector<uint64_t> tab = layer_tables();
         hip_check(hipMemcpy(ctx->tables, tab.data(), tab.size() * 8, hipMemcpyHostToDevice), "table upload");
         ctx->path = env_int("XL_LAYER_PATH", 1);
-        need(ctx->path >= 0 && ctx->path <= 3, XL_E_ARG, "XL_LAYER_PATH must be 0, 1, 2 or 3");
+        need(ctx->path >= 0 && ctx->path <= 4, XL_E_ARG, "XL_LAYER_PATH must be 0, 1, 2, 3 or 4");
         *out = ctx;
     });
     if (rc != XL_OK && ctx) xl_close(ctx);

@@ -640,13 +640,15 @@ hipError_t launch_stream_t(const Layer3Args& args, int grid, hipStream_t s) {
     const int nq_wg = (quads + grid - 1) / grid;
     const int P = args.k * nq_wg;
     const int nbh = args.ff / 256;
-    // most blocks one step needs: the picks first needed by NW consecutive passes
+    // most blocks one step needs: the picks first needed by NW consecutive passes,
+    // in workgroups owning quads / grid and quads / grid + 1 row groups
     int most = 0;
-    for (int j = 0; j * NW < P; ++j) {
-        const int lo = std::min(args.k, (NW * j + nq_wg - 1) / nq_wg);
-        const int hi = std::min(args.k, (NW * j + NW + nq_wg - 1) / nq_wg);
-        most = std::max(most, (hi - lo) * nbh);
-    }
+    for (int nq = quads / grid; nq <= nq_wg; ++nq)
+        for (int j = 0; j * NW < args.k * nq; ++j) {
+            const int lo = std::min(args.k, (NW * j + nq - 1) / nq);
+            const int hi = std::min(args.k, (NW * j + NW + nq - 1) / nq);
+            most = std::max(most, (hi - lo) * nbh);
+        }
     if ((SG + W - 1) / W > MG || args.n_experts > 65536 || args.dim > 4096 || args.ff > 4096 || (P + NW - 1) / NW > MD || (most + NW - 1) / NW > MQ || P * RD > kS_YFloats ||
         grid > quads || args.k * (args.ff + 64) > kS_HQBytes || args.k * args.ff > kHBufWords || !args.hbuf ||
         !args.slab)   // regular layers only: every matrix is found from its expert id
@@ -668,7 +670,7 @@ hipError_t launch_stream(const Layer3Args& args, int cus, hipStream_t s) {
     if (lg == 16 && pg == 1 && ld == 8 && pd == 1)    // 1024 x 512
         return launch_stream_t<8, 16, 1, 8, 1, 6, 2, 3, 1, 2>(args, grid, s);
     if (lg == 4 && pg == 1 && ld == 4 && pd == 3)     // 256 x 768
-        return launch_stream_t<8, 4, 1, 4, 3, 6, 2, 3, 1, 2>(args, grid, s);
+        return launch_stream_t<8, 4, 1, 4, 3, 6, 2, 3, 1, 3>(args, grid, s);
     return hipErrorNotSupported;
 }
 

@@ -293,3 +293,32 @@ def test_layer_paths_agree(orc, dim, ff, sig, monkeypatch):
     finally:
         for lane in lanes.values():
             lane.close()
+
+
+@pytest.mark.parametrize("dim,ff,k", [(4096, 3072, 6), (4096, 3072, 4), (4096, 3072, 1), (1024, 512, 8),
+                                      (1024, 512, 12), (1024, 512, 16), (256, 768, 6), (256, 768, 12)])
+def test_streaming_kernel_pick_counts(orc, dim, ff, k, monkeypatch):
+    # XL_LAYER_PATH=4 runs the streaming kernel or fails: pick counts that give
+    # one, two or three down steps and steps staging one to eight picks must
+    # match the oracle and repeat bit for bit.
+    step(f"streaming kernel dim={dim} ff={ff} k={k}")
+    E = 24
+    rng = np.random.default_rng(dim + ff + k)
+    types = types_map(1, E, 16, 17)
+    monkeypatch.setenv("XL_LAYER_PATH", "4")
+    lane = xl.Lane(dim, ff, 1, E, types, max_picks=16)
+    try:
+        lane.generate(seed=91)
+        for trial in range(2):
+            ids, w = route(rng.standard_normal(E).astype(np.float32), k)
+            x = rng.standard_normal(dim).astype(np.float32)
+            shared = rng.standard_normal(dim).astype(np.float32) if trial else None
+            rows = [orc.expert((16, 16, 17), *orc.gen_expert((16, 16, 17), 91, 0, int(e), dim, ff), dim, ff, x)
+                    for e in ids]
+            want = orc.combine(ids, w, np.stack(rows), shared)
+            got = lane.layer_forward(0, ids, w, x, shared)
+            again = lane.layer_forward(0, ids, w, x, shared)
+            assert np.array_equal(got.view(np.uint32), again.view(np.uint32)), trial
+            assert max_rel(got, want) < TOL, (trial, max_rel(got, want))
+    finally:
+        lane.close()

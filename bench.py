@@ -13,6 +13,9 @@ steps touch different experts (the bank is ~3.9 GB, far beyond the 256 MB MALL).
   0  one config-1 expert per step (k = 1, w = 1), fresh expert each step;
   2  all-IQ1_M bank, 6 distinct experts drawn with p ~ rank^-1.1 over a seeded
      permutation (Zipf: hot experts recur, so the MALL can serve part of it);
+  4  grouped: 512 tokens per step, each with its own top-6 of 384 config-1
+     experts (xl_grouped_forward_async: every touched expert read once per 16
+     of its pairs, int8 MFMA);
   3  a 40-layer pass per step: 40 x 384 experts whose whole-expert type is
      drawn 17 % IQ2_XS / 19 % IQ2_XXS / 64 % IQ1_M, top-6 per layer, the
      hidden carried layer to layer through an RMS normalization (torch ops on
@@ -158,7 +161,8 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=0, help="timed steps (default: 2000 layers' worth)")
     ap.add_argument("--warmup", type=int, default=-1)
-    ap.add_argument("--config", type=int, default=1, choices=(0, 1, 2, 3))
+    ap.add_argument("--config", type=int, default=1, choices=(0, 1, 2, 3, 4))
+    ap.add_argument("--tokens", type=int, default=512, help="config 4: tokens per grouped call")
     ap.add_argument("--routes", type=int, default=512)
     ap.add_argument("--cpu-layers", type=int, default=0)
     ap.add_argument("--cpu-threads", type=int, default=0)
@@ -170,8 +174,9 @@ def main():
         sys.exit(2)
     cfg = args.config
     L = N_LAYERS_3 if cfg == 3 else 1
-    steps = args.steps or (50 if cfg == 3 else 2000)
-    warmup = args.warmup if args.warmup >= 0 else (5 if cfg == 3 else 100)
+    TOK = args.tokens if cfg == 4 else 1
+    steps = args.steps or {3: 50, 4: 50}.get(cfg, 2000)
+    warmup = args.warmup if args.warmup >= 0 else {3: 5, 4: 5}.get(cfg, 100)
 
     import torch
     import crosslane_amd as xl
@@ -183,7 +188,7 @@ def main():
         types = np.zeros((1, E, 3), np.int32)
         t3 = (29, 29, 29) if cfg == 2 else (GATE_T, GATE_T, DOWN_T)
         types[..., 0], types[..., 1], types[..., 2] = t3
-    lane = xl.Lane(DIM, FF, L, E, types, max_picks=8)
+    lane = xl.Lane(DIM, FF, L, E, types, max_picks=8, max_tokens=TOK if cfg == 4 else 0)
     lane.generate(SEED)
     n_r = args.routes
     if cfg == 0:
@@ -194,6 +199,12 @@ def main():
     elif cfg == 2:
         ids, w, x = zipf_routes(n_r, SEED)
         ids, w = ids[:, None, :], w[:, None, :]
+    elif cfg == 4:
+        n_r = min(n_r, 8)   # route sets of TOK tokens each
+        per = [routes(TOK, SEED + 200 + r) for r in range(n_r)]
+        ids = np.stack([p[0] for p in per])   # [n_r, TOK, K]
+        w = np.stack([p[1] for p in per])
+        x = np.stack([p[2] for p in per])     # [n_r, TOK, DIM]
     elif cfg == 3:
         n_r = min(n_r, 64)
         per = [routes(n_r, SEED + 100 + l) for l in range(L)]
@@ -206,8 +217,12 @@ def main():
     k = ids.shape[2]
     # algorithmic bytes per step, averaged over the routes the timed steps use
     used = [(warmup + i) % n_r for i in range(steps)]
-    step_bytes = np.array([sum(expert_bytes(types[l, e]) for l in range(L) for e in ids[r, l]) + L * 2 * DIM * 4
-                           for r in range(n_r)], np.float64)
+    if cfg == 4:   # every touched expert once, plus the tokens in and out
+        step_bytes = np.array([sum(expert_bytes(types[0, e]) for e in np.unique(ids[r])) + TOK * 2 * DIM * 4
+                               for r in range(n_r)], np.float64)
+    else:
+        step_bytes = np.array([sum(expert_bytes(types[l, e]) for l in range(L) for e in ids[r, l]) + L * 2 * DIM * 4
+                               for r in range(n_r)], np.float64)
     bytes_per_step = float(step_bytes[used].mean())
 
     # A dedicated (non-default) stream: the library launches on it and the
@@ -219,11 +234,14 @@ def main():
         d_w = torch.from_numpy(w).cuda()
         d_x = torch.from_numpy(x).cuda()
         d_h = torch.zeros((L + 1, DIM), dtype=torch.float32, device="cuda")   # config 3: the carried hidden
-        d_out = torch.zeros((n_r, DIM), dtype=torch.float32, device="cuda")
+        d_out = torch.zeros((n_r, TOK, DIM) if cfg == 4 else (n_r, DIM), dtype=torch.float32, device="cuda")
     torch.cuda.synchronize()
 
     def step(i):
         r = i % n_r
+        if cfg == 4:
+            lane.grouped_forward_async(0, d_ids[r], d_w[r], d_x[r], d_out[r], stream=sp)
+            return
         if cfg != 3:
             lane.layer_forward_async(0, d_ids[r, 0], d_w[r, 0], d_x[r], d_out[r], stream=sp)
             return
@@ -251,22 +269,26 @@ def main():
         assert bool(torch.isfinite(d_h).all()), "non-finite hidden in the 40-layer pass"
     ms = t0.elapsed_time(t1)
     us_step = ms * 1e3 / steps
-    us_layer = us_step / L
+    us_layer = us_step / L   # config 4: one grouped call of TOK tokens
     gbs = bytes_per_step / (us_step * 1e-6) / 1e9
 
     # One kernel launch per layer: the layer kernel's average duration is the
     # timed region's event time over the launches (rocprofv3 --kernel-trace of
     # the same command agrees; see profiles/). Config 3's figure also holds the
     # normalization between layers, so it bounds the kernel from below.
-    kernel = ("xl::dev::stream_kernel (single-launch layer)" if cfg in (0, 1)
-              else "xl::dev::layer3_kernel (all-types single-launch layer)")
+    kernel = {0: "xl::dev::stream_kernel (single-launch layer)", 1: "xl::dev::stream_kernel (single-launch layer)",
+              4: "grouped path (bucket, Q8_K, gu_kernel, Q8_K, dn_kernel, combine: 6 launches per step)"}.get(
+        cfg, "xl::dev::layer3_kernel (all-types single-launch layer)")
     traffic = measured_traffic() if cfg == 1 else None
 
     cpu = None
     if not args.no_cpu:
         threads = args.cpu_threads or min(16, os.cpu_count() or 1)
-        cpu_layers = args.cpu_layers or {0: 1500, 1: 500, 2: 500, 3: 500}[cfg]
-        cpu = cpu_baseline(cpu_layers, threads, config=cfg)
+        cpu_layers = args.cpu_layers or {0: 1500, 1: 500, 2: 500, 3: 500, 4: 500}[cfg]
+        cpu = cpu_baseline(cpu_layers, threads, config=1 if cfg == 4 else cfg)
+        if cfg == 4:   # the CPU chain has no grouping: TOK per-token layers per step
+            cpu["value"] = round(bytes_per_step / (cpu["us_per_layer"] * 1e-6 * TOK) / 1e9, 3)
+            cpu["sample"] += f"; per step = {TOK} such token layers (algorithmic bytes of the grouped step)"
 
     workloads = {
         0: "config0: one expert per step (k=1, w=1) of 384 resident, d_model 4096, d_ff 3072, "
@@ -277,6 +299,8 @@ def main():
            "fixed-order combine",
         3: "config3: 40-layer pass per token, 40 x 384 experts typed 17% IQ2_XS / 19% IQ2_XXS / 64% IQ1_M, "
            "top-6 per layer, hidden carried through RMS normalization",
+        4: f"config4: grouped, {TOK} tokens x N(0,1)[4096], per-token top-6 of 384 config-1 experts, "
+           "fixed-order combine per token",
     }
     line = {
         "metric": "routed-expert µs/layer (top-6, batch 1) + achieved HBM GB/s vs MI355X peak",
@@ -285,8 +309,8 @@ def main():
         "hbm_frac": round(gbs / HBM_PEAK_GBS, 4),
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "int8",
         "data": "synthetic (seeded IQ blocks generated on device, N(0,1) activations and router logits)",
-        "config": {"workload": workloads[cfg], "layers_per_step": L, "bytes_per_step": int(round(bytes_per_step)),
-                   "routes": n_r},
+        "config": {"workload": workloads[cfg], "layers_per_step": L, "tokens_per_step": TOK,
+                   "bytes_per_step": int(round(bytes_per_step)), "routes": n_r},
         "roofline": {"bound": "hbm", "kernel": kernel,
                      "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": traffic,

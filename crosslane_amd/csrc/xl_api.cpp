@@ -155,7 +155,19 @@ struct xl_context {
     // kernel only (a layer it cannot run is an error). XL_LAYER_PATH selects;
     // shapes without a single-launch instance use separate launches.
     int path = 1;
+    // Grouped path: 1 = the MFMA kernels where the layer's types allow, else one
+    // layer call per token (default); 0 = per-token calls only; 2 = the MFMA
+    // kernels only (a layer they cannot run is an error). XL_GROUPED_PATH selects.
+    int gpath = 1;
     float* hbuf = nullptr;      // streaming kernel's h exchange (2 x kHBufWords, sentinel-filled)
+    // grouped path (xl_grouped.hip), sized by max_tokens * max_picks pairs
+    struct Group {
+        int32_t* ids = nullptr; float* w = nullptr; float* x = nullptr; float* shared = nullptr; float* out = nullptr;
+        int8_t* xq = nullptr; float* xd = nullptr;
+        int32_t* order = nullptr; int4* tasks = nullptr; int32_t* n_tasks = nullptr;
+        float* h = nullptr; int8_t* hq = nullptr; float* hd = nullptr; float* y = nullptr;
+        uint64_t hq_bytes = 0;
+    } grp;
     uint32_t* sync = nullptr;   // counters of the cooperative fused kernel
     uint64_t* htag = nullptr;   // single-launch handoff buffers (Layer3Args)
     uint64_t* hqtag = nullptr;
@@ -409,6 +421,28 @@ int32_t xl_open(uint32_t abi_version, const xl_config* cfg, xl_context** out, xl
             {reinterpret_cast<void**>(&ctx->tables), uint64_t(xl::kLayer3TableBytes)},
             {reinterpret_cast<void**>(&ctx->timeline), uint64_t(ctx->cus) * 16 * 32 * 8},
         };
+        if (cfg->max_tokens > 0) {
+            const uint64_t T = uint64_t(cfg->max_tokens), GP = T * uint64_t(P);
+            auto& g = ctx->grp;
+            g.hq_bytes = GP * uint64_t(ff / 256) * 512;
+            const std::vector<Part> gparts = {
+                {reinterpret_cast<void**>(&g.ids), GP * 4},
+                {reinterpret_cast<void**>(&g.w), GP * 4},
+                {reinterpret_cast<void**>(&g.x), T * dim * 4},
+                {reinterpret_cast<void**>(&g.shared), T * dim * 4},
+                {reinterpret_cast<void**>(&g.out), T * dim * 4},
+                {reinterpret_cast<void**>(&g.xq), T * dim},
+                {reinterpret_cast<void**>(&g.xd), T * (dim / 256) * 4},
+                {reinterpret_cast<void**>(&g.order), GP * 4},
+                {reinterpret_cast<void**>(&g.tasks), uint64_t(xl::group_max_tasks(int64_t(GP), cfg->n_experts)) * 16},
+                {reinterpret_cast<void**>(&g.n_tasks), 256},
+                {reinterpret_cast<void**>(&g.h), GP * ff * 4},
+                {reinterpret_cast<void**>(&g.hq), g.hq_bytes},
+                {reinterpret_cast<void**>(&g.hd), GP * (ff / 256) * 4},
+                {reinterpret_cast<void**>(&g.y), GP * dim * 4},
+            };
+            parts.insert(parts.end(), gparts.begin(), gparts.end());
+        }
         uint64_t total = 0;
         for (auto& p : parts) total += xl::align256(p.bytes);
         hip_check(hipMalloc(&ctx->ws, total), "workspace hipMalloc");
@@ -431,10 +465,13 @@ int32_t xl_open(uint32_t abi_version, const xl_config* cfg, xl_context** out, xl
         hip_check(hipMemset(ctx->hqtag, 0, size_t(P) * ff * 2), "tag clear");
         hip_check(hipMemset(ctx->ctl, 0, 256), "epoch clear");
         hip_check(hipMemset(ctx->hbuf, 0xff, size_t(2) * xl::kHBufWords * 4), "h exchange fill");
+        if (ctx->grp.hq) hip_check(hipMemset(ctx->grp.hq, 0, ctx->grp.hq_bytes), "grouped Q8_K(h) clear");   // the zero halves
         const std::vector<uint64_t> tab = layer_tables();
         hip_check(hipMemcpy(ctx->tables, tab.data(), tab.size() * 8, hipMemcpyHostToDevice), "table upload");
         ctx->path = env_int("XL_LAYER_PATH", 1);
         need(ctx->path >= 0 && ctx->path <= 4, XL_E_ARG, "XL_LAYER_PATH must be 0, 1, 2, 3 or 4");
+        ctx->gpath = env_int("XL_GROUPED_PATH", 1);
+        need(ctx->gpath >= 0 && ctx->gpath <= 2, XL_E_ARG, "XL_GROUPED_PATH must be 0, 1 or 2");
         *out = ctx;
     });
     if (rc != XL_OK && ctx) xl_close(ctx);
@@ -636,6 +673,86 @@ int32_t xl_experts_forward(xl_context* ctx, int32_t layer, const int32_t* ids, i
 int32_t xl_expert_forward(xl_context* ctx, int32_t layer, int32_t expert, const float* x, float* y, xl_error* err) {
     const int32_t id = expert;
     return xl_experts_forward(ctx, layer, &id, 1, x, y, err);
+}
+
+namespace {
+
+// Enqueues T tokens of layer `layer` on stream s: the grouped MFMA kernels when
+// the layer's gate/up are IQ2_XXS and its down IQ2_XS, otherwise one layer
+// call per token. All pointers are device pointers.
+void enqueue_grouped(xl_context* ctx, int32_t layer, int32_t T, int32_t k, const int32_t* d_ids, const float* d_w,
+                     const float* d_x, const float* d_shared, float* d_out, hipStream_t s) {
+    const int dim = ctx->cfg.dim, E = ctx->cfg.n_experts;
+    const int gu_mask = ctx->gu_mask[size_t(layer)], dn_mask = ctx->dn_mask[size_t(layer)];
+    Marks mark(ctx, s);
+    mark("");
+    if (ctx->gpath != 0 && gu_mask == 1 && dn_mask == 2) {
+        xl::GroupArgs a{};
+        a.descs = ctx->d_descs + size_t(layer) * E;
+        a.ids = d_ids; a.w = d_w; a.x = d_x; a.shared = d_shared; a.out = d_out;
+        a.T = T; a.k = k; a.n_experts = E; a.dim = dim; a.ff = ctx->cfg.ff;
+        const auto& g = ctx->grp;
+        a.xq = g.xq; a.xd = g.xd; a.order = g.order; a.tasks = g.tasks; a.n_tasks = g.n_tasks;
+        a.h = g.h; a.hq = g.hq; a.hd = g.hd; a.y = g.y;
+        a.tables = ctx->tables; a.err = ctx->err_flag;
+        const hipError_t e = xl::dev::launch_grouped(a, ctx->cus, s);
+        if (e == hipSuccess) {
+            mark("grouped");
+            return;
+        }
+        if (e != hipErrorNotSupported) hip_check(e, "grouped launch");
+        (void)hipGetLastError();
+    }
+    need(ctx->gpath != 2, XL_E_ARG, "XL_GROUPED_PATH=2: the grouped MFMA kernels cannot run this layer");
+    for (int t = 0; t < T; ++t)
+        enqueue_layer(ctx, layer, d_ids + size_t(t) * k, d_w + size_t(t) * k, k, d_x + size_t(t) * dim,
+                      d_shared ? d_shared + size_t(t) * dim : nullptr, d_out + size_t(t) * dim, s);
+}
+
+void check_grouped(const xl_context* ctx, int32_t T, int32_t k) {
+    need(ctx->cfg.max_tokens > 0, XL_E_STATE, "grouped path unused: the context was opened with max_tokens = 0");
+    need(T >= 1 && T <= ctx->cfg.max_tokens, XL_E_ARG, "token count outside 1..max_tokens");
+    need(k >= 1 && k <= ctx->cfg.max_picks, XL_E_ARG, "pick count outside 1..max_picks");
+}
+
+}  // namespace
+
+int32_t xl_grouped_forward(xl_context* ctx, int32_t layer, int32_t T, int32_t k, const int32_t* ids, const float* w,
+                           const float* x, const float* shared_or_null, float* out, xl_error* err) {
+    return guarded(ctx, err, [&] {
+        ready(ctx, true);
+        check_layer(ctx, layer);
+        check_grouped(ctx, T, k);
+        need(ids && w && x && out, XL_E_ARG, "null pointer");
+        const int dim = ctx->cfg.dim;
+        for (int t = 0; t < T; ++t) check_ids(ctx, ids + size_t(t) * k, k);
+        check_finite(w, size_t(T) * k, "route weights");
+        check_finite(x, size_t(T) * dim, "input vectors");
+        if (shared_or_null) check_finite(shared_or_null, size_t(T) * dim, "shared vectors");
+        hipStream_t s = ctx->stream;
+        auto& g = ctx->grp;
+        const size_t P = size_t(T) * k, X = size_t(T) * dim;
+        hip_check(hipMemcpyAsync(g.ids, ids, sizeof(int32_t) * P, hipMemcpyHostToDevice, s), "ids upload");
+        hip_check(hipMemcpyAsync(g.w, w, sizeof(float) * P, hipMemcpyHostToDevice, s), "weights upload");
+        hip_check(hipMemcpyAsync(g.x, x, sizeof(float) * X, hipMemcpyHostToDevice, s), "x upload");
+        if (shared_or_null)
+            hip_check(hipMemcpyAsync(g.shared, shared_or_null, sizeof(float) * X, hipMemcpyHostToDevice, s), "shared upload");
+        enqueue_grouped(ctx, layer, T, k, g.ids, g.w, g.x, shared_or_null ? g.shared : nullptr, g.out, s);
+        hip_check(hipMemcpyAsync(out, g.out, sizeof(float) * X, hipMemcpyDeviceToHost, s), "output download");
+        drain(ctx, s);
+    });
+}
+
+int32_t xl_grouped_forward_async(xl_context* ctx, int32_t layer, int32_t T, int32_t k, const int32_t* d_ids,
+                                 const float* d_w, const float* d_x, const float* d_shared_or_null, float* d_out,
+                                 void* stream, xl_error* err) {
+    return guarded(ctx, err, [&] {
+        ready(ctx, true);
+        check_layer(ctx, layer);
+        check_grouped(ctx, T, k);
+        need(d_ids && d_w && d_x && d_out, XL_E_ARG, "null device pointer");
+        enqueue_grouped(ctx, layer, T, k, d_ids, d_w, d_x, d_shared_or_null, d_out, pick_stream(ctx, stream));
+    });
 }
 
 int32_t xl_layer_forward(xl_context* ctx, int32_t layer, const int32_t* ids, const float* w, int32_t k, const float* x,

@@ -1,0 +1,494 @@
+// CDNA4 (gfx950) grouped routed-expert path: T tokens, each with its own k
+// picks, reading every touched expert's weights once per 16 of its (token,
+// pick) pairs. The result is that of T independent layer calls
+// (WarmRedirect::warm_compute_many per token, engine/strata/warm/runtime.hpp:13,
+// then the fixed-order join of runtime.cpp:183-188): per (row, pair) the same
+// exact integer block partials and the same fp16(d) * d_x fma over blocks in
+// block order as the row kernels.
+//
+//   bucket_kernel    one workgroup: pairs bucketed by expert id into tasks of
+//                    at most 16 pairs of one expert
+//   q8k_rows_kernel  Q8_K (q8k_core.hpp:30-38) of token rows (x) and pair rows
+//                    (h), written in the operand order of the MFMA kernels
+//   gu_kernel        gate/up + SwiGLU of every task (IQ2_XXS)
+//   dn_kernel        down of every task (IQ2_XS)
+//   gcombine_kernel  fixed-order combine per token, + shared
+//
+// MFMA: v_mfma_i32_16x16x32_i8 with M = pairs, N = weight rows, K = the 32
+// weights of one sub-block. Lane l supplies A[l % 16][8 (l / 16) .. + 7] (8
+// quants of pair l % 16), B[8 (l / 16) .. + 7][l % 16] (grid entry l / 16 of
+// row l % 16: 8 weights) and receives D[4 (l / 16) + r][l % 16], r = 0..3. The
+// lane that decodes a row's entry therefore also holds that row's outputs and
+// applies the row's sub-block scale (2s + 1) to them as integers: the block
+// partials are exact. Any K order works as long as A and B agree, which the
+// chunk-major activation layouts below guarantee.
+//
+// Weights stream from HBM through registers: each wave loads its 16 rows' next
+// block while it computes the current one, and touches the block four ahead
+// with one dword per row so that its lines are in L2 when the real loads come.
+#include <hip/hip_runtime.h>
+
+#include "xl_dev.hpp"
+#include "xl_format.hpp"
+#include "xl_internal.hpp"
+
+namespace xl::dev {
+namespace {
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+
+constexpr int kTile = 16;   // pairs per task (the MFMA M dimension)
+// Expanded codebook tables (layer_tables() in xl_api.cpp): 128 sign entries of
+// 16 B (byte mask, then the mask's low bits), the IQ2_XXS grid (256 x 8 B), the
+// IQ2_XS grid (512 x 8 B).
+constexpr int kTabSgn = 0, kTabXXS = 2048, kTabXS = 4096;
+
+// LDS of the MFMA kernels: grid entries as 16 B (g, -g) in C copies per entry
+// (lane copy = lane % C, so the 16 lanes of one ds_read_b128 pass never share
+// a bank), sign masks as 8 B in 32 copies (the 32 lanes of one ds_read_b64 pass
+// never share a bank) indexed by a whole byte whose top bit is not a sign bit.
+constexpr int kL_GRID = 0, kL_SGN = 65536, kL_Bytes = 131072;
+constexpr int kCopiesXXS = 16;   // 256 entries x 256 B: the entry byte lands in address byte 1
+constexpr int kCopiesXS = 8;     // 512 entries x 128 B: the 9-bit entry lands at address bit 7
+
+// Values every lane of the wave holds alike, moved to scalar registers (buffer
+// descriptors built from them stay scalar: no waterfall loops).
+__device__ __forceinline__ int uni(int v) { return __builtin_amdgcn_readfirstlane(v); }
+__device__ __forceinline__ const uint8_t* uni(const uint8_t* p) {
+    const uint64_t v = reinterpret_cast<uint64_t>(p);
+    const uint32_t lo = __builtin_amdgcn_readfirstlane(uint32_t(v)), hi = __builtin_amdgcn_readfirstlane(uint32_t(v >> 32));
+    return reinterpret_cast<const uint8_t*>((uint64_t(hi) << 32) | lo);
+}
+__device__ __forceinline__ int4 task_at(const int4* tasks, int i) {
+    const int4 t = tasks[i];
+    return make_int4(uni(t.x), uni(t.y), uni(t.z), 0);
+}
+__device__ __forceinline__ MatRef mat_at(const ExpertDesc* d, int e, int role) {
+    const MatRef m = d[e].m[role];
+    MatRef u;
+    u.base = uni(m.base);
+    u.off1 = (uint64_t(uint32_t(uni(int(m.off1 >> 32)))) << 32) | uint32_t(uni(int(uint32_t(m.off1))));
+    u.off2 = (uint64_t(uint32_t(uni(int(m.off2 >> 32)))) << 32) | uint32_t(uni(int(uint32_t(m.off2))));
+    u.type = uni(m.type);
+    u.nb = uni(m.nb);
+    return u;
+}
+
+__device__ __forceinline__ uint32_t perm(uint32_t hi, uint32_t lo, uint32_t sel) {
+    return __builtin_amdgcn_perm(hi, lo, sel);
+}
+__device__ __forceinline__ uint32_t bfi(uint32_t m, uint32_t x, uint32_t y) { return (m & x) | (~m & y); }
+__device__ __forceinline__ long pack64(uint32_t lo, uint32_t hi) {
+    return static_cast<long>((uint64_t(hi) << 32) | lo);
+}
+__device__ __forceinline__ v4i mfma(long a, long b, v4i c) {
+    return __builtin_amdgcn_mfma_i32_16x16x32_i8(a, b, c, 0, 0, 0);
+}
+__device__ __forceinline__ int mad24(int a, int b, int c) { return __mul24(a, b) + c; }   // v_mad_i32_i24
+// Bytewise negation of grid bytes (all in 1..127, so no byte borrows).
+__device__ __forceinline__ uint64_t neg_grid(uint64_t g) { return ~g + 0x0101010101010101ull; }
+
+// Sign tables: 256 rows (row r = sign entry r & 127) x 32 copies x 8 B.
+__device__ __forceinline__ void fill_signs(uint8_t* lds, const uint64_t* tab, int t, int nt) {
+    for (int i = t; i < 256 * 32; i += nt)
+        *reinterpret_cast<uint64_t*>(lds + kL_SGN + 8 * i) = tab[kTabSgn / 8 + 2 * ((i >> 5) & 127)];
+}
+// Grid tables: E entries x C copies x 16 B (g, -g).
+template <int E, int C>
+__device__ __forceinline__ void fill_grid(uint8_t* lds, const uint64_t* grid, int t, int nt) {
+    for (int i = t; i < E * C; i += nt) {
+        const uint64_t g = grid[i / C], n = neg_grid(g);
+        *reinterpret_cast<uint4*>(lds + kL_GRID + 16 * i) =
+            make_uint4(uint32_t(g), uint32_t(g >> 32), uint32_t(n), uint32_t(n >> 32));
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Buckets: counts per expert in LDS, one scan, then each valid pair takes a
+// slot of its expert's range. The slot order inside a range varies run to run;
+// no result depends on it (every output of a pair is computed from that pair's
+// operands only, in a fixed order).
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(1024) void bucket_kernel(GroupArgs a) {
+    __shared__ int cnt[kGroupMaxExperts];
+    __shared__ int cur[kGroupMaxExperts];
+    __shared__ int part[2 * 1024];
+    const int t = threadIdx.x, P = a.T * a.k, E = a.n_experts;
+    for (int e = t; e < E; e += 1024) cnt[e] = 0;
+    __syncthreads();
+    for (int p = t; p < P; p += 1024) {
+        const int e = a.ids[p];
+        if (e >= 0 && e < E) atomicAdd(&cnt[e], 1);
+        else atomicOr(a.err, kDevErrExpertId);
+    }
+    __syncthreads();
+    const int per = (E + 1023) / 1024, e0 = min(E, t * per), e1 = min(E, e0 + per);
+    int sp = 0, st = 0;
+    for (int e = e0; e < e1; ++e) {
+        sp += cnt[e];
+        st += (cnt[e] + kTile - 1) / kTile;
+    }
+    part[t] = sp;
+    part[1024 + t] = st;
+    __syncthreads();
+    for (int off = 1; off < 1024; off <<= 1) {   // inclusive scans of pairs and tasks
+        const int v0 = t >= off ? part[t - off] : 0, v1 = t >= off ? part[1024 + t - off] : 0;
+        __syncthreads();
+        part[t] += v0;
+        part[1024 + t] += v1;
+        __syncthreads();
+    }
+    int bp = part[t] - sp, bt = part[1024 + t] - st;
+    for (int e = e0; e < e1; ++e) {
+        const int c = cnt[e];
+        for (int i = 0; i * kTile < c; ++i) a.tasks[bt + i] = make_int4(e, bp + kTile * i, min(kTile, c - kTile * i), 0);
+        cur[e] = bp;
+        bp += c;
+        bt += (c + kTile - 1) / kTile;
+    }
+    if (t == 1023) *a.n_tasks = part[2047];
+    __syncthreads();
+    for (int p = t; p < P; p += 1024) {
+        const int e = a.ids[p];
+        if (e >= 0 && e < E) a.order[atomicAdd(&cur[e], 1)] = p;
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Q8_K of 256-value blocks of rows, one wave per block. Output orders:
+//   ROWS_X: per block, chunk e (entry e of every sub-block) holds the 8 quants
+//           of entry e of sub-blocks 0..7: byte e * 64 + 8 c + j;
+//   ROWS_H: per block 512 B, chunk e holds per sub-block c 16 B {A1, A2}: the 8
+//           quants of entry e in A1 when e < 2 (the first 16 weights of the
+//           sub-block, scale nibble 0), in A2 when e >= 2; the other half stays
+//           zero (cleared once, never written).
+// Pair rows of a bad id are skipped (their h is never written).
+// ---------------------------------------------------------------------------
+enum { ROWS_X = 0, ROWS_H = 1 };
+template <int MODE>
+__global__ __launch_bounds__(256) void q8k_rows_kernel(const float* __restrict__ src, int rows, int nb,
+                                                       int8_t* __restrict__ q, float* __restrict__ d,
+                                                       const int32_t* __restrict__ ids, int n_experts,
+                                                       int* __restrict__ err) {
+    const int b = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (b >= rows * nb) return;   // wave-uniform
+    if (MODE == ROWS_H) {
+        const int e = ids[b / nb];
+        if (e < 0 || e >= n_experts) return;
+    }
+    const int lane = threadIdx.x & 63;
+    const float4 v4 = reinterpret_cast<const float4*>(src + size_t(b) * 256)[lane];
+    const float v[4] = {v4.x, v4.y, v4.z, v4.w};
+    const Q8Lane r = q8k_lane(v, lane);
+    if (!r.finite && lane == 0) atomicOr(err, kDevErrNonFinite);
+    const int c = lane >> 3, e = (lane >> 1) & 3, j = 4 * (lane & 1);   // values 4 lane .. + 3
+    if (MODE == ROWS_X)
+        *reinterpret_cast<uint32_t*>(q + size_t(b) * 256 + 64 * e + 8 * c + j) = r.packed;
+    else
+        *reinterpret_cast<uint32_t*>(q + size_t(b) * 512 + 128 * e + 16 * c + (e >= 2 ? 8 : 0) + j) = r.packed;
+    if (lane == 0) d[b] = r.d;
+}
+
+// Keeps a value alive without storing it (the L2 line touches).
+__device__ __forceinline__ void sink(uint32_t& acc, uint32_t v) { acc ^= v; }
+
+// Buffer loads: the base in a scalar descriptor, the per-lane byte offset in
+// voffset, a uniform plane offset in soffset.
+typedef uint32_t v4u32 __attribute__((ext_vector_type(4)));
+typedef uint32_t v2u32 __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void* p) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, -1, 0x00020000);
+}
+__device__ __forceinline__ uint4 ld128(__amdgpu_buffer_rsrc_t r, uint32_t v, uint32_t so = 0) {
+    const v4u32 q = __builtin_amdgcn_raw_buffer_load_b128(r, v, so, 0);
+    return make_uint4(q.x, q.y, q.z, q.w);
+}
+__device__ __forceinline__ uint2 ld64(__amdgpu_buffer_rsrc_t r, uint32_t v, uint32_t so = 0) {
+    const v2u32 q = __builtin_amdgcn_raw_buffer_load_b64(r, v, so, 0);
+    return make_uint2(q.x, q.y);
+}
+__device__ __forceinline__ uint32_t ld32(__amdgpu_buffer_rsrc_t r, uint32_t v, uint32_t so = 0) {
+    return __builtin_amdgcn_raw_buffer_load_b32(r, v, so, 0);
+}
+__device__ __forceinline__ uint16_t ld16(__amdgpu_buffer_rsrc_t r, uint32_t v, uint32_t so = 0) {
+    return __builtin_amdgcn_raw_buffer_load_b16(r, v, so, 0);
+}
+
+// One block's operands for one wave.
+struct GuOps {
+    uint4 g[4], u[4], a[4];   // gate / up quants of the lane's row, the lane's activation chunk
+    uint16_t dg, du;          // fp16 block scales
+    float xd[4];              // Q8_K(x) block scales of the lane's 4 output pairs
+};
+struct DnOps {
+    uint4 q[4], a[8];         // down codes of the lane's row, the lane's split activation chunk
+    uint2 s;                  // scale nibbles
+    uint16_t d;               // fp16 block scale
+    float hd[4];              // Q8_K(h) block scales of the lane's 4 output pairs
+};
+
+// ---------------------------------------------------------------------------
+// gate/up + SwiGLU. Work item = (task, group of NW * 16 rows); wave wv owns
+// rows 16 wv .. + 15 of the group in gate and up.
+// ---------------------------------------------------------------------------
+template <int NW>
+__global__ __launch_bounds__(NW * 64, 1) void gu_kernel(GroupArgs a) {
+    __shared__ __attribute__((aligned(16))) uint8_t lds[kL_Bytes];
+    const int t = threadIdx.x, lane = t & 63, wv = t >> 6;
+    fill_grid<256, kCopiesXXS>(lds, a.tables + kTabXXS / 8, t, NW * 64);
+    fill_signs(lds, a.tables, t, NW * 64);
+    __syncthreads();
+
+    const int col = lane & 15, e4 = lane >> 4;
+    const int nb = a.dim / 256, groups = a.ff / (NW * 16);
+    const int items = uni(*a.n_tasks) * groups;
+    const uint32_t lo_g = uint32_t(lane & (kCopiesXXS - 1)) << 4;        // kL_GRID = 0
+    const uint32_t lo_s = (uint32_t(lane & 31) << 3) | (1u << 16);       // kL_SGN = 1 << 16
+    const uint32_t sel = 0x0C020000u | (uint32_t(4 + e4) << 8);          // address byte 1 <- byte e4 of the word
+    uint32_t sunk = 0;
+    for (int item = blockIdx.x; item < items; item += gridDim.x) {
+        const int task = item / groups, grp = item - task * groups;
+        const int4 tk = task_at(a.tasks, task);
+        const int row = grp * NW * 16 + wv * 16 + col;
+        const int pa = a.order[tk.y + (col < tk.z ? col : 0)];   // A operand: pair col of the task
+        const uint32_t va = uint32_t((pa / a.k) * a.dim + 64 * e4);   // the lane's activation chunk, block 0
+        int po[4];
+        uint32_t vxd[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int pos = 4 * e4 + r;
+            po[r] = pos < tk.z ? a.order[tk.y + pos] : -1;
+            vxd[r] = uint32_t((po[r] >= 0 ? po[r] / a.k : pa / a.k) * nb) * 4u;
+        }
+        const MatRef G = mat_at(a.descs, tk.x, 0), U = mat_at(a.descs, tk.x, 1);
+        const __amdgpu_buffer_rsrc_t rg = rsrc(G.base), ru = rsrc(U.base), rx = rsrc(a.xq), rxd = rsrc(a.xd);
+        const uint32_t vq = uint32_t(row * nb) * 64u, vd = uint32_t(row * nb) * 2u;
+        const uint32_t og = uint32_t(G.off1), ou = uint32_t(U.off1);
+        auto load = [&](GuOps& o, int blk) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                o.g[i] = ld128(rg, vq + 64u * blk + 16u * i);
+                o.u[i] = ld128(ru, vq + 64u * blk + 16u * i);
+                o.a[i] = ld128(rx, va + 256u * blk + 16u * i);
+            }
+            o.dg = ld16(rg, vd + 2u * blk, og);
+            o.du = ld16(ru, vd + 2u * blk, ou);
+#pragma unroll
+            for (int r = 0; r < 4; ++r) o.xd[r] = __uint_as_float(ld32(rxd, vxd[r] + 4u * blk));
+        };
+        auto touch = [&](int blk) { return ld32(rg, vq + 64u * blk) ^ ld32(ru, vq + 64u * blk); };
+        float accg[4] = {0.0f, 0.0f, 0.0f, 0.0f}, accu[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+        auto compute = [&](const GuOps& o) {
+            int big[4] = {0, 0, 0, 0}, biu[4] = {0, 0, 0, 0};
+#pragma unroll
+            for (int c = 0; c < 8; ++c) {
+                const uint32_t* wg = reinterpret_cast<const uint32_t*>(o.g) + 2 * c;
+                const uint32_t* wu = reinterpret_cast<const uint32_t*>(o.u) + 2 * c;
+                const uint32_t* av = reinterpret_cast<const uint32_t*>(o.a) + 2 * c;
+                const long A = pack64(av[0], av[1]);
+                {
+                    const uint4 g = *reinterpret_cast<const uint4*>(lds + perm(wg[0], lo_g, sel));
+                    const uint2 m = *reinterpret_cast<const uint2*>(lds + perm(wg[1], lo_s, sel));
+                    const v4i C = mfma(A, pack64(bfi(m.x, g.z, g.x), bfi(m.y, g.w, g.y)), v4i{0, 0, 0, 0});
+                    const int ls = int(__builtin_amdgcn_udot4((wg[1] >> 7) & 0x01010101u, 0x10080402u, 1u, false));
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) big[r] = mad24(ls, C[r], big[r]);
+                }
+                {
+                    const uint4 g = *reinterpret_cast<const uint4*>(lds + perm(wu[0], lo_g, sel));
+                    const uint2 m = *reinterpret_cast<const uint2*>(lds + perm(wu[1], lo_s, sel));
+                    const v4i C = mfma(A, pack64(bfi(m.x, g.z, g.x), bfi(m.y, g.w, g.y)), v4i{0, 0, 0, 0});
+                    const int ls = int(__builtin_amdgcn_udot4((wu[1] >> 7) & 0x01010101u, 0x10080402u, 1u, false));
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) biu[r] = mad24(ls, C[r], biu[r]);
+                }
+            }
+            const float dgf = h2f(o.dg), duf = h2f(o.du);
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                accg[r] = fmaf(__fmul_rn(dgf, o.xd[r]), float(big[r]), accg[r]);
+                accu[r] = fmaf(__fmul_rn(duf, o.xd[r]), float(biu[r]), accu[r]);
+            }
+        };
+        // Two operand sets alternate over a 4-step unrolled loop (no register
+        // copies, so no wait ever covers a load issued in the same step); line
+        // touches four blocks ahead in four fixed registers.
+        GuOps s0, s1;
+        load(s0, 0);
+        uint32_t t0 = touch(min(1, nb - 1)), t1 = touch(min(2, nb - 1)), t2 = touch(min(3, nb - 1)),
+                 t3 = touch(min(4, nb - 1));
+        for (int b = 0; b < nb; b += 4) {
+            load(s1, min(b + 1, nb - 1));
+            sink(sunk, t0);
+            t0 = touch(min(b + 5, nb - 1));
+            compute(s0);
+            load(s0, min(b + 2, nb - 1));
+            sink(sunk, t1);
+            t1 = touch(min(b + 6, nb - 1));
+            if (b + 1 < nb) compute(s1);
+            load(s1, min(b + 3, nb - 1));
+            sink(sunk, t2);
+            t2 = touch(min(b + 7, nb - 1));
+            if (b + 2 < nb) compute(s0);
+            load(s0, min(b + 4, nb - 1));
+            sink(sunk, t3);
+            t3 = touch(min(b + 8, nb - 1));
+            if (b + 3 < nb) compute(s1);
+        }
+        sink(sunk, t0 ^ t1 ^ t2 ^ t3);
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+            if (po[r] >= 0)
+                a.h[size_t(po[r]) * a.ff + row] = silu_mul3(__fmul_rn(0.125f, accg[r]), __fmul_rn(0.125f, accu[r]));
+    }
+    if (sunk == 0x9e3779b9u && lane == 64) a.h[0] = 0.0f;   // never true (lane < 64): keeps the touches
+}
+
+// ---------------------------------------------------------------------------
+// down. Work item = (task, group of NW * 16 output rows). IQ2_XS keeps a scale
+// nibble per 16 weights: per sub-block one MFMA over the first half (A1) and
+// one over the second (A2), from the zero-interleaved Q8_K(h) chunks.
+// ---------------------------------------------------------------------------
+template <int NW>
+__global__ __launch_bounds__(NW * 64, 1) void dn_kernel(GroupArgs a) {
+    __shared__ __attribute__((aligned(16))) uint8_t lds[kL_Bytes];
+    const int t = threadIdx.x, lane = t & 63, wv = t >> 6;
+    fill_grid<512, kCopiesXS>(lds, a.tables + kTabXS / 8, t, NW * 64);
+    fill_signs(lds, a.tables, t, NW * 64);
+    __syncthreads();
+
+    const int col = lane & 15, e4 = lane >> 4;
+    const int nb = a.ff / 256, groups = a.dim / (NW * 16);
+    const int items = uni(*a.n_tasks) * groups;
+    const uint32_t lo_x = uint32_t(lane & (kCopiesXS - 1)) << 4;        // kL_GRID = 0
+    const uint32_t lo_s = (uint32_t(lane & 31) << 3) | (1u << 16);      // kL_SGN = 1 << 16
+    const uint32_t selc = 0x0C0C0000u | (uint32_t(2 * e4 + 1) << 8) | uint32_t(2 * e4);   // code e4 of 4 u16
+    const uint32_t sel0 = 0x0C020400u;                                  // address byte 1 <- byte 0 of the code
+    uint32_t sunk = 0;
+    for (int item = blockIdx.x; item < items; item += gridDim.x) {
+        const int task = item / groups, grp = item - task * groups;
+        const int4 tk = task_at(a.tasks, task);
+        const int row = grp * NW * 16 + wv * 16 + col;
+        const int pa = a.order[tk.y + (col < tk.z ? col : 0)];
+        const uint32_t va = uint32_t(pa * nb) * 512u + 128u * e4;   // the lane's split activation chunk, block 0
+        int po[4];
+        uint32_t vhd[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int pos = 4 * e4 + r;
+            po[r] = pos < tk.z ? a.order[tk.y + pos] : -1;
+            vhd[r] = uint32_t((po[r] >= 0 ? po[r] : pa) * nb) * 4u;
+        }
+        const MatRef D = mat_at(a.descs, tk.x, 2);
+        const __amdgpu_buffer_rsrc_t rd = rsrc(D.base), rh = rsrc(a.hq), rhd = rsrc(a.hd);
+        const uint32_t vq = uint32_t(row * nb) * 64u, vs = uint32_t(row * nb) * 8u, vd = uint32_t(row * nb) * 2u;
+        const uint32_t os = uint32_t(D.off1), od = uint32_t(D.off2);
+        auto load = [&](DnOps& o, int blk) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) o.q[i] = ld128(rd, vq + 64u * blk + 16u * i);
+#pragma unroll
+            for (int i = 0; i < 8; ++i) o.a[i] = ld128(rh, va + 512u * blk + 16u * i);
+            o.s = ld64(rd, vs + 8u * blk, os);
+            o.d = ld16(rd, vd + 2u * blk, od);
+#pragma unroll
+            for (int r = 0; r < 4; ++r) o.hd[r] = __uint_as_float(ld32(rhd, vhd[r] + 4u * blk));
+        };
+        auto touch = [&](int blk) { return ld32(rd, vq + 64u * blk); };
+        float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+        auto compute = [&](const DnOps& o) {
+            int bi[4] = {0, 0, 0, 0};
+#pragma unroll
+            for (int c = 0; c < 8; ++c) {
+                const uint32_t* w = reinterpret_cast<const uint32_t*>(o.q) + 2 * c;
+                const uint32_t* av = reinterpret_cast<const uint32_t*>(o.a) + 4 * c;
+                const uint32_t code = perm(w[1], w[0], selc);
+                const uint4 g = *reinterpret_cast<const uint4*>(lds + ((code & 0xff80u) | lo_x));
+                const uint2 m = *reinterpret_cast<const uint2*>(lds + perm(code, lo_s, sel0));
+                const long B = pack64(bfi(m.x, g.z, g.x), bfi(m.y, g.w, g.y));
+                const v4i C1 = mfma(pack64(av[0], av[1]), B, v4i{0, 0, 0, 0});
+                const v4i C2 = mfma(pack64(av[2], av[3]), B, v4i{0, 0, 0, 0});
+                const uint32_t sb = ((c < 4 ? o.s.x : o.s.y) >> (8 * (c & 3))) & 0xffu;
+                const int ls1 = int(((sb & 15u) << 1) | 1u), ls2 = int(((sb >> 3) & 30u) | 1u);
+#pragma unroll
+                for (int r = 0; r < 4; ++r) bi[r] = mad24(ls2, C2[r], mad24(ls1, C1[r], bi[r]));
+            }
+            const float ddf = h2f(o.d);
+#pragma unroll
+            for (int r = 0; r < 4; ++r) acc[r] = fmaf(__fmul_rn(ddf, o.hd[r]), float(bi[r]), acc[r]);
+        };
+        DnOps s0, s1;
+        load(s0, 0);
+        uint32_t t0 = touch(min(1, nb - 1)), t1 = touch(min(2, nb - 1)), t2 = touch(min(3, nb - 1)),
+                 t3 = touch(min(4, nb - 1));
+        for (int b = 0; b < nb; b += 4) {
+            load(s1, min(b + 1, nb - 1));
+            sink(sunk, t0);
+            t0 = touch(min(b + 5, nb - 1));
+            compute(s0);
+            load(s0, min(b + 2, nb - 1));
+            sink(sunk, t1);
+            t1 = touch(min(b + 6, nb - 1));
+            if (b + 1 < nb) compute(s1);
+            load(s1, min(b + 3, nb - 1));
+            sink(sunk, t2);
+            t2 = touch(min(b + 7, nb - 1));
+            if (b + 2 < nb) compute(s0);
+            load(s0, min(b + 4, nb - 1));
+            sink(sunk, t3);
+            t3 = touch(min(b + 8, nb - 1));
+            if (b + 3 < nb) compute(s1);
+        }
+        sink(sunk, t0 ^ t1 ^ t2 ^ t3);
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+            if (po[r] >= 0) a.y[size_t(po[r]) * a.dim + row] = __fmul_rn(0.125f, acc[r]);
+    }
+    if (sunk == 0x9e3779b9u && lane == 64) a.y[0] = 0.0f;   // never true (lane < 64): keeps the touches
+}
+
+// ---------------------------------------------------------------------------
+// Fixed-order combine per token (runtime.cpp:183-188): ascending expert id,
+// out = fma(w, y, out) from +0, then + shared. A bad id contributes nothing.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void gcombine_kernel(GroupArgs a) {
+    const int tok = blockIdx.y, c = blockIdx.x * 256 + threadIdx.x;
+    if (c >= a.dim) return;
+    const int32_t* ids = a.ids + size_t(tok) * a.k;
+    int order[16];
+    int n = 0;
+    for (int i = 0; i < a.k; ++i)
+        if (ids[i] >= 0 && ids[i] < a.n_experts) order[n++] = i;
+    for (int i = 1; i < n; ++i)
+        for (int j = i; j > 0 && ids[order[j]] < ids[order[j - 1]]; --j) {
+            const int s = order[j]; order[j] = order[j - 1]; order[j - 1] = s;
+        }
+    float acc = 0.0f;
+    for (int i = 0; i < n; ++i) {
+        const int p = tok * a.k + order[i];
+        acc = fmaf(a.w[p], a.y[size_t(p) * a.dim + c], acc);
+    }
+    if (a.shared) acc = __fadd_rn(acc, a.shared[size_t(tok) * a.dim + c]);
+    a.out[size_t(tok) * a.dim + c] = acc;
+}
+
+}  // namespace
+
+hipError_t launch_grouped(const GroupArgs& args, int cus, hipStream_t s) {
+    constexpr int NW = 8;
+    if (args.T < 1 || args.k < 1 || args.k > 16 || args.n_experts > kGroupMaxExperts || args.dim % (NW * 16) ||
+        args.ff % (NW * 16) || args.dim % 256 || args.ff % 256 || args.dim > 4096 || args.ff > 4096)
+        return hipErrorNotSupported;
+    const int P = args.T * args.k;
+    hipLaunchKernelGGL(bucket_kernel, dim3(1), dim3(1024), 0, s, args);
+    const int nbx = args.dim / 256, nbh = args.ff / 256;
+    hipLaunchKernelGGL(q8k_rows_kernel<ROWS_X>, dim3((args.T * nbx + 3) / 4), dim3(256), 0, s, args.x, args.T, nbx,
+                       args.xq, args.xd, args.ids, args.n_experts, args.err);
+    hipLaunchKernelGGL(gu_kernel<NW>, dim3(cus), dim3(NW * 64), 0, s, args);
+    hipLaunchKernelGGL(q8k_rows_kernel<ROWS_H>, dim3((P * nbh + 3) / 4), dim3(256), 0, s, args.h, P, nbh, args.hq,
+                       args.hd, args.ids, args.n_experts, args.err);
+    hipLaunchKernelGGL(dn_kernel<NW>, dim3(cus), dim3(NW * 64), 0, s, args);
+    hipLaunchKernelGGL(gcombine_kernel, dim3((args.dim + 255) / 256, args.T), dim3(256), 0, s, args);
+    return hipGetLastError();
+}
+
+}  // namespace xl::dev

@@ -90,6 +90,30 @@ struct Layer3Args {
     float* hbuf;                // streaming kernel: 2 x kHBufWords h words, sentinel-filled (see xl_stream.hip)
 };
 constexpr int kHBufWords = 16 * 4096;      // k_max * ff_max
+
+// Arguments of the grouped path (xl_grouped.hip): T tokens with k picks each,
+// P = T * k (token, pick) pairs, pair p = token p / k. Device pointers.
+struct GroupArgs {
+    const ExpertDesc* descs;    // this layer's n_experts descriptors
+    const int32_t* ids;         // P expert ids
+    const float* w;             // P route weights
+    const float* x;             // T * dim
+    const float* shared;        // T * dim, or null
+    float* out;                 // T * dim
+    int T, k, n_experts, dim, ff;
+    int8_t* xq; float* xd;      // Q8_K(x) of every token, split form: T * dim quants, T * dim / 256 scales
+    int32_t* order;             // P pair indices, bucketed by expert id (bad ids left out)
+    int4* tasks;                // (expert, first slot in order, pairs <= 16, 0) per task
+    int32_t* n_tasks;           // tasks written by the bucket kernel
+    float* h;                   // P * ff
+    int8_t* hq; float* hd;      // Q8_K(h): P * ff / 256 blocks of 512 B (the down kernel's half-split form), scales
+    float* y;                   // P * dim
+    const uint64_t* tables;     // expanded codebooks (kLayer3TableBytes)
+    int* err;
+};
+constexpr int kGroupMaxExperts = 8192;   // experts per layer the bucket kernel counts in LDS
+// Tasks the bucket kernel can write for P pairs: one per started tile of 16 pairs of an expert.
+inline int64_t group_max_tasks(int64_t P, int64_t n_experts) { return P / 16 + (P < n_experts ? P : n_experts) + 1; }
 constexpr int kLayer3TableBytes = 24576;   // expanded codebooks of the single-launch kernel
 
 namespace dev {
@@ -100,6 +124,9 @@ hipError_t launch_layer3(const Layer3Args& args, int gu_types, int dn_types, int
 // Streaming layer for IQ2_XXS gate/up + IQ2_XS down: hipErrorNotSupported when
 // (dim, ff, k) has no instance.
 hipError_t launch_stream(const Layer3Args& args, int cus, hipStream_t s);
+// Grouped path: hipErrorNotSupported unless gate/up are IQ2_XXS, down IQ2_XS and
+// the shapes fit (dim, ff multiples of 128; n_experts <= kGroupMaxExperts).
+hipError_t launch_grouped(const GroupArgs& args, int cus, hipStream_t s);
 // Fused layer: returns hipErrorNotSupported when (dim, ff) has no fused
 // instance or the device cannot hold the cooperative grid.
 hipError_t launch_layer_fused(const LayerArgs& args, int type_mask, int cus, hipStream_t s);

@@ -74,6 +74,8 @@ _SIGNATURES = {
     "xl_expert_trace": (_I32, [_P, _I32, _I32, _f32p, _P, _P, _P, _P, _P, _ErrP]),
     "xl_layer_forward_async": (_I32, [_P, _I32, _P, _P, _I32, _P, _P, _P, _P, _ErrP]),
     "xl_sync": (_I32, [_P, _P, _ErrP]),
+    "xl_grouped_forward": (_I32, [_P, _I32, _I32, _I32, _i32p, _f32p, _f32p, _P, _f32p, _ErrP]),
+    "xl_grouped_forward_async": (_I32, [_P, _I32, _I32, _I32, _P, _P, _P, _P, _P, _P, _ErrP]),
     "xl_quantize_q8k_async": (_I32, [_P, _P, _I32, _I32, _P, _P, _ErrP]),
     "xl_matvec_async": (_I32, [_P, _I32, _P, _I32, _I32, _P, _P, _P, _P, _ErrP]),
     "xl_profile_begin": (_I32, [_P, _I32, _ErrP]),
@@ -246,6 +248,19 @@ class Lane:
                    None if sh is None else sh.ctypes.data, out)
         return out
 
+    def grouped_forward(self, layer: int, ids: np.ndarray, weights: np.ndarray, x: np.ndarray,
+                        shared: Optional[np.ndarray] = None) -> np.ndarray:
+        """T tokens at once: ids, weights [T, k]; x, shared [T, dim] -> out [T, dim]."""
+        ids = np.ascontiguousarray(ids, dtype=np.int32)
+        T, k = ids.shape
+        w = np.ascontiguousarray(weights, dtype=np.float32).reshape(T, k)
+        x = np.ascontiguousarray(x, dtype=np.float32).reshape(T, self.dim)
+        sh = None if shared is None else np.ascontiguousarray(shared, dtype=np.float32).reshape(T, self.dim)
+        out = np.zeros((T, self.dim), dtype=np.float32)
+        self._call("xl_grouped_forward", layer, T, k, ids.reshape(-1), w.reshape(-1), x.reshape(-1),
+                   None if sh is None else sh.ctypes.data, out.reshape(-1))
+        return out
+
     def expert_trace(self, layer: int, e: int, x: np.ndarray) -> dict:
         ff, dim = self.ff, self.dim
         g = np.zeros(ff, np.float32); u = np.zeros(ff, np.float32); h = np.zeros(ff, np.float32)
@@ -258,6 +273,12 @@ class Lane:
     def layer_forward_async(self, layer: int, ids, w, x, out, shared=None, stream=None) -> None:
         self._call("xl_layer_forward_async", layer, _ptr(ids), _ptr(w), int(ids.numel()), _ptr(x), _ptr(shared),
                    _ptr(out), None if stream is None else int(stream))
+
+    def grouped_forward_async(self, layer: int, ids, w, x, out, shared=None, stream=None) -> None:
+        """ids, w: [T, k] device tensors; x, out (and shared): [T, dim]."""
+        T, k = int(ids.shape[0]), int(ids.shape[1])
+        self._call("xl_grouped_forward_async", layer, T, k, _ptr(ids), _ptr(w), _ptr(x), _ptr(shared), _ptr(out),
+                   None if stream is None else int(stream))
 
     def sync(self, stream=None) -> None:
         self._call("xl_sync", None if stream is None else int(stream))

@@ -120,6 +120,22 @@ int32_t xl_layer_forward_async(xl_context* ctx, int32_t layer, const int32_t* d_
                                xl_error* err);
 int32_t xl_sync(xl_context* ctx, void* stream, xl_error* err);
 
+/* ---- grouped tokens (prefill / batched decode) ------------------------------
+ * T tokens, each with its own k picks: ids and w are T x k (token-major), x,
+ * shared and out T x dim. The result is that of T xl_layer_forward calls (per
+ * token: WarmRedirect::warm_compute_many, engine/strata/warm/runtime.hpp:13,
+ * then warm_execute's fixed-order combine, runtime.cpp:180-188), with every
+ * touched expert's weights read once per 16 of its (token, pick) pairs on
+ * int8 MFMA for IQ2_XXS gate/up + IQ2_XS down layers (other layers run one
+ * layer call per token). Needs a context opened with max_tokens >= T; picks
+ * of one token unique. The async form takes device pointers and checks ids on
+ * the device (a bad id sets the flag; that pick contributes nothing). */
+int32_t xl_grouped_forward(xl_context* ctx, int32_t layer, int32_t T, int32_t k, const int32_t* ids, const float* w,
+                           const float* x, const float* shared_or_null, float* out, xl_error* err);
+int32_t xl_grouped_forward_async(xl_context* ctx, int32_t layer, int32_t T, int32_t k, const int32_t* d_ids,
+                                 const float* d_w, const float* d_x, const float* d_shared_or_null, float* d_out,
+                                 void* stream, xl_error* err);
+
 /* ---- primitives (device pointers) -----------------------------------------
  * q8k_* : Q8_K quantization of rows x k floats (k a multiple of 256) into
  * rows*k/256 blocks of 292 bytes (q8k_core.hpp:13-38, hip_q8k.hpp:9). */

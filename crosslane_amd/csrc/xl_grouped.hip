@@ -278,31 +278,43 @@ __global__ __launch_bounds__(NW * 64, 1) void gu_kernel(GroupArgs a) {
         };
         auto touch = [&](int blk) { return ld32(rg, vq + 64u * blk) ^ ld32(ru, vq + 64u * blk); };
         float accg[4] = {0.0f, 0.0f, 0.0f, 0.0f}, accu[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+        // Sub-block c of a matrix: its grid entry (g, -g) and sign mask from LDS,
+        // then B = signed entry, one MFMA, the row's (2s + 1) on the four outputs.
+        // All eight gate lookups are issued first; each up lookup is issued as a
+        // gate one is consumed, so about seven are in flight throughout.
+        struct Look { uint4 g; uint2 m; };
+        auto look = [&](const uint4* q, int c) {
+            const uint32_t* w = reinterpret_cast<const uint32_t*>(q) + 2 * c;
+            Look L;
+            L.g = *reinterpret_cast<const uint4*>(lds + perm(w[0], lo_g, sel));
+            L.m = *reinterpret_cast<const uint2*>(lds + perm(w[1], lo_s, sel));
+            return L;
+        };
+        auto use = [&](const Look& L, const uint4* q, int c, long A, int (&bi)[4]) {
+            const uint32_t aux = reinterpret_cast<const uint32_t*>(q)[2 * c + 1];
+            const v4i C = mfma(A, pack64(bfi(L.m.x, L.g.z, L.g.x), bfi(L.m.y, L.g.w, L.g.y)), v4i{0, 0, 0, 0});
+            const int ls = int(__builtin_amdgcn_udot4((aux >> 7) & 0x01010101u, 0x10080402u, 1u, false));
+#pragma unroll
+            for (int r = 0; r < 4; ++r) bi[r] = mad24(ls, C[r], bi[r]);
+        };
         auto compute = [&](const GuOps& o) {
             int big[4] = {0, 0, 0, 0}, biu[4] = {0, 0, 0, 0};
+            long A[8];
 #pragma unroll
             for (int c = 0; c < 8; ++c) {
-                const uint32_t* wg = reinterpret_cast<const uint32_t*>(o.g) + 2 * c;
-                const uint32_t* wu = reinterpret_cast<const uint32_t*>(o.u) + 2 * c;
                 const uint32_t* av = reinterpret_cast<const uint32_t*>(o.a) + 2 * c;
-                const long A = pack64(av[0], av[1]);
-                {
-                    const uint4 g = *reinterpret_cast<const uint4*>(lds + perm(wg[0], lo_g, sel));
-                    const uint2 m = *reinterpret_cast<const uint2*>(lds + perm(wg[1], lo_s, sel));
-                    const v4i C = mfma(A, pack64(bfi(m.x, g.z, g.x), bfi(m.y, g.w, g.y)), v4i{0, 0, 0, 0});
-                    const int ls = int(__builtin_amdgcn_udot4((wg[1] >> 7) & 0x01010101u, 0x10080402u, 1u, false));
-#pragma unroll
-                    for (int r = 0; r < 4; ++r) big[r] = mad24(ls, C[r], big[r]);
-                }
-                {
-                    const uint4 g = *reinterpret_cast<const uint4*>(lds + perm(wu[0], lo_g, sel));
-                    const uint2 m = *reinterpret_cast<const uint2*>(lds + perm(wu[1], lo_s, sel));
-                    const v4i C = mfma(A, pack64(bfi(m.x, g.z, g.x), bfi(m.y, g.w, g.y)), v4i{0, 0, 0, 0});
-                    const int ls = int(__builtin_amdgcn_udot4((wu[1] >> 7) & 0x01010101u, 0x10080402u, 1u, false));
-#pragma unroll
-                    for (int r = 0; r < 4; ++r) biu[r] = mad24(ls, C[r], biu[r]);
-                }
+                A[c] = pack64(av[0], av[1]);
             }
+            Look L[8];
+#pragma unroll
+            for (int c = 0; c < 8; ++c) L[c] = look(o.g, c);
+#pragma unroll
+            for (int c = 0; c < 8; ++c) {
+                use(L[c], o.g, c, A[c], big);
+                L[c] = look(o.u, c);
+            }
+#pragma unroll
+            for (int c = 0; c < 8; ++c) use(L[c], o.u, c, A[c], biu);
             const float dgf = h2f(o.dg), duf = h2f(o.du);
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
@@ -321,18 +333,22 @@ __global__ __launch_bounds__(NW * 64, 1) void gu_kernel(GroupArgs a) {
             load(s1, min(b + 1, nb - 1));
             sink(sunk, t0);
             t0 = touch(min(b + 5, nb - 1));
+            __builtin_amdgcn_sched_barrier(0);   // the loads stay ahead of the compute
             compute(s0);
             load(s0, min(b + 2, nb - 1));
             sink(sunk, t1);
             t1 = touch(min(b + 6, nb - 1));
+            __builtin_amdgcn_sched_barrier(0);
             if (b + 1 < nb) compute(s1);
             load(s1, min(b + 3, nb - 1));
             sink(sunk, t2);
             t2 = touch(min(b + 7, nb - 1));
+            __builtin_amdgcn_sched_barrier(0);
             if (b + 2 < nb) compute(s0);
             load(s0, min(b + 4, nb - 1));
             sink(sunk, t3);
             t3 = touch(min(b + 8, nb - 1));
+            __builtin_amdgcn_sched_barrier(0);
             if (b + 3 < nb) compute(s1);
         }
         sink(sunk, t0 ^ t1 ^ t2 ^ t3);
@@ -397,14 +413,20 @@ __global__ __launch_bounds__(NW * 64, 1) void dn_kernel(GroupArgs a) {
         float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
         auto compute = [&](const DnOps& o) {
             int bi[4] = {0, 0, 0, 0};
+            uint32_t code[8];
+            uint4 g[8];
+            uint2 m[8];
+#pragma unroll
+            for (int c = 0; c < 8; ++c) {   // all eight lookups in flight before the first use
+                const uint32_t* w = reinterpret_cast<const uint32_t*>(o.q) + 2 * c;
+                code[c] = perm(w[1], w[0], selc);
+                g[c] = *reinterpret_cast<const uint4*>(lds + ((code[c] & 0xff80u) | lo_x));
+                m[c] = *reinterpret_cast<const uint2*>(lds + perm(code[c], lo_s, sel0));
+            }
 #pragma unroll
             for (int c = 0; c < 8; ++c) {
-                const uint32_t* w = reinterpret_cast<const uint32_t*>(o.q) + 2 * c;
                 const uint32_t* av = reinterpret_cast<const uint32_t*>(o.a) + 4 * c;
-                const uint32_t code = perm(w[1], w[0], selc);
-                const uint4 g = *reinterpret_cast<const uint4*>(lds + ((code & 0xff80u) | lo_x));
-                const uint2 m = *reinterpret_cast<const uint2*>(lds + perm(code, lo_s, sel0));
-                const long B = pack64(bfi(m.x, g.z, g.x), bfi(m.y, g.w, g.y));
+                const long B = pack64(bfi(m[c].x, g[c].z, g[c].x), bfi(m[c].y, g[c].w, g[c].y));
                 const v4i C1 = mfma(pack64(av[0], av[1]), B, v4i{0, 0, 0, 0});
                 const v4i C2 = mfma(pack64(av[2], av[3]), B, v4i{0, 0, 0, 0});
                 const uint32_t sb = ((c < 4 ? o.s.x : o.s.y) >> (8 * (c & 3))) & 0xffu;
@@ -424,18 +446,22 @@ __global__ __launch_bounds__(NW * 64, 1) void dn_kernel(GroupArgs a) {
             load(s1, min(b + 1, nb - 1));
             sink(sunk, t0);
             t0 = touch(min(b + 5, nb - 1));
+            __builtin_amdgcn_sched_barrier(0);   // the loads stay ahead of the compute
             compute(s0);
             load(s0, min(b + 2, nb - 1));
             sink(sunk, t1);
             t1 = touch(min(b + 6, nb - 1));
+            __builtin_amdgcn_sched_barrier(0);
             if (b + 1 < nb) compute(s1);
             load(s1, min(b + 3, nb - 1));
             sink(sunk, t2);
             t2 = touch(min(b + 7, nb - 1));
+            __builtin_amdgcn_sched_barrier(0);
             if (b + 2 < nb) compute(s0);
             load(s0, min(b + 4, nb - 1));
             sink(sunk, t3);
             t3 = touch(min(b + 8, nb - 1));
+            __builtin_amdgcn_sched_barrier(0);
             if (b + 3 < nb) compute(s1);
         }
         sink(sunk, t0 ^ t1 ^ t2 ^ t3);

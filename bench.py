@@ -163,6 +163,9 @@ def main():
     ap.add_argument("--warmup", type=int, default=-1)
     ap.add_argument("--config", type=int, default=1, choices=(0, 1, 2, 3, 4))
     ap.add_argument("--tokens", type=int, default=512, help="config 4: tokens per grouped call")
+    ap.add_argument("--device-route", action="store_true",
+                    help="configs 1, 4: route each step on the GPU from N(0,1) logits (route.cpp router: "
+                         "sqrt-softplus scores, top-6, normalized weights) inside the timed region")
     ap.add_argument("--routes", type=int, default=512)
     ap.add_argument("--cpu-layers", type=int, default=0)
     ap.add_argument("--cpu-threads", type=int, default=0)
@@ -215,6 +218,13 @@ def main():
         ids, w, x = routes(n_r, SEED)
         ids, w = ids[:, None, :], w[:, None, :]
     k = ids.shape[2]
+    droute = args.device_route and cfg in (1, 4)
+    if droute:   # fresh N(0,1) logits per route; the ids / weights come from the device router
+        lrng = np.random.default_rng(SEED + 7)
+        logits = lrng.standard_normal((n_r, TOK if cfg == 4 else 1, E)).astype(np.float32)
+        from oracle.oracle import Oracle   # checker only: the expected picks for the byte count
+        orc_ids = np.stack([Oracle().route(logits[r], K)[0] for r in range(n_r)])
+        ids = orc_ids if cfg == 4 else orc_ids.reshape(n_r, 1, K)
     # algorithmic bytes per step, averaged over the routes the timed steps use
     used = [(warmup + i) % n_r for i in range(steps)]
     if cfg == 4:   # every touched expert once, plus the tokens in and out
@@ -235,10 +245,17 @@ def main():
         d_x = torch.from_numpy(x).cuda()
         d_h = torch.zeros((L + 1, DIM), dtype=torch.float32, device="cuda")   # config 3: the carried hidden
         d_out = torch.zeros((n_r, TOK, DIM) if cfg == 4 else (n_r, DIM), dtype=torch.float32, device="cuda")
+        d_logits = torch.from_numpy(logits).cuda() if droute else None
     torch.cuda.synchronize()
 
     def step(i):
         r = i % n_r
+        if droute and cfg == 4:
+            lane.grouped_forward_routed_async(0, d_logits[r], K, d_x[r], d_out[r], stream=sp)
+            return
+        if droute:
+            lane.layer_forward_routed_async(0, d_logits[r, 0], K, d_x[r], d_out[r], stream=sp)
+            return
         if cfg == 4:
             lane.grouped_forward_async(0, d_ids[r], d_w[r], d_x[r], d_out[r], stream=sp)
             return
@@ -309,7 +326,8 @@ def main():
         "hbm_frac": round(gbs / HBM_PEAK_GBS, 4),
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "int8",
         "data": "synthetic (seeded IQ blocks generated on device, N(0,1) activations and router logits)",
-        "config": {"workload": workloads[cfg], "layers_per_step": L, "tokens_per_step": TOK,
+        "config": {"workload": workloads[cfg] + ("; routed on the GPU each step (route.cpp router)" if droute else ""),
+                   "layers_per_step": L, "tokens_per_step": TOK,
                    "bytes_per_step": int(round(bytes_per_step)), "routes": n_r},
         "roofline": {"bound": "hbm", "kernel": kernel,
                      "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",

@@ -755,6 +755,59 @@ int32_t xl_grouped_forward_async(xl_context* ctx, int32_t layer, int32_t T, int3
     });
 }
 
+int32_t xl_route_async(xl_context* ctx, const float* d_logits, int32_t T, int32_t stride, const float* d_bias_or_null,
+                       int32_t n, int32_t k, float scale, int32_t* d_ids, float* d_w, void* stream, xl_error* err) {
+    return guarded(ctx, err, [&] {
+        ready(ctx, false);
+        need(d_logits && d_ids && d_w, XL_E_ARG, "null device pointer");
+        need(T >= 1, XL_E_ARG, "token count below 1");
+        need(n >= 1 && n <= xl::kRouteMaxExperts, XL_E_ARG, "expert count outside 1..4096");
+        need(k >= 1 && k <= 16 && k <= n, XL_E_ARG, "pick count outside 1..min(16, n)");
+        need(stride >= n, XL_E_ARG, "logit stride below the expert count");
+        need(std::isfinite(scale) && scale >= 0.0f, XL_E_ARG, "route scale must be finite and >= 0");
+        hip_check(xl::dev::launch_route(d_logits, T, stride, d_bias_or_null, n, k, scale, d_ids, d_w, ctx->err_flag,
+                                        pick_stream(ctx, stream)),
+                  "route launch");
+    });
+}
+
+int32_t xl_layer_forward_routed_async(xl_context* ctx, int32_t layer, const float* d_logits, const float* d_bias_or_null,
+                                      int32_t k, float scale, const float* d_x, const float* d_shared_or_null,
+                                      float* d_out, void* stream, xl_error* err) {
+    return guarded(ctx, err, [&] {
+        ready(ctx, true);
+        check_layer(ctx, layer);
+        need(k >= 1 && k <= ctx->cfg.max_picks, XL_E_ARG, "pick count outside 1..max_picks");
+        need(ctx->cfg.n_experts <= xl::kRouteMaxExperts, XL_E_ARG, "router: more than 4096 experts");
+        need(std::isfinite(scale) && scale >= 0.0f, XL_E_ARG, "route scale must be finite and >= 0");
+        need(d_logits && d_x && d_out, XL_E_ARG, "null device pointer");
+        hipStream_t s = pick_stream(ctx, stream);
+        const int n = ctx->cfg.n_experts;
+        hip_check(xl::dev::launch_route(d_logits, 1, n, d_bias_or_null, n, k, scale, ctx->ids, ctx->w, ctx->err_flag, s),
+                  "route launch");
+        enqueue_layer(ctx, layer, ctx->ids, ctx->w, k, d_x, d_shared_or_null, d_out, s);
+    });
+}
+
+int32_t xl_grouped_forward_routed_async(xl_context* ctx, int32_t layer, int32_t T, const float* d_logits,
+                                        const float* d_bias_or_null, int32_t k, float scale, const float* d_x,
+                                        const float* d_shared_or_null, float* d_out, void* stream, xl_error* err) {
+    return guarded(ctx, err, [&] {
+        ready(ctx, true);
+        check_layer(ctx, layer);
+        check_grouped(ctx, T, k);
+        need(ctx->cfg.n_experts <= xl::kRouteMaxExperts, XL_E_ARG, "router: more than 4096 experts");
+        need(std::isfinite(scale) && scale >= 0.0f, XL_E_ARG, "route scale must be finite and >= 0");
+        need(d_logits && d_x && d_out, XL_E_ARG, "null device pointer");
+        hipStream_t s = pick_stream(ctx, stream);
+        const int n = ctx->cfg.n_experts;
+        auto& g = ctx->grp;
+        hip_check(xl::dev::launch_route(d_logits, T, n, d_bias_or_null, n, k, scale, g.ids, g.w, ctx->err_flag, s),
+                  "route launch");
+        enqueue_grouped(ctx, layer, T, k, g.ids, g.w, d_x, d_shared_or_null, d_out, s);
+    });
+}
+
 int32_t xl_layer_forward(xl_context* ctx, int32_t layer, const int32_t* ids, const float* w, int32_t k, const float* x,
                          const float* shared_or_null, float* out, xl_error* err) {
     return guarded(ctx, err, [&] {

@@ -111,7 +111,8 @@ struct GroupArgs {
     const uint64_t* tables;     // expanded codebooks (kLayer3TableBytes)
     int* err;
 };
-constexpr int kGroupMaxExperts = 8192;   // experts per layer the bucket kernel counts in LDS
+constexpr int kGroupMaxExperts = 8192;
+constexpr int kRouteMaxExperts = 4096;   // router: scores and keys of one token in LDS   // experts per layer the bucket kernel counts in LDS
 // Tasks the bucket kernel can write for P pairs: one per started tile of 16 pairs of an expert.
 inline int64_t group_max_tasks(int64_t P, int64_t n_experts) { return P / 16 + (P < n_experts ? P : n_experts) + 1; }
 constexpr int kLayer3TableBytes = 24576;   // expanded codebooks of the single-launch kernel
@@ -147,6 +148,9 @@ hipError_t launch_down(const ExpertDesc* descs, const int32_t* ids, int k, int n
 // launch's matrices; sizes the LDS codebook region.
 int type_bit(int type);
 // Fixed-order combine: ascending id, out = fma(w, y, out), then + shared.
+// Router (route.cpp:15-37) of T tokens of n <= kRouteMaxExperts logits.
+hipError_t launch_route(const float* logits, int T, int stride, const float* bias, int n, int k, float scale,
+                        int32_t* ids, float* w, int* err, hipStream_t s);
 hipError_t launch_combine(const int32_t* ids, const float* w, int k, const float* y, int dim, const float* shared,
                           float* out, hipStream_t s);
 // Seeded generation of one planar matrix (role 0 gate, 1 up, 2 down).

@@ -76,6 +76,9 @@ _SIGNATURES = {
     "xl_sync": (_I32, [_P, _P, _ErrP]),
     "xl_grouped_forward": (_I32, [_P, _I32, _I32, _I32, _i32p, _f32p, _f32p, _P, _f32p, _ErrP]),
     "xl_grouped_forward_async": (_I32, [_P, _I32, _I32, _I32, _P, _P, _P, _P, _P, _P, _ErrP]),
+    "xl_route_async": (_I32, [_P, _P, _I32, _I32, _P, _I32, _I32, C.c_float, _P, _P, _P, _ErrP]),
+    "xl_layer_forward_routed_async": (_I32, [_P, _I32, _P, _P, _I32, C.c_float, _P, _P, _P, _P, _ErrP]),
+    "xl_grouped_forward_routed_async": (_I32, [_P, _I32, _I32, _P, _P, _I32, C.c_float, _P, _P, _P, _P, _ErrP]),
     "xl_quantize_q8k_async": (_I32, [_P, _P, _I32, _I32, _P, _P, _ErrP]),
     "xl_matvec_async": (_I32, [_P, _I32, _P, _I32, _I32, _P, _P, _P, _P, _ErrP]),
     "xl_profile_begin": (_I32, [_P, _I32, _ErrP]),
@@ -279,6 +282,22 @@ class Lane:
         T, k = int(ids.shape[0]), int(ids.shape[1])
         self._call("xl_grouped_forward_async", layer, T, k, _ptr(ids), _ptr(w), _ptr(x), _ptr(shared), _ptr(out),
                    None if stream is None else int(stream))
+
+    def route_async(self, logits, k: int, ids, w, scale: float = 1.0, bias=None, stream=None) -> None:
+        """logits: [T, n] device tensor; ids (int32), w: [T, k] device tensors."""
+        T, n = int(logits.shape[0]), int(logits.shape[1])
+        self._call("xl_route_async", _ptr(logits), T, int(logits.stride(0)), _ptr(bias), n, k, float(scale), _ptr(ids),
+                   _ptr(w), None if stream is None else int(stream))
+
+    def layer_forward_routed_async(self, layer: int, logits, k: int, x, out, scale: float = 1.0, bias=None,
+                                   shared=None, stream=None) -> None:
+        self._call("xl_layer_forward_routed_async", layer, _ptr(logits), _ptr(bias), k, float(scale), _ptr(x),
+                   _ptr(shared), _ptr(out), None if stream is None else int(stream))
+
+    def grouped_forward_routed_async(self, layer: int, logits, k: int, x, out, scale: float = 1.0, bias=None,
+                                     shared=None, stream=None) -> None:
+        self._call("xl_grouped_forward_routed_async", layer, int(logits.shape[0]), _ptr(logits), _ptr(bias), k,
+                   float(scale), _ptr(x), _ptr(shared), _ptr(out), None if stream is None else int(stream))
 
     def sync(self, stream=None) -> None:
         self._call("xl_sync", None if stream is None else int(stream))

@@ -136,6 +136,26 @@ int32_t xl_grouped_forward_async(xl_context* ctx, int32_t layer, int32_t T, int3
                                  const float* d_w, const float* d_x, const float* d_shared_or_null, float* d_out,
                                  void* stream, xl_error* err);
 
+/* ---- router (device pointers) -----------------------------------------------
+ * route.cpp:15-37 (route_cpu) on the device, per token: score =
+ * sqrt(softplus(logit)) (the logit itself above 20), key = score + bias (a null
+ * bias is zeros); k rounds of the first largest key (ties: lower index), each
+ * taking the expert out; weight = score / (sum of the picked scores + 1e-20) *
+ * scale. logits T x stride (n used, n <= 4096), ids and w T x k (k <= 16).
+ * A non-finite logit or key sets the device flag (the reference throws). */
+int32_t xl_route_async(xl_context* ctx, const float* d_logits, int32_t T, int32_t stride, const float* d_bias_or_null,
+                       int32_t n, int32_t k, float scale, int32_t* d_ids, float* d_w, void* stream, xl_error* err);
+/* The router over the layer's n_experts logits, then the layer call on its ids
+ * and weights, both on `stream` (no host round trip; the route result lives in
+ * the context's workspace, so routed calls on one context are stream-ordered). */
+int32_t xl_layer_forward_routed_async(xl_context* ctx, int32_t layer, const float* d_logits, const float* d_bias_or_null,
+                                      int32_t k, float scale, const float* d_x, const float* d_shared_or_null,
+                                      float* d_out, void* stream, xl_error* err);
+/* The same for T tokens (logits T x n_experts) into xl_grouped_forward_async. */
+int32_t xl_grouped_forward_routed_async(xl_context* ctx, int32_t layer, int32_t T, const float* d_logits,
+                                        const float* d_bias_or_null, int32_t k, float scale, const float* d_x,
+                                        const float* d_shared_or_null, float* d_out, void* stream, xl_error* err);
+
 /* ---- primitives (device pointers) -----------------------------------------
  * q8k_* : Q8_K quantization of rows x k floats (k a multiple of 256) into
  * rows*k/256 blocks of 292 bytes (q8k_core.hpp:13-38, hip_q8k.hpp:9). */

@@ -54,6 +54,7 @@ class Oracle:
         L.orc_expert.argtypes = [_i32p, _u8p, _u8p, _u8p, C.c_int, C.c_int, _f32p, _f32p, _P, _P, _P, C.c_int]
         L.orc_down_from_hidden.argtypes = [C.c_int, _u8p, C.c_int, C.c_int, _f32p, _f32p, C.c_int]
         L.orc_combine.argtypes = [_i32p, _f32p, C.c_int, _f32p, C.c_int, _P, _f32p]
+        L.orc_route.argtypes = [_f32p, C.c_int, _P, C.c_int, C.c_int, C.c_int, C.c_float, _i32p, _f32p]
         L.orc_gen_key.argtypes = [C.c_uint64, C.c_uint32, C.c_uint32, C.c_uint32]
         L.orc_gen_key.restype = C.c_uint64
         L.orc_gen_block.argtypes = [C.c_int, C.c_uint64, C.c_uint64, _u8p]
@@ -121,6 +122,16 @@ class Oracle:
         self.lib.orc_combine(ids, w, k, rows.reshape(-1), dim, None if sh is None else sh.ctypes.data, out)
         return out
 
+    def route(self, logits, k, scale=1.0, bias=None):
+        """route.cpp:15-37 for logits [T, n] (or [n]): ids, weights [T, k]."""
+        lg = np.ascontiguousarray(np.atleast_2d(logits), dtype=np.float32)
+        T, n = lg.shape
+        b = None if bias is None else np.ascontiguousarray(bias, dtype=np.float32)
+        ids = np.zeros((T, k), np.int32); w = np.zeros((T, k), np.float32)
+        self.lib.orc_route(lg.reshape(-1), n, None if b is None else b.ctypes.data, n, T, k, scale, ids.reshape(-1),
+                           w.reshape(-1))
+        return ids, w
+
     # -- generator -------------------------------------------------------
     def gen_key(self, seed, layer, expert, role) -> int:
         return int(self.lib.orc_gen_key(seed, layer, expert, role))
@@ -170,6 +181,7 @@ class Reference:
         L.ref_decode.argtypes = [C.c_int, _u8p, C.c_int, _i32p, _i32p, C.POINTER(C.c_float)]
         L.ref_matvec.argtypes = [C.c_int, _u8p, C.c_int, C.c_int, _P, _f32p, C.c_int]
         L.ref_combine.argtypes = [_i32p, _f32p, C.c_int, _f32p, C.c_int, _f32p, _f32p]
+        L.ref_route.argtypes = [_f32p, C.c_int, _f32p, C.c_int, C.c_int, C.c_int, C.c_float, _i32p, _f32p]
         L.ref_expert.argtypes = [_i32p, _u8p, _u8p, _u8p, C.c_int, C.c_int, _f32p, _f32p, C.c_int]
 
     @staticmethod
@@ -214,6 +226,14 @@ class Reference:
         self.lib.ref_expert(np.asarray(types, dtype=np.int32), gate.reshape(-1), up.reshape(-1), down.reshape(-1),
                             dim, ff, np.ascontiguousarray(x, dtype=np.float32), y, threads)
         return y
+
+    def route(self, logits, k, scale=1.0, bias=None):
+        lg = np.ascontiguousarray(np.atleast_2d(logits), dtype=np.float32)
+        T, n = lg.shape
+        b = np.zeros(n, np.float32) if bias is None else np.ascontiguousarray(bias, dtype=np.float32)
+        ids = np.zeros((T, k), np.int32); w = np.zeros((T, k), np.float32)
+        self.lib.ref_route(lg.reshape(-1), n, b, n, T, k, scale, ids.reshape(-1), w.reshape(-1))
+        return ids, w
 
     def combine(self, ids, w, rows, shared):
         rows = np.ascontiguousarray(rows, dtype=np.float32)

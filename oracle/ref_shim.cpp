@@ -7,6 +7,7 @@
 //   sycl/stage/wiring/q8k_core.hpp (+ q8k_tables.inc): Q8_K quant and IQ dots
 //   sycl/moe/core.hpp (+ format.hpp, tables.hpp):     per-32 decoder
 //   warm/other_combine.hpp:                             fixed-order combine
+//   sycl/route/route.hpp, route.cpp (compiled alongside): route_cpu
 #include <array>
 #include <atomic>
 #include <cstring>
@@ -17,6 +18,7 @@
 #include "q8k_core.hpp"
 #include "core.hpp"
 #include "other_combine.hpp"
+#include "route.hpp"
 
 namespace q = strata::wiring::q8k;
 namespace m = strata::ds4::moe;
@@ -66,6 +68,12 @@ void ref_expert(const int* types, const uint8_t* gate, const uint8_t* up, const 
     for (int i = 0; i < ff; ++i) h[size_t(i)] = q::swiglu(g[size_t(i)], u[size_t(i)], 0.0f);
     for (int b = 0; b < ff / 256; ++b) q::quant_block(h.data() + 256 * b, hq[size_t(b)]);
     ref_matvec(types[2], down, dim, ff, hq.data(), y, threads);
+}
+void ref_route(const float* logits, int stride, const float* bias, int n, int T, int k, float scale, int* ids, float* w) {
+    const auto r = strata::ds4::route_port::route_cpu(std::span<const float>(logits, size_t(T) * size_t(stride)),
+                                                      size_t(stride), std::span<const float>(bias, size_t(n)),
+                                                      size_t(T), size_t(k), scale);
+    for (size_t i = 0; i < r.ids.size(); ++i) { ids[i] = r.ids[i]; w[i] = r.weights[i]; }
 }
 void ref_combine(const int* ids, const float* w, int k, const float* rows, int dim, const float* shared, float* out) {
     std::array<std::vector<std::pair<size_t, std::vector<float>>>, 1> results;

@@ -5,7 +5,9 @@
  * Citations are to the reference tree (engine/strata/...). */
 #include "xl_oracle.h"
 
+#include <float.h>
 #include <math.h>
+#include <stdlib.h>
 #include <pthread.h>
 #include <stdatomic.h>
 #include <string.h>
@@ -308,6 +310,43 @@ void orc_combine(const int32_t* ids, const float* w, int k, const float* rows, i
     }
     if (shared)
         for (int c = 0; c < dim; ++c) out[c] += shared[c];
+}
+
+/* ---- router: route.cpp:15-37 ---------------------------------------------
+ * Per token: softplus(l) (l itself above 20), its square root as the score,
+ * the score plus the expert's bias as the selection key; k rounds of "first
+ * largest key" (strict >), each taking the expert out; the scores of the picks
+ * summed in pick order; weight = score / (sum + 1e-20) * scale. Every step in
+ * single precision with separate roundings (this file is built without FMA
+ * contraction). */
+void orc_route(const float* logits, int stride, const float* bias, int n, int T, int k, float scale, int32_t* ids,
+               float* w) {
+    float* sc = (float*)malloc(sizeof(float) * (size_t)n);
+    float* key = (float*)malloc(sizeof(float) * (size_t)n);
+    for (int t = 0; t < T; ++t) {
+        const float* lg = logits + (size_t)t * stride;
+        for (int e = 0; e < n; ++e) {
+            const float l = lg[e];
+            const float sp = l > 20.0f ? l : log1pf(expf(l));
+            sc[e] = sqrtf(sp);
+            key[e] = sc[e] + (bias ? bias[e] : 0.0f);
+        }
+        float sum = 0.0f;
+        for (int i = 0; i < k; ++i) {
+            int best = 0;
+            for (int e = 1; e < n; ++e)
+                if (key[e] > key[best]) best = e;
+            ids[(size_t)t * k + i] = best;
+            sum += sc[best];
+            key[best] = -FLT_MAX;
+        }
+        for (int i = 0; i < k; ++i) {
+            const float q = sc[ids[(size_t)t * k + i]] / (sum + 1e-20f);
+            w[(size_t)t * k + i] = q * scale;
+        }
+    }
+    free(sc);
+    free(key);
 }
 
 /* ---- generator (this build's spec; restated independently) ------------- */

@@ -12,11 +12,13 @@
  *                                           hsum, dot, swiglu
  *   sycl/moe/core.hpp:67,78-105              per-32 decode (brute-force check)
  *   warm/runtime.cpp:183-188                 fixed-order combine
+ *   sycl/route/route.cpp:15-37               router: sqrt(softplus) scores,
+ *                                           biased top-k, normalized weights
  *   sycl/moe/cpu_lane.cpp:70-81              64-row jobs over worker threads
  *
  * Parity pins (see tests/): every function here is checked against
  * oracle/_ref (the reference's own q8k_core.hpp / core.hpp / other_combine.hpp
- * compiled from /root/reference) where that builds, against closed forms
+ * and route.cpp compiled from /root/reference) where that builds, against closed forms
  * (zero and one-hot Q8_K blocks, round-half-even ties, ksigns parity) and
  * against a brute-force dequantize-and-multiply integer dot.
  */
@@ -65,6 +67,11 @@ void orc_combine(const int32_t* ids, const float* w, int k, const float* rows, i
 
 /* Generator restated: one AoS block, and one whole matrix (n x k). */
 uint64_t orc_gen_key(uint64_t seed, uint32_t layer, uint32_t expert, uint32_t role);
+/* Router of route.cpp:15-37 (route_cpu) for T tokens: logits T x stride (the
+ * first n used), bias n (NULL = zeros); ids / w: T x k. */
+void orc_route(const float* logits, int stride, const float* bias, int n, int T, int k, float scale, int32_t* ids,
+               float* w);
+
 void orc_gen_block(int type, uint64_t key, uint64_t blk, uint8_t* out);
 void orc_gen_matrix(int type, uint64_t seed, uint32_t layer, uint32_t expert, uint32_t role, int n, int k, uint8_t* out);
 

@@ -88,6 +88,23 @@ def main():
     for i, (ids, w, rows, shared, y) in enumerate(cases):
         out[f"comb{i}_ids"], out[f"comb{i}_w"], out[f"comb{i}_rows"] = ids, w, rows
         out[f"comb{i}_shared"], out[f"comb{i}_out"] = shared, y
+    # Router (route.cpp:15-37): N(0,1) logits, the softplus cut at 20, very
+    # negative logits, bias on and off, equal keys (first index wins), k = n.
+    rcases = []
+    lg = rng.standard_normal((16, 384)).astype(np.float32)
+    rcases.append((lg, np.zeros(384, np.float32), 6, 1.0))
+    lg = (rng.standard_normal((8, 384)) * 15).astype(np.float32)
+    lg[:, :8] = np.array([19.99, 20.0, 20.01, 25.0, -90.0, -200.0, 0.0, -0.0], np.float32)
+    rcases.append((lg, (rng.standard_normal(384) * 0.2).astype(np.float32), 8, 2.5))
+    lg = np.tile(np.array([1.0, 3.0, 3.0, 2.0, 3.0, -1.0], np.float32), (2, 1))
+    rcases.append((lg, np.array([0.0, 0.0, 0.0, 0.0, 0.0, 5.0], np.float32), 3, 1.0))
+    lg = rng.standard_normal((4, 16)).astype(np.float32)
+    rcases.append((lg, np.zeros(16, np.float32), 16, 0.5))
+    for i, (lg, b, k, scale) in enumerate(rcases):
+        ids, w = ref.route(lg, k, scale, b)
+        out[f"route{i}_logits"], out[f"route{i}_bias"] = lg, b
+        out[f"route{i}_k_scale"] = np.array([k, scale], np.float32)
+        out[f"route{i}_ids"], out[f"route{i}_w"] = ids, w
     np.savez_compressed(OUT, **out)
     print("wrote", OUT, sum(v.nbytes for v in out.values()), "bytes")
 

@@ -210,3 +210,43 @@ def test_codebook_self_consistency(orc):
     ks = orc.ksigns()
     for i in range(128):
         assert ks[i] & 0x7F == i and bin(int(ks[i])).count("1") % 2 == 0
+
+
+# ---- router (route.cpp:15-37) ------------------------------------------------
+def test_route_golden(orc):
+    for i in range(4):
+        lg, b = GOLD[f"route{i}_logits"], GOLD[f"route{i}_bias"]
+        k, scale = GOLD[f"route{i}_k_scale"]
+        ids, w = orc.route(lg, int(k), float(scale), b)
+        assert np.array_equal(ids, GOLD[f"route{i}_ids"]), i
+        assert np.array_equal(w.view(np.uint32), GOLD[f"route{i}_w"].view(np.uint32)), i
+
+
+def test_route_vs_reference_random(orc, ref, rng):
+    for T, n, k, s in ((32, 384, 6, 1.0), (8, 4096, 8, 2.5), (3, 7, 7, 0.0)):
+        lg = (rng.standard_normal((T, n)) * rng.choice([0.5, 4.0, 40.0])).astype(np.float32)
+        b = (rng.standard_normal(n) * 0.3).astype(np.float32)
+        a, c = orc.route(lg, k, s, b), ref.route(lg, k, s, b)
+        assert np.array_equal(a[0], c[0])
+        assert np.array_equal(a[1].view(np.uint32), c[1].view(np.uint32))
+
+
+def test_route_independent_forms(orc, rng):
+    # With no bias the key sqrt(softplus(l)) is increasing in l: the picks are
+    # the stable descending order of the logits. The weights against a float64
+    # restatement of score / sum(scores) * scale.
+    lg = rng.standard_normal((40, 384)).astype(np.float32)
+    ids, w = orc.route(lg, 6, 1.75)
+    for t in range(40):
+        assert np.array_equal(ids[t], np.argsort(-lg[t], kind="stable")[:6])
+        sc = np.sqrt(np.log1p(np.exp(lg[t, ids[t]].astype(np.float64))))
+        np.testing.assert_allclose(w[t], sc / sc.sum() * 1.75, rtol=2e-6)
+    # equal keys: the first index wins; k = n picks every expert once
+    ids, _ = orc.route(np.array([[2.0, 5.0, 5.0, 5.0]], np.float32), 2)
+    assert ids.tolist() == [[1, 2]]
+    ids, w = orc.route(rng.standard_normal((3, 9)).astype(np.float32), 9, 1.0)
+    assert all(sorted(r) == list(range(9)) for r in ids.tolist())
+    np.testing.assert_allclose(w.sum(axis=1), 1.0, rtol=1e-6)
+    # above 20 the score is sqrt(l) itself
+    ids, w = orc.route(np.array([[30.0, 25.0]], np.float32), 2)
+    np.testing.assert_allclose(w[0], np.sqrt([30.0, 25.0]) / np.sqrt([30.0, 25.0]).sum(), rtol=1e-6)

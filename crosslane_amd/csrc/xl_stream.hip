@@ -665,8 +665,11 @@ hipError_t launch_stream(const Layer3Args& args, int cus, hipStream_t s) {
     if (!row_shape(args.dim, lg, pg) || !row_shape(args.ff, ld, pd)) return hipErrorNotSupported;
     const int RD = 64 / ld;
     const int grid = std::min(cus, args.dim / RD);
-    if (lg == 64 && pg == 1 && ld == 16 && pd == 3)   // 4096 x 3072
+    if (lg == 64 && pg == 1 && ld == 16 && pd == 3) {   // 4096 x 3072: slots and steps sized by the pick count
+        if (args.k <= 2) return launch_stream_t<8, 64, 1, 16, 3, 3, 1, 3, 1, 3>(args, grid, s);
+        if (args.k <= 4) return launch_stream_t<8, 64, 1, 16, 3, 6, 2, 3, 2, 3>(args, grid, s);
         return launch_stream_t<8, 64, 1, 16, 3, 9, 3, 3, 3, 3>(args, grid, s);
+    }
     if (lg == 16 && pg == 1 && ld == 8 && pd == 1)    // 1024 x 512
         return launch_stream_t<8, 16, 1, 8, 1, 6, 2, 3, 1, 2>(args, grid, s);
     if (lg == 4 && pg == 1 && ld == 4 && pd == 3)     // 256 x 768

@@ -295,7 +295,8 @@ def test_layer_paths_agree(orc, dim, ff, sig, monkeypatch):
             lane.close()
 
 
-@pytest.mark.parametrize("dim,ff,k", [(4096, 3072, 6), (4096, 3072, 4), (4096, 3072, 1), (1024, 512, 8),
+@pytest.mark.parametrize("dim,ff,k", [(4096, 3072, 6), (4096, 3072, 5), (4096, 3072, 4), (4096, 3072, 3),
+                                      (4096, 3072, 2), (4096, 3072, 1), (1024, 512, 8),
                                       (1024, 512, 12), (1024, 512, 16), (256, 768, 6), (256, 768, 12)])
 def test_streaming_kernel_pick_counts(orc, dim, ff, k, monkeypatch):
     # XL_LAYER_PATH=4 runs the streaming kernel or fails: pick counts that give

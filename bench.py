@@ -18,9 +18,10 @@ steps touch different experts (the bank is ~3.9 GB, far beyond the 256 MB MALL).
      of its pairs, int8 MFMA);
   3  a 40-layer pass per step: 40 x 384 experts whose whole-expert type is
      drawn 17 % IQ2_XS / 19 % IQ2_XXS / 64 % IQ1_M, top-6 per layer, the
-     hidden carried layer to layer through an RMS normalization (torch ops on
-     the same stream, inside the timed region: the model's RMSNorm stand-in,
-     without which the quadratic SwiGLU overflows f32 within a few layers).
+     hidden carried layer to layer through an RMS normalization (torch's
+     rms_norm on the same stream, inside the timed region: the model's RMSNorm
+     stand-in, without which the quadratic SwiGLU overflows f32 within a few
+     layers).
 
 Prints one JSON line: value = achieved algorithmic HBM GB/s (selected experts'
 weight bytes + x in + out per layer), plus us_per_layer; the roofline of the
@@ -182,6 +183,7 @@ def main():
     warmup = args.warmup if args.warmup >= 0 else {3: 5, 4: 5}.get(cfg, 100)
 
     import torch
+    import torch.nn.functional as F
     import crosslane_amd as xl
 
     # ---- bank and routes
@@ -244,6 +246,7 @@ def main():
         d_w = torch.from_numpy(w).cuda()
         d_x = torch.from_numpy(x).cuda()
         d_h = torch.zeros((L + 1, DIM), dtype=torch.float32, device="cuda")   # config 3: the carried hidden
+        d_y = torch.zeros(DIM, dtype=torch.float32, device="cuda")             # config 3: a layer's raw output
         d_out = torch.zeros((n_r, TOK, DIM) if cfg == 4 else (n_r, DIM), dtype=torch.float32, device="cuda")
         d_logits = torch.from_numpy(logits).cuda() if droute else None
     torch.cuda.synchronize()
@@ -265,9 +268,8 @@ def main():
         with torch.cuda.stream(stream):
             d_h[0].copy_(d_x[r])
             for l in range(L):
-                lane.layer_forward_async(l, d_ids[r, l], d_w[r, l], d_h[l], d_h[l + 1], stream=sp)
-                y = d_h[l + 1]
-                y.mul_(torch.rsqrt(y.square().mean() + 1e-6))   # RMS-normalized hidden for the next layer
+                lane.layer_forward_async(l, d_ids[r, l], d_w[r, l], d_h[l], d_y, stream=sp)
+                d_h[l + 1].copy_(F.rms_norm(d_y, (DIM,), eps=1e-6))   # RMS-normalized hidden for the next layer
 
     for i in range(warmup):
         step(i)

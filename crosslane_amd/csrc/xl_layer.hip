@@ -65,8 +65,9 @@ struct Lay {
     static constexpr int SGN = 0;                                            // 128 rows {M.lo, M.hi, M1.lo, M1.hi}
     static constexpr int XXS = SGN + ((TM & 3) ? 128 * CS * 16 : 0);         // 256 rows of 8 magnitudes
     static constexpr int XS = XXS + ((TM & 1) ? 256 * CXXS * 8 : 0);         // 512 rows of 8 magnitudes
-    static constexpr int IQ1 = XS + ((TM & 2) ? 512 * CXS * 8 : 0);          // 2048 rows of 8 values (one copy)
-    static constexpr int XQ = IQ1 + ((TM & 4) ? 2048 * 8 : 0);               // Q8_K(x) quants (dim <= 4096)
+    static constexpr int C1 = TM == 4 ? 4 : 1;          // IQ1 grid copies (room for them only without the IQ2 tables)
+    static constexpr int IQ1 = XS + ((TM & 2) ? 512 * CXS * 8 : 0);          // 2048 rows of 8 values
+    static constexpr int XQ = IQ1 + ((TM & 4) ? 2048 * 8 * C1 : 0);          // Q8_K(x) quants (dim <= 4096)
     static constexpr int XD = XQ + 4096;                                     // Q8_K(x) scales (16)
     static constexpr int Y = XD + 64;                                        // y staging
     static constexpr int HQ = Y + kYStage * 4;
@@ -89,16 +90,28 @@ __device__ __forceinline__ Lut make_lut(int lane) {
     L.sgn = LY::SGN + uint32_t(lane % LY::CS) * 16;
     L.xxs = LY::XXS + uint32_t(lane % LY::CXXS) * 8;
     L.xs = LY::XS + uint32_t(lane % LY::CXS) * 8;
-    L.iq1 = LY::IQ1;
+    L.iq1 = LY::IQ1 + uint32_t(lane % LY::C1) * 8;
     return L;
 }
 
-// Activations of the pairs a lane owns: 64 Q8_K bytes per pair and the pair's block scale.
+// Activations of the pairs a lane owns: 64 Q8_K bytes per pair, the pair's
+// block scale, and (for IQ1_M rows) the sums of its eight groups of 8 quants,
+// which every row's delta term reuses.
 template <int P>
 struct Act3 {
     uint32_t a[P][16];
     float d[P];
+    int gs[P][8];
 };
+template <int TM, int P>
+__device__ __forceinline__ void group_sums(Act3<P>& A) {
+    if constexpr (TM & 4) {
+#pragma unroll
+        for (int q = 0; q < P; ++q)
+#pragma unroll
+            for (int g = 0; g < 8; ++g) A.gs[q][g] = sdot4(0x01010101u, A.a[q][2 * g + 1], sdot4(0x01010101u, A.a[q][2 * g], 0));
+    }
+}
 
 
 // The pair decoders issue every codebook lookup of the pair before using any:
@@ -154,15 +167,18 @@ __device__ __forceinline__ int pair_xs3(const uint8_t* lds, const Lut& L, const 
     return total;
 }
 // IQ1_M pair as the single integer sum over its 64 weights of (2s+1)*(8*grid + delta)*q;
-// the delta part uses the group sums of the quants.
-__device__ __forceinline__ int pair_iq13(const uint8_t* lds, const Lut& L, const uint32_t* w, uint32_t scw, const uint32_t* a) {
+// the delta part uses the group sums of the quants (gs, computed once per activation load).
+template <int TM>
+__device__ __forceinline__ int pair_iq13(const uint8_t* lds, const Lut& L, const uint32_t* w, uint32_t scw, const uint32_t* a,
+                                         const int* gs) {
+    constexpr int S1 = Lay<TM>::C1 * 8;   // entry stride
     uint2 gr[8];
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
         const int s = e / 4, g = e % 4;
         const uint32_t nib = (w[2] >> (16 * s + 4 * g)) & 15u;
         const uint32_t idx = ((w[s] >> (8 * g)) & 255u) | ((nib & 7u) << 8);
-        gr[e] = *reinterpret_cast<const uint2*>(lds + L.iq1 + (idx << 3));
+        gr[e] = *reinterpret_cast<const uint2*>(lds + L.iq1 + idx * S1);
     }
     int total = 0;
 #pragma unroll
@@ -174,7 +190,7 @@ __device__ __forceinline__ int pair_iq13(const uint8_t* lds, const Lut& L, const
             const uint32_t nib = (w[2] >> (16 * s + 4 * g)) & 15u;
             const uint32_t a0 = a[8 * s + 2 * g], a1 = a[8 * s + 2 * g + 1];
             const int m = sdot4(gr[e].y, a1, sdot4(gr[e].x, a0, 0));
-            const int sg = sdot4(0x01010101u, a1, sdot4(0x01010101u, a0, 0));
+            const int sg = gs[e];
             const int dl = (nib & 8u) ? -sg : sg;
             if (g < 2) { m0 += m; d0 += dl; } else { m1 += m; d1 += dl; }
         }
@@ -189,7 +205,7 @@ __device__ __forceinline__ int pair_iq13(const uint8_t* lds, const Lut& L, const
 // per block are exact, the float order is this kernel's own).
 template <int T, int TM>
 __device__ __forceinline__ float pair_term(const uint8_t* lds, const Lut& L, const Raw3& r, int p, const uint32_t* a,
-                                           float dx, float acc) {
+                                           const int* gs, float dx, float acc) {
     int I;
     uint32_t d16;
     if constexpr (T == kIQ2_XXS) {
@@ -200,7 +216,7 @@ __device__ __forceinline__ float pair_term(const uint8_t* lds, const Lut& L, con
         d16 = r.h[1];
     } else {
         const uint32_t scw = ((p & 2) ? r.w[4] : r.w[3]) >> (16 * (p & 1));
-        I = pair_iq13(lds, L, r.w, scw, a);
+        I = pair_iq13<TM>(lds, L, r.w, scw, a, gs);
         d16 = ((r.w[3] >> 12) & 0xfu) | ((r.w[3] >> 24) & 0xf0u) | ((r.w[4] >> 4) & 0xf00u) | ((r.w[4] >> 16) & 0xf000u);
     }
     return fmaf(__fmul_rn(h2f(d16), dx), float(I), acc);
@@ -217,17 +233,17 @@ __device__ __forceinline__ float row_sum(const uint8_t* lds, const Lut& L, int t
     if constexpr (TM == 1 || TM == 2 || TM == 4) {
         constexpr int T = TM == 1 ? kIQ2_XXS : TM == 2 ? kIQ2_XS : kIQ1_M;
 #pragma unroll
-        for (int j = 0; j < P; ++j) acc = pair_term<T, LT>(lds, L, r[j], l + LPR * j, A.a[j], A.d[j], acc);
+        for (int j = 0; j < P; ++j) acc = pair_term<T, LT>(lds, L, r[j], l + LPR * j, A.a[j], A.gs[j], A.d[j], acc);
     } else {
         if (has_type<kIQ2_XXS, TM>() && type == kIQ2_XXS) {
 #pragma unroll
-            for (int j = 0; j < P; ++j) acc = pair_term<kIQ2_XXS, LT>(lds, L, r[j], l + LPR * j, A.a[j], A.d[j], acc);
+            for (int j = 0; j < P; ++j) acc = pair_term<kIQ2_XXS, LT>(lds, L, r[j], l + LPR * j, A.a[j], A.gs[j], A.d[j], acc);
         } else if (has_type<kIQ2_XS, TM>() && type == kIQ2_XS) {
 #pragma unroll
-            for (int j = 0; j < P; ++j) acc = pair_term<kIQ2_XS, LT>(lds, L, r[j], l + LPR * j, A.a[j], A.d[j], acc);
+            for (int j = 0; j < P; ++j) acc = pair_term<kIQ2_XS, LT>(lds, L, r[j], l + LPR * j, A.a[j], A.gs[j], A.d[j], acc);
         } else if (has_type<kIQ1_M, TM>()) {
 #pragma unroll
-            for (int j = 0; j < P; ++j) acc = pair_term<kIQ1_M, LT>(lds, L, r[j], l + LPR * j, A.a[j], A.d[j], acc);
+            for (int j = 0; j < P; ++j) acc = pair_term<kIQ1_M, LT>(lds, L, r[j], l + LPR * j, A.a[j], A.gs[j], A.d[j], acc);
         }
     }
     return acc;
@@ -310,7 +326,7 @@ __global__ __launch_bounds__(NW * 64, 1) void layer3_kernel(Layer3Args a) {
         if constexpr (TM & 3) lds_dma<NW>(lds, LY::HQ, gt + kG_SGN, 2048, wv, lane);
         if constexpr (TM & 1) lds_dma<NW>(lds, LY::HQ + 2048, gt + kG_XXS, 2048, wv, lane);
         if constexpr (TM & 2) lds_dma<NW>(lds, LY::HQ + 4096, gt + kG_XS, 4096, wv, lane);
-        if constexpr (TM & 4) lds_dma<NW>(lds, LY::IQ1, gt + kG_IQ1, 16384, wv, lane);
+        if constexpr (TM & 4) lds_dma<NW>(lds, LY::C1 > 1 ? LY::HQ : LY::IQ1, gt + kG_IQ1, 16384, wv, lane);
     }
     constexpr int UX = (16 + NW - 1) / NW;
     float4 xv[UX];
@@ -352,6 +368,7 @@ __global__ __launch_bounds__(NW * 64, 1) void layer3_kernel(Layer3Args a) {
     if constexpr (TM & 3) lds_replicate<NW * 64>(lds, LY::SGN, LY::HQ, 128, 16, LY::CS, t);
     if constexpr (TM & 1) lds_replicate<NW * 64>(lds, LY::XXS, LY::HQ + 2048, 256, 8, LY::CXXS, t);
     if constexpr (TM & 2) lds_replicate<NW * 64>(lds, LY::XS, LY::HQ + 4096, 512, 8, LY::CXS, t);
+    if constexpr ((TM & 4) && LY::C1 > 1) lds_replicate<NW * 64>(lds, LY::IQ1, LY::HQ, 2048, 8, LY::C1, t);
 #pragma unroll
     for (int u = 0; u < UX; ++u) {
         const int b = wv + NW * u;
@@ -403,6 +420,7 @@ __global__ __launch_bounds__(NW * 64, 1) void layer3_kernel(Layer3Args a) {
             }
             A.d[q] = reinterpret_cast<const float*>(lds + LY::XD)[p >> 2];
         }
+        group_sums<GUT>(A);
         // Fully unrolled (no break): the per-slot references stay in registers.
 #pragma unroll
         for (int j = 0; j < MG; ++j) {
@@ -527,6 +545,7 @@ __global__ __launch_bounds__(NW * 64, 1) void layer3_kernel(Layer3Args a) {
                             }
                             B.d[q] = reinterpret_cast<const float*>(hq + ff)[p >> 2];
                         }
+                        group_sums<DNT>(B);
                         cur = i;
                     }
                     y = __fmul_rn(0.125f, gsum<LD>(row_sum<DNT, TM, PD>(lds, L, dm[j].type, rd[j % (WIND + 1)], B, lD, LD)));
@@ -576,7 +595,8 @@ static hipError_t launch3(const Layer3Args& args, int grid, hipStream_t s) {
     const int P = args.k * nq_wg;
     const int nqb = args.k * (args.ff / 256);
     if ((SG + W - 1) / W > MG || (P + NW - 1) / NW > MD || nqb > W || P * RD > kYStage || grid > quads ||
-        args.ff > 4096 || Lay<GUT | DNT>::HQ + args.k * (args.ff + 64) > kLdsBytes)
+        args.ff > 4096 || Lay<GUT | DNT>::HQ + args.k * (args.ff + 64) > kLdsBytes ||
+        Lay<GUT | DNT>::HQ + 16384 > kLdsBytes)   // the codebooks' single copies are staged there
         return hipErrorNotSupported;
     hipLaunchKernelGGL((layer3_kernel<NW, LG, PG, LD, PD, MG, MD, WIN, WIND, GUT, DNT>), dim3(grid), dim3(NW * 64), 0, s,
                        args);
@@ -584,10 +604,12 @@ static hipError_t launch3(const Layer3Args& args, int grid, hipStream_t s) {
 }
 
 // Instances by block-type set: (gate/up types, down types) exactly ({IQ2_XXS},
-// {IQ2_XS}) has its own instance; anything else takes the all-types one.
+// {IQ2_XS}) and ({IQ1_M}, {IQ1_M}) have their own instances; anything else
+// takes the all-types one.
 template <int NW, int LG, int PG, int LD, int PD, int MG, int MD, int WIN, int WIND>
 static hipError_t launch3_types(const Layer3Args& args, int gu_types, int dn_types, int grid, hipStream_t s) {
     if (gu_types == 1 && dn_types == 2) return launch3<NW, LG, PG, LD, PD, MG, MD, WIN, WIND, 1, 2>(args, grid, s);
+    if (gu_types == 4 && dn_types == 4) return launch3<NW, LG, PG, LD, PD, MG, MD, WIN, WIND, 4, 4>(args, grid, s);
     return launch3<NW, LG, PG, LD, PD, MG, MD, WIN, WIND, 7, 7>(args, grid, s);
 }
 

@@ -252,7 +252,8 @@ def test_matvec_any_fp16_scale(probe, orc, t):
     assert max_rel(got, want) < TOL
 
 
-@pytest.mark.parametrize("dim,ff,sig", [(4096, 3072, None), (4096, 3072, (16, 16, 17)), (1024, 512, (17, 17, 16)),
+@pytest.mark.parametrize("dim,ff,sig", [(4096, 3072, None), (4096, 3072, (16, 16, 17)), (4096, 3072, (29, 29, 29)),
+                                        (1024, 512, (17, 17, 16)),
                                         (1024, 512, (16, 16, 17)), (256, 768, (16, 16, 17)),
                                         (256, 768, (29, 29, 17)), (512, 256, (16, 16, 29)), (256, 256, (17, 17, 17))])
 def test_layer_paths_agree(orc, dim, ff, sig, monkeypatch):

@@ -7,6 +7,6 @@ There is no fallback path: if the HIP library is missing, importing the lane
 raises.
 """
 from .lane import (  # noqa: F401
-    IQ1_M, IQ2_XS, IQ2_XXS, BLOCK_BYTES, Lane, XLError, codebook, generate_host, lib, planar_bytes, repack,
-    restore,
+    IQ1_M, IQ2_XS, IQ2_XXS, BLOCK_BYTES, Lane, XLError, codebook, generate_host, lib, pack_meta, pack_types,
+    planar_bytes, repack, restore,
 )

@@ -15,8 +15,11 @@
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
+#include <fstream>
+#include <map>
 #include <new>
 #include <set>
+#include <sstream>
 #include <stdexcept>
 #include <string>
 #include <vector>
@@ -610,6 +613,169 @@ int32_t xl_bank_upload(xl_context* ctx, int32_t layer, int32_t expert, int32_t r
         hip_check(hipMemcpyAsync(const_cast<uint8_t*>(m.base), planar.data(), P.bytes, hipMemcpyHostToDevice, ctx->stream),
                   "weight upload");
         hip_check(hipStreamSynchronize(ctx->stream), "weight upload drain");
+    });
+}
+
+// ---- pack loader -----------------------------------------------------------------
+// The reference's weight pack (sycl/stage/wiring/pack_source.cpp:144-186): a
+// directory with ds4.txt ("key value" lines: model_dir, format, hidden_size,
+// num_hidden_layers, n_routed_experts, num_experts_per_tok,
+// moe_intermediate_size, ...) and tensors.txt ("file <i> <name>" and
+// "t <name> <dtype> <file> <offset> <bytes> <shape...>" lines) over shard
+// files in model_dir. Routed experts are layers.<l>.ffn.experts.<e>.w1 (gate),
+// .w3 (up) and .w2 (down) .weight, raw ggml blocks (engine/strata/warm/
+// test_mmvq.py:111-137 writes the same layout).
+namespace {
+
+struct PackTensor {
+    std::string dtype;
+    int file = -1;
+    uint64_t offset = 0, bytes = 0;
+};
+struct Pack {
+    std::string dir, model_dir;
+    std::map<std::string, std::string> kv;
+    std::vector<std::string> files;
+    std::map<std::string, PackTensor> t;
+    int num(const char* key) const {
+        const auto it = kv.find(key);
+        if (it == kv.end()) fail(XL_E_ARG, "pack ds4.txt: %s missing", key);
+        char* end = nullptr;
+        const long v = std::strtol(it->second.c_str(), &end, 10);
+        if (*end || v < 0 || v > (1L << 30)) fail(XL_E_ARG, "pack ds4.txt: %s is not a count", key);
+        return int(v);
+    }
+};
+
+std::string slurp(const std::string& path) {
+    std::ifstream f(path, std::ios::binary);
+    if (!f) fail(XL_E_ARG, "pack: cannot read %s", path.c_str());
+    std::ostringstream s;
+    s << f.rdbuf();
+    return s.str();
+}
+
+Pack read_pack(const char* dir) {
+    need(dir != nullptr && *dir, XL_E_ARG, "null pack directory");
+    Pack p;
+    p.dir = dir;
+    {
+        std::istringstream f(slurp(p.dir + "/ds4.txt"));
+        std::string line;
+        while (std::getline(f, line)) {
+            const size_t sp = line.find(' ');
+            if (sp != std::string::npos) p.kv[line.substr(0, sp)] = line.substr(sp + 1);
+        }
+    }
+    const auto fmt = p.kv.find("format");
+    need(fmt != p.kv.end() && fmt->second == "gguf", XL_E_ARG, "pack: only the gguf format is admitted");
+    const auto md = p.kv.find("model_dir");
+    need(md != p.kv.end() && !md->second.empty(), XL_E_ARG, "pack ds4.txt: model_dir missing");
+    p.model_dir = md->second[0] == '/' ? md->second : p.dir + "/" + md->second;
+    std::istringstream f(slurp(p.dir + "/tensors.txt"));
+    std::string line;
+    while (std::getline(f, line)) {
+        std::istringstream s(line);
+        std::string tag;
+        s >> tag;
+        if (tag == "file") {
+            int i = -1;
+            std::string name;
+            s >> i >> name;
+            need(i >= 0 && i < (1 << 20) && !name.empty(), XL_E_ARG, "pack tensors.txt: bad file line");
+            if (int(p.files.size()) <= i) p.files.resize(size_t(i) + 1);
+            p.files[size_t(i)] = name;
+        } else if (tag == "t") {
+            std::string name;
+            PackTensor x;
+            s >> name >> x.dtype >> x.file >> x.offset >> x.bytes;
+            need(!s.fail() && !name.empty(), XL_E_ARG, "pack tensors.txt: bad tensor line");
+            need(p.t.emplace(name, x).second, XL_E_ARG, "pack tensors.txt: duplicate tensor");
+        }
+    }
+    return p;
+}
+
+int32_t ggml_type_of(const std::string& dtype) {
+    if (dtype == "IQ2_XXS") return xl::kIQ2_XXS;
+    if (dtype == "IQ2_XS") return xl::kIQ2_XS;
+    if (dtype == "IQ1_M") return xl::kIQ1_M;
+    return -1;
+}
+
+const char* kRoleName[3] = {"w1", "w3", "w2"};   // gate, up, down
+
+const PackTensor& expert_tensor(const Pack& p, int layer, int expert, int role) {
+    const std::string name = "layers." + std::to_string(layer) + ".ffn.experts." + std::to_string(expert) + "." +
+                             kRoleName[role] + ".weight";
+    const auto it = p.t.find(name);
+    if (it == p.t.end()) fail(XL_E_ARG, "pack: tensor %s missing", name.c_str());
+    return it->second;
+}
+
+}  // namespace
+
+int32_t xl_pack_meta_get(const char* pack_dir, xl_pack_meta* out, xl_error* err) {
+    return guarded(nullptr, err, [&] {
+        need(out != nullptr, XL_E_ARG, "null output");
+        need(out->struct_bytes == sizeof(xl_pack_meta), XL_E_VERSION, "xl_pack_meta size mismatch");
+        const Pack p = read_pack(pack_dir);
+        out->dim = p.num("hidden_size");
+        out->ff = p.num("moe_intermediate_size");
+        out->n_layers = p.num("num_hidden_layers");
+        out->n_experts = p.num("n_routed_experts");
+        out->top_k = p.num("num_experts_per_tok");
+    });
+}
+
+int32_t xl_pack_types(const char* pack_dir, int32_t first_layer, int32_t n_layers, int32_t n_experts, int32_t* types,
+                      xl_error* err) {
+    return guarded(nullptr, err, [&] {
+        need(types != nullptr && first_layer >= 0 && n_layers >= 1 && n_experts >= 1, XL_E_ARG, "bad layer window");
+        const Pack p = read_pack(pack_dir);
+        for (int l = 0; l < n_layers; ++l)
+            for (int e = 0; e < n_experts; ++e)
+                for (int r = 0; r < 3; ++r) {
+                    const int32_t t = ggml_type_of(expert_tensor(p, first_layer + l, e, r).dtype);
+                    need(t > 0, XL_E_ARG, "pack: an expert matrix is not IQ2_XXS / IQ2_XS / IQ1_M");
+                    types[(size_t(l) * n_experts + e) * 3 + r] = t;
+                }
+    });
+}
+
+int32_t xl_bank_load_pack(xl_context* ctx, const char* pack_dir, int32_t first_layer, xl_error* err) {
+    return guarded(ctx, err, [&] {
+        ready(ctx, true);
+        const Pack p = read_pack(pack_dir);
+        need(p.num("hidden_size") == ctx->cfg.dim && p.num("moe_intermediate_size") == ctx->cfg.ff, XL_E_ARG,
+             "pack: hidden_size / moe_intermediate_size differ from the context's dim / ff");
+        need(p.num("n_routed_experts") == ctx->cfg.n_experts, XL_E_ARG, "pack: n_routed_experts differs from the context");
+        need(first_layer >= 0 && first_layer + ctx->cfg.n_layers <= p.num("num_hidden_layers"), XL_E_ARG,
+             "pack: layer window past num_hidden_layers");
+        std::vector<uint8_t> buf;
+        std::vector<std::ifstream> shards(p.files.size());
+        for (int l = 0; l < ctx->cfg.n_layers; ++l)
+            for (int e = 0; e < ctx->cfg.n_experts; ++e)
+                for (int r = 0; r < 3; ++r) {
+                    const PackTensor& x = expert_tensor(p, first_layer + l, e, r);
+                    const xl::MatRef& m = ctx->descs[size_t(l) * ctx->cfg.n_experts + e].m[r];
+                    need(ggml_type_of(x.dtype) == m.type, XL_E_ARG, "pack: a matrix type differs from the bank's");
+                    need(x.file >= 0 && size_t(x.file) < p.files.size() && !p.files[size_t(x.file)].empty(), XL_E_ARG,
+                         "pack: tensor names an unknown shard");
+                    auto& sh = shards[size_t(x.file)];
+                    if (!sh.is_open()) {
+                        sh.open(p.model_dir + "/" + p.files[size_t(x.file)], std::ios::binary);
+                        if (!sh) fail(XL_E_ARG, "pack: cannot open shard %s", p.files[size_t(x.file)].c_str());
+                    }
+                    buf.resize(x.bytes);
+                    sh.seekg(std::streamoff(x.offset));
+                    sh.read(reinterpret_cast<char*>(buf.data()), std::streamsize(x.bytes));
+                    need(bool(sh) && uint64_t(sh.gcount()) == x.bytes, XL_E_ARG, "pack: tensor extent past shard end");
+                    xl_error e2{};
+                    const int32_t rc = xl_bank_upload(ctx, l, e, r, buf.data(), x.bytes, &e2);
+                    if (rc != XL_OK) fail(rc, "pack: layer %d expert %d %s: %s", first_layer + l, e, kRoleName[r], e2.message);
+                }
+        ctx->generated = false;
     });
 }
 

@@ -57,6 +57,11 @@ _i32p = np.ctypeslib.ndpointer(np.int32, flags="C_CONTIGUOUS")
 _u64p = np.ctypeslib.ndpointer(np.uint64, flags="C_CONTIGUOUS")
 _ErrP = C.POINTER(_Err)
 
+class _PackMeta(C.Structure):
+    _fields_ = [("struct_bytes", C.c_uint32), ("dim", C.c_int32), ("ff", C.c_int32), ("n_layers", C.c_int32),
+                ("n_experts", C.c_int32), ("top_k", C.c_int32)]
+
+
 _SIGNATURES = {
     "xl_abi_version": (C.c_uint32, []),
     "xl_open": (_I32, [C.c_uint32, C.POINTER(_Config), C.POINTER(_P), _ErrP]),
@@ -77,6 +82,9 @@ _SIGNATURES = {
     "xl_grouped_forward": (_I32, [_P, _I32, _I32, _I32, _i32p, _f32p, _f32p, _P, _f32p, _ErrP]),
     "xl_grouped_forward_async": (_I32, [_P, _I32, _I32, _I32, _P, _P, _P, _P, _P, _P, _ErrP]),
     "xl_route_async": (_I32, [_P, _P, _I32, _I32, _P, _I32, _I32, C.c_float, _P, _P, _P, _ErrP]),
+    "xl_pack_meta_get": (_I32, [C.c_char_p, C.POINTER(_PackMeta), _ErrP]),
+    "xl_pack_types": (_I32, [C.c_char_p, _I32, _I32, _I32, _i32p, _ErrP]),
+    "xl_bank_load_pack": (_I32, [_P, C.c_char_p, _I32, _ErrP]),
     "xl_layer_forward_routed_async": (_I32, [_P, _I32, _P, _P, _I32, C.c_float, _P, _P, _P, _P, _ErrP]),
     "xl_grouped_forward_routed_async": (_I32, [_P, _I32, _I32, _P, _P, _I32, C.c_float, _P, _P, _P, _P, _ErrP]),
     "xl_quantize_q8k_async": (_I32, [_P, _P, _I32, _I32, _P, _P, _ErrP]),
@@ -163,6 +171,23 @@ def codebook(which: int) -> np.ndarray:
     return out
 
 
+def pack_meta(pack_dir: str) -> dict:
+    """Shape of a weight pack (ds4.txt): dim, ff, n_layers, n_experts, top_k."""
+    m = _PackMeta(C.sizeof(_PackMeta))
+    err = _Err()
+    _check(lib().xl_pack_meta_get(os.fsencode(pack_dir), C.byref(m), C.byref(err)), err)
+    return {f: getattr(m, f) for f, _ in _PackMeta._fields_[1:]}
+
+
+def pack_types(pack_dir: str, first_layer: int, n_layers: int, n_experts: int) -> np.ndarray:
+    """Block types [n_layers, n_experts, 3] (gate, up, down) of a pack's layer window."""
+    out = np.zeros((n_layers, n_experts, 3), np.int32)
+    err = _Err()
+    _check(lib().xl_pack_types(os.fsencode(pack_dir), first_layer, n_layers, n_experts, out.reshape(-1), C.byref(err)),
+           err)
+    return out
+
+
 # ---- the lane ------------------------------------------------------------------
 class Lane:
     """One context: a resident bank of n_layers x n_experts experts on one GPU."""
@@ -205,6 +230,10 @@ class Lane:
     # -- bank
     def generate(self, seed: int) -> None:
         self._call("xl_bank_generate", C.c_uint64(seed))
+
+    def load_pack(self, pack_dir: str, first_layer: int = 0) -> None:
+        """Uploads every expert of pack layers first_layer .. + n_layers - 1."""
+        self._call("xl_bank_load_pack", os.fsencode(pack_dir), first_layer)
 
     def upload(self, layer: int, expert: int, role: int, aos: np.ndarray) -> None:
         aos = np.ascontiguousarray(aos, dtype=np.uint8)

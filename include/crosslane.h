@@ -92,6 +92,25 @@ int32_t xl_bank_info_get(const xl_context* ctx, xl_bank_info* out);
  * engine/strata/warm/runtime.hpp:14). */
 int32_t xl_contains(const xl_context* ctx, int32_t layer, int32_t expert);
 
+/* ---- weight pack -------------------------------------------------------------
+ * The reference's pack directory (engine/strata/sycl/stage/wiring/
+ * pack_source.cpp:144-186): ds4.txt (model_dir, format gguf, hidden_size,
+ * moe_intermediate_size, num_hidden_layers, n_routed_experts,
+ * num_experts_per_tok, ...) and tensors.txt over shard files; routed experts
+ * are layers.<l>.ffn.experts.<e>.w1 / w3 / w2 .weight (gate / up / down) in
+ * raw ggml blocks. Host only: xl_pack_meta_get reads the shape, xl_pack_types
+ * the block types of a layer window (layout as xl_bank_create takes them);
+ * xl_bank_load_pack uploads every expert of the context's n_layers, pack
+ * layers first_layer.. (dim, ff and n_experts must match the pack). */
+typedef struct xl_pack_meta {
+    uint32_t struct_bytes; /* sizeof(xl_pack_meta) */
+    int32_t dim, ff, n_layers, n_experts, top_k;
+} xl_pack_meta;
+int32_t xl_pack_meta_get(const char* pack_dir, xl_pack_meta* out, xl_error* err);
+int32_t xl_pack_types(const char* pack_dir, int32_t first_layer, int32_t n_layers, int32_t n_experts, int32_t* types,
+                      xl_error* err);
+int32_t xl_bank_load_pack(xl_context* ctx, const char* pack_dir, int32_t first_layer, xl_error* err);
+
 /* ---- lane calls, host memory, synchronous --------------------------------
  * xl_expert_forward   = WarmRedirect::warm_compute        (runtime.hpp:15)
  * xl_experts_forward  = WarmRedirect::warm_compute_many   (runtime.hpp:13):

@@ -24,8 +24,11 @@
 // chunk-major activation layouts below guarantee.
 //
 // Weights stream from HBM through registers: each wave loads its 16 rows' next
-// block while it computes the current one, and touches the block four ahead
-// with one dword per row so that its lines are in L2 when the real loads come.
+// block while it computes the current one, and touches the line four blocks
+// ahead with one dword per row so that it is in L2 when the real loads come.
+// The per-block scales are staged in LDS once per work item: the kernels are
+// bound by the texture-address unit, which costs the same per load
+// instruction whatever its width.
 #include <hip/hip_runtime.h>
 
 #include "xl_dev.hpp"
@@ -47,7 +50,13 @@ constexpr int kTabSgn = 0, kTabXXS = 2048, kTabXS = 4096;
 // (lane copy = lane % C, so the 16 lanes of one ds_read_b128 pass never share
 // a bank), sign masks as 8 B in 32 copies (the 32 lanes of one ds_read_b64 pass
 // never share a bank) indexed by a whole byte whose top bit is not a sign bit.
-constexpr int kL_GRID = 0, kL_SGN = 65536, kL_Bytes = 131072;
+constexpr int kL_GRID = 0, kL_SGN = 65536, kL_TAB = 131072;
+// Per work item, staged once by the workgroup (each wave would otherwise issue
+// these small loads every block): the 16 pairs' activation block scales
+// [block][pair] (f32), then the item's 128 rows' fp16 block scales [row][block]
+// for each matrix, then (down) the rows' IQ2_XS scale bytes [row][block][8].
+constexpr int kL_PD = kL_TAB, kL_RD = kL_PD + 16 * 16 * 4, kL_RS = kL_RD + 2 * 128 * 16 * 2;
+constexpr int kL_Bytes = kL_RS + 128 * 16 * 8;
 constexpr int kCopiesXXS = 16;   // 256 entries x 256 B: the entry byte lands in address byte 1
 constexpr int kCopiesXS = 8;     // 512 entries x 128 B: the 9-bit entry lands at address bit 7
 
@@ -217,15 +226,30 @@ __device__ __forceinline__ uint16_t ld16(__amdgpu_buffer_rsrc_t r, uint32_t v, u
 // One block's operands for one wave.
 struct GuOps {
     uint4 g[4], u[4], a[4];   // gate / up quants of the lane's row, the lane's activation chunk
-    uint16_t dg, du;          // fp16 block scales
-    float xd[4];              // Q8_K(x) block scales of the lane's 4 output pairs
 };
 struct DnOps {
     uint4 q[4], a[8];         // down codes of the lane's row, the lane's split activation chunk
-    uint2 s;                  // scale nibbles
-    uint16_t d;               // fp16 block scale
-    float hd[4];              // Q8_K(h) block scales of the lane's 4 output pairs
 };
+
+// Stages one item's pair scales (scl: one f32 per (pair row, block), pairs of
+// the task's order slots) and `mats` planes of fp16 row scales (128 rows from
+// row0, nb per row, contiguous in each plane) into LDS, between two barriers.
+template <int NT>
+__device__ __forceinline__ void stage_item(uint8_t* lds, const GroupArgs& a, const int4& tk, const float* scl, int per_pair,
+                                           int nb, const uint8_t* const* planes, int mats, int row0, int t) {
+    __syncthreads();   // every wave is done with the previous item's staging
+    for (int i = t; i < 16 * nb; i += NT) {
+        const int pos = i & 15, blk = i >> 4;
+        const int p = a.order[tk.y + min(pos, tk.z - 1)];
+        reinterpret_cast<float*>(lds + kL_PD)[i] = scl[size_t(per_pair ? p : p / a.k) * nb + blk];
+    }
+    const int chunks = 128 * nb * 2 / 16;   // 16-byte pieces of one plane's 128 rows
+    for (int i = t; i < mats * chunks; i += NT) {
+        const int m = i / chunks, c = i - m * chunks;
+        const uint4 v = reinterpret_cast<const uint4*>(planes[m] + size_t(row0) * nb * 2)[c];
+        *reinterpret_cast<uint4*>(lds + kL_RD + m * 128 * 16 * 2 + 16 * c) = v;
+    }
+}
 
 // ---------------------------------------------------------------------------
 // gate/up + SwiGLU. Work item = (task, group of NW * 16 rows); wave wv owns
@@ -253,17 +277,18 @@ __global__ __launch_bounds__(NW * 64, 1) void gu_kernel(GroupArgs a) {
         const int pa = a.order[tk.y + (col < tk.z ? col : 0)];   // A operand: pair col of the task
         const uint32_t va = uint32_t((pa / a.k) * a.dim + 64 * e4);   // the lane's activation chunk, block 0
         int po[4];
-        uint32_t vxd[4];
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
             const int pos = 4 * e4 + r;
             po[r] = pos < tk.z ? a.order[tk.y + pos] : -1;
-            vxd[r] = uint32_t((po[r] >= 0 ? po[r] / a.k : pa / a.k) * nb) * 4u;
         }
         const MatRef G = mat_at(a.descs, tk.x, 0), U = mat_at(a.descs, tk.x, 1);
-        const __amdgpu_buffer_rsrc_t rg = rsrc(G.base), ru = rsrc(U.base), rx = rsrc(a.xq), rxd = rsrc(a.xd);
-        const uint32_t vq = uint32_t(row * nb) * 64u, vd = uint32_t(row * nb) * 2u;
-        const uint32_t og = uint32_t(G.off1), ou = uint32_t(U.off1);
+        {
+            const uint8_t* planes[2] = {G.base + G.off1, U.base + U.off1};
+            stage_item<NW * 64>(lds, a, tk, a.xd, 0, nb, planes, 2, grp * NW * 16, t);
+        }
+        const __amdgpu_buffer_rsrc_t rg = rsrc(G.base), ru = rsrc(U.base), rx = rsrc(a.xq);
+        const uint32_t vq = uint32_t(row * nb) * 64u;
         auto load = [&](GuOps& o, int blk) {
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
@@ -271,10 +296,6 @@ __global__ __launch_bounds__(NW * 64, 1) void gu_kernel(GroupArgs a) {
                 o.u[i] = ld128(ru, vq + 64u * blk + 16u * i);
                 o.a[i] = ld128(rx, va + 256u * blk + 16u * i);
             }
-            o.dg = ld16(rg, vd + 2u * blk, og);
-            o.du = ld16(ru, vd + 2u * blk, ou);
-#pragma unroll
-            for (int r = 0; r < 4; ++r) o.xd[r] = __uint_as_float(ld32(rxd, vxd[r] + 4u * blk));
         };
         auto touch = [&](int blk) { return ld32(rg, vq + 64u * blk) ^ ld32(ru, vq + 64u * blk); };
         float accg[4] = {0.0f, 0.0f, 0.0f, 0.0f}, accu[4] = {0.0f, 0.0f, 0.0f, 0.0f};
@@ -297,7 +318,11 @@ __global__ __launch_bounds__(NW * 64, 1) void gu_kernel(GroupArgs a) {
 #pragma unroll
             for (int r = 0; r < 4; ++r) bi[r] = mad24(ls, C[r], bi[r]);
         };
+        const uint16_t* sdg = reinterpret_cast<const uint16_t*>(lds + kL_RD) + (wv * 16 + col) * nb;
+        const uint16_t* sdu = sdg + 128 * 16;
+        int blk_c = 0;   // block the next compute() handles
         auto compute = [&](const GuOps& o) {
+            const int b = blk_c++;
             int big[4] = {0, 0, 0, 0}, biu[4] = {0, 0, 0, 0};
             long A[8];
 #pragma unroll
@@ -315,20 +340,23 @@ __global__ __launch_bounds__(NW * 64, 1) void gu_kernel(GroupArgs a) {
             }
 #pragma unroll
             for (int c = 0; c < 8; ++c) use(L[c], o.u, c, A[c], biu);
-            const float dgf = h2f(o.dg), duf = h2f(o.du);
+            const float dgf = h2f(sdg[b]), duf = h2f(sdu[b]);
+            const float4 xd4 = *reinterpret_cast<const float4*>(lds + kL_PD + 64 * b + 16 * e4);
+            const float xd[4] = {xd4.x, xd4.y, xd4.z, xd4.w};
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
-                accg[r] = fmaf(__fmul_rn(dgf, o.xd[r]), float(big[r]), accg[r]);
-                accu[r] = fmaf(__fmul_rn(duf, o.xd[r]), float(biu[r]), accu[r]);
+                accg[r] = fmaf(__fmul_rn(dgf, xd[r]), float(big[r]), accg[r]);
+                accu[r] = fmaf(__fmul_rn(duf, xd[r]), float(biu[r]), accu[r]);
             }
         };
         // Two operand sets alternate over a 4-step unrolled loop (no register
         // copies, so no wait ever covers a load issued in the same step); line
         // touches four blocks ahead in four fixed registers.
+        // A row's blocks 2j and 2j + 1 share a 128-byte line: one touch per line.
         GuOps s0, s1;
+        __syncthreads();   // the item's scales are staged
         load(s0, 0);
-        uint32_t t0 = touch(min(1, nb - 1)), t1 = touch(min(2, nb - 1)), t2 = touch(min(3, nb - 1)),
-                 t3 = touch(min(4, nb - 1));
+        uint32_t t0 = touch(min(1, nb - 1)), t2 = touch(min(3, nb - 1));
         for (int b = 0; b < nb; b += 4) {
             load(s1, min(b + 1, nb - 1));
             sink(sunk, t0);
@@ -336,8 +364,6 @@ __global__ __launch_bounds__(NW * 64, 1) void gu_kernel(GroupArgs a) {
             __builtin_amdgcn_sched_barrier(0);   // the loads stay ahead of the compute
             compute(s0);
             load(s0, min(b + 2, nb - 1));
-            sink(sunk, t1);
-            t1 = touch(min(b + 6, nb - 1));
             __builtin_amdgcn_sched_barrier(0);
             if (b + 1 < nb) compute(s1);
             load(s1, min(b + 3, nb - 1));
@@ -346,12 +372,10 @@ __global__ __launch_bounds__(NW * 64, 1) void gu_kernel(GroupArgs a) {
             __builtin_amdgcn_sched_barrier(0);
             if (b + 2 < nb) compute(s0);
             load(s0, min(b + 4, nb - 1));
-            sink(sunk, t3);
-            t3 = touch(min(b + 8, nb - 1));
             __builtin_amdgcn_sched_barrier(0);
             if (b + 3 < nb) compute(s1);
         }
-        sink(sunk, t0 ^ t1 ^ t2 ^ t3);
+        sink(sunk, t0 ^ t2);
 #pragma unroll
         for (int r = 0; r < 4; ++r)
             if (po[r] >= 0)
@@ -388,30 +412,36 @@ __global__ __launch_bounds__(NW * 64, 1) void dn_kernel(GroupArgs a) {
         const int pa = a.order[tk.y + (col < tk.z ? col : 0)];
         const uint32_t va = uint32_t(pa * nb) * 512u + 128u * e4;   // the lane's split activation chunk, block 0
         int po[4];
-        uint32_t vhd[4];
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
             const int pos = 4 * e4 + r;
             po[r] = pos < tk.z ? a.order[tk.y + pos] : -1;
-            vhd[r] = uint32_t((po[r] >= 0 ? po[r] : pa) * nb) * 4u;
         }
         const MatRef D = mat_at(a.descs, tk.x, 2);
-        const __amdgpu_buffer_rsrc_t rd = rsrc(D.base), rh = rsrc(a.hq), rhd = rsrc(a.hd);
-        const uint32_t vq = uint32_t(row * nb) * 64u, vs = uint32_t(row * nb) * 8u, vd = uint32_t(row * nb) * 2u;
-        const uint32_t os = uint32_t(D.off1), od = uint32_t(D.off2);
+        {
+            const int row0 = grp * NW * 16;
+            const uint8_t* planes[1] = {D.base + D.off2};
+            stage_item<NW * 64>(lds, a, tk, a.hd, 1, nb, planes, 1, row0, t);
+            const int chunks = 128 * nb * 8 / 16;   // the rows' IQ2_XS scale bytes
+            for (int i = t; i < chunks; i += NW * 64)
+                *reinterpret_cast<uint4*>(lds + kL_RS + 16 * i) =
+                    reinterpret_cast<const uint4*>(D.base + D.off1 + size_t(row0) * nb * 8)[i];
+        }
+        const __amdgpu_buffer_rsrc_t rd = rsrc(D.base), rh = rsrc(a.hq);
+        const uint32_t vq = uint32_t(row * nb) * 64u;
         auto load = [&](DnOps& o, int blk) {
 #pragma unroll
             for (int i = 0; i < 4; ++i) o.q[i] = ld128(rd, vq + 64u * blk + 16u * i);
 #pragma unroll
             for (int i = 0; i < 8; ++i) o.a[i] = ld128(rh, va + 512u * blk + 16u * i);
-            o.s = ld64(rd, vs + 8u * blk, os);
-            o.d = ld16(rd, vd + 2u * blk, od);
-#pragma unroll
-            for (int r = 0; r < 4; ++r) o.hd[r] = __uint_as_float(ld32(rhd, vhd[r] + 4u * blk));
         };
         auto touch = [&](int blk) { return ld32(rd, vq + 64u * blk); };
         float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+        const int rl = wv * 16 + col;   // the lane's row within the item
+        int blk_c = 0;                   // block the next compute() handles
         auto compute = [&](const DnOps& o) {
+            const int b = blk_c++;
+            const uint2 sc = *reinterpret_cast<const uint2*>(lds + kL_RS + 8 * (rl * nb + b));
             int bi[4] = {0, 0, 0, 0};
             uint32_t code[8];
             uint4 g[8];
@@ -429,19 +459,21 @@ __global__ __launch_bounds__(NW * 64, 1) void dn_kernel(GroupArgs a) {
                 const long B = pack64(bfi(m[c].x, g[c].z, g[c].x), bfi(m[c].y, g[c].w, g[c].y));
                 const v4i C1 = mfma(pack64(av[0], av[1]), B, v4i{0, 0, 0, 0});
                 const v4i C2 = mfma(pack64(av[2], av[3]), B, v4i{0, 0, 0, 0});
-                const uint32_t sb = ((c < 4 ? o.s.x : o.s.y) >> (8 * (c & 3))) & 0xffu;
+                const uint32_t sb = ((c < 4 ? sc.x : sc.y) >> (8 * (c & 3))) & 0xffu;
                 const int ls1 = int(((sb & 15u) << 1) | 1u), ls2 = int(((sb >> 3) & 30u) | 1u);
 #pragma unroll
                 for (int r = 0; r < 4; ++r) bi[r] = mad24(ls2, C2[r], mad24(ls1, C1[r], bi[r]));
             }
-            const float ddf = h2f(o.d);
+            const float ddf = h2f(reinterpret_cast<const uint16_t*>(lds + kL_RD)[rl * nb + b]);
+            const float4 hd4 = *reinterpret_cast<const float4*>(lds + kL_PD + 64 * b + 16 * e4);
+            const float hd[4] = {hd4.x, hd4.y, hd4.z, hd4.w};
 #pragma unroll
-            for (int r = 0; r < 4; ++r) acc[r] = fmaf(__fmul_rn(ddf, o.hd[r]), float(bi[r]), acc[r]);
+            for (int r = 0; r < 4; ++r) acc[r] = fmaf(__fmul_rn(ddf, hd[r]), float(bi[r]), acc[r]);
         };
         DnOps s0, s1;
+        __syncthreads();   // the item's scales are staged
         load(s0, 0);
-        uint32_t t0 = touch(min(1, nb - 1)), t1 = touch(min(2, nb - 1)), t2 = touch(min(3, nb - 1)),
-                 t3 = touch(min(4, nb - 1));
+        uint32_t t0 = touch(min(1, nb - 1)), t2 = touch(min(3, nb - 1));
         for (int b = 0; b < nb; b += 4) {
             load(s1, min(b + 1, nb - 1));
             sink(sunk, t0);
@@ -449,8 +481,6 @@ __global__ __launch_bounds__(NW * 64, 1) void dn_kernel(GroupArgs a) {
             __builtin_amdgcn_sched_barrier(0);   // the loads stay ahead of the compute
             compute(s0);
             load(s0, min(b + 2, nb - 1));
-            sink(sunk, t1);
-            t1 = touch(min(b + 6, nb - 1));
             __builtin_amdgcn_sched_barrier(0);
             if (b + 1 < nb) compute(s1);
             load(s1, min(b + 3, nb - 1));
@@ -459,12 +489,10 @@ __global__ __launch_bounds__(NW * 64, 1) void dn_kernel(GroupArgs a) {
             __builtin_amdgcn_sched_barrier(0);
             if (b + 2 < nb) compute(s0);
             load(s0, min(b + 4, nb - 1));
-            sink(sunk, t3);
-            t3 = touch(min(b + 8, nb - 1));
             __builtin_amdgcn_sched_barrier(0);
             if (b + 3 < nb) compute(s1);
         }
-        sink(sunk, t0 ^ t1 ^ t2 ^ t3);
+        sink(sunk, t0 ^ t2);
 #pragma unroll
         for (int r = 0; r < 4; ++r)
             if (po[r] >= 0) a.y[size_t(po[r]) * a.dim + row] = __fmul_rn(0.125f, acc[r]);

@@ -65,7 +65,10 @@ struct Lay {
     static constexpr int SGN = 0;                                            // 128 rows {M.lo, M.hi, M1.lo, M1.hi}
     static constexpr int XXS = SGN + ((TM & 3) ? 128 * CS * 16 : 0);         // 256 rows of 8 magnitudes
     static constexpr int XS = XXS + ((TM & 1) ? 256 * CXXS * 8 : 0);         // 512 rows of 8 magnitudes
-    static constexpr int C1 = TM == 4 ? 4 : 1;          // IQ1 grid copies (room for them only without the IQ2 tables)
+    // IQ1 grid copies: only without the IQ2 tables is there room for copies and
+    // for staging the single copy (at HQ, where those tables' copies would be staged).
+    static constexpr int C1 = TM == 4 ? 4 : 1;
+    static_assert(C1 == 1 || (TM & 3) == 0, "the IQ1 single copy is staged where the IQ2 tables' are");
     static constexpr int IQ1 = XS + ((TM & 2) ? 512 * CXS * 8 : 0);          // 2048 rows of 8 values
     static constexpr int XQ = IQ1 + ((TM & 4) ? 2048 * 8 * C1 : 0);          // Q8_K(x) quants (dim <= 4096)
     static constexpr int XD = XQ + 4096;                                     // Q8_K(x) scales (16)

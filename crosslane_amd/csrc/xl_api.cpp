@@ -177,6 +177,7 @@ struct xl_context {
     uint64_t* hdtag = nullptr;
     uint32_t* ctl = nullptr;
     uint64_t* tables = nullptr;
+    float* p32d = nullptr;      // per32 scales: act_max / 32 of the input, then max_picks * ff / 32 of h
     uint64_t* timeline = nullptr;   // per-wave timestamps of the last profiled single launch
     uint64_t timeline_words = 0;
     // stage profiling (xl_profile_begin / xl_profile_end): events recorded
@@ -359,6 +360,39 @@ void enqueue_layer(xl_context* ctx, int32_t layer, const int32_t* d_ids, const f
     }
 }
 
+// Enqueues the per32 layer (hip_resident_bank.hpp:185-200 with the kernels of
+// hip_experts.hip): quant32(x), gate and up rows of every pick in one launch,
+// SwiGLU, quant32(h) of every pick, down rows into y (k x dim), then the
+// fixed-order combine into out when out is given.
+void enqueue_per32(xl_context* ctx, int32_t layer, const int32_t* d_ids, const float* d_w, int32_t k, const float* d_x,
+                   const float* d_shared, float* d_y, float* d_out, hipStream_t s) {
+    const int dim = ctx->cfg.dim, ff = ctx->cfg.ff, E = ctx->cfg.n_experts;
+    const xl::ExpertDesc* descs = ctx->d_descs + size_t(layer) * E;
+    float* xd = ctx->p32d;
+    float* hd = ctx->p32d + ctx->act_max / 32;
+    const xl::MatRef none{};
+    Marks mark(ctx, s);
+    mark("");
+    hip_check(xl::dev::launch_quant32(d_x, 1, dim, ctx->xq, xd, ctx->err_flag, s), "quant32(x) launch");
+    mark("quant32_x");
+    hip_check(xl::dev::launch_mv32(descs, d_ids, none, k, E, 0, 2, ff, dim, ctx->xq, 0, xd, 0, ctx->g, ctx->u,
+                                   size_t(ff), ctx->tables, ctx->err_flag, s),
+              "per32 gate/up launch");
+    mark("gate_up32");
+    hip_check(xl::dev::launch_swiglu32(ctx->g, ctx->u, k * ff, ctx->h, s), "SwiGLU launch");
+    mark("swiglu");
+    hip_check(xl::dev::launch_quant32(ctx->h, k, ff, ctx->hq, hd, ctx->err_flag, s), "quant32(h) launch");
+    mark("quant32_h");
+    hip_check(xl::dev::launch_mv32(descs, d_ids, none, k, E, 2, 1, dim, ff, ctx->hq, size_t(ff), hd, size_t(ff / 32),
+                                   d_y, nullptr, size_t(dim), ctx->tables, ctx->err_flag, s),
+              "per32 down launch");
+    mark("down32");
+    if (d_out) {
+        hip_check(xl::dev::launch_combine(d_ids, d_w, k, d_y, dim, d_shared, d_out, s), "combine launch");
+        mark("combine");
+    }
+}
+
 }  // namespace
 
 extern "C" {
@@ -422,6 +456,7 @@ int32_t xl_open(uint32_t abi_version, const xl_config* cfg, xl_context** out, xl
             {reinterpret_cast<void**>(&ctx->ctl), 256},
             {reinterpret_cast<void**>(&ctx->hbuf), uint64_t(2) * xl::kHBufWords * 4},
             {reinterpret_cast<void**>(&ctx->tables), uint64_t(xl::kLayer3TableBytes)},
+            {reinterpret_cast<void**>(&ctx->p32d), (uint64_t(ctx->act_max / 32) + uint64_t(P) * (ff / 32)) * 4},
             {reinterpret_cast<void**>(&ctx->timeline), uint64_t(ctx->cus) * 16 * 32 * 8},
         };
         if (cfg->max_tokens > 0) {
@@ -1031,6 +1066,85 @@ int32_t xl_layer_forward_async(xl_context* ctx, int32_t layer, const int32_t* d_
         need(k >= 1 && k <= ctx->cfg.max_picks, XL_E_ARG, "pick count outside 1..max_picks");
         need(d_ids && d_w && d_x && d_out, XL_E_ARG, "null device pointer");
         enqueue_layer(ctx, layer, d_ids, d_w, k, d_x, d_shared_or_null, d_out, pick_stream(ctx, stream));
+    });
+}
+
+int32_t xl_layer_forward_per32(xl_context* ctx, int32_t layer, const int32_t* ids, const float* w, int32_t k,
+                               const float* x, const float* shared_or_null, float* y_or_null, float* out_or_null,
+                               xl_error* err) {
+    return guarded(ctx, err, [&] {
+        ready(ctx, true);
+        check_layer(ctx, layer);
+        check_ids(ctx, ids, k);
+        check_finite(x, size_t(ctx->cfg.dim), "input vector");
+        need(y_or_null || out_or_null, XL_E_ARG, "neither per-pick outputs nor a combined output requested");
+        if (out_or_null) check_finite(w, size_t(k), "route weights");
+        if (out_or_null && shared_or_null) check_finite(shared_or_null, size_t(ctx->cfg.dim), "shared vector");
+        hipStream_t s = ctx->stream;
+        const int dim = ctx->cfg.dim;
+        hip_check(hipMemcpyAsync(ctx->ids, ids, sizeof(int32_t) * k, hipMemcpyHostToDevice, s), "ids upload");
+        if (out_or_null) hip_check(hipMemcpyAsync(ctx->w, w, sizeof(float) * k, hipMemcpyHostToDevice, s), "weights upload");
+        hip_check(hipMemcpyAsync(ctx->x, x, sizeof(float) * dim, hipMemcpyHostToDevice, s), "x upload");
+        const bool sh = out_or_null && shared_or_null;
+        if (sh)
+            hip_check(hipMemcpyAsync(ctx->shared, shared_or_null, sizeof(float) * dim, hipMemcpyHostToDevice, s),
+                      "shared upload");
+        enqueue_per32(ctx, layer, ctx->ids, ctx->w, k, ctx->x, sh ? ctx->shared : nullptr, ctx->y,
+                      out_or_null ? ctx->out : nullptr, s);
+        if (y_or_null)
+            hip_check(hipMemcpyAsync(y_or_null, ctx->y, sizeof(float) * size_t(k) * dim, hipMemcpyDeviceToHost, s),
+                      "per-pick output download");
+        if (out_or_null)
+            hip_check(hipMemcpyAsync(out_or_null, ctx->out, sizeof(float) * dim, hipMemcpyDeviceToHost, s),
+                      "output download");
+        drain(ctx, s);
+    });
+}
+
+int32_t xl_layer_forward_per32_async(xl_context* ctx, int32_t layer, const int32_t* d_ids, const float* d_w, int32_t k,
+                                     const float* d_x, const float* d_shared_or_null, float* d_y,
+                                     float* d_out_or_null, void* stream, xl_error* err) {
+    return guarded(ctx, err, [&] {
+        ready(ctx, true);
+        check_layer(ctx, layer);
+        need(k >= 1 && k <= ctx->cfg.max_picks, XL_E_ARG, "pick count outside 1..max_picks");
+        need(d_ids && d_x && d_y, XL_E_ARG, "null device pointer");
+        need(!d_out_or_null || d_w, XL_E_ARG, "a combined output needs route weights");
+        enqueue_per32(ctx, layer, d_ids, d_w, k, d_x, d_shared_or_null, d_y, d_out_or_null, pick_stream(ctx, stream));
+    });
+}
+
+int32_t xl_quantize_per32_async(xl_context* ctx, const float* d_x, int32_t rows, int32_t k, int8_t* d_q, float* d_d,
+                                void* stream, xl_error* err) {
+    return guarded(ctx, err, [&] {
+        ready(ctx, false);
+        need(d_x && d_q && d_d, XL_E_ARG, "null device pointer");
+        need(rows >= 1 && k >= 32 && k % 32 == 0, XL_E_ARG, "rows >= 1 and k a positive multiple of 32");
+        need(int64_t(rows) * k <= int64_t(1) << 30, XL_E_ARG, "more than 2^30 values");
+        hip_check(xl::dev::launch_quant32(d_x, rows, k, d_q, d_d, ctx->err_flag, pick_stream(ctx, stream)),
+                  "quant32 launch");
+    });
+}
+
+int32_t xl_matvec_per32_async(xl_context* ctx, int32_t type, const void* d_planar, int32_t n, int32_t k,
+                              const int8_t* d_q, const float* d_d, float* d_y, void* stream, xl_error* err) {
+    return guarded(ctx, err, [&] {
+        ready(ctx, false);
+        need(xl::supported_type(type), XL_E_ARG, "unsupported block type");
+        need(d_planar && d_q && d_d && d_y, XL_E_ARG, "null device pointer");
+        need(reinterpret_cast<uintptr_t>(d_q) % 16 == 0, XL_E_ARG, "quants not 16-byte aligned");
+        need(n >= 1 && n <= (1 << 24) && k >= 256 && k % 256 == 0 && k <= (1 << 20), XL_E_ARG,
+             "n in 1..2^24 and k a multiple of 256 up to 2^20");
+        const auto P = xl::plane_layout(type, matrix_blocks(n, k));
+        xl::MatRef m{};
+        m.base = static_cast<const uint8_t*>(d_planar);
+        m.off1 = P.off[1];
+        m.off2 = P.off[2];
+        m.type = type;
+        m.nb = k / 256;
+        hip_check(xl::dev::launch_mv32(nullptr, nullptr, m, 1, 0, 0, 1, n, k, d_q, 0, d_d, 0, d_y, nullptr, 0,
+                                       ctx->tables, ctx->err_flag, pick_stream(ctx, stream)),
+                  "per32 matvec launch");
     });
 }
 

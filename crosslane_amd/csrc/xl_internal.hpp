@@ -153,6 +153,18 @@ hipError_t launch_route(const float* logits, int T, int stride, const float* bia
                         int32_t* ids, float* w, int* err, hipStream_t s);
 hipError_t launch_combine(const int32_t* ids, const float* w, int k, const float* y, int dim, const float* shared,
                           float* out, hipStream_t s);
+// per32 mode (xl_per32.hip): per-32 activation quantization of rows x k values
+// (k a multiple of 32) into q (int8) and d (one float per 32).
+hipError_t launch_quant32(const float* x, int rows, int k, int8_t* q, float* d, int* err, hipStream_t s);
+// per32 rows of roles role0 .. role0 + roles - 1 (at most 2) of every pick's
+// expert (ids == nullptr: the one matrix `single`, picks = 1): y_r[pick *
+// y_stride + row] from q + pick * q_stride (16-byte aligned) and d + pick * d_stride.
+hipError_t launch_mv32(const ExpertDesc* descs, const int32_t* ids, const MatRef& single, int picks, int n_experts,
+                       int role0, int roles, int n, int k, const int8_t* q, size_t q_stride, const float* d,
+                       size_t d_stride, float* y0, float* y1, size_t y_stride, const uint64_t* tables, int* err,
+                       hipStream_t s);
+// h = g / (1 + exp(-g)) * u over n values.
+hipError_t launch_swiglu32(const float* g, const float* u, int n, float* h, hipStream_t s);
 // Seeded generation of one planar matrix (role 0 gate, 1 up, 2 down).
 hipError_t launch_generate(uint8_t* base, int type, int n, int k, uint64_t seed, uint32_t layer, uint32_t expert,
                            uint32_t role, hipStream_t s);

@@ -89,6 +89,10 @@ _SIGNATURES = {
     "xl_grouped_forward_routed_async": (_I32, [_P, _I32, _I32, _P, _P, _I32, C.c_float, _P, _P, _P, _P, _ErrP]),
     "xl_quantize_q8k_async": (_I32, [_P, _P, _I32, _I32, _P, _P, _ErrP]),
     "xl_matvec_async": (_I32, [_P, _I32, _P, _I32, _I32, _P, _P, _P, _P, _ErrP]),
+    "xl_layer_forward_per32": (_I32, [_P, _I32, _i32p, _P, _I32, _f32p, _P, _P, _P, _ErrP]),
+    "xl_layer_forward_per32_async": (_I32, [_P, _I32, _P, _P, _I32, _P, _P, _P, _P, _P, _ErrP]),
+    "xl_quantize_per32_async": (_I32, [_P, _P, _I32, _I32, _P, _P, _P, _ErrP]),
+    "xl_matvec_per32_async": (_I32, [_P, _I32, _P, _I32, _I32, _P, _P, _P, _P, _ErrP]),
     "xl_profile_begin": (_I32, [_P, _I32, _ErrP]),
     "xl_profile_end": (_I32, [_P, _f32p, _I32, C.POINTER(_I32), C.POINTER(_I32), C.c_char_p, _I32, _ErrP]),
     "xl_profile_timeline": (_I32, [_P, _u64p, _I32, C.POINTER(_I32), _ErrP]),
@@ -293,6 +297,20 @@ class Lane:
                    None if sh is None else sh.ctypes.data, out.reshape(-1))
         return out
 
+    def layer_forward_per32(self, layer: int, ids: Sequence[int], x: np.ndarray,
+                            weights: Optional[Sequence[float]] = None, shared: Optional[np.ndarray] = None):
+        """per32 layer (the reference's HIP lane arithmetic): returns (y [k, dim]
+        per-pick down outputs, out [dim] their combine, or None without weights)."""
+        ids = np.ascontiguousarray(ids, dtype=np.int32)
+        y = np.zeros((ids.size, self.dim), dtype=np.float32)
+        out = None if weights is None else np.zeros(self.dim, dtype=np.float32)
+        w = None if weights is None else np.ascontiguousarray(weights, dtype=np.float32)
+        sh = None if shared is None else np.ascontiguousarray(shared, dtype=np.float32)
+        self._call("xl_layer_forward_per32", layer, ids, None if w is None else w.ctypes.data, ids.size,
+                   np.ascontiguousarray(x, dtype=np.float32), None if sh is None else sh.ctypes.data, y.ctypes.data,
+                   None if out is None else out.ctypes.data)
+        return y, out
+
     def expert_trace(self, layer: int, e: int, x: np.ndarray) -> dict:
         ff, dim = self.ff, self.dim
         g = np.zeros(ff, np.float32); u = np.zeros(ff, np.float32); h = np.zeros(ff, np.float32)
@@ -352,6 +370,17 @@ class Lane:
 
     def quantize_q8k_async(self, x, rows: int, k: int, q8k_out, stream=None) -> None:
         self._call("xl_quantize_q8k_async", _ptr(x), rows, k, _ptr(q8k_out), None if stream is None else int(stream))
+
+    def layer_forward_per32_async(self, layer: int, ids, x, y, w=None, out=None, shared=None, stream=None) -> None:
+        self._call("xl_layer_forward_per32_async", layer, _ptr(ids), _ptr(w), int(ids.numel()), _ptr(x), _ptr(shared),
+                   _ptr(y), _ptr(out), None if stream is None else int(stream))
+
+    def quantize_per32_async(self, x, rows: int, k: int, q, d, stream=None) -> None:
+        self._call("xl_quantize_per32_async", _ptr(x), rows, k, _ptr(q), _ptr(d), None if stream is None else int(stream))
+
+    def matvec_per32_async(self, t: int, planar, n: int, k: int, q, d, y, stream=None) -> None:
+        self._call("xl_matvec_per32_async", t, _ptr(planar), n, k, _ptr(q), _ptr(d), _ptr(y),
+                   None if stream is None else int(stream))
 
     def matvec_async(self, t: int, planar, n: int, k: int, x, y, partials=None, stream=None) -> None:
         self._call("xl_matvec_async", t, _ptr(planar), n, k, _ptr(x), _ptr(y), _ptr(partials),

@@ -186,6 +186,33 @@ int32_t xl_quantize_q8k_async(xl_context* ctx, const float* d_x, int32_t rows, i
 int32_t xl_matvec_async(xl_context* ctx, int32_t type, const void* d_planar, int32_t n, int32_t k, const float* d_x,
                         float* d_y, int32_t* d_partials, void* stream, xl_error* err);
 
+/* ---- per32 mode (the reference's production HIP lane arithmetic) ----------
+ * Replaces hipex::quantize / hipex::project (engine/strata/warm/hip_experts.hpp,
+ * hip_experts.hip:43-64) and the SoA branch of enqueue_layer
+ * (hip_resident_bank.hpp:185-200), bit for bit: activations quantized per 32
+ * values (d = max|x| / 127, q = round-half-even(x / d)); a row is 32 lanes,
+ * lane l taking sub-blocks l, l + 32, ...: acc = fma(d_x, (fp16(d) * 0.125) *
+ * float(s0 * a + s1 * b), acc), then an xor butterfly 16..1 and lane 0 + 0.
+ * SwiGLU g / (1 + exp(-g)) * u on the device's expf (the reference's upstream
+ * swiglu kernel is not in its tree).
+ * xl_layer_forward_per32: y (k x dim, may be null) the per-pick down outputs
+ * (the reference's batch_y), out (dim, may be null, needs w) their fixed-order
+ * combine (+ shared). The async form takes device pointers (d_y required). */
+int32_t xl_layer_forward_per32(xl_context* ctx, int32_t layer, const int32_t* ids, const float* w, int32_t k,
+                               const float* x, const float* shared_or_null, float* y_or_null, float* out_or_null,
+                               xl_error* err);
+int32_t xl_layer_forward_per32_async(xl_context* ctx, int32_t layer, const int32_t* d_ids, const float* d_w, int32_t k,
+                                     const float* d_x, const float* d_shared_or_null, float* d_y,
+                                     float* d_out_or_null, void* stream, xl_error* err);
+/* rows x k floats (k a multiple of 32) into rows*k int8 d_q and rows*k/32 d_d
+ * (hip_experts.hip:17-26, hipex::quantize). */
+int32_t xl_quantize_per32_async(xl_context* ctx, const float* d_x, int32_t rows, int32_t k, int8_t* d_q, float* d_d,
+                                void* stream, xl_error* err);
+/* One planar matrix (n x k) times per32 activations (d_q 16-byte aligned, k
+ * int8; d_d k/32 scales): y[n] (dot_kernel<Type>, hip_experts.hip:27-41). */
+int32_t xl_matvec_per32_async(xl_context* ctx, int32_t type, const void* d_planar, int32_t n, int32_t k,
+                              const int8_t* d_q, const float* d_d, float* d_y, void* stream, xl_error* err);
+
 /* ---- stage profiling --------------------------------------------------------
  * Between xl_profile_begin and xl_profile_end, the first max_calls layer calls
  * record a HIP event before and after each kernel on the stream it runs on

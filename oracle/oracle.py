@@ -55,6 +55,12 @@ class Oracle:
         L.orc_down_from_hidden.argtypes = [C.c_int, _u8p, C.c_int, C.c_int, _f32p, _f32p, C.c_int]
         L.orc_combine.argtypes = [_i32p, _f32p, C.c_int, _f32p, C.c_int, _P, _f32p]
         L.orc_route.argtypes = [_f32p, C.c_int, _P, C.c_int, C.c_int, C.c_int, C.c_float, _i32p, _f32p]
+        _i8p = np.ctypeslib.ndpointer(np.int8, flags="C_CONTIGUOUS")
+        L.orc_quant32.argtypes = [_f32p, C.c_int, _i8p, _f32p]
+        L.orc_row32.argtypes = [C.c_int, _u8p, C.c_int, _i8p, _f32p]
+        L.orc_row32.restype = C.c_float
+        L.orc_matvec32.argtypes = [C.c_int, _u8p, C.c_int, C.c_int, _i8p, _f32p, _f32p]
+        L.orc_expert32.argtypes = [_i32p, _u8p, _u8p, _u8p, C.c_int, C.c_int, _f32p, _f32p, _P, _P, _P]
         L.orc_gen_key.argtypes = [C.c_uint64, C.c_uint32, C.c_uint32, C.c_uint32]
         L.orc_gen_key.restype = C.c_uint64
         L.orc_gen_block.argtypes = [C.c_int, C.c_uint64, C.c_uint64, _u8p]
@@ -122,6 +128,31 @@ class Oracle:
         self.lib.orc_combine(ids, w, k, rows.reshape(-1), dim, None if sh is None else sh.ctypes.data, out)
         return out
 
+    # -- per32 arithmetic (the production HIP lane) ------------------------
+    def quant32(self, x):
+        x = np.ascontiguousarray(x, dtype=np.float32).reshape(-1)
+        q = np.zeros(x.size, np.int8); d = np.zeros(x.size // 32, np.float32)
+        self.lib.orc_quant32(x, x.size, q, d)
+        return q, d
+
+    def row32(self, t, row, k, q, d) -> float:
+        return float(self.lib.orc_row32(t, np.ascontiguousarray(row, dtype=np.uint8).reshape(-1), k,
+                                        np.ascontiguousarray(q, dtype=np.int8), np.ascontiguousarray(d, dtype=np.float32)))
+
+    def matvec32(self, t, w, n, k, q, d):
+        y = np.zeros(n, np.float32)
+        self.lib.orc_matvec32(t, np.ascontiguousarray(w, dtype=np.uint8).reshape(-1), n, k,
+                              np.ascontiguousarray(q, dtype=np.int8), np.ascontiguousarray(d, dtype=np.float32), y)
+        return y
+
+    def expert32(self, types, gate, up, down, dim, ff, x, intermediates=False):
+        y = np.zeros(dim, np.float32)
+        g = np.zeros(ff, np.float32); u = np.zeros(ff, np.float32); h = np.zeros(ff, np.float32)
+        self.lib.orc_expert32(np.asarray(types, dtype=np.int32), gate.reshape(-1), up.reshape(-1), down.reshape(-1), dim,
+                              ff, np.ascontiguousarray(x, dtype=np.float32), y, g.ctypes.data, u.ctypes.data,
+                              h.ctypes.data)
+        return (y, g, u, h) if intermediates else y
+
     def route(self, logits, k, scale=1.0, bias=None):
         """route.cpp:15-37 for logits [T, n] (or [n]): ids, weights [T, k]."""
         lg = np.ascontiguousarray(np.atleast_2d(logits), dtype=np.float32)
@@ -182,6 +213,8 @@ class Reference:
         L.ref_matvec.argtypes = [C.c_int, _u8p, C.c_int, C.c_int, _P, _f32p, C.c_int]
         L.ref_combine.argtypes = [_i32p, _f32p, C.c_int, _f32p, C.c_int, _f32p, _f32p]
         L.ref_route.argtypes = [_f32p, C.c_int, _f32p, C.c_int, C.c_int, C.c_int, C.c_float, _i32p, _f32p]
+        L.ref_row32.argtypes = [C.c_int, _u8p, C.c_int, np.ctypeslib.ndpointer(np.int8, flags="C_CONTIGUOUS"), _f32p]
+        L.ref_row32.restype = C.c_float
         L.ref_expert.argtypes = [_i32p, _u8p, _u8p, _u8p, C.c_int, C.c_int, _f32p, _f32p, C.c_int]
 
     @staticmethod
@@ -234,6 +267,10 @@ class Reference:
         ids = np.zeros((T, k), np.int32); w = np.zeros((T, k), np.float32)
         self.lib.ref_route(lg.reshape(-1), n, b, n, T, k, scale, ids.reshape(-1), w.reshape(-1))
         return ids, w
+
+    def row32(self, t, row, k, q, d) -> float:
+        return float(self.lib.ref_row32(t, np.ascontiguousarray(row, dtype=np.uint8).reshape(-1), k,
+                                        np.ascontiguousarray(q, dtype=np.int8), np.ascontiguousarray(d, dtype=np.float32)))
 
     def combine(self, ids, w, rows, shared):
         rows = np.ascontiguousarray(rows, dtype=np.float32)

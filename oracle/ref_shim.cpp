@@ -9,6 +9,7 @@
 //   warm/other_combine.hpp:                             fixed-order combine
 //   sycl/route/route.hpp, route.cpp (compiled alongside): route_cpu
 #include <array>
+#include <cmath>
 #include <atomic>
 #include <cstring>
 #include <span>
@@ -68,6 +69,24 @@ void ref_expert(const int* types, const uint8_t* gate, const uint8_t* up, const 
     for (int i = 0; i < ff; ++i) h[size_t(i)] = q::swiglu(g[size_t(i)], u[size_t(i)], 0.0f);
     for (int b = 0; b < ff / 256; ++b) q::quant_block(h.data() + 256 * b, hq[size_t(b)]);
     ref_matvec(types[2], down, dim, ff, hq.data(), y, threads);
+}
+// One row through the reference's per-32 lane<> and the butterfly of
+// warm/expert_check.cpp:50-55 (the CPU control of the production HIP lane).
+struct RefMath {
+    static float fma(float a, float b, float c) { return std::fma(a, b, c); }
+    static float exp(float a) { return std::exp(a); }
+    static float min(float a, float b) { return std::fmin(a, b); }
+    static float max(float a, float b) { return std::fmax(a, b); }
+};
+float ref_row32(int t, const uint8_t* row, int k, const int8_t* xq, const float* xd) {
+    const m::Type ty = t == 16 ? m::Type::iq2_xxs : t == 17 ? m::Type::iq2_xs : m::Type::iq1_m;
+    std::array<float, 32> lane;
+    for (int l = 0; l < 32; ++l) lane[size_t(l)] = m::lane<RefMath>(ty, row, k, nullptr, xq, xd, l, true);
+    for (int o = 16; o; o >>= 1) {
+        const auto old = lane;
+        for (int l = 0; l < 32; ++l) lane[size_t(l)] = old[size_t(l)] + old[size_t(l ^ o)];
+    }
+    return 1.0f * lane[0] + 0.0f;
 }
 void ref_route(const float* logits, int stride, const float* bias, int n, int T, int k, float scale, int* ids, float* w) {
     const auto r = strata::ds4::route_port::route_cpu(std::span<const float>(logits, size_t(T) * size_t(stride)),

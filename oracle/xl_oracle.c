@@ -188,45 +188,124 @@ void orc_block_partials(int t, const uint8_t* w, const orc_q8k* a, int nb, int32
     }
 }
 
-/* Brute force, written from the per-32 decode of sycl/moe/core.hpp:78-105:
- * natural value order, per-16 odd sub-scales, IQ1_M values 8*grid + delta. */
-int64_t orc_brute_block(int t, const uint8_t* blk, const orc_q8k* a) {
+/* Per-32 decode of sub-block ib of a 256-weight block, written from
+ * sycl/moe/core.hpp:78-105: natural value order, per-16 odd sub-scales (sc),
+ * IQ2 values +-grid, IQ1_M values 8*grid + delta. */
+static void p32_decode(int t, const uint8_t* blk, int ib, int val[32], int sc[2]) {
     tables();
+    if (t == 16 || t == 17) {
+        const uint8_t* p = blk + 2 + 8 * ib;
+        const uint32_t aux = u32(p + 4);
+        for (int l = 0; l < 4; ++l) {
+            const unsigned code = u16(p + 2 * l);
+            const uint64_t grid = t == 16 ? g_iq2xxs[p[l]] : g_iq2xs[code & 511];
+            const unsigned sg = g_ksigns[(t == 16 ? (aux >> (7 * l)) : (code >> 9)) & 127];
+            for (int j = 0; j < 8; ++j) {
+                const int q = (int)((grid >> (8 * j)) & 255);
+                val[8 * l + j] = ((sg >> j) & 1) ? -q : q;
+            }
+        }
+        if (t == 16) sc[0] = sc[1] = 2 * (int)(aux >> 28) + 1;
+        else { sc[0] = 2 * (blk[66 + ib] & 15) + 1; sc[1] = 2 * (blk[66 + ib] >> 4) + 1; }
+    } else {
+        const unsigned word = u16(blk + 48 + 2 * (ib >> 1));
+        sc[0] = 2 * (int)((word >> (6 * (ib & 1))) & 7) + 1;
+        sc[1] = 2 * (int)((word >> (6 * (ib & 1) + 3)) & 7) + 1;
+        for (int l = 0; l < 4; ++l) {
+            const unsigned h = blk[32 + 2 * ib + l / 2];
+            const unsigned nib = (l & 1) ? (h >> 4) : (h & 15);
+            const unsigned idx = blk[4 * ib + l] | ((nib & 7) << 8);
+            const int delta = (nib & 8) ? -1 : 1;
+            for (int j = 0; j < 8; ++j) {
+                const int g = (int)(int8_t)(uint8_t)(g_iq1s[idx] >> (8 * j));
+                val[8 * l + j] = 8 * g + delta;
+            }
+        }
+    }
+}
+/* The block's super-scale as core.hpp:86,99 take it: half(d) * 0.125 (IQ1_M's
+ * fp16 d is spread over the top nibbles of its four scale words). */
+static float p32_scale(int t, const uint8_t* blk) {
+    if (t == 29) {
+        const uint16_t d = (uint16_t)((u16(blk + 48) >> 12) | ((u16(blk + 50) >> 8) & 0xf0) | ((u16(blk + 52) >> 4) & 0xf00) |
+                                      (u16(blk + 54) & 0xf000));
+        return orc_half(d) * 0.125f;
+    }
+    return orc_half(u16(blk)) * 0.125f;
+}
+
+/* Brute force over the per-32 decode, against a Q8_K activation block. */
+int64_t orc_brute_block(int t, const uint8_t* blk, const orc_q8k* a) {
     int64_t total = 0;
     for (int ib = 0; ib < 8; ++ib) {
         int val[32], sc[2];
-        if (t == 16 || t == 17) {
-            const uint8_t* p = blk + 2 + 8 * ib;
-            const uint32_t aux = u32(p + 4);
-            for (int l = 0; l < 4; ++l) {
-                const unsigned code = u16(p + 2 * l);
-                const uint64_t grid = t == 16 ? g_iq2xxs[p[l]] : g_iq2xs[code & 511];
-                const unsigned sg = g_ksigns[(t == 16 ? (aux >> (7 * l)) : (code >> 9)) & 127];
-                for (int j = 0; j < 8; ++j) {
-                    const int q = (int)((grid >> (8 * j)) & 255);
-                    val[8 * l + j] = ((sg >> j) & 1) ? -q : q;
-                }
-            }
-            if (t == 16) sc[0] = sc[1] = 2 * (int)(aux >> 28) + 1;
-            else { sc[0] = 2 * (blk[66 + ib] & 15) + 1; sc[1] = 2 * (blk[66 + ib] >> 4) + 1; }
-        } else {
-            const unsigned word = u16(blk + 48 + 2 * (ib >> 1));
-            sc[0] = 2 * (int)((word >> (6 * (ib & 1))) & 7) + 1;
-            sc[1] = 2 * (int)((word >> (6 * (ib & 1) + 3)) & 7) + 1;
-            for (int l = 0; l < 4; ++l) {
-                const unsigned h = blk[32 + 2 * ib + l / 2];
-                const unsigned nib = (l & 1) ? (h >> 4) : (h & 15);
-                const unsigned idx = blk[4 * ib + l] | ((nib & 7) << 8);
-                const int delta = (nib & 8) ? -1 : 1;
-                for (int j = 0; j < 8; ++j) {
-                    const int g = (int)(int8_t)(uint8_t)(g_iq1s[idx] >> (8 * j));
-                    val[8 * l + j] = 8 * g + delta;
-                }
-            }
-        }
+        p32_decode(t, blk, ib, val, sc);
         for (int j = 0; j < 32; ++j) total += (int64_t)sc[j / 16] * val[j] * a->qs[32 * ib + j];
     }
     return total;
+}
+
+/* ---- per32 arithmetic (the reference's production HIP lane) ---------------
+ * Activation quantization per 32 values (hip_experts.hip:17-26,
+ * expert_check.cpp:44-47): d = max|x| / 127, q = round-half-even(x / d), a
+ * zero block all zero. */
+void orc_quant32(const float* x, int k, int8_t* q, float* d) {
+    for (int b = 0; b < k / 32; ++b) {
+        float am = 0.0f;
+        for (int j = 0; j < 32; ++j) am = fmaxf(am, fabsf(x[32 * b + j]));
+        d[b] = am / 127.0f;
+        for (int j = 0; j < 32; ++j) q[32 * b + j] = (int8_t)(am > 0.0f ? (int)nearbyintf(x[32 * b + j] / d[b]) : 0);
+    }
+}
+/* One row (core.hpp:66-87 lane<> + sub_dot<>, expert_check.cpp:50-55): lane
+ * l of 32 takes sub-blocks l, l + 32, ...: dot = (d * 0.125) * float(s0 * a +
+ * s1 * b) (a, b: the integer dots of the two 16-value halves), acc = fma(xd,
+ * dot, acc); then lane[l] = old[l] + old[l ^ o] for o = 16, 8, 4, 2, 1, and
+ * lane 0 + 0. */
+float orc_row32(int t, const uint8_t* row, int k, const int8_t* xq, const float* xd) {
+    float lane[32];
+    const int bb = orc_block_bytes(t);
+    for (int l = 0; l < 32; ++l) {
+        float acc = 0.0f;
+        for (int kb = l; kb < k / 32; kb += 32) {
+            const uint8_t* blk = row + (size_t)(kb / 8) * bb;
+            int val[32], sc[2], a = 0, b = 0;
+            p32_decode(t, blk, kb & 7, val, sc);
+            for (int j = 0; j < 16; ++j) { a += val[j] * xq[32 * kb + j]; b += val[16 + j] * xq[32 * kb + 16 + j]; }
+            const float dot = p32_scale(t, blk) * (float)(sc[0] * a + sc[1] * b);
+            acc = fmaf(xd[kb], dot, acc);
+        }
+        lane[l] = acc;
+    }
+    for (int o = 16; o; o >>= 1) {
+        float old[32];
+        memcpy(old, lane, sizeof old);
+        for (int l = 0; l < 32; ++l) lane[l] = old[l] + old[l ^ o];
+    }
+    return 1.0f * lane[0] + 0.0f;
+}
+void orc_matvec32(int t, const uint8_t* w, int n, int k, const int8_t* xq, const float* xd, float* y) {
+    const size_t rb = (size_t)(k / 256) * orc_block_bytes(t);
+    for (int r = 0; r < n; ++r) y[r] = orc_row32(t, w + (size_t)r * rb, k, xq, xd);
+}
+/* The per32 expert chain: Q32(x), gate and up rows, SwiGLU (core.hpp:88, the
+ * same form as q8k_core.hpp:92-95), Q32(h), down rows. g, u, h may be NULL. */
+void orc_expert32(const int types[3], const uint8_t* gate, const uint8_t* up, const uint8_t* down, int dim, int ff,
+                  const float* x, float* y, float* g, float* u, float* h) {
+    int8_t* q = (int8_t*)malloc((size_t)(dim > ff ? dim : ff));
+    float* d = (float*)malloc(sizeof(float) * (size_t)((dim > ff ? dim : ff) / 32));
+    float* gg = (float*)malloc(sizeof(float) * (size_t)ff * 3);
+    float *uu = gg + ff, *hh = gg + 2 * ff;
+    orc_quant32(x, dim, q, d);
+    orc_matvec32(types[0], gate, ff, dim, q, d, gg);
+    orc_matvec32(types[1], up, ff, dim, q, d, uu);
+    for (int i = 0; i < ff; ++i) hh[i] = orc_swiglu(gg[i], uu[i], 0.0f);
+    orc_quant32(hh, ff, q, d);
+    orc_matvec32(types[2], down, dim, ff, q, d, y);
+    if (g) memcpy(g, gg, sizeof(float) * (size_t)ff);
+    if (u) memcpy(u, uu, sizeof(float) * (size_t)ff);
+    if (h) memcpy(h, hh, sizeof(float) * (size_t)ff);
+    free(q); free(d); free(gg);
 }
 
 /* q8k_core.hpp:92-95 */

@@ -10,7 +10,9 @@
  *   sycl/stage/wiring/q8k_core.hpp:17-95   half, nearest, quant_block,
  *                                           integer_lane, scale, dot_lane,
  *                                           hsum, dot, swiglu
- *   sycl/moe/core.hpp:67,78-105              per-32 decode (brute-force check)
+ *   sycl/moe/core.hpp:66-105                 per-32 decode (brute-force check) and
+ *                                           the per32 row dot of the production
+ *                                           HIP lane (with hip_experts.hip:17-39)
  *   warm/runtime.cpp:183-188                 fixed-order combine
  *   sycl/route/route.cpp:15-37               router: sqrt(softplus) scores,
  *                                           biased top-k, normalized weights
@@ -67,6 +69,16 @@ void orc_combine(const int32_t* ids, const float* w, int k, const float* rows, i
 
 /* Generator restated: one AoS block, and one whole matrix (n x k). */
 uint64_t orc_gen_key(uint64_t seed, uint32_t layer, uint32_t expert, uint32_t role);
+/* per32 arithmetic of the reference's production HIP lane (hip_experts.hip:
+ * 17-39, sycl/moe/core.hpp:66-88, warm/expert_check.cpp:44-55): activation
+ * blocks of 32 (q int8, one f32 scale each), per-sub-block float dots summed by
+ * 32 strided lanes and a butterfly. */
+void orc_quant32(const float* x, int k, int8_t* q, float* d);
+float orc_row32(int type, const uint8_t* row, int k, const int8_t* xq, const float* xd);
+void orc_matvec32(int type, const uint8_t* w, int n, int k, const int8_t* xq, const float* xd, float* y);
+void orc_expert32(const int types[3], const uint8_t* gate, const uint8_t* up, const uint8_t* down, int dim, int ff,
+                  const float* x, float* y, float* g, float* u, float* h);
+
 /* Router of route.cpp:15-37 (route_cpu) for T tokens: logits T x stride (the
  * first n used), bias n (NULL = zeros); ids / w: T x k. */
 void orc_route(const float* logits, int stride, const float* bias, int n, int T, int k, float scale, int32_t* ids,

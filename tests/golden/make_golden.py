@@ -105,6 +105,17 @@ def main():
         out[f"route{i}_logits"], out[f"route{i}_bias"] = lg, b
         out[f"route{i}_k_scale"] = np.array([k, scale], np.float32)
         out[f"route{i}_ids"], out[f"route{i}_w"] = ids, w
+    # per32 rows (sycl/moe/core.hpp lane<> + the expert_check.cpp:50-55 butterfly):
+    # 4 rows per type at k = 1024 and 4096 against per-32 quantized N(0,1) activations.
+    from oracle.oracle import Oracle   # the per-32 quantizer has no CPU reference function to call
+    orc = Oracle()
+    for t in (16, 17, 29):
+        for k in (1024, 4096):
+            x = rng.standard_normal(k).astype(np.float32)
+            q, d = orc.quant32(x)
+            rows = orc.gen_matrix(t, 0x32, 0, 0, 0, 4, k).reshape(4, -1)
+            out[f"row32_{t}_{k}_q"], out[f"row32_{t}_{k}_d"], out[f"row32_{t}_{k}_rows"] = q, d, rows
+            out[f"row32_{t}_{k}_y"] = np.array([ref.row32(t, rows[r], k, q, d) for r in range(4)], np.float32)
     np.savez_compressed(OUT, **out)
     print("wrote", OUT, sum(v.nbytes for v in out.values()), "bytes")
 

@@ -250,3 +250,50 @@ def test_route_independent_forms(orc, rng):
     # above 20 the score is sqrt(l) itself
     ids, w = orc.route(np.array([[30.0, 25.0]], np.float32), 2)
     np.testing.assert_allclose(w[0], np.sqrt([30.0, 25.0]) / np.sqrt([30.0, 25.0]).sum(), rtol=1e-6)
+
+
+# ---- per32 arithmetic (the production HIP lane) -------------------------------
+def test_quant32_closed_forms(orc, rng):
+    x = np.zeros(96, np.float32)
+    x[40] = -3.5                                   # one-hot in block 1
+    x[64:96] = np.arange(32, dtype=np.float32) - 10.5   # ramp with .5 fractions in block 2
+    q, d = orc.quant32(x)
+    assert (q[:32] == 0).all() and d[0] == 0.0
+    assert q[40] == -127 and np.float32(d[1]) == np.float32(3.5) / np.float32(127.0)
+    assert (q[32:40] == 0).all() and (q[41:64] == 0).all()
+    want = np.rint((x[64:96] / d[2]).astype(np.float32)).astype(np.int8)   # np.rint: half to even
+    assert np.array_equal(q[64:96], want) and abs(q[64:96]).max() == 127
+    x = (rng.standard_normal(32 * 64) * rng.choice([1e-3, 1.0, 1e3])).astype(np.float32)
+    q, d = orc.quant32(x)
+    err = np.abs(x - q.astype(np.float64) * np.repeat(d, 32))
+    assert (err <= np.repeat(d, 32) * 0.5000001).all()
+
+
+def test_row32_golden(orc):
+    for t in (16, 17, 29):
+        for k in (1024, 4096):
+            q, d, rows = GOLD[f"row32_{t}_{k}_q"], GOLD[f"row32_{t}_{k}_d"], GOLD[f"row32_{t}_{k}_rows"]
+            got = np.array([orc.row32(t, rows[r], k, q, d) for r in range(4)], np.float32)
+            assert np.array_equal(got.view(np.uint32), GOLD[f"row32_{t}_{k}_y"].view(np.uint32)), (t, k)
+
+
+@pytest.mark.parametrize("t", [16, 17, 29])
+def test_row32_vs_reference_and_float64(orc, ref, t, rng):
+    for k in (256, 3072, 4096):
+        x = rng.standard_normal(k).astype(np.float32)
+        q, d = orc.quant32(x)
+        rows = orc.gen_matrix(t, 77, 1, 2, 0, 6, k).reshape(6, -1)
+        for r in range(6):
+            y = orc.row32(t, rows[r], k, q, d)
+            assert np.float32(y).view(np.uint32) == np.float32(ref.row32(t, rows[r], k, q, d)).view(np.uint32)
+        # independent of the float order: a float64 sum over the reference's own
+        # per-32 decoder (values, odd half scales, d / 8)
+        w = orc.matvec32(t, rows.reshape(-1), 6, k, q, d)
+        for r in range(6):
+            tot = 0.0
+            for kb in range(k // 32):
+                vals, sc, d8 = ref.decode(t, rows[r], kb)
+                qq = q[32 * kb:32 * kb + 32].astype(np.int64)
+                i = sc[0] * int(np.dot(vals[:16], qq[:16])) + sc[1] * int(np.dot(vals[16:], qq[16:]))
+                tot += float(d[kb]) * float(d8) * i
+            assert abs(w[r] - tot) <= 2e-5 * (abs(tot) + 1e-3), (r, w[r], tot)

@@ -167,6 +167,9 @@ def main():
     ap.add_argument("--device-route", action="store_true",
                     help="configs 1, 4: route each step on the GPU from N(0,1) logits (route.cpp router: "
                          "sqrt-softplus scores, top-6, normalized weights) inside the timed region")
+    ap.add_argument("--per32", action="store_true",
+                    help="configs 0-2: the per32 mode (the reference's production HIP lane arithmetic) "
+                         "instead of the Q8_K chain")
     ap.add_argument("--routes", type=int, default=512)
     ap.add_argument("--cpu-layers", type=int, default=0)
     ap.add_argument("--cpu-threads", type=int, default=0)
@@ -177,6 +180,9 @@ def main():
               "the routed-expert path runs on a single MI355X holding the whole bank", file=sys.stderr)
         sys.exit(2)
     cfg = args.config
+    if args.per32 and (cfg > 2 or args.device_route):
+        print("bench.py: --per32 applies to configs 0-2 without --device-route", file=sys.stderr)
+        sys.exit(2)
     L = N_LAYERS_3 if cfg == 3 else 1
     TOK = args.tokens if cfg == 4 else 1
     steps = args.steps or {3: 50, 4: 50}.get(cfg, 2000)
@@ -249,6 +255,7 @@ def main():
         d_y = torch.zeros(DIM, dtype=torch.float32, device="cuda")             # config 3: a layer's raw output
         d_out = torch.zeros((n_r, TOK, DIM) if cfg == 4 else (n_r, DIM), dtype=torch.float32, device="cuda")
         d_logits = torch.from_numpy(logits).cuda() if droute else None
+        d_y32 = torch.zeros((K, DIM), dtype=torch.float32, device="cuda") if args.per32 else None
     torch.cuda.synchronize()
 
     def step(i):
@@ -261,6 +268,9 @@ def main():
             return
         if cfg == 4:
             lane.grouped_forward_async(0, d_ids[r], d_w[r], d_x[r], d_out[r], stream=sp)
+            return
+        if args.per32:
+            lane.layer_forward_per32_async(0, d_ids[r, 0], d_x[r], d_y32, w=d_w[r, 0], out=d_out[r], stream=sp)
             return
         if cfg != 3:
             lane.layer_forward_async(0, d_ids[r, 0], d_w[r, 0], d_x[r], d_out[r], stream=sp)
@@ -298,10 +308,12 @@ def main():
     kernel = {0: "xl::dev::stream_kernel (single-launch layer)", 1: "xl::dev::stream_kernel (single-launch layer)",
               4: "grouped path (bucket, Q8_K, gu_kernel, Q8_K, dn_kernel, combine: 6 launches per step)"}.get(
         cfg, "xl::dev::layer3_kernel (all-types single-launch layer)")
-    traffic = measured_traffic() if cfg == 1 else None
+    if args.per32:
+        kernel = "per32 chain (quant32, mv32 gate+up, swiglu32, quant32, mv32 down, combine: 6 launches per step)"
+    traffic = measured_traffic() if cfg == 1 and not args.per32 else None
 
     cpu = None
-    if not args.no_cpu:
+    if not args.no_cpu and not args.per32:   # the CPU baseline times the Q8_K chain
         threads = args.cpu_threads or min(16, os.cpu_count() or 1)
         cpu_layers = args.cpu_layers or {0: 1500, 1: 500, 2: 500, 3: 500, 4: 500}[cfg]
         cpu = cpu_baseline(cpu_layers, threads, config=1 if cfg == 4 else cfg)
@@ -328,7 +340,8 @@ def main():
         "hbm_frac": round(gbs / HBM_PEAK_GBS, 4),
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "int8",
         "data": "synthetic (seeded IQ blocks generated on device, N(0,1) activations and router logits)",
-        "config": {"workload": workloads[cfg] + ("; routed on the GPU each step (route.cpp router)" if droute else ""),
+        "config": {"workload": workloads[cfg] + ("; routed on the GPU each step (route.cpp router)" if droute else "")
+                    + ("; per32 mode (per-32 int8 activations, hip_experts.hip arithmetic)" if args.per32 else ""),
                    "layers_per_step": L, "tokens_per_step": TOK,
                    "bytes_per_step": int(round(bytes_per_step)), "routes": n_r},
         "roofline": {"bound": "hbm", "kernel": kernel,

@@ -298,6 +298,7 @@ void enqueue_layer(xl_context* ctx, int32_t layer, const int32_t* d_ids, const f
         a.descs = descs; a.ids = d_ids; a.w = d_w; a.x = d_x; a.shared = d_shared; a.out = d_out;
         a.k = k; a.n_experts = E; a.dim = dim; a.ff = ff;
         a.htag = ctx->htag; a.hqtag = ctx->hqtag; a.hdtag = ctx->hdtag; a.ctl = ctx->ctl; a.err = ctx->err_flag;
+        a.lim = ctx->cfg.swiglu_limit;
         a.tables = ctx->tables;
         a.hbuf = ctx->hbuf;
         if (ctx->prof.on && ctx->prof.calls <= ctx->prof.max_calls) {
@@ -334,6 +335,7 @@ void enqueue_layer(xl_context* ctx, int32_t layer, const int32_t* d_ids, const f
         a.k = k; a.n_experts = E; a.dim = dim; a.ff = ff;
         a.xq = ctx->xq; a.xd = ctx->xd; a.h = ctx->h; a.hq = ctx->hq; a.hd = ctx->hd; a.y = ctx->y;
         a.sync = ctx->sync; a.err = ctx->err_flag; a.codes = ctx->codes;
+        a.lim = ctx->cfg.swiglu_limit;
         const hipError_t e = xl::dev::launch_layer_fused(a, gu_mask | dn_mask, ctx->cus, s);
         if (e == hipSuccess) {
             mark("layer");
@@ -345,7 +347,7 @@ void enqueue_layer(xl_context* ctx, int32_t layer, const int32_t* d_ids, const f
     hip_check(xl::dev::launch_q8k(d_x, dim / 256, ctx->xq, ctx->xd, nullptr, ctx->err_flag, s), "Q8_K(x) launch");
     mark("q8k_x");
     hip_check(xl::dev::launch_gate_up(descs, d_ids, k, E, dim, ff, ctx->xq, ctx->xd, ctx->codes, ctx->h, g_dbg, u_dbg,
-                                      ctx->err_flag, ctx->grid_gu, gu_mask, s),
+                                      ctx->err_flag, ctx->grid_gu, gu_mask, ctx->cfg.swiglu_limit, s),
               "gate/up launch");
     mark("gate_up");
     hip_check(xl::dev::launch_q8k(ctx->h, k * ff / 256, ctx->hq, ctx->hd, nullptr, ctx->err_flag, s), "Q8_K(h) launch");
@@ -379,7 +381,7 @@ void enqueue_per32(xl_context* ctx, int32_t layer, const int32_t* d_ids, const f
                                    size_t(ff), ctx->tables, ctx->err_flag, s),
               "per32 gate/up launch");
     mark("gate_up32");
-    hip_check(xl::dev::launch_swiglu32(ctx->g, ctx->u, k * ff, ctx->h, s), "SwiGLU launch");
+    hip_check(xl::dev::launch_swiglu32(ctx->g, ctx->u, k * ff, ctx->cfg.swiglu_limit, ctx->h, s), "SwiGLU launch");
     mark("swiglu");
     hip_check(xl::dev::launch_quant32(ctx->h, k, ff, ctx->hq, hd, ctx->err_flag, s), "quant32(h) launch");
     mark("quant32_h");
@@ -414,6 +416,7 @@ int32_t xl_open(uint32_t abi_version, const xl_config* cfg, xl_context** out, xl
         need(cfg->n_experts >= 1 && cfg->n_experts <= 65536, XL_E_ARG, "n_experts outside 1..65536");
         need(cfg->max_picks >= 1 && cfg->max_picks <= 16, XL_E_ARG, "max_picks outside 1..16");
         need(cfg->max_tokens >= 0 && cfg->max_tokens <= 65536, XL_E_ARG, "max_tokens outside 0..65536");
+        need(std::isfinite(cfg->swiglu_limit), XL_E_ARG, "swiglu_limit not finite");
         int ndev = 0;
         hip_check(hipGetDeviceCount(&ndev), "hipGetDeviceCount");
         need(cfg->device >= 0 && cfg->device < ndev, XL_E_ARG, "device ordinal out of range");
@@ -680,6 +683,14 @@ struct Pack {
         if (*end || v < 0 || v > (1L << 30)) fail(XL_E_ARG, "pack ds4.txt: %s is not a count", key);
         return int(v);
     }
+    double real(const char* key, double dflt) const {
+        const auto it = kv.find(key);
+        if (it == kv.end()) return dflt;
+        char* end = nullptr;
+        const double v = std::strtod(it->second.c_str(), &end);
+        if (*end || !std::isfinite(v)) fail(XL_E_ARG, "pack ds4.txt: %s is not a finite number", key);
+        return v;
+    }
 };
 
 std::string slurp(const std::string& path) {
@@ -760,6 +771,7 @@ int32_t xl_pack_meta_get(const char* pack_dir, xl_pack_meta* out, xl_error* err)
         out->n_layers = p.num("num_hidden_layers");
         out->n_experts = p.num("n_routed_experts");
         out->top_k = p.num("num_experts_per_tok");
+        out->swiglu_limit = float(p.real("swiglu_limit", 0.0));
     });
 }
 
@@ -896,6 +908,7 @@ void enqueue_grouped(xl_context* ctx, int32_t layer, int32_t T, int32_t k, const
         a.xq = g.xq; a.xd = g.xd; a.order = g.order; a.tasks = g.tasks; a.n_tasks = g.n_tasks;
         a.h = g.h; a.hq = g.hq; a.hd = g.hd; a.y = g.y;
         a.tables = ctx->tables; a.err = ctx->err_flag;
+        a.lim = ctx->cfg.swiglu_limit;
         const hipError_t e = xl::dev::launch_grouped(a, ctx->cus, s);
         if (e == hipSuccess) {
             mark("grouped");

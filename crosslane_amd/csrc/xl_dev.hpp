@@ -115,8 +115,18 @@ __device__ __forceinline__ Q8Lane q8k_lane(const float v[4], int lane) {
     return r;
 }
 
-__device__ __forceinline__ float silu_mul3(float g, float u) {
-    // q8k_core.hpp:92-95 with limit 0: (g / (1 + exp(-g))) * u
+// SwiGLU limit (q8k_core.hpp:92-93, the pack's swiglu_limit): with lim > 0,
+// g = min(g, lim) and u = min(max(u, -lim), lim) before the product.
+__device__ __forceinline__ void swiglu_clamp(float& g, float& u, float lim) {
+    if (lim > 0.0f) {
+        g = fminf(g, lim);
+        u = fminf(fmaxf(u, -lim), lim);
+    }
+}
+
+__device__ __forceinline__ float silu_mul3(float g, float u, float lim) {
+    // q8k_core.hpp:92-95: (g / (1 + exp(-g))) * u after the limit
+    swiglu_clamp(g, u, lim);
     const float e = expf(-g);
     return __fmul_rn(__fdiv_rn(g, __fadd_rn(1.0f, e)), u);
 }

@@ -379,7 +379,7 @@ __global__ __launch_bounds__(NW * 64, 1) void gu_kernel(GroupArgs a) {
 #pragma unroll
         for (int r = 0; r < 4; ++r)
             if (po[r] >= 0)
-                a.h[size_t(po[r]) * a.ff + row] = silu_mul3(__fmul_rn(0.125f, accg[r]), __fmul_rn(0.125f, accu[r]));
+                a.h[size_t(po[r]) * a.ff + row] = silu_mul3(__fmul_rn(0.125f, accg[r]), __fmul_rn(0.125f, accu[r]), a.lim);
     }
     if (sunk == 0x9e3779b9u && lane == 64) a.h[0] = 0.0f;   // never true (lane < 64): keeps the touches
 }

@@ -57,6 +57,7 @@ struct LayerArgs {
     float* y;                   // k * dim
     uint32_t* sync;             // kSyncWords zeroed counters; the kernel re-zeroes them on exit
     int* err;
+    float lim;                  // SwiGLU limit (> 0: g = min(g, lim), u = clamp(u, -lim, lim))
     const uint16_t* codes;
     int need;                   // codebooks to expand (filled in by the launcher)
     int per_g, per_d;           // row slots per wave (filled in by the launcher)
@@ -77,6 +78,7 @@ struct Layer3Args {
     uint64_t* hdtag;            // k * ff/256 words: (Q8_K(h) block scale bits, epoch << 32)
     uint32_t* ctl;              // [0] epoch of the last launch, [1] arrival counter (zero between launches)
     int* err;
+    float lim;                  // SwiGLU limit (> 0: g = min(g, lim), u = clamp(u, -lim, lim))
     const uint64_t* tables;     // expanded codebooks (kLayer3TableBytes), see kG_* in xl_layer.hip
     // Regular layers (all experts with the same three block types, each
     // expert's matrices consecutive in the layer slab): matrix (id, role)
@@ -110,6 +112,7 @@ struct GroupArgs {
     float* y;                   // P * dim
     const uint64_t* tables;     // expanded codebooks (kLayer3TableBytes)
     int* err;
+    float lim;                  // SwiGLU limit (> 0: g = min(g, lim), u = clamp(u, -lim, lim))
 };
 constexpr int kGroupMaxExperts = 8192;
 constexpr int kRouteMaxExperts = 4096;   // router: scores and keys of one token in LDS   // experts per layer the bucket kernel counts in LDS
@@ -139,7 +142,7 @@ hipError_t launch_matvec(const MatRef& m, int n, int k, const int8_t* aq, const 
 // Gate/up + SwiGLU for k picks: h[i*ff + r] = silu(gate_i . x) * (up_i . x).
 hipError_t launch_gate_up(const ExpertDesc* descs, const int32_t* ids, int k, int n_experts, int dim, int ff,
                           const int8_t* xq, const float* xd, const uint16_t* codes, float* h, float* g_dbg,
-                          float* u_dbg, int* err, int target_wgs, int type_mask, hipStream_t s);
+                          float* u_dbg, int* err, int target_wgs, int type_mask, float lim, hipStream_t s);
 // Down for k picks: y[i*dim + r] = down_i . Q8_K(h_i).
 hipError_t launch_down(const ExpertDesc* descs, const int32_t* ids, int k, int n_experts, int dim, int ff,
                        const int8_t* hq, const float* hd, const uint16_t* codes, float* y, int* err, int target_wgs,
@@ -163,8 +166,8 @@ hipError_t launch_mv32(const ExpertDesc* descs, const int32_t* ids, const MatRef
                        int role0, int roles, int n, int k, const int8_t* q, size_t q_stride, const float* d,
                        size_t d_stride, float* y0, float* y1, size_t y_stride, const uint64_t* tables, int* err,
                        hipStream_t s);
-// h = g / (1 + exp(-g)) * u over n values.
-hipError_t launch_swiglu32(const float* g, const float* u, int n, float* h, hipStream_t s);
+// h = g / (1 + exp(-g)) * u over n values (lim > 0: g, u clamped first).
+hipError_t launch_swiglu32(const float* g, const float* u, int n, float lim, float* h, hipStream_t s);
 // Seeded generation of one planar matrix (role 0 gate, 1 up, 2 down).
 hipError_t launch_generate(uint8_t* base, int type, int n, int k, uint64_t seed, uint32_t layer, uint32_t expert,
                            uint32_t role, hipStream_t s);

@@ -113,8 +113,13 @@ __global__ __launch_bounds__(256) void q8k_kernel(const float* __restrict__ x, i
               threadIdx.x & 63);
 }
 
-__device__ __forceinline__ float silu_mul(float g, float u) {
-    // q8k_core.hpp:92-95 with limit 0: (g / (1 + exp(-g))) * u
+__device__ __forceinline__ float silu_mul(float g, float u, float lim) {
+    // q8k_core.hpp:92-95: the limit (lim > 0: g = min(g, lim), u = clamp(u,
+    // -lim, lim)), then (g / (1 + exp(-g))) * u
+    if (lim > 0.0f) {
+        g = fminf(g, lim);
+        u = fminf(fmaxf(u, -lim), lim);
+    }
     const float e = expf(-g);
     return __fmul_rn(__fdiv_rn(g, __fadd_rn(1.0f, e)), u);
 }
@@ -157,7 +162,7 @@ __global__ __launch_bounds__(256) void gate_up_kernel(const ExpertDesc* __restri
                                                       const int8_t* __restrict__ xq, const float* __restrict__ xd,
                                                       const uint16_t* __restrict__ codes, int need,
                                                       float* __restrict__ h, float* __restrict__ g_dbg,
-                                                      float* __restrict__ u_dbg, int* __restrict__ err) {
+                                                      float* __restrict__ u_dbg, int* __restrict__ err, float lim) {
     extern __shared__ uint8_t lds[];
     constexpr int RPW = 64 / LPR;
     const int lane = threadIdx.x & 63, grp = lane / LPR, l = lane % LPR;
@@ -192,7 +197,7 @@ __global__ __launch_bounds__(256) void gate_up_kernel(const ExpertDesc* __restri
             const float g = dot_raw<LPR, PPL, false>(rg[u], type, row, D.m[0].nb, l, A, lds, nullptr, true);
             const float v = dot_raw<LPR, PPL, false>(ru[u], type, row, D.m[1].nb, l, A, lds, nullptr, true);
             if (l == 0) {
-                h[size_t(i) * ff + row] = silu_mul(g, v);
+                h[size_t(i) * ff + row] = silu_mul(g, v, lim);
                 if (g_dbg) g_dbg[size_t(i) * ff + row] = g;
                 if (u_dbg) u_dbg[size_t(i) * ff + row] = v;
             }
@@ -493,7 +498,7 @@ __global__ __launch_bounds__(256) void layer_kernel(LayerArgs a) {
                     const int type = D->m[0].type;
                     const float g = dot_raw<LG, PG, false>(rg[u], type, row, D->m[0].nb, lG, A, lds, nullptr, true);
                     const float v = dot_raw<LG, PG, false>(ru[u], type, row, D->m[1].nb, lG, A, lds, nullptr, true);
-                    if (lG == 0) coh_stf(a.h + size_t(i) * a.ff + row, silu_mul(g, v));
+                    if (lG == 0) coh_stf(a.h + size_t(i) * a.ff + row, silu_mul(g, v, a.lim));
                 }
         }
         // publish rows per pick (a wave's range spans at most a few picks)
@@ -666,7 +671,7 @@ static int wg_per_pick(int slots, int umax, int k, int target_wgs) {
 
 hipError_t launch_gate_up(const ExpertDesc* descs, const int32_t* ids, int k, int n_experts, int dim, int ff,
                           const int8_t* xq, const float* xd, const uint16_t* codes, float* h, float* g_dbg,
-                          float* u_dbg, int* err, int target_wgs, int type_mask, hipStream_t s) {
+                          float* u_dbg, int* err, int target_wgs, int type_mask, float lim, hipStream_t s) {
     int lpr, ppl;
     if (!row_shape(dim, lpr, ppl) || k <= 0) return hipErrorInvalidValue;
     constexpr int U = 4;
@@ -676,7 +681,7 @@ hipError_t launch_gate_up(const ExpertDesc* descs, const int32_t* ids, int k, in
 #define XL_GU(L, P)                                                                                                   \
     if (lpr == L && ppl == P) {                                                                                       \
         hipLaunchKernelGGL((gate_up_kernel<L, P, U>), dim3(k * wgpp), dim3(256), lds, s, descs, ids, n_experts, ff,   \
-                           wgpp, xq, xd, codes, need, h, g_dbg, u_dbg, err);                                          \
+                           wgpp, xq, xd, codes, need, h, g_dbg, u_dbg, err, lim);                                     \
         return hipGetLastError();                                                                                     \
     }
     XL_SHAPES(XL_GU)

@@ -439,7 +439,7 @@ __global__ __launch_bounds__(NW * 64, 1) void layer3_kernel(Layer3Args a) {
                 if (gid[j] >= 0) {
                     const float g = gsum<LG>(row_sum<GUT, TM, PG>(lds, L, gm[j].type, rg[j % WIN], A, lG, LG));
                     const float u = gsum<LG>(row_sum<GUT, TM, PG>(lds, L, gm[j].type, ru[j % WIN], A, lG, LG));
-                    hv = silu_mul3(__fmul_rn(0.125f, g), __fmul_rn(0.125f, u));
+                    hv = silu_mul3(__fmul_rn(0.125f, g), __fmul_rn(0.125f, u), a.lim);
                 }
                 if (lG == LG - 1) coh_st64(a.htag + size_t(i) * ff + row, tag_word(__float_as_uint(hv), epoch));
                 mark(8 + j);

@@ -10,13 +10,15 @@
 //                   float(s0 * a + s1 * b) (a, b: the integer dots of the two
 //                   16-weight halves, s: odd sub-scales), acc = fma(xd, dot,
 //                   acc); then a 16-8-4-2-1 butterfly and lane 0 + 0
-//   swiglu32_kernel g / (1 + exp(-g)) * u (the device's expf)
+//   swiglu32_kernel g / (1 + exp(-g)) * u (the device's expf; g and u clamped
+//                   first when the SwiGLU limit is set)
 //
 // The bank's planar blocks are decoded directly (xl_format.hpp layout); the
 // codebooks come from the context's expanded tables. Build with
 // -ffp-contract=off: every float operation above is a separate IEEE rounding.
 #include <hip/hip_runtime.h>
 
+#include "xl_dev.hpp"
 #include "xl_format.hpp"
 #include "xl_internal.hpp"
 
@@ -25,11 +27,9 @@ namespace {
 
 constexpr int kTabSgn = 0, kTabXXS = 256, kTabXS = 512, kTabIQ1 = 1024;   // u64 row offsets (layer_tables)
 
-__device__ __forceinline__ int sdot4(uint32_t a, uint32_t b, int c) { return __builtin_amdgcn_sdot4(int(a), int(b), c, false); }
-__device__ __forceinline__ uint32_t xad(uint32_t a, uint32_t b, uint32_t c) { return (a ^ b) + c; }
-__device__ __forceinline__ float h2f(uint16_t h) { return float(__builtin_bit_cast(_Float16, h)); }
-__device__ __forceinline__ uint16_t rd16(const uint8_t* p) { return *reinterpret_cast<const uint16_t*>(p); }
-__device__ __forceinline__ uint32_t rd32(const uint8_t* p) { return *reinterpret_cast<const uint32_t*>(p); }
+// Aligned loads: p is 2- (ld16) or 4-byte (ld32) aligned.
+__device__ __forceinline__ uint16_t ld16(const uint8_t* p) { return *reinterpret_cast<const uint16_t*>(p); }
+__device__ __forceinline__ uint32_t ld32(const uint8_t* p) { return *reinterpret_cast<const uint32_t*>(p); }
 
 // Sub-block kb (32 weights) of row `row`: the two half integer dots against the
 // 8 activation words q, the odd half scales and the block's d * 0.125.
@@ -44,14 +44,14 @@ __device__ __forceinline__ Sub32 sub32(const MatRef& m, int row, int kb, const u
     int half[2] = {0, 0};
     if (m.type == kIQ2_XXS || m.type == kIQ2_XS) {
         const uint8_t* p = m.base + blk * 64 + 8 * ib;
-        const uint32_t w0 = rd32(p), w1 = rd32(p + 4);
+        const uint32_t w0 = ld32(p), w1 = ld32(p + 4);
         uint16_t d16;
         if (m.type == kIQ2_XXS) {   // four grid bytes; aux bytes sign7 | (scale bit) << 7
             int s = 0;
 #pragma unroll
             for (int l = 0; l < 4; ++l) s |= int((w1 >> (8 * l + 7)) & 1u) << l;
             r.s0 = r.s1 = 2 * s + 1;
-            d16 = rd16(m.base + m.off1 + blk * 2);
+            d16 = ld16(m.base + m.off1 + blk * 2);
 #pragma unroll
             for (int l = 0; l < 4; ++l) {
                 const uint64_t g = tab[kTabXXS + ((w0 >> (8 * l)) & 255u)];
@@ -64,7 +64,7 @@ __device__ __forceinline__ Sub32 sub32(const MatRef& m, int row, int kb, const u
             const uint32_t sb = m.base[m.off1 + blk * 8 + ib];
             r.s0 = 2 * int(sb & 15u) + 1;
             r.s1 = 2 * int(sb >> 4) + 1;
-            d16 = rd16(m.base + m.off2 + blk * 2);
+            d16 = ld16(m.base + m.off2 + blk * 2);
 #pragma unroll
             for (int l = 0; l < 4; ++l) {
                 const uint32_t c = ((l < 2 ? w0 : w1) >> (16 * (l & 1))) & 0xffffu;
@@ -80,11 +80,11 @@ __device__ __forceinline__ Sub32 sub32(const MatRef& m, int row, int kb, const u
         const uint8_t* qs = m.base + blk * 32 + 4 * ib;
         const uint8_t* qh = m.base + m.off1 + blk * 16 + 2 * ib;
         const uint8_t* sc = m.base + m.off2 + blk * 8;
-        const uint32_t w = rd16(sc + 2 * (ib >> 1));
+        const uint32_t w = ld16(sc + 2 * (ib >> 1));
         r.s0 = 2 * int((w >> (6 * (ib & 1))) & 7u) + 1;
         r.s1 = 2 * int((w >> (6 * (ib & 1) + 3)) & 7u) + 1;
-        const uint16_t d16 = uint16_t((rd16(sc) >> 12) | ((rd16(sc + 2) >> 8) & 0xf0u) | ((rd16(sc + 4) >> 4) & 0xf00u) |
-                                      (rd16(sc + 6) & 0xf000u));
+        const uint16_t d16 = uint16_t((ld16(sc) >> 12) | ((ld16(sc + 2) >> 8) & 0xf0u) | ((ld16(sc + 4) >> 4) & 0xf00u) |
+                                      (ld16(sc + 6) & 0xf000u));
         r.d8 = __fmul_rn(h2f(d16), 0.125f);
 #pragma unroll
         for (int l = 0; l < 4; ++l) {
@@ -155,9 +155,9 @@ __global__ __launch_bounds__(256) void mv32_kernel(const ExpertDesc* __restrict_
 }
 
 __global__ __launch_bounds__(256) void swiglu32_kernel(const float* __restrict__ g, const float* __restrict__ u, int n,
-                                                       float* __restrict__ h) {
+                                                       float lim, float* __restrict__ h) {
     const int i = blockIdx.x * 256 + threadIdx.x;
-    if (i < n) h[i] = __fmul_rn(__fdiv_rn(g[i], __fadd_rn(1.0f, expf(-g[i]))), u[i]);
+    if (i < n) h[i] = silu_mul3(g[i], u[i], lim);
 }
 
 }  // namespace
@@ -179,8 +179,8 @@ hipError_t launch_mv32(const ExpertDesc* descs, const int32_t* ids, const MatRef
     return hipGetLastError();
 }
 
-hipError_t launch_swiglu32(const float* g, const float* u, int n, float* h, hipStream_t s) {
-    hipLaunchKernelGGL(swiglu32_kernel, dim3((n + 255) / 256), dim3(256), 0, s, g, u, n, h);
+hipError_t launch_swiglu32(const float* g, const float* u, int n, float lim, float* h, hipStream_t s) {
+    hipLaunchKernelGGL(swiglu32_kernel, dim3((n + 255) / 256), dim3(256), 0, s, g, u, n, lim, h);
     return hipGetLastError();
 }
 

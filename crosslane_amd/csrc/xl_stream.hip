@@ -113,7 +113,9 @@ __device__ __forceinline__ uint32_t neg_bytes(uint32_t x) {
 // h = silu(g) * u with the hardware exp2 and reciprocal (about 1 ulp each): h
 // only feeds Q8_K(h), and the layer output is held to a relative 1e-3, not to
 // the bits of the reference's expf. g -> -inf gives -0, g -> +inf gives g * u.
-__device__ __forceinline__ float silu_fast(float g, float u) {
+// The SwiGLU limit (lim > 0) clamps g and u first, as q8k_core.hpp:92-93.
+__device__ __forceinline__ float silu_fast(float g, float u, float lim) {
+    swiglu_clamp(g, u, lim);
     const float e = __builtin_amdgcn_exp2f(__fmul_rn(g, -1.4426950408889634f));
     return __fmul_rn(__fmul_rn(g, __builtin_amdgcn_rcpf(__fadd_rn(1.0f, e))), u);
 }
@@ -512,7 +514,7 @@ __global__ __launch_bounds__(NW * 64, 1) void stream_kernel(Layer3Args a) {
             bu = mine ? u : bu;
             hidx = mine ? hrow(j) + rG : hidx;
             if (b == kBatch - 1 || j == MG - 1) {
-                const float hv = silu_fast(__fmul_rn(0.125f, bg), __fmul_rn(0.125f, bu));
+                const float hv = silu_fast(__fmul_rn(0.125f, bg), __fmul_rn(0.125f, bu), a.lim);
                 const uint32_t hb = __float_as_uint(hv) == kSentinel ? kQNaN : __float_as_uint(hv);
                 if (lG >= LG - 1 - b && hidx >= 0)
                     __hip_atomic_store(reinterpret_cast<uint32_t*>(hcur) + hidx, hb, __ATOMIC_RELAXED,

@@ -23,7 +23,7 @@ import numpy as np
 
 IQ2_XXS, IQ2_XS, IQ1_M = 16, 17, 29
 BLOCK_BYTES = {IQ2_XXS: 66, IQ2_XS: 74, IQ1_M: 56}
-ABI_VERSION = 1
+ABI_VERSION = 2
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "libcrosslane.so")
 
@@ -41,7 +41,7 @@ class _Err(C.Structure):
 class _Config(C.Structure):
     _fields_ = [("struct_bytes", C.c_uint32), ("device", C.c_int32), ("dim", C.c_int32), ("ff", C.c_int32),
                 ("n_layers", C.c_int32), ("n_experts", C.c_int32), ("max_picks", C.c_int32),
-                ("max_tokens", C.c_int32)]
+                ("max_tokens", C.c_int32), ("swiglu_limit", C.c_float)]
 
 
 class _BankInfo(C.Structure):
@@ -59,7 +59,7 @@ _ErrP = C.POINTER(_Err)
 
 class _PackMeta(C.Structure):
     _fields_ = [("struct_bytes", C.c_uint32), ("dim", C.c_int32), ("ff", C.c_int32), ("n_layers", C.c_int32),
-                ("n_experts", C.c_int32), ("top_k", C.c_int32)]
+                ("n_experts", C.c_int32), ("top_k", C.c_int32), ("swiglu_limit", C.c_float)]
 
 
 _SIGNATURES = {
@@ -176,7 +176,7 @@ def codebook(which: int) -> np.ndarray:
 
 
 def pack_meta(pack_dir: str) -> dict:
-    """Shape of a weight pack (ds4.txt): dim, ff, n_layers, n_experts, top_k."""
+    """Shape of a weight pack (ds4.txt): dim, ff, n_layers, n_experts, top_k, swiglu_limit."""
     m = _PackMeta(C.sizeof(_PackMeta))
     err = _Err()
     _check(lib().xl_pack_meta_get(os.fsencode(pack_dir), C.byref(m), C.byref(err)), err)
@@ -197,9 +197,10 @@ class Lane:
     """One context: a resident bank of n_layers x n_experts experts on one GPU."""
 
     def __init__(self, dim: int, ff: int, n_layers: int, n_experts: int, types: np.ndarray,
-                 max_picks: int = 8, max_tokens: int = 0, device: int = 0):
+                 max_picks: int = 8, max_tokens: int = 0, device: int = 0, swiglu_limit: float = 0.0):
         L = lib()
-        cfg = _Config(C.sizeof(_Config), device, dim, ff, n_layers, n_experts, max_picks, max_tokens)
+        cfg = _Config(C.sizeof(_Config), device, dim, ff, n_layers, n_experts, max_picks, max_tokens,
+                      float(swiglu_limit))
         ctx = _P()
         err = _Err()
         _check(L.xl_open(ABI_VERSION, C.byref(cfg), C.byref(ctx), C.byref(err)), err)

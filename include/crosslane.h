@@ -23,7 +23,7 @@
 extern "C" {
 #endif
 
-#define XL_ABI_VERSION 1u
+#define XL_ABI_VERSION 2u
 
 enum {
     XL_OK = 0,
@@ -52,6 +52,9 @@ typedef struct xl_config {
     int32_t n_experts;     /* routed experts per layer */
     int32_t max_picks;     /* top-k bound, 1..16 (reference kPicks = 8, model_meta.hpp:18) */
     int32_t max_tokens;    /* grouped-path token bound (0 = grouped path unused) */
+    float swiglu_limit;    /* SwiGLU limit (model_meta.hpp:34 `lim`, the pack's swiglu_limit):
+                              > 0 clamps g to <= lim and u to [-lim, lim] before
+                              SiLU(g) * u (q8k_core.hpp:92-95); <= 0: no clamp */
 } xl_config;
 
 typedef struct xl_bank_info {
@@ -105,6 +108,7 @@ int32_t xl_contains(const xl_context* ctx, int32_t layer, int32_t expert);
 typedef struct xl_pack_meta {
     uint32_t struct_bytes; /* sizeof(xl_pack_meta) */
     int32_t dim, ff, n_layers, n_experts, top_k;
+    float swiglu_limit;    /* ds4.txt swiglu_limit, 0 when absent (pack_source.cpp:99) */
 } xl_pack_meta;
 int32_t xl_pack_meta_get(const char* pack_dir, xl_pack_meta* out, xl_error* err);
 int32_t xl_pack_types(const char* pack_dir, int32_t first_layer, int32_t n_layers, int32_t n_experts, int32_t* types,

@@ -51,7 +51,7 @@ class Oracle:
         L.orc_matvec.argtypes = [C.c_int, _u8p, C.c_int, C.c_int, _P, _f32p, C.c_int]
         L.orc_swiglu.argtypes = [C.c_float, C.c_float, C.c_float]
         L.orc_swiglu.restype = C.c_float
-        L.orc_expert.argtypes = [_i32p, _u8p, _u8p, _u8p, C.c_int, C.c_int, _f32p, _f32p, _P, _P, _P, C.c_int]
+        L.orc_expert.argtypes = [_i32p, _u8p, _u8p, _u8p, C.c_int, C.c_int, _f32p, _f32p, _P, _P, _P, C.c_int, C.c_float]
         L.orc_down_from_hidden.argtypes = [C.c_int, _u8p, C.c_int, C.c_int, _f32p, _f32p, C.c_int]
         L.orc_combine.argtypes = [_i32p, _f32p, C.c_int, _f32p, C.c_int, _P, _f32p]
         L.orc_route.argtypes = [_f32p, C.c_int, _P, C.c_int, C.c_int, C.c_int, C.c_float, _i32p, _f32p]
@@ -60,7 +60,7 @@ class Oracle:
         L.orc_row32.argtypes = [C.c_int, _u8p, C.c_int, _i8p, _f32p]
         L.orc_row32.restype = C.c_float
         L.orc_matvec32.argtypes = [C.c_int, _u8p, C.c_int, C.c_int, _i8p, _f32p, _f32p]
-        L.orc_expert32.argtypes = [_i32p, _u8p, _u8p, _u8p, C.c_int, C.c_int, _f32p, _f32p, _P, _P, _P]
+        L.orc_expert32.argtypes = [_i32p, _u8p, _u8p, _u8p, C.c_int, C.c_int, _f32p, _f32p, _P, _P, _P, C.c_float]
         L.orc_gen_key.argtypes = [C.c_uint64, C.c_uint32, C.c_uint32, C.c_uint32]
         L.orc_gen_key.restype = C.c_uint64
         L.orc_gen_block.argtypes = [C.c_int, C.c_uint64, C.c_uint64, _u8p]
@@ -106,12 +106,12 @@ class Oracle:
     def swiglu(self, g: float, u: float, limit: float = 0.0) -> float:
         return float(self.lib.orc_swiglu(g, u, limit))
 
-    def expert(self, types, gate, up, down, dim, ff, x, threads=8, intermediates=False):
+    def expert(self, types, gate, up, down, dim, ff, x, threads=8, intermediates=False, limit=0.0):
         y = np.zeros(dim, dtype=np.float32)
         g = np.zeros(ff, dtype=np.float32); u = np.zeros(ff, dtype=np.float32); h = np.zeros(ff, dtype=np.float32)
         self.lib.orc_expert(np.asarray(types, dtype=np.int32), gate.reshape(-1), up.reshape(-1), down.reshape(-1),
                             dim, ff, np.ascontiguousarray(x, dtype=np.float32), y,
-                            g.ctypes.data, u.ctypes.data, h.ctypes.data, threads)
+                            g.ctypes.data, u.ctypes.data, h.ctypes.data, threads, float(limit))
         return (y, g, u, h) if intermediates else y
 
     def down_from_hidden(self, t, down, dim, ff, h, threads=8):
@@ -145,12 +145,12 @@ class Oracle:
                               np.ascontiguousarray(q, dtype=np.int8), np.ascontiguousarray(d, dtype=np.float32), y)
         return y
 
-    def expert32(self, types, gate, up, down, dim, ff, x, intermediates=False):
+    def expert32(self, types, gate, up, down, dim, ff, x, intermediates=False, limit=0.0):
         y = np.zeros(dim, np.float32)
         g = np.zeros(ff, np.float32); u = np.zeros(ff, np.float32); h = np.zeros(ff, np.float32)
         self.lib.orc_expert32(np.asarray(types, dtype=np.int32), gate.reshape(-1), up.reshape(-1), down.reshape(-1), dim,
                               ff, np.ascontiguousarray(x, dtype=np.float32), y, g.ctypes.data, u.ctypes.data,
-                              h.ctypes.data)
+                              h.ctypes.data, float(limit))
         return (y, g, u, h) if intermediates else y
 
     def route(self, logits, k, scale=1.0, bias=None):
@@ -215,7 +215,7 @@ class Reference:
         L.ref_route.argtypes = [_f32p, C.c_int, _f32p, C.c_int, C.c_int, C.c_int, C.c_float, _i32p, _f32p]
         L.ref_row32.argtypes = [C.c_int, _u8p, C.c_int, np.ctypeslib.ndpointer(np.int8, flags="C_CONTIGUOUS"), _f32p]
         L.ref_row32.restype = C.c_float
-        L.ref_expert.argtypes = [_i32p, _u8p, _u8p, _u8p, C.c_int, C.c_int, _f32p, _f32p, C.c_int]
+        L.ref_expert.argtypes = [_i32p, _u8p, _u8p, _u8p, C.c_int, C.c_int, _f32p, _f32p, C.c_int, C.c_float]
 
     @staticmethod
     def available() -> bool:
@@ -254,10 +254,10 @@ class Reference:
         self.lib.ref_decode(t, np.ascontiguousarray(row), kb, q, s, C.byref(d))
         return q, s, d.value
 
-    def expert(self, types, gate, up, down, dim, ff, x, threads=8):
+    def expert(self, types, gate, up, down, dim, ff, x, threads=8, limit=0.0):
         y = np.zeros(dim, dtype=np.float32)
         self.lib.ref_expert(np.asarray(types, dtype=np.int32), gate.reshape(-1), up.reshape(-1), down.reshape(-1),
-                            dim, ff, np.ascontiguousarray(x, dtype=np.float32), y, threads)
+                            dim, ff, np.ascontiguousarray(x, dtype=np.float32), y, threads, float(limit))
         return y
 
     def route(self, logits, k, scale=1.0, bias=None):

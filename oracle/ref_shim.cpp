@@ -57,16 +57,16 @@ void ref_matvec(int t, const uint8_t* w, int n, int k, const void* a, float* y, 
     run(); for (auto& th : pool) th.join();
 }
 // One expert chain with the reference's functions: Q8_K(x), gate/up rows,
-// SwiGLU (limit 0), Q8_K(h), down rows (the CPU lane order, cpu_lane.cpp:157-168).
+// SwiGLU (with the limit), Q8_K(h), down rows (the CPU lane order, cpu_lane.cpp:157-168).
 void ref_expert(const int* types, const uint8_t* gate, const uint8_t* up, const uint8_t* down, int dim, int ff,
-                const float* x, float* y, int threads) {
+                const float* x, float* y, int threads, float lim) {
     std::vector<q::Block> xq(static_cast<size_t>(dim / 256)), hq(static_cast<size_t>(ff / 256));
     for (int b = 0; b < dim / 256; ++b) q::quant_block(x + 256 * b, xq[size_t(b)]);
     const size_t nff = static_cast<size_t>(ff);
     std::vector<float> g(nff), u(nff), h(nff);
     ref_matvec(types[0], gate, ff, dim, xq.data(), g.data(), threads);
     ref_matvec(types[1], up, ff, dim, xq.data(), u.data(), threads);
-    for (int i = 0; i < ff; ++i) h[size_t(i)] = q::swiglu(g[size_t(i)], u[size_t(i)], 0.0f);
+    for (int i = 0; i < ff; ++i) h[size_t(i)] = q::swiglu(g[size_t(i)], u[size_t(i)], lim);
     for (int b = 0; b < ff / 256; ++b) q::quant_block(h.data() + 256 * b, hq[size_t(b)]);
     ref_matvec(types[2], down, dim, ff, hq.data(), y, threads);
 }

@@ -291,7 +291,7 @@ void orc_matvec32(int t, const uint8_t* w, int n, int k, const int8_t* xq, const
 /* The per32 expert chain: Q32(x), gate and up rows, SwiGLU (core.hpp:88, the
  * same form as q8k_core.hpp:92-95), Q32(h), down rows. g, u, h may be NULL. */
 void orc_expert32(const int types[3], const uint8_t* gate, const uint8_t* up, const uint8_t* down, int dim, int ff,
-                  const float* x, float* y, float* g, float* u, float* h) {
+                  const float* x, float* y, float* g, float* u, float* h, float limit) {
     int8_t* q = (int8_t*)malloc((size_t)(dim > ff ? dim : ff));
     float* d = (float*)malloc(sizeof(float) * (size_t)((dim > ff ? dim : ff) / 32));
     float* gg = (float*)malloc(sizeof(float) * (size_t)ff * 3);
@@ -299,7 +299,7 @@ void orc_expert32(const int types[3], const uint8_t* gate, const uint8_t* up, co
     orc_quant32(x, dim, q, d);
     orc_matvec32(types[0], gate, ff, dim, q, d, gg);
     orc_matvec32(types[1], up, ff, dim, q, d, uu);
-    for (int i = 0; i < ff; ++i) hh[i] = orc_swiglu(gg[i], uu[i], 0.0f);
+    for (int i = 0; i < ff; ++i) hh[i] = orc_swiglu(gg[i], uu[i], limit);
     orc_quant32(hh, ff, q, d);
     orc_matvec32(types[2], down, dim, ff, q, d, y);
     if (g) memcpy(g, gg, sizeof(float) * (size_t)ff);
@@ -361,13 +361,13 @@ void orc_down_from_hidden(int type, const uint8_t* down, int dim, int ff, const 
 
 /* Expert chain, as the CPU lane runs it (cpu_lane.cpp:157-168). */
 void orc_expert(const int types[3], const uint8_t* gate, const uint8_t* up, const uint8_t* down, int dim, int ff,
-                const float* x, float* y, float* g_out, float* u_out, float* h_out, int threads) {
+                const float* x, float* y, float* g_out, float* u_out, float* h_out, int threads, float limit) {
     orc_q8k xq[64];
     float g[16384], u[16384], h[16384];
     orc_quantize_row(x, dim, xq);
     orc_matvec(types[0], gate, ff, dim, xq, g, threads);
     orc_matvec(types[1], up, ff, dim, xq, u, threads);
-    for (int i = 0; i < ff; ++i) h[i] = orc_swiglu(g[i], u[i], 0.0f);
+    for (int i = 0; i < ff; ++i) h[i] = orc_swiglu(g[i], u[i], limit);
     orc_down_from_hidden(types[2], down, dim, ff, h, y, threads);
     if (g_out) memcpy(g_out, g, sizeof(float) * (size_t)ff);
     if (u_out) memcpy(u_out, u, sizeof(float) * (size_t)ff);

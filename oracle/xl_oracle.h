@@ -55,10 +55,11 @@ int64_t orc_brute_block(int type, const uint8_t* blk, const orc_q8k* a);
 void orc_matvec(int type, const uint8_t* w, int n, int k, const orc_q8k* a, float* y, int threads);
 float orc_swiglu(float g, float u, float limit);
 
-/* One expert: y = down(SwiGLU(gate x, up x)). Optional intermediates. */
+/* One expert: y = down(SwiGLU(gate x, up x)), SwiGLU with the limit (0: none).
+ * Optional intermediates. */
 void orc_expert(const int types[3], const uint8_t* gate, const uint8_t* up, const uint8_t* down,
                 int dim, int ff, const float* x, float* y, float* g_out, float* u_out, float* h_out,
-                int threads);
+                int threads, float limit);
 /* Down half only, from a given hidden vector h (used to compare with the
  * device's own SwiGLU output). */
 void orc_down_from_hidden(int type, const uint8_t* down, int dim, int ff, const float* h, float* y, int threads);
@@ -77,7 +78,7 @@ void orc_quant32(const float* x, int k, int8_t* q, float* d);
 float orc_row32(int type, const uint8_t* row, int k, const int8_t* xq, const float* xd);
 void orc_matvec32(int type, const uint8_t* w, int n, int k, const int8_t* xq, const float* xd, float* y);
 void orc_expert32(const int types[3], const uint8_t* gate, const uint8_t* up, const uint8_t* down, int dim, int ff,
-                  const float* x, float* y, float* g, float* u, float* h);
+                  const float* x, float* y, float* g, float* u, float* h, float limit);
 
 /* Router of route.cpp:15-37 (route_cpu) for T tokens: logits T x stride (the
  * first n used), bias n (NULL = zeros); ids / w: T x k. */

@@ -13,11 +13,13 @@ NAMES = {16: "IQ2_XXS", 17: "IQ2_XS", 29: "IQ1_M"}
 ROLE = ("w1", "w3", "w2")
 
 
-def write_pack(path, orc, sigs, dim, ff, n_experts, seed, shards=2, top_k=6):
+def write_pack(path, orc, sigs, dim, ff, n_experts, seed, shards=2, top_k=6, swiglu_limit=None):
     """sigs[l] = (gate, up, down) ggml types of layer l. Returns path."""
     os.makedirs(path, exist_ok=True)
     meta = {"model_dir": path, "format": "gguf", "hidden_size": dim, "num_hidden_layers": len(sigs),
             "n_routed_experts": n_experts, "num_experts_per_tok": top_k, "moe_intermediate_size": ff}
+    if swiglu_limit is not None:
+        meta["swiglu_limit"] = swiglu_limit
     with open(os.path.join(path, "ds4.txt"), "w") as f:
         f.write("".join(f"{k} {v}\n" for k, v in meta.items()))
     data = [bytearray() for _ in range(shards)]

@@ -31,22 +31,26 @@ def test_exports_every_declared_symbol():
 
 
 def test_abi_version():
-    assert xl.lib().xl_abi_version() == 1
+    assert xl.lib().xl_abi_version() == L.ABI_VERSION == 2
 
 
 def test_open_rejects_version_and_size_before_device():
-    cfg = L._Config(C.sizeof(L._Config), 0, 4096, 3072, 1, 384, 8, 0)
+    cfg = L._Config(C.sizeof(L._Config), 0, 4096, 3072, 1, 384, 8, 0, 0.0)
     ctx, err = C.c_void_p(), L._Err()
-    assert xl.lib().xl_open(2, C.byref(cfg), C.byref(ctx), C.byref(err)) == 5
+    v = L.ABI_VERSION
+    assert xl.lib().xl_open(v + 1, C.byref(cfg), C.byref(ctx), C.byref(err)) == 5
     assert b"version" in err.message and not ctx.value
-    cfg.struct_bytes = 8
-    assert xl.lib().xl_open(1, C.byref(cfg), C.byref(ctx), C.byref(err)) == 5
+    cfg.struct_bytes = 32   # the version-1 layout (no swiglu_limit)
+    assert xl.lib().xl_open(v, C.byref(cfg), C.byref(ctx), C.byref(err)) == 5
     cfg.struct_bytes = C.sizeof(L._Config)
     cfg.dim = 1000
-    assert xl.lib().xl_open(1, C.byref(cfg), C.byref(ctx), C.byref(err)) == 1
+    assert xl.lib().xl_open(v, C.byref(cfg), C.byref(ctx), C.byref(err)) == 1
     assert b"dim" in err.message
     cfg.dim, cfg.max_picks = 4096, 17
-    assert xl.lib().xl_open(1, C.byref(cfg), C.byref(ctx), C.byref(err)) == 1
+    assert xl.lib().xl_open(v, C.byref(cfg), C.byref(ctx), C.byref(err)) == 1
+    cfg.max_picks, cfg.swiglu_limit = 8, float("inf")
+    assert xl.lib().xl_open(v, C.byref(cfg), C.byref(ctx), C.byref(err)) == 1
+    assert b"swiglu_limit" in err.message
 
 
 @pytest.mark.parametrize("t", [16, 17, 29])

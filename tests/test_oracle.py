@@ -297,3 +297,19 @@ def test_row32_vs_reference_and_float64(orc, ref, t, rng):
                 i = sc[0] * int(np.dot(vals[:16], qq[:16])) + sc[1] * int(np.dot(vals[16:], qq[16:]))
                 tot += float(d[kb]) * float(d8) * i
             assert abs(w[r] - tot) <= 2e-5 * (abs(tot) + 1e-3), (r, w[r], tot)
+
+
+@pytest.mark.parametrize("limit", [0.0, 1.0, 7.0])
+def test_expert_chain_vs_reference_with_limit(orc, ref, rng, limit):
+    """The Q8_K expert chain with the SwiGLU limit (model_meta.hpp:34 lim):
+    bit-identical to the reference's own functions; the limit must bite."""
+    t3, dim, ff = (16, 16, 17), 1024, 512
+    mats = orc.gen_expert(t3, 5, 0, 3, dim, ff)
+    x = rng.standard_normal(dim).astype(np.float32)
+    y, g, u, h = orc.expert(t3, *mats, dim, ff, x, intermediates=True, limit=limit)
+    assert np.array_equal(y.view(np.uint32), ref.expert(t3, *mats, dim, ff, x, limit=limit).view(np.uint32))
+    if limit > 0:
+        assert (np.abs(g) > limit).any() or (np.abs(u) > limit).any()
+        assert not np.array_equal(y, orc.expert(t3, *mats, dim, ff, x))
+        want = [orc.swiglu(min(a, limit), min(max(b, -limit), limit)) for a, b in zip(g, u)]
+        assert np.array_equal(h, np.array(want, np.float32))

@@ -16,7 +16,13 @@ SIGS = [(16, 16, 17), (29, 29, 29), (17, 17, 29), (16, 16, 16)]
 
 def test_meta_and_types(orc, tmp_path):
     p = write_pack(str(tmp_path / "pack"), orc, SIGS, 256, 512, 4, seed=3)
-    assert xl.pack_meta(p) == {"dim": 256, "ff": 512, "n_layers": 4, "n_experts": 4, "top_k": 6}
+    assert xl.pack_meta(p) == {"dim": 256, "ff": 512, "n_layers": 4, "n_experts": 4, "top_k": 6, "swiglu_limit": 0.0}
+    q = write_pack(str(tmp_path / "pack_lim"), orc, SIGS[:1], 256, 256, 1, seed=3, swiglu_limit=7)
+    assert xl.pack_meta(q)["swiglu_limit"] == 7.0
+    ds4 = open(os.path.join(q, "ds4.txt")).read()
+    open(os.path.join(q, "ds4.txt"), "w").write(ds4.replace("swiglu_limit 7", "swiglu_limit seven"))
+    with pytest.raises(xl.XLError, match="swiglu_limit"):
+        xl.pack_meta(q)
     t = xl.pack_types(p, 1, 3, 4)
     for l in range(3):
         assert (t[l] == np.array(SIGS[l + 1], np.int32)).all()

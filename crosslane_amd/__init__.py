@@ -8,5 +8,5 @@ raises.
 """
 from .lane import (  # noqa: F401
     IQ1_M, IQ2_XS, IQ2_XXS, BLOCK_BYTES, Lane, XLError, codebook, generate_host, lib, pack_meta, pack_types,
-    planar_bytes, repack, restore,
+    planar_bytes, repack, restore, shared_work_bytes,
 )

@@ -8,7 +8,7 @@ import sys
 PKG = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(PKG, "csrc")
 LIB = os.path.join(PKG, "libcrosslane.so")
-SOURCES = ["xl_kernels.hip", "xl_layer.hip", "xl_stream.hip", "xl_grouped.hip", "xl_per32.hip", "xl_api.cpp"]
+SOURCES = ["xl_kernels.hip", "xl_layer.hip", "xl_stream.hip", "xl_grouped.hip", "xl_per32.hip", "xl_hc.hip", "xl_api.cpp"]
 HEADERS = ["xl_format.hpp", "xl_rows.hpp", "xl_internal.hpp", "xl_dev.hpp", "xl_codebooks.inc", "exports.map"]
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")

@@ -362,6 +362,44 @@ void enqueue_layer(xl_context* ctx, int32_t layer, const int32_t* d_ids, const f
     }
 }
 
+// A per32 matrix: planar IQ (xl_format.hpp) or raw dense ggml blocks.
+xl::MatRef per32_matrix(int type, const void* base, int n, int k) {
+    need(reinterpret_cast<uintptr_t>(base) % 16 == 0, XL_E_ARG, "matrix not 16-byte aligned");
+    xl::MatRef m{};
+    m.base = static_cast<const uint8_t*>(base);
+    m.type = type;
+    if (xl::dense_type(type)) {
+        m.nb = k / xl::dense_block_values(type);
+    } else {
+        const auto P = xl::plane_layout(type, matrix_blocks(n, k));
+        m.off1 = P.off[1];
+        m.off2 = P.off[2];
+        m.nb = k / 256;
+    }
+    return m;
+}
+
+// Shared-expert workspace of T tokens: g, u, h (T x ff floats), Q32(x) and
+// Q32(h) quants and scales, each 256-byte aligned.
+struct SharedWork {
+    uint64_t g, u, h, xq, hq, xd, hd, bytes;
+};
+SharedWork shared_work(int dim, int ff, int T) {
+    SharedWork w{};
+    uint64_t at = 0;
+    const auto take = [&](uint64_t bytes) { const uint64_t o = at; at += (bytes + 255) & ~uint64_t(255); return o; };
+    const uint64_t t = uint64_t(T);
+    w.g = take(t * ff * 4);
+    w.u = take(t * ff * 4);
+    w.h = take(t * ff * 4);
+    w.xq = take(t * dim);
+    w.hq = take(t * ff);
+    w.xd = take(t * (dim / 32) * 4);
+    w.hd = take(t * (ff / 32) * 4);
+    w.bytes = at;
+    return w;
+}
+
 // Enqueues the per32 layer (hip_resident_bank.hpp:185-200 with the kernels of
 // hip_experts.hip): quant32(x), gate and up rows of every pick in one launch,
 // SwiGLU, quant32(h) of every pick, down rows into y (k x dim), then the
@@ -377,7 +415,7 @@ void enqueue_per32(xl_context* ctx, int32_t layer, const int32_t* d_ids, const f
     mark("");
     hip_check(xl::dev::launch_quant32(d_x, 1, dim, ctx->xq, xd, ctx->err_flag, s), "quant32(x) launch");
     mark("quant32_x");
-    hip_check(xl::dev::launch_mv32(descs, d_ids, none, k, E, 0, 2, ff, dim, ctx->xq, 0, xd, 0, ctx->g, ctx->u,
+    hip_check(xl::dev::launch_mv32(descs, d_ids, none, none, k, E, 0, 2, ff, dim, ctx->xq, 0, xd, 0, ctx->g, ctx->u,
                                    size_t(ff), ctx->tables, ctx->err_flag, s),
               "per32 gate/up launch");
     mark("gate_up32");
@@ -385,7 +423,7 @@ void enqueue_per32(xl_context* ctx, int32_t layer, const int32_t* d_ids, const f
     mark("swiglu");
     hip_check(xl::dev::launch_quant32(ctx->h, k, ff, ctx->hq, hd, ctx->err_flag, s), "quant32(h) launch");
     mark("quant32_h");
-    hip_check(xl::dev::launch_mv32(descs, d_ids, none, k, E, 2, 1, dim, ff, ctx->hq, size_t(ff), hd, size_t(ff / 32),
+    hip_check(xl::dev::launch_mv32(descs, d_ids, none, none, k, E, 2, 1, dim, ff, ctx->hq, size_t(ff), hd, size_t(ff / 32),
                                    d_y, nullptr, size_t(dim), ctx->tables, ctx->err_flag, s),
               "per32 down launch");
     mark("down32");
@@ -1143,21 +1181,84 @@ int32_t xl_matvec_per32_async(xl_context* ctx, int32_t type, const void* d_plana
                               const int8_t* d_q, const float* d_d, float* d_y, void* stream, xl_error* err) {
     return guarded(ctx, err, [&] {
         ready(ctx, false);
-        need(xl::supported_type(type), XL_E_ARG, "unsupported block type");
+        need(xl::supported_type(type) || xl::dense_type(type), XL_E_ARG, "unsupported block type");
         need(d_planar && d_q && d_d && d_y, XL_E_ARG, "null device pointer");
         need(reinterpret_cast<uintptr_t>(d_q) % 16 == 0, XL_E_ARG, "quants not 16-byte aligned");
         need(n >= 1 && n <= (1 << 24) && k >= 256 && k % 256 == 0 && k <= (1 << 20), XL_E_ARG,
              "n in 1..2^24 and k a multiple of 256 up to 2^20");
-        const auto P = xl::plane_layout(type, matrix_blocks(n, k));
-        xl::MatRef m{};
-        m.base = static_cast<const uint8_t*>(d_planar);
-        m.off1 = P.off[1];
-        m.off2 = P.off[2];
-        m.type = type;
-        m.nb = k / 256;
-        hip_check(xl::dev::launch_mv32(nullptr, nullptr, m, 1, 0, 0, 1, n, k, d_q, 0, d_d, 0, d_y, nullptr, 0,
+        const xl::MatRef m = per32_matrix(type, d_planar, n, k);
+        hip_check(xl::dev::launch_mv32(nullptr, nullptr, m, m, 1, 0, 0, 1, n, k, d_q, 0, d_d, 0, d_y, nullptr, 0,
                                        ctx->tables, ctx->err_flag, pick_stream(ctx, stream)),
                   "per32 matvec launch");
+    });
+}
+
+uint64_t xl_shared_work_bytes(int32_t dim, int32_t ff, int32_t T) {
+    if (dim < 256 || ff < 256 || dim % 256 || ff % 256 || dim > (1 << 16) || ff > (1 << 16) || T < 1 || T > 8192)
+        return 0;
+    return shared_work(dim, ff, T).bytes;
+}
+
+int32_t xl_shared_forward_async(xl_context* ctx, int32_t type_gate, const void* d_gate, int32_t type_up,
+                                const void* d_up, int32_t type_down, const void* d_down, int32_t ff, int32_t T,
+                                const float* d_x, float* d_out, void* d_work, uint64_t work_bytes, void* stream,
+                                xl_error* err) {
+    return guarded(ctx, err, [&] {
+        ready(ctx, false);
+        const int dim = ctx->cfg.dim;
+        need(d_gate && d_up && d_down && d_x && d_out && d_work, XL_E_ARG, "null device pointer");
+        need(ff >= 256 && ff % 256 == 0 && ff <= (1 << 16), XL_E_ARG, "shared ff a multiple of 256 up to 65536");
+        need(T >= 1 && T <= 8192, XL_E_ARG, "T outside 1..8192");
+        for (const int32_t t : {type_gate, type_up, type_down})
+            need(xl::supported_type(t) || xl::dense_type(t), XL_E_ARG, "unsupported shared-expert block type");
+        const SharedWork w = shared_work(dim, ff, T);
+        need(work_bytes >= w.bytes, XL_E_ARG, "workspace smaller than xl_shared_work_bytes(dim, ff)");
+        need(reinterpret_cast<uintptr_t>(d_work) % 256 == 0, XL_E_ARG, "workspace not 256-byte aligned");
+        uint8_t* base = static_cast<uint8_t*>(d_work);
+        float* g = reinterpret_cast<float*>(base + w.g);
+        float* u = reinterpret_cast<float*>(base + w.u);
+        float* h = reinterpret_cast<float*>(base + w.h);
+        int8_t* xq = reinterpret_cast<int8_t*>(base + w.xq);
+        int8_t* hq = reinterpret_cast<int8_t*>(base + w.hq);
+        float* xd = reinterpret_cast<float*>(base + w.xd);
+        float* hd = reinterpret_cast<float*>(base + w.hd);
+        const xl::MatRef mg = per32_matrix(type_gate, d_gate, ff, dim), mu = per32_matrix(type_up, d_up, ff, dim);
+        const xl::MatRef md = per32_matrix(type_down, d_down, dim, ff);
+        hipStream_t s = pick_stream(ctx, stream);
+        // hip_backend.cpp:664-666: mv(gate, up), swiglu, mv(down), T tokens per launch
+        hip_check(xl::dev::launch_quant32(d_x, T, dim, xq, xd, ctx->err_flag, s), "quant32(x) launch");
+        hip_check(xl::dev::launch_mv32(nullptr, nullptr, mg, mu, T, 0, 0, 2, ff, dim, xq, size_t(dim), xd,
+                                       size_t(dim / 32), g, u, size_t(ff), ctx->tables, ctx->err_flag, s),
+                  "shared gate/up launch");
+        hip_check(xl::dev::launch_swiglu32(g, u, T * ff, ctx->cfg.swiglu_limit, h, s), "shared SwiGLU launch");
+        hip_check(xl::dev::launch_quant32(h, T, ff, hq, hd, ctx->err_flag, s), "quant32(h) launch");
+        hip_check(xl::dev::launch_mv32(nullptr, nullptr, md, md, T, 0, 0, 1, dim, ff, hq, size_t(ff), hd,
+                                       size_t(ff / 32), d_out, nullptr, size_t(dim), ctx->tables, ctx->err_flag, s),
+                  "shared down launch");
+    });
+}
+
+int32_t xl_hc_post_async(xl_context* ctx, const float* d_y, const float* d_res, const float* d_post,
+                         const float* d_comb, int32_t D, int32_t H, int32_t T, float* d_out, void* stream,
+                         xl_error* err) {
+    return guarded(ctx, err, [&] {
+        ready(ctx, false);
+        need(d_y && d_res && d_post && d_comb && d_out, XL_E_ARG, "null device pointer");
+        need(D >= 1 && D <= 32768 && H >= 1 && H <= 4 && T >= 1 && T <= 8192, XL_E_ARG,
+             "hc geometry: D in 1..32768, H in 1..4, T in 1..8192");
+        const uint64_t ob = uint64_t(T) * H * D * 4;
+        const auto overlaps = [&](const void* p, uint64_t bytes) {
+            const uintptr_t a = reinterpret_cast<uintptr_t>(d_out), b = reinterpret_cast<uintptr_t>(p);
+            return a <= b ? b - a < ob : a - b < bytes;
+        };
+        // hc.cpp:108-109,113-114: out may be res itself (in place), never a
+        // partial overlap with res nor any overlap with y, post or comb.
+        need(d_out == d_res || !overlaps(d_res, ob), XL_E_ARG, "hc output overlaps the residual streams");
+        need(!overlaps(d_y, uint64_t(T) * D * 4) && !overlaps(d_post, uint64_t(T) * 32) &&
+                 !overlaps(d_comb, uint64_t(T) * 256),
+             XL_E_ARG, "hc output overlaps an input");
+        hip_check(xl::dev::launch_hc_post(d_y, d_res, d_post, d_comb, D, H, T, d_out, pick_stream(ctx, stream)),
+                  "hc_post launch");
     });
 }
 

@@ -32,6 +32,16 @@ static_assert(sizeof(Q8K) == 292, "Q8_K block is 292 bytes");
 static_assert(offsetof(Q8K, qs) == 4 && offsetof(Q8K, bsums) == 260, "Q8_K field offsets");
 
 XL_HD constexpr bool supported_type(int t) { return t == kIQ2_XXS || t == kIQ2_XS || t == kIQ1_M; }
+
+// Dense formats of the shared-expert matrices (per32 rows only; stored as raw
+// ggml blocks, row-major, no planar split): Q8_0 (34 B per 32 values), Q4_K
+// (144 B per 256), Q5_K (176 B per 256), Q6_K (210 B per 256).
+enum : int { kQ8_0 = 8, kQ4_K = 12, kQ5_K = 13, kQ6_K = 14 };
+XL_HD constexpr bool dense_type(int t) { return t == kQ8_0 || t == kQ4_K || t == kQ5_K || t == kQ6_K; }
+XL_HD constexpr int dense_block_bytes(int t) {
+    return t == kQ8_0 ? 34 : t == kQ4_K ? 144 : t == kQ5_K ? 176 : t == kQ6_K ? 210 : 0;
+}
+XL_HD constexpr int dense_block_values(int t) { return t == kQ8_0 ? 32 : 256; }
 XL_HD constexpr int block_bytes(int t) {
     return t == kIQ2_XXS ? 66 : t == kIQ2_XS ? 74 : t == kIQ1_M ? 56 : 0;
 }

@@ -160,12 +160,19 @@ hipError_t launch_combine(const int32_t* ids, const float* w, int k, const float
 // (k a multiple of 32) into q (int8) and d (one float per 32).
 hipError_t launch_quant32(const float* x, int rows, int k, int8_t* q, float* d, int* err, hipStream_t s);
 // per32 rows of roles role0 .. role0 + roles - 1 (at most 2) of every pick's
-// expert (ids == nullptr: the one matrix `single`, picks = 1): y_r[pick *
-// y_stride + row] from q + pick * q_stride (16-byte aligned) and d + pick * d_stride.
-hipError_t launch_mv32(const ExpertDesc* descs, const int32_t* ids, const MatRef& single, int picks, int n_experts,
-                       int role0, int roles, int n, int k, const int8_t* q, size_t q_stride, const float* d,
-                       size_t d_stride, float* y0, float* y1, size_t y_stride, const uint64_t* tables, int* err,
-                       hipStream_t s);
+// expert (ids == nullptr: the matrices single0 / single1 for roles 0 / 1):
+// y_r[pick * y_stride + row] from q + pick * q_stride (16-byte aligned) and
+// d + pick * d_stride. Matrices: planar IQ types or raw dense blocks (Q8_0,
+// Q4_K, Q5_K, Q6_K, base 16-byte aligned).
+hipError_t launch_mv32(const ExpertDesc* descs, const int32_t* ids, const MatRef& single0, const MatRef& single1,
+                       int picks, int n_experts, int role0, int roles, int n, int k, const int8_t* q, size_t q_stride,
+                       const float* d, size_t d_stride, float* y0, float* y1, size_t y_stride,
+                       const uint64_t* tables, int* err, hipStream_t s);
+// Hyper-connection post (sycl/hc/core.hpp:81-86) of T tokens, H <= 4 streams
+// of D: out[t][k][e] = post[t][k] * y[t][e] + sum_j comb[t][j * H + k] *
+// res[t][j][e]; out may equal res (in place).
+hipError_t launch_hc_post(const float* y, const float* res, const float* post, const float* comb, int D, int H, int T,
+                          float* out, hipStream_t s);
 // h = g / (1 + exp(-g)) * u over n values (lim > 0: g, u clamped first).
 hipError_t launch_swiglu32(const float* g, const float* u, int n, float lim, float* h, hipStream_t s);
 // Seeded generation of one planar matrix (role 0 gate, 1 up, 2 down).

@@ -14,7 +14,11 @@
 //                   first when the SwiGLU limit is set)
 //
 // The bank's planar blocks are decoded directly (xl_format.hpp layout); the
-// codebooks come from the context's expanded tables. Build with
+// codebooks come from the context's expanded tables. The dense formats of the
+// shared-expert matrices (Q8_0, Q4_K, Q5_K, Q6_K) are read as raw ggml blocks:
+// Q4_K / Q5_K subtract the min term as two fmas (corr = fma(m, sum x[0..15],
+// m * sum x[16..31]), dot = fma(d, float(s * (a + b)), -corr)); Q6_K values are
+// q - 32 with signed per-16 scales; Q8_0 accumulates fma(d * d_x, float(dot)). Build with
 // -ffp-contract=off: every float operation above is a separate IEEE rounding.
 #include <hip/hip_runtime.h>
 
@@ -35,12 +39,94 @@ __device__ __forceinline__ uint32_t ld32(const uint8_t* p) { return *reinterpret
 // 8 activation words q, the odd half scales and the block's d * 0.125.
 struct Sub32 {
     int a, b, s0, s1;
-    float d8;
+    float d8;          // the sub-block's d (IQ types: fp16 d * 0.125)
+    int sa, sb;        // Q4_K / Q5_K: the two half sums of the activations
+    float m;           // Q4_K / Q5_K: fp16 dmin * min (both halves)
 };
+
+// 32 bytes at a 2-byte-aligned address as eight words (the Q8_0 / Q6_K rows).
+__device__ __forceinline__ void ld32b_a2(const uint8_t* p, uint32_t* w) {
+    const uint16_t* h = reinterpret_cast<const uint16_t*>(p);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) w[j] = uint32_t(h[2 * j]) | (uint32_t(h[2 * j + 1]) << 16);
+}
+// 32 bytes at a 16-byte-aligned address (the Q4_K / Q5_K planes).
+__device__ __forceinline__ void ld32b_a16(const uint8_t* p, uint32_t* w) {
+    const uint4 lo = reinterpret_cast<const uint4*>(p)[0], hi = reinterpret_cast<const uint4*>(p)[1];
+    w[0] = lo.x; w[1] = lo.y; w[2] = lo.z; w[3] = lo.w; w[4] = hi.x; w[5] = hi.y; w[6] = hi.z; w[7] = hi.w;
+}
+
+// Dense sub-block kb (32 values) of row `row` (raw ggml blocks).
+__device__ __forceinline__ Sub32 sub32_dense(const MatRef& m, int row, int kb, const uint32_t* q) {
+    Sub32 r{0, 0, 1, 1, 0.0f, 0, 0, 0.0f};
+    uint32_t v[8];
+    if (m.type == kQ8_0) {
+        const uint8_t* b = m.base + (size_t(row) * m.nb + kb) * 34;
+        r.d8 = h2f(ld16(b));
+        ld32b_a2(b + 2, v);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            r.a = sdot4(v[j], q[j], r.a);
+            r.b = sdot4(v[4 + j], q[4 + j], r.b);
+        }
+        return r;
+    }
+    const int ib = kb & 7;
+    if (m.type == kQ6_K) {
+        const uint8_t* b = m.base + (size_t(row) * m.nb + (kb >> 3)) * 210;
+        const int h = ib >> 2, quarter = ib & 3;
+        uint32_t hi[8];
+        ld32b_a2(b + 64 * h + ((quarter & 1) ? 32 : 0), v);
+        ld32b_a2(b + 128 + 32 * h, hi);
+        const uint32_t sc = ld16(b + 192 + 8 * h + 2 * quarter);
+        r.s0 = int(int8_t(sc & 255u));
+        r.s1 = int(int8_t(sc >> 8));
+        r.d8 = h2f(ld16(b + 208));
+        int sx0 = 0, sx1 = 0;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const uint32_t w6 = ((v[j] >> (4 * (quarter >> 1))) & 0x0f0f0f0fu) | (((hi[j] >> (2 * quarter)) & 0x03030303u) << 4);
+            if (j < 4) { r.a = sdot4(w6, q[j], r.a); sx0 = sdot4(0x01010101u, q[j], sx0); }
+            else { r.b = sdot4(w6, q[j], r.b); sx1 = sdot4(0x01010101u, q[j], sx1); }
+        }
+        r.a -= 32 * sx0;   // values q - 32: exact integer correction
+        r.b -= 32 * sx1;
+        return r;
+    }
+    // Q4_K / Q5_K
+    const uint8_t* b = m.base + (size_t(row) * m.nb + (kb >> 3)) * (m.type == kQ5_K ? 176 : 144);
+    const uint32_t dd = ld32(b), s03 = ld32(b + 4), s47 = ld32(b + 8), s8b = ld32(b + 12);
+    const auto sbyte = [&](int i) -> uint32_t {
+        const uint32_t w = i < 4 ? s03 : i < 8 ? s47 : s8b;
+        return (w >> (8 * (i & 3))) & 255u;
+    };
+    int scale, mn;
+    if (ib < 4) {
+        scale = int(sbyte(ib) & 63u);
+        mn = int(sbyte(ib + 4) & 63u);
+    } else {
+        scale = int((sbyte(ib + 4) & 15u) | ((sbyte(ib - 4) >> 6) << 4));
+        mn = int((sbyte(ib + 4) >> 4) | ((sbyte(ib) >> 6) << 4));
+    }
+    r.s0 = r.s1 = scale;
+    r.d8 = h2f(uint16_t(dd & 0xffffu));
+    r.m = __fmul_rn(h2f(uint16_t(dd >> 16)), float(mn));
+    ld32b_a16(b + (m.type == kQ5_K ? 48 : 16) + 32 * (ib >> 1), v);
+    uint32_t hb[8];
+    if (m.type == kQ5_K) ld32b_a16(b + 16, hb);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        uint32_t w = (v[j] >> (4 * (ib & 1))) & 0x0f0f0f0fu;
+        if (m.type == kQ5_K) w |= ((hb[j] >> ib) & 0x01010101u) << 4;
+        if (j < 4) { r.a = sdot4(w, q[j], r.a); r.sa = sdot4(0x01010101u, q[j], r.sa); }
+        else { r.b = sdot4(w, q[j], r.b); r.sb = sdot4(0x01010101u, q[j], r.sb); }
+    }
+    return r;
+}
 __device__ __forceinline__ Sub32 sub32(const MatRef& m, int row, int kb, const uint32_t* q, const uint64_t* tab) {
     const size_t blk = size_t(row) * m.nb + (kb >> 3);
     const int ib = kb & 7;
-    Sub32 r{0, 0, 1, 1, 0.0f};
+    Sub32 r{0, 0, 1, 1, 0.0f, 0, 0, 0.0f};
     int half[2] = {0, 0};
     if (m.type == kIQ2_XXS || m.type == kIQ2_XS) {
         const uint8_t* p = m.base + blk * 64 + 8 * ib;
@@ -118,15 +204,16 @@ __global__ __launch_bounds__(256) void quant32_kernel(const float* __restrict__ 
 // Rows of one or two roles of every pick: grid (ceil(n / 8), picks, roles), 8
 // rows per 256-thread workgroup, 32 lanes per row. Role role0 + z writes yz.
 // Activations: q + pick * q_stride (k int8), d + pick * d_stride (k / 32
-// scales); output y + pick * y_stride. ids == nullptr: the one matrix `single`.
+// scales); output y + pick * y_stride. ids == nullptr: the matrices single0
+// (z = 0) and single1 (z = 1) for every pick.
 __global__ __launch_bounds__(256) void mv32_kernel(const ExpertDesc* __restrict__ descs, const int32_t* __restrict__ ids,
-                                                   MatRef single, int n_experts, int role0, int n, int k,
+                                                   MatRef single0, MatRef single1, int n_experts, int role0, int n, int k,
                                                    const int8_t* __restrict__ q, size_t q_stride,
                                                    const float* __restrict__ d, size_t d_stride, float* __restrict__ y0,
                                                    float* __restrict__ y1, size_t y_stride,
                                                    const uint64_t* __restrict__ tab, int* __restrict__ err) {
     const int pick = blockIdx.y;
-    MatRef m = single;
+    MatRef m = blockIdx.z ? single1 : single0;
     if (ids) {
         const int id = ids[pick];
         if (id < 0 || id >= n_experts) {   // the pick contributes nothing (the combine skips it)
@@ -145,8 +232,18 @@ __global__ __launch_bounds__(256) void mv32_kernel(const ExpertDesc* __restrict_
             const uint4* qw = reinterpret_cast<const uint4*>(qp + 32 * kb);
             const uint4 lo = qw[0], hi = qw[1];
             const uint32_t a[8] = {lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
-            const Sub32 s = sub32(m, row, kb, a, tab);
-            const float dot = __fmul_rn(s.d8, float(s.s0 * s.a + s.s1 * s.b));
+            if (m.type == kQ8_0) {   // core.hpp:80: fma(d * d_x, float(dot), acc)
+                const Sub32 s = sub32_dense(m, row, kb, a);
+                acc = fmaf(__fmul_rn(s.d8, dp[kb]), float(s.a + s.b), acc);
+                continue;
+            }
+            const Sub32 s = dense_type(m.type) ? sub32_dense(m, row, kb, a) : sub32(m, row, kb, a, tab);
+            const int isum = s.s0 * s.a + s.s1 * s.b;
+            float dot = __fmul_rn(s.d8, float(isum));
+            if (m.type == kQ4_K || m.type == kQ5_K) {   // core.hpp:62-65: the min term as two fmas
+                const float corr = fmaf(s.m, float(s.sa), __fmul_rn(s.m, float(s.sb)));
+                dot = fmaf(s.d8, float(isum), -corr);
+            }
             acc = fmaf(dp[kb], dot, acc);
         }
 #pragma unroll
@@ -169,13 +266,13 @@ hipError_t launch_quant32(const float* x, int rows, int k, int8_t* q, float* d, 
     return hipGetLastError();
 }
 
-hipError_t launch_mv32(const ExpertDesc* descs, const int32_t* ids, const MatRef& single, int picks, int n_experts,
-                       int role0, int roles, int n, int k, const int8_t* q, size_t q_stride, const float* d,
-                       size_t d_stride, float* y0, float* y1, size_t y_stride, const uint64_t* tables, int* err,
-                       hipStream_t s) {
+hipError_t launch_mv32(const ExpertDesc* descs, const int32_t* ids, const MatRef& single0, const MatRef& single1,
+                       int picks, int n_experts, int role0, int roles, int n, int k, const int8_t* q, size_t q_stride,
+                       const float* d, size_t d_stride, float* y0, float* y1, size_t y_stride,
+                       const uint64_t* tables, int* err, hipStream_t s) {
     if (picks < 1 || roles < 1 || roles > 2 || n < 1 || k < 256 || k % 256) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(mv32_kernel, dim3((n + 7) / 8, picks, roles), dim3(256), 0, s, descs, ids, single, n_experts,
-                       role0, n, k, q, q_stride, d, d_stride, y0, y1, y_stride, tables, err);
+    hipLaunchKernelGGL(mv32_kernel, dim3((n + 7) / 8, picks, roles), dim3(256), 0, s, descs, ids, single0, single1,
+                       n_experts, role0, n, k, q, q_stride, d, d_stride, y0, y1, y_stride, tables, err);
     return hipGetLastError();
 }
 

@@ -93,6 +93,10 @@ _SIGNATURES = {
     "xl_layer_forward_per32_async": (_I32, [_P, _I32, _P, _P, _I32, _P, _P, _P, _P, _P, _ErrP]),
     "xl_quantize_per32_async": (_I32, [_P, _P, _I32, _I32, _P, _P, _P, _ErrP]),
     "xl_matvec_per32_async": (_I32, [_P, _I32, _P, _I32, _I32, _P, _P, _P, _P, _ErrP]),
+    "xl_shared_work_bytes": (C.c_uint64, [_I32, _I32, _I32]),
+    "xl_shared_forward_async": (_I32, [_P, _I32, _P, _I32, _P, _I32, _P, _I32, _I32, _P, _P, _P, C.c_uint64, _P,
+                                       _ErrP]),
+    "xl_hc_post_async": (_I32, [_P, _P, _P, _P, _P, _I32, _I32, _I32, _P, _P, _ErrP]),
     "xl_profile_begin": (_I32, [_P, _I32, _ErrP]),
     "xl_profile_end": (_I32, [_P, _f32p, _I32, C.POINTER(_I32), C.POINTER(_I32), C.c_char_p, _I32, _ErrP]),
     "xl_profile_timeline": (_I32, [_P, _u64p, _I32, C.POINTER(_I32), _ErrP]),
@@ -181,6 +185,11 @@ def pack_meta(pack_dir: str) -> dict:
     err = _Err()
     _check(lib().xl_pack_meta_get(os.fsencode(pack_dir), C.byref(m), C.byref(err)), err)
     return {f: getattr(m, f) for f, _ in _PackMeta._fields_[1:]}
+
+
+def shared_work_bytes(dim: int, ff: int, T: int = 1) -> int:
+    """Workspace bytes xl_shared_forward_async needs for T tokens."""
+    return int(lib().xl_shared_work_bytes(dim, ff, T))
 
 
 def pack_types(pack_dir: str, first_layer: int, n_layers: int, n_experts: int) -> np.ndarray:
@@ -381,6 +390,20 @@ class Lane:
 
     def matvec_per32_async(self, t: int, planar, n: int, k: int, q, d, y, stream=None) -> None:
         self._call("xl_matvec_per32_async", t, _ptr(planar), n, k, _ptr(q), _ptr(d), _ptr(y),
+                   None if stream is None else int(stream))
+
+    def shared_forward_async(self, types, gate, up, down, ff: int, x, out, work, stream=None) -> None:
+        """Shared-expert FFN of T tokens: x, out [T, dim] device tensors; gate, up,
+        down raw ggml (dense) or planar (IQ) device bytes; work >= shared_work_bytes."""
+        T = int(x.numel()) // self.dim
+        self._call("xl_shared_forward_async", int(types[0]), _ptr(gate), int(types[1]), _ptr(up), int(types[2]),
+                   _ptr(down), ff, T, _ptr(x), _ptr(out), _ptr(work), int(work.numel() * work.element_size()),
+                   None if stream is None else int(stream))
+
+    def hc_post_async(self, y, res, post, comb, out, stream=None) -> None:
+        """y [T, D], res / out [T, H, D], post [T, 8], comb [T, 64] device tensors."""
+        T, H, D = (int(v) for v in res.shape)
+        self._call("xl_hc_post_async", _ptr(y), _ptr(res), _ptr(post), _ptr(comb), D, H, T, _ptr(out),
                    None if stream is None else int(stream))
 
     def matvec_async(self, t: int, planar, n: int, k: int, x, y, partials=None, stream=None) -> None:

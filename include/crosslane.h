@@ -212,10 +212,37 @@ int32_t xl_layer_forward_per32_async(xl_context* ctx, int32_t layer, const int32
  * (hip_experts.hip:17-26, hipex::quantize). */
 int32_t xl_quantize_per32_async(xl_context* ctx, const float* d_x, int32_t rows, int32_t k, int8_t* d_q, float* d_d,
                                 void* stream, xl_error* err);
-/* One planar matrix (n x k) times per32 activations (d_q 16-byte aligned, k
- * int8; d_d k/32 scales): y[n] (dot_kernel<Type>, hip_experts.hip:27-41). */
+/* One matrix (n x k) times per32 activations (d_q 16-byte aligned, k int8;
+ * d_d k/32 scales): y[n] (dot_kernel<Type>, hip_experts.hip:27-41; the lane<>
+ * of sycl/moe/core.hpp:69-84 for the dense formats). d_planar (16-byte
+ * aligned): an IQ matrix in the planar layout of xl_repack, or raw ggml blocks
+ * of the dense formats Q8_0 (8), Q4_K (12), Q5_K (13), Q6_K (14). */
 int32_t xl_matvec_per32_async(xl_context* ctx, int32_t type, const void* d_planar, int32_t n, int32_t k,
                               const int8_t* d_q, const float* d_d, float* d_y, void* stream, xl_error* err);
+
+/* ---- around the routed experts (device pointers) ----------------------------
+ * Shared-expert FFN (hip_backend.cpp:664-666: mv(w1, w3), swiglu, mv(w2), the
+ * per32 arithmetic of the production GEMV, SwiGLU with the context's limit)
+ * for T tokens: out[T x dim] from x[T x dim]. Matrices: gate and up ff x dim,
+ * down dim x ff, each raw ggml blocks of a dense format (Q8_0, Q4_K, Q5_K,
+ * Q6_K: the pack's ffn.shared_experts.w1 / w3 / w2 bytes) or planar IQ. The
+ * caller's workspace (256-byte aligned, xl_shared_work_bytes(dim, ff, T)
+ * bytes) holds the intermediates; nothing is allocated. The result is what
+ * xl_layer_forward takes as its shared row. */
+uint64_t xl_shared_work_bytes(int32_t dim, int32_t ff, int32_t T);
+int32_t xl_shared_forward_async(xl_context* ctx, int32_t type_gate, const void* d_gate, int32_t type_up,
+                                const void* d_up, int32_t type_down, const void* d_down, int32_t ff, int32_t T,
+                                const float* d_x, float* d_out, void* d_work, uint64_t work_bytes, void* stream,
+                                xl_error* err);
+/* Hyper-connection post after the MoE block (hip_backend.cpp:777 k4::hc_post;
+ * sycl/hc/hc.cpp:107-115, core.hpp:81-86): for T tokens and H <= 4 streams of
+ * D, out[t][k][e] = post[t][k] * y[t][e] + sum_j comb[t][j * H + k] *
+ * res[t][j][e] (j ascending, separate roundings). y T x D, res and out T x H x
+ * D, post T x 8, comb T x 64. out may be res (in place); other overlaps are
+ * rejected. */
+int32_t xl_hc_post_async(xl_context* ctx, const float* d_y, const float* d_res, const float* d_post,
+                         const float* d_comb, int32_t D, int32_t H, int32_t T, float* d_out, void* stream,
+                         xl_error* err);
 
 /* ---- stage profiling --------------------------------------------------------
  * Between xl_profile_begin and xl_profile_end, the first max_calls layer calls

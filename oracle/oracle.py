@@ -60,6 +60,10 @@ class Oracle:
         L.orc_row32.argtypes = [C.c_int, _u8p, C.c_int, _i8p, _f32p]
         L.orc_row32.restype = C.c_float
         L.orc_matvec32.argtypes = [C.c_int, _u8p, C.c_int, C.c_int, _i8p, _f32p, _f32p]
+        L.orc_row_bytes32.argtypes = [C.c_int, C.c_int]
+        L.orc_row_bytes32.restype = C.c_int
+        L.orc_dequant32.argtypes = [C.c_int, _u8p, C.c_int, np.ctypeslib.ndpointer(np.float64, flags="C_CONTIGUOUS")]
+        L.orc_hc_post.argtypes = [_f32p, _f32p, _f32p, _f32p, C.c_int, C.c_int, C.c_int, _f32p]
         L.orc_expert32.argtypes = [_i32p, _u8p, _u8p, _u8p, C.c_int, C.c_int, _f32p, _f32p, _P, _P, _P, C.c_float]
         L.orc_gen_key.argtypes = [C.c_uint64, C.c_uint32, C.c_uint32, C.c_uint32]
         L.orc_gen_key.restype = C.c_uint64
@@ -145,6 +149,21 @@ class Oracle:
                               np.ascontiguousarray(q, dtype=np.int8), np.ascontiguousarray(d, dtype=np.float32), y)
         return y
 
+    def row_bytes32(self, t, k) -> int:
+        return int(self.lib.orc_row_bytes32(t, k))
+
+    def dequant32(self, t, row, kb):
+        out = np.zeros(32, np.float64)
+        self.lib.orc_dequant32(t, np.ascontiguousarray(row, dtype=np.uint8).reshape(-1), kb, out)
+        return out
+
+    def hc_post(self, y, res, post, comb, D, H, T):
+        """sycl/hc/core.hpp:81-86: y [T, D], res [T, H, D], post [T, 8], comb [T, 64] -> [T, H, D]."""
+        out = np.zeros((T, H, D), np.float32)
+        self.lib.orc_hc_post(*(np.ascontiguousarray(a, dtype=np.float32).reshape(-1) for a in (y, res, post, comb)),
+                             D, H, T, out.reshape(-1))
+        return out
+
     def expert32(self, types, gate, up, down, dim, ff, x, intermediates=False, limit=0.0):
         y = np.zeros(dim, np.float32)
         g = np.zeros(ff, np.float32); u = np.zeros(ff, np.float32); h = np.zeros(ff, np.float32)
@@ -209,7 +228,8 @@ class Reference:
         L.ref_nearest.argtypes = [C.c_float]
         L.ref_nearest.restype = C.c_int
         L.ref_table.argtypes = [C.c_int, _u64p]
-        L.ref_decode.argtypes = [C.c_int, _u8p, C.c_int, _i32p, _i32p, C.POINTER(C.c_float)]
+        L.ref_decode.argtypes = [C.c_int, _u8p, C.c_int, _i32p, _i32p, C.POINTER(C.c_float), _P]
+        L.ref_hc_post.argtypes = [_f32p, _f32p, _f32p, _f32p, C.c_int, C.c_int, C.c_int, _f32p]
         L.ref_matvec.argtypes = [C.c_int, _u8p, C.c_int, C.c_int, _P, _f32p, C.c_int]
         L.ref_combine.argtypes = [_i32p, _f32p, C.c_int, _f32p, C.c_int, _f32p, _f32p]
         L.ref_route.argtypes = [_f32p, C.c_int, _f32p, C.c_int, C.c_int, C.c_int, C.c_float, _i32p, _f32p]
@@ -250,9 +270,21 @@ class Reference:
         return out
 
     def decode(self, t, row, kb):
+        q, s, d, _ = self.decode_full(t, row, kb)
+        return q, s, d
+
+    def decode_full(self, t, row, kb):
+        """core.hpp decode: values, per-16 scales, d, per-16 min terms."""
         q = np.zeros(32, dtype=np.int32); s = np.zeros(2, dtype=np.int32); d = C.c_float()
-        self.lib.ref_decode(t, np.ascontiguousarray(row), kb, q, s, C.byref(d))
-        return q, s, d.value
+        m = np.zeros(2, dtype=np.float32)
+        self.lib.ref_decode(t, np.ascontiguousarray(row), kb, q, s, C.byref(d), m.ctypes.data)
+        return q, s, d.value, m
+
+    def hc_post(self, y, res, post, comb, D, H, T):
+        out = np.zeros((T, H, D), np.float32)
+        self.lib.ref_hc_post(*(np.ascontiguousarray(a, dtype=np.float32).reshape(-1) for a in (y, res, post, comb)),
+                             D, H, T, out.reshape(-1))
+        return out
 
     def expert(self, types, gate, up, down, dim, ff, x, threads=8, limit=0.0):
         y = np.zeros(dim, dtype=np.float32)

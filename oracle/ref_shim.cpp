@@ -8,6 +8,7 @@
 //   sycl/moe/core.hpp (+ format.hpp, tables.hpp):     per-32 decoder
 //   warm/other_combine.hpp:                             fixed-order combine
 //   sycl/route/route.hpp, route.cpp (compiled alongside): route_cpu
+//   sycl/hc/core.hpp:                                   hyper-connection post
 #include <array>
 #include <cmath>
 #include <atomic>
@@ -20,6 +21,7 @@
 #include "core.hpp"
 #include "other_combine.hpp"
 #include "route.hpp"
+#include "hc/core.hpp"
 
 namespace q = strata::wiring::q8k;
 namespace m = strata::ds4::moe;
@@ -40,12 +42,29 @@ void ref_table(int which, uint64_t* out) {
     else if (which == 2) std::memcpy(out, q::iq1s_grid, sizeof q::iq1s_grid);
     else for (int i = 0; i < 128; ++i) out[i] = q::ksigns_iq2xs[i];
 }
-// Per-32 decode of sub-block kb of one row (types: 16, 17, 29).
-void ref_decode(int t, const uint8_t* row, int kb, int* q32, int* s2, float* d) {
-    const m::Type ty = t == 16 ? m::Type::iq2_xxs : t == 17 ? m::Type::iq2_xs : m::Type::iq1_m;
-    const auto s = m::decode(ty, row, kb);
+static m::Type ref_type(int t) {
+    switch (t) {
+    case 16: return m::Type::iq2_xxs;
+    case 17: return m::Type::iq2_xs;
+    case 8: return m::Type::q8_0;
+    case 12: return m::Type::q4_k;
+    case 13: return m::Type::q5_k;
+    case 14: return m::Type::q6_k;
+    default: return m::Type::iq1_m;
+    }
+}
+// Per-32 decode of sub-block kb of one row (types 16, 17, 29, 8, 12, 13, 14);
+// m2 (may be null) receives the two per-16 min terms.
+void ref_decode(int t, const uint8_t* row, int kb, int* q32, int* s2, float* d, float* m2) {
+    const auto s = m::decode(ref_type(t), row, kb);
     for (int j = 0; j < 32; ++j) q32[j] = s.q[j];
     s2[0] = s.s[0]; s2[1] = s.s[1]; *d = s.d;
+    if (m2) { m2[0] = s.m[0]; m2[1] = s.m[1]; }
+}
+// hc_scalar::post over T tokens x D values.
+void ref_hc_post(const float* y, const float* res, const float* post, const float* comb, int D, int H, int T, float* out) {
+    for (int t = 0; t < T; ++t)
+        for (int e = 0; e < D; ++e) strata::ds4::hc_scalar::post(y, res, post, comb, D, H, t, e, out);
 }
 // Matvec over threads with the reference's dot, rows split in 64-row jobs.
 void ref_matvec(int t, const uint8_t* w, int n, int k, const void* a, float* y, int threads) {
@@ -79,7 +98,7 @@ struct RefMath {
     static float max(float a, float b) { return std::fmax(a, b); }
 };
 float ref_row32(int t, const uint8_t* row, int k, const int8_t* xq, const float* xd) {
-    const m::Type ty = t == 16 ? m::Type::iq2_xxs : t == 17 ? m::Type::iq2_xs : m::Type::iq1_m;
+    const m::Type ty = ref_type(t);
     std::array<float, 32> lane;
     for (int l = 0; l < 32; ++l) lane[size_t(l)] = m::lane<RefMath>(ty, row, k, nullptr, xq, xd, l, true);
     for (int o = 16; o; o >>= 1) {

@@ -257,22 +257,94 @@ void orc_quant32(const float* x, int k, int8_t* q, float* d) {
         for (int j = 0; j < 32; ++j) q[32 * b + j] = (int8_t)(am > 0.0f ? (int)nearbyintf(x[32 * b + j] / d[b]) : 0);
     }
 }
+/* ---- per32 dense formats (the shared-expert matrices) ---------------------
+ * ggml block layouts (sycl/moe/format.hpp:10-45 names and sizes; sub-block
+ * decode as sycl/moe/core.hpp:17,47-58 reads them):
+ *   Q8_0 (8)  34 B per 32: fp16 d, int8 q[32]; value d * q.
+ *   Q4_K (12) 144 B per 256: fp16 d, fp16 dmin, 12 packed 6-bit (scale, min)
+ *             pairs, 128 B of nibbles (sub-blocks 2i, 2i+1 = low, high nibbles
+ *             of bytes 32i..32i+31); value d * sc * q - dmin * m.
+ *   Q5_K (13) 176 B: as Q4_K plus 32 B of fifth bits before the nibbles (bit
+ *             ib of byte j is the fifth bit of value j of sub-block ib).
+ *   Q6_K (14) 210 B: 128 B low nibbles, 64 B of 2-bit highs, 16 int8 scales
+ *             (one per 16 values), fp16 d last; value d * sc * (q - 32). */
+typedef struct { int q[32]; int s[2]; float d; float m[2]; int has_min; } p32_sub;
+
+static int p32_block_bytes(int t) {
+    switch (t) { case 8: return 34; case 12: return 144; case 13: return 176; case 14: return 210; default: return orc_block_bytes(t); }
+}
+static int p32_subs_per_block(int t) { return t == 8 ? 1 : 8; }
+int orc_row_bytes32(int t, int k) { return (k / (32 * p32_subs_per_block(t))) * p32_block_bytes(t); }
+
+/* ggml's 6-bit (scale, min) unpacking of K-quant sub-block j from 12 bytes. */
+static void kq_scale_min(const uint8_t* sc, int j, int* scale, int* mn) {
+    if (j < 4) { *scale = sc[j] & 63; *mn = sc[j + 4] & 63; }
+    else { *scale = (sc[j + 4] & 15) | ((sc[j - 4] >> 6) << 4); *mn = (sc[j + 4] >> 4) | ((sc[j] >> 6) << 4); }
+}
+
+static void p32_sub_get(int t, const uint8_t* row, int kb, p32_sub* s) {
+    const uint8_t* blk = row + (size_t)(kb / p32_subs_per_block(t)) * p32_block_bytes(t);
+    const int ib = kb & 7;
+    memset(s, 0, sizeof *s);
+    s->s[0] = s->s[1] = 1;
+    if (t == 8) {
+        s->d = orc_half(u16(blk));
+        for (int j = 0; j < 32; ++j) s->q[j] = (int8_t)blk[2 + j];
+    } else if (t == 12 || t == 13) {
+        int sc, mn;
+        kq_scale_min(blk + 4, ib, &sc, &mn);
+        s->s[0] = s->s[1] = sc;
+        s->d = orc_half(u16(blk));
+        s->m[0] = s->m[1] = orc_half(u16(blk + 2)) * (float)mn;
+        s->has_min = 1;
+        const uint8_t* nib = blk + (t == 13 ? 48 : 16) + 32 * (ib >> 1);
+        for (int j = 0; j < 32; ++j) {
+            int q = (nib[j] >> (4 * (ib & 1))) & 15;
+            if (t == 13) q |= ((blk[16 + j] >> ib) & 1) << 4;
+            s->q[j] = q;
+        }
+    } else if (t == 14) {
+        const int h = ib >> 2, quarter = ib & 3;
+        const uint8_t* lo = blk + 64 * h + ((quarter & 1) ? 32 : 0);
+        const uint8_t* hi = blk + 128 + 32 * h;
+        for (int j = 0; j < 32; ++j)
+            s->q[j] = (((lo[j] >> (4 * (quarter >> 1))) & 15) | (((hi[j] >> (2 * quarter)) & 3) << 4)) - 32;
+        s->s[0] = (int8_t)blk[192 + 8 * h + 2 * quarter];
+        s->s[1] = (int8_t)blk[193 + 8 * h + 2 * quarter];
+        s->d = orc_half(u16(blk + 208));
+    } else {
+        p32_decode(t, blk, ib, s->q, s->s);
+        s->d = p32_scale(t, blk);
+    }
+}
+
 /* One row (core.hpp:66-87 lane<> + sub_dot<>, expert_check.cpp:50-55): lane
- * l of 32 takes sub-blocks l, l + 32, ...: dot = (d * 0.125) * float(s0 * a +
- * s1 * b) (a, b: the integer dots of the two 16-value halves), acc = fma(xd,
- * dot, acc); then lane[l] = old[l] + old[l ^ o] for o = 16, 8, 4, 2, 1, and
- * lane 0 + 0. */
+ * l of 32 takes sub-blocks l, l + 32, ...: dot = d * float(s0 * a + s1 * b)
+ * (a, b: the integer dots of the two 16-value halves; IQ types d = fp16 d *
+ * 0.125), for Q4_K / Q5_K minus the min term as two fmas (corr = fma(m0,
+ * float(sum x[0..15]), m1 * float(sum x[16..31])), dot = fma(d, float(s0 * a +
+ * s1 * b), -corr)), acc = fma(xd, dot, acc); Q8_0: acc = fma(d * xd,
+ * float(dot32), acc). Then lane[l] = old[l] + old[l ^ o] for o = 16, 8, 4, 2,
+ * 1, and lane 0 + 0. */
 float orc_row32(int t, const uint8_t* row, int k, const int8_t* xq, const float* xd) {
     float lane[32];
-    const int bb = orc_block_bytes(t);
     for (int l = 0; l < 32; ++l) {
         float acc = 0.0f;
         for (int kb = l; kb < k / 32; kb += 32) {
-            const uint8_t* blk = row + (size_t)(kb / 8) * bb;
-            int val[32], sc[2], a = 0, b = 0;
-            p32_decode(t, blk, kb & 7, val, sc);
-            for (int j = 0; j < 16; ++j) { a += val[j] * xq[32 * kb + j]; b += val[16 + j] * xq[32 * kb + 16 + j]; }
-            const float dot = p32_scale(t, blk) * (float)(sc[0] * a + sc[1] * b);
+            p32_sub s;
+            p32_sub_get(t, row, kb, &s);
+            const int8_t* x = xq + 32 * kb;
+            int a = 0, b = 0, sa = 0, sb = 0;
+            for (int j = 0; j < 16; ++j) { a += s.q[j] * x[j]; b += s.q[16 + j] * x[16 + j]; sa += x[j]; sb += x[16 + j]; }
+            if (t == 8) {
+                acc = fmaf(s.d * xd[kb], (float)(a + b), acc);
+                continue;
+            }
+            float dot = s.d * (float)(s.s[0] * a + s.s[1] * b);
+            if (s.has_min) {
+                const float corr = fmaf(s.m[0], (float)sa, s.m[1] * (float)sb);
+                dot = fmaf(s.d, (float)(s.s[0] * a + s.s[1] * b), -corr);
+            }
             acc = fmaf(xd[kb], dot, acc);
         }
         lane[l] = acc;
@@ -285,8 +357,18 @@ float orc_row32(int t, const uint8_t* row, int k, const int8_t* xq, const float*
     return 1.0f * lane[0] + 0.0f;
 }
 void orc_matvec32(int t, const uint8_t* w, int n, int k, const int8_t* xq, const float* xd, float* y) {
-    const size_t rb = (size_t)(k / 256) * orc_block_bytes(t);
+    const size_t rb = (size_t)orc_row_bytes32(t, k);
     for (int r = 0; r < n; ++r) y[r] = orc_row32(t, w + (size_t)r * rb, k, xq, xd);
+}
+/* Dequantized sub-block kb of one row, in double: (value_j)_j with the per-16
+ * scales and mins applied (for the independent float64 checks). */
+void orc_dequant32(int t, const uint8_t* row, int kb, double* out) {
+    p32_sub s;
+    p32_sub_get(t, row, kb, &s);
+    for (int j = 0; j < 32; ++j) {
+        const int h = j / 16;
+        out[j] = t == 8 ? (double)s.d * s.q[j] : (double)s.d * s.s[h] * s.q[j] - (s.has_min ? (double)s.m[h] : 0.0);
+    }
 }
 /* The per32 expert chain: Q32(x), gate and up rows, SwiGLU (core.hpp:88, the
  * same form as q8k_core.hpp:92-95), Q32(h), down rows. g, u, h may be NULL. */
@@ -389,6 +471,23 @@ void orc_combine(const int32_t* ids, const float* w, int k, const float* rows, i
     }
     if (shared)
         for (int c = 0; c < dim; ++c) out[c] += shared[c];
+}
+
+/* ---- hyper-connection post (sycl/hc/core.hpp:81-86, hc.cpp:107-110) --------
+ * T tokens, H <= 4 residual streams of D: out[t][k][e] = post[t][k] * y[t][e]
+ * + comb[t][j][k] * res[t][j][e] for j = 0..H-1, accumulated in that order with
+ * separate roundings. post: T x 8 floats, comb: T x 64 (row j, column k at
+ * j * H + k). */
+void orc_hc_post(const float* y, const float* res, const float* post, const float* comb, int D, int H, int T, float* out) {
+    for (int t = 0; t < T; ++t)
+        for (int e = 0; e < D; ++e) {
+            const float v = y[(size_t)t * D + e];
+            for (int k = 0; k < H; ++k) {
+                float a = post[t * 8 + k] * v;
+                for (int j = 0; j < H; ++j) a += comb[t * 64 + j * H + k] * res[((size_t)t * H + j) * D + e];
+                out[((size_t)t * H + k) * D + e] = a;
+            }
+        }
 }
 
 /* ---- router: route.cpp:15-37 ---------------------------------------------

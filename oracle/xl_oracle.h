@@ -75,6 +75,10 @@ uint64_t orc_gen_key(uint64_t seed, uint32_t layer, uint32_t expert, uint32_t ro
  * blocks of 32 (q int8, one f32 scale each), per-sub-block float dots summed by
  * 32 strided lanes and a butterfly. */
 void orc_quant32(const float* x, int k, int8_t* q, float* d);
+/* Row bytes of a per32 matrix: IQ types (16, 17, 29) and the dense formats
+ * Q8_0 (8), Q4_K (12), Q5_K (13), Q6_K (14) of the shared-expert matrices. */
+int orc_row_bytes32(int type, int k);
+void orc_dequant32(int type, const uint8_t* row, int kb, double* out);
 float orc_row32(int type, const uint8_t* row, int k, const int8_t* xq, const float* xd);
 void orc_matvec32(int type, const uint8_t* w, int n, int k, const int8_t* xq, const float* xd, float* y);
 void orc_expert32(const int types[3], const uint8_t* gate, const uint8_t* up, const uint8_t* down, int dim, int ff,
@@ -91,6 +95,9 @@ void orc_gen_matrix(int type, uint64_t seed, uint32_t layer, uint32_t expert, ui
 /* Expanded codebooks (u64 rows) and the ksigns table, for table checks. */
 void orc_codebook(int which, uint64_t* out); /* 0: iq2xxs[256] 1: iq2xs[512] 2: iq1s[2048] */
 uint8_t orc_ksigns(int i);
+
+/* Hyper-connection post (sycl/hc/core.hpp:81-86) of T tokens, H streams of D. */
+void orc_hc_post(const float* y, const float* res, const float* post, const float* comb, int D, int H, int T, float* out);
 
 #ifdef __cplusplus
 }

@@ -116,6 +116,25 @@ def main():
             rows = orc.gen_matrix(t, 0x32, 0, 0, 0, 4, k).reshape(4, -1)
             out[f"row32_{t}_{k}_q"], out[f"row32_{t}_{k}_d"], out[f"row32_{t}_{k}_rows"] = q, d, rows
             out[f"row32_{t}_{k}_y"] = np.array([ref.row32(t, rows[r], k, q, d) for r in range(4)], np.float32)
+    # per32 rows of the dense shared-expert formats (Q8_0, Q4_K, Q5_K, Q6_K) at
+    # k = 1024 (own generator, so the vectors above keep their values).
+    from tests.dense import dense_matrix
+    rng2 = np.random.default_rng(0xD3)
+    for t in (8, 12, 13, 14):
+        k = 1024
+        x = (rng2.standard_normal(k) * 2.0).astype(np.float32)
+        q, d = orc.quant32(x)
+        rows = dense_matrix(t, 4, k, seed=t).reshape(4, -1)
+        out[f"row32_{t}_{k}_q"], out[f"row32_{t}_{k}_d"], out[f"row32_{t}_{k}_rows"] = q, d, rows
+        out[f"row32_{t}_{k}_y"] = np.array([ref.row32(t, rows[r], k, q, d) for r in range(4)], np.float32)
+    # hyper-connection post (sycl/hc/core.hpp:81-86): T = 2 tokens, H = 4 streams, D = 64
+    T, H, D = 2, 4, 64
+    hy = rng2.standard_normal((T, D)).astype(np.float32)
+    hres = rng2.standard_normal((T, H, D)).astype(np.float32)
+    hpost = (rng2.random((T, 8)) * 2).astype(np.float32)
+    hcomb = rng2.random((T, 64)).astype(np.float32)
+    out["hc_y"], out["hc_res"], out["hc_post"], out["hc_comb"] = hy, hres, hpost, hcomb
+    out["hc_out"] = ref.hc_post(hy, hres, hpost, hcomb, D, H, T)
     np.savez_compressed(OUT, **out)
     print("wrote", OUT, sum(v.nbytes for v in out.values()), "bytes")
 

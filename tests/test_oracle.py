@@ -313,3 +313,65 @@ def test_expert_chain_vs_reference_with_limit(orc, ref, rng, limit):
         assert not np.array_equal(y, orc.expert(t3, *mats, dim, ff, x))
         want = [orc.swiglu(min(a, limit), min(max(b, -limit), limit)) for a, b in zip(g, u)]
         assert np.array_equal(h, np.array(want, np.float32))
+
+
+# ---- per32 dense formats (shared-expert matrices) and hc_post ------------------
+@pytest.mark.parametrize("t", [8, 12, 13, 14])
+def test_row32_dense_vs_reference_and_float64(orc, ref, t, rng):
+    from tests.dense import dense_matrix
+    for k in (256, 1024, 4096):
+        x = (rng.standard_normal(k) * 3.0).astype(np.float32)
+        q, d = orc.quant32(x)
+        n = 5
+        w = dense_matrix(t, n, k, seed=k)
+        rb = orc.row_bytes32(t, k)
+        assert w.size == n * rb
+        y = orc.matvec32(t, w, n, k, q, d)
+        for r in range(n):
+            row = w[r * rb:(r + 1) * rb]
+            assert np.float32(y[r]).view(np.uint32) == np.float32(ref.row32(t, row, k, q, d)).view(np.uint32), (t, k, r)
+            tot = 0.0
+            for kb in range(k // 32):
+                vals, sc, dd, mm = ref.decode_full(t, row, kb)
+                deq = (float(dd) * vals.astype(np.float64) if t == 8 else
+                       float(dd) * np.repeat(sc, 16) * vals - np.repeat(mm.astype(np.float64), 16))
+                assert np.allclose(orc.dequant32(t, row, kb), deq, rtol=1e-12, atol=0), (t, kb)
+                tot += float(d[kb]) * float(np.dot(deq, q[32 * kb:32 * kb + 32]))
+            assert abs(y[r] - tot) <= 2e-5 * (np.abs(y).max() + 1e-3), (t, k, r, y[r], tot)
+
+
+def test_row32_dense_golden(orc):
+    for t in (8, 12, 13, 14):
+        q, d, rows = GOLD[f"row32_{t}_1024_q"], GOLD[f"row32_{t}_1024_d"], GOLD[f"row32_{t}_1024_rows"]
+        got = np.array([orc.row32(t, rows[r], 1024, q, d) for r in range(rows.shape[0])], np.float32)
+        assert np.array_equal(got.view(np.uint32), GOLD[f"row32_{t}_1024_y"].view(np.uint32)), t
+
+
+def test_hc_post_reference_golden_and_closed_form(orc, ref, rng):
+    T, H, D = 3, 4, 96
+    y = rng.standard_normal((T, D)).astype(np.float32)
+    res = rng.standard_normal((T, H, D)).astype(np.float32)
+    post = rng.random((T, 8)).astype(np.float32) * 2
+    comb = rng.random((T, 64)).astype(np.float32)
+    got = orc.hc_post(y, res, post, comb, D, H, T)
+    assert np.array_equal(got.view(np.uint32), ref.hc_post(y, res, post, comb, D, H, T).view(np.uint32))
+    g = {k: GOLD[f"hc_{k}"] for k in ("y", "res", "post", "comb", "out")}
+    Tg, Hg, Dg = g["out"].shape
+    assert np.array_equal(orc.hc_post(g["y"], g["res"], g["post"], g["comb"], Dg, Hg, Tg).view(np.uint32),
+                          g["out"].view(np.uint32))
+    # post = 1, comb = identity: out[k] = y + res[k], one rounding
+    eye = np.zeros((T, 64), np.float32)
+    for k in range(H):
+        eye[:, k * H + k] = 1.0
+    out = orc.hc_post(y, res, np.ones((T, 8), np.float32), eye, D, H, T)
+    assert np.array_equal(out, (y[:, None, :] + res).astype(np.float32))
+    # a transposed comb (k * H + j) gives a different answer
+    assert not np.array_equal(got, orc.hc_post(y, res, post, _transpose_comb(comb, H), D, H, T))
+
+
+def _transpose_comb(comb, H):
+    c = comb.copy()
+    for j in range(H):
+        for k in range(H):
+            c[:, j * H + k] = comb[:, k * H + j]
+    return c

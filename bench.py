@@ -63,6 +63,25 @@ def expert_bytes(t3) -> int:
     return FF * (DIM // 256) * (BYTES[t3[0]] + BYTES[t3[1]]) + DIM * (FF // 256) * BYTES[t3[2]]
 
 
+SHARED_T = (13, 13, 14)    # config 5 shared expert: Q5_K gate/up, Q6_K down (the pack's K-quants)
+DENSE_BYTES = {8: 34, 12: 144, 13: 176, 14: 210}
+DENSE_VALUES = {8: 32, 12: 256, 13: 256, 14: 256}
+HC_H = 4                   # hyper-connection streams
+
+
+def dense_bytes(t, n, k) -> int:
+    return n * (k // DENSE_VALUES[t]) * DENSE_BYTES[t]
+
+
+def dense_matrix(t, n, k, rng):
+    """Uniform random ggml blocks of a dense format with finite fp16 scales in [1e-3, 1e-2)."""
+    nb = n * (k // DENSE_VALUES[t])
+    blk = rng.integers(0, 256, size=(nb, DENSE_BYTES[t]), dtype=np.uint8)
+    for off in {8: (0,), 12: (0, 2), 13: (0, 2), 14: (208,)}[t]:
+        blk[:, off:off + 2] = rng.uniform(1e-3, 1e-2, nb).astype(np.float16).view(np.uint8).reshape(nb, 2)
+    return blk.reshape(-1)
+
+
 def measured_traffic():
     """HBM bytes per layer launch from the committed counter summary, or None."""
     try:
@@ -162,7 +181,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=0, help="timed steps (default: 2000 layers' worth)")
     ap.add_argument("--warmup", type=int, default=-1)
-    ap.add_argument("--config", type=int, default=1, choices=(0, 1, 2, 3, 4))
+    ap.add_argument("--config", type=int, default=1, choices=(0, 1, 2, 3, 4, 5))
     ap.add_argument("--tokens", type=int, default=512, help="config 4: tokens per grouped call")
     ap.add_argument("--device-route", action="store_true",
                     help="configs 1, 4: route each step on the GPU from N(0,1) logits (route.cpp router: "
@@ -226,6 +245,14 @@ def main():
         ids, w, x = routes(n_r, SEED)
         ids, w = ids[:, None, :], w[:, None, :]
     k = ids.shape[2]
+    blk = None
+    if cfg == 5:   # the MoE block around the layer: shared FFN, hc_post inputs
+        srng = np.random.default_rng(SEED + 5)
+        blk = {"mats": [dense_matrix(SHARED_T[0], FF, DIM, srng), dense_matrix(SHARED_T[1], FF, DIM, srng),
+                        dense_matrix(SHARED_T[2], DIM, FF, srng)],
+               "res": srng.standard_normal((n_r, HC_H, DIM)).astype(np.float32),
+               "post": (srng.random((n_r, 8)) * 2).astype(np.float32),
+               "comb": srng.random((n_r, 64)).astype(np.float32)}
     droute = args.device_route and cfg in (1, 4)
     if droute:   # fresh N(0,1) logits per route; the ids / weights come from the device router
         lrng = np.random.default_rng(SEED + 7)
@@ -241,6 +268,9 @@ def main():
     else:
         step_bytes = np.array([sum(expert_bytes(types[l, e]) for l in range(L) for e in ids[r, l]) + L * 2 * DIM * 4
                                for r in range(n_r)], np.float64)
+    if cfg == 5:   # + shared matrices, the shared row out and in, hc_post's y, res, post, comb, out
+        step_bytes += (dense_bytes(SHARED_T[0], FF, DIM) + dense_bytes(SHARED_T[1], FF, DIM)
+                       + dense_bytes(SHARED_T[2], DIM, FF) + 2 * DIM * 4 + DIM * 4 + 2 * HC_H * DIM * 4 + 72 * 4)
     bytes_per_step = float(step_bytes[used].mean())
 
     # A dedicated (non-default) stream: the library launches on it and the
@@ -256,6 +286,12 @@ def main():
         d_out = torch.zeros((n_r, TOK, DIM) if cfg == 4 else (n_r, DIM), dtype=torch.float32, device="cuda")
         d_logits = torch.from_numpy(logits).cuda() if droute else None
         d_y32 = torch.zeros((K, DIM), dtype=torch.float32, device="cuda") if args.per32 else None
+        if blk:
+            d_mats = [torch.from_numpy(m).cuda() for m in blk["mats"]]
+            d_res, d_post, d_comb = (torch.from_numpy(blk[key]).cuda() for key in ("res", "post", "comb"))
+            d_sh = torch.zeros((1, DIM), dtype=torch.float32, device="cuda")
+            d_h2 = torch.zeros((HC_H, DIM), dtype=torch.float32, device="cuda").view(1, HC_H, DIM)
+            d_work = torch.empty(xl.shared_work_bytes(DIM, FF, 1), dtype=torch.uint8, device="cuda")
     torch.cuda.synchronize()
 
     def step(i):
@@ -268,6 +304,12 @@ def main():
             return
         if cfg == 4:
             lane.grouped_forward_async(0, d_ids[r], d_w[r], d_x[r], d_out[r], stream=sp)
+            return
+        if cfg == 5:   # shared FFN -> routed layer (+ shared row) -> hc_post, one stream
+            lane.shared_forward_async(SHARED_T, *d_mats, FF, d_x[r], d_sh, d_work, stream=sp)
+            lane.layer_forward_async(0, d_ids[r, 0], d_w[r, 0], d_x[r], d_out[r], shared=d_sh, stream=sp)
+            lane.hc_post_async(d_out[r].view(1, DIM), d_res[r:r + 1], d_post[r:r + 1], d_comb[r:r + 1], d_h2,
+                               stream=sp)
             return
         if args.per32:
             lane.layer_forward_per32_async(0, d_ids[r, 0], d_x[r], d_y32, w=d_w[r, 0], out=d_out[r], stream=sp)
@@ -308,12 +350,15 @@ def main():
     kernel = {0: "xl::dev::stream_kernel (single-launch layer)", 1: "xl::dev::stream_kernel (single-launch layer)",
               4: "grouped path (bucket, Q8_K, gu_kernel, Q8_K, dn_kernel, combine: 6 launches per step)"}.get(
         cfg, "xl::dev::layer3_kernel (all-types single-launch layer)")
+    if cfg == 5:
+        kernel = ("MoE block: shared FFN (quant32, mv32 gate+up, swiglu32, quant32, mv32 down) + stream_kernel "
+                  "+ hc_post_kernel: 7 launches per step")
     if args.per32:
         kernel = "per32 chain (quant32, mv32 gate+up, swiglu32, quant32, mv32 down, combine: 6 launches per step)"
     traffic = measured_traffic() if cfg == 1 and not args.per32 else None
 
     cpu = None
-    if not args.no_cpu and not args.per32:   # the CPU baseline times the Q8_K chain
+    if not args.no_cpu and not args.per32 and cfg != 5:   # the CPU baseline times the Q8_K chain
         threads = args.cpu_threads or min(16, os.cpu_count() or 1)
         cpu_layers = args.cpu_layers or {0: 1500, 1: 500, 2: 500, 3: 500, 4: 500}[cfg]
         cpu = cpu_baseline(cpu_layers, threads, config=1 if cfg == 4 else cfg)
@@ -332,6 +377,8 @@ def main():
            "top-6 per layer, hidden carried through RMS normalization",
         4: f"config4: grouped, {TOK} tokens x N(0,1)[4096], per-token top-6 of 384 config-1 experts, "
            "fixed-order combine per token",
+        5: "config5: MoE block of one token: shared-expert FFN (Q5_K gate/up, Q6_K down, 4096x3072, per32), "
+           "config-1 routed layer with the shared row added last, hc_post over 4 streams",
     }
     line = {
         "metric": "routed-expert µs/layer (top-6, batch 1) + achieved HBM GB/s vs MI355X peak",

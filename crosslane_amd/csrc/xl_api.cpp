@@ -379,10 +379,10 @@ xl::MatRef per32_matrix(int type, const void* base, int n, int k) {
     return m;
 }
 
-// Shared-expert workspace of T tokens: g, u, h (T x ff floats), Q32(x) and
-// Q32(h) quants and scales, each 256-byte aligned.
+// Shared-expert workspace of T tokens: g, u (T x ff floats), Q32(x) and Q32(h)
+// quants and scales, each 256-byte aligned.
 struct SharedWork {
-    uint64_t g, u, h, xq, hq, xd, hd, bytes;
+    uint64_t g, u, xq, hq, xd, hd, bytes;
 };
 SharedWork shared_work(int dim, int ff, int T) {
     SharedWork w{};
@@ -391,7 +391,6 @@ SharedWork shared_work(int dim, int ff, int T) {
     const uint64_t t = uint64_t(T);
     w.g = take(t * ff * 4);
     w.u = take(t * ff * 4);
-    w.h = take(t * ff * 4);
     w.xq = take(t * dim);
     w.hq = take(t * ff);
     w.xd = take(t * (dim / 32) * 4);
@@ -419,10 +418,9 @@ void enqueue_per32(xl_context* ctx, int32_t layer, const int32_t* d_ids, const f
                                    size_t(ff), ctx->tables, ctx->err_flag, s),
               "per32 gate/up launch");
     mark("gate_up32");
-    hip_check(xl::dev::launch_swiglu32(ctx->g, ctx->u, k * ff, ctx->cfg.swiglu_limit, ctx->h, s), "SwiGLU launch");
-    mark("swiglu");
-    hip_check(xl::dev::launch_quant32(ctx->h, k, ff, ctx->hq, hd, ctx->err_flag, s), "quant32(h) launch");
-    mark("quant32_h");
+    hip_check(xl::dev::launch_swiglu_quant32(ctx->g, ctx->u, k, ff, ctx->cfg.swiglu_limit, ctx->hq, hd, s),
+              "SwiGLU + quant32(h) launch");
+    mark("swiglu_quant32");
     hip_check(xl::dev::launch_mv32(descs, d_ids, none, none, k, E, 2, 1, dim, ff, ctx->hq, size_t(ff), hd, size_t(ff / 32),
                                    d_y, nullptr, size_t(dim), ctx->tables, ctx->err_flag, s),
               "per32 down launch");
@@ -1217,7 +1215,6 @@ int32_t xl_shared_forward_async(xl_context* ctx, int32_t type_gate, const void* 
         uint8_t* base = static_cast<uint8_t*>(d_work);
         float* g = reinterpret_cast<float*>(base + w.g);
         float* u = reinterpret_cast<float*>(base + w.u);
-        float* h = reinterpret_cast<float*>(base + w.h);
         int8_t* xq = reinterpret_cast<int8_t*>(base + w.xq);
         int8_t* hq = reinterpret_cast<int8_t*>(base + w.hq);
         float* xd = reinterpret_cast<float*>(base + w.xd);
@@ -1230,8 +1227,8 @@ int32_t xl_shared_forward_async(xl_context* ctx, int32_t type_gate, const void* 
         hip_check(xl::dev::launch_mv32(nullptr, nullptr, mg, mu, T, 0, 0, 2, ff, dim, xq, size_t(dim), xd,
                                        size_t(dim / 32), g, u, size_t(ff), ctx->tables, ctx->err_flag, s),
                   "shared gate/up launch");
-        hip_check(xl::dev::launch_swiglu32(g, u, T * ff, ctx->cfg.swiglu_limit, h, s), "shared SwiGLU launch");
-        hip_check(xl::dev::launch_quant32(h, T, ff, hq, hd, ctx->err_flag, s), "quant32(h) launch");
+        hip_check(xl::dev::launch_swiglu_quant32(g, u, T, ff, ctx->cfg.swiglu_limit, hq, hd, s),
+                  "shared SwiGLU + quant32(h) launch");
         hip_check(xl::dev::launch_mv32(nullptr, nullptr, md, md, T, 0, 0, 1, dim, ff, hq, size_t(ff), hd,
                                        size_t(ff / 32), d_out, nullptr, size_t(dim), ctx->tables, ctx->err_flag, s),
                   "shared down launch");

@@ -173,8 +173,10 @@ hipError_t launch_mv32(const ExpertDesc* descs, const int32_t* ids, const MatRef
 // res[t][j][e]; out may equal res (in place).
 hipError_t launch_hc_post(const float* y, const float* res, const float* post, const float* comb, int D, int H, int T,
                           float* out, hipStream_t s);
-// h = g / (1 + exp(-g)) * u over n values (lim > 0: g, u clamped first).
-hipError_t launch_swiglu32(const float* g, const float* u, int n, float lim, float* h, hipStream_t s);
+// h = g / (1 + exp(-g)) * u (lim > 0: g, u clamped first) of rows x k values,
+// quantized per 32 into q, d exactly as launch_quant32 would quantize h.
+hipError_t launch_swiglu_quant32(const float* g, const float* u, int rows, int k, float lim, int8_t* q, float* d,
+                                 hipStream_t s);
 // Seeded generation of one planar matrix (role 0 gate, 1 up, 2 down).
 hipError_t launch_generate(uint8_t* base, int type, int n, int k, uint64_t seed, uint32_t layer, uint32_t expert,
                            uint32_t role, hipStream_t s);

@@ -10,8 +10,10 @@
 //                   float(s0 * a + s1 * b) (a, b: the integer dots of the two
 //                   16-weight halves, s: odd sub-scales), acc = fma(xd, dot,
 //                   acc); then a 16-8-4-2-1 butterfly and lane 0 + 0
-//   swiglu32_kernel g / (1 + exp(-g)) * u (the device's expf; g and u clamped
-//                   first when the SwiGLU limit is set)
+//   swiglu_quant32_kernel
+//                   h = g / (1 + exp(-g)) * u (the device's expf; g and u
+//                   clamped first when the SwiGLU limit is set), quantized per
+//                   32 as quant32_kernel does
 //
 // The bank's planar blocks are decoded directly (xl_format.hpp layout); the
 // codebooks come from the context's expanded tables. The dense formats of the
@@ -251,10 +253,21 @@ __global__ __launch_bounds__(256) void mv32_kernel(const ExpertDesc* __restrict_
     if (row < n && l == 0) y[pick * y_stride + row] = __fadd_rn(acc, 0.0f);
 }
 
-__global__ __launch_bounds__(256) void swiglu32_kernel(const float* __restrict__ g, const float* __restrict__ u, int n,
-                                                       float lim, float* __restrict__ h) {
+// h = SwiGLU(g, u) (limit applied) quantized per 32 as quant32_kernel does, in
+// one pass: the same h values, the same quants and scales, no h round trip.
+__global__ __launch_bounds__(256) void swiglu_quant32_kernel(const float* __restrict__ g, const float* __restrict__ u,
+                                                             int nblk, float lim, int8_t* __restrict__ q,
+                                                             float* __restrict__ d) {
     const int i = blockIdx.x * 256 + threadIdx.x;
-    if (i < n) h[i] = silu_mul3(g[i], u[i], lim);
+    const bool in = (i >> 5) < nblk;
+    const float v = in ? silu_mul3(g[i], u[i], lim) : 0.0f;
+    float am = fabsf(v);
+#pragma unroll
+    for (int o = 16; o > 0; o >>= 1) am = fmaxf(am, __shfl_xor(am, o, 32));
+    if (!in) return;
+    const float sc = __fdiv_rn(am, 127.0f);
+    q[i] = int8_t(am > 0.0f ? __float2int_rn(__fdiv_rn(v, sc)) : 0);
+    if ((i & 31) == 0) d[i >> 5] = sc;
 }
 
 }  // namespace
@@ -276,8 +289,11 @@ hipError_t launch_mv32(const ExpertDesc* descs, const int32_t* ids, const MatRef
     return hipGetLastError();
 }
 
-hipError_t launch_swiglu32(const float* g, const float* u, int n, float lim, float* h, hipStream_t s) {
-    hipLaunchKernelGGL(swiglu32_kernel, dim3((n + 255) / 256), dim3(256), 0, s, g, u, n, lim, h);
+hipError_t launch_swiglu_quant32(const float* g, const float* u, int rows, int k, float lim, int8_t* q, float* d,
+                                 hipStream_t s) {
+    if (rows < 1 || k < 32 || k % 32) return hipErrorInvalidValue;
+    const int nblk = rows * (k / 32);
+    hipLaunchKernelGGL(swiglu_quant32_kernel, dim3((nblk * 32 + 255) / 256), dim3(256), 0, s, g, u, nblk, lim, q, d);
     return hipGetLastError();
 }
 

@@ -17,6 +17,9 @@
  *   sycl/route/route.cpp:15-37               router: sqrt(softplus) scores,
  *                                           biased top-k, normalized weights
  *   sycl/moe/cpu_lane.cpp:70-81              64-row jobs over worker threads
+ *   sycl/moe/core.hpp:9-12,17,47-65,80       per32 rows of the dense shared-expert
+ *                                           formats (Q8_0, Q4_K, Q5_K, Q6_K)
+ *   sycl/hc/core.hpp:81-86                   hyper-connection post
  *
  * Parity pins (see tests/): every function here is checked against
  * oracle/_ref (the reference's own q8k_core.hpp / core.hpp / other_combine.hpp

@@ -156,18 +156,21 @@ __device__ __forceinline__ int sum_xxs(const Looks& L, const uint32_t* w, const 
 }
 // IQ2_XS pair (w0..3: 8 codes {sign7 | grid9 << 7}, sc: the pair's two scale
 // bytes): the exact integer sum with the 16-weight scales (q8k_core.hpp:116-140).
-__device__ __forceinline__ int pair_xs(const uint8_t* lds, uint32_t lo_x, uint32_t lo_s, const uint32_t* w, uint32_t sc,
-                                       const uint32_t* a) {
-    uint2 g[8];
-    uint2 m[8];
+// Split like the IQ2_XXS decoder, so that a pass issues the next pair's
+// lookups before the current pair's arithmetic waits on its own.
+__device__ __forceinline__ Looks look_xs(const uint8_t* lds, uint32_t lo_x, uint32_t lo_s, const uint32_t* w) {
+    Looks L;
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
         const uint32_t h = e & 1;
         // grid row * 32 = (code >> 7) << 5: one shift and one v_and_or_b32 with the lane's copy
         const uint32_t sh = h ? (w[e >> 1] >> 18) : (w[e >> 1] >> 2);
-        g[e] = *reinterpret_cast<const uint2*>(lds + ((sh & 0x3fe0u) | lo_x));
-        m[e] = *reinterpret_cast<const uint2*>(lds + perm(w[e >> 1], lo_s, sel_b(2 * h)));
+        L.g[e] = *reinterpret_cast<const uint2*>(lds + ((sh & 0x3fe0u) | lo_x));
+        L.m[e] = *reinterpret_cast<const uint2*>(lds + perm(w[e >> 1], lo_s, sel_b(2 * h)));
     }
+    return L;
+}
+__device__ __forceinline__ int sum_xs(const Looks& L, uint32_t sc, const uint32_t* a) {
     int total = 0;
 #pragma unroll
     for (int s = 0; s < 2; ++s) {
@@ -176,8 +179,8 @@ __device__ __forceinline__ int pair_xs(const uint8_t* lds, uint32_t lo_x, uint32
         for (int q = 0; q < 4; ++q) {
             const int e = 4 * s + q;
             int& acc = q < 2 ? lo : hi;
-            acc = sdot4(xad(g[e].x, m[e].x, m[e].x & 0x01010101u), a[8 * s + 2 * q], acc);
-            acc = sdot4(xad(g[e].y, m[e].y, m[e].y & 0x01010101u), a[8 * s + 2 * q + 1], acc);
+            acc = sdot4(xad(L.g[e].x, L.m[e].x, L.m[e].x & 0x01010101u), a[8 * s + 2 * q], acc);
+            acc = sdot4(xad(L.g[e].y, L.m[e].y, L.m[e].y & 0x01010101u), a[8 * s + 2 * q + 1], acc);
         }
         const uint32_t byte = (sc >> (8 * s)) & 255u;
         total += __mul24(lo, int(2u * (byte & 15u) + 1u)) + __mul24(hi, int(2u * (byte >> 4) + 1u));
@@ -190,6 +193,10 @@ struct Act {
     uint32_t a[P][16];
     float d[P];
 };
+// Q8_K quants staged in LDS: byte o of a row sits at qswz(o), the 16-byte
+// chunk index XORed with bits 1-2 of the pair (64-byte) index, so that lanes
+// reading consecutive pairs hit different banks.
+__device__ __forceinline__ int qswz(int o) { return o ^ (((o >> 7) & 3) << 4); }
 // Activations of pairs lp, lp + L, ... from a Q8_K vector in LDS (quants at
 // base, block scales at base + scl).
 template <int P>
@@ -197,10 +204,9 @@ __device__ __forceinline__ void load_act(Act<P>& A, const uint8_t* lds, int base
 #pragma unroll
     for (int q = 0; q < P; ++q) {
         const int p = lp + L * q;
-        const uint4* src = reinterpret_cast<const uint4*>(lds + base + 64 * p);
 #pragma unroll
         for (int c = 0; c < 4; ++c) {
-            const uint4 v = src[c];
+            const uint4 v = *reinterpret_cast<const uint4*>(lds + base + qswz(64 * p + 16 * c));
             A.a[q][4 * c] = v.x; A.a[q][4 * c + 1] = v.y; A.a[q][4 * c + 2] = v.z; A.a[q][4 * c + 3] = v.w;
         }
         A.d[q] = reinterpret_cast<const float*>(lds + base + scl)[p >> 2];
@@ -225,21 +231,27 @@ __device__ __forceinline__ bool h_ready(const uint4& v) {
 // d = 0 and q = 0. The two divisions run once for all NB blocks (lane m
 // divides for block m); nearest is v_rndne (exact for |is * v| < 2^22) and
 // the quants are packed as q + 128 bytes by v_cvt_pk_u8_f32 (exact integers).
-template <int CTRL>
-__device__ __forceinline__ uint32_t umax_dpp(uint32_t a) {   // lanes the pattern leaves out keep a
-    return max(a, uint32_t(__builtin_amdgcn_update_dpp(int(a), int(a), CTRL, 0xF, 0xF, false)));
+// One DPP max step on every block at once: the NB chains are independent, so
+// each fills the others' DPP wait states. old = 0 is max's identity, which lets
+// the compiler fold the move into v_max_u32_dpp.
+template <int CTRL, int RM, int NB>
+__device__ __forceinline__ void umax_dpp_n(uint32_t (&a)[NB]) {
+#pragma unroll
+    for (int m = 0; m < NB; ++m) a[m] = max(a[m], uint32_t(__builtin_amdgcn_update_dpp(0, int(a[m]), CTRL, RM, 0xF, false)));
 }
-// The wave's largest magnitude as a bit pattern: magnitudes of floats order as
-// their bits do, so integer max needs no NaN canonicalization (a NaN or an
-// infinity wins and is caught by the finiteness test on the result).
-__device__ __forceinline__ uint32_t wave_umax(uint32_t a) {
-    a = umax_dpp<0xB1>(a);
-    a = umax_dpp<0x4E>(a);
-    a = umax_dpp<0x141>(a);
-    a = umax_dpp<0x140>(a);    // every lane: its row's max
-    a = max(a, uint32_t(__builtin_amdgcn_update_dpp(0, int(a), 0x142, 0xA, 0xF, false)));   // rows 1, 3
-    a = max(a, uint32_t(__builtin_amdgcn_update_dpp(0, int(a), 0x143, 0xC, 0xF, false)));   // rows 2, 3
-    return uint32_t(__builtin_amdgcn_readlane(int(a), 63));
+// The wave's largest magnitude of each block, as a bit pattern: magnitudes of
+// floats order as their bits do, so integer max needs no NaN canonicalization
+// (a NaN or an infinity wins and is caught by the finiteness test on the result).
+template <int NB>
+__device__ __forceinline__ void wave_umax_n(uint32_t (&a)[NB], uint32_t (&out)[NB]) {
+    umax_dpp_n<0xB1, 0xF>(a);
+    umax_dpp_n<0x4E, 0xF>(a);
+    umax_dpp_n<0x141, 0xF>(a);
+    umax_dpp_n<0x140, 0xF>(a);   // every lane: its row's max
+    umax_dpp_n<0x142, 0xA>(a);   // rows 1, 3
+    umax_dpp_n<0x143, 0xC>(a);   // rows 2, 3
+#pragma unroll
+    for (int m = 0; m < NB; ++m) out[m] = uint32_t(__builtin_amdgcn_readlane(int(a[m]), 63));
 }
 // Returns false if a value of blocks 0..nvalid-1 is not finite (the others may hold anything).
 // |is * v| <= 127 (1 + 2^-24)^2 < 127.5 for every v of the block, so nearest(is * v)
@@ -248,21 +260,25 @@ template <int NB>
 __device__ __forceinline__ bool q8k_blocks(const uint4 (&hv)[NB], int nvalid, int lane, uint32_t (&packed)[NB],
                                            float (&d)[NB]) {
     bool fin = true;
-    uint32_t am[NB];
-    float mxv = 0.0f;
+    uint32_t x[NB][4], ab[NB][4], am[NB], mxa[NB];
 #pragma unroll
     for (int m = 0; m < NB; ++m) {
         // opaque copies: a select chain over the block's words would otherwise be
         // turned into an indexed load from a stack copy of the block
-        uint32_t x0 = hv[m].x, x1 = hv[m].y, x2 = hv[m].z, x3 = hv[m].w;
-        asm volatile("" : "+v"(x0), "+v"(x1), "+v"(x2), "+v"(x3));
-        const uint32_t a0 = x0 & 0x7fffffffu, a1 = x1 & 0x7fffffffu;
-        const uint32_t a2 = x2 & 0x7fffffffu, a3 = x3 & 0x7fffffffu;
-        am[m] = wave_umax(max(max(a0, a1), max(a2, a3)));
+        x[m][0] = hv[m].x; x[m][1] = hv[m].y; x[m][2] = hv[m].z; x[m][3] = hv[m].w;
+        asm volatile("" : "+v"(x[m][0]), "+v"(x[m][1]), "+v"(x[m][2]), "+v"(x[m][3]));
+#pragma unroll
+        for (int i = 0; i < 4; ++i) ab[m][i] = x[m][i] & 0x7fffffffu;
+        mxa[m] = max(max(ab[m][0], ab[m][1]), max(ab[m][2], ab[m][3]));
+    }
+    wave_umax_n<NB>(mxa, am);
+    float mxv = 0.0f;
+#pragma unroll
+    for (int m = 0; m < NB; ++m) {
         fin = fin & ((m >= nvalid) | (am[m] <= 0x7f7fffffu));
-        const bool e0 = a0 == am[m], e1 = a1 == am[m], e2 = a2 == am[m];
-        const uint32_t sel = e0 ? x0 : e1 ? x1 : e2 ? x2 : x3;
-        const uint64_t hit = __builtin_amdgcn_ballot_w64(e0 | e1 | e2 | (a3 == am[m]));
+        const bool e0 = ab[m][0] == am[m], e1 = ab[m][1] == am[m], e2 = ab[m][2] == am[m];
+        const uint32_t sel = e0 ? x[m][0] : e1 ? x[m][1] : e2 ? x[m][2] : x[m][3];
+        const uint64_t hit = __builtin_amdgcn_ballot_w64(e0 | e1 | e2 | (ab[m][3] == am[m]));
         const int first = int(__builtin_ctzll(hit | (uint64_t(1) << 63)));
         const float mx = __uint_as_float(uint32_t(__builtin_amdgcn_readlane(int(sel), first)));
         mxv = lane == m ? mx : mxv;
@@ -272,11 +288,10 @@ __device__ __forceinline__ bool q8k_blocks(const uint4 (&hv)[NB], int nvalid, in
 #pragma unroll
     for (int m = 0; m < NB; ++m) {
         const float is = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(isv), m));
-        const uint32_t vb[4] = {hv[m].x, hv[m].y, hv[m].z, hv[m].w};
         uint32_t p = 0;
 #pragma unroll
         for (int j = 0; j < 4; ++j)   // q + 128 in 1..255, an exact integer: the byte conversion is exact
-            p = __builtin_amdgcn_cvt_pk_u8_f32(__fadd_rn(__builtin_rintf(__fmul_rn(is, __uint_as_float(vb[j]))), 128.0f), j, p);
+            p = __builtin_amdgcn_cvt_pk_u8_f32(__fadd_rn(__builtin_rintf(__fmul_rn(is, __uint_as_float(x[m][j]))), 128.0f), j, p);
         const bool zero = am[m] == 0u;
         packed[m] = zero ? 0u : p ^ 0x80808080u;
         d[m] = zero ? 0.0f : __int_as_float(__builtin_amdgcn_readlane(__float_as_int(dv), m));
@@ -425,7 +440,7 @@ __global__ __launch_bounds__(NW * 64, 1) void stream_kernel(Layer3Args a) {
         for (int u = 0; u < UX; ++u) {
             const int b = wv + NW * u;
             if (b < nbx) {
-                reinterpret_cast<uint32_t*>(lds + kS_XQ + 256 * b)[lane] = xp[u];
+                *reinterpret_cast<uint32_t*>(lds + kS_XQ + qswz(256 * b + 4 * lane)) = xp[u];
                 if (lane == 0) reinterpret_cast<float*>(lds + kS_XQ + 4096)[b] = xd[u];
             }
         }
@@ -582,11 +597,12 @@ __global__ __launch_bounds__(NW * 64, 1) void stream_kernel(Layer3Args a) {
                         if (bq < nb) {
                             const int blk = b0 + bq, i = blk / nbh, bb = blk - i * nbh;
                             uint8_t* hq = lds + kS_HQ + i * hq_stride;
-                            reinterpret_cast<uint32_t*>(hq + 256 * bb)[lane] = hp[m];
+                            *reinterpret_cast<uint32_t*>(hq + qswz(256 * bb + 4 * lane)) = hp[m];
                             if (lane == 0) reinterpret_cast<float*>(hq + ff)[bb] = hd[m];
                         }
                     }
                 }
+                if (j < 3) mark(17 + j);
                 lds_barrier();
                 mark(25 + 2 * j);
                 if constexpr (j + 2 < MD) h_issue.template operator()<j + 2>();
@@ -595,10 +611,13 @@ __global__ __launch_bounds__(NW * 64, 1) void stream_kernel(Layer3Args a) {
                     const int i = dpick(j);
                     if (j == 0 || i != dpick(j > 0 ? j - 1 : 0)) load_act<PD>(B, lds, kS_HQ + i * hq_stride, ff, lD, LD);
                     float f = 0.0f;
+                    Looks Lx[2];
+                    Lx[0] = look_xs(lds, lo_x, lo_s, rd[j % (WIND + 1)][0].w);
 #pragma unroll
                     for (int q = 0; q < PD; ++q) {
                         const Raw3& D0 = rd[j % (WIND + 1)][q];
-                        const int I = pair_xs(lds, lo_x, lo_s, D0.w, D0.h[0], B.a[q]);
+                        if (q + 1 < PD) Lx[(q + 1) & 1] = look_xs(lds, lo_x, lo_s, rd[j % (WIND + 1)][q + 1].w);
+                        const int I = sum_xs(Lx[q & 1], D0.h[0], B.a[q]);
                         f = fmaf(__fmul_rn(h2f(D0.h[1]), B.d[q]), float(I), f);
                     }
                     float okf = ((dok >> j) & 1u) ? 0.125f : 0.0f;   // opaque, as in gate/up

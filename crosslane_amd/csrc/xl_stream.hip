@@ -502,6 +502,15 @@ __global__ __launch_bounds__(NW * 64, 1) void stream_kernel(Layer3Args a) {
         float bg = 0.0f, bu = 0.0f;   // lane LG-1-b of each row group: slot b of the batch
         int hidx = 0;                 // that slot's h word (pick * ff + row)
         static_for<MG>([&]<int j>() {
+            // The SIMD arbiter favours older waves, so the first NW/2 waves of a
+            // workgroup would finish gate/up well before their SIMD partners (which
+            // then run alone, latency-bound, while the down phase waits for them).
+            // The younger half runs at wave priority 1 for the first two thirds of
+            // its slots, which evens out the finish times.
+            if constexpr (j == 0) {
+                if (wv >= NW / 2) __builtin_amdgcn_s_setprio(1);
+            }
+            if constexpr (j == (2 * MG) / 3) __builtin_amdgcn_s_setprio(0);
             if constexpr (j >= 1 && j + WIN - 1 < MG) load_slot.template operator()<j + WIN - 1>();
             if constexpr (j >= MG - WIND) load_pass.template operator()<j - (MG - WIND)>();   // the down stream starts under the last slots
             float fg = 0.0f, fu = 0.0f;
@@ -539,6 +548,7 @@ __global__ __launch_bounds__(NW * 64, 1) void stream_kernel(Layer3Args a) {
         });
     }
     mark(3);
+    __builtin_amdgcn_s_setprio(0);
 
     // ---- down: step j quantizes the h of the picks it needs, then every wave runs pass j
     float* ys = reinterpret_cast<float*>(lds + kS_Y);

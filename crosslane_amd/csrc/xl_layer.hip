@@ -427,6 +427,11 @@ __global__ __launch_bounds__(NW * 64, 1) void layer3_kernel(Layer3Args a) {
         // Fully unrolled (no break): the per-slot references stay in registers.
 #pragma unroll
         for (int j = 0; j < MG; ++j) {
+            // Older waves win the SIMD arbiter; the younger half of the workgroup
+            // runs at wave priority 1 for two thirds of its slots so that both
+            // halves finish gate/up together (the down phase waits for the last).
+            if (j == 0 && wv >= NW / 2) __builtin_amdgcn_s_setprio(1);
+            if (j == (2 * MG) / 3) __builtin_amdgcn_s_setprio(0);
             if (j < ng) {
                 if (j >= 1 && j + WIN - 1 < MG) load_slot(j + WIN - 1, (j + WIN - 1) % WIN);
                 if (j >= MG - WIND && nd > 0) {   // static position for the common case ng == MG
@@ -447,6 +452,7 @@ __global__ __launch_bounds__(NW * 64, 1) void layer3_kernel(Layer3Args a) {
         }
     }
     mark(3);
+    __builtin_amdgcn_s_setprio(0);
     // waves with fewer slots start their down stream here
 #pragma unroll
     for (int j = 0; j < WIND; ++j)

@@ -203,54 +203,94 @@ __global__ __launch_bounds__(256) void quant32_kernel(const float* __restrict__ 
     if ((i & 31) == 0) d[i >> 5] = sc;
 }
 
-// Rows of one or two roles of every pick: grid (ceil(n / 8), picks, roles), 8
-// rows per 256-thread workgroup, 32 lanes per row. Role role0 + z writes yz.
-// Activations: q + pick * q_stride (k int8), d + pick * d_stride (k / 32
-// scales); output y + pick * y_stride. ids == nullptr: the matrices single0
-// (z = 0) and single1 (z = 1) for every pick.
-__global__ __launch_bounds__(256) void mv32_kernel(const ExpertDesc* __restrict__ descs, const int32_t* __restrict__ ids,
-                                                   MatRef single0, MatRef single1, int n_experts, int role0, int n, int k,
-                                                   const int8_t* __restrict__ q, size_t q_stride,
-                                                   const float* __restrict__ d, size_t d_stride, float* __restrict__ y0,
-                                                   float* __restrict__ y1, size_t y_stride,
-                                                   const uint64_t* __restrict__ tab, int* __restrict__ err) {
-    const int pick = blockIdx.y;
-    MatRef m = blockIdx.z ? single1 : single0;
-    if (ids) {
-        const int id = ids[pick];
-        if (id < 0 || id >= n_experts) {   // the pick contributes nothing (the combine skips it)
-            if (blockIdx.x == 0 && threadIdx.x == 0) atomicOr(err, kDevErrExpertId);
-            return;
-        }
-        m = descs[id].m[role0 + blockIdx.z];
-    }
-    float* y = blockIdx.z ? y1 : y0;
-    const int row = blockIdx.x * 8 + (threadIdx.x >> 5), l = threadIdx.x & 31;
-    const int8_t* qp = q + pick * q_stride;
-    const float* dp = d + pick * d_stride;
+// One lane's share of a row: sub-blocks l, l + 32, ... in that order, four per
+// pass, each pass's loads all issued before its arithmetic (a sub-block past
+// the row's end reads sub-block 0 and leaves acc as it is). T fixes the block
+// type, so every type test in the decoders folds away.
+template <int T>
+__device__ __forceinline__ float row_acc(MatRef m, int row, int l, int nk, const int8_t* qp, const float* dp,
+                                         const uint64_t* tab) {
+    m.type = T;
     float acc = 0.0f;
-    if (row < n)
-        for (int kb = l; kb < k / 32; kb += 32) {
+    for (int k0 = 0; k0 < nk; k0 += 128) {
+#pragma unroll
+        for (int it = 0; it < 4; ++it) {
+            const int kr = k0 + l + 32 * it;
+            const bool ok = kr < nk;
+            const int kb = ok ? kr : 0;
             const uint4* qw = reinterpret_cast<const uint4*>(qp + 32 * kb);
             const uint4 lo = qw[0], hi = qw[1];
             const uint32_t a[8] = {lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
-            if (m.type == kQ8_0) {   // core.hpp:80: fma(d * d_x, float(dot), acc)
+            float next;
+            if constexpr (T == kQ8_0) {   // core.hpp:80: fma(d * d_x, float(dot), acc)
                 const Sub32 s = sub32_dense(m, row, kb, a);
-                acc = fmaf(__fmul_rn(s.d8, dp[kb]), float(s.a + s.b), acc);
+                next = fmaf(__fmul_rn(s.d8, dp[kb]), float(s.a + s.b), acc);
+            } else {
+                const Sub32 s = dense_type(T) ? sub32_dense(m, row, kb, a) : sub32(m, row, kb, a, tab);
+                const int isum = s.s0 * s.a + s.s1 * s.b;
+                float dot = __fmul_rn(s.d8, float(isum));
+                if constexpr (T == kQ4_K || T == kQ5_K) {   // core.hpp:62-65: the min term as two fmas
+                    const float corr = fmaf(s.m, float(s.sa), __fmul_rn(s.m, float(s.sb)));
+                    dot = fmaf(s.d8, float(isum), -corr);
+                }
+                next = fmaf(dp[kb], dot, acc);
+            }
+            acc = ok ? next : acc;
+        }
+    }
+    return acc;
+}
+
+// Rows of one or two roles of every pick: grid (G, 1, roles), 256 threads, 8
+// rows per step, 32 lanes per row; workgroup g takes the row groups (pick,
+// group) = g, g + G, ... of its role, so that the codebooks it stages in LDS
+// once serve many rows. Role role0 + z writes yz. Activations: q + pick *
+// q_stride (k int8), d + pick * d_stride (k / 32 scales); output y + pick *
+// y_stride. ids == nullptr: the matrices single0 (z = 0) and single1 (z = 1)
+// for every pick. stage: the launch has IQ matrices (their codebooks go to LDS).
+constexpr int kTabBytes = 24576;   // layer_tables: sign masks, IQ2_XXS, IQ2_XS, IQ1 grids
+__global__ __launch_bounds__(256) void mv32_kernel(const ExpertDesc* __restrict__ descs, const int32_t* __restrict__ ids,
+                                                   MatRef single0, MatRef single1, int picks, int n_experts, int role0,
+                                                   int n, int k, const int8_t* __restrict__ q, size_t q_stride,
+                                                   const float* __restrict__ d, size_t d_stride, float* __restrict__ y0,
+                                                   float* __restrict__ y1, size_t y_stride,
+                                                   const uint64_t* __restrict__ tab, int stage, int* __restrict__ err) {
+    __shared__ __attribute__((aligned(16))) uint64_t stab[kTabBytes / 8];
+    if (stage) {
+        for (int c = threadIdx.x; c < kTabBytes / 16; c += 256)
+            reinterpret_cast<uint4*>(stab)[c] = reinterpret_cast<const uint4*>(tab)[c];
+        __syncthreads();
+    }
+    float* y = blockIdx.z ? y1 : y0;
+    const int l = threadIdx.x & 31, rgp = (n + 7) / 8, total = picks * rgp;
+    for (int w = blockIdx.x; w < total; w += gridDim.x) {
+        const int pick = w / rgp, row = (w - pick * rgp) * 8 + (threadIdx.x >> 5);
+        MatRef m = blockIdx.z ? single1 : single0;
+        if (ids) {
+            const int id = ids[pick];
+            if (id < 0 || id >= n_experts) {   // the pick contributes nothing (the combine skips it)
+                if (threadIdx.x == 0) atomicOr(err, kDevErrExpertId);
                 continue;
             }
-            const Sub32 s = dense_type(m.type) ? sub32_dense(m, row, kb, a) : sub32(m, row, kb, a, tab);
-            const int isum = s.s0 * s.a + s.s1 * s.b;
-            float dot = __fmul_rn(s.d8, float(isum));
-            if (m.type == kQ4_K || m.type == kQ5_K) {   // core.hpp:62-65: the min term as two fmas
-                const float corr = fmaf(s.m, float(s.sa), __fmul_rn(s.m, float(s.sb)));
-                dot = fmaf(s.d8, float(isum), -corr);
-            }
-            acc = fmaf(dp[kb], dot, acc);
+            m = descs[id].m[role0 + blockIdx.z];
+        }
+        const int8_t* qp = q + pick * q_stride;
+        const float* dp = d + pick * d_stride;
+        const int rr = row < n ? row : n - 1;   // rows past the end compute row n - 1 and store nothing
+        float acc = 0.0f;
+        switch (m.type) {   // uniform per workgroup
+        case kIQ2_XXS: acc = row_acc<kIQ2_XXS>(m, rr, l, k / 32, qp, dp, stab); break;
+        case kIQ2_XS: acc = row_acc<kIQ2_XS>(m, rr, l, k / 32, qp, dp, stab); break;
+        case kIQ1_M: acc = row_acc<kIQ1_M>(m, rr, l, k / 32, qp, dp, stab); break;
+        case kQ8_0: acc = row_acc<kQ8_0>(m, rr, l, k / 32, qp, dp, stab); break;
+        case kQ4_K: acc = row_acc<kQ4_K>(m, rr, l, k / 32, qp, dp, stab); break;
+        case kQ5_K: acc = row_acc<kQ5_K>(m, rr, l, k / 32, qp, dp, stab); break;
+        default: acc = row_acc<kQ6_K>(m, rr, l, k / 32, qp, dp, stab); break;
         }
 #pragma unroll
-    for (int o = 16; o > 0; o >>= 1) acc = __fadd_rn(acc, __shfl_xor(acc, o, 32));
-    if (row < n && l == 0) y[pick * y_stride + row] = __fadd_rn(acc, 0.0f);
+        for (int o = 16; o > 0; o >>= 1) acc = __fadd_rn(acc, __shfl_xor(acc, o, 32));
+        if (row < n && l == 0) y[pick * y_stride + row] = __fadd_rn(acc, 0.0f);
+    }
 }
 
 // h = SwiGLU(g, u) (limit applied) quantized per 32 as quant32_kernel does, in
@@ -284,8 +324,12 @@ hipError_t launch_mv32(const ExpertDesc* descs, const int32_t* ids, const MatRef
                        const float* d, size_t d_stride, float* y0, float* y1, size_t y_stride,
                        const uint64_t* tables, int* err, hipStream_t s) {
     if (picks < 1 || roles < 1 || roles > 2 || n < 1 || k < 256 || k % 256) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(mv32_kernel, dim3((n + 7) / 8, picks, roles), dim3(256), 0, s, descs, ids, single0, single1,
-                       n_experts, role0, n, k, q, q_stride, d, d_stride, y0, y1, y_stride, tables, err);
+    // Bank matrices (ids) may be any IQ type; a single pair of dense matrices needs no codebook.
+    const int stage = ids || !dense_type(single0.type) || (roles > 1 && !dense_type(single1.type));
+    const int total = picks * ((n + 7) / 8);
+    const int G = stage ? (total < 512 ? total : 512) : total;   // staging workgroups take several row groups
+    hipLaunchKernelGGL(mv32_kernel, dim3(G, 1, roles), dim3(256), 0, s, descs, ids, single0, single1, picks,
+                       n_experts, role0, n, k, q, q_stride, d, d_stride, y0, y1, y_stride, tables, stage, err);
     return hipGetLastError();
 }
 

@@ -1281,6 +1281,17 @@ int32_t xl_quantize_q8k_async(xl_context* ctx, const float* d_x, int32_t rows, i
     });
 }
 
+int32_t xl_swiglu_async(xl_context* ctx, const float* d_g, const float* d_u, int32_t n, float limit, float* d_h,
+                        void* stream, xl_error* err) {
+    return guarded(ctx, err, [&] {
+        ready(ctx, false);
+        need(d_g && d_u && d_h, XL_E_ARG, "null device pointer");
+        need(n >= 1 && n <= (1 << 28), XL_E_ARG, "n outside 1..2^28");
+        need(std::isfinite(limit), XL_E_ARG, "limit not finite");
+        hip_check(xl::dev::launch_swiglu(d_g, d_u, n, limit, d_h, pick_stream(ctx, stream)), "SwiGLU launch");
+    });
+}
+
 int32_t xl_matvec_async(xl_context* ctx, int32_t type, const void* d_planar, int32_t n, int32_t k, const float* d_x,
                         float* d_y, int32_t* d_partials, void* stream, xl_error* err) {
     return guarded(ctx, err, [&] {

@@ -177,6 +177,8 @@ hipError_t launch_hc_post(const float* y, const float* res, const float* post, c
 // quantized per 32 into q, d exactly as launch_quant32 would quantize h.
 hipError_t launch_swiglu_quant32(const float* g, const float* u, int rows, int k, float lim, int8_t* q, float* d,
                                  hipStream_t s);
+// h = SwiGLU(g, u) elementwise over n values, with the limit (lim <= 0: none).
+hipError_t launch_swiglu(const float* g, const float* u, int n, float lim, float* h, hipStream_t s);
 // Seeded generation of one planar matrix (role 0 gate, 1 up, 2 down).
 hipError_t launch_generate(uint8_t* base, int type, int n, int k, uint64_t seed, uint32_t layer, uint32_t expert,
                            uint32_t role, hipStream_t s);

@@ -263,6 +263,14 @@ __device__ __forceinline__ float combine_one(const int32_t* ids, const float* w,
     return acc;
 }
 
+// h = SwiGLU(g, u) with the limit, elementwise (hip_q8k.hip activate_kernel,
+// q8k_core.hpp:92-95 per element).
+__global__ __launch_bounds__(256) void swiglu_kernel(const float* __restrict__ g, const float* __restrict__ u, int n,
+                                                     float lim, float* __restrict__ h) {
+    const int i = blockIdx.x * 256 + threadIdx.x;
+    if (i < n) h[i] = silu_mul(g[i], u[i], lim);
+}
+
 __global__ __launch_bounds__(256) void combine_kernel(const int32_t* __restrict__ ids, const float* __restrict__ w,
                                                       int k, const float* __restrict__ y, int dim,
                                                       const float* __restrict__ shared, float* __restrict__ out) {
@@ -725,6 +733,12 @@ hipError_t launch_combine(const int32_t* ids, const float* w, int k, const float
                           float* out, hipStream_t s) {
     if (k < 0 || k > 16) return hipErrorInvalidValue;
     hipLaunchKernelGGL(combine_kernel, dim3((dim + 255) / 256), dim3(256), 0, s, ids, w, k, y, dim, shared, out);
+    return hipGetLastError();
+}
+
+hipError_t launch_swiglu(const float* g, const float* u, int n, float lim, float* h, hipStream_t s) {
+    if (n < 1) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(swiglu_kernel, dim3((n + 255) / 256), dim3(256), 0, s, g, u, n, lim, h);
     return hipGetLastError();
 }
 

@@ -9,7 +9,9 @@
 //                   takes sub-blocks l, l + 32, ...: dot = (fp16(d) * 0.125) *
 //                   float(s0 * a + s1 * b) (a, b: the integer dots of the two
 //                   16-weight halves, s: odd sub-scales), acc = fma(xd, dot,
-//                   acc); then a 16-8-4-2-1 butterfly and lane 0 + 0
+//                   acc); then a 16-8-4-2-1 butterfly and lane 0 + 0.
+//                   Persistent workgroups (row groups g, g + G, ...) with the
+//                   expanded codebooks staged in LDS once each
 //   swiglu_quant32_kernel
 //                   h = g / (1 + exp(-g)) * u (the device's expf; g and u
 //                   clamped first when the SwiGLU limit is set), quantized per
@@ -165,8 +167,8 @@ __device__ __forceinline__ Sub32 sub32(const MatRef& m, int row, int kb, const u
         }
         r.d8 = __fmul_rn(h2f(d16), 0.125f);
     } else {   // IQ1_M: qs, qh nibbles (3 index bits + delta sign), scale words with the fp16 d in their top nibbles
-        const uint8_t* qs = m.base + blk * 32 + 4 * ib;
-        const uint8_t* qh = m.base + m.off1 + blk * 16 + 2 * ib;
+        const uint32_t qs = ld32(m.base + blk * 32 + 4 * ib);               // four low index bytes
+        const uint32_t qh = ld16(m.base + m.off1 + blk * 16 + 2 * ib);      // two high-bit / delta bytes
         const uint8_t* sc = m.base + m.off2 + blk * 8;
         const uint32_t w = ld16(sc + 2 * (ib >> 1));
         r.s0 = 2 * int((w >> (6 * (ib & 1))) & 7u) + 1;
@@ -176,8 +178,8 @@ __device__ __forceinline__ Sub32 sub32(const MatRef& m, int row, int kb, const u
         r.d8 = __fmul_rn(h2f(d16), 0.125f);
 #pragma unroll
         for (int l = 0; l < 4; ++l) {
-            const uint32_t h = qh[l >> 1], nib = (l & 1) ? (h >> 4) : (h & 15u);
-            const uint64_t g = tab[kTabIQ1 + (qs[l] | ((nib & 7u) << 8))];
+            const uint32_t h = (qh >> (8 * (l >> 1))) & 255u, nib = (l & 1) ? (h >> 4) : (h & 15u);
+            const uint64_t g = tab[kTabIQ1 + (((qs >> (8 * l)) & 255u) | ((nib & 7u) << 8))];
             const int mdot = sdot4(uint32_t(g >> 32), q[2 * l + 1], sdot4(uint32_t(g), q[2 * l], 0));
             const int qsum = sdot4(0x01010101u, q[2 * l + 1], sdot4(0x01010101u, q[2 * l], 0));
             half[l >> 1] += 8 * mdot + ((nib & 8u) ? -qsum : qsum);   // values 8 * grid + delta

@@ -89,6 +89,7 @@ _SIGNATURES = {
     "xl_grouped_forward_routed_async": (_I32, [_P, _I32, _I32, _P, _P, _I32, C.c_float, _P, _P, _P, _P, _ErrP]),
     "xl_quantize_q8k_async": (_I32, [_P, _P, _I32, _I32, _P, _P, _ErrP]),
     "xl_matvec_async": (_I32, [_P, _I32, _P, _I32, _I32, _P, _P, _P, _P, _ErrP]),
+    "xl_swiglu_async": (_I32, [_P, _P, _P, _I32, C.c_float, _P, _P, _ErrP]),
     "xl_layer_forward_per32": (_I32, [_P, _I32, _i32p, _P, _I32, _f32p, _P, _P, _P, _ErrP]),
     "xl_layer_forward_per32_async": (_I32, [_P, _I32, _P, _P, _I32, _P, _P, _P, _P, _P, _ErrP]),
     "xl_quantize_per32_async": (_I32, [_P, _P, _I32, _I32, _P, _P, _P, _ErrP]),
@@ -404,6 +405,10 @@ class Lane:
         """y [T, D], res / out [T, H, D], post [T, 8], comb [T, 64] device tensors."""
         T, H, D = (int(v) for v in res.shape)
         self._call("xl_hc_post_async", _ptr(y), _ptr(res), _ptr(post), _ptr(comb), D, H, T, _ptr(out),
+                   None if stream is None else int(stream))
+
+    def swiglu_async(self, g, u, h, limit: float = 0.0, stream=None) -> None:
+        self._call("xl_swiglu_async", _ptr(g), _ptr(u), int(g.numel()), float(limit), _ptr(h),
                    None if stream is None else int(stream))
 
     def matvec_async(self, t: int, planar, n: int, k: int, x, y, partials=None, stream=None) -> None:

@@ -184,6 +184,11 @@ int32_t xl_grouped_forward_routed_async(xl_context* ctx, int32_t layer, int32_t 
  * rows*k/256 blocks of 292 bytes (q8k_core.hpp:13-38, hip_q8k.hpp:9). */
 int32_t xl_quantize_q8k_async(xl_context* ctx, const float* d_x, int32_t rows, int32_t k, void* d_q8k, void* stream,
                               xl_error* err);
+/* h[n] = SwiGLU(g, u) with the limit (q8k::activate, hip_q8k.hpp:10;
+ * q8k_core.hpp:92-95): limit > 0 clamps g to <= limit and u to [-limit,
+ * limit], then g / (1 + exp(-g)) * u on the device's expf. */
+int32_t xl_swiglu_async(xl_context* ctx, const float* d_g, const float* d_u, int32_t n, float limit, float* d_h,
+                        void* stream, xl_error* err);
 /* One planar matrix (n x k) times Q8_K(x): y[n] and, when non-null, the
  * per-block int32 partials (n*k/256 ints; IQ1_M: (main, delta) pairs).
  * Replaces q8k::mv (hip_q8k.hpp:10). d_x is the f32 input vector. */

@@ -324,3 +324,19 @@ def test_streaming_kernel_pick_counts(orc, dim, ff, k, monkeypatch):
             assert max_rel(got, want) < TOL, (trial, max_rel(got, want))
     finally:
         lane.close()
+
+
+@pytest.mark.parametrize("limit", [0.0, 7.0])
+def test_swiglu_primitive(probe, orc, rng, limit):
+    """xl_swiglu_async (q8k::activate): the device's expf differs from the host's
+    by an ulp or so, so the check is within 4 ulps; the clamp itself is exact."""
+    step(f"swiglu limit={limit}")
+    g = (rng.standard_normal(5000) * 8).astype(np.float32)
+    u = (rng.standard_normal(5000) * 8).astype(np.float32)
+    h = torch.zeros(5000, dtype=torch.float32, device="cuda")
+    probe.swiglu_async(dev(g), dev(u), h, limit)
+    probe.sync()
+    want = np.array([orc.swiglu(a, b, limit) for a, b in zip(g, u)], np.float32)
+    got = h.cpu().numpy()
+    ulp = np.abs(got.view(np.int32).astype(np.int64) - want.view(np.int32).astype(np.int64))
+    assert ulp.max() <= 4, ulp.max()

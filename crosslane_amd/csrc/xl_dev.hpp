@@ -115,6 +115,11 @@ __device__ __forceinline__ Q8Lane q8k_lane(const float v[4], int lane) {
     return r;
 }
 
+// Q8_K quants staged in LDS: byte o of a row sits at qswz(o), the 16-byte
+// chunk index XORed with bits 1-2 of the pair (64-byte) index, so that lanes
+// reading consecutive pairs hit different banks.
+__device__ __forceinline__ int qswz(int o) { return o ^ (((o >> 7) & 3) << 4); }
+
 // SwiGLU limit (q8k_core.hpp:92-93, the pack's swiglu_limit): with lim > 0,
 // g = min(g, lim) and u = min(max(u, -lim), lim) before the product.
 __device__ __forceinline__ void swiglu_clamp(float& g, float& u, float lim) {

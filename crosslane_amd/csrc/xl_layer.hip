@@ -379,7 +379,7 @@ __global__ __launch_bounds__(NW * 64, 1) void layer3_kernel(Layer3Args a) {
             const float v[4] = {xv[u].x, xv[u].y, xv[u].z, xv[u].w};
             const Q8Lane q = q8k_lane(v, lane);
             if (!q.finite && lane == 0) set_err(a.err, kDevErrNonFinite);
-            reinterpret_cast<uint32_t*>(lds + LY::XQ + 256 * b)[lane] = q.packed;
+            *reinterpret_cast<uint32_t*>(lds + LY::XQ + qswz(256 * b + 4 * lane)) = q.packed;
             if (lane == 0) reinterpret_cast<float*>(lds + LY::XD)[b] = q.d;
         }
     }
@@ -415,10 +415,9 @@ __global__ __launch_bounds__(NW * 64, 1) void layer3_kernel(Layer3Args a) {
 #pragma unroll
         for (int q = 0; q < PG; ++q) {
             const int p = lG + LG * q;
-            const uint4* src = reinterpret_cast<const uint4*>(lds + LY::XQ + 64 * p);
 #pragma unroll
             for (int c = 0; c < 4; ++c) {
-                const uint4 v = src[c];
+                const uint4 v = *reinterpret_cast<const uint4*>(lds + LY::XQ + qswz(64 * p + 16 * c));
                 A.a[q][4 * c] = v.x; A.a[q][4 * c + 1] = v.y; A.a[q][4 * c + 2] = v.z; A.a[q][4 * c + 3] = v.w;
             }
             A.d[q] = reinterpret_cast<const float*>(lds + LY::XD)[p >> 2];
@@ -529,7 +528,7 @@ __global__ __launch_bounds__(NW * 64, 1) void layer3_kernel(Layer3Args a) {
                             }
 #pragma unroll
                             for (int c = 0; c < 16; ++c)
-                                if (c < per) reinterpret_cast<uint32_t*>(hq)[per * lane + c] = uint32_t(w16[c]);
+                                if (c < per) *reinterpret_cast<uint32_t*>(hq + qswz(4 * (per * lane + c))) = uint32_t(w16[c]);
                             if (lane < nbh) reinterpret_cast<uint32_t*>(hq + ff)[lane] = uint32_t(dw);
                             // LDS writes of one wave land in order: the flag goes last
                             if (lane == 0) __hip_atomic_store(&s_hq_ready[i], epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
@@ -546,10 +545,9 @@ __global__ __launch_bounds__(NW * 64, 1) void layer3_kernel(Layer3Args a) {
 #pragma unroll
                         for (int q = 0; q < PD; ++q) {
                             const int p = lD + LD * q;
-                            const uint4* srcl = reinterpret_cast<const uint4*>(hq + 64 * p);
 #pragma unroll
                             for (int c = 0; c < 4; ++c) {
-                                const uint4 v = srcl[c];
+                                const uint4 v = *reinterpret_cast<const uint4*>(hq + qswz(64 * p + 16 * c));
                                 B.a[q][4 * c] = v.x; B.a[q][4 * c + 1] = v.y; B.a[q][4 * c + 2] = v.z; B.a[q][4 * c + 3] = v.w;
                             }
                             B.d[q] = reinterpret_cast<const float*>(hq + ff)[p >> 2];

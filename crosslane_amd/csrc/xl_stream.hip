@@ -193,10 +193,6 @@ struct Act {
     uint32_t a[P][16];
     float d[P];
 };
-// Q8_K quants staged in LDS: byte o of a row sits at qswz(o), the 16-byte
-// chunk index XORed with bits 1-2 of the pair (64-byte) index, so that lanes
-// reading consecutive pairs hit different banks.
-__device__ __forceinline__ int qswz(int o) { return o ^ (((o >> 7) & 3) << 4); }
 // Activations of pairs lp, lp + L, ... from a Q8_K vector in LDS (quants at
 // base, block scales at base + scl).
 template <int P>

@@ -501,7 +501,7 @@ int32_t xl_open(uint32_t abi_version, const xl_config* cfg, xl_context** out, xl
         if (cfg->max_tokens > 0) {
             const uint64_t T = uint64_t(cfg->max_tokens), GP = T * uint64_t(P);
             auto& g = ctx->grp;
-            g.hq_bytes = GP * uint64_t(ff / 256) * 512;
+            g.hq_bytes = GP * uint64_t(ff);
             const std::vector<Part> gparts = {
                 {reinterpret_cast<void**>(&g.ids), GP * 4},
                 {reinterpret_cast<void**>(&g.w), GP * 4},
@@ -542,7 +542,6 @@ int32_t xl_open(uint32_t abi_version, const xl_config* cfg, xl_context** out, xl
         hip_check(hipMemset(ctx->hqtag, 0, size_t(P) * ff * 2), "tag clear");
         hip_check(hipMemset(ctx->ctl, 0, 256), "epoch clear");
         hip_check(hipMemset(ctx->hbuf, 0xff, size_t(2) * xl::kHBufWords * 4), "h exchange fill");
-        if (ctx->grp.hq) hip_check(hipMemset(ctx->grp.hq, 0, ctx->grp.hq_bytes), "grouped Q8_K(h) clear");   // the zero halves
         const std::vector<uint64_t> tab = layer_tables();
         hip_check(hipMemcpy(ctx->tables, tab.data(), tab.size() * 8, hipMemcpyHostToDevice), "table upload");
         ctx->path = env_int("XL_LAYER_PATH", 1);

@@ -164,14 +164,10 @@ __global__ __launch_bounds__(1024) void bucket_kernel(GroupArgs a) {
 }
 
 // ---------------------------------------------------------------------------
-// Q8_K of 256-value blocks of rows, one wave per block. Output orders:
-//   ROWS_X: per block, chunk e (entry e of every sub-block) holds the 8 quants
-//           of entry e of sub-blocks 0..7: byte e * 64 + 8 c + j;
-//   ROWS_H: per block 512 B, chunk e holds per sub-block c 16 B {A1, A2}: the 8
-//           quants of entry e in A1 when e < 2 (the first 16 weights of the
-//           sub-block, scale nibble 0), in A2 when e >= 2; the other half stays
-//           zero (cleared once, never written).
-// Pair rows of a bad id are skipped (their h is never written).
+// Q8_K of 256-value blocks of rows, one wave per block, in the operand order of
+// the MFMA kernels: per block, chunk e (entry e of every sub-block) holds the 8
+// quants of entry e of sub-blocks 0..7: byte e * 64 + 8 c + j. ROWS_X: token
+// rows; ROWS_H: pair rows, skipped for a bad id (their h is never written).
 // ---------------------------------------------------------------------------
 enum { ROWS_X = 0, ROWS_H = 1 };
 template <int MODE>
@@ -191,10 +187,7 @@ __global__ __launch_bounds__(256) void q8k_rows_kernel(const float* __restrict__
     const Q8Lane r = q8k_lane(v, lane);
     if (!r.finite && lane == 0) atomicOr(err, kDevErrNonFinite);
     const int c = lane >> 3, e = (lane >> 1) & 3, j = 4 * (lane & 1);   // values 4 lane .. + 3
-    if (MODE == ROWS_X)
-        *reinterpret_cast<uint32_t*>(q + size_t(b) * 256 + 64 * e + 8 * c + j) = r.packed;
-    else
-        *reinterpret_cast<uint32_t*>(q + size_t(b) * 512 + 128 * e + 16 * c + (e >= 2 ? 8 : 0) + j) = r.packed;
+    *reinterpret_cast<uint32_t*>(q + size_t(b) * 256 + 64 * e + 8 * c + j) = r.packed;
     if (lane == 0) d[b] = r.d;
 }
 
@@ -225,10 +218,61 @@ __device__ __forceinline__ uint16_t ld16(__amdgpu_buffer_rsrc_t r, uint32_t v, u
 
 // One block's operands for one wave.
 struct GuOps {
-    uint4 g[4], u[4], a[4];   // gate / up quants of the lane's row, the lane's activation chunk
+    uint4 g, u, a[4];   // 16-B part e4 of the row's gate / up block, the lane's activation chunk
 };
+
+// Exchanges across the four 16-lane groups (e4 = lane / 16) of a wave.
+__device__ __forceinline__ void swap32(uint32_t& x, uint32_t& y) {   // lanes 32.. of x <-> lanes ..31 of y
+    const auto r = __builtin_amdgcn_permlane32_swap(x, y, false, false);
+    x = r[0];
+    y = r[1];
+}
+__device__ __forceinline__ void swap16(uint32_t& x, uint32_t& y) {   // odd groups of x <-> even groups of y
+    const auto r = __builtin_amdgcn_permlane16_swap(x, y, false, false);
+    x = r[0];
+    y = r[1];
+}
+// v[j] of group g -> v[g] of group j, lane by lane within the groups.
+__device__ __forceinline__ void xpose4(uint32_t (&v)[4]) {
+    swap32(v[0], v[2]);
+    swap32(v[1], v[3]);
+    swap16(v[0], v[1]);
+    swap16(v[2], v[3]);
+}
+// Every group's byte x (placed at byte e4 by the caller) in every group.
+__device__ __forceinline__ uint32_t gather4(uint32_t x) {
+    uint32_t y = x;
+    swap32(x, y);
+    x |= y;
+    y = x;
+    swap16(x, y);
+    return x | y;
+}
+
+// IQ2_XXS block of the MFMA lane (col, e4) from 16-B parts: lane (col, g) loaded
+// bytes 16 g .. + 15 of row col's block (sub-blocks 2g and 2g + 1: grid bytes,
+// then aux bytes = 7 sign bits | scale bit k in byte k). Afterwards u[j] holds
+// {grid, aux} bytes of entry e4 of sub-blocks 2j (bytes 0, 1) and 2j + 1 (bytes
+// 2, 3), and s holds the 4-bit scale of sub-block c at bits 4c .. 4c + 3.
+struct XxsLane {
+    uint32_t u[4], s;
+};
+__device__ __forceinline__ XxsLane xxs_lane(const uint4& w, int e4) {
+    const uint32_t p01 = perm(w.y, w.x, 0x05010400u), p01b = perm(w.y, w.x, 0x07030602u);
+    const uint32_t p23 = perm(w.w, w.z, 0x05010400u), p23b = perm(w.w, w.z, 0x07030602u);
+    XxsLane r;
+    r.u[0] = perm(p23, p01, 0x05040100u);    // entry 0 of both sub-blocks
+    r.u[1] = perm(p23, p01, 0x07060302u);
+    r.u[2] = perm(p23b, p01b, 0x05040100u);
+    r.u[3] = perm(p23b, p01b, 0x07060302u);
+    xpose4(r.u);
+    const uint32_t sa = __builtin_amdgcn_udot4((w.y >> 7) & 0x01010101u, 0x08040201u, 0u, false);
+    const uint32_t sb = __builtin_amdgcn_udot4((w.w >> 7) & 0x01010101u, 0x08040201u, 0u, false);
+    r.s = gather4((sa | (sb << 4)) << (8 * e4));
+    return r;
+}
 struct DnOps {
-    uint4 q[4], a[8];         // down codes of the lane's row, the lane's split activation chunk
+    uint4 q, a[4];      // 16-B part e4 of the row's down block, the lane's activation chunk
 };
 
 // Stages one item's pair scales (scl: one f32 per (pair row, block), pairs of
@@ -268,7 +312,6 @@ __global__ __launch_bounds__(NW * 64, 1) void gu_kernel(GroupArgs a) {
     const int items = uni(*a.n_tasks) * groups;
     const uint32_t lo_g = uint32_t(lane & (kCopiesXXS - 1)) << 4;        // kL_GRID = 0
     const uint32_t lo_s = (uint32_t(lane & 31) << 3) | (1u << 16);       // kL_SGN = 1 << 16
-    const uint32_t sel = 0x0C020000u | (uint32_t(4 + e4) << 8);          // address byte 1 <- byte e4 of the word
     uint32_t sunk = 0;
     for (int item = blockIdx.x; item < items; item += gridDim.x) {
         const int task = item / groups, grp = item - task * groups;
@@ -290,12 +333,10 @@ __global__ __launch_bounds__(NW * 64, 1) void gu_kernel(GroupArgs a) {
         const __amdgpu_buffer_rsrc_t rg = rsrc(G.base), ru = rsrc(U.base), rx = rsrc(a.xq);
         const uint32_t vq = uint32_t(row * nb) * 64u;
         auto load = [&](GuOps& o, int blk) {
+            o.g = ld128(rg, vq + 64u * blk + 16u * e4);
+            o.u = ld128(ru, vq + 64u * blk + 16u * e4);
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                o.g[i] = ld128(rg, vq + 64u * blk + 16u * i);
-                o.u[i] = ld128(ru, vq + 64u * blk + 16u * i);
-                o.a[i] = ld128(rx, va + 256u * blk + 16u * i);
-            }
+            for (int i = 0; i < 4; ++i) o.a[i] = ld128(rx, va + 256u * blk + 16u * i);
         };
         auto touch = [&](int blk) { return ld32(rg, vq + 64u * blk) ^ ld32(ru, vq + 64u * blk); };
         float accg[4] = {0.0f, 0.0f, 0.0f, 0.0f}, accu[4] = {0.0f, 0.0f, 0.0f, 0.0f};
@@ -304,17 +345,16 @@ __global__ __launch_bounds__(NW * 64, 1) void gu_kernel(GroupArgs a) {
         // All eight gate lookups are issued first; each up lookup is issued as a
         // gate one is consumed, so about seven are in flight throughout.
         struct Look { uint4 g; uint2 m; };
-        auto look = [&](const uint4* q, int c) {
-            const uint32_t* w = reinterpret_cast<const uint32_t*>(q) + 2 * c;
+        auto look = [&](const XxsLane& X, int c) {   // grid byte -> address byte 1, then the aux byte
+            const uint32_t w = X.u[c >> 1], h = uint32_t(c & 1) * 2u;
             Look L;
-            L.g = *reinterpret_cast<const uint4*>(lds + perm(w[0], lo_g, sel));
-            L.m = *reinterpret_cast<const uint2*>(lds + perm(w[1], lo_s, sel));
+            L.g = *reinterpret_cast<const uint4*>(lds + perm(w, lo_g, 0x0C020000u | ((4u + h) << 8)));
+            L.m = *reinterpret_cast<const uint2*>(lds + perm(w, lo_s, 0x0C020000u | ((5u + h) << 8)));
             return L;
         };
-        auto use = [&](const Look& L, const uint4* q, int c, long A, int (&bi)[4]) {
-            const uint32_t aux = reinterpret_cast<const uint32_t*>(q)[2 * c + 1];
+        auto use = [&](const Look& L, const XxsLane& X, int c, long A, int (&bi)[4]) {
             const v4i C = mfma(A, pack64(bfi(L.m.x, L.g.z, L.g.x), bfi(L.m.y, L.g.w, L.g.y)), v4i{0, 0, 0, 0});
-            const int ls = int(__builtin_amdgcn_udot4((aux >> 7) & 0x01010101u, 0x10080402u, 1u, false));
+            const int ls = int(__builtin_amdgcn_ubfe(X.s, 4 * c, 4) * 2u + 1u);
 #pragma unroll
             for (int r = 0; r < 4; ++r) bi[r] = mad24(ls, C[r], bi[r]);
         };
@@ -330,16 +370,17 @@ __global__ __launch_bounds__(NW * 64, 1) void gu_kernel(GroupArgs a) {
                 const uint32_t* av = reinterpret_cast<const uint32_t*>(o.a) + 2 * c;
                 A[c] = pack64(av[0], av[1]);
             }
+            const XxsLane XG = xxs_lane(o.g, e4), XU = xxs_lane(o.u, e4);
             Look L[8];
 #pragma unroll
-            for (int c = 0; c < 8; ++c) L[c] = look(o.g, c);
+            for (int c = 0; c < 8; ++c) L[c] = look(XG, c);
 #pragma unroll
             for (int c = 0; c < 8; ++c) {
-                use(L[c], o.g, c, A[c], big);
-                L[c] = look(o.u, c);
+                use(L[c], XG, c, A[c], big);
+                L[c] = look(XU, c);
             }
 #pragma unroll
-            for (int c = 0; c < 8; ++c) use(L[c], o.u, c, A[c], biu);
+            for (int c = 0; c < 8; ++c) use(L[c], XU, c, A[c], biu);
             const float dgf = h2f(sdg[b]), duf = h2f(sdu[b]);
             const float4 xd4 = *reinterpret_cast<const float4*>(lds + kL_PD + 64 * b + 16 * e4);
             const float xd[4] = {xd4.x, xd4.y, xd4.z, xd4.w};
@@ -384,10 +425,22 @@ __global__ __launch_bounds__(NW * 64, 1) void gu_kernel(GroupArgs a) {
     if (sunk == 0x9e3779b9u && lane == 64) a.h[0] = 0.0f;   // never true (lane < 64): keeps the touches
 }
 
+// IQ2_XS block of the MFMA lane (col, e4) from 16-B parts, as xxs_lane: u[j]
+// holds the 16-bit code (9-bit grid index at bits 7..15, sign bits 0..6) of
+// entry e4 of sub-block 2j (low half) and 2j + 1 (high half).
+__device__ __forceinline__ void xs_lane(const uint4& w, uint32_t (&u)[4]) {
+    u[0] = perm(w.z, w.x, 0x05040100u);
+    u[1] = perm(w.z, w.x, 0x07060302u);
+    u[2] = perm(w.w, w.y, 0x05040100u);
+    u[3] = perm(w.w, w.y, 0x07060302u);
+    xpose4(u);
+}
+
 // ---------------------------------------------------------------------------
 // down. Work item = (task, group of NW * 16 output rows). IQ2_XS keeps a scale
-// nibble per 16 weights: per sub-block one MFMA over the first half (A1) and
-// one over the second (A2), from the zero-interleaved Q8_K(h) chunks.
+// nibble per 16 weights (entries 0, 1 of a sub-block: ls1; entries 2, 3: ls2):
+// per sub-block one MFMA over all 32 weights (C) and one with entries 2, 3 of B
+// zeroed (C1), then ls1 C1 + ls2 (C - C1) as ls2 C + (ls1 - ls2) C1, exactly.
 // ---------------------------------------------------------------------------
 template <int NW>
 __global__ __launch_bounds__(NW * 64, 1) void dn_kernel(GroupArgs a) {
@@ -402,15 +455,14 @@ __global__ __launch_bounds__(NW * 64, 1) void dn_kernel(GroupArgs a) {
     const int items = uni(*a.n_tasks) * groups;
     const uint32_t lo_x = uint32_t(lane & (kCopiesXS - 1)) << 4;        // kL_GRID = 0
     const uint32_t lo_s = (uint32_t(lane & 31) << 3) | (1u << 16);      // kL_SGN = 1 << 16
-    const uint32_t selc = 0x0C0C0000u | (uint32_t(2 * e4 + 1) << 8) | uint32_t(2 * e4);   // code e4 of 4 u16
-    const uint32_t sel0 = 0x0C020400u;                                  // address byte 1 <- byte 0 of the code
+    const uint32_t mk = e4 < 2 ? ~0u : 0u;                               // lanes of entries 0, 1
     uint32_t sunk = 0;
     for (int item = blockIdx.x; item < items; item += gridDim.x) {
         const int task = item / groups, grp = item - task * groups;
         const int4 tk = task_at(a.tasks, task);
         const int row = grp * NW * 16 + wv * 16 + col;
         const int pa = a.order[tk.y + (col < tk.z ? col : 0)];
-        const uint32_t va = uint32_t(pa * nb) * 512u + 128u * e4;   // the lane's split activation chunk, block 0
+        const uint32_t va = uint32_t(pa * nb) * 256u + 64u * e4;   // the lane's activation chunk, block 0
         int po[4];
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
@@ -430,10 +482,9 @@ __global__ __launch_bounds__(NW * 64, 1) void dn_kernel(GroupArgs a) {
         const __amdgpu_buffer_rsrc_t rd = rsrc(D.base), rh = rsrc(a.hq);
         const uint32_t vq = uint32_t(row * nb) * 64u;
         auto load = [&](DnOps& o, int blk) {
+            o.q = ld128(rd, vq + 64u * blk + 16u * e4);
 #pragma unroll
-            for (int i = 0; i < 4; ++i) o.q[i] = ld128(rd, vq + 64u * blk + 16u * i);
-#pragma unroll
-            for (int i = 0; i < 8; ++i) o.a[i] = ld128(rh, va + 512u * blk + 16u * i);
+            for (int i = 0; i < 4; ++i) o.a[i] = ld128(rh, va + 256u * blk + 16u * i);
         };
         auto touch = [&](int blk) { return ld32(rd, vq + 64u * blk); };
         float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
@@ -443,26 +494,27 @@ __global__ __launch_bounds__(NW * 64, 1) void dn_kernel(GroupArgs a) {
             const int b = blk_c++;
             const uint2 sc = *reinterpret_cast<const uint2*>(lds + kL_RS + 8 * (rl * nb + b));
             int bi[4] = {0, 0, 0, 0};
-            uint32_t code[8];
+            uint32_t u[4];
+            xs_lane(o.q, u);
             uint4 g[8];
             uint2 m[8];
 #pragma unroll
             for (int c = 0; c < 8; ++c) {   // all eight lookups in flight before the first use
-                const uint32_t* w = reinterpret_cast<const uint32_t*>(o.q) + 2 * c;
-                code[c] = perm(w[1], w[0], selc);
-                g[c] = *reinterpret_cast<const uint4*>(lds + ((code[c] & 0xff80u) | lo_x));
-                m[c] = *reinterpret_cast<const uint2*>(lds + perm(code[c], lo_s, sel0));
+                const uint32_t w = u[c >> 1], code = (c & 1) ? w >> 16 : w;
+                g[c] = *reinterpret_cast<const uint4*>(lds + ((code & 0xff80u) | lo_x));
+                m[c] = *reinterpret_cast<const uint2*>(lds + perm(w, lo_s, (c & 1) ? 0x0C020600u : 0x0C020400u));
             }
 #pragma unroll
             for (int c = 0; c < 8; ++c) {
-                const uint32_t* av = reinterpret_cast<const uint32_t*>(o.a) + 4 * c;
-                const long B = pack64(bfi(m[c].x, g[c].z, g[c].x), bfi(m[c].y, g[c].w, g[c].y));
-                const v4i C1 = mfma(pack64(av[0], av[1]), B, v4i{0, 0, 0, 0});
-                const v4i C2 = mfma(pack64(av[2], av[3]), B, v4i{0, 0, 0, 0});
+                const uint32_t* av = reinterpret_cast<const uint32_t*>(o.a) + 2 * c;
+                const long A = pack64(av[0], av[1]);
+                const uint32_t blo = bfi(m[c].x, g[c].z, g[c].x), bhi = bfi(m[c].y, g[c].w, g[c].y);
+                const v4i C = mfma(A, pack64(blo, bhi), v4i{0, 0, 0, 0});
+                const v4i C1 = mfma(A, pack64(blo & mk, bhi & mk), v4i{0, 0, 0, 0});
                 const uint32_t sb = ((c < 4 ? sc.x : sc.y) >> (8 * (c & 3))) & 0xffu;
                 const int ls1 = int(((sb & 15u) << 1) | 1u), ls2 = int(((sb >> 3) & 30u) | 1u);
 #pragma unroll
-                for (int r = 0; r < 4; ++r) bi[r] = mad24(ls2, C2[r], mad24(ls1, C1[r], bi[r]));
+                for (int r = 0; r < 4; ++r) bi[r] = mad24(ls2, C[r], mad24(ls1 - ls2, C1[r], bi[r]));
             }
             const float ddf = h2f(reinterpret_cast<const uint16_t*>(lds + kL_RD)[rl * nb + b]);
             const float4 hd4 = *reinterpret_cast<const float4*>(lds + kL_PD + 64 * b + 16 * e4);

@@ -167,7 +167,7 @@ struct xl_context {
     struct Group {
         int32_t* ids = nullptr; float* w = nullptr; float* x = nullptr; float* shared = nullptr; float* out = nullptr;
         int8_t* xq = nullptr; float* xd = nullptr;
-        int32_t* order = nullptr; int4* tasks = nullptr; int32_t* n_tasks = nullptr;
+        int32_t* order = nullptr; int32_t* pos = nullptr; int4* tasks = nullptr; int32_t* n_tasks = nullptr;
         float* h = nullptr; int8_t* hq = nullptr; float* hd = nullptr; float* y = nullptr;
         uint64_t hq_bytes = 0;
     } grp;
@@ -501,16 +501,18 @@ int32_t xl_open(uint32_t abi_version, const xl_config* cfg, xl_context** out, xl
         if (cfg->max_tokens > 0) {
             const uint64_t T = uint64_t(cfg->max_tokens), GP = T * uint64_t(P);
             auto& g = ctx->grp;
-            g.hq_bytes = GP * uint64_t(ff);
+            const uint64_t slots = 16 * uint64_t(xl::group_max_tasks(int64_t(GP), cfg->n_experts));
+            g.hq_bytes = slots * uint64_t(ff);
             const std::vector<Part> gparts = {
                 {reinterpret_cast<void**>(&g.ids), GP * 4},
                 {reinterpret_cast<void**>(&g.w), GP * 4},
                 {reinterpret_cast<void**>(&g.x), T * dim * 4},
                 {reinterpret_cast<void**>(&g.shared), T * dim * 4},
                 {reinterpret_cast<void**>(&g.out), T * dim * 4},
-                {reinterpret_cast<void**>(&g.xq), T * dim},
+                {reinterpret_cast<void**>(&g.xq), slots * dim},
                 {reinterpret_cast<void**>(&g.xd), T * (dim / 256) * 4},
-                {reinterpret_cast<void**>(&g.order), GP * 4},
+                {reinterpret_cast<void**>(&g.order), slots * 4},
+                {reinterpret_cast<void**>(&g.pos), GP * 4},
                 {reinterpret_cast<void**>(&g.tasks), uint64_t(xl::group_max_tasks(int64_t(GP), cfg->n_experts)) * 16},
                 {reinterpret_cast<void**>(&g.n_tasks), 256},
                 {reinterpret_cast<void**>(&g.h), GP * ff * 4},
@@ -940,7 +942,7 @@ void enqueue_grouped(xl_context* ctx, int32_t layer, int32_t T, int32_t k, const
         a.ids = d_ids; a.w = d_w; a.x = d_x; a.shared = d_shared; a.out = d_out;
         a.T = T; a.k = k; a.n_experts = E; a.dim = dim; a.ff = ctx->cfg.ff;
         const auto& g = ctx->grp;
-        a.xq = g.xq; a.xd = g.xd; a.order = g.order; a.tasks = g.tasks; a.n_tasks = g.n_tasks;
+        a.xq = g.xq; a.xd = g.xd; a.order = g.order; a.pos = g.pos; a.tasks = g.tasks; a.n_tasks = g.n_tasks;
         a.h = g.h; a.hq = g.hq; a.hd = g.hd; a.y = g.y;
         a.tables = ctx->tables; a.err = ctx->err_flag;
         a.lim = ctx->cfg.swiglu_limit;

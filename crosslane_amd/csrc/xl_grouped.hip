@@ -113,10 +113,11 @@ __device__ __forceinline__ void fill_grid(uint8_t* lds, const uint64_t* grid, in
 }
 
 // ---------------------------------------------------------------------------
-// Buckets: counts per expert in LDS, one scan, then each valid pair takes a
-// slot of its expert's range. The slot order inside a range varies run to run;
-// no result depends on it (every output of a pair is computed from that pair's
-// operands only, in a fixed order).
+// Buckets: counts per expert in LDS, one scan of pairs and tasks, then each
+// valid pair takes a slot of its expert's tasks (task i: slots 16 i .. + 15).
+// The slot order inside an expert varies run to run; no result depends on it
+// (every output of a pair is computed from that pair's operands only, in a
+// fixed order).
 // ---------------------------------------------------------------------------
 __global__ __launch_bounds__(1024) void bucket_kernel(GroupArgs a) {
     __shared__ int cnt[kGroupMaxExperts];
@@ -132,62 +133,70 @@ __global__ __launch_bounds__(1024) void bucket_kernel(GroupArgs a) {
     }
     __syncthreads();
     const int per = (E + 1023) / 1024, e0 = min(E, t * per), e1 = min(E, e0 + per);
-    int sp = 0, st = 0;
-    for (int e = e0; e < e1; ++e) {
-        sp += cnt[e];
-        st += (cnt[e] + kTile - 1) / kTile;
-    }
-    part[t] = sp;
-    part[1024 + t] = st;
+    int st = 0;
+    for (int e = e0; e < e1; ++e) st += (cnt[e] + kTile - 1) / kTile;
+    part[t] = st;
     __syncthreads();
-    for (int off = 1; off < 1024; off <<= 1) {   // inclusive scans of pairs and tasks
-        const int v0 = t >= off ? part[t - off] : 0, v1 = t >= off ? part[1024 + t - off] : 0;
+    for (int off = 1; off < 1024; off <<= 1) {   // inclusive scan of tasks
+        const int v = t >= off ? part[t - off] : 0;
         __syncthreads();
-        part[t] += v0;
-        part[1024 + t] += v1;
+        part[t] += v;
         __syncthreads();
     }
-    int bp = part[t] - sp, bt = part[1024 + t] - st;
+    int bt = part[t] - st;
     for (int e = e0; e < e1; ++e) {
         const int c = cnt[e];
-        for (int i = 0; i * kTile < c; ++i) a.tasks[bt + i] = make_int4(e, bp + kTile * i, min(kTile, c - kTile * i), 0);
-        cur[e] = bp;
-        bp += c;
+        for (int i = 0; i * kTile < c; ++i)
+            a.tasks[bt + i] = make_int4(e, kTile * (bt + i), min(kTile, c - kTile * i), 0);
+        cur[e] = kTile * bt;   // the expert's first slot; its pairs fill its tasks' slots in turn
         bt += (c + kTile - 1) / kTile;
     }
-    if (t == 1023) *a.n_tasks = part[2047];
+    if (t == 1023) *a.n_tasks = part[1023];
     __syncthreads();
     for (int p = t; p < P; p += 1024) {
         const int e = a.ids[p];
-        if (e >= 0 && e < E) a.order[atomicAdd(&cur[e], 1)] = p;
+        int slot = -1;
+        if (e >= 0 && e < E) {
+            slot = atomicAdd(&cur[e], 1);   // consecutive per expert: its tasks' slots have no gaps before the last
+            a.order[slot] = p;
+        }
+        a.pos[p] = slot;
     }
 }
 
 // ---------------------------------------------------------------------------
-// Q8_K of 256-value blocks of rows, one wave per block, in the operand order of
-// the MFMA kernels: per block, chunk e (entry e of every sub-block) holds the 8
-// quants of entry e of sub-blocks 0..7: byte e * 64 + 8 c + j. ROWS_X: token
-// rows; ROWS_H: pair rows, skipped for a bad id (their h is never written).
+// Q8_K of 256-value blocks of rows, one wave per block, written to the slots of
+// the row's pairs (ROWS_X: a token row goes to its k pairs' slots; ROWS_H: a
+// pair row to its slot; bad ids have none) in the operand order of the MFMA
+// kernels. Task i's slots form one region of nb * 4 KiB; in it, per block b,
+// the 16-B piece i of chunk e (the 8 quants of entry e of sub-blocks 2i and
+// 2i + 1) of slot s sits at ((4 b + i) * 4 + e) * 256 + 16 s, so that four lanes
+// of consecutive slots read 64 contiguous bytes.
 // ---------------------------------------------------------------------------
+__device__ __forceinline__ size_t slot_off(int slot, int nb, int blk, int piece, int chunk) {
+    return size_t(slot >> 4) * size_t(nb) * 4096 + size_t(((4 * blk + piece) * 4 + chunk) * 256 + 16 * (slot & 15));
+}
 enum { ROWS_X = 0, ROWS_H = 1 };
 template <int MODE>
 __global__ __launch_bounds__(256) void q8k_rows_kernel(const float* __restrict__ src, int rows, int nb,
                                                        int8_t* __restrict__ q, float* __restrict__ d,
-                                                       const int32_t* __restrict__ ids, int n_experts,
+                                                       const int32_t* __restrict__ pos, int k,
                                                        int* __restrict__ err) {
     const int b = blockIdx.x * 4 + (threadIdx.x >> 6);
     if (b >= rows * nb) return;   // wave-uniform
-    if (MODE == ROWS_H) {
-        const int e = ids[b / nb];
-        if (e < 0 || e >= n_experts) return;
-    }
+    const int row = b / nb, blk = b - row * nb;
+    if (MODE == ROWS_H && pos[row] < 0) return;
     const int lane = threadIdx.x & 63;
     const float4 v4 = reinterpret_cast<const float4*>(src + size_t(b) * 256)[lane];
     const float v[4] = {v4.x, v4.y, v4.z, v4.w};
     const Q8Lane r = q8k_lane(v, lane);
     if (!r.finite && lane == 0) atomicOr(err, kDevErrNonFinite);
-    const int c = lane >> 3, e = (lane >> 1) & 3, j = 4 * (lane & 1);   // values 4 lane .. + 3
-    *reinterpret_cast<uint32_t*>(q + size_t(b) * 256 + 64 * e + 8 * c + j) = r.packed;
+    const int c = lane >> 3, e = (lane >> 1) & 3, j = 8 * (c & 1) + 4 * (lane & 1);   // values 4 lane .. + 3
+    const int np = MODE == ROWS_X ? k : 1;
+    for (int i = 0; i < np; ++i) {
+        const int slot = pos[MODE == ROWS_X ? row * k + i : row];
+        if (slot >= 0) *reinterpret_cast<uint32_t*>(q + slot_off(slot, nb, blk, c >> 1, e) + j) = r.packed;
+    }
     if (lane == 0) d[b] = r.d;
 }
 
@@ -317,8 +326,9 @@ __global__ __launch_bounds__(NW * 64, 1) void gu_kernel(GroupArgs a) {
         const int task = item / groups, grp = item - task * groups;
         const int4 tk = task_at(a.tasks, task);
         const int row = grp * NW * 16 + wv * 16 + col;
-        const int pa = a.order[tk.y + (col < tk.z ? col : 0)];   // A operand: pair col of the task
-        const uint32_t va = uint32_t((pa / a.k) * a.dim + 64 * e4);   // the lane's activation chunk, block 0
+        // A operand: slot col of the task (past its pairs: unused slot memory, whose
+        // outputs are discarded), the lane's chunk e4, block 0
+        const uint32_t va = uint32_t(slot_off(tk.y, nb, 0, 0, e4) + 16 * col);
         int po[4];
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
@@ -336,7 +346,7 @@ __global__ __launch_bounds__(NW * 64, 1) void gu_kernel(GroupArgs a) {
             o.g = ld128(rg, vq + 64u * blk + 16u * e4);
             o.u = ld128(ru, vq + 64u * blk + 16u * e4);
 #pragma unroll
-            for (int i = 0; i < 4; ++i) o.a[i] = ld128(rx, va + 256u * blk + 16u * i);
+            for (int i = 0; i < 4; ++i) o.a[i] = ld128(rx, va + 4096u * blk + 1024u * i);
         };
         auto touch = [&](int blk) { return ld32(rg, vq + 64u * blk) ^ ld32(ru, vq + 64u * blk); };
         float accg[4] = {0.0f, 0.0f, 0.0f, 0.0f}, accu[4] = {0.0f, 0.0f, 0.0f, 0.0f};
@@ -461,8 +471,7 @@ __global__ __launch_bounds__(NW * 64, 1) void dn_kernel(GroupArgs a) {
         const int task = item / groups, grp = item - task * groups;
         const int4 tk = task_at(a.tasks, task);
         const int row = grp * NW * 16 + wv * 16 + col;
-        const int pa = a.order[tk.y + (col < tk.z ? col : 0)];
-        const uint32_t va = uint32_t(pa * nb) * 256u + 64u * e4;   // the lane's activation chunk, block 0
+        const uint32_t va = uint32_t(slot_off(tk.y, nb, 0, 0, e4) + 16 * col);   // as in gu_kernel
         int po[4];
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
@@ -484,7 +493,7 @@ __global__ __launch_bounds__(NW * 64, 1) void dn_kernel(GroupArgs a) {
         auto load = [&](DnOps& o, int blk) {
             o.q = ld128(rd, vq + 64u * blk + 16u * e4);
 #pragma unroll
-            for (int i = 0; i < 4; ++i) o.a[i] = ld128(rh, va + 256u * blk + 16u * i);
+            for (int i = 0; i < 4; ++i) o.a[i] = ld128(rh, va + 4096u * blk + 1024u * i);
         };
         auto touch = [&](int blk) { return ld32(rd, vq + 64u * blk); };
         float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
@@ -588,10 +597,10 @@ hipError_t launch_grouped(const GroupArgs& args, int cus, hipStream_t s) {
     hipLaunchKernelGGL(bucket_kernel, dim3(1), dim3(1024), 0, s, args);
     const int nbx = args.dim / 256, nbh = args.ff / 256;
     hipLaunchKernelGGL(q8k_rows_kernel<ROWS_X>, dim3((args.T * nbx + 3) / 4), dim3(256), 0, s, args.x, args.T, nbx,
-                       args.xq, args.xd, args.ids, args.n_experts, args.err);
+                       args.xq, args.xd, args.pos, args.k, args.err);
     hipLaunchKernelGGL(gu_kernel<NW>, dim3(cus), dim3(NW * 64), 0, s, args);
     hipLaunchKernelGGL(q8k_rows_kernel<ROWS_H>, dim3((P * nbh + 3) / 4), dim3(256), 0, s, args.h, P, nbh, args.hq,
-                       args.hd, args.ids, args.n_experts, args.err);
+                       args.hd, args.pos, args.k, args.err);
     hipLaunchKernelGGL(dn_kernel<NW>, dim3(cus), dim3(NW * 64), 0, s, args);
     hipLaunchKernelGGL(gcombine_kernel, dim3((args.dim + 255) / 256, args.T), dim3(256), 0, s, args);
     return hipGetLastError();

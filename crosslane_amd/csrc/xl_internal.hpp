@@ -103,12 +103,14 @@ struct GroupArgs {
     const float* shared;        // T * dim, or null
     float* out;                 // T * dim
     int T, k, n_experts, dim, ff;
-    int8_t* xq; float* xd;      // Q8_K(x) of every token, split form: T * dim quants, T * dim / 256 scales
-    int32_t* order;             // P pair indices, bucketed by expert id (bad ids left out)
-    int4* tasks;                // (expert, first slot in order, pairs <= 16, 0) per task
+    // Slots: task i owns slots 16 i .. 16 i + 15, its pairs in the first ones.
+    int8_t* xq; float* xd;      // Q8_K(x): quants per slot (16 * max tasks * dim, the MFMA order), scales per token
+    int32_t* order;             // pair of each used slot (16 * max tasks)
+    int32_t* pos;               // slot of each pair (P; -1 for a bad id)
+    int4* tasks;                // (expert, first slot, pairs <= 16, 0) per task
     int32_t* n_tasks;           // tasks written by the bucket kernel
     float* h;                   // P * ff
-    int8_t* hq; float* hd;      // Q8_K(h): P * ff / 256 blocks of 512 B (the down kernel's half-split form), scales
+    int8_t* hq; float* hd;      // Q8_K(h): quants per slot (16 * max tasks * ff), scales per pair
     float* y;                   // P * dim
     const uint64_t* tables;     // expanded codebooks (kLayer3TableBytes)
     int* err;

@@ -73,6 +73,33 @@ def test_grouped_vs_oracle_and_layer_calls(orc, dim, ff, E, T, k, skewed, monkey
         lane.close()
 
 
+@pytest.mark.parametrize("T", [16, 17, 33])
+def test_grouped_task_boundaries(orc, T, monkeypatch):
+    """Expert 0 picked by every token: exactly one full 16-pair task (T = 16),
+    a full task plus a one-pair task (17), two full tasks plus one (33); the
+    second pick spreads over experts 1..3. Against per-token layer calls and
+    the oracle."""
+    dim, ff, E, k = 1024, 512, 4, 2
+    step(f"grouped task boundaries T={T}")
+    monkeypatch.setenv("XL_GROUPED_PATH", "2")
+    types = types_map(1, E, 16, 17)
+    lane = xl.Lane(dim, ff, 1, E, types, max_picks=k, max_tokens=64)
+    try:
+        lane.generate(seed=9)
+        rng = np.random.default_rng(T)
+        ids = np.stack([np.zeros(T, np.int32), (1 + np.arange(T) % 3).astype(np.int32)], axis=1)
+        w = rng.random((T, k)).astype(np.float32)
+        x = rng.standard_normal((T, dim)).astype(np.float32)
+        got = lane.grouped_forward(0, ids, w, x)
+        per = np.stack([lane.layer_forward(0, ids[t], w[t], x[t]) for t in range(T)])
+        assert max_rel(got, per) < TOL, max_rel(got, per)
+        pick = [0, 15, T - 1]
+        want = oracle_out(orc, types, 9, dim, ff, ids[pick], w[pick], x[pick], None)
+        assert max_rel(got[pick], want) < TOL, max_rel(got[pick], want)
+    finally:
+        lane.close()
+
+
 def test_grouped_async_and_other_types(orc):
     # Device pointers on a caller stream; a layer whose types the MFMA kernels do
     # not take (IQ1_M) runs one layer call per token and matches those calls bit

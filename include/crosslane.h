@@ -51,7 +51,12 @@ typedef struct xl_config {
     int32_t n_layers;      /* layers in the bank */
     int32_t n_experts;     /* routed experts per layer */
     int32_t max_picks;     /* top-k bound, 1..16 (reference kPicks = 8, model_meta.hpp:18) */
-    int32_t max_tokens;    /* grouped-path token bound (0 = grouped path unused) */
+    int32_t max_tokens;    /* grouped-path token bound (0 = grouped path unused). Its
+                              workspace, with P = max_tokens * max_picks: about
+                              16 * (P / 16 + min(P, n_experts) + 1) * (dim + ff) bytes
+                              of per-slot quants plus 4 * P * (dim + ff) bytes of h
+                              and per-pick rows (~200 MB at 512 tokens, 8 picks,
+                              384 experts, 4096 x 3072) */
     float swiglu_limit;    /* SwiGLU limit (model_meta.hpp:34 `lim`, the pack's swiglu_limit):
                               > 0 clamps g to <= lim and u to [-lim, lim] before
                               SiLU(g) * u (q8k_core.hpp:92-95); <= 0: no clamp */

@@ -1,20 +1,27 @@
-"""Builds libcrosslane.so in-tree with hipcc for gfx950 (no JIT cache)."""
+"""Builds libcrosslane.so in-tree with hipcc for gfx950 (no JIT cache).
+
+Every source is compiled to its own object in parallel (each carries its own
+gfx950 code object; no relocatable device code is needed), then linked once.
+"""
 from __future__ import annotations
 
 import os
 import subprocess
 import sys
+from concurrent.futures import ThreadPoolExecutor
 
 PKG = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(PKG, "csrc")
 LIB = os.path.join(PKG, "libcrosslane.so")
-SOURCES = ["xl_kernels.hip", "xl_layer.hip", "xl_stream.hip", "xl_grouped.hip", "xl_per32.hip", "xl_hc.hip", "xl_api.cpp"]
+OBJDIR = os.path.join(PKG, "_build")
+SOURCES = ["xl_kernels.hip", "xl_layer.hip", "xl_stream.hip", "xl_grouped.hip", "xl_per32.hip", "xl_hc.hip",
+           "xl_api.cpp"]
 HEADERS = ["xl_format.hpp", "xl_rows.hpp", "xl_internal.hpp", "xl_dev.hpp", "xl_codebooks.inc", "exports.map"]
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = os.environ.get("XL_OFFLOAD_ARCH", "gfx950")
-FLAGS = [
-    f"--offload-arch={ARCH}", "-O3", "-std=c++20", "-fPIC", "-shared",
+CFLAGS = [
+    f"--offload-arch={ARCH}", "-O3", "-std=c++20", "-fPIC",
     # IEEE-exact arithmetic: no implicit FMA contraction, no fast math.
     "-ffp-contract=off", "-fno-fast-math",
     # Packed-FP32 VALU forms are kept out of the generated code.
@@ -23,20 +30,35 @@ FLAGS = [
     # broadcast their result at once, which stalls on the return value.
     "-mllvm", "-amdgpu-atomic-optimizer-strategy=None",
     "-Wall", "-Wno-unused-function", "-Wno-unknown-pragmas",
-    f"-Wl,--version-script={os.path.join(CSRC, 'exports.map')}",
 ]
+LDFLAGS = [f"--offload-arch={ARCH}", "-shared", "-fPIC", f"-Wl,--version-script={os.path.join(CSRC, 'exports.map')}"]
 
 
-def build(verbose: bool = False) -> str:
-    srcs = [os.path.join(CSRC, s) for s in SOURCES]
-    tmp = LIB + ".tmp"
-    cmd = [HIPCC, *FLAGS, *srcs, "-o", tmp]
+def _compile(src: str, verbose: bool) -> str:
+    obj = os.path.join(OBJDIR, os.path.splitext(src)[0] + ".o")
+    cmd = [HIPCC, *CFLAGS, "-c", os.path.join(CSRC, src), "-o", obj]
     if verbose:
         print(" ".join(cmd), flush=True)
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         sys.stderr.write(r.stdout + r.stderr)
-        raise RuntimeError("hipcc build of libcrosslane.so failed")
+        raise RuntimeError(f"hipcc build of {src} failed")
+    return obj
+
+
+def build(verbose: bool = False, jobs: int = 0) -> str:
+    os.makedirs(OBJDIR, exist_ok=True)
+    jobs = jobs or max(1, min(len(SOURCES), os.cpu_count() or 1))
+    with ThreadPoolExecutor(jobs) as pool:
+        objs = list(pool.map(lambda s: _compile(s, verbose), SOURCES))
+    tmp = LIB + ".tmp"
+    cmd = [HIPCC, *LDFLAGS, *objs, "-o", tmp]
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        sys.stderr.write(r.stdout + r.stderr)
+        raise RuntimeError("hipcc link of libcrosslane.so failed")
     os.replace(tmp, LIB)
     return LIB
 

@@ -188,6 +188,13 @@ struct xl_context {
         std::vector<hipEvent_t> ev;      // max_calls * (kMaxStages + 1)
         std::vector<std::string> names;
     } prof;
+    // Call ordering across streams: every device call records `done` on its
+    // stream when it has been enqueued; a call on another stream first waits
+    // for it, so the calls of one context never overlap whatever streams they
+    // name (they share the workspace, the exchange buffers and the counters).
+    hipEvent_t done = nullptr;
+    hipStream_t last_stream = nullptr;
+    bool has_last = false;
 };
 
 namespace {
@@ -254,6 +261,31 @@ void ready(const xl_context* ctx, bool need_bank) {
 
 hipStream_t pick_stream(const xl_context* ctx, void* s) { return s ? static_cast<hipStream_t>(s) : ctx->stream; }
 
+// Orders one call's device work after the context's previous call (see
+// xl_context::done): waits on another stream's last call at construction,
+// records this call's end at destruction (also when the call failed part way:
+// what it enqueued is then ordered too).
+struct Ordered {
+    xl_context* ctx;
+    hipStream_t s;
+    bool carried = false;   // the call's last launch already carries `done` as its stop event
+    Ordered(xl_context* c, hipStream_t st) : ctx(c), s(st) {
+        if (ctx->has_last && ctx->last_stream != s) hip_check(hipStreamWaitEvent(s, ctx->done, 0), "order after the previous call");
+    }
+    // The single-launch layer calls hand `done` to the launch itself (no marker
+    // packet between back-to-back layers); other calls record it here.
+    hipEvent_t stop() const { return ctx->done; }
+    void carried_by_launch(bool yes) { carried = yes; }
+    ~Ordered() {
+        if (carried || hipEventRecord(ctx->done, s) == hipSuccess) {
+            ctx->last_stream = s;
+            ctx->has_last = true;
+        }
+    }
+    Ordered(const Ordered&) = delete;
+    Ordered& operator=(const Ordered&) = delete;
+};
+
 // Reads and checks the device error flag after draining the stream.
 void drain(xl_context* ctx, hipStream_t s) {
     hip_check(hipStreamSynchronize(s), "stream synchronize");
@@ -285,9 +317,11 @@ void check_layer(const xl_context* ctx, int32_t layer) {
 
 // Enqueues the routed-expert layer on stream s: Q8_K(x), gate/up + SwiGLU,
 // Q8_K(h), down, fixed-order combine. All pointers are device pointers.
-void enqueue_layer(xl_context* ctx, int32_t layer, const int32_t* d_ids, const float* d_w, int32_t k, const float* d_x,
+// Returns true when the layer ran as one launch carrying `stop` (recorded as it
+// completes); false when it took separate launches, which leave `stop` alone.
+bool enqueue_layer(xl_context* ctx, int32_t layer, const int32_t* d_ids, const float* d_w, int32_t k, const float* d_x,
                    const float* d_shared, float* d_out, hipStream_t s, float* g_dbg = nullptr,
-                   float* u_dbg = nullptr) {
+                   float* u_dbg = nullptr, hipEvent_t stop = nullptr) {
     const int dim = ctx->cfg.dim, ff = ctx->cfg.ff, E = ctx->cfg.n_experts;
     const xl::ExpertDesc* descs = ctx->d_descs + size_t(layer) * E;
     const int gu_mask = ctx->gu_mask[size_t(layer)], dn_mask = ctx->dn_mask[size_t(layer)];
@@ -314,16 +348,16 @@ void enqueue_layer(xl_context* ctx, int32_t layer, const int32_t* d_ids, const f
         if (d_out) {
             hipError_t e = hipErrorNotSupported;
             if ((ctx->path == 1 || ctx->path == 4) && gu_mask == 1 && dn_mask == 2) {
-                e = xl::dev::launch_stream(a, ctx->cus, s);
+                e = xl::dev::launch_stream(a, ctx->cus, s, stop);
                 if (e != hipSuccess && e != hipErrorNotSupported) hip_check(e, "streaming layer");
                 (void)hipGetLastError();
             }
             need(ctx->path != 4 || e == hipSuccess, XL_E_ARG, "XL_LAYER_PATH=4: no streaming-kernel instance for this layer");
-            if (e == hipErrorNotSupported) e = xl::dev::launch_layer3(a, gu_mask, dn_mask, ctx->cus, s);
+            if (e == hipErrorNotSupported) e = xl::dev::launch_layer3(a, gu_mask, dn_mask, ctx->cus, s, stop);
             if (e == hipSuccess) {
                 if (a.trace) ctx->timeline_words = uint64_t(ctx->cus) * 16 * 32;
                 mark("layer");
-                return;
+                return stop != nullptr;
             }
             if (e != hipErrorNotSupported) hip_check(e, "single-launch layer");
             (void)hipGetLastError();   // no instance for this shape: separate launches below
@@ -339,7 +373,7 @@ void enqueue_layer(xl_context* ctx, int32_t layer, const int32_t* d_ids, const f
         const hipError_t e = xl::dev::launch_layer_fused(a, gu_mask | dn_mask, ctx->cus, s);
         if (e == hipSuccess) {
             mark("layer");
-            return;
+            return false;
         }
         if (e != hipErrorNotSupported) hip_check(e, "fused layer launch");
         (void)hipGetLastError();   // shape without a fused instance: separate launches below
@@ -360,6 +394,7 @@ void enqueue_layer(xl_context* ctx, int32_t layer, const int32_t* d_ids, const f
         hip_check(xl::dev::launch_combine(d_ids, d_w, k, ctx->y, dim, d_shared, d_out, s), "combine launch");
         mark("combine");
     }
+    return false;
 }
 
 // A per32 matrix: planar IQ (xl_format.hpp) or raw dense ggml blocks.
@@ -463,6 +498,7 @@ int32_t xl_open(uint32_t abi_version, const xl_config* cfg, xl_context** out, xl
         hip_check(hipGetDeviceProperties(&prop, cfg->device), "hipGetDeviceProperties");
         ctx->cus = prop.multiProcessorCount;
         hip_check(hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking), "hipStreamCreate");
+        hip_check(hipEventCreateWithFlags(&ctx->done, hipEventDisableTiming), "hipEventCreate");
         ctx->grid_gu = env_int("XL_WGS_GATE_UP", 4 * ctx->cus);
         ctx->grid_down = env_int("XL_WGS_DOWN", 4 * ctx->cus);
 
@@ -559,10 +595,17 @@ int32_t xl_open(uint32_t abi_version, const xl_config* cfg, xl_context** out, xl
 void xl_close(xl_context* ctx) {
     if (!ctx) return;
     (void)hipSetDevice(ctx->cfg.device);
+    // The last call may have run on a caller stream: wait for it, then for the
+    // context stream, before any memory goes back.
+    if (ctx->done && ctx->has_last) (void)hipEventSynchronize(ctx->done);
     if (ctx->stream) (void)hipStreamSynchronize(ctx->stream);
+    for (auto& e : ctx->prof.ev)   // profiling left active (xl_profile_end never called)
+        if (e) (void)hipEventDestroy(e);
+    ctx->prof.ev.clear();
     for (auto* s : ctx->slabs) (void)hipFree(s);
     if (ctx->d_descs) (void)hipFree(ctx->d_descs);
     if (ctx->ws) (void)hipFree(ctx->ws);
+    if (ctx->done) (void)hipEventDestroy(ctx->done);
     if (ctx->stream) (void)hipStreamDestroy(ctx->stream);
     delete ctx;
 }
@@ -655,6 +698,7 @@ int32_t xl_bank_generate(xl_context* ctx, uint64_t seed, xl_error* err) {
     return guarded(ctx, err, [&] {
         ready(ctx, true);
         const int L = ctx->cfg.n_layers, E = ctx->cfg.n_experts, dim = ctx->cfg.dim, ff = ctx->cfg.ff;
+        Ordered ord(ctx, ctx->stream);
         for (int l = 0; l < L; ++l)
             for (int e = 0; e < E; ++e)
                 for (int r = 0; r < 3; ++r) {
@@ -685,6 +729,7 @@ int32_t xl_bank_upload(xl_context* ctx, int32_t layer, int32_t expert, int32_t r
         const auto* src = static_cast<const uint8_t*>(aos);
         for (uint64_t b = 0; b < nblk; ++b)
             xl::block_to_planes(m.type, src + b * xl::block_bytes(m.type), planar.data(), P, b);
+        Ordered ord(ctx, ctx->stream);
         hip_check(hipMemcpyAsync(const_cast<uint8_t*>(m.base), planar.data(), P.bytes, hipMemcpyHostToDevice, ctx->stream),
                   "weight upload");
         hip_check(hipStreamSynchronize(ctx->stream), "weight upload drain");
@@ -876,6 +921,7 @@ int32_t xl_bank_download(xl_context* ctx, int32_t layer, int32_t expert, int32_t
         need(bytes == nblk * uint64_t(xl::block_bytes(m.type)), XL_E_ARG, "output byte extent differs from shape");
         const auto P = xl::plane_layout(m.type, nblk);
         std::vector<uint8_t> planar(P.bytes);
+        Ordered ord(ctx, ctx->stream);
         hip_check(hipMemcpyAsync(planar.data(), m.base, P.bytes, hipMemcpyDeviceToHost, ctx->stream), "weight download");
         hip_check(hipStreamSynchronize(ctx->stream), "weight download drain");
         auto* dst = static_cast<uint8_t*>(aos);
@@ -909,6 +955,7 @@ int32_t xl_experts_forward(xl_context* ctx, int32_t layer, const int32_t* ids, i
         check_finite(x, size_t(ctx->cfg.dim), "input vector");
         need(ys != nullptr, XL_E_ARG, "null output");
         hipStream_t s = ctx->stream;
+        Ordered ord(ctx, s);
         hip_check(hipMemcpyAsync(ctx->ids, ids, sizeof(int32_t) * k, hipMemcpyHostToDevice, s), "ids upload");
         hip_check(hipMemcpyAsync(ctx->x, x, sizeof(float) * ctx->cfg.dim, hipMemcpyHostToDevice, s), "x upload");
         enqueue_layer(ctx, layer, ctx->ids, nullptr, k, ctx->x, nullptr, nullptr, s);
@@ -981,6 +1028,7 @@ int32_t xl_grouped_forward(xl_context* ctx, int32_t layer, int32_t T, int32_t k,
         check_finite(x, size_t(T) * dim, "input vectors");
         if (shared_or_null) check_finite(shared_or_null, size_t(T) * dim, "shared vectors");
         hipStream_t s = ctx->stream;
+        Ordered ord(ctx, s);
         auto& g = ctx->grp;
         const size_t P = size_t(T) * k, X = size_t(T) * dim;
         hip_check(hipMemcpyAsync(g.ids, ids, sizeof(int32_t) * P, hipMemcpyHostToDevice, s), "ids upload");
@@ -1002,7 +1050,9 @@ int32_t xl_grouped_forward_async(xl_context* ctx, int32_t layer, int32_t T, int3
         check_layer(ctx, layer);
         check_grouped(ctx, T, k);
         need(d_ids && d_w && d_x && d_out, XL_E_ARG, "null device pointer");
-        enqueue_grouped(ctx, layer, T, k, d_ids, d_w, d_x, d_shared_or_null, d_out, pick_stream(ctx, stream));
+        hipStream_t s = pick_stream(ctx, stream);
+        Ordered ord(ctx, s);
+        enqueue_grouped(ctx, layer, T, k, d_ids, d_w, d_x, d_shared_or_null, d_out, s);
     });
 }
 
@@ -1016,8 +1066,9 @@ int32_t xl_route_async(xl_context* ctx, const float* d_logits, int32_t T, int32_
         need(k >= 1 && k <= 16 && k <= n, XL_E_ARG, "pick count outside 1..min(16, n)");
         need(stride >= n, XL_E_ARG, "logit stride below the expert count");
         need(std::isfinite(scale) && scale >= 0.0f, XL_E_ARG, "route scale must be finite and >= 0");
-        hip_check(xl::dev::launch_route(d_logits, T, stride, d_bias_or_null, n, k, scale, d_ids, d_w, ctx->err_flag,
-                                        pick_stream(ctx, stream)),
+        hipStream_t s = pick_stream(ctx, stream);
+        Ordered ord(ctx, s);
+        hip_check(xl::dev::launch_route(d_logits, T, stride, d_bias_or_null, n, k, scale, d_ids, d_w, ctx->err_flag, s),
                   "route launch");
     });
 }
@@ -1033,10 +1084,12 @@ int32_t xl_layer_forward_routed_async(xl_context* ctx, int32_t layer, const floa
         need(std::isfinite(scale) && scale >= 0.0f, XL_E_ARG, "route scale must be finite and >= 0");
         need(d_logits && d_x && d_out, XL_E_ARG, "null device pointer");
         hipStream_t s = pick_stream(ctx, stream);
+        Ordered ord(ctx, s);
         const int n = ctx->cfg.n_experts;
         hip_check(xl::dev::launch_route(d_logits, 1, n, d_bias_or_null, n, k, scale, ctx->ids, ctx->w, ctx->err_flag, s),
                   "route launch");
-        enqueue_layer(ctx, layer, ctx->ids, ctx->w, k, d_x, d_shared_or_null, d_out, s);
+        ord.carried_by_launch(enqueue_layer(ctx, layer, ctx->ids, ctx->w, k, d_x, d_shared_or_null, d_out, s, nullptr,
+                                            nullptr, ord.stop()));
     });
 }
 
@@ -1051,6 +1104,7 @@ int32_t xl_grouped_forward_routed_async(xl_context* ctx, int32_t layer, int32_t 
         need(std::isfinite(scale) && scale >= 0.0f, XL_E_ARG, "route scale must be finite and >= 0");
         need(d_logits && d_x && d_out, XL_E_ARG, "null device pointer");
         hipStream_t s = pick_stream(ctx, stream);
+        Ordered ord(ctx, s);
         const int n = ctx->cfg.n_experts;
         auto& g = ctx->grp;
         hip_check(xl::dev::launch_route(d_logits, T, n, d_bias_or_null, n, k, scale, g.ids, g.w, ctx->err_flag, s),
@@ -1070,6 +1124,7 @@ int32_t xl_layer_forward(xl_context* ctx, int32_t layer, const int32_t* ids, con
         if (shared_or_null) check_finite(shared_or_null, size_t(ctx->cfg.dim), "shared vector");
         need(out != nullptr, XL_E_ARG, "null output");
         hipStream_t s = ctx->stream;
+        Ordered ord(ctx, s);
         const int dim = ctx->cfg.dim;
         hip_check(hipMemcpyAsync(ctx->ids, ids, sizeof(int32_t) * k, hipMemcpyHostToDevice, s), "ids upload");
         hip_check(hipMemcpyAsync(ctx->w, w, sizeof(float) * k, hipMemcpyHostToDevice, s), "weights upload");
@@ -1092,6 +1147,7 @@ int32_t xl_expert_trace(xl_context* ctx, int32_t layer, int32_t expert, const fl
         check_ids(ctx, &id, 1);
         check_finite(x, size_t(ctx->cfg.dim), "input vector");
         hipStream_t s = ctx->stream;
+        Ordered ord(ctx, s);
         const int dim = ctx->cfg.dim, ff = ctx->cfg.ff;
         hip_check(hipMemcpyAsync(ctx->ids, &id, sizeof id, hipMemcpyHostToDevice, s), "ids upload");
         hip_check(hipMemcpyAsync(ctx->x, x, sizeof(float) * dim, hipMemcpyHostToDevice, s), "x upload");
@@ -1115,7 +1171,10 @@ int32_t xl_layer_forward_async(xl_context* ctx, int32_t layer, const int32_t* d_
         check_layer(ctx, layer);
         need(k >= 1 && k <= ctx->cfg.max_picks, XL_E_ARG, "pick count outside 1..max_picks");
         need(d_ids && d_w && d_x && d_out, XL_E_ARG, "null device pointer");
-        enqueue_layer(ctx, layer, d_ids, d_w, k, d_x, d_shared_or_null, d_out, pick_stream(ctx, stream));
+        hipStream_t s = pick_stream(ctx, stream);
+        Ordered ord(ctx, s);
+        ord.carried_by_launch(enqueue_layer(ctx, layer, d_ids, d_w, k, d_x, d_shared_or_null, d_out, s, nullptr, nullptr,
+                                            ord.stop()));
     });
 }
 
@@ -1131,6 +1190,7 @@ int32_t xl_layer_forward_per32(xl_context* ctx, int32_t layer, const int32_t* id
         if (out_or_null) check_finite(w, size_t(k), "route weights");
         if (out_or_null && shared_or_null) check_finite(shared_or_null, size_t(ctx->cfg.dim), "shared vector");
         hipStream_t s = ctx->stream;
+        Ordered ord(ctx, s);
         const int dim = ctx->cfg.dim;
         hip_check(hipMemcpyAsync(ctx->ids, ids, sizeof(int32_t) * k, hipMemcpyHostToDevice, s), "ids upload");
         if (out_or_null) hip_check(hipMemcpyAsync(ctx->w, w, sizeof(float) * k, hipMemcpyHostToDevice, s), "weights upload");
@@ -1160,7 +1220,9 @@ int32_t xl_layer_forward_per32_async(xl_context* ctx, int32_t layer, const int32
         need(k >= 1 && k <= ctx->cfg.max_picks, XL_E_ARG, "pick count outside 1..max_picks");
         need(d_ids && d_x && d_y, XL_E_ARG, "null device pointer");
         need(!d_out_or_null || d_w, XL_E_ARG, "a combined output needs route weights");
-        enqueue_per32(ctx, layer, d_ids, d_w, k, d_x, d_shared_or_null, d_y, d_out_or_null, pick_stream(ctx, stream));
+        hipStream_t s = pick_stream(ctx, stream);
+        Ordered ord(ctx, s);
+        enqueue_per32(ctx, layer, d_ids, d_w, k, d_x, d_shared_or_null, d_y, d_out_or_null, s);
     });
 }
 
@@ -1171,7 +1233,9 @@ int32_t xl_quantize_per32_async(xl_context* ctx, const float* d_x, int32_t rows,
         need(d_x && d_q && d_d, XL_E_ARG, "null device pointer");
         need(rows >= 1 && k >= 32 && k % 32 == 0, XL_E_ARG, "rows >= 1 and k a positive multiple of 32");
         need(int64_t(rows) * k <= int64_t(1) << 30, XL_E_ARG, "more than 2^30 values");
-        hip_check(xl::dev::launch_quant32(d_x, rows, k, d_q, d_d, ctx->err_flag, pick_stream(ctx, stream)),
+        hipStream_t s = pick_stream(ctx, stream);
+        Ordered ord(ctx, s);
+        hip_check(xl::dev::launch_quant32(d_x, rows, k, d_q, d_d, ctx->err_flag, s),
                   "quant32 launch");
     });
 }
@@ -1186,8 +1250,10 @@ int32_t xl_matvec_per32_async(xl_context* ctx, int32_t type, const void* d_plana
         need(n >= 1 && n <= (1 << 24) && k >= 256 && k % 256 == 0 && k <= (1 << 20), XL_E_ARG,
              "n in 1..2^24 and k a multiple of 256 up to 2^20");
         const xl::MatRef m = per32_matrix(type, d_planar, n, k);
+        hipStream_t s = pick_stream(ctx, stream);
+        Ordered ord(ctx, s);
         hip_check(xl::dev::launch_mv32(nullptr, nullptr, m, m, 1, 0, 0, 1, n, k, d_q, 0, d_d, 0, d_y, nullptr, 0,
-                                       ctx->tables, ctx->err_flag, pick_stream(ctx, stream)),
+                                       ctx->tables, ctx->err_flag, s),
                   "per32 matvec launch");
     });
 }
@@ -1223,6 +1289,7 @@ int32_t xl_shared_forward_async(xl_context* ctx, int32_t type_gate, const void* 
         const xl::MatRef mg = per32_matrix(type_gate, d_gate, ff, dim), mu = per32_matrix(type_up, d_up, ff, dim);
         const xl::MatRef md = per32_matrix(type_down, d_down, dim, ff);
         hipStream_t s = pick_stream(ctx, stream);
+        Ordered ord(ctx, s);
         // hip_backend.cpp:664-666: mv(gate, up), swiglu, mv(down), T tokens per launch
         hip_check(xl::dev::launch_quant32(d_x, T, dim, xq, xd, ctx->err_flag, s), "quant32(x) launch");
         hip_check(xl::dev::launch_mv32(nullptr, nullptr, mg, mu, T, 0, 0, 2, ff, dim, xq, size_t(dim), xd,
@@ -1255,7 +1322,9 @@ int32_t xl_hc_post_async(xl_context* ctx, const float* d_y, const float* d_res, 
         need(!overlaps(d_y, uint64_t(T) * D * 4) && !overlaps(d_post, uint64_t(T) * 32) &&
                  !overlaps(d_comb, uint64_t(T) * 256),
              XL_E_ARG, "hc output overlaps an input");
-        hip_check(xl::dev::launch_hc_post(d_y, d_res, d_post, d_comb, D, H, T, d_out, pick_stream(ctx, stream)),
+        hipStream_t s = pick_stream(ctx, stream);
+        Ordered ord(ctx, s);
+        hip_check(xl::dev::launch_hc_post(d_y, d_res, d_post, d_comb, D, H, T, d_out, s),
                   "hc_post launch");
     });
 }
@@ -1264,6 +1333,8 @@ int32_t xl_sync(xl_context* ctx, void* stream, xl_error* err) {
     return guarded(ctx, err, [&] {
         need(ctx != nullptr, XL_E_ARG, "null context");
         hip_check(hipSetDevice(ctx->cfg.device), "hipSetDevice");
+        // the context's last call first (it may have run on another stream), then the named stream
+        if (ctx->has_last) hip_check(hipEventSynchronize(ctx->done), "last call synchronize");
         drain(ctx, pick_stream(ctx, stream));
     });
 }
@@ -1276,8 +1347,9 @@ int32_t xl_quantize_q8k_async(xl_context* ctx, const float* d_x, int32_t rows, i
         need(rows >= 1 && k >= 256 && k % 256 == 0, XL_E_ARG, "rows >= 1 and k a positive multiple of 256");
         const uint64_t nblocks = uint64_t(rows) * uint64_t(k / 256);
         need(nblocks <= uint64_t(ctx->act_max / 256), XL_E_ARG, "more blocks than the activation workspace holds");
-        hip_check(xl::dev::launch_q8k(d_x, int(nblocks), ctx->xq, ctx->xd, static_cast<uint8_t*>(d_q8k), ctx->err_flag,
-                                      pick_stream(ctx, stream)),
+        hipStream_t s = pick_stream(ctx, stream);
+        Ordered ord(ctx, s);
+        hip_check(xl::dev::launch_q8k(d_x, int(nblocks), ctx->xq, ctx->xd, static_cast<uint8_t*>(d_q8k), ctx->err_flag, s),
                   "Q8_K launch");
     });
 }
@@ -1289,7 +1361,9 @@ int32_t xl_swiglu_async(xl_context* ctx, const float* d_g, const float* d_u, int
         need(d_g && d_u && d_h, XL_E_ARG, "null device pointer");
         need(n >= 1 && n <= (1 << 28), XL_E_ARG, "n outside 1..2^28");
         need(std::isfinite(limit), XL_E_ARG, "limit not finite");
-        hip_check(xl::dev::launch_swiglu(d_g, d_u, n, limit, d_h, pick_stream(ctx, stream)), "SwiGLU launch");
+        hipStream_t s = pick_stream(ctx, stream);
+        Ordered ord(ctx, s);
+        hip_check(xl::dev::launch_swiglu(d_g, d_u, n, limit, d_h, s), "SwiGLU launch");
     });
 }
 
@@ -1303,6 +1377,7 @@ int32_t xl_matvec_async(xl_context* ctx, int32_t type, const void* d_planar, int
         need(n >= 1 && xl::row_shape(k, lpr, ppl), XL_E_ARG, "unsupported matvec shape");
         need(k <= ctx->act_max, XL_E_ARG, "k exceeds the activation workspace");
         hipStream_t s = pick_stream(ctx, stream);
+        Ordered ord(ctx, s);
         hip_check(xl::dev::launch_q8k(d_x, k / 256, ctx->xq, ctx->xd, nullptr, ctx->err_flag, s), "Q8_K launch");
         const auto P = xl::plane_layout(type, matrix_blocks(n, k));
         xl::MatRef m{};
@@ -1358,6 +1433,19 @@ int32_t xl_profile_end(xl_context* ctx, float* stage_ms, int32_t max_stages, int
             for (int i = 0; i < S && i < int(P.names.size()); ++i) { if (i) all += ','; all += P.names[i]; }
             std::snprintf(names, size_t(names_bytes), "%s", all.c_str());
         }
+    });
+}
+
+int32_t xl_debug_set_launch_count(xl_context* ctx, uint32_t launches, xl_error* err) {
+    return guarded(ctx, err, [&] {
+        ready(ctx, false);
+        hipStream_t s = ctx->stream;
+        Ordered ord(ctx, s);
+        // ctl[0]: the all-types kernel's epoch, ctl[2]: the streaming kernel's launch
+        // count (its parity); the arrival counters ctl[1], ctl[3] are zero between launches.
+        const uint32_t w[4] = {launches, 0u, launches, 0u};
+        hip_check(hipMemcpyAsync(ctx->ctl, w, sizeof w, hipMemcpyHostToDevice, s), "launch count upload");
+        hip_check(hipStreamSynchronize(s), "launch count drain");
     });
 }
 

@@ -126,10 +126,13 @@ namespace dev {
 // Single-launch layer: hipErrorNotSupported when (dim, ff, k) has no instance.
 // gu_types / dn_types: block types among the layer's gate/up / down matrices
 // (bits 1 IQ2_XXS, 2 IQ2_XS, 4 IQ1_M) select the kernel instance.
-hipError_t launch_layer3(const Layer3Args& args, int gu_types, int dn_types, int cus, hipStream_t s);
+// `stop` (may be null) is recorded as the launch completes (hipExtLaunchKernel's
+// stop event: no extra packet on the stream).
+hipError_t launch_layer3(const Layer3Args& args, int gu_types, int dn_types, int cus, hipStream_t s,
+                         hipEvent_t stop = nullptr);
 // Streaming layer for IQ2_XXS gate/up + IQ2_XS down: hipErrorNotSupported when
 // (dim, ff, k) has no instance.
-hipError_t launch_stream(const Layer3Args& args, int cus, hipStream_t s);
+hipError_t launch_stream(const Layer3Args& args, int cus, hipStream_t s, hipEvent_t stop = nullptr);
 // Grouped path: hipErrorNotSupported unless gate/up are IQ2_XXS, down IQ2_XS and
 // the shapes fit (dim, ff multiples of 128; n_experts <= kGroupMaxExperts).
 hipError_t launch_grouped(const GroupArgs& args, int cus, hipStream_t s);

@@ -29,13 +29,15 @@
 // are resident at once. Every wait is bounded: on expiry the kernel raises
 // kDevErrTimeout and finishes.
 //
-// Epoch: each launch reads the device word E and tags its data E + 1; the last
-// workgroup to arrive (an arrival counter) stores E + 1 for the next launch.
-// The tag never comes from the host, so a captured launch can be replayed.
+// Epoch: each launch reads the device word E and tags its data E + 1 (0 is
+// skipped: zero is what unwritten tags hold); the last workgroup to arrive (an
+// arrival counter) stores that tag for the next launch. The tag never comes
+// from the host, so a captured launch can be replayed.
 //
 // Cross-workgroup data moves through agent-scope (sc1) atomic loads and stores,
 // which are coherent across the XCDs' L2 caches; every published word carries
 // its own tag, so no store ordering wait is needed.
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 
 #include "xl_dev.hpp"
@@ -388,7 +390,10 @@ __global__ __launch_bounds__(NW * 64, 1) void layer3_kernel(Layer3Args a) {
         s_w[lane] = cw;
     }
     if (t < 16) s_hq_ready[t] = 0u;
-    if (t == 0) s_epoch = e_prev + 1u;
+    // Epoch 0 is never used: tags start zeroed (and s_hq_ready is zeroed every
+    // launch), so a launch tagging with 0 would read words no one has written.
+    // After 2^32 - 1 launches the count wraps from 0xffffffff to 1.
+    if (t == 0) s_epoch = e_prev + 1u == 0u ? 1u : e_prev + 1u;
     lds_barrier();
     const uint32_t epoch = s_epoch;
     // Arrival: this workgroup has read the epoch word. Whoever arrives last
@@ -593,7 +598,7 @@ __global__ __launch_bounds__(NW * 64, 1) void layer3_kernel(Layer3Args a) {
 
 // ---- launcher ------------------------------------------------------------------------------
 template <int NW, int LG, int PG, int LD, int PD, int MG, int MD, int WIN, int WIND, int GUT, int DNT>
-static hipError_t launch3(const Layer3Args& args, int grid, hipStream_t s) {
+static hipError_t launch3(const Layer3Args& args, int grid, hipStream_t s, hipEvent_t stop) {
     constexpr int RG = 64 / LG, RD = 64 / LD;
     const int W = grid * NW;
     const int SG = args.k * (args.ff / RG);
@@ -605,8 +610,8 @@ static hipError_t launch3(const Layer3Args& args, int grid, hipStream_t s) {
         args.ff > 4096 || Lay<GUT | DNT>::HQ + args.k * (args.ff + 64) > kLdsBytes ||
         Lay<GUT | DNT>::HQ + 16384 > kLdsBytes)   // the codebooks' single copies are staged there
         return hipErrorNotSupported;
-    hipLaunchKernelGGL((layer3_kernel<NW, LG, PG, LD, PD, MG, MD, WIN, WIND, GUT, DNT>), dim3(grid), dim3(NW * 64), 0, s,
-                       args);
+    hipExtLaunchKernelGGL((layer3_kernel<NW, LG, PG, LD, PD, MG, MD, WIN, WIND, GUT, DNT>), dim3(grid), dim3(NW * 64), 0,
+                          s, nullptr, stop, 0, args);
     return hipGetLastError();
 }
 
@@ -614,28 +619,29 @@ static hipError_t launch3(const Layer3Args& args, int grid, hipStream_t s) {
 // {IQ2_XS}) and ({IQ1_M}, {IQ1_M}) have their own instances; anything else
 // takes the all-types one.
 template <int NW, int LG, int PG, int LD, int PD, int MG, int MD, int WIN, int WIND>
-static hipError_t launch3_types(const Layer3Args& args, int gu_types, int dn_types, int grid, hipStream_t s) {
-    if (gu_types == 1 && dn_types == 2) return launch3<NW, LG, PG, LD, PD, MG, MD, WIN, WIND, 1, 2>(args, grid, s);
-    if (gu_types == 4 && dn_types == 4) return launch3<NW, LG, PG, LD, PD, MG, MD, WIN, WIND, 4, 4>(args, grid, s);
-    return launch3<NW, LG, PG, LD, PD, MG, MD, WIN, WIND, 7, 7>(args, grid, s);
+static hipError_t launch3_types(const Layer3Args& args, int gu_types, int dn_types, int grid, hipStream_t s,
+                                hipEvent_t stop) {
+    if (gu_types == 1 && dn_types == 2) return launch3<NW, LG, PG, LD, PD, MG, MD, WIN, WIND, 1, 2>(args, grid, s, stop);
+    if (gu_types == 4 && dn_types == 4) return launch3<NW, LG, PG, LD, PD, MG, MD, WIN, WIND, 4, 4>(args, grid, s, stop);
+    return launch3<NW, LG, PG, LD, PD, MG, MD, WIN, WIND, 7, 7>(args, grid, s, stop);
 }
 
-hipError_t launch_layer3(const Layer3Args& args, int gu_types, int dn_types, int cus, hipStream_t s) {
+hipError_t launch_layer3(const Layer3Args& args, int gu_types, int dn_types, int cus, hipStream_t s, hipEvent_t stop) {
     if (args.k < 1 || args.k > 16 || args.dim > 4096) return hipErrorNotSupported;
     int lg, pg, ld, pd;
     if (!row_shape(args.dim, lg, pg) || !row_shape(args.ff, ld, pd)) return hipErrorNotSupported;
     const int RD = 64 / ld;
     const int grid = std::min(cus, args.dim / RD);
     if (lg == 64 && pg == 1 && ld == 16 && pd == 3)   // 4096 x 3072
-        return launch3_types<8, 64, 1, 16, 3, 9, 3, 3, 1>(args, gu_types, dn_types, grid, s);
+        return launch3_types<8, 64, 1, 16, 3, 9, 3, 3, 1>(args, gu_types, dn_types, grid, s, stop);
     if (lg == 16 && pg == 1 && ld == 8 && pd == 1)    // 1024 x 512
-        return launch3<8, 16, 1, 8, 1, 6, 2, 3, 1, 7, 7>(args, grid, s);
+        return launch3<8, 16, 1, 8, 1, 6, 2, 3, 1, 7, 7>(args, grid, s, stop);
     if (lg == 4 && pg == 1 && ld == 4 && pd == 3)     // 256 x 768
-        return launch3<8, 4, 1, 4, 3, 6, 2, 3, 1, 7, 7>(args, grid, s);
+        return launch3<8, 4, 1, 4, 3, 6, 2, 3, 1, 7, 7>(args, grid, s, stop);
     if (lg == 8 && pg == 1 && ld == 4 && pd == 1)     // 512 x 256
-        return launch3<8, 8, 1, 4, 1, 6, 2, 3, 1, 7, 7>(args, grid, s);
+        return launch3<8, 8, 1, 4, 1, 6, 2, 3, 1, 7, 7>(args, grid, s, stop);
     if (lg == 4 && pg == 1 && ld == 4 && pd == 1)     // 256 x 256
-        return launch3<8, 4, 1, 4, 1, 6, 2, 3, 1, 7, 7>(args, grid, s);
+        return launch3<8, 4, 1, 4, 1, 6, 2, 3, 1, 7, 7>(args, grid, s, stop);
     return hipErrorNotSupported;
 }
 

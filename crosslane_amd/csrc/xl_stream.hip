@@ -38,6 +38,7 @@
 // The launch parity comes from a device word advanced by the last workgroup to
 // arrive (an arrival counter), never from the host, so a captured launch can
 // be replayed.
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 
 #include <utility>
@@ -108,16 +109,6 @@ __device__ __forceinline__ uint32_t neg_bytes(uint32_t x) {
     const uint32_t lo = ((x & 0x00ff00ffu) ^ 0x00ff00ffu) + 0x00010001u;   // bytes 0, 2 (a carry lands in 1, 3)
     const uint32_t hi = ((x & 0xff00ff00u) ^ 0xff00ff00u) + 0x01000100u;   // bytes 1, 3
     return (lo & 0x00ff00ffu) | (hi & 0xff00ff00u);
-}
-
-// h = silu(g) * u with the hardware exp2 and reciprocal (about 1 ulp each): h
-// only feeds Q8_K(h), and the layer output is held to a relative 1e-3, not to
-// the bits of the reference's expf. g -> -inf gives -0, g -> +inf gives g * u.
-// The SwiGLU limit (lim > 0) clamps g and u first, as q8k_core.hpp:92-93.
-__device__ __forceinline__ float silu_fast(float g, float u, float lim) {
-    swiglu_clamp(g, u, lim);
-    const float e = __builtin_amdgcn_exp2f(__fmul_rn(g, -1.4426950408889634f));
-    return __fmul_rn(__fmul_rn(g, __builtin_amdgcn_rcpf(__fadd_rn(1.0f, e))), u);
 }
 
 // ---- pair decoders -------------------------------------------------------------------------
@@ -534,7 +525,10 @@ __global__ __launch_bounds__(NW * 64, 1) void stream_kernel(Layer3Args a) {
             bu = mine ? u : bu;
             hidx = mine ? hrow(j) + rG : hidx;
             if (b == kBatch - 1 || j == MG - 1) {
-                const float hv = silu_fast(__fmul_rn(0.125f, bg), __fmul_rn(0.125f, bu), a.lim);
+                // (g / (1 + exp(-g))) * u with the device expf and an IEEE division, as
+                // q8k_core.hpp:92-95: an approximate exp or reciprocal moves h by an ulp
+                // often enough to flip Q8_K(h) quants (a 1e-4-scale output change each)
+                const float hv = silu_mul3(__fmul_rn(0.125f, bg), __fmul_rn(0.125f, bu), a.lim);
                 const uint32_t hb = __float_as_uint(hv) == kSentinel ? kQNaN : __float_as_uint(hv);
                 if (lG >= LG - 1 - b && hidx >= 0)
                     __hip_atomic_store(reinterpret_cast<uint32_t*>(hcur) + hidx, hb, __ATOMIC_RELAXED,
@@ -659,7 +653,7 @@ __global__ __launch_bounds__(NW * 64, 1) void stream_kernel(Layer3Args a) {
 }
 
 template <int NW, int LG, int PG, int LD, int PD, int MG, int MD, int WIN, int WIND, int MQ>
-hipError_t launch_stream_t(const Layer3Args& args, int grid, hipStream_t s) {
+hipError_t launch_stream_t(const Layer3Args& args, int grid, hipStream_t s, hipEvent_t stop) {
     constexpr int RG = 64 / LG, RD = 64 / LD;
     const int W = grid * NW;
     const int SG = args.k * (args.ff / RG);
@@ -680,27 +674,28 @@ hipError_t launch_stream_t(const Layer3Args& args, int grid, hipStream_t s) {
         grid > quads || args.k * (args.ff + 64) > kS_HQBytes || args.k * args.ff > kHBufWords || !args.hbuf ||
         !args.slab)   // regular layers only: every matrix is found from its expert id
         return hipErrorNotSupported;
-    hipLaunchKernelGGL((stream_kernel<NW, LG, PG, LD, PD, MG, MD, WIN, WIND, MQ>), dim3(grid), dim3(NW * 64), 0, s, args);
+    hipExtLaunchKernelGGL((stream_kernel<NW, LG, PG, LD, PD, MG, MD, WIN, WIND, MQ>), dim3(grid), dim3(NW * 64), 0, s,
+                          nullptr, stop, 0, args);
     return hipGetLastError();
 }
 
 }  // namespace
 
-hipError_t launch_stream(const Layer3Args& args, int cus, hipStream_t s) {
+hipError_t launch_stream(const Layer3Args& args, int cus, hipStream_t s, hipEvent_t stop) {
     if (args.k < 1 || args.k > 16 || args.dim > 4096 || args.ff > 4096) return hipErrorNotSupported;
     int lg, pg, ld, pd;
     if (!row_shape(args.dim, lg, pg) || !row_shape(args.ff, ld, pd)) return hipErrorNotSupported;
     const int RD = 64 / ld;
     const int grid = std::min(cus, args.dim / RD);
     if (lg == 64 && pg == 1 && ld == 16 && pd == 3) {   // 4096 x 3072: slots and steps sized by the pick count
-        if (args.k <= 2) return launch_stream_t<8, 64, 1, 16, 3, 3, 1, 3, 1, 3>(args, grid, s);
-        if (args.k <= 4) return launch_stream_t<8, 64, 1, 16, 3, 6, 2, 3, 2, 3>(args, grid, s);
-        return launch_stream_t<8, 64, 1, 16, 3, 9, 3, 3, 3, 3>(args, grid, s);
+        if (args.k <= 2) return launch_stream_t<8, 64, 1, 16, 3, 3, 1, 3, 1, 3>(args, grid, s, stop);
+        if (args.k <= 4) return launch_stream_t<8, 64, 1, 16, 3, 6, 2, 3, 2, 3>(args, grid, s, stop);
+        return launch_stream_t<8, 64, 1, 16, 3, 9, 3, 3, 3, 3>(args, grid, s, stop);
     }
     if (lg == 16 && pg == 1 && ld == 8 && pd == 1)    // 1024 x 512
-        return launch_stream_t<8, 16, 1, 8, 1, 6, 2, 3, 1, 2>(args, grid, s);
+        return launch_stream_t<8, 16, 1, 8, 1, 6, 2, 3, 1, 2>(args, grid, s, stop);
     if (lg == 4 && pg == 1 && ld == 4 && pd == 3)     // 256 x 768
-        return launch_stream_t<8, 4, 1, 4, 3, 6, 2, 3, 1, 3>(args, grid, s);
+        return launch_stream_t<8, 4, 1, 4, 3, 6, 2, 3, 1, 3>(args, grid, s, stop);
     return hipErrorNotSupported;
 }
 

@@ -17,6 +17,7 @@ from __future__ import annotations
 
 import ctypes as C
 import os
+import sys
 from typing import Optional, Sequence
 
 import numpy as np
@@ -101,6 +102,7 @@ _SIGNATURES = {
     "xl_profile_begin": (_I32, [_P, _I32, _ErrP]),
     "xl_profile_end": (_I32, [_P, _f32p, _I32, C.POINTER(_I32), C.POINTER(_I32), C.c_char_p, _I32, _ErrP]),
     "xl_profile_timeline": (_I32, [_P, _u64p, _I32, C.POINTER(_I32), _ErrP]),
+    "xl_debug_set_launch_count": (_I32, [_P, C.c_uint32, _ErrP]),
     "xl_planar_bytes": (C.c_uint64, [_I32, _I32, _I32]),
     "xl_repack": (_I32, [_I32, _I32, _I32, _P, _P]),
     "xl_restore": (_I32, [_I32, _I32, _I32, _P, _P]),
@@ -231,6 +233,11 @@ class Lane:
             self._ctx = None
 
     def __del__(self):
+        # At interpreter shutdown the HIP runtime (and torch's hold on it) may
+        # already be torn down; process exit releases the device memory anyway,
+        # so the context is left to it rather than closed into a dead runtime.
+        if sys.is_finalizing():
+            return
         try:
             self.close()
         except Exception:
@@ -378,6 +385,11 @@ class Lane:
         n = _I32()
         self._call("xl_profile_timeline", out, out.size, C.byref(n))
         return out[: n.value].reshape(-1, 32)
+
+    def debug_set_launch_count(self, launches: int) -> None:
+        """Sets the single-launch kernels' launch counters (epoch / parity) as if
+        `launches` launches had run: for testing their wrap at 2^32."""
+        self._call("xl_debug_set_launch_count", C.c_uint32(launches & 0xFFFFFFFF))
 
     def quantize_q8k_async(self, x, rows: int, k: int, q8k_out, stream=None) -> None:
         self._call("xl_quantize_q8k_async", _ptr(x), rows, k, _ptr(q8k_out), None if stream is None else int(stream))

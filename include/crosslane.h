@@ -6,6 +6,16 @@
  * when `err` is non-null, fills it; the context also keeps the last error.
  * A context is driven by one caller thread at a time (the reference drives its
  * HIP lane from one dedicated worker thread, engine/strata/warm/worker.hpp:9-18).
+ * Its device work is ordered: every call that enqueues work waits (on the GPU,
+ * hipStreamWaitEvent) for the context's previous call when that one named
+ * another stream, so calls on one context never overlap, whatever streams they
+ * name (they share the context's workspace, exchange buffers and counters).
+ * The single-launch layer kernels spin on data other workgroups of the same
+ * launch produce: they need all their workgroups resident at once (one per CU)
+ * and make progress only while no other kernel holds the CUs they wait for.
+ * Two contexts, or another persistent kernel, launched concurrently on other
+ * streams can starve them; such a wait ends in the device error flag
+ * (XL_E_DEVICE, "layer wait timeout") after about a second, not in a hang.
  * No call allocates device memory after xl_bank_create (the workspace is sized
  * at xl_open, like the reference's arena reservation,
  * engine/strata/sycl/stage/wiring/hip_resident_bank.hpp:63-94).
@@ -274,6 +284,13 @@ int32_t xl_profile_end(xl_context* ctx, float* stage_ms, int32_t max_stages, int
  * (a count, not a stamp), 24 + 2j step j's h complete, 25 + 2j step j's
  * Q8_K(h) staged. A diagnostic aid: it has no counterpart in the reference. */
 int32_t xl_profile_timeline(xl_context* ctx, uint64_t* out, int32_t max_words, int32_t* n_words, xl_error* err);
+
+/* Sets the single-launch kernels' device launch counters (the all-types
+ * kernel's epoch and the streaming kernel's launch count, whose parity picks
+ * its h exchange buffer) to `launches`, as if that many launches had run. A
+ * diagnostic aid for testing the counters' wrap at 2^32; it has no
+ * counterpart in the reference. */
+int32_t xl_debug_set_launch_count(xl_context* ctx, uint32_t launches, xl_error* err);
 
 /* ---- host utilities (no device needed) ------------------------------------ */
 uint64_t xl_planar_bytes(int32_t type, int32_t n, int32_t k);

@@ -582,6 +582,8 @@ int32_t xl_open(uint32_t abi_version, const xl_config* cfg, xl_context** out, xl
         hip_check(hipMemset(ctx->hbuf, 0xff, size_t(2) * xl::kHBufWords * 4), "h exchange fill");
         const std::vector<uint64_t> tab = layer_tables();
         hip_check(hipMemcpy(ctx->tables, tab.data(), tab.size() * 8, hipMemcpyHostToDevice), "table upload");
+        void* scratch = nullptr;   // the no-allocation scratch's address on this device, looked up once
+        hip_check(xl::dev::noalloc_scratch(cfg->device, &scratch), "no-allocation scratch address");
         ctx->path = env_int("XL_LAYER_PATH", 1);
         need(ctx->path >= 0 && ctx->path <= 4, XL_E_ARG, "XL_LAYER_PATH must be 0, 1, 2, 3 or 4");
         ctx->gpath = env_int("XL_GROUPED_PATH", 1);
@@ -1264,42 +1266,82 @@ uint64_t xl_shared_work_bytes(int32_t dim, int32_t ff, int32_t T) {
     return shared_work(dim, ff, T).bytes;
 }
 
+namespace {
+
+void check_shared(const xl_context* ctx, int32_t type_gate, const void* d_gate, int32_t type_up, const void* d_up,
+                  int32_t type_down, const void* d_down, int32_t ff, int32_t T, const float* d_x, const float* d_out) {
+    need(d_gate && d_up && d_down && d_x && d_out, XL_E_ARG, "null device pointer");
+    need(ff >= 256 && ff % 256 == 0 && ff <= (1 << 16), XL_E_ARG, "shared ff a multiple of 256 up to 65536");
+    need(T >= 1 && T <= 8192, XL_E_ARG, "T outside 1..8192");
+    for (const int32_t t : {type_gate, type_up, type_down})
+        need(xl::supported_type(t) || xl::dense_type(t), XL_E_ARG, "unsupported shared-expert block type");
+    (void)ctx;
+}
+
+// hip_backend.cpp:664-666: mv(gate, up), swiglu, mv(down), T tokens per launch,
+// the intermediates carved from `base` (256-byte aligned, w.bytes long).
+void enqueue_shared(xl_context* ctx, int32_t type_gate, const void* d_gate, int32_t type_up, const void* d_up,
+                    int32_t type_down, const void* d_down, int32_t ff, int32_t T, const float* d_x, float* d_out,
+                    uint8_t* base, const SharedWork& w, hipStream_t s) {
+    const int dim = ctx->cfg.dim;
+    float* g = reinterpret_cast<float*>(base + w.g);
+    float* u = reinterpret_cast<float*>(base + w.u);
+    int8_t* xq = reinterpret_cast<int8_t*>(base + w.xq);
+    int8_t* hq = reinterpret_cast<int8_t*>(base + w.hq);
+    float* xd = reinterpret_cast<float*>(base + w.xd);
+    float* hd = reinterpret_cast<float*>(base + w.hd);
+    const xl::MatRef mg = per32_matrix(type_gate, d_gate, ff, dim), mu = per32_matrix(type_up, d_up, ff, dim);
+    const xl::MatRef md = per32_matrix(type_down, d_down, dim, ff);
+    hip_check(xl::dev::launch_quant32(d_x, T, dim, xq, xd, ctx->err_flag, s), "quant32(x) launch");
+    hip_check(xl::dev::launch_mv32(nullptr, nullptr, mg, mu, T, 0, 0, 2, ff, dim, xq, size_t(dim), xd,
+                                   size_t(dim / 32), g, u, size_t(ff), ctx->tables, ctx->err_flag, s),
+              "shared gate/up launch");
+    hip_check(xl::dev::launch_swiglu_quant32(g, u, T, ff, ctx->cfg.swiglu_limit, hq, hd, s),
+              "shared SwiGLU + quant32(h) launch");
+    hip_check(xl::dev::launch_mv32(nullptr, nullptr, md, md, T, 0, 0, 1, dim, ff, hq, size_t(ff), hd,
+                                   size_t(ff / 32), d_out, nullptr, size_t(dim), ctx->tables, ctx->err_flag, s),
+              "shared down launch");
+}
+
+}  // namespace
+
 int32_t xl_shared_forward_async(xl_context* ctx, int32_t type_gate, const void* d_gate, int32_t type_up,
                                 const void* d_up, int32_t type_down, const void* d_down, int32_t ff, int32_t T,
                                 const float* d_x, float* d_out, void* d_work, uint64_t work_bytes, void* stream,
                                 xl_error* err) {
     return guarded(ctx, err, [&] {
         ready(ctx, false);
-        const int dim = ctx->cfg.dim;
-        need(d_gate && d_up && d_down && d_x && d_out && d_work, XL_E_ARG, "null device pointer");
-        need(ff >= 256 && ff % 256 == 0 && ff <= (1 << 16), XL_E_ARG, "shared ff a multiple of 256 up to 65536");
-        need(T >= 1 && T <= 8192, XL_E_ARG, "T outside 1..8192");
-        for (const int32_t t : {type_gate, type_up, type_down})
-            need(xl::supported_type(t) || xl::dense_type(t), XL_E_ARG, "unsupported shared-expert block type");
-        const SharedWork w = shared_work(dim, ff, T);
+        check_shared(ctx, type_gate, d_gate, type_up, d_up, type_down, d_down, ff, T, d_x, d_out);
+        need(d_work != nullptr, XL_E_ARG, "null workspace");
+        const SharedWork w = shared_work(ctx->cfg.dim, ff, T);
         need(work_bytes >= w.bytes, XL_E_ARG, "workspace smaller than xl_shared_work_bytes(dim, ff)");
         need(reinterpret_cast<uintptr_t>(d_work) % 256 == 0, XL_E_ARG, "workspace not 256-byte aligned");
-        uint8_t* base = static_cast<uint8_t*>(d_work);
-        float* g = reinterpret_cast<float*>(base + w.g);
-        float* u = reinterpret_cast<float*>(base + w.u);
-        int8_t* xq = reinterpret_cast<int8_t*>(base + w.xq);
-        int8_t* hq = reinterpret_cast<int8_t*>(base + w.hq);
-        float* xd = reinterpret_cast<float*>(base + w.xd);
-        float* hd = reinterpret_cast<float*>(base + w.hd);
-        const xl::MatRef mg = per32_matrix(type_gate, d_gate, ff, dim), mu = per32_matrix(type_up, d_up, ff, dim);
-        const xl::MatRef md = per32_matrix(type_down, d_down, dim, ff);
         hipStream_t s = pick_stream(ctx, stream);
         Ordered ord(ctx, s);
-        // hip_backend.cpp:664-666: mv(gate, up), swiglu, mv(down), T tokens per launch
-        hip_check(xl::dev::launch_quant32(d_x, T, dim, xq, xd, ctx->err_flag, s), "quant32(x) launch");
-        hip_check(xl::dev::launch_mv32(nullptr, nullptr, mg, mu, T, 0, 0, 2, ff, dim, xq, size_t(dim), xd,
-                                       size_t(dim / 32), g, u, size_t(ff), ctx->tables, ctx->err_flag, s),
-                  "shared gate/up launch");
-        hip_check(xl::dev::launch_swiglu_quant32(g, u, T, ff, ctx->cfg.swiglu_limit, hq, hd, s),
-                  "shared SwiGLU + quant32(h) launch");
-        hip_check(xl::dev::launch_mv32(nullptr, nullptr, md, md, T, 0, 0, 1, dim, ff, hq, size_t(ff), hd,
-                                       size_t(ff / 32), d_out, nullptr, size_t(dim), ctx->tables, ctx->err_flag, s),
-                  "shared down launch");
+        enqueue_shared(ctx, type_gate, d_gate, type_up, d_up, type_down, d_down, ff, T, d_x, d_out,
+                       static_cast<uint8_t*>(d_work), w, s);
+    });
+}
+
+int32_t xl_shared_forward_noalloc(xl_context* ctx, int32_t type_gate, const void* d_gate, int32_t type_up,
+                                  const void* d_up, int32_t type_down, const void* d_down, int32_t ff, int32_t T,
+                                  const float* d_x, float* d_out, void* stream, xl_error* err) {
+    return guarded(ctx, err, [&] {
+        ready(ctx, false);
+        check_shared(ctx, type_gate, d_gate, type_up, d_up, type_down, d_down, ff, T, d_x, d_out);
+        const SharedWork w = shared_work(ctx->cfg.dim, ff, T);
+        if (w.bytes > xl::kNoAllocScratchBytes)
+            fail(XL_E_ARG, "xl_shared_forward_noalloc: %llu bytes of intermediates for T = %d exceed the %llu-byte "
+                           "static scratch (xl_shared_work_bytes gives the need; use xl_shared_forward_async)",
+                 (unsigned long long)w.bytes, T, (unsigned long long)xl::kNoAllocScratchBytes);
+        void* scratch = nullptr;   // this device's copy (found once, at xl_open)
+        hip_check(xl::dev::noalloc_scratch(ctx->cfg.device, &scratch), "no-allocation scratch address");
+        hipStream_t s = pick_stream(ctx, stream);
+        Ordered ord(ctx, s);
+        // Every intermediate is written before it is read (quant32 fills xq/xd, the
+        // gate/up rows fill g/u, the SwiGLU fills hq/hd): nothing to clear.
+        enqueue_shared(ctx, type_gate, d_gate, type_up, d_up, type_down, d_down, ff, T, d_x, d_out,
+                       static_cast<uint8_t*>(scratch), w, s);
     });
 }
 

@@ -122,7 +122,13 @@ constexpr int kRouteMaxExperts = 4096;   // router: scores and keys of one token
 inline int64_t group_max_tasks(int64_t P, int64_t n_experts) { return P / 16 + (P < n_experts ? P : n_experts) + 1; }
 constexpr int kLayer3TableBytes = 24576;   // expanded codebooks of the single-launch kernel
 
+// Size of the no-allocation entry point's static device scratch (xl_noalloc.hip).
+constexpr uint64_t kNoAllocScratchBytes = uint64_t(8) << 20;
+
 namespace dev {
+// Device address of this GPU's copy of the no-allocation scratch (looked up
+// once per device by hipGetSymbolAddress, with `device` current; then cached).
+hipError_t noalloc_scratch(int device, void** out);
 // Single-launch layer: hipErrorNotSupported when (dim, ff, k) has no instance.
 // gu_types / dn_types: block types among the layer's gate/up / down matrices
 // (bits 1 IQ2_XXS, 2 IQ2_XS, 4 IQ1_M) select the kernel instance.

@@ -98,6 +98,7 @@ _SIGNATURES = {
     "xl_shared_work_bytes": (C.c_uint64, [_I32, _I32, _I32]),
     "xl_shared_forward_async": (_I32, [_P, _I32, _P, _I32, _P, _I32, _P, _I32, _I32, _P, _P, _P, C.c_uint64, _P,
                                        _ErrP]),
+    "xl_shared_forward_noalloc": (_I32, [_P, _I32, _P, _I32, _P, _I32, _P, _I32, _I32, _P, _P, _P, _ErrP]),
     "xl_hc_post_async": (_I32, [_P, _P, _P, _P, _P, _I32, _I32, _I32, _P, _P, _ErrP]),
     "xl_profile_begin": (_I32, [_P, _I32, _ErrP]),
     "xl_profile_end": (_I32, [_P, _f32p, _I32, C.POINTER(_I32), C.POINTER(_I32), C.c_char_p, _I32, _ErrP]),
@@ -412,6 +413,13 @@ class Lane:
         self._call("xl_shared_forward_async", int(types[0]), _ptr(gate), int(types[1]), _ptr(up), int(types[2]),
                    _ptr(down), ff, T, _ptr(x), _ptr(out), _ptr(work), int(work.numel() * work.element_size()),
                    None if stream is None else int(stream))
+
+    def shared_forward_noalloc(self, types, gate, up, down, ff: int, x, out, stream=None) -> None:
+        """The shared-expert FFN with its intermediates in the library's static
+        device scratch (no workspace, no allocation): x, out [T, dim]."""
+        T = int(x.numel()) // self.dim
+        self._call("xl_shared_forward_noalloc", int(types[0]), _ptr(gate), int(types[1]), _ptr(up), int(types[2]),
+                   _ptr(down), ff, T, _ptr(x), _ptr(out), None if stream is None else int(stream))
 
     def hc_post_async(self, y, res, post, comb, out, stream=None) -> None:
         """y [T, D], res / out [T, H, D], post [T, 8], comb [T, 64] device tensors."""

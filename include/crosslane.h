@@ -254,6 +254,18 @@ int32_t xl_shared_forward_async(xl_context* ctx, int32_t type_gate, const void* 
                                 const void* d_up, int32_t type_down, const void* d_down, int32_t ff, int32_t T,
                                 const float* d_x, float* d_out, void* d_work, uint64_t work_bytes, void* stream,
                                 xl_error* err);
+/* The shared-expert FFN without a caller workspace: the same kernels and
+ * result as xl_shared_forward_async, its intermediates in a static device
+ * array of 8 MiB (the library's own, held by every GPU it runs on until the
+ * process ends). No counterpart in the reference: it is for callers that
+ * cannot allocate device memory (code under HIP graph capture, tight serving
+ * loops, harnesses that forbid hipMalloc). It calls no hipMalloc / hipFree.
+ * XL_E_ARG when xl_shared_work_bytes(dim, ff, T) exceeds 8 MiB (T up to 250 at
+ * dim 4096 x ff 3072). Every call on one GPU shares that GPU's array: calls
+ * that overlap on a GPU (through any context or stream) race. */
+int32_t xl_shared_forward_noalloc(xl_context* ctx, int32_t type_gate, const void* d_gate, int32_t type_up,
+                                  const void* d_up, int32_t type_down, const void* d_down, int32_t ff, int32_t T,
+                                  const float* d_x, float* d_out, void* stream, xl_error* err);
 /* Hyper-connection post after the MoE block (hip_backend.cpp:777 k4::hc_post;
  * sycl/hc/hc.cpp:107-115, core.hpp:81-86): for T tokens and H <= 4 streams of
  * D, out[t][k][e] = post[t][k] * y[t][e] + sum_j comb[t][j * H + k] *

@@ -317,11 +317,22 @@ void check_layer(const xl_context* ctx, int32_t layer) {
 
 // Enqueues the routed-expert layer on stream s: Q8_K(x), gate/up + SwiGLU,
 // Q8_K(h), down, fixed-order combine. All pointers are device pointers.
+// Parity trace outputs of one single-launch layer call (Layer3Args::tq8x ...),
+// and which kernel ran (1 streaming, 3 all-types).
+struct LayerTrace {
+    uint8_t* q8x = nullptr;
+    uint8_t* q8h = nullptr;
+    float* h = nullptr;
+    int32_t* ints = nullptr;
+    int kernel = 0;
+};
+
 // Returns true when the layer ran as one launch carrying `stop` (recorded as it
 // completes); false when it took separate launches, which leave `stop` alone.
+// With `tr`, the layer must run as one launch (XL_E_ARG otherwise).
 bool enqueue_layer(xl_context* ctx, int32_t layer, const int32_t* d_ids, const float* d_w, int32_t k, const float* d_x,
                    const float* d_shared, float* d_out, hipStream_t s, float* g_dbg = nullptr,
-                   float* u_dbg = nullptr, hipEvent_t stop = nullptr) {
+                   float* u_dbg = nullptr, hipEvent_t stop = nullptr, LayerTrace* tr = nullptr) {
     const int dim = ctx->cfg.dim, ff = ctx->cfg.ff, E = ctx->cfg.n_experts;
     const xl::ExpertDesc* descs = ctx->d_descs + size_t(layer) * E;
     const int gu_mask = ctx->gu_mask[size_t(layer)], dn_mask = ctx->dn_mask[size_t(layer)];
@@ -339,6 +350,7 @@ bool enqueue_layer(xl_context* ctx, int32_t layer, const int32_t* d_ids, const f
             a.trace = ctx->timeline;
             hip_check(hipMemsetAsync(ctx->timeline, 0, size_t(ctx->cus) * 16 * 32 * 8, s), "timeline clear");
         }
+        if (tr) { a.tq8x = tr->q8x; a.tq8h = tr->q8h; a.th = tr->h; a.tint = tr->ints; }
         const LayerShape& ls = ctx->layer_shape[size_t(layer)];
         if (ls.regular) {
             a.slab = ctx->slabs[size_t(layer)];
@@ -353,7 +365,11 @@ bool enqueue_layer(xl_context* ctx, int32_t layer, const int32_t* d_ids, const f
                 (void)hipGetLastError();
             }
             need(ctx->path != 4 || e == hipSuccess, XL_E_ARG, "XL_LAYER_PATH=4: no streaming-kernel instance for this layer");
-            if (e == hipErrorNotSupported) e = xl::dev::launch_layer3(a, gu_mask, dn_mask, ctx->cus, s, stop);
+            if (tr && e == hipSuccess) tr->kernel = 1;
+            if (e == hipErrorNotSupported) {
+                e = xl::dev::launch_layer3(a, gu_mask, dn_mask, ctx->cus, s, stop);
+                if (tr && e == hipSuccess) tr->kernel = 3;
+            }
             if (e == hipSuccess) {
                 if (a.trace) ctx->timeline_words = uint64_t(ctx->cus) * 16 * 32;
                 mark("layer");
@@ -363,6 +379,7 @@ bool enqueue_layer(xl_context* ctx, int32_t layer, const int32_t* d_ids, const f
             (void)hipGetLastError();   // no instance for this shape: separate launches below
         }
     }
+    need(tr == nullptr, XL_E_ARG, "trace: this layer does not run as a single launch (shape, path or output)");
     if (ctx->path == 2 && !g_dbg && !u_dbg) {
         xl::LayerArgs a{};
         a.descs = descs; a.ids = d_ids; a.w = d_w; a.x = d_x; a.shared = d_shared; a.out = d_out;
@@ -980,7 +997,7 @@ namespace {
 // the layer's gate/up are IQ2_XXS and its down IQ2_XS, otherwise one layer
 // call per token. All pointers are device pointers.
 void enqueue_grouped(xl_context* ctx, int32_t layer, int32_t T, int32_t k, const int32_t* d_ids, const float* d_w,
-                     const float* d_x, const float* d_shared, float* d_out, hipStream_t s) {
+                     const float* d_x, const float* d_shared, float* d_out, hipStream_t s, LayerTrace* tr = nullptr) {
     const int dim = ctx->cfg.dim, E = ctx->cfg.n_experts;
     const int gu_mask = ctx->gu_mask[size_t(layer)], dn_mask = ctx->dn_mask[size_t(layer)];
     Marks mark(ctx, s);
@@ -995,8 +1012,12 @@ void enqueue_grouped(xl_context* ctx, int32_t layer, int32_t T, int32_t k, const
         a.h = g.h; a.hq = g.hq; a.hd = g.hd; a.y = g.y;
         a.tables = ctx->tables; a.err = ctx->err_flag;
         a.lim = ctx->cfg.swiglu_limit;
+        if (tr) { a.tq8x = tr->q8x; a.tq8h = tr->q8h; a.tint = tr->ints; }
         const hipError_t e = xl::dev::launch_grouped(a, ctx->cus, s);
         if (e == hipSuccess) {
+            if (tr && tr->h)   // the pairs' h as the gate/up kernel wrote it for Q8_K(h)
+                hip_check(hipMemcpyAsync(tr->h, g.h, sizeof(float) * size_t(T) * k * ctx->cfg.ff,
+                                         hipMemcpyDeviceToDevice, s), "trace h copy");
             mark("grouped");
             return;
         }
@@ -1004,6 +1025,7 @@ void enqueue_grouped(xl_context* ctx, int32_t layer, int32_t T, int32_t k, const
         (void)hipGetLastError();
     }
     need(ctx->gpath != 2, XL_E_ARG, "XL_GROUPED_PATH=2: the grouped MFMA kernels cannot run this layer");
+    need(tr == nullptr, XL_E_ARG, "trace: this layer does not run on the grouped MFMA kernels");
     for (int t = 0; t < T; ++t)
         enqueue_layer(ctx, layer, d_ids + size_t(t) * k, d_w + size_t(t) * k, k, d_x + size_t(t) * dim,
                       d_shared ? d_shared + size_t(t) * dim : nullptr, d_out + size_t(t) * dim, s);
@@ -1177,6 +1199,48 @@ int32_t xl_layer_forward_async(xl_context* ctx, int32_t layer, const int32_t* d_
         Ordered ord(ctx, s);
         ord.carried_by_launch(enqueue_layer(ctx, layer, d_ids, d_w, k, d_x, d_shared_or_null, d_out, s, nullptr, nullptr,
                                             ord.stop()));
+    });
+}
+
+int32_t xl_layer_trace_async(xl_context* ctx, int32_t layer, const int32_t* d_ids, const float* d_w, int32_t k,
+                             const float* d_x, const float* d_shared_or_null, float* d_out, void* d_q8x, void* d_q8h,
+                             float* d_h, int32_t* d_ints, int32_t* kernel_out, void* stream, xl_error* err) {
+    return guarded(ctx, err, [&] {
+        ready(ctx, true);
+        check_layer(ctx, layer);
+        need(k >= 1 && k <= ctx->cfg.max_picks, XL_E_ARG, "pick count outside 1..max_picks");
+        need(d_ids && d_w && d_x && d_out, XL_E_ARG, "null device pointer");
+        need(d_q8x || d_q8h || d_h || d_ints, XL_E_ARG, "trace: no output requested");
+        LayerTrace tr;
+        tr.q8x = static_cast<uint8_t*>(d_q8x);
+        tr.q8h = static_cast<uint8_t*>(d_q8h);
+        tr.h = d_h;
+        tr.ints = d_ints;
+        hipStream_t s = pick_stream(ctx, stream);
+        Ordered ord(ctx, s);
+        ord.carried_by_launch(
+            enqueue_layer(ctx, layer, d_ids, d_w, k, d_x, d_shared_or_null, d_out, s, nullptr, nullptr, ord.stop(), &tr));
+        if (kernel_out) *kernel_out = tr.kernel;
+    });
+}
+
+int32_t xl_grouped_trace_async(xl_context* ctx, int32_t layer, int32_t T, int32_t k, const int32_t* d_ids,
+                               const float* d_w, const float* d_x, const float* d_shared_or_null, float* d_out,
+                               void* d_q8x, void* d_q8h, float* d_h, int32_t* d_ints, void* stream, xl_error* err) {
+    return guarded(ctx, err, [&] {
+        ready(ctx, true);
+        check_layer(ctx, layer);
+        check_grouped(ctx, T, k);
+        need(d_ids && d_w && d_x && d_out, XL_E_ARG, "null device pointer");
+        need(d_q8x || d_q8h || d_h || d_ints, XL_E_ARG, "trace: no output requested");
+        LayerTrace tr;
+        tr.q8x = static_cast<uint8_t*>(d_q8x);
+        tr.q8h = static_cast<uint8_t*>(d_q8h);
+        tr.h = d_h;
+        tr.ints = d_ints;
+        hipStream_t s = pick_stream(ctx, stream);
+        Ordered ord(ctx, s);
+        enqueue_grouped(ctx, layer, T, k, d_ids, d_w, d_x, d_shared_or_null, d_out, s, &tr);
     });
 }
 

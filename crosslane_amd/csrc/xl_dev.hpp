@@ -280,6 +280,24 @@ __device__ __forceinline__ void lds_barrier() {
     asm volatile("" ::: "memory");
 }
 
+// ---- parity trace ---------------------------------------------------------------------------
+// Sum over each aligned quad of lanes (DPP), in every lane of the quad: the four
+// pairs a quad holds form one 256-weight block, so this is a row's block integer.
+__device__ __forceinline__ int quad_isum(int v) {
+    v += __builtin_amdgcn_update_dpp(0, v, 0xB1, 0xF, 0xF, false);   // quad_perm [1,0,3,2]
+    v += __builtin_amdgcn_update_dpp(0, v, 0x4E, 0xF, 0xF, false);   // quad_perm [2,3,0,1]
+    return v;
+}
+// One wave writes a 292-byte Q8_K block (q8k_core.hpp:13: d, qs[256], bsums[16])
+// from its scale and lane l's four quants (values 4l .. 4l + 3).
+__device__ __forceinline__ void trace_q8_block(uint8_t* dst, float d, uint32_t packed, int lane) {
+    if (lane == 0) *reinterpret_cast<float*>(dst) = d;
+    *reinterpret_cast<uint32_t*>(dst + 4 + 4 * lane) = packed;
+    const int s = __builtin_amdgcn_sdot4(int(packed), 0x01010101, 0, false);   // the lane's four quants
+    const int b = quad_isum(s);                                                  // values 16 j .. 16 j + 15
+    if ((lane & 3) == 0) *reinterpret_cast<int16_t*>(dst + 260 + 2 * (lane >> 2)) = int16_t(b);
+}
+
 // ---- bounded waits -------------------------------------------------------------------------
 constexpr uint32_t kPollLimit = 1u << 21;   // polls (each a device-memory round trip): about a second
 

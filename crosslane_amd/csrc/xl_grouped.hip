@@ -180,11 +180,13 @@ __device__ __forceinline__ size_t slot_off(int slot, int nb, int blk, int piece,
     return size_t(slot >> 4) * size_t(nb) * 4096 + size_t(((4 * blk + piece) * 4 + chunk) * 256 + 16 * (slot & 15));
 }
 enum { ROWS_X = 0, ROWS_H = 1 };
-template <int MODE>
+// trace (null outside the parity trace): the row's blocks also as 292-byte Q8_K
+// blocks, row-major (a token's for ROWS_X, a pair's for ROWS_H).
+template <int MODE, bool TR>
 __global__ __launch_bounds__(256) void q8k_rows_kernel(const float* __restrict__ src, int rows, int nb,
                                                        int8_t* __restrict__ q, float* __restrict__ d,
                                                        const int32_t* __restrict__ pos, int k,
-                                                       int* __restrict__ err) {
+                                                       int* __restrict__ err, uint8_t* __restrict__ trace) {
     const int b = blockIdx.x * 4 + (threadIdx.x >> 6);
     if (b >= rows * nb) return;   // wave-uniform
     const int row = b / nb, blk = b - row * nb;
@@ -201,6 +203,9 @@ __global__ __launch_bounds__(256) void q8k_rows_kernel(const float* __restrict__
         if (slot >= 0) *reinterpret_cast<uint32_t*>(q + slot_off(slot, nb, blk, c >> 1, e) + j) = r.packed;
     }
     if (lane == 0) d[b] = r.d;
+    if constexpr (TR) {
+        if (trace) trace_q8_block(trace + size_t(b) * 292, r.d, r.packed, lane);
+    }
 }
 
 // Keeps a value alive without storing it (the L2 line touches).
@@ -311,7 +316,8 @@ __device__ __forceinline__ void stage_item(uint8_t* lds, const GroupArgs& a, con
 // gate/up + SwiGLU. Work item = (task, group of NW * 16 rows); wave wv owns
 // rows 16 wv .. + 15 of the group in gate and up.
 // ---------------------------------------------------------------------------
-template <int NW>
+// TR: also write each pair's block integers (GroupArgs::tint).
+template <int NW, bool TR>
 __global__ __launch_bounds__(NW * 64, 1) void gu_kernel(GroupArgs a) {
     __shared__ __attribute__((aligned(16))) uint8_t lds[kL_Bytes];
     const int t = threadIdx.x, lane = t & 63, wv = t >> 6;
@@ -394,6 +400,16 @@ __global__ __launch_bounds__(NW * 64, 1) void gu_kernel(GroupArgs a) {
             }
 #pragma unroll
             for (int c = 0; c < 8; ++c) use(L[c], XU, c, A[c], biu);
+            if constexpr (TR) {   // pair po[r]'s block integers of this lane's row
+                const size_t rec = 2 * size_t(a.ff) * nb + size_t(a.dim) * (a.ff / 256);
+#pragma unroll
+                for (int r = 0; r < 4; ++r)
+                    if (a.tint && po[r] >= 0) {
+                        const size_t o = size_t(po[r]) * rec + size_t(row) * nb + size_t(b);
+                        a.tint[o] = big[r];
+                        a.tint[o + size_t(a.ff) * nb] = biu[r];
+                    }
+            }
             const float dgf = h2f(sdg[b]), duf = h2f(sdu[b]);
             const float4 xd4 = *reinterpret_cast<const float4*>(lds + kL_PD + 64 * b + 16 * e4);
             const float xd[4] = {xd4.x, xd4.y, xd4.z, xd4.w};
@@ -455,7 +471,7 @@ __device__ __forceinline__ void xs_lane(const uint4& w, uint32_t (&u)[4]) {
 // per sub-block one MFMA over all 32 weights (C) and one with entries 2, 3 of B
 // zeroed (C1), then ls1 C1 + ls2 (C - C1) as ls2 C + (ls1 - ls2) C1, exactly.
 // ---------------------------------------------------------------------------
-template <int NW>
+template <int NW, bool TR>
 __global__ __launch_bounds__(NW * 64, 1) void dn_kernel(GroupArgs a) {
     __shared__ __attribute__((aligned(16))) uint8_t lds[kL_Bytes];
     const int t = threadIdx.x, lane = t & 63, wv = t >> 6;
@@ -528,6 +544,14 @@ __global__ __launch_bounds__(NW * 64, 1) void dn_kernel(GroupArgs a) {
 #pragma unroll
                 for (int r = 0; r < 4; ++r) bi[r] = mad24(ls2, C[r], mad24(ls1 - ls2, C1[r], bi[r]));
             }
+            if constexpr (TR) {
+                const int nbx = a.dim / 256;
+                const size_t rec = 2 * size_t(a.ff) * nbx + size_t(a.dim) * nb;
+#pragma unroll
+                for (int r = 0; r < 4; ++r)
+                    if (a.tint && po[r] >= 0)
+                        a.tint[size_t(po[r]) * rec + 2 * size_t(a.ff) * nbx + size_t(row) * nb + size_t(b)] = bi[r];
+            }
             const float ddf = h2f(reinterpret_cast<const uint16_t*>(lds + kL_RD)[rl * nb + b]);
             const float4 hd4 = *reinterpret_cast<const float4*>(lds + kL_PD + 64 * b + 16 * e4);
             const float hd[4] = {hd4.x, hd4.y, hd4.z, hd4.w};
@@ -599,12 +623,21 @@ hipError_t launch_grouped(const GroupArgs& args, int cus, hipStream_t s) {
     const int P = args.T * args.k;
     hipLaunchKernelGGL(bucket_kernel, dim3(1), dim3(1024), 0, s, args);
     const int nbx = args.dim / 256, nbh = args.ff / 256;
-    hipLaunchKernelGGL(q8k_rows_kernel<ROWS_X>, dim3((args.T * nbx + 3) / 4), dim3(256), 0, s, args.x, args.T, nbx,
-                       args.xq, args.xd, args.pos, args.k, args.err);
-    hipLaunchKernelGGL(gu_kernel<NW>, dim3(cus), dim3(NW * 64), 0, s, args);
-    hipLaunchKernelGGL(q8k_rows_kernel<ROWS_H>, dim3((P * nbh + 3) / 4), dim3(256), 0, s, args.h, P, nbh, args.hq,
-                       args.hd, args.pos, args.k, args.err);
-    hipLaunchKernelGGL(dn_kernel<NW>, dim3(cus), dim3(NW * 64), 0, s, args);
+    if (args.tq8x || args.tq8h || args.th || args.tint) {   // the parity trace (separate instances)
+        hipLaunchKernelGGL((q8k_rows_kernel<ROWS_X, true>), dim3((args.T * nbx + 3) / 4), dim3(256), 0, s, args.x,
+                           args.T, nbx, args.xq, args.xd, args.pos, args.k, args.err, args.tq8x);
+        hipLaunchKernelGGL((gu_kernel<NW, true>), dim3(cus), dim3(NW * 64), 0, s, args);
+        hipLaunchKernelGGL((q8k_rows_kernel<ROWS_H, true>), dim3((P * nbh + 3) / 4), dim3(256), 0, s, args.h, P, nbh,
+                           args.hq, args.hd, args.pos, args.k, args.err, args.tq8h);
+        hipLaunchKernelGGL((dn_kernel<NW, true>), dim3(cus), dim3(NW * 64), 0, s, args);
+    } else {
+        hipLaunchKernelGGL((q8k_rows_kernel<ROWS_X, false>), dim3((args.T * nbx + 3) / 4), dim3(256), 0, s, args.x,
+                           args.T, nbx, args.xq, args.xd, args.pos, args.k, args.err, nullptr);
+        hipLaunchKernelGGL((gu_kernel<NW, false>), dim3(cus), dim3(NW * 64), 0, s, args);
+        hipLaunchKernelGGL((q8k_rows_kernel<ROWS_H, false>), dim3((P * nbh + 3) / 4), dim3(256), 0, s, args.h, P, nbh,
+                           args.hq, args.hd, args.pos, args.k, args.err, nullptr);
+        hipLaunchKernelGGL((dn_kernel<NW, false>), dim3(cus), dim3(NW * 64), 0, s, args);
+    }
     hipLaunchKernelGGL(gcombine_kernel, dim3((args.dim + 255) / 256, args.T), dim3(256), 0, s, args);
     return hipGetLastError();
 }

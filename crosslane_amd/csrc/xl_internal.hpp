@@ -90,6 +90,15 @@ struct Layer3Args {
     int rtype[3];
     uint64_t* trace;            // null, or 32 timestamps (s_memrealtime) per wave of the grid
     float* hbuf;                // streaming kernel: 2 x kHBufWords h words, sentinel-filled (see xl_stream.hip)
+    // Parity trace (all null unless traced; xl_layer_trace_async): the launch's own
+    // Q8_K(x) and Q8_K(h) as 292-byte blocks (q8x: dim/256, q8h: k * ff/256, as
+    // staged in workgroup 0's LDS), its h (k * ff floats) and every row's integer
+    // per 256-weight block (tint: per pick, gate ff x dim/256, up ff x dim/256,
+    // down dim x ff/256; IQ1_M rows: 8 * main + delta).
+    uint8_t* tq8x;
+    uint8_t* tq8h;
+    float* th;
+    int32_t* tint;
 };
 constexpr int kHBufWords = 16 * 4096;      // k_max * ff_max
 
@@ -115,6 +124,14 @@ struct GroupArgs {
     const uint64_t* tables;     // expanded codebooks (kLayer3TableBytes)
     int* err;
     float lim;                  // SwiGLU limit (> 0: g = min(g, lim), u = clamp(u, -lim, lim))
+    // Parity trace (all null unless traced; xl_grouped_trace_async): Q8_K(x) per
+    // token (T x dim/256 blocks of 292 bytes), Q8_K(h) per pair (P x ff/256), h
+    // per pair (P x ff floats) and the block integers per pair (layout as
+    // Layer3Args::tint, one record per pair).
+    uint8_t* tq8x;
+    uint8_t* tq8h;
+    float* th;
+    int32_t* tint;
 };
 constexpr int kGroupMaxExperts = 8192;
 constexpr int kRouteMaxExperts = 4096;   // router: scores and keys of one token in LDS   // experts per layer the bucket kernel counts in LDS

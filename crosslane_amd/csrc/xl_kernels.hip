@@ -650,7 +650,7 @@ hipError_t launch_matvec(const MatRef& m, int n, int k, const int8_t* aq, const 
     if (!row_shape(k, lpr, ppl) || n <= 0 || !supported_type(m.type)) return hipErrorInvalidValue;
     const int rpw = 64 / lpr, slots = (n + rpw - 1) / rpw;
     const int grid = (slots + 3) / 4 < 1024 ? (slots + 3) / 4 : 1024;
-    const int need = need_of(type_bit(m.type)) | (partials && m.type == kIQ1_M ? kNeedPlain : 0);
+    const int need = need_of(type_bit(m.type));
     const size_t lds = size_t(lds_bytes_for(need));
 #define XL_MV(L, P)                                                                                                   \
     if (lpr == L && ppl == P) {                                                                                       \

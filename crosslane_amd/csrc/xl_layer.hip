@@ -208,9 +208,10 @@ __device__ __forceinline__ int pair_iq13(const uint8_t* lds, const Lut& L, const
 // One pair's contribution fma(fp16(d_w) * d_x, I, acc); the row is then summed
 // over its lanes and scaled by 1/8 (q8k_core.hpp:87-91 regrouped: the integers
 // per block are exact, the float order is this kernel's own).
+// Io (null outside the parity trace): receives the pair's integer.
 template <int T, int TM>
 __device__ __forceinline__ float pair_term(const uint8_t* lds, const Lut& L, const Raw3& r, int p, const uint32_t* a,
-                                           const int* gs, float dx, float acc) {
+                                           const int* gs, float dx, float acc, int* Io) {
     int I;
     uint32_t d16;
     if constexpr (T == kIQ2_XXS) {
@@ -224,31 +225,37 @@ __device__ __forceinline__ float pair_term(const uint8_t* lds, const Lut& L, con
         I = pair_iq13<TM>(lds, L, r.w, scw, a, gs);
         d16 = ((r.w[3] >> 12) & 0xfu) | ((r.w[3] >> 24) & 0xf0u) | ((r.w[4] >> 4) & 0xf00u) | ((r.w[4] >> 16) & 0xf000u);
     }
+    if (Io) *Io = I;
     return fmaf(__fmul_rn(h2f(d16), dx), float(I), acc);
 }
 template <int T, int TM>
 __device__ __forceinline__ bool has_type() {
     return (T == kIQ2_XXS && (TM & 1)) || (T == kIQ2_XS && (TM & 2)) || (T == kIQ1_M && (TM & 4));
 }
-// Lane partial of one row (TM: types possible for this row; LT: types held in LDS).
+// Lane partial of one row (TM: types possible for this row; LT: types held in
+// LDS). Io (null outside the parity trace): the lane's P pair integers.
 template <int TM, int LT, int P>
 __device__ __forceinline__ float row_sum(const uint8_t* lds, const Lut& L, int type, const Raw3* r, const Act3<P>& A, int l,
-                                         int LPR) {
+                                         int LPR, int* Io = nullptr) {
     float acc = 0.0f;
     if constexpr (TM == 1 || TM == 2 || TM == 4) {
         constexpr int T = TM == 1 ? kIQ2_XXS : TM == 2 ? kIQ2_XS : kIQ1_M;
 #pragma unroll
-        for (int j = 0; j < P; ++j) acc = pair_term<T, LT>(lds, L, r[j], l + LPR * j, A.a[j], A.gs[j], A.d[j], acc);
+        for (int j = 0; j < P; ++j)
+            acc = pair_term<T, LT>(lds, L, r[j], l + LPR * j, A.a[j], A.gs[j], A.d[j], acc, Io ? Io + j : nullptr);
     } else {
         if (has_type<kIQ2_XXS, TM>() && type == kIQ2_XXS) {
 #pragma unroll
-            for (int j = 0; j < P; ++j) acc = pair_term<kIQ2_XXS, LT>(lds, L, r[j], l + LPR * j, A.a[j], A.gs[j], A.d[j], acc);
+            for (int j = 0; j < P; ++j)
+                acc = pair_term<kIQ2_XXS, LT>(lds, L, r[j], l + LPR * j, A.a[j], A.gs[j], A.d[j], acc, Io ? Io + j : nullptr);
         } else if (has_type<kIQ2_XS, TM>() && type == kIQ2_XS) {
 #pragma unroll
-            for (int j = 0; j < P; ++j) acc = pair_term<kIQ2_XS, LT>(lds, L, r[j], l + LPR * j, A.a[j], A.gs[j], A.d[j], acc);
+            for (int j = 0; j < P; ++j)
+                acc = pair_term<kIQ2_XS, LT>(lds, L, r[j], l + LPR * j, A.a[j], A.gs[j], A.d[j], acc, Io ? Io + j : nullptr);
         } else if (has_type<kIQ1_M, TM>()) {
 #pragma unroll
-            for (int j = 0; j < P; ++j) acc = pair_term<kIQ1_M, LT>(lds, L, r[j], l + LPR * j, A.a[j], A.gs[j], A.d[j], acc);
+            for (int j = 0; j < P; ++j)
+                acc = pair_term<kIQ1_M, LT>(lds, L, r[j], l + LPR * j, A.a[j], A.gs[j], A.d[j], acc, Io ? Io + j : nullptr);
         }
     }
     return acc;
@@ -260,7 +267,9 @@ __device__ __forceinline__ float row_sum(const uint8_t* lds, const Lut& L, int t
 // GUT / DNT: block types among the gate/up / down matrices (bits 1 IQ2_XXS,
 // 2 IQ2_XS, 4 IQ1_M). MG / MD: most gate/up slots / down passes one wave
 // holds; WIN: gate/up slots in flight per wave; WIND: down passes in flight.
-template <int NW, int LG, int PG, int LD, int PD, int MG, int MD, int WIN, int WIND, int GUT, int DNT>
+// TR: also write the parity trace (Layer3Args::tq8x ...); the untraced instance
+// compiles none of it.
+template <int NW, int LG, int PG, int LD, int PD, int MG, int MD, int WIN, int WIND, int GUT, int DNT, bool TR>
 __global__ __launch_bounds__(NW * 64, 1) void layer3_kernel(Layer3Args a) {
     __shared__ __attribute__((aligned(16))) uint8_t lds[kLdsBytes];
     __shared__ uint32_t s_epoch;
@@ -396,6 +405,13 @@ __global__ __launch_bounds__(NW * 64, 1) void layer3_kernel(Layer3Args a) {
     if (t == 0) s_epoch = e_prev + 1u == 0u ? 1u : e_prev + 1u;
     lds_barrier();
     const uint32_t epoch = s_epoch;
+    if constexpr (TR) {   // workgroup 0's staged Q8_K(x), as the gate/up rows read it
+        if (blockIdx.x == 0 && a.tq8x)
+            for (int b = wv; b < nbx; b += NW)
+                trace_q8_block(a.tq8x + 292 * b, reinterpret_cast<const float*>(lds + LY::XD)[b],
+                               *reinterpret_cast<const uint32_t*>(lds + LY::XQ + qswz(256 * b + 4 * lane)), lane);
+    }
+    const size_t rec = 2 * size_t(ff) * nbx + size_t(dim) * nbh;   // trace integers per pick
     // Arrival: this workgroup has read the epoch word. Whoever arrives last
     // advances it, at the end of the kernel (the count is not awaited before).
     uint32_t arrived = 0;
@@ -446,11 +462,26 @@ __global__ __launch_bounds__(NW * 64, 1) void layer3_kernel(Layer3Args a) {
                 const int i = s / sppG, row = (s - i * sppG) * RG + rG;
                 float hv = 0.0f;
                 if (gid[j] >= 0) {
-                    const float g = gsum<LG>(row_sum<GUT, TM, PG>(lds, L, gm[j].type, rg[j % WIN], A, lG, LG));
-                    const float u = gsum<LG>(row_sum<GUT, TM, PG>(lds, L, gm[j].type, ru[j % WIN], A, lG, LG));
+                    int Ig[PG], Iu[PG];
+                    const float g = gsum<LG>(row_sum<GUT, TM, PG>(lds, L, gm[j].type, rg[j % WIN], A, lG, LG, TR ? Ig : nullptr));
+                    const float u = gsum<LG>(row_sum<GUT, TM, PG>(lds, L, gm[j].type, ru[j % WIN], A, lG, LG, TR ? Iu : nullptr));
                     hv = silu_mul3(__fmul_rn(0.125f, g), __fmul_rn(0.125f, u), a.lim);
+                    if constexpr (TR) {   // the row's block integers: a quad holds one block's four pairs
+#pragma unroll
+                        for (int q = 0; q < PG; ++q) {
+                            const int bg = quad_isum(Ig[q]), bu = quad_isum(Iu[q]);
+                            if (a.tint && (lG & 3) == 0) {
+                                const size_t o = size_t(i) * rec + size_t(row) * nbx + size_t((lG + LG * q) >> 2);
+                                a.tint[o] = bg;
+                                a.tint[o + size_t(ff) * nbx] = bu;
+                            }
+                        }
+                    }
                 }
                 if (lG == LG - 1) coh_st64(a.htag + size_t(i) * ff + row, tag_word(__float_as_uint(hv), epoch));
+                if constexpr (TR) {
+                    if (a.th && lG == LG - 1 && gid[j] >= 0) a.th[size_t(i) * ff + row] = hv;
+                }
                 mark(8 + j);
             }
         }
@@ -560,7 +591,18 @@ __global__ __launch_bounds__(NW * 64, 1) void layer3_kernel(Layer3Args a) {
                         group_sums<DNT>(B);
                         cur = i;
                     }
-                    y = __fmul_rn(0.125f, gsum<LD>(row_sum<DNT, TM, PD>(lds, L, dm[j].type, rd[j % (WIND + 1)], B, lD, LD)));
+                    int Id[PD];
+                    y = __fmul_rn(0.125f, gsum<LD>(row_sum<DNT, TM, PD>(lds, L, dm[j].type, rd[j % (WIND + 1)], B, lD, LD,
+                                                                        TR ? Id : nullptr)));
+                    if constexpr (TR) {
+#pragma unroll
+                        for (int q = 0; q < PD; ++q) {
+                            const int bi = quad_isum(Id[q]);
+                            if (a.tint && (lD & 3) == 0)
+                                a.tint[size_t(i) * rec + 2 * size_t(ff) * nbx + size_t(drow[j]) * nbh +
+                                       size_t((lD + LD * q) >> 2)] = bi;
+                        }
+                    }
                 }
                 if (lD == LD - 1) ys[(wv + NW * j) * RD + rD] = y;
                 if (j == 0) mark(5);
@@ -569,6 +611,16 @@ __global__ __launch_bounds__(NW * 64, 1) void layer3_kernel(Layer3Args a) {
     }
     mark(6);
     lds_barrier();
+    if constexpr (TR) {   // workgroup 0's staged Q8_K(h) of every pick it staged, as its down passes read it
+        if (blockIdx.x == 0 && a.tq8h)
+            for (int blk = wv; blk < k * nbh; blk += NW) {
+                const int i = blk / nbh, bb = blk - i * nbh;
+                if (s_hq_ready[i] != epoch) continue;   // a bad id: nothing staged
+                const uint8_t* hq = lds + LY::HQ + i * hq_stride;
+                trace_q8_block(a.tq8h + 292 * blk, reinterpret_cast<const float*>(hq + ff)[bb],
+                               *reinterpret_cast<const uint32_t*>(hq + qswz(256 * bb + 4 * lane)), lane);
+            }
+    }
 
     // ---- fixed-order combine of this workgroup's rows
     const int nrows = nq_wg * RD;
@@ -599,6 +651,7 @@ __global__ __launch_bounds__(NW * 64, 1) void layer3_kernel(Layer3Args a) {
 // ---- launcher ------------------------------------------------------------------------------
 template <int NW, int LG, int PG, int LD, int PD, int MG, int MD, int WIN, int WIND, int GUT, int DNT>
 static hipError_t launch3(const Layer3Args& args, int grid, hipStream_t s, hipEvent_t stop) {
+    const bool tr = args.tq8x || args.tq8h || args.th || args.tint;
     constexpr int RG = 64 / LG, RD = 64 / LD;
     const int W = grid * NW;
     const int SG = args.k * (args.ff / RG);
@@ -610,8 +663,12 @@ static hipError_t launch3(const Layer3Args& args, int grid, hipStream_t s, hipEv
         args.ff > 4096 || Lay<GUT | DNT>::HQ + args.k * (args.ff + 64) > kLdsBytes ||
         Lay<GUT | DNT>::HQ + 16384 > kLdsBytes)   // the codebooks' single copies are staged there
         return hipErrorNotSupported;
-    hipExtLaunchKernelGGL((layer3_kernel<NW, LG, PG, LD, PD, MG, MD, WIN, WIND, GUT, DNT>), dim3(grid), dim3(NW * 64), 0,
-                          s, nullptr, stop, 0, args);
+    if (tr)
+        hipExtLaunchKernelGGL((layer3_kernel<NW, LG, PG, LD, PD, MG, MD, WIN, WIND, GUT, DNT, true>), dim3(grid),
+                              dim3(NW * 64), 0, s, nullptr, stop, 0, args);
+    else
+        hipExtLaunchKernelGGL((layer3_kernel<NW, LG, PG, LD, PD, MG, MD, WIN, WIND, GUT, DNT, false>), dim3(grid),
+                              dim3(NW * 64), 0, s, nullptr, stop, 0, args);
     return hipGetLastError();
 }
 

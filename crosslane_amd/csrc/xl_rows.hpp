@@ -31,21 +31,19 @@ constexpr int kLdsXXS = 0;          // IQ2_XXS grid: 256 rows x 8 B
 constexpr int kLdsXS = 2048;        // IQ2_XS grid: 512 rows x 8 B
 constexpr int kLdsSign = 6144;      // 256 rows x 16 B: {M.lo, M.hi, M1.lo, M1.hi} of ksigns[b & 127]
 constexpr int kLdsIQ1 = 10240;      // 4096 rows x 8 B: row (nib << 8 | idx_lo) = 8*grid[idx] + (nib & 8 ? -1 : 1)
-constexpr int kLdsIQ1Plain = 43008; // 2048 rows x 8 B plain IQ1 grid (partials probe only)
 constexpr int kLdsEnd2 = kLdsIQ1;   // bytes needed by IQ2 types only
-constexpr int kLdsEnd1 = kLdsIQ1Plain;
-constexpr int kLdsEndAll = kLdsIQ1Plain + 16384;
+constexpr int kLdsEnd1 = kLdsIQ1 + 4096 * 8;
 
 // Compact code buffer in device memory: 2-bit symbols, 8 per u16.
 constexpr int kCodesXXS = 0, kCodesXS = 256, kCodesIQ1 = 768, kCodesTotal = 768 + 2048;
 
-enum : int { kNeedXXS = 1, kNeedXS = 2, kNeedIQ1 = 4, kNeedPlain = 8 };
+enum : int { kNeedXXS = 1, kNeedXS = 2, kNeedIQ1 = 4 };
 
 __device__ __forceinline__ int need_mask(int type) {
     return type == kIQ2_XXS ? kNeedXXS : type == kIQ2_XS ? kNeedXS : type == kIQ1_M ? kNeedIQ1 : 0;
 }
 inline int lds_bytes_for(int need) {
-    return (need & kNeedPlain) ? kLdsEndAll : (need & kNeedIQ1) ? kLdsEnd1 : kLdsEnd2;
+    return (need & kNeedIQ1) ? kLdsEnd1 : kLdsEnd2;
 }
 
 __device__ __forceinline__ uint64_t expand_mag(uint32_t code) {
@@ -102,7 +100,6 @@ __device__ __forceinline__ void codes_fill(uint8_t* lds, const CodeRegs& c, int 
             // 11-bit grid index idx = r << 8 | t; rows (nib << 8 | t) for nib = r (delta +1) and r | 8 (delta -1)
             G[kLdsIQ1 / 8 + (r << 8) + t] = expand_iq1(c.iq1[r], 8, 1);
             G[kLdsIQ1 / 8 + ((r | 8) << 8) + t] = expand_iq1(c.iq1[r], 8, -1);
-            if (need & kNeedPlain) G[kLdsIQ1Plain / 8 + 256 * r + t] = expand_iq1(c.iq1[r], 1, 0);
         }
     }
 }
@@ -295,30 +292,6 @@ __device__ __forceinline__ int pair_iq1(const uint8_t* lds, uint32_t q0, uint32_
     }
     return total;
 }
-// IQ1_M (main, delta) separately from the plain grid (partials probe only).
-__device__ __forceinline__ int2 pair_iq1_split(const uint8_t* lds, uint32_t q0, uint32_t q1, uint32_t h, uint32_t scw,
-                                               const uint32_t* a) {
-    int2 out = make_int2(0, 0);
-#pragma unroll
-    for (int s = 0; s < 2; ++s) {
-        const uint32_t qw = s ? q1 : q0;
-        int mlo = 0, mhi = 0, dlo = 0, dhi = 0;
-#pragma unroll
-        for (int g = 0; g < 4; ++g) {
-            const uint32_t nib = (h >> (16 * s + 4 * g)) & 15u;
-            const uint2 gr = lds8(lds, kLdsIQ1Plain + ((((qw >> (8 * g)) & 255u) | ((nib & 7u) << 8)) << 3));
-            const uint32_t a0 = a[8 * s + 2 * g], a1 = a[8 * s + 2 * g + 1];
-            const int m = dot4(gr.y, a1, dot4(gr.x, a0, 0));
-            const int sum = dot4(0x01010101u, a1, dot4(0x01010101u, a0, 0));
-            const int d = (nib & 8u) ? -sum : sum;
-            if (g < 2) { mlo += m; dlo += d; } else { mhi += m; dhi += d; }
-        }
-        const int slo = int(2u * ((scw >> (6 * s)) & 7u) + 1u), shi = int(2u * ((scw >> (6 * s + 3)) & 7u) + 1u);
-        out.x += slo * mlo + shi * mhi;
-        out.y += slo * dlo + shi * dhi;
-    }
-    return out;
-}
 __device__ __forceinline__ uint32_t iq1_scale_word(uint32_t sw0, uint32_t sw1, int pp) {
     return ((pp & 2) ? sw1 : sw0) >> (16 * (pp & 1));
 }
@@ -327,7 +300,7 @@ __device__ __forceinline__ uint32_t iq1_d(uint32_t sw0, uint32_t sw1) {
 }
 
 // Row value, replicated over the row group. With PART, lane 4q of the group
-// also writes its block's exact integer(s): IQ2 one int, IQ1_M (main, delta).
+// also writes its block's exact integer (IQ1_M: 8 * main + delta).
 template <int T, int LPR, int PPL, bool PART>
 __device__ __forceinline__ float dot_raw_t(const Raw<PPL>& r, int row, int nb, int l, const Act<PPL>& A,
                                            const uint8_t* lds, int32_t* __restrict__ partials, bool valid) {
@@ -348,16 +321,10 @@ __device__ __forceinline__ float dot_raw_t(const Raw<PPL>& r, int row, int nb, i
             I = pair_iq1(lds, v[0], v[1], v[2], iq1_scale_word(v[3], v[4], p & 3), A.a[j]);
             d16 = iq1_d(v[3], v[4]);
         }
-        if constexpr (PART) {
+        if constexpr (PART) {   // the block's integer as the value path forms it (IQ1_M: 8 * main + delta)
             const uint64_t blk = uint64_t(row) * uint64_t(nb) + uint64_t(p >> 2);
-            if constexpr (T == kIQ1_M) {
-                const int2 md = pair_iq1_split(lds, v[0], v[1], v[2], iq1_scale_word(v[3], v[4], p & 3), A.a[j]);
-                const int im = quad_sum(md.x), id = quad_sum(md.y);
-                if (valid && (l & 3) == 0) { partials[2 * blk] = im; partials[2 * blk + 1] = id; }
-            } else {
-                const int ib = quad_sum(I);
-                if (valid && (l & 3) == 0) partials[blk] = ib;
-            }
+            const int ib = quad_sum(I);
+            if (valid && (l & 3) == 0) partials[blk] = ib;
         }
         const float db = __fmul_rn(f16_to_f32(d16), A.d[j]);
         acc = fmaf(db, float(I), acc);

@@ -292,7 +292,9 @@ __device__ __forceinline__ bool q8k_blocks(const uint4 (&hv)[NB], int nvalid, in
 // slots / down passes per wave; WIN: gate/up slots in flight per wave; WIND:
 // down passes in flight; MQ: most Q8_K(h) blocks one wave quantizes per step.
 constexpr int kBatch = 3;   // gate/up slots per SiLU batch
-template <int NW, int LG, int PG, int LD, int PD, int MG, int MD, int WIN, int WIND, int MQ>
+// TR: also write the parity trace (Layer3Args::tq8x ...); the untraced instance
+// compiles none of it.
+template <int NW, int LG, int PG, int LD, int PD, int MG, int MD, int WIN, int WIND, int MQ, bool TR>
 __global__ __launch_bounds__(NW * 64, 1) void stream_kernel(Layer3Args a) {
     static_assert(WIN <= MG && WIND <= MD && WIND <= MG && MG <= 32 && MD <= 32, "prefetch depths, metadata lanes");
     __shared__ __attribute__((aligned(16))) Smem sm;
@@ -446,6 +448,12 @@ __global__ __launch_bounds__(NW * 64, 1) void stream_kernel(Layer3Args a) {
     }
     if (t == 0) sm.parity = (e_prev + 1u) & 1u;
     lds_barrier();
+    if constexpr (TR) {   // workgroup 0's staged Q8_K(x), as the gate/up rows read it
+        if (blockIdx.x == 0 && a.tq8x)
+            for (int b = wv; b < nbx; b += NW)
+                trace_q8_block(a.tq8x + 292 * b, reinterpret_cast<const float*>(lds + kS_XQ + 4096)[b],
+                               *reinterpret_cast<const uint32_t*>(lds + kS_XQ + qswz(256 * b + 4 * lane)), lane);
+    }
     const uint32_t parity = __builtin_amdgcn_readfirstlane(sm.parity);   // uniform: keeps buffer bases scalar
     float* const hcur = a.hbuf + size_t(parity) * kHBufWords;
     // Arrival: the last workgroup to arrive advances the launch count at its end.
@@ -509,6 +517,16 @@ __global__ __launch_bounds__(NW * 64, 1) void stream_kernel(Layer3Args a) {
                 const Looks Lu = look_xxs(lds, lo_g, lo_s, U0.w);
                 const int Ig = sum_xxs(Lg, G0.w, A.a[q], NA[q]);
                 const int Iu = sum_xxs(Lu, U0.w, A.a[q], NA[q]);
+                if constexpr (TR) {   // the row's block integers: a quad holds one block's four pairs
+                    const int bg = quad_isum(Ig), bu = quad_isum(Iu);
+                    if (a.tint && ((gok >> j) & 1u) && (lG & 3) == 0) {
+                        const uint32_t m = gsl(j);
+                        const size_t rec = size_t((m >> 12) & 15u) * (2 * size_t(ff) * nbx + size_t(dim) * nbh);
+                        const size_t o = rec + size_t(int(m & 0xfffu) + rG) * nbx + size_t((lG + LG * q) >> 2);
+                        a.tint[o] = bg;
+                        a.tint[o + size_t(ff) * nbx] = bu;
+                    }
+                }
                 fg = fmaf(__fmul_rn(h2f(G0.h[0]), A.d[q]), float(Ig), fg);
                 fu = fmaf(__fmul_rn(h2f(U0.h[0]), A.d[q]), float(Iu), fu);
             }
@@ -533,6 +551,9 @@ __global__ __launch_bounds__(NW * 64, 1) void stream_kernel(Layer3Args a) {
                 if (lG >= LG - 1 - b && hidx >= 0)
                     __hip_atomic_store(reinterpret_cast<uint32_t*>(hcur) + hidx, hb, __ATOMIC_RELAXED,
                                        __HIP_MEMORY_SCOPE_AGENT);
+                if constexpr (TR) {
+                    if (a.th && lG >= LG - 1 - b && hidx >= 0) a.th[hidx] = __uint_as_float(hb);
+                }
             }
             mark(8 + j);
         });
@@ -618,6 +639,15 @@ __global__ __launch_bounds__(NW * 64, 1) void stream_kernel(Layer3Args a) {
                         const Raw3& D0 = rd[j % (WIND + 1)][q];
                         if (q + 1 < PD) Lx[(q + 1) & 1] = look_xs(lds, lo_x, lo_s, rd[j % (WIND + 1)][q + 1].w);
                         const int I = sum_xs(Lx[q & 1], D0.h[0], B.a[q]);
+                        if constexpr (TR) {
+                            const int bi = quad_isum(I);
+                            if (a.tint && ((dok >> j) & 1u) && (lD & 3) == 0) {
+                                const uint32_t m = dsl(j);
+                                const size_t rec = size_t((m >> 12) & 15u) * (2 * size_t(ff) * nbx + size_t(dim) * nbh);
+                                a.tint[rec + 2 * size_t(ff) * nbx + size_t(int(m & 0xfffu) + rD) * nbh +
+                                       size_t((lD + LD * q) >> 2)] = bi;
+                            }
+                        }
                         f = fmaf(__fmul_rn(h2f(D0.h[1]), B.d[q]), float(I), f);
                     }
                     float okf = ((dok >> j) & 1u) ? 0.125f : 0.0f;   // opaque, as in gate/up
@@ -631,6 +661,15 @@ __global__ __launch_bounds__(NW * 64, 1) void stream_kernel(Layer3Args a) {
     }
     mark(6);
     lds_barrier();
+    if constexpr (TR) {   // workgroup 0's staged Q8_K(h) of every pick, as its down passes read it
+        if (blockIdx.x == 0 && a.tq8h)
+            for (int blk = wv; blk < k * nbh; blk += NW) {
+                const int i = blk / nbh, bb = blk - i * nbh;
+                const uint8_t* hq = lds + kS_HQ + i * hq_stride;
+                trace_q8_block(a.tq8h + 292 * blk, reinterpret_cast<const float*>(hq + ff)[bb],
+                               *reinterpret_cast<const uint32_t*>(hq + qswz(256 * bb + 4 * lane)), lane);
+            }
+    }
 
     // ---- fixed-order combine of this workgroup's rows
     const int nrows = nq_wg * RD;
@@ -654,6 +693,7 @@ __global__ __launch_bounds__(NW * 64, 1) void stream_kernel(Layer3Args a) {
 
 template <int NW, int LG, int PG, int LD, int PD, int MG, int MD, int WIN, int WIND, int MQ>
 hipError_t launch_stream_t(const Layer3Args& args, int grid, hipStream_t s, hipEvent_t stop) {
+    const bool tr = args.tq8x || args.tq8h || args.th || args.tint;
     constexpr int RG = 64 / LG, RD = 64 / LD;
     const int W = grid * NW;
     const int SG = args.k * (args.ff / RG);
@@ -674,8 +714,12 @@ hipError_t launch_stream_t(const Layer3Args& args, int grid, hipStream_t s, hipE
         grid > quads || args.k * (args.ff + 64) > kS_HQBytes || args.k * args.ff > kHBufWords || !args.hbuf ||
         !args.slab)   // regular layers only: every matrix is found from its expert id
         return hipErrorNotSupported;
-    hipExtLaunchKernelGGL((stream_kernel<NW, LG, PG, LD, PD, MG, MD, WIN, WIND, MQ>), dim3(grid), dim3(NW * 64), 0, s,
-                          nullptr, stop, 0, args);
+    if (tr)
+        hipExtLaunchKernelGGL((stream_kernel<NW, LG, PG, LD, PD, MG, MD, WIN, WIND, MQ, true>), dim3(grid),
+                              dim3(NW * 64), 0, s, nullptr, stop, 0, args);
+    else
+        hipExtLaunchKernelGGL((stream_kernel<NW, LG, PG, LD, PD, MG, MD, WIN, WIND, MQ, false>), dim3(grid),
+                              dim3(NW * 64), 0, s, nullptr, stop, 0, args);
     return hipGetLastError();
 }
 

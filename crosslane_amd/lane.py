@@ -80,6 +80,8 @@ _SIGNATURES = {
     "xl_expert_trace": (_I32, [_P, _I32, _I32, _f32p, _P, _P, _P, _P, _P, _ErrP]),
     "xl_layer_forward_async": (_I32, [_P, _I32, _P, _P, _I32, _P, _P, _P, _P, _ErrP]),
     "xl_sync": (_I32, [_P, _P, _ErrP]),
+    "xl_layer_trace_async": (_I32, [_P, _I32, _P, _P, _I32, _P, _P, _P, _P, _P, _P, _P, C.POINTER(_I32), _P, _ErrP]),
+    "xl_grouped_trace_async": (_I32, [_P, _I32, _I32, _I32, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _ErrP]),
     "xl_grouped_forward": (_I32, [_P, _I32, _I32, _I32, _i32p, _f32p, _f32p, _P, _f32p, _ErrP]),
     "xl_grouped_forward_async": (_I32, [_P, _I32, _I32, _I32, _P, _P, _P, _P, _P, _P, _ErrP]),
     "xl_route_async": (_I32, [_P, _P, _I32, _I32, _P, _I32, _I32, C.c_float, _P, _P, _P, _ErrP]),
@@ -342,6 +344,23 @@ class Lane:
     def layer_forward_async(self, layer: int, ids, w, x, out, shared=None, stream=None) -> None:
         self._call("xl_layer_forward_async", layer, _ptr(ids), _ptr(w), int(ids.numel()), _ptr(x), _ptr(shared),
                    _ptr(out), None if stream is None else int(stream))
+
+    def layer_trace_async(self, layer: int, ids, w, x, out, q8x=None, q8h=None, h=None, ints=None, shared=None,
+                          stream=None) -> int:
+        """The single-launch layer call with its own Q8_K(x) / Q8_K(h) blocks (uint8
+        tensors of 292-byte blocks), h and block integers written out; returns the
+        kernel that ran (1 streaming, 3 all-types)."""
+        kern = _I32()
+        self._call("xl_layer_trace_async", layer, _ptr(ids), _ptr(w), int(ids.numel()), _ptr(x), _ptr(shared),
+                   _ptr(out), _ptr(q8x), _ptr(q8h), _ptr(h), _ptr(ints), C.byref(kern),
+                   None if stream is None else int(stream))
+        return kern.value
+
+    def grouped_trace_async(self, layer: int, ids, w, x, out, q8x=None, q8h=None, h=None, ints=None, shared=None,
+                            stream=None) -> None:
+        T, k = int(ids.shape[0]), int(ids.shape[1])
+        self._call("xl_grouped_trace_async", layer, T, k, _ptr(ids), _ptr(w), _ptr(x), _ptr(shared), _ptr(out),
+                   _ptr(q8x), _ptr(q8h), _ptr(h), _ptr(ints), None if stream is None else int(stream))
 
     def grouped_forward_async(self, layer: int, ids, w, x, out, shared=None, stream=None) -> None:
         """ids, w: [T, k] device tensors; x, out (and shared): [T, dim]."""

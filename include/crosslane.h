@@ -174,6 +174,32 @@ int32_t xl_grouped_forward_async(xl_context* ctx, int32_t layer, int32_t T, int3
                                  const float* d_w, const float* d_x, const float* d_shared_or_null, float* d_out,
                                  void* stream, xl_error* err);
 
+/* ---- parity trace (device pointers) -------------------------------------------
+ * The layer call's own intermediates, written by the kernel that computes it
+ * (the reference's probe dumps its lane's Q8_K bytes the same way,
+ * parity/hip_resident_check.cpp:91-127): the same single launch
+ * xl_layer_forward_async would make, plus
+ *   q8x  dim/256 Q8_K blocks (292 bytes: d, qs[256], bsums[16]; q8k_core.hpp:13)
+ *        of x, as the launch staged them for its gate/up rows;
+ *   q8h  k * ff/256 blocks, pick i's Q8_K(h) as staged for its down rows;
+ *   h    k * ff floats, the SwiGLU output the launch quantized;
+ *   ints per pick (ids order): gate ff x dim/256, up ff x dim/256, down
+ *        dim x ff/256 int32, each row's exact integer per 256-weight block (as
+ *        xl_matvec_async's partials; IQ1_M: 8 * main + delta);
+ * kernel_out (host, may be null): 1 the streaming kernel ran, 3 the all-types
+ * kernel. Any of q8x, q8h, h, ints may be null (not all). XL_E_ARG when the
+ * layer does not run as a single launch. A diagnostic aid (no counterpart in
+ * the reference beyond its probe); it runs the traced kernel instances. */
+int32_t xl_layer_trace_async(xl_context* ctx, int32_t layer, const int32_t* d_ids, const float* d_w, int32_t k,
+                             const float* d_x, const float* d_shared_or_null, float* d_out, void* d_q8x, void* d_q8h,
+                             float* d_h, int32_t* d_ints, int32_t* kernel_out, void* stream, xl_error* err);
+/* The same for the grouped MFMA path (XL_E_ARG when the layer does not run on
+ * it): q8x per token (T x dim/256 blocks), q8h, h and ints per pair (P = T * k,
+ * token-major), layouts as above. */
+int32_t xl_grouped_trace_async(xl_context* ctx, int32_t layer, int32_t T, int32_t k, const int32_t* d_ids,
+                               const float* d_w, const float* d_x, const float* d_shared_or_null, float* d_out,
+                               void* d_q8x, void* d_q8h, float* d_h, int32_t* d_ints, void* stream, xl_error* err);
+
 /* ---- router (device pointers) -----------------------------------------------
  * route.cpp:15-37 (route_cpu) on the device, per token: score =
  * sqrt(softplus(logit)) (the logit itself above 20), key = score + bias (a null
@@ -205,8 +231,10 @@ int32_t xl_quantize_q8k_async(xl_context* ctx, const float* d_x, int32_t rows, i
 int32_t xl_swiglu_async(xl_context* ctx, const float* d_g, const float* d_u, int32_t n, float limit, float* d_h,
                         void* stream, xl_error* err);
 /* One planar matrix (n x k) times Q8_K(x): y[n] and, when non-null, the
- * per-block int32 partials (n*k/256 ints; IQ1_M: (main, delta) pairs).
- * Replaces q8k::mv (hip_q8k.hpp:10). d_x is the f32 input vector. */
+ * per-block int32 partials (n*k/256 ints: each row's exact integer per
+ * 256-weight block, sum of (2s+1) * grid * sign * q over the block; IQ1_M:
+ * 8 * main + delta, the integer the decoder forms). Replaces q8k::mv
+ * (hip_q8k.hpp:10). d_x is the f32 input vector. */
 int32_t xl_matvec_async(xl_context* ctx, int32_t type, const void* d_planar, int32_t n, int32_t k, const float* d_x,
                         float* d_y, int32_t* d_partials, void* stream, xl_error* err);
 

@@ -46,6 +46,7 @@ class Oracle:
         L.orc_dot.restype = C.c_float
         L.orc_block_partials.argtypes = [C.c_int, _u8p, _P, C.c_int, _i32p]
         L.orc_integer_lane.argtypes = [C.c_int, _u8p, _P, C.c_int, C.POINTER(C.c_int32), C.POINTER(C.c_int32)]
+        L.orc_matrix_ints.argtypes = [C.c_int, _u8p, C.c_int, C.c_int, _P, _i32p, C.c_int]
         L.orc_brute_block.argtypes = [C.c_int, _u8p, _P]
         L.orc_brute_block.restype = C.c_int64
         L.orc_matvec.argtypes = [C.c_int, _u8p, C.c_int, C.c_int, _P, _f32p, C.c_int]
@@ -92,6 +93,15 @@ class Oracle:
     def block_partials(self, t: int, row: np.ndarray, act: np.ndarray) -> np.ndarray:
         out = np.zeros(act.size * (2 if t == 29 else 1), dtype=np.int32)
         self.lib.orc_block_partials(t, np.ascontiguousarray(row), act.ctypes.data, act.size, out)
+        return out
+
+    def matrix_ints(self, t: int, w: np.ndarray, n: int, k: int, act: np.ndarray, threads: int = 8) -> np.ndarray:
+        """[n, k/256] block integers of an AoS matrix against Q8_K blocks act
+        (IQ1_M: 8 * main + delta, the integer the device decoders form)."""
+        act = np.ascontiguousarray(act)
+        assert act.size == k // 256
+        out = np.zeros((n, k // 256), np.int32)
+        self.lib.orc_matrix_ints(t, np.ascontiguousarray(w).reshape(-1), n, k, act.ctypes.data, out.reshape(-1), threads)
         return out
 
     def integer_lane(self, t: int, block: np.ndarray, act_block: np.ndarray, lane: int):

@@ -188,6 +188,41 @@ void orc_block_partials(int t, const uint8_t* w, const orc_q8k* a, int nb, int32
     }
 }
 
+/* Block integers of n rows of k/256 blocks against one Q8_K vector: one int
+ * per (row, block), the sum over the 8 AVX2 lanes of integer_lane; IQ1_M
+ * folds (main, delta) to 8 * main + delta. Rows split over `threads`. */
+typedef struct { int t, n, nb, r0, r1; const uint8_t* w; const orc_q8k* a; int32_t* out; } MiJob;
+static void* mi_run(void* p) {
+    const MiJob* j = (const MiJob*)p;
+    const size_t rb = (size_t)j->nb * (size_t)orc_block_bytes(j->t);
+    int32_t tmp[2 * 64];
+    for (int r = j->r0; r < j->r1; ++r) {
+        for (int b0 = 0; b0 < j->nb; b0 += 64) {
+            const int nb = j->nb - b0 < 64 ? j->nb - b0 : 64;
+            orc_block_partials(j->t, j->w + (size_t)r * rb + (size_t)b0 * orc_block_bytes(j->t), j->a + b0, nb, tmp);
+            for (int b = 0; b < nb; ++b)
+                j->out[(size_t)r * j->nb + b0 + b] = j->t == 29 ? 8 * tmp[2 * b] + tmp[2 * b + 1] : tmp[b];
+        }
+    }
+    return NULL;
+}
+void orc_matrix_ints(int t, const uint8_t* w, int n, int k, const orc_q8k* a, int32_t* out, int threads) {
+    if (threads < 1) threads = 1;
+    if (threads > 64) threads = 64;
+    pthread_t th[64];
+    MiJob jobs[64];
+    const int per = (n + threads - 1) / threads;
+    int used = 0;
+    for (int i = 0; i < threads; ++i) {
+        const int r0 = i * per, r1 = r0 + per < n ? r0 + per : n;
+        if (r0 >= r1) break;
+        jobs[i] = (MiJob){t, n, k / 256, r0, r1, w, a, out};
+        pthread_create(&th[i], NULL, mi_run, &jobs[i]);
+        ++used;
+    }
+    for (int i = 0; i < used; ++i) pthread_join(th[i], NULL);
+}
+
 /* Per-32 decode of sub-block ib of a 256-weight block, written from
  * sycl/moe/core.hpp:78-105: natural value order, per-16 odd sub-scales (sc),
  * IQ2 values +-grid, IQ1_M values 8*grid + delta. */

@@ -51,6 +51,9 @@ float orc_dot(int type, const uint8_t* w, const orc_q8k* a, int nb);
 /* Per-block integer partials: Sum over the 8 AVX2 lanes of integer_lane.
  * IQ2 types write one int per block; IQ1_M writes (main, delta) pairs. */
 void orc_block_partials(int type, const uint8_t* w, const orc_q8k* a, int nb, int32_t* out);
+/* Block integers of an n x k matrix (AoS rows) against one Q8_K vector of
+ * k/256 blocks: n * k/256 ints, row-major; IQ1_M: 8 * main + delta. */
+void orc_matrix_ints(int type, const uint8_t* w, int n, int k, const orc_q8k* a, int32_t* out, int threads);
 /* Brute force: dequantize to signed ints with per-16 scales and multiply.
  * IQ2: returns Sum (2s+1)*sign*grid*q; IQ1_M: returns 8*main + delta. */
 int64_t orc_brute_block(int type, const uint8_t* blk, const orc_q8k* a);

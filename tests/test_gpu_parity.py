@@ -72,13 +72,15 @@ def test_matvec_partials_exact(probe, orc, t, n, k):
     x = np.random.default_rng(n * k + t).standard_normal(k).astype(np.float32)
     y = torch.zeros(n, dtype=torch.float32, device="cuda")
     nb = k // 256
-    parts = torch.zeros(n * nb * (2 if t == 29 else 1), dtype=torch.int32, device="cuda")
+    parts = torch.zeros(n * nb, dtype=torch.int32, device="cuda")
     probe.matvec_async(t, planar, n, k, dev(x), y, parts)
     probe.sync()
     act = orc.quantize(x)
     rb = nb * BLOCK_BYTES[t]
-    want_parts = np.concatenate([orc.block_partials(t, aos[r * rb:(r + 1) * rb], act) for r in range(n)])
-    assert np.array_equal(parts.cpu().numpy(), want_parts)
+    bp = np.stack([orc.block_partials(t, aos[r * rb:(r + 1) * rb], act) for r in range(n)])
+    # one int per block; IQ1_M's (main, delta) enter as 8 * main + delta, the integer the decoder forms
+    want_parts = (8 * bp[:, 0::2] + bp[:, 1::2]) if t == 29 else bp
+    assert np.array_equal(parts.cpu().numpy(), want_parts.reshape(-1))
     want_y = orc.matvec(t, aos, n, k, act)
     assert max_rel(y.cpu().numpy(), want_y) < TOL
 

@@ -125,6 +125,20 @@ def test_block_partials_brute_force(orc, t, rng):
 
 
 @pytest.mark.parametrize("t", [16, 17, 29])
+def test_matrix_ints_brute_force(orc, t, rng):
+    # orc_matrix_ints (the device trace's comparison target) against the
+    # brute-force block dot, row by row, over several threads.
+    n, k = 37, 1280
+    act = orc.quantize(rng.standard_normal(k).astype(np.float32))
+    w = orc.gen_matrix(t, 9, 1, 2, 1, n, k)
+    got = orc.matrix_ints(t, w, n, k, act, threads=3)
+    bb = BLOCK_BYTES[t]
+    want = np.array([[orc.brute_block(t, w[(r * (k // 256) + b) * bb:(r * (k // 256) + b + 1) * bb], act[b:b + 1])
+                      for b in range(k // 256)] for r in range(n)], np.int64)
+    assert np.array_equal(got.astype(np.int64), want)
+
+
+@pytest.mark.parametrize("t", [16, 17, 29])
 def test_brute_force_vs_reference_decoder(orc, ref, t, rng):
     # Reference per-32 decoder (sycl/moe/core.hpp): values and odd sub-scales.
     w = orc.gen_matrix(t, 11, 1, 2, 0, 4, 256)

@@ -498,8 +498,10 @@ int32_t xl_open(uint32_t abi_version, const xl_config* cfg, xl_context** out, xl
         need(cfg != nullptr, XL_E_ARG, "null config");
         need(cfg->struct_bytes == sizeof(xl_config), XL_E_VERSION, "xl_config size mismatch");
         int lpr, ppl;
-        need(xl::row_shape(cfg->dim, lpr, ppl), XL_E_ARG, "dim not supported (256..4096, see row_shape)");
-        need(xl::row_shape(cfg->ff, lpr, ppl), XL_E_ARG, "ff not supported (256..4096, see row_shape)");
+        need(xl::row_shape(cfg->dim, lpr, ppl), XL_E_ARG,
+             "dim not supported (256, 512, 768, 1024, 2048, 2304, 3072, 4096 or 5120)");
+        need(xl::row_shape(cfg->ff, lpr, ppl), XL_E_ARG,
+             "ff not supported (256, 512, 768, 1024, 2048, 2304, 3072, 4096 or 5120)");
         need(cfg->n_layers >= 1 && cfg->n_layers <= 4096, XL_E_ARG, "n_layers outside 1..4096");
         need(cfg->n_experts >= 1 && cfg->n_experts <= 65536, XL_E_ARG, "n_experts outside 1..65536");
         need(cfg->max_picks >= 1 && cfg->max_picks <= 16, XL_E_ARG, "max_picks outside 1..16");
@@ -520,7 +522,7 @@ int32_t xl_open(uint32_t abi_version, const xl_config* cfg, xl_context** out, xl
         ctx->grid_down = env_int("XL_WGS_DOWN", 4 * ctx->cus);
 
         const int P = cfg->max_picks, dim = cfg->dim, ff = cfg->ff;
-        ctx->act_max = std::max({dim, ff, 4096});
+        ctx->act_max = std::max({dim, ff, xl::kMaxRowK});
         struct Part { void** p; uint64_t bytes; };
         const uint64_t code_bytes = (256 + 512 + 2048) * 2;
         std::vector<Part> parts = {

@@ -58,8 +58,16 @@ constexpr int kL_GRID = 0, kL_SGN = 65536, kL_TAB = 131072;
 // these small loads every block): the 16 pairs' activation block scales
 // [block][pair] (f32), then the item's 128 rows' fp16 block scales [row][block]
 // for each matrix, then (down) the rows' IQ2_XS scale bytes [row][block][8].
-constexpr int kL_PD = kL_TAB, kL_RD = kL_PD + 16 * 16 * 4, kL_RS = kL_RD + 2 * 128 * 16 * 2;
-constexpr int kL_Bytes = kL_RS + 128 * 16 * 8;
+// Blocks per row these regions hold: gate/up rows of dim <= kMaxRowK, down
+// rows of ff <= 4096.
+constexpr int kGuNb = kMaxRowK / 256, kDnNb = 16;
+constexpr int kL_PD = kL_TAB;
+constexpr int kL_RDG = kL_PD + 16 * kGuNb * 4;     // gate/up: 2 planes of 128 rows x kGuNb fp16 scales
+constexpr int kL_GuBytes = kL_RDG + 2 * 128 * kGuNb * 2;
+constexpr int kL_RDD = kL_PD + 16 * kDnNb * 4;     // down: 128 rows x kDnNb fp16 scales, then scale bytes
+constexpr int kL_RS = kL_RDD + 128 * kDnNb * 2;
+constexpr int kL_DnBytes = kL_RS + 128 * kDnNb * 8;
+static_assert(kL_GuBytes <= 160 * 1024 && kL_DnBytes <= 160 * 1024, "LDS budget");
 constexpr int kCopiesXXS = 16;   // 256 entries x 256 B: the entry byte lands in address byte 1
 constexpr int kCopiesXS = 8;     // 512 entries x 128 B: the 9-bit entry lands at address bit 7
 
@@ -295,9 +303,11 @@ struct DnOps {
 // Stages one item's pair scales (scl: one f32 per (pair row, block), pairs of
 // the task's order slots) and `mats` planes of fp16 row scales (128 rows from
 // row0, nb per row, contiguous in each plane) into LDS, between two barriers.
+// The planes go to LDS at rd, `mstride` bytes apart.
 template <int NT>
 __device__ __forceinline__ void stage_item(uint8_t* lds, const GroupArgs& a, const int4& tk, const float* scl, int per_pair,
-                                           int nb, const uint8_t* const* planes, int mats, int row0, int t) {
+                                           int nb, const uint8_t* const* planes, int mats, int row0, int t, int rd,
+                                           int mstride) {
     __syncthreads();   // every wave is done with the previous item's staging
     for (int i = t; i < 16 * nb; i += NT) {
         const int pos = i & 15, blk = i >> 4;
@@ -308,7 +318,7 @@ __device__ __forceinline__ void stage_item(uint8_t* lds, const GroupArgs& a, con
     for (int i = t; i < mats * chunks; i += NT) {
         const int m = i / chunks, c = i - m * chunks;
         const uint4 v = reinterpret_cast<const uint4*>(planes[m] + size_t(row0) * nb * 2)[c];
-        *reinterpret_cast<uint4*>(lds + kL_RD + m * 128 * 16 * 2 + 16 * c) = v;
+        *reinterpret_cast<uint4*>(lds + rd + m * mstride + 16 * c) = v;
     }
 }
 
@@ -319,7 +329,7 @@ __device__ __forceinline__ void stage_item(uint8_t* lds, const GroupArgs& a, con
 // TR: also write each pair's block integers (GroupArgs::tint).
 template <int NW, bool TR>
 __global__ __launch_bounds__(NW * 64, 1) void gu_kernel(GroupArgs a) {
-    __shared__ __attribute__((aligned(16))) uint8_t lds[kL_Bytes];
+    __shared__ __attribute__((aligned(16))) uint8_t lds[kL_GuBytes];
     const int t = threadIdx.x, lane = t & 63, wv = t >> 6;
     fill_grid<256, kCopiesXXS>(lds, a.tables + kTabXXS / 8, t, NW * 64);
     fill_signs(lds, a.tables, t, NW * 64);
@@ -347,7 +357,7 @@ __global__ __launch_bounds__(NW * 64, 1) void gu_kernel(GroupArgs a) {
         const MatRef G = mat_at(a.descs, tk.x, 0), U = mat_at(a.descs, tk.x, 1);
         {
             const uint8_t* planes[2] = {G.base + G.off1, U.base + U.off1};
-            stage_item<NW * 64>(lds, a, tk, a.xd, 0, nb, planes, 2, grp * NW * 16, t);
+            stage_item<NW * 64>(lds, a, tk, a.xd, 0, nb, planes, 2, grp * NW * 16, t, kL_RDG, 128 * kGuNb * 2);
         }
         const __amdgpu_buffer_rsrc_t rg = rsrc(G.base), ru = rsrc(U.base), rx = rsrc(a.xq);
         const uint32_t vq = uint32_t(row * nb) * 64u;
@@ -377,8 +387,8 @@ __global__ __launch_bounds__(NW * 64, 1) void gu_kernel(GroupArgs a) {
 #pragma unroll
             for (int r = 0; r < 4; ++r) bi[r] = mad24(ls, C[r], bi[r]);
         };
-        const uint16_t* sdg = reinterpret_cast<const uint16_t*>(lds + kL_RD) + (wv * 16 + col) * nb;
-        const uint16_t* sdu = sdg + 128 * 16;
+        const uint16_t* sdg = reinterpret_cast<const uint16_t*>(lds + kL_RDG) + (wv * 16 + col) * nb;
+        const uint16_t* sdu = sdg + 128 * kGuNb;
         int blk_c = 0;   // block the next compute() handles
         auto compute = [&](const GuOps& o) {
             const int b = blk_c++;
@@ -473,7 +483,7 @@ __device__ __forceinline__ void xs_lane(const uint4& w, uint32_t (&u)[4]) {
 // ---------------------------------------------------------------------------
 template <int NW, bool TR>
 __global__ __launch_bounds__(NW * 64, 1) void dn_kernel(GroupArgs a) {
-    __shared__ __attribute__((aligned(16))) uint8_t lds[kL_Bytes];
+    __shared__ __attribute__((aligned(16))) uint8_t lds[kL_DnBytes];
     const int t = threadIdx.x, lane = t & 63, wv = t >> 6;
     fill_grid<512, kCopiesXS>(lds, a.tables + kTabXS / 8, t, NW * 64);
     fill_signs(lds, a.tables, t, NW * 64);
@@ -501,7 +511,7 @@ __global__ __launch_bounds__(NW * 64, 1) void dn_kernel(GroupArgs a) {
         {
             const int row0 = grp * NW * 16;
             const uint8_t* planes[1] = {D.base + D.off2};
-            stage_item<NW * 64>(lds, a, tk, a.hd, 1, nb, planes, 1, row0, t);
+            stage_item<NW * 64>(lds, a, tk, a.hd, 1, nb, planes, 1, row0, t, kL_RDD, 0);
             const int chunks = 128 * nb * 8 / 16;   // the rows' IQ2_XS scale bytes
             for (int i = t; i < chunks; i += NW * 64)
                 *reinterpret_cast<uint4*>(lds + kL_RS + 16 * i) =
@@ -552,7 +562,7 @@ __global__ __launch_bounds__(NW * 64, 1) void dn_kernel(GroupArgs a) {
                     if (a.tint && po[r] >= 0)
                         a.tint[size_t(po[r]) * rec + 2 * size_t(a.ff) * nbx + size_t(row) * nb + size_t(b)] = bi[r];
             }
-            const float ddf = h2f(reinterpret_cast<const uint16_t*>(lds + kL_RD)[rl * nb + b]);
+            const float ddf = h2f(reinterpret_cast<const uint16_t*>(lds + kL_RDD)[rl * nb + b]);
             const float4 hd4 = *reinterpret_cast<const float4*>(lds + kL_PD + 64 * b + 16 * e4);
             const float hd[4] = {hd4.x, hd4.y, hd4.z, hd4.w};
 #pragma unroll
@@ -618,7 +628,7 @@ __global__ __launch_bounds__(256) void gcombine_kernel(GroupArgs a) {
 hipError_t launch_grouped(const GroupArgs& args, int cus, hipStream_t s) {
     constexpr int NW = 8;
     if (args.T < 1 || args.k < 1 || args.k > 16 || args.n_experts > kGroupMaxExperts || args.dim % (NW * 16) ||
-        args.ff % (NW * 16) || args.dim % 256 || args.ff % 256 || args.dim > 4096 || args.ff > 4096)
+        args.ff % (NW * 16) || args.dim % 256 || args.ff % 256 || args.dim > kGuNb * 256 || args.ff > kDnNb * 256)
         return hipErrorNotSupported;
     const int P = args.T * args.k;
     hipLaunchKernelGGL(bucket_kernel, dim3(1), dim3(1024), 0, s, args);

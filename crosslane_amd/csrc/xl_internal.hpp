@@ -29,6 +29,8 @@ struct ExpertDesc {
 
 // Shapes accepted by the specialized row kernels: K (the contraction length)
 // maps to lanes-per-row LPR and pairs-per-lane PPL with LPR * PPL * 64 == K.
+// 2304 and 5120 are the DeepSeek-V4.1 expert's ff and dim
+// (engine/strata/fixtures/moe/cpu_lane_fixture.cpp:17).
 inline bool row_shape(int k, int& lpr, int& ppl) {
     if (k <= 0 || k % 256) return false;
     const int pairs = k / 64;
@@ -37,10 +39,11 @@ inline bool row_shape(int k, int& lpr, int& ppl) {
     lpr = l;
     ppl = pairs / l;
     switch (k) {
-        case 256: case 512: case 768: case 1024: case 2048: case 3072: case 4096: return true;
+        case 256: case 512: case 768: case 1024: case 2048: case 2304: case 3072: case 4096: case 5120: return true;
         default: return false;
     }
 }
+constexpr int kMaxRowK = 5120;   // the longest row any kernel stages
 
 // Arguments of the fused layer kernel (device pointers).
 struct LayerArgs {

@@ -631,7 +631,11 @@ __global__ __launch_bounds__(256) void generate_kernel(uint8_t* __restrict__ bas
 // ---------------------------------------------------------------------------
 // Launchers
 // ---------------------------------------------------------------------------
-#define XL_SHAPES(X) X(4, 1) X(8, 1) X(4, 3) X(16, 1) X(32, 1) X(16, 3) X(64, 1)
+#define XL_SHAPES(X) X(4, 1) X(8, 1) X(4, 3) X(16, 1) X(32, 1) X(4, 9) X(16, 3) X(64, 1) X(16, 5)
+// Row slots a wave holds in flight: fewer for long lanes (PPL pairs each), so
+// that the raw words and activations stay within the register file.
+constexpr int gu_slots(int ppl) { return ppl >= 9 ? 1 : ppl >= 5 ? 2 : 4; }
+constexpr int dn_slots(int ppl) { return ppl >= 5 ? 1 : 2; }
 
 static int need_of(int type_mask) {
     return ((type_mask & 1) ? kNeedXXS : 0) | ((type_mask & 2) ? kNeedXS : 0) | ((type_mask & 4) ? kNeedIQ1 : 0);
@@ -682,12 +686,12 @@ hipError_t launch_gate_up(const ExpertDesc* descs, const int32_t* ids, int k, in
                           float* u_dbg, int* err, int target_wgs, int type_mask, float lim, hipStream_t s) {
     int lpr, ppl;
     if (!row_shape(dim, lpr, ppl) || k <= 0) return hipErrorInvalidValue;
-    constexpr int U = 4;
-    const int wgpp = wg_per_pick(ff / (64 / lpr), U, k, target_wgs);
     const int need = need_of(type_mask);
     const size_t lds = size_t(lds_bytes_for(need));
 #define XL_GU(L, P)                                                                                                   \
     if (lpr == L && ppl == P) {                                                                                       \
+        constexpr int U = gu_slots(P);                                                                                \
+        const int wgpp = wg_per_pick(ff / (64 / lpr), U, k, target_wgs);                                             \
         hipLaunchKernelGGL((gate_up_kernel<L, P, U>), dim3(k * wgpp), dim3(256), lds, s, descs, ids, n_experts, ff,   \
                            wgpp, xq, xd, codes, need, h, g_dbg, u_dbg, err, lim);                                     \
         return hipGetLastError();                                                                                     \
@@ -702,12 +706,12 @@ hipError_t launch_down(const ExpertDesc* descs, const int32_t* ids, int k, int n
                        int type_mask, hipStream_t s) {
     int lpr, ppl;
     if (!row_shape(ff, lpr, ppl) || k <= 0) return hipErrorInvalidValue;
-    constexpr int U = 2;
-    const int wgpp = wg_per_pick(dim / (64 / lpr), U, k, target_wgs);
     const int need = need_of(type_mask);
     const size_t lds = size_t(lds_bytes_for(need));
 #define XL_DN(L, P)                                                                                                   \
     if (lpr == L && ppl == P) {                                                                                       \
+        constexpr int U = dn_slots(P);                                                                                \
+        const int wgpp = wg_per_pick(dim / (64 / lpr), U, k, target_wgs);                                            \
         hipLaunchKernelGGL((down_kernel<L, P, U>), dim3(k * wgpp), dim3(256), lds, s, descs, ids, n_experts, dim, ff, \
                            wgpp, hq, hd, codes, need, y, err);                                                        \
         return hipGetLastError();                                                                                     \

@@ -72,9 +72,9 @@ struct Lay {
     static constexpr int C1 = TM == 4 ? 4 : 1;
     static_assert(C1 == 1 || (TM & 3) == 0, "the IQ1 single copy is staged where the IQ2 tables' are");
     static constexpr int IQ1 = XS + ((TM & 2) ? 512 * CXS * 8 : 0);          // 2048 rows of 8 values
-    static constexpr int XQ = IQ1 + ((TM & 4) ? 2048 * 8 * C1 : 0);          // Q8_K(x) quants (dim <= 4096)
-    static constexpr int XD = XQ + 4096;                                     // Q8_K(x) scales (16)
-    static constexpr int Y = XD + 64;                                        // y staging
+    static constexpr int XQ = IQ1 + ((TM & 4) ? 2048 * 8 * C1 : 0);          // Q8_K(x) quants (dim <= kMaxRowK)
+    static constexpr int XD = XQ + kMaxRowK;                                 // Q8_K(x) scales (kMaxRowK / 256)
+    static constexpr int Y = XD + kMaxRowK / 64;                             // y staging
     static constexpr int HQ = Y + kYStage * 4;
     static_assert(HQ + 8192 <= kLdsBytes, "LDS budget");
 };
@@ -269,7 +269,9 @@ __device__ __forceinline__ float row_sum(const uint8_t* lds, const Lut& L, int t
 // holds; WIN: gate/up slots in flight per wave; WIND: down passes in flight.
 // TR: also write the parity trace (Layer3Args::tq8x ...); the untraced instance
 // compiles none of it.
-template <int NW, int LG, int PG, int LD, int PD, int MG, int MD, int WIN, int WIND, int GUT, int DNT, bool TR>
+// DP: pairs of a down row when LD * PD * 64 exceeds ff (0: exactly LD * PD).
+// Lanes past them load the row's last pair (in bounds) against zero activations.
+template <int NW, int LG, int PG, int LD, int PD, int MG, int MD, int WIN, int WIND, int GUT, int DNT, bool TR, int DP>
 __global__ __launch_bounds__(NW * 64, 1) void layer3_kernel(Layer3Args a) {
     __shared__ __attribute__((aligned(16))) uint8_t lds[kLdsBytes];
     __shared__ uint32_t s_epoch;
@@ -279,6 +281,8 @@ __global__ __launch_bounds__(NW * 64, 1) void layer3_kernel(Layer3Args a) {
     constexpr int TM = GUT | DNT;
     using LY = Lay<TM>;
     constexpr int RG = 64 / LG, RD = 64 / LD;
+    constexpr int NPD = DP ? DP : LD * PD;   // live pairs of a down row
+    static_assert(NPD <= LD * PD && (LD * PD - NPD) < LD, "only the last pair slot of a lane may be dead");
     const int t = threadIdx.x, lane = t & 63;
     const int wv = __builtin_amdgcn_readfirstlane(t >> 6);   // wave-uniform: keeps slot/pick/matrix math scalar
     const int G = gridDim.x, W = G * NW, gw = blockIdx.x * NW + wv;
@@ -342,7 +346,7 @@ __global__ __launch_bounds__(NW * 64, 1) void layer3_kernel(Layer3Args a) {
         if constexpr (TM & 2) lds_dma<NW>(lds, LY::HQ + 4096, gt + kG_XS, 4096, wv, lane);
         if constexpr (TM & 4) lds_dma<NW>(lds, LY::C1 > 1 ? LY::HQ : LY::IQ1, gt + kG_IQ1, 16384, wv, lane);
     }
-    constexpr int UX = (16 + NW - 1) / NW;
+    constexpr int UX = (kMaxRowK / 256 + NW - 1) / NW;
     float4 xv[UX];
 #pragma unroll
     for (int u = 0; u < UX; ++u) {
@@ -426,7 +430,8 @@ __global__ __launch_bounds__(NW * 64, 1) void layer3_kernel(Layer3Args a) {
     Raw3 rd[WIND + 1][PD];   // ring of down passes in flight
     auto load_pass = [&](int j) {
 #pragma unroll
-        for (int q = 0; q < PD; ++q) load_pair_t<DNT>(rd[j % (WIND + 1)][q], dm[j], drow[j] - rD, rD, lD + LD * q);
+        for (int q = 0; q < PD; ++q)
+            load_pair_t<DNT>(rd[j % (WIND + 1)][q], dm[j], drow[j] - rD, rD, min(lD + LD * q, NPD - 1));
     };
     int issued = 0;   // down passes issued so far (wave-uniform)
 
@@ -581,12 +586,15 @@ __global__ __launch_bounds__(NW * 64, 1) void layer3_kernel(Layer3Args a) {
 #pragma unroll
                         for (int q = 0; q < PD; ++q) {
                             const int p = lD + LD * q;
+                            const bool live = p < NPD;   // a dead pair slot: zero activations
+                            const int pl = live ? p : NPD - 1;
 #pragma unroll
                             for (int c = 0; c < 4; ++c) {
-                                const uint4 v = *reinterpret_cast<const uint4*>(hq + qswz(64 * p + 16 * c));
-                                B.a[q][4 * c] = v.x; B.a[q][4 * c + 1] = v.y; B.a[q][4 * c + 2] = v.z; B.a[q][4 * c + 3] = v.w;
+                                const uint4 v = *reinterpret_cast<const uint4*>(hq + qswz(64 * pl + 16 * c));
+                                B.a[q][4 * c] = live ? v.x : 0u; B.a[q][4 * c + 1] = live ? v.y : 0u;
+                                B.a[q][4 * c + 2] = live ? v.z : 0u; B.a[q][4 * c + 3] = live ? v.w : 0u;
                             }
-                            B.d[q] = reinterpret_cast<const float*>(hq + ff)[p >> 2];
+                            B.d[q] = live ? reinterpret_cast<const float*>(hq + ff)[pl >> 2] : 0.0f;
                         }
                         group_sums<DNT>(B);
                         cur = i;
@@ -598,7 +606,7 @@ __global__ __launch_bounds__(NW * 64, 1) void layer3_kernel(Layer3Args a) {
 #pragma unroll
                         for (int q = 0; q < PD; ++q) {
                             const int bi = quad_isum(Id[q]);
-                            if (a.tint && (lD & 3) == 0)
+                            if (a.tint && (lD & 3) == 0 && lD + LD * q < NPD)
                                 a.tint[size_t(i) * rec + 2 * size_t(ff) * nbx + size_t(drow[j]) * nbh +
                                        size_t((lD + LD * q) >> 2)] = bi;
                         }
@@ -649,7 +657,7 @@ __global__ __launch_bounds__(NW * 64, 1) void layer3_kernel(Layer3Args a) {
 }
 
 // ---- launcher ------------------------------------------------------------------------------
-template <int NW, int LG, int PG, int LD, int PD, int MG, int MD, int WIN, int WIND, int GUT, int DNT>
+template <int NW, int LG, int PG, int LD, int PD, int MG, int MD, int WIN, int WIND, int GUT, int DNT, int DP = 0>
 static hipError_t launch3(const Layer3Args& args, int grid, hipStream_t s, hipEvent_t stop) {
     const bool tr = args.tq8x || args.tq8h || args.th || args.tint;
     constexpr int RG = 64 / LG, RD = 64 / LD;
@@ -664,10 +672,10 @@ static hipError_t launch3(const Layer3Args& args, int grid, hipStream_t s, hipEv
         Lay<GUT | DNT>::HQ + 16384 > kLdsBytes)   // the codebooks' single copies are staged there
         return hipErrorNotSupported;
     if (tr)
-        hipExtLaunchKernelGGL((layer3_kernel<NW, LG, PG, LD, PD, MG, MD, WIN, WIND, GUT, DNT, true>), dim3(grid),
+        hipExtLaunchKernelGGL((layer3_kernel<NW, LG, PG, LD, PD, MG, MD, WIN, WIND, GUT, DNT, true, DP>), dim3(grid),
                               dim3(NW * 64), 0, s, nullptr, stop, 0, args);
     else
-        hipExtLaunchKernelGGL((layer3_kernel<NW, LG, PG, LD, PD, MG, MD, WIN, WIND, GUT, DNT, false>), dim3(grid),
+        hipExtLaunchKernelGGL((layer3_kernel<NW, LG, PG, LD, PD, MG, MD, WIN, WIND, GUT, DNT, false, DP>), dim3(grid),
                               dim3(NW * 64), 0, s, nullptr, stop, 0, args);
     return hipGetLastError();
 }
@@ -675,18 +683,23 @@ static hipError_t launch3(const Layer3Args& args, int grid, hipStream_t s, hipEv
 // Instances by block-type set: (gate/up types, down types) exactly ({IQ2_XXS},
 // {IQ2_XS}) and ({IQ1_M}, {IQ1_M}) have their own instances; anything else
 // takes the all-types one.
-template <int NW, int LG, int PG, int LD, int PD, int MG, int MD, int WIN, int WIND>
+template <int NW, int LG, int PG, int LD, int PD, int MG, int MD, int WIN, int WIND, int DP = 0>
 static hipError_t launch3_types(const Layer3Args& args, int gu_types, int dn_types, int grid, hipStream_t s,
                                 hipEvent_t stop) {
-    if (gu_types == 1 && dn_types == 2) return launch3<NW, LG, PG, LD, PD, MG, MD, WIN, WIND, 1, 2>(args, grid, s, stop);
-    if (gu_types == 4 && dn_types == 4) return launch3<NW, LG, PG, LD, PD, MG, MD, WIN, WIND, 4, 4>(args, grid, s, stop);
-    return launch3<NW, LG, PG, LD, PD, MG, MD, WIN, WIND, 7, 7>(args, grid, s, stop);
+    if (gu_types == 1 && dn_types == 2)
+        return launch3<NW, LG, PG, LD, PD, MG, MD, WIN, WIND, 1, 2, DP>(args, grid, s, stop);
+    if (gu_types == 4 && dn_types == 4)
+        return launch3<NW, LG, PG, LD, PD, MG, MD, WIN, WIND, 4, 4, DP>(args, grid, s, stop);
+    return launch3<NW, LG, PG, LD, PD, MG, MD, WIN, WIND, 7, 7, DP>(args, grid, s, stop);
 }
 
 hipError_t launch_layer3(const Layer3Args& args, int gu_types, int dn_types, int cus, hipStream_t s, hipEvent_t stop) {
-    if (args.k < 1 || args.k > 16 || args.dim > 4096) return hipErrorNotSupported;
+    if (args.k < 1 || args.k > 16 || args.dim > kMaxRowK) return hipErrorNotSupported;
     int lg, pg, ld, pd;
     if (!row_shape(args.dim, lg, pg) || !row_shape(args.ff, ld, pd)) return hipErrorNotSupported;
+    if (lg == 16 && pg == 5 && ld == 4 && pd == 9)   // 5120 x 2304 (the real expert), down rows as 16 lanes x 3 pairs
+        return launch3_types<8, 16, 5, 16, 3, 3, 5, 1, 1, 36>(args, gu_types, dn_types, std::min(cus, args.dim / 4),
+                                                              s, stop);
     const int RD = 64 / ld;
     const int grid = std::min(cus, args.dim / RD);
     if (lg == 64 && pg == 1 && ld == 16 && pd == 3)   // 4096 x 3072

@@ -56,8 +56,8 @@ typedef struct xl_error {
 typedef struct xl_config {
     uint32_t struct_bytes; /* sizeof(xl_config) */
     int32_t device;        /* HIP device ordinal */
-    int32_t dim;           /* d_model: 256..4096, a multiple of 256 */
-    int32_t ff;            /* d_ff:    256..4096, a multiple of 256 */
+    int32_t dim;           /* d_model and d_ff: 256, 512, 768, 1024, 2048, 2304, */
+    int32_t ff;            /* 3072, 4096 or 5120 (the real expert: dim 5120, ff 2304) */
     int32_t n_layers;      /* layers in the bank */
     int32_t n_experts;     /* routed experts per layer */
     int32_t max_picks;     /* top-k bound, 1..16 (reference kPicks = 8, model_meta.hpp:18) */

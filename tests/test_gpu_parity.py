@@ -64,7 +64,8 @@ def test_q8k_bit_exact(probe, orc, rng):
 
 # ---- matvec + per-block partials -------------------------------------------------
 @pytest.mark.parametrize("t", [16, 17, 29])
-@pytest.mark.parametrize("n,k", [(64, 256), (96, 512), (40, 768), (128, 1024), (64, 2048), (256, 3072), (256, 4096)])
+@pytest.mark.parametrize("n,k", [(64, 256), (96, 512), (40, 768), (128, 1024), (64, 2048), (48, 2304), (256, 3072),
+                                 (256, 4096), (64, 5120)])
 def test_matvec_partials_exact(probe, orc, t, n, k):
     step(f"matvec type={t} n={n} k={k}")
     aos = orc.gen_matrix(t, 1234 + k, 0, t, 0, n, k)

@@ -28,9 +28,11 @@ weight bytes + x in + out per layer), plus us_per_layer; the roofline of the
 layer kernel (one launch per layer, so its average duration is the timed
 region's HIP-event time on the launching stream divided by the launches; HBM
 traffic per launch from the committed rocprofv3 FETCH_SIZE / WRITE_SIZE
-summary in profiles/, config 1); and the CPU baseline (the reference's own
-q8k_core.hpp chain, compiled from the reference sources into oracle/_ref, timed
-on a bounded sample on the host cores).
+summary in profiles/, config 1); and the CPU baseline (the AVX2 restatement of
+the reference CPU lane in oracle/cpu_lane.c, bit-identical to the scalar
+restatement, at 1 worker and at the box's CPU share with its phase split, and
+the reference's own scalar q8k_core.hpp chain from oracle/_ref beside it, on a
+bounded sample on the host cores).
 """
 from __future__ import annotations
 
@@ -134,17 +136,49 @@ def mixed_types(n_layers, seed):
     return np.repeat(t[..., None], 3, axis=-1).astype(np.int32)
 
 
-def cpu_baseline(layers: int, threads: int, pool: int = 48, config: int = 1):
-    """The reference's own CPU chain (oracle/_ref) on `layers` routed layers of
-    the config's shape.
+def host_info():
+    """Host CPU model, physical cores and logical CPUs this process may use, ISA."""
+    model, cores, flags = "unknown", set(), set()
+    allowed = os.sched_getaffinity(0)
+    try:
+        cpu, phys, core = None, None, None
+        for line in open("/proc/cpuinfo"):
+            k, _, v = line.partition(":")
+            k, v = k.strip(), v.strip()
+            if k == "processor":
+                cpu = int(v)
+            elif k == "model name" and model == "unknown":
+                model = v
+            elif k == "physical id":
+                phys = v
+            elif k == "core id":
+                core = v
+                if cpu in allowed:
+                    cores.add((phys, core))
+            elif k == "flags" and not flags:
+                flags = set(v.split())
+    except OSError:
+        pass
+    isa = [f for f in ("avx2", "fma", "avx512f", "avx512bw", "avx512_vnni") if f in flags]
+    return {"cpu": model, "physical_cores": len(cores) or len(allowed), "logical_cpus": len(allowed),
+            "isa_present": isa}
+
+
+def cpu_baseline(budget_s: float = 12.0, pool: int = 48, config: int = 1, max_threads: int = 0):
+    """The CPU baseline: this repo's AVX2 restatement of the reference CPU lane
+    (oracle/cpu_lane.c: ggml's AVX2 lane and FMA order, bit-identical to the
+    scalar restatement; 64-row jobs, phases q1 / gate_up / q2 / down,
+    engine/strata/sycl/moe/cpu_lane.cpp:70-81,157-170), at 1 worker and at the
+    box's CPU share (physical cores, capped at the share), plus the reference's
+    own scalar q8k_core.hpp chain (oracle/_ref) on a few layers, labelled.
 
     The picks are drawn from a pool of `pool` generated experts (48 x ~9 MB,
-    beyond the host caches) whose types follow the config; generation is not
-    timed."""
+    beyond the host caches) typed as the config's; generation is not timed."""
     from oracle.oracle import Oracle, Reference   # checker/baseline only
     orc = Oracle()
-    kind = "reference" if Reference.available() else "port"
-    impl = Reference() if kind == "reference" else orc
+    host = host_info()
+    share = max_threads or int(os.environ.get("OMP_NUM_THREADS", "0") or 0) or min(16, host["logical_cpus"])
+    workers = sorted({1, min(host["physical_cores"], share), min(host["logical_cpus"], share)})
     rng = np.random.default_rng(SEED + 1)
     if config == 2:
         ptypes = [(29, 29, 29)] * pool
@@ -155,24 +189,72 @@ def cpu_baseline(layers: int, threads: int, pool: int = 48, config: int = 1):
         ptypes = [(GATE_T, GATE_T, DOWN_T)] * pool
     k = 1 if config == 0 else K
     mats = [orc.gen_expert(ptypes[e], SEED, 0, e, DIM, FF) for e in range(pool)]   # not timed
-    elapsed = 0.0
-    nbytes = 0
-    for _ in range(layers):
-        ids = rng.choice(pool, size=k, replace=False).astype(np.int32)
-        w = rng.random(k).astype(np.float32)
-        x = rng.standard_normal(DIM).astype(np.float32)
-        t0 = time.perf_counter()
-        rows = np.stack([impl.expert(ptypes[e], *mats[e], DIM, FF, x, threads=threads) for e in ids])
-        impl.combine(ids, w, rows, np.zeros(DIM, np.float32)) if kind == "reference" else orc.combine(ids, w, rows)
-        elapsed += time.perf_counter() - t0
-        nbytes += sum(expert_bytes(ptypes[e]) for e in ids) + 2 * DIM * 4
-    us = elapsed / layers * 1e6
+    draws = [(rng.choice(pool, size=k, replace=False).astype(np.int32), rng.random(k).astype(np.float32),
+              rng.standard_normal(DIM).astype(np.float32)) for _ in range(64)]
+    avx2 = orc.lane_avx2()
+
+    def run(n_threads, seconds, min_reps=5):
+        """2 warm-up layers, then layers until `seconds` (at least min_reps)."""
+        times, phases, nbytes = [], np.zeros(5, np.float64), 0
+        for i in range(2):
+            ids, w, x = draws[i]
+            orc.lane_layer([ptypes[e] for e in ids], [mats[e] for e in ids], ids, w, x, DIM, FF, threads=n_threads)
+        t_end = time.perf_counter() + seconds
+        i = 0
+        while len(times) < min_reps or time.perf_counter() < t_end:
+            ids, w, x = draws[(2 + i) % len(draws)]
+            i += 1
+            t0 = time.perf_counter()
+            orc.lane_layer([ptypes[e] for e in ids], [mats[e] for e in ids], ids, w, x, DIM, FF, threads=n_threads,
+                           phases=phases)
+            times.append(time.perf_counter() - t0)
+            nbytes += sum(expert_bytes(ptypes[e]) for e in ids) + 2 * DIM * 4
+        t = np.array(times)
+        return {"us_per_layer": round(float(np.median(t)) * 1e6, 1), "us_min": round(float(t.min()) * 1e6, 1),
+                "us_max": round(float(t.max()) * 1e6, 1), "layers": len(t),
+                "GB_s": round(nbytes / t.sum() / 1e9, 3),
+                "phases_us": dict(zip(("q1", "gate_up", "q2", "down", "combine"),
+                                      (phases / len(t) / 1e3).round(1).tolist()))}
+
+    per = {}
+    if avx2:
+        for n in workers:
+            per[str(n)] = run(n, budget_s * (0.35 if n == 1 else 0.5 / max(1, len(workers) - 1)))
+    best = str(workers[-1])
+    # The reference's own scalar chain (q8k_core.hpp compiled from /root/reference), a few layers
+    scalar = None
+    if Reference.available():
+        ref = Reference()
+        t_all, nb, n_l = 0.0, 0, 0
+        t_end = time.perf_counter() + budget_s * 0.15
+        while n_l < 2 or time.perf_counter() < t_end:
+            ids, w, x = draws[n_l % len(draws)]
+            t0 = time.perf_counter()
+            rows = np.stack([ref.expert(ptypes[e], *mats[e], DIM, FF, x, threads=share) for e in ids])
+            ref.combine(ids, w, rows, np.zeros(DIM, np.float32))
+            t_all += time.perf_counter() - t0
+            nb += sum(expert_bytes(ptypes[e]) for e in ids) + 2 * DIM * 4
+            n_l += 1
+        scalar = {"kind": "reference", "GB_s": round(nb / t_all / 1e9, 3), "us_per_layer": round(t_all / n_l * 1e6, 1),
+                  "threads": share, "layers": n_l,
+                  "what": "the reference's own scalar q8k_core.hpp chain (oracle/_ref), 64-row jobs"}
+    if not avx2:   # no AVX2 on this host: the scalar reference chain is the baseline
+        return {"value": scalar["GB_s"] if scalar else None, "unit": "GB/s", "cores": share,
+                "kind": "reference", "host": host, "sample": "host without AVX2: scalar reference chain only",
+                "scalar_reference": scalar}
+    top = per[best]
     return {
-        "value": round(nbytes / elapsed / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": kind,
-        "us_per_layer": round(us, 1),
-        "sample": f"{layers} config-{config} layers ({k} expert(s) + combine each, drawn from {pool} generated "
-                  f"experts), {'reference q8k_core.hpp chain from oracle/_ref' if kind == 'reference' else 'oracle port'}, "
-                  f"{threads} threads, {elapsed:.1f} s timed",
+        "value": top["GB_s"], "unit": "GB/s", "cores": int(best), "kind": "port",
+        "us_per_layer": top["us_per_layer"], "us_min": top["us_min"], "us_max": top["us_max"],
+        "phases_us": top["phases_us"],
+        "sample": f"{top['layers']} config-{config} layers ({k} expert(s) + combine each, drawn from {pool} generated "
+                  f"experts) on the AVX2 restatement of the reference CPU lane (oracle/cpu_lane.c, bit-identical to "
+                  f"the scalar restatement), {best} workers in 64-row jobs (the box's CPU share; physical cores "
+                  f"{host['physical_cores']}, logical {host['logical_cpus']}), median of the timed layers",
+        "workers": per,
+        "host": dict(host, isa_used="AVX2 + FMA (256-bit)", box_share=share,
+                     compiler="gcc -O2 -mfma -mavx2 -fopenmp -ffp-contract=off -fno-fast-math"),
+        "scalar_reference": scalar,
     }
 
 
@@ -190,8 +272,8 @@ def main():
                     help="configs 0-2: the per32 mode (the reference's production HIP lane arithmetic) "
                          "instead of the Q8_K chain")
     ap.add_argument("--routes", type=int, default=512)
-    ap.add_argument("--cpu-layers", type=int, default=0)
-    ap.add_argument("--cpu-threads", type=int, default=0)
+    ap.add_argument("--cpu-seconds", type=float, default=12.0, help="CPU baseline time budget")
+    ap.add_argument("--cpu-threads", type=int, default=0, help="CPU baseline worker cap (default: the box's share)")
     ap.add_argument("--no-cpu", action="store_true")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -359,10 +441,8 @@ def main():
 
     cpu = None
     if not args.no_cpu and not args.per32 and cfg != 5:   # the CPU baseline times the Q8_K chain
-        threads = args.cpu_threads or min(16, os.cpu_count() or 1)
-        cpu_layers = args.cpu_layers or {0: 1500, 1: 500, 2: 500, 3: 500, 4: 500}[cfg]
-        cpu = cpu_baseline(cpu_layers, threads, config=1 if cfg == 4 else cfg)
-        if cfg == 4:   # the CPU chain has no grouping: TOK per-token layers per step
+        cpu = cpu_baseline(args.cpu_seconds, config=1 if cfg == 4 else cfg, max_threads=args.cpu_threads)
+        if cfg == 4 and cpu["value"] is not None:   # the CPU lane has no grouping: TOK per-token layers per step
             cpu["value"] = round(bytes_per_step / (cpu["us_per_layer"] * 1e-6 * TOK) / 1e9, 3)
             cpu["sample"] += f"; per step = {TOK} such token layers (algorithmic bytes of the grouped step)"
 

@@ -47,6 +47,11 @@ class Oracle:
         L.orc_block_partials.argtypes = [C.c_int, _u8p, _P, C.c_int, _i32p]
         L.orc_integer_lane.argtypes = [C.c_int, _u8p, _P, C.c_int, C.POINTER(C.c_int32), C.POINTER(C.c_int32)]
         L.orc_matrix_ints.argtypes = [C.c_int, _u8p, C.c_int, C.c_int, _P, _i32p, C.c_int]
+        L.orc_lane_avx2.restype = C.c_int
+        L.orc_lane_dot.argtypes = [C.c_int, _u8p, _P, C.c_int]
+        L.orc_lane_dot.restype = C.c_float
+        L.orc_lane_layer.argtypes = [C.c_int, _i32p, _P, C.c_int, C.c_int, _f32p, _i32p, _f32p, _f32p, C.c_float,
+                                     C.c_int, np.ctypeslib.ndpointer(np.float64, flags="C_CONTIGUOUS")]
         L.orc_brute_block.argtypes = [C.c_int, _u8p, _P]
         L.orc_brute_block.restype = C.c_int64
         L.orc_matvec.argtypes = [C.c_int, _u8p, C.c_int, C.c_int, _P, _f32p, C.c_int]
@@ -102,6 +107,28 @@ class Oracle:
         assert act.size == k // 256
         out = np.zeros((n, k // 256), np.int32)
         self.lib.orc_matrix_ints(t, np.ascontiguousarray(w).reshape(-1), n, k, act.ctypes.data, out.reshape(-1), threads)
+        return out
+
+    # -- the AVX2 CPU lane (cpu_lane.c) ----------------------------------
+    def lane_avx2(self) -> bool:
+        return bool(self.lib.orc_lane_avx2())
+
+    def lane_dot(self, t: int, row: np.ndarray, act: np.ndarray) -> float:
+        return float(self.lib.orc_lane_dot(t, np.ascontiguousarray(row), act.ctypes.data, act.size))
+
+    def lane_layer(self, types, mats, ids, w, x, dim, ff, threads=1, limit=0.0, phases=None):
+        """One routed layer on the AVX2 lane: types [k, 3], mats a list of k
+        (gate, up, down) AoS arrays; phases (5 float64, added to): q1, gate_up,
+        q2, down, combine ns."""
+        k = len(ids)
+        t = np.ascontiguousarray(types, dtype=np.int32).reshape(-1)
+        flat = [np.ascontiguousarray(m) for tri in mats for m in tri]
+        ptrs = (C.c_void_p * (3 * k))(*[m.ctypes.data for m in flat])
+        out = np.zeros(dim, np.float32)
+        ph = phases if phases is not None else np.zeros(5, np.float64)
+        self.lib.orc_lane_layer(k, t, C.cast(ptrs, C.c_void_p), dim, ff, np.ascontiguousarray(x, dtype=np.float32),
+                                np.ascontiguousarray(ids, dtype=np.int32), np.ascontiguousarray(w, dtype=np.float32),
+                                out, float(limit), int(threads), ph)
         return out
 
     def integer_lane(self, t: int, block: np.ndarray, act_block: np.ndarray, lane: int):

@@ -20,6 +20,8 @@
  *   sycl/moe/core.hpp:9-12,17,47-65,80       per32 rows of the dense shared-expert
  *                                           formats (Q8_0, Q4_K, Q5_K, Q6_K)
  *   sycl/hc/core.hpp:81-86                   hyper-connection post
+ *   sycl/moe/cpu_lane.cpp:70-81,157-170      the AVX2 CPU lane (cpu_lane.c): 64-row
+ *                                           jobs, phases q1 / gate_up / q2 / down
  *
  * Parity pins (see tests/): every function here is checked against
  * oracle/_ref (the reference's own q8k_core.hpp / core.hpp / other_combine.hpp
@@ -101,6 +103,15 @@ void orc_gen_matrix(int type, uint64_t seed, uint32_t layer, uint32_t expert, ui
 /* Expanded codebooks (u64 rows) and the ksigns table, for table checks. */
 void orc_codebook(int which, uint64_t* out); /* 0: iq2xxs[256] 1: iq2xs[512] 2: iq1s[2048] */
 uint8_t orc_ksigns(int i);
+
+/* AVX2 CPU lane (cpu_lane.c, the CPU baseline): 1 when the host has AVX2 and
+ * FMA; one row dot bit-identical to orc_dot; one routed layer in the reference
+ * CPU lane's phases (q1, gate_up, q2, down, combine nanoseconds added to
+ * phase_ns[0..4]) over `threads` workers in 64-row jobs. */
+int orc_lane_avx2(void);
+float orc_lane_dot(int type, const uint8_t* w, const orc_q8k* a, int nb);
+void orc_lane_layer(int k, const int* types, const uint8_t* const* mats, int dim, int ff, const float* x,
+                    const int32_t* ids, const float* w, float* out, float limit, int threads, double* phase_ns);
 
 /* Hyper-connection post (sycl/hc/core.hpp:81-86) of T tokens, H streams of D. */
 void orc_hc_post(const float* y, const float* res, const float* post, const float* comb, int D, int H, int T, float* out);

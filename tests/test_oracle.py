@@ -139,6 +139,44 @@ def test_matrix_ints_brute_force(orc, t, rng):
 
 
 @pytest.mark.parametrize("t", [16, 17, 29])
+def test_avx2_lane_rows_bit_identical(orc, t, rng):
+    # The CPU baseline's AVX2 rows (cpu_lane.c) against the scalar AVX2-order
+    # restatement, bit for bit, on generated rows and golden activations.
+    if not orc.lane_avx2():
+        pytest.skip("host without AVX2 + FMA")
+    gold = np.load(os.path.join(os.path.dirname(__file__), "golden", "reference_vectors.npz"))
+    k = 1024
+    w = orc.gen_matrix(t, 21, 0, t, 1, 24, k)
+    rb = (k // 256) * BLOCK_BYTES[t]
+    acts = [orc.quantize(rng.standard_normal(k).astype(np.float32) * s) for s in (1e-3, 1.0, 1e3)]
+    acts.append(orc.quantize(np.resize(gold["q8k_x"].reshape(-1), k).astype(np.float32)))
+    for act in acts:
+        for r in range(24):
+            row = w[r * rb:(r + 1) * rb]
+            assert np.float32(orc.lane_dot(t, row, act)).view(np.uint32) == np.float32(orc.dot(t, row, act)).view(np.uint32)
+
+
+def test_avx2_lane_layer_bit_identical(orc, rng):
+    # One routed layer on the AVX2 lane (threads, 64-row jobs, phases) equals the
+    # scalar oracle's expert chain + fixed-order combine bit for bit.
+    if not orc.lane_avx2():
+        pytest.skip("host without AVX2 + FMA")
+    dim, ff = 1024, 768
+    sigs = [(16, 16, 17), (29, 29, 29), (17, 17, 16)]
+    ids = np.array([5, 2, 9], np.int32)
+    w = np.array([0.5, 0.3, 0.2], np.float32)
+    x = rng.standard_normal(dim).astype(np.float32)
+    mats = [orc.gen_expert(s, 3, 0, int(e), dim, ff) for s, e in zip(sigs, ids)]
+    for limit in (0.0, 7.0):
+        ph = np.zeros(5, np.float64)
+        got = orc.lane_layer(np.array(sigs), mats, ids, w, x, dim, ff, threads=3, limit=limit, phases=ph)
+        rows = np.stack([orc.expert(s, *m, dim, ff, x, limit=limit) for s, m in zip(sigs, mats)])
+        want = orc.combine(ids, w, rows)
+        assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+        assert np.all(ph[:4] > 0)
+
+
+@pytest.mark.parametrize("t", [16, 17, 29])
 def test_brute_force_vs_reference_decoder(orc, ref, t, rng):
     # Reference per-32 decoder (sycl/moe/core.hpp): values and odd sub-scales.
     w = orc.gen_matrix(t, 11, 1, 2, 0, 4, 256)

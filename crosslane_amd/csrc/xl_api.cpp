@@ -151,18 +151,21 @@ struct xl_context {
     xl::ExpertDesc* d_descs = nullptr;
     uint64_t payload = 0, allocated = 0;
     int grid_gu = 0, grid_down = 0;
-    // Layer path: 1 = single launch (default: the streaming kernel of
-    // xl_stream.hip for IQ2_XXS gate/up + IQ2_XS down layers, else the
-    // all-types kernel of xl_layer.hip), 3 = the all-types single launch only,
-    // 2 = cooperative fused kernel, 0 = separate launches, 4 = the streaming
-    // kernel only (a layer it cannot run is an error). XL_LAYER_PATH selects;
-    // shapes without a single-launch instance use separate launches.
+    // Layer path: 1 = single launch (default: for IQ2_XXS gate/up + IQ2_XS down
+    // layers the unit kernel of xl_unit.hip, else the streaming kernel of
+    // xl_stream.hip; other layers the all-types kernel of xl_layer.hip), 3 = the
+    // all-types single launch only, 2 = cooperative fused kernel, 0 = separate
+    // launches, 4 = the streaming kernel only, 5 = the unit kernel only (a layer
+    // they cannot run is an error). XL_LAYER_PATH selects; shapes without a
+    // single-launch instance use separate launches.
     int path = 1;
     // Grouped path: 1 = the MFMA kernels where the layer's types allow, else one
     // layer call per token (default); 0 = per-token calls only; 2 = the MFMA
     // kernels only (a layer they cannot run is an error). XL_GROUPED_PATH selects.
     int gpath = 1;
     float* hbuf = nullptr;      // streaming kernel's h exchange (2 x kHBufWords, sentinel-filled)
+    float* part = nullptr;      // unit kernel's down partials (max_picks * ff/256 units x dim floats)
+    uint32_t* ucnt = nullptr;   // unit kernel's partial counters (2 x 256 words, zeroed at open)
     // grouped path (xl_grouped.hip), sized by max_tokens * max_picks pairs
     struct Group {
         int32_t* ids = nullptr; float* w = nullptr; float* x = nullptr; float* shared = nullptr; float* out = nullptr;
@@ -338,7 +341,7 @@ bool enqueue_layer(xl_context* ctx, int32_t layer, const int32_t* d_ids, const f
     const int gu_mask = ctx->gu_mask[size_t(layer)], dn_mask = ctx->dn_mask[size_t(layer)];
     Marks mark(ctx, s);
     mark("");
-    if ((ctx->path == 1 || ctx->path == 3 || ctx->path == 4) && !g_dbg && !u_dbg) {
+    if ((ctx->path == 1 || ctx->path == 3 || ctx->path == 4 || ctx->path == 5) && !g_dbg && !u_dbg) {
         xl::Layer3Args a{};
         a.descs = descs; a.ids = d_ids; a.w = d_w; a.x = d_x; a.shared = d_shared; a.out = d_out;
         a.k = k; a.n_experts = E; a.dim = dim; a.ff = ff;
@@ -346,6 +349,8 @@ bool enqueue_layer(xl_context* ctx, int32_t layer, const int32_t* d_ids, const f
         a.lim = ctx->cfg.swiglu_limit;
         a.tables = ctx->tables;
         a.hbuf = ctx->hbuf;
+        a.part = ctx->part;
+        a.ucnt = ctx->ucnt;
         if (ctx->prof.on && ctx->prof.calls <= ctx->prof.max_calls) {
             a.trace = ctx->timeline;
             hip_check(hipMemsetAsync(ctx->timeline, 0, size_t(ctx->cus) * 16 * 32 * 8, s), "timeline clear");
@@ -359,13 +364,20 @@ bool enqueue_layer(xl_context* ctx, int32_t layer, const int32_t* d_ids, const f
         }
         if (d_out) {
             hipError_t e = hipErrorNotSupported;
-            if ((ctx->path == 1 || ctx->path == 4) && gu_mask == 1 && dn_mask == 2) {
+            if (ctx->path == 5 && gu_mask == 1 && dn_mask == 2) {
+                e = xl::dev::launch_unit(a, ctx->cus, s, stop);
+                if (e != hipSuccess && e != hipErrorNotSupported) hip_check(e, "unit layer");
+                (void)hipGetLastError();
+                if (tr && e == hipSuccess) tr->kernel = 5;
+            }
+            need(ctx->path != 5 || e == hipSuccess, XL_E_ARG, "XL_LAYER_PATH=5: no unit-kernel instance for this layer");
+            if ((ctx->path == 1 || ctx->path == 4) && e == hipErrorNotSupported && gu_mask == 1 && dn_mask == 2) {
                 e = xl::dev::launch_stream(a, ctx->cus, s, stop);
                 if (e != hipSuccess && e != hipErrorNotSupported) hip_check(e, "streaming layer");
                 (void)hipGetLastError();
+                if (tr && e == hipSuccess) tr->kernel = 1;
             }
             need(ctx->path != 4 || e == hipSuccess, XL_E_ARG, "XL_LAYER_PATH=4: no streaming-kernel instance for this layer");
-            if (tr && e == hipSuccess) tr->kernel = 1;
             if (e == hipErrorNotSupported) {
                 e = xl::dev::launch_layer3(a, gu_mask, dn_mask, ctx->cus, s, stop);
                 if (tr && e == hipSuccess) tr->kernel = 3;
@@ -549,6 +561,8 @@ int32_t xl_open(uint32_t abi_version, const xl_config* cfg, xl_context** out, xl
             {reinterpret_cast<void**>(&ctx->hdtag), uint64_t(P) * (ff / 256) * 8},
             {reinterpret_cast<void**>(&ctx->ctl), 256},
             {reinterpret_cast<void**>(&ctx->hbuf), uint64_t(2) * xl::kHBufWords * 4},
+            {reinterpret_cast<void**>(&ctx->part), uint64_t(P) * (ff / 256) * dim * 4},
+            {reinterpret_cast<void**>(&ctx->ucnt), 2 * 256 * 4},
             {reinterpret_cast<void**>(&ctx->tables), uint64_t(xl::kLayer3TableBytes)},
             {reinterpret_cast<void**>(&ctx->p32d), (uint64_t(ctx->act_max / 32) + uint64_t(P) * (ff / 32)) * 4},
             {reinterpret_cast<void**>(&ctx->timeline), uint64_t(ctx->cus) * 16 * 32 * 8},
@@ -598,13 +612,14 @@ int32_t xl_open(uint32_t abi_version, const xl_config* cfg, xl_context** out, xl
         hip_check(hipMemset(ctx->hdtag, 0, size_t(P) * (ff / 256) * 8), "tag clear");
         hip_check(hipMemset(ctx->hqtag, 0, size_t(P) * ff * 2), "tag clear");
         hip_check(hipMemset(ctx->ctl, 0, 256), "epoch clear");
+        hip_check(hipMemset(ctx->ucnt, 0, 2 * 256 * 4), "unit counter clear");
         hip_check(hipMemset(ctx->hbuf, 0xff, size_t(2) * xl::kHBufWords * 4), "h exchange fill");
         const std::vector<uint64_t> tab = layer_tables();
         hip_check(hipMemcpy(ctx->tables, tab.data(), tab.size() * 8, hipMemcpyHostToDevice), "table upload");
         void* scratch = nullptr;   // the no-allocation scratch's address on this device, looked up once
         hip_check(xl::dev::noalloc_scratch(cfg->device, &scratch), "no-allocation scratch address");
         ctx->path = env_int("XL_LAYER_PATH", 1);
-        need(ctx->path >= 0 && ctx->path <= 4, XL_E_ARG, "XL_LAYER_PATH must be 0, 1, 2, 3 or 4");
+        need(ctx->path >= 0 && ctx->path <= 5, XL_E_ARG, "XL_LAYER_PATH must be 0, 1, 2, 3, 4 or 5");
         ctx->gpath = env_int("XL_GROUPED_PATH", 1);
         need(ctx->gpath >= 0 && ctx->gpath <= 2, XL_E_ARG, "XL_GROUPED_PATH must be 0, 1 or 2");
         *out = ctx;
@@ -1553,6 +1568,8 @@ int32_t xl_debug_set_launch_count(xl_context* ctx, uint32_t launches, xl_error* 
         // count (its parity); the arrival counters ctl[1], ctl[3] are zero between launches.
         const uint32_t w[4] = {launches, 0u, launches, 0u};
         hip_check(hipMemcpyAsync(ctx->ctl, w, sizeof w, hipMemcpyHostToDevice, s), "launch count upload");
+        // the unit kernel's partial counters of both parities start from zero again
+        hip_check(hipMemsetAsync(ctx->ucnt, 0, 2 * 256 * 4, s), "unit counter clear");
         hip_check(hipStreamSynchronize(s), "launch count drain");
     });
 }

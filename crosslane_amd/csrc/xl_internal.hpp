@@ -102,6 +102,8 @@ struct Layer3Args {
     uint8_t* tq8h;
     float* th;
     int32_t* tint;
+    float* part;                // unit kernel: per (pick, h block) unit, dim float partials of the down rows
+    uint32_t* ucnt;             // unit kernel: 2 sets (launch parity) of 8 partial counters, 32 words apart (2 x 256 words)
 };
 constexpr int kHBufWords = 16 * 4096;      // k_max * ff_max
 
@@ -159,6 +161,9 @@ hipError_t launch_layer3(const Layer3Args& args, int gu_types, int dn_types, int
 // Streaming layer for IQ2_XXS gate/up + IQ2_XS down: hipErrorNotSupported when
 // (dim, ff, k) has no instance.
 hipError_t launch_stream(const Layer3Args& args, int cus, hipStream_t s, hipEvent_t stop = nullptr);
+// Unit layer (xl_unit.hip) for IQ2_XXS gate/up + IQ2_XS down: hipErrorNotSupported
+// when (dim, ff, k) has no instance.
+hipError_t launch_unit(const Layer3Args& args, int cus, hipStream_t s, hipEvent_t stop = nullptr);
 // Grouped path: hipErrorNotSupported unless gate/up are IQ2_XXS, down IQ2_XS and
 // the shapes fit (dim, ff multiples of 128; n_experts <= kGroupMaxExperts).
 hipError_t launch_grouped(const GroupArgs& args, int cus, hipStream_t s);

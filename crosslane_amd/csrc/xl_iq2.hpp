@@ -1,0 +1,236 @@
+// IQ2 row decoding of the streaming layer kernels (xl_stream.hip, xl_unit.hip),
+// gfx950: perm-addressed, bank-interleaved LDS codebook copies, sign masks
+// applied to the activations (IQ2_XXS) or to the grid (IQ2_XS), the Q8_K
+// quantizer of several blocks at once, and the sentinel h exchange words.
+#pragma once
+#include <hip/hip_runtime.h>
+
+#include <utility>
+
+#include "xl_dev.hpp"
+
+namespace xl::dev {
+namespace {
+
+// f.template operator()<J>() for J = 0 .. N-1: the index is a constant in the
+// body, so ring slots indexed by it stay in registers (a runtime loop index,
+// even of a loop unrolled later, leaves them to memory).
+template <int N, class F>
+__device__ __forceinline__ void static_for(F&& f) {
+    [&]<int... Js>(std::integer_sequence<int, Js...>) { (f.template operator()<Js>(), ...); }(std::make_integer_sequence<int, N>{});
+}
+
+// Lane constants of the lookups: byte 0 is the lane's copy offset, byte 2 the
+// table base in 64-KB units; v_perm_b32 puts the index byte in byte 1.
+__device__ __forceinline__ uint32_t perm(uint32_t idx_word, uint32_t lane_word, uint32_t sel) {
+    return __builtin_amdgcn_perm(idx_word, lane_word, sel);
+}
+// selector: byte0 <- lane_word.byte0, byte1 <- idx_word.byte(q), byte2 <- lane_word.byte2, byte3 <- 0
+__device__ __forceinline__ constexpr uint32_t sel_b(int q) { return 0x0C020400u + (uint32_t(q) << 8); }
+
+constexpr uint32_t kSentinel = 0xffffffffu;
+constexpr uint32_t kQNaN = 0x7fc00000u;
+
+// Sign row r: M has 0xff in the bytes of negative weights (7 sign bits of r
+// plus their parity, as ksigns_iq2xs). Two ways to apply it, one op per dword:
+// select between a and -a (v_bfi_b32: the activation takes the sign), or
+// (g ^ M) + (M & 0x01010101), which negates exactly those bytes of g (grid
+// bytes are 1..127, so no carry crosses a byte).
+__device__ __forceinline__ uint2 sign_row(uint32_t r) {
+    const uint32_t s7 = r & 127u;
+    const uint32_t s8 = s7 | ((__builtin_popcount(s7) & 1u) << 7);
+    const uint32_t clo = ((s8 & 15u) * 0x00204081u) & 0x01010101u;
+    const uint32_t chi = ((s8 >> 4) * 0x00204081u) & 0x01010101u;
+    return make_uint2(clo * 255u, chi * 255u);
+}
+__device__ __forceinline__ uint32_t bfi(uint32_t m, uint32_t x, uint32_t y) { return (m & x) | (~m & y); }   // v_bfi_b32
+// Bytewise two's-complement negation: (~x + 1) per byte = (x ^ 0xff..) + 0x01.. with no
+// carry across bytes except for a 0x00 byte, whose carry is masked off byte by byte.
+__device__ __forceinline__ uint32_t neg_bytes(uint32_t x) {
+    const uint32_t lo = ((x & 0x00ff00ffu) ^ 0x00ff00ffu) + 0x00010001u;   // bytes 0, 2 (a carry lands in 1, 3)
+    const uint32_t hi = ((x & 0xff00ff00u) ^ 0xff00ff00u) + 0x01000100u;   // bytes 1, 3
+    return (lo & 0x00ff00ffu) | (hi & 0xff00ff00u);
+}
+
+// ---- pair decoders -------------------------------------------------------------------------
+// Codebook rows of one pair: 8 grid rows and 8 sign masks. The decoders are
+// split into lookups and arithmetic so that a slot issues both of its rows'
+// lookups before either row's arithmetic waits on them.
+struct Looks {
+    uint2 g[8], m[8];
+};
+// IQ2_XXS pair (w0..3: two sub-blocks of {4 grid bytes, 4 sign|scale-bit bytes}).
+__device__ __forceinline__ Looks look_xxs(const uint8_t* lds, uint32_t lo_g, uint32_t lo_s, const uint32_t* w) {
+    Looks L;
+#pragma unroll
+    for (int s = 0; s < 2; ++s)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            L.g[4 * s + q] = *reinterpret_cast<const uint2*>(lds + perm(w[2 * s], lo_g, sel_b(q)));
+            L.m[4 * s + q] = *reinterpret_cast<const uint2*>(lds + perm(w[2 * s + 1], lo_s, sel_b(q)));
+        }
+    return L;
+}
+// Against 64 Q8_K quants a (and their negations na): the exact integer sum of
+// (2s+1) * grid * sign * q over the pair (q8k_core.hpp:96-114 regrouped per
+// sub-block; the sign is applied to q).
+__device__ __forceinline__ int sum_xxs(const Looks& L, const uint32_t* w, const uint32_t* a, const uint32_t* na) {
+    int acc[2] = {0, 0};
+#pragma unroll
+    for (int s = 0; s < 2; ++s)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const int e = 4 * s + q, k0 = 8 * s + 2 * q;
+            acc[s] = sdot4(L.g[e].x, bfi(L.m[e].x, na[k0], a[k0]), acc[s]);
+            acc[s] = sdot4(L.g[e].y, bfi(L.m[e].y, na[k0 + 1], a[k0 + 1]), acc[s]);
+        }
+    return __mul24(acc[0], xxs_sc(w[1])) + __mul24(acc[1], xxs_sc(w[3]));
+}
+// IQ2_XS pair (w0..3: 8 codes {sign7 | grid9 << 7}, sc: the pair's two scale
+// bytes): the exact integer sum with the 16-weight scales (q8k_core.hpp:116-140).
+// Split like the IQ2_XXS decoder, so that a pass issues the next pair's
+// lookups before the current pair's arithmetic waits on its own.
+__device__ __forceinline__ Looks look_xs(const uint8_t* lds, uint32_t lo_x, uint32_t lo_s, const uint32_t* w) {
+    Looks L;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+        const uint32_t h = e & 1;
+        // grid row * 32 = (code >> 7) << 5: one shift and one v_and_or_b32 with the lane's copy
+        const uint32_t sh = h ? (w[e >> 1] >> 18) : (w[e >> 1] >> 2);
+        L.g[e] = *reinterpret_cast<const uint2*>(lds + ((sh & 0x3fe0u) | lo_x));
+        L.m[e] = *reinterpret_cast<const uint2*>(lds + perm(w[e >> 1], lo_s, sel_b(2 * h)));
+    }
+    return L;
+}
+__device__ __forceinline__ int sum_xs(const Looks& L, uint32_t sc, const uint32_t* a) {
+    int total = 0;
+#pragma unroll
+    for (int s = 0; s < 2; ++s) {
+        int lo = 0, hi = 0;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const int e = 4 * s + q;
+            int& acc = q < 2 ? lo : hi;
+            acc = sdot4(xad(L.g[e].x, L.m[e].x, L.m[e].x & 0x01010101u), a[8 * s + 2 * q], acc);
+            acc = sdot4(xad(L.g[e].y, L.m[e].y, L.m[e].y & 0x01010101u), a[8 * s + 2 * q + 1], acc);
+        }
+        const uint32_t byte = (sc >> (8 * s)) & 255u;
+        total += __mul24(lo, int(2u * (byte & 15u) + 1u)) + __mul24(hi, int(2u * (byte >> 4) + 1u));
+    }
+    return total;
+}
+
+template <int P>
+struct Act {
+    uint32_t a[P][16];
+    float d[P];
+};
+// Activations of pairs lp, lp + L, ... from a Q8_K vector in LDS (quants at
+// base, block scales at base + scl).
+template <int P>
+__device__ __forceinline__ void load_act(Act<P>& A, const uint8_t* lds, int base, int scl, int lp, int L) {
+#pragma unroll
+    for (int q = 0; q < P; ++q) {
+        const int p = lp + L * q;
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+            const uint4 v = *reinterpret_cast<const uint4*>(lds + base + qswz(64 * p + 16 * c));
+            A.a[q][4 * c] = v.x; A.a[q][4 * c + 1] = v.y; A.a[q][4 * c + 2] = v.z; A.a[q][4 * c + 3] = v.w;
+        }
+        A.d[q] = reinterpret_cast<const float*>(lds + base + scl)[p >> 2];
+    }
+}
+
+// Coherent (sc1) 16-byte load of 4 h words; a sentinel word means "not yet".
+__device__ __forceinline__ uint4 h_load(const float* hb, uint32_t word) {
+    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc((void*)hb, (short)0, -1, 0x00020000);
+    const v4u32 v = __builtin_amdgcn_raw_buffer_load_b128(rs, word * 4, 0, 16);   // per-lane offset: voffset
+    return make_uint4(v.x, v.y, v.z, v.w);
+}
+__device__ __forceinline__ bool h_ready(const uint4& v) {
+    return (v.x != kSentinel) & (v.y != kSentinel) & (v.z != kSentinel) & (v.w != kSentinel);
+}
+
+// ---- Q8_K of NB blocks at once ---------------------------------------------------------------
+// Block m is held by the wave as v[m] (lane l owns values 4l..4l+3). Bit-exact
+// with q8k_core.hpp:30-38: mx is the first value of largest magnitude (found
+// as the wave's largest magnitude, then the lowest position holding it), is =
+// -127/mx, q = min(127, nearest(is * v)), d = 1/is; an all-zero block gives
+// d = 0 and q = 0. The two divisions run once for all NB blocks (lane m
+// divides for block m); nearest is v_rndne (exact for |is * v| < 2^22) and
+// the quants are packed as q + 128 bytes by v_cvt_pk_u8_f32 (exact integers).
+// One DPP max step on every block at once: the NB chains are independent, so
+// each fills the others' DPP wait states. old = 0 is max's identity, which lets
+// the compiler fold the move into v_max_u32_dpp.
+template <int CTRL, int RM, int NB>
+__device__ __forceinline__ void umax_dpp_n(uint32_t (&a)[NB]) {
+#pragma unroll
+    for (int m = 0; m < NB; ++m) a[m] = max(a[m], uint32_t(__builtin_amdgcn_update_dpp(0, int(a[m]), CTRL, RM, 0xF, false)));
+}
+// The wave's largest magnitude of each block, as a bit pattern: magnitudes of
+// floats order as their bits do, so integer max needs no NaN canonicalization
+// (a NaN or an infinity wins and is caught by the finiteness test on the result).
+template <int NB>
+__device__ __forceinline__ void wave_umax_n(uint32_t (&a)[NB], uint32_t (&out)[NB]) {
+    umax_dpp_n<0xB1, 0xF>(a);
+    umax_dpp_n<0x4E, 0xF>(a);
+    umax_dpp_n<0x141, 0xF>(a);
+    umax_dpp_n<0x140, 0xF>(a);   // every lane: its row's max
+    umax_dpp_n<0x142, 0xA>(a);   // rows 1, 3
+    umax_dpp_n<0x143, 0xC>(a);   // rows 2, 3
+#pragma unroll
+    for (int m = 0; m < NB; ++m) out[m] = uint32_t(__builtin_amdgcn_readlane(int(a[m]), 63));
+}
+// Returns false if a value of blocks 0..nvalid-1 is not finite (the others may hold anything).
+// |is * v| <= 127 (1 + 2^-24)^2 < 127.5 for every v of the block, so nearest(is * v)
+// never exceeds 127 and the reference's min(127, .) never applies.
+template <int NB>
+__device__ __forceinline__ bool q8k_blocks(const uint4 (&hv)[NB], int nvalid, int lane, uint32_t (&packed)[NB],
+                                           float (&d)[NB]) {
+    bool fin = true;
+    uint32_t x[NB][4], ab[NB][4], am[NB], mxa[NB];
+#pragma unroll
+    for (int m = 0; m < NB; ++m) {
+        // opaque copies: a select chain over the block's words would otherwise be
+        // turned into an indexed load from a stack copy of the block
+        x[m][0] = hv[m].x; x[m][1] = hv[m].y; x[m][2] = hv[m].z; x[m][3] = hv[m].w;
+        asm volatile("" : "+v"(x[m][0]), "+v"(x[m][1]), "+v"(x[m][2]), "+v"(x[m][3]));
+#pragma unroll
+        for (int i = 0; i < 4; ++i) ab[m][i] = x[m][i] & 0x7fffffffu;
+        mxa[m] = max(max(ab[m][0], ab[m][1]), max(ab[m][2], ab[m][3]));
+    }
+    wave_umax_n<NB>(mxa, am);
+    float mxv = 0.0f;
+#pragma unroll
+    for (int m = 0; m < NB; ++m) {
+        fin = fin & ((m >= nvalid) | (am[m] <= 0x7f7fffffu));
+        // mx: the magnitude am[m] with the sign of the block's first value of that
+        // magnitude (the lane's first match by a bit scan, the wave's by a ballot;
+        // integer ops only, no select over the block's words)
+        const uint32_t hm = uint32_t(ab[m][0] == am[m]) | (uint32_t(ab[m][1] == am[m]) << 1) |
+                            (uint32_t(ab[m][2] == am[m]) << 2) | (uint32_t(ab[m][3] == am[m]) << 3);
+        const uint32_t sg = (x[m][0] >> 31) | ((x[m][1] >> 31) << 1) | ((x[m][2] >> 31) << 2) | ((x[m][3] >> 31) << 3);
+        const uint32_t sb = (sg >> __builtin_ctz(hm | 16u)) & 1u;
+        const uint64_t hit = __builtin_amdgcn_ballot_w64(hm != 0u);
+        const int first = int(__builtin_ctzll(hit | (uint64_t(1) << 63)));
+        const float mx = __uint_as_float(am[m] | (uint32_t(__builtin_amdgcn_readlane(int(sb), first)) << 31));
+        mxv = lane == m ? mx : mxv;
+    }
+    const float isv = __fdiv_rn(-127.0f, mxv);
+    const float dv = __fdiv_rn(1.0f, isv);
+#pragma unroll
+    for (int m = 0; m < NB; ++m) {
+        const float is = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(isv), m));
+        uint32_t p = 0;
+#pragma unroll
+        for (int j = 0; j < 4; ++j)   // q + 128 in 1..255, an exact integer: the byte conversion is exact
+            p = __builtin_amdgcn_cvt_pk_u8_f32(__fadd_rn(__builtin_rintf(__fmul_rn(is, __uint_as_float(x[m][j]))), 128.0f), j, p);
+        const bool zero = am[m] == 0u;
+        packed[m] = zero ? 0u : p ^ 0x80808080u;
+        d[m] = zero ? 0.0f : __int_as_float(__builtin_amdgcn_readlane(__float_as_int(dv), m));
+    }
+    return fin;
+}
+
+}  // namespace
+}  // namespace xl::dev

@@ -21,7 +21,7 @@ from tests.test_gpu_parity import TOL, dev, route, step, types_map
 pytestmark = pytest.mark.gpu
 torch = pytest.importorskip("torch")
 
-DIM, FF, E, K, SEED = 1024, 512, 16, 6, 0x2517
+DIM, FF, E, K, SEED = 4096, 3072, 16, 6, 0x2517
 
 
 def routes(n, seed):
@@ -38,7 +38,8 @@ def oracle_layer(orc, sig, ids, w, x):
     return orc.combine(ids, w, np.stack(rows))
 
 
-@pytest.mark.parametrize("path,sig", [("4", (16, 16, 17)), ("3", (16, 16, 17)), ("3", (29, 29, 29))])
+@pytest.mark.parametrize("path,sig", [("5", (16, 16, 17)), ("4", (16, 16, 17)), ("3", (16, 16, 17)),
+                                      ("3", (29, 29, 29))])
 def test_two_streams_one_context(orc, monkeypatch, path, sig):
     monkeypatch.setenv("XL_LAYER_PATH", path)
     step(f"two streams: XL_LAYER_PATH={path} sig={sig}")
@@ -66,7 +67,7 @@ def test_two_streams_one_context(orc, monkeypatch, path, sig):
         lane.close()
 
 
-@pytest.mark.parametrize("path", ["4", "3"])
+@pytest.mark.parametrize("path", ["5", "4", "3"])
 def test_launch_counter_wrap(orc, monkeypatch, path):
     monkeypatch.setenv("XL_LAYER_PATH", path)
     step(f"counter wrap: XL_LAYER_PATH={path}")

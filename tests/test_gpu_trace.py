@@ -3,7 +3,7 @@
 The north star's exact bars (Q8_K activation bytes and per-block int32
 partials) are checked here on what the hot kernels themselves stage and form,
 through the parity trace (xl_layer_trace_async, xl_grouped_trace_async): the
-streaming kernel (configs 0 and 1), the all-types kernel with its IQ2, IQ1_M
+streaming kernel (configs 0 and 1), the unit kernel, the all-types kernel with its IQ2, IQ1_M
 and mixed-type instances (configs 2 and 3), and the grouped MFMA kernels
 (config 4). For each launch:
 
@@ -55,9 +55,13 @@ def check_pick(orc, sig, mats, dim, ff, q8x, h, q8h, ints, tag):
 
 LAYER_CASES = [
     # (XL_LAYER_PATH, dim, ff, E, k, layer type map kind, expected kernel)
-    ("1", 4096, 3072, 12, 6, "iq2", 1),     # config 1: streaming kernel
+    ("1", 4096, 3072, 12, 6, "iq2", 1),     # config 1: the streaming kernel
     ("1", 4096, 3072, 12, 1, "iq2", 1),     # config 0: one pick (1-2 pick instance)
-    ("1", 4096, 3072, 12, 3, "iq2", 1),     # 3-4 pick instance
+    ("4", 4096, 3072, 12, 3, "iq2", 1),     # 3-4 pick instance
+    ("5", 4096, 3072, 12, 6, "iq2", 5),     # the unit kernel
+    ("5", 4096, 3072, 12, 1, "iq2", 5),
+    ("5", 4096, 3072, 12, 3, "iq2", 5),
+    ("5", 4096, 3072, 12, 8, "iq2", 5),
     ("1", 1024, 512, 8, 6, "iq2", 1),
     ("3", 4096, 3072, 12, 6, "iq2", 3),     # all-types kernel, IQ2 instance
     ("3", 4096, 3072, 12, 6, "iq1", 3),     # config 2: IQ1_M-only instance

@@ -429,9 +429,11 @@ def main():
     # timed region's event time over the launches (rocprofv3 --kernel-trace of
     # the same command agrees; see profiles/). Config 3's figure also holds the
     # normalization between layers, so it bounds the kernel from below.
-    kernel = {0: "xl::dev::stream_kernel (single-launch layer)", 1: "xl::dev::stream_kernel (single-launch layer)",
-              4: "grouped path (bucket, Q8_K, gu_kernel, Q8_K, dn_kernel, combine: 6 launches per step)"}.get(
-        cfg, "xl::dev::layer3_kernel (all-types single-launch layer)")
+    kernel = {0: "xl::dev::stream_kernel (single-launch layer, IQ2 instance)",
+              1: "xl::dev::stream_kernel (single-launch layer, IQ2 instance)",
+              2: "xl::dev::stream_kernel (single-launch layer, IQ1_M instance)",
+              3: "xl::dev::stream_kernel (single-launch layer, mixed-type instance)",
+              4: "grouped path (bucket, Q8_K, gu_kernel, Q8_K, dn_kernel, combine: 6 launches per step)"}.get(cfg)
     if cfg == 5:
         kernel = ("MoE block: shared FFN (quant32, mv32 gate+up, swiglu32, quant32, mv32 down) + stream_kernel "
                   "+ hc_post_kernel: 7 launches per step")

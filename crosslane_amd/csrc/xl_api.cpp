@@ -82,12 +82,13 @@ std::vector<uint64_t> device_tables() {
     return t;
 }
 
-// Expanded codebooks of the single-launch kernel (byte layout kG_* in
+// Expanded codebooks of the single-launch kernels (byte layout kG_* in
 // xl_layer.hip), one copy each: sign rows {M, M & 0x01..01} where M has 0xff in
-// the bytes of negative weights, then the IQ2_XXS, IQ2_XS and IQ1 grids.
+// the bytes of negative weights, then the IQ2_XXS, IQ2_XS and IQ1 grids, then
+// the streaming kernels' IQ1_M value rows (at kTableIQ1X).
 std::vector<uint64_t> layer_tables() {
     std::vector<uint64_t> t;
-    t.reserve(xl::kLayer3TableBytes / 8);
+    t.reserve(xl::kTableBytes / 8);
     for (int i = 0; i < 128; ++i) {
         const uint8_t sg = ksigns(i);
         uint64_t m = 0;
@@ -100,6 +101,19 @@ std::vector<uint64_t> layer_tables() {
     for (int i = 0; i < 512; ++i) t.push_back(expand_codes(kIq2xsCodes[i], false));
     for (int i = 0; i < 2048; ++i) t.push_back(expand_codes(kIq1sCodes[i], true));
     if (t.size() * 8 != size_t(xl::kLayer3TableBytes)) throw Failure(XL_E_STATE, "expanded table size");
+    // IQ1_M value rows: row (nib << 8 | lo) holds 8 * grid[(nib & 7) << 8 | lo] + delta,
+    // delta = -1 when bit 3 of the nibble is set, else +1 (one byte per weight)
+    for (int nib = 0; nib < 16; ++nib)
+        for (int lo = 0; lo < 256; ++lo) {
+            const uint64_t g = expand_codes(kIq1sCodes[((nib & 7) << 8) | lo], true);
+            uint64_t v = 0;
+            for (int j = 0; j < 8; ++j) {
+                const int s = int(int8_t(uint8_t(g >> (8 * j))));
+                v |= uint64_t(uint8_t(int8_t(8 * s + ((nib & 8) ? -1 : 1)))) << (8 * j);
+            }
+            t.push_back(v);
+        }
+    if (t.size() * 8 != size_t(xl::kTableBytes)) throw Failure(XL_E_STATE, "expanded table size");
     return t;
 }
 
@@ -371,8 +385,8 @@ bool enqueue_layer(xl_context* ctx, int32_t layer, const int32_t* d_ids, const f
                 if (tr && e == hipSuccess) tr->kernel = 5;
             }
             need(ctx->path != 5 || e == hipSuccess, XL_E_ARG, "XL_LAYER_PATH=5: no unit-kernel instance for this layer");
-            if ((ctx->path == 1 || ctx->path == 4) && e == hipErrorNotSupported && gu_mask == 1 && dn_mask == 2) {
-                e = xl::dev::launch_stream(a, ctx->cus, s, stop);
+            if ((ctx->path == 1 || ctx->path == 4) && e == hipErrorNotSupported) {
+                e = xl::dev::launch_stream(a, gu_mask, dn_mask, ctx->cus, s, stop);
                 if (e != hipSuccess && e != hipErrorNotSupported) hip_check(e, "streaming layer");
                 (void)hipGetLastError();
                 if (tr && e == hipSuccess) tr->kernel = 1;
@@ -563,7 +577,7 @@ int32_t xl_open(uint32_t abi_version, const xl_config* cfg, xl_context** out, xl
             {reinterpret_cast<void**>(&ctx->hbuf), uint64_t(2) * xl::kHBufWords * 4},
             {reinterpret_cast<void**>(&ctx->part), uint64_t(P) * (ff / 256) * dim * 4},
             {reinterpret_cast<void**>(&ctx->ucnt), 2 * 256 * 4},
-            {reinterpret_cast<void**>(&ctx->tables), uint64_t(xl::kLayer3TableBytes)},
+            {reinterpret_cast<void**>(&ctx->tables), uint64_t(xl::kTableBytes)},
             {reinterpret_cast<void**>(&ctx->p32d), (uint64_t(ctx->act_max / 32) + uint64_t(P) * (ff / 32)) * 4},
             {reinterpret_cast<void**>(&ctx->timeline), uint64_t(ctx->cus) * 16 * 32 * 8},
         };

@@ -82,7 +82,7 @@ struct Layer3Args {
     uint32_t* ctl;              // [0] epoch of the last launch, [1] arrival counter (zero between launches)
     int* err;
     float lim;                  // SwiGLU limit (> 0: g = min(g, lim), u = clamp(u, -lim, lim))
-    const uint64_t* tables;     // expanded codebooks (kLayer3TableBytes), see kG_* in xl_layer.hip
+    const uint64_t* tables;     // expanded codebooks (kTableBytes), see kG_* in xl_layer.hip
     // Regular layers (all experts with the same three block types, each
     // expert's matrices consecutive in the layer slab): matrix (id, role)
     // starts at slab + id * estride + roff[role] and no descriptor is read.
@@ -143,6 +143,10 @@ constexpr int kRouteMaxExperts = 4096;   // router: scores and keys of one token
 // Tasks the bucket kernel can write for P pairs: one per started tile of 16 pairs of an expert.
 inline int64_t group_max_tasks(int64_t P, int64_t n_experts) { return P / 16 + (P < n_experts ? P : n_experts) + 1; }
 constexpr int kLayer3TableBytes = 24576;   // expanded codebooks of the single-launch kernel
+// Then the IQ1_M value rows of the streaming kernels: 4096 rows of 8 int8,
+// row (nib << 8 | idx_lo) = 8 * grid[(nib & 7) << 8 | idx_lo] + (nib & 8 ? -1 : 1).
+constexpr int kTableIQ1X = kLayer3TableBytes;
+constexpr int kTableBytes = kTableIQ1X + 4096 * 8;
 
 // Size of the no-allocation entry point's static device scratch (xl_noalloc.hip).
 constexpr uint64_t kNoAllocScratchBytes = uint64_t(8) << 20;
@@ -158,9 +162,13 @@ hipError_t noalloc_scratch(int device, void** out);
 // stop event: no extra packet on the stream).
 hipError_t launch_layer3(const Layer3Args& args, int gu_types, int dn_types, int cus, hipStream_t s,
                          hipEvent_t stop = nullptr);
-// Streaming layer for IQ2_XXS gate/up + IQ2_XS down: hipErrorNotSupported when
-// (dim, ff, k) has no instance.
-hipError_t launch_stream(const Layer3Args& args, int cus, hipStream_t s, hipEvent_t stop = nullptr);
+// Streaming layer (xl_stream*.hip): instances for IQ2_XXS gate/up + IQ2_XS down,
+// IQ1_M only, and any mix of the three types (per matrix, read from each
+// pick's descriptor); hipErrorNotSupported when (dim, ff, k, types) has none.
+hipError_t launch_stream(const Layer3Args& args, int gu_types, int dn_types, int cus, hipStream_t s,
+                         hipEvent_t stop = nullptr);
+hipError_t launch_stream_iq1(const Layer3Args& args, int cus, hipStream_t s, hipEvent_t stop);
+hipError_t launch_stream_mix(const Layer3Args& args, int cus, hipStream_t s, hipEvent_t stop);
 // Unit layer (xl_unit.hip) for IQ2_XXS gate/up + IQ2_XS down: hipErrorNotSupported
 // when (dim, ff, k) has no instance.
 hipError_t launch_unit(const Layer3Args& args, int cus, hipStream_t s, hipEvent_t stop = nullptr);

@@ -1,6 +1,6 @@
-// IQ2 row decoding of the streaming layer kernels (xl_stream.hip, xl_unit.hip),
-// gfx950: perm-addressed, bank-interleaved LDS codebook copies, sign masks
-// applied to the activations (IQ2_XXS) or to the grid (IQ2_XS), the Q8_K
+// Row decoding of the streaming layer kernels (xl_stream*.hip, xl_unit.hip),
+// gfx950: perm-addressed, bank-interleaved LDS codebook copies, IQ2 sign masks
+// applied to the activations or to the grid, IQ1_M value rows, the Q8_K
 // quantizer of several blocks at once, and the sentinel h exchange words.
 #pragma once
 #include <hip/hip_runtime.h>
@@ -60,15 +60,22 @@ struct Looks {
     uint2 g[8], m[8];
 };
 // IQ2_XXS pair (w0..3: two sub-blocks of {4 grid bytes, 4 sign|scale-bit bytes}).
-__device__ __forceinline__ Looks look_xxs(const uint8_t* lds, uint32_t lo_g, uint32_t lo_s, const uint32_t* w) {
-    Looks L;
+// The *_to forms write the caller's Looks field by field, so that a decoder
+// chosen at run time among several leaves every field in a register.
+__device__ __forceinline__ void look_xxs_to(Looks& L, const uint8_t* lds, uint32_t lo_g, uint32_t lo_s, const uint32_t* w) {
 #pragma unroll
     for (int s = 0; s < 2; ++s)
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
-            L.g[4 * s + q] = *reinterpret_cast<const uint2*>(lds + perm(w[2 * s], lo_g, sel_b(q)));
+            // sign row first: every *_to form's last write is L.g[7], so that the
+            // compiler's merging of the branches' last lookups keeps one destination
             L.m[4 * s + q] = *reinterpret_cast<const uint2*>(lds + perm(w[2 * s + 1], lo_s, sel_b(q)));
+            L.g[4 * s + q] = *reinterpret_cast<const uint2*>(lds + perm(w[2 * s], lo_g, sel_b(q)));
         }
+}
+__device__ __forceinline__ Looks look_xxs(const uint8_t* lds, uint32_t lo_g, uint32_t lo_s, const uint32_t* w) {
+    Looks L;
+    look_xxs_to(L, lds, lo_g, lo_s, w);
     return L;
 }
 // Against 64 Q8_K quants a (and their negations na): the exact integer sum of
@@ -90,16 +97,19 @@ __device__ __forceinline__ int sum_xxs(const Looks& L, const uint32_t* w, const 
 // bytes): the exact integer sum with the 16-weight scales (q8k_core.hpp:116-140).
 // Split like the IQ2_XXS decoder, so that a pass issues the next pair's
 // lookups before the current pair's arithmetic waits on its own.
-__device__ __forceinline__ Looks look_xs(const uint8_t* lds, uint32_t lo_x, uint32_t lo_s, const uint32_t* w) {
-    Looks L;
+__device__ __forceinline__ void look_xs_to(Looks& L, const uint8_t* lds, uint32_t lo_x, uint32_t lo_s, const uint32_t* w) {
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
         const uint32_t h = e & 1;
         // grid row * 32 = (code >> 7) << 5: one shift and one v_and_or_b32 with the lane's copy
         const uint32_t sh = h ? (w[e >> 1] >> 18) : (w[e >> 1] >> 2);
-        L.g[e] = *reinterpret_cast<const uint2*>(lds + ((sh & 0x3fe0u) | lo_x));
         L.m[e] = *reinterpret_cast<const uint2*>(lds + perm(w[e >> 1], lo_s, sel_b(2 * h)));
+        L.g[e] = *reinterpret_cast<const uint2*>(lds + ((sh & 0x3fe0u) | lo_x));
     }
+}
+__device__ __forceinline__ Looks look_xs(const uint8_t* lds, uint32_t lo_x, uint32_t lo_s, const uint32_t* w) {
+    Looks L;
+    look_xs_to(L, lds, lo_x, lo_s, w);
     return L;
 }
 __device__ __forceinline__ int sum_xs(const Looks& L, uint32_t sc, const uint32_t* a) {
@@ -118,6 +128,69 @@ __device__ __forceinline__ int sum_xs(const Looks& L, uint32_t sc, const uint32_
         total += __mul24(lo, int(2u * (byte & 15u) + 1u)) + __mul24(hi, int(2u * (byte >> 4) + 1u));
     }
     return total;
+}
+
+// IQ2_XXS pair with the signs applied to the grid bytes instead of the
+// activations ((g ^ M) + (M & 0x01010101), no negated activations needed): the
+// same integer as sum_xxs.
+__device__ __forceinline__ int sum_xxs_g(const Looks& L, const uint32_t* w, const uint32_t* a) {
+    int acc[2] = {0, 0};
+#pragma unroll
+    for (int s = 0; s < 2; ++s)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const int e = 4 * s + q, k0 = 8 * s + 2 * q;
+            acc[s] = sdot4(xad(L.g[e].x, L.m[e].x, L.m[e].x & 0x01010101u), a[k0], acc[s]);
+            acc[s] = sdot4(xad(L.g[e].y, L.m[e].y, L.m[e].y & 0x01010101u), a[k0 + 1], acc[s]);
+        }
+    return __mul24(acc[0], xxs_sc(w[1])) + __mul24(acc[1], xxs_sc(w[3]));
+}
+
+// IQ1_M. The value rows sit at LDS byte 0: row (nib << 8 | idx_lo) holds the 8
+// bytes 8 * grid + delta of the 11-bit grid index (nib & 7) << 8 | idx_lo, delta
+// -1 when bit 3 of the group's nibble is set, else +1 (kTableIQ1X). One lookup
+// and two v_dot4 give a group's exact 8 * main + delta integer. The lookup
+// address (nib << 8 | idx_lo) << 3 is one v_perm_b32 of the index byte and the
+// nibble byte, then one shift.
+// Pair (Raw3): w0, w1 = the low index bytes of sub-blocks 0 and 1, w2 = the
+// eight groups' nibbles (group 4 s + g at bits 16 s + 4 g), w3, w4 = the
+// block's scale words.
+__device__ __forceinline__ void look_iq1_to(Looks& L, const uint8_t* lds, const uint32_t* w) {
+    const uint32_t ne = w[2] & 0x0f0f0f0fu;          // nibbles 0, 2, 4, 6 in bytes 0 .. 3
+    const uint32_t no = (w[2] >> 4) & 0x0f0f0f0fu;   // nibbles 1, 3, 5, 7
+#pragma unroll
+    for (int s = 0; s < 2; ++s)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+            const int n = 4 * s + g;
+            // byte 0 <- index byte g of w[s], byte 1 <- nibble n, bytes 2, 3 <- 0
+            const uint32_t r = __builtin_amdgcn_perm((n & 1) ? no : ne, w[s],
+                                                     0x0C0C0000u | (uint32_t(4 + (n >> 1)) << 8) | uint32_t(g));
+            L.g[n] = *reinterpret_cast<const uint2*>(lds + (r << 3));
+        }
+}
+// Against 64 Q8_K quants a: the exact pair integer, sum over the four 16-weight
+// groups of (2 sc + 1) * (8 * main + delta) (q8k_core.hpp's IQ1_M terms times
+// 8); scw = the pair's 16-bit scale word (3 bits per 16 weights).
+__device__ __forceinline__ int sum_iq1(const Looks& L, uint32_t scw, const uint32_t* a) {
+    int total = 0;
+#pragma unroll
+    for (int s = 0; s < 2; ++s) {
+        int lo = 0, hi = 0;
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+            int& acc = g < 2 ? lo : hi;
+            acc = sdot4(L.g[4 * s + g].x, a[8 * s + 2 * g], acc);
+            acc = sdot4(L.g[4 * s + g].y, a[8 * s + 2 * g + 1], acc);
+        }
+        total += __mul24(lo, int(2u * ((scw >> (6 * s)) & 7u) + 1u)) + __mul24(hi, int(2u * ((scw >> (6 * s + 3)) & 7u) + 1u));
+    }
+    return total;
+}
+// The pair's scale word (pair pp of its block) and the block's fp16 scale.
+__device__ __forceinline__ uint32_t iq1_scw(const uint32_t* w, int pp) { return ((pp & 2) ? w[4] : w[3]) >> (16 * (pp & 1)); }
+__device__ __forceinline__ uint32_t iq1_d16(const uint32_t* w) {
+    return ((w[3] >> 12) & 0xfu) | ((w[3] >> 24) & 0xf0u) | ((w[4] >> 4) & 0xf00u) | ((w[4] >> 16) & 0xf000u);
 }
 
 template <int P>

@@ -1,0 +1,707 @@
+// The routed-expert layer in one streaming launch (gfx950). Instances by the
+// block types of the layer's matrices (GT: gate/up, DT: down; bits 1 IQ2_XXS,
+// 2 IQ2_XS, 4 IQ1_M): IQ2_XXS gate/up with IQ2_XS down (xl_stream.hip),
+// IQ1_M only (xl_stream_iq1.hip), and any mix (xl_stream_mix.hip: each pick's
+// three matrices found from its descriptor, their types read per slot).
+//
+// One workgroup of NW waves per CU. The decode work per 8-weight group is one
+// grid lookup, (IQ2) one sign lookup, the sign applied by one op per dword,
+// and two v_dot4; everything else is laid out so that nothing more is needed:
+//
+//   codebooks  bank-interleaved copies whose row stride is 256 bytes, so a
+//              lookup address is one v_perm_b32 of the index byte and the
+//              lane's copy offset: IQ2_XXS grid 32 copies (16 in the mixed
+//              instance, sharing each 256-byte row with 16 sign copies), sign
+//              rows likewise, IQ2_XS grid 4 copies. The sign table has 256
+//              rows, indexed by the whole byte (bit 7 is ignored: it carries a
+//              scale bit for IQ2_XXS and a grid bit for IQ2_XS). IQ1_M: one
+//              copy of 4096 value rows (8 * grid + delta) at LDS byte 0.
+//   gate/up    slot s of the k*ff rows (pick-major) belongs to wave s mod W;
+//              the rows' SiLU runs once per batch of kBatch slots, one lane
+//              per slot, and h goes out as plain 32-bit words.
+//   h exchange two buffers of k_max*ff_max floats, used by alternate launches
+//              of this kernel. A buffer holds the sentinel 0xffffffff (a NaN no
+//              arithmetic produces; a computed h with those bits is stored as
+//              the canonical NaN) in every word before its launch: each launch
+//              refills the other buffer, which the previous launch used.
+//              Readers poll for non-sentinel words, so no fence is needed.
+//   down       workgroup g owns output row groups {g, g+G, ...} of every pick;
+//              its passes (row group, pick) are dealt to its waves in pick
+//              order, one pass per wave per step. Before step j the workgroup
+//              quantizes the h of the picks that step needs (Q8_K, one block
+//              per wave at a time) into LDS, from loads issued one step ahead:
+//              early steps need early picks, whose h is complete while later
+//              picks are still being produced.
+//   combine    fixed order (ascending expert id, sequential fma, then + shared;
+//              engine/strata/warm/runtime.cpp:183-188), per workgroup.
+//
+// Waits only point backwards (down waits on gate/up, which waits on nothing)
+// and the grid is at most one workgroup per CU, so every workgroup runs once
+// the CUs are free and the grid drains. Every wait is bounded: on expiry the
+// kernel raises kDevErrTimeout and finishes.
+//
+// The launch parity comes from a device word advanced by the last workgroup to
+// arrive (an arrival counter), never from the host, so a captured launch can
+// be replayed.
+#pragma once
+#include <hip/hip_ext.h>
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <utility>
+
+#include "xl_dev.hpp"
+#include "xl_internal.hpp"
+#include "xl_iq2.hpp"
+
+namespace xl::dev {
+namespace {
+
+// ---- LDS maps (bytes), by the union M of the gate/up and down type masks -----------------------
+// SGN/XXS: sign masks and IQ2_XXS grid, 256 rows of 256 bytes each (lookup
+// address = index << 8 | the lane's copy offset | table base); XS: IQ2_XS grid
+// (512 rows x 4 copies x 8 B); IQ1: IQ1_M value rows; XQ: Q8_K(x) (dim quants,
+// swizzled, then 16 block scales; gate/up phase); HQ: Q8_K(h) of the picks
+// (down phase, over a region gate/up no longer reads); Y: y staging.
+template <int M>
+struct SLay;
+template <>
+struct SLay<3> {   // IQ2_XXS gate/up, IQ2_XS down
+    static constexpr int CP = 32;                         // grid and sign copies
+    static constexpr int SGN = 0, XXS = 65536;            // two tables of 32 copies
+    static constexpr int SGN_IN_ROW = 0;                  // byte of the sign copies in a row
+    static constexpr int XS = 131072, IQ1 = -1;
+    static constexpr int XQ = 147456, HQ = 65536, Y = 147456;   // HQ over the XXS grid, Y over XQ
+    static constexpr int Bytes = 151616;
+    static constexpr int HQBytes = 65536;
+};
+template <>
+struct SLay<4> {   // IQ1_M only
+    static constexpr int CP = 0, SGN = -1, XXS = -1, SGN_IN_ROW = 0, XS = -1;
+    static constexpr int IQ1 = 0;
+    static constexpr int XQ = 32768, HQ = 32768, Y = 98304;   // HQ over XQ
+    static constexpr int Bytes = 102400;
+    static constexpr int HQBytes = 65536;
+};
+template <>
+struct SLay<7> {   // any mix: one 256-byte row holds 16 grid copies, then 16 sign copies
+    static constexpr int CP = 16;
+    static constexpr int XXS = 65536, SGN = 65536, SGN_IN_ROW = 128;
+    static constexpr int IQ1 = 0, XS = 32768, Y = 49152;
+    static constexpr int XQ = 131072, HQ = 131072;   // HQ over XQ
+    static constexpr int Bytes = 163584;
+    static constexpr int HQBytes = Bytes - HQ;
+};
+constexpr int kS_YFloats = 1024;
+
+// Global codebooks (layer_tables in xl_api.cpp): IQ2_XXS grid, IQ2_XS grid, IQ1_M value rows.
+constexpr int kG_XXS = 2048, kG_XS = 4096;
+
+template <int M>
+struct Smem {
+    uint8_t b[SLay<M>::Bytes];   // first, so that its LDS address is 0 and table bases fold into offsets
+    int ids[16];
+    float w[16];
+    int order[16];   // picks by ascending expert id (stable: equal ids keep pick order)
+    uint32_t parity;
+};
+
+// Type of a matrix whose mask has one bit.
+template <int TM>
+constexpr int single_type() { return TM == 1 ? kIQ2_XXS : TM == 2 ? kIQ2_XS : kIQ1_M; }
+template <int TM>
+constexpr bool one_type() { return TM == 1 || TM == 2 || TM == 4; }
+
+// Lane constants of the codebook lookups.
+struct LoLanes {
+    uint32_t g, s, x;
+};
+// Lookups of one pair of type `type` (TM: the matrix's type mask; one bit = known
+// at compile time, else the wave-uniform runtime type picks the decoder).
+template <int TM>
+__device__ __forceinline__ void look_any(Looks& L, int type, const uint8_t* lds, const LoLanes& lo, const Raw3& r) {
+    const int t = one_type<TM>() ? single_type<TM>() : type;
+    if ((TM & 1) && t == kIQ2_XXS) look_xxs_to(L, lds, lo.g, lo.s, r.w);
+    else if ((TM & 2) && t == kIQ2_XS) look_xs_to(L, lds, lo.x, lo.s, r.w);
+    else look_iq1_to(L, lds, r.w);
+}
+// The pair's exact integer against quants a (na: their negations, used by
+// IQ2_XXS when NA; without, its signs go on the grid) and its fp16 scale.
+template <int TM, bool NA>
+__device__ __forceinline__ int sum_any(int type, const Looks& L, const Raw3& r, const uint32_t* a, const uint32_t* na,
+                                       int pp, uint32_t& d16) {
+    const int t = one_type<TM>() ? single_type<TM>() : type;
+    if ((TM & 1) && t == kIQ2_XXS) {
+        d16 = r.h[0];
+        if constexpr (NA) return sum_xxs(L, r.w, a, na);
+        else return sum_xxs_g(L, r.w, a);
+    }
+    if ((TM & 2) && t == kIQ2_XS) {
+        d16 = r.h[1];
+        return sum_xs(L, r.h[0], a);
+    }
+    d16 = iq1_d16(r.w);
+    return sum_iq1(L, iq1_scw(r.w, pp), a);
+}
+
+// ---- the kernel ----------------------------------------------------------------------------
+// LG x PG: lanes per gate/up row and pairs per lane (LG * PG * 64 == dim);
+// LD x PD: the same for down rows (LD * PD * 64 == ff). MG / MD: most gate/up
+// slots / down passes per wave; WIN: gate/up slots in flight per wave; WIND:
+// down passes in flight; MQ: most Q8_K(h) blocks one wave quantizes per step.
+constexpr int kBatch = 3;   // gate/up slots per SiLU batch
+// TR: also write the parity trace (Layer3Args::tq8x ...); the untraced instance
+// compiles none of it.
+template <int NW, int LG, int PG, int LD, int PD, int MG, int MD, int WIN, int WIND, int MQ, int GT, int DT, bool TR>
+__global__ __launch_bounds__(NW * 64, 1) void stream_kernel(Layer3Args a) {
+    static_assert(WIN <= MG && WIND <= MD && WIND <= MG && MG <= 32 && MD <= 32, "prefetch depths, metadata lanes");
+    constexpr int M = (GT == 1 && DT == 2) ? 3 : (GT == 4 && DT == 4) ? 4 : 7;
+    constexpr bool MIX = M == 7;   // matrices from per-(pick, role) lane tables, types at run time
+    using LY = SLay<M>;
+    static_assert(MIX || (one_type<GT>() && one_type<DT>()), "single-type instances");
+    __shared__ __attribute__((aligned(16))) Smem<M> sm;
+    uint8_t* const lds = sm.b;
+    constexpr int RG = 64 / LG, RD = 64 / LD;
+    const int t = threadIdx.x, lane = t & 63;
+    const int wv = __builtin_amdgcn_readfirstlane(t >> 6);
+    const int G = gridDim.x, W = G * NW, gw = blockIdx.x * NW + wv;
+    const int k = a.k, ff = a.ff, dim = a.dim;
+    const int lG = lane % LG, rG = lane / LG, lD = lane % LD, rD = lane / LD;
+    const int nbx = dim / 256, nbh = ff / 256;
+    auto mark = [&](int n) {
+        if (a.trace && lane == 0) a.trace[size_t(gw) * 32 + n] = __builtin_amdgcn_s_memrealtime();
+    };
+
+    // ---- this wave's work: gate/up slots gw + W*j, down passes wv + NW*j (pick-major)
+    const int sppG = ff / RG, SG = k * sppG;
+    const int ng = SG > gw ? min(MG, (SG - gw + W - 1) / W) : 0;
+    const int quads = dim / RD;
+    const int nq_wg = quads > int(blockIdx.x) ? (quads - int(blockIdx.x) + G - 1) / G : 0;
+    const int P = k * nq_wg;
+    const int nd = P > wv ? min(MD, (P - wv + NW - 1) / NW) : 0;
+    // Slot and pass metadata, computed lane-parallel and kept in one register:
+    // lane j < 32 holds gate/up slot j, lane 32 + j down pass j, packed as
+    // expert << 16 | pick << 12 | first row (bad ids read expert 0 and are
+    // masked out). A use reads its lane back (v_readlane), so the scalar
+    // registers stay free for the loads' addresses.
+    const int idl = a.ids[lane < k ? lane : k - 1];   // unconditional loads keep the wait counts exact
+    const int idv = lane < k ? idl : -1;
+    uint32_t meta;
+    uint64_t okmask;   // bit j: slot j is this wave's with a valid id; bit 32 + j: pass j likewise
+    {
+        const bool isd = lane >= 32;
+        const int j = lane & 31;
+        const int n = isd ? nd : ng;
+        const int jj = j < n ? j : n > 0 ? n - 1 : 0;   // past the last: repeat a valid row
+        const int unit = isd ? wv + NW * jj : gw + W * jj;
+        const int per = isd ? nq_wg : sppG;
+        const int pick = n > 0 ? unit / per : 0;
+        const int row = isd ? (n > 0 ? (int(blockIdx.x) + G * (unit - pick * nq_wg)) * RD : 0)
+                            : (unit - pick * sppG) * RG;
+        const int id = __shfl(idv, min(pick, 15));
+        const bool ok = n > 0 && id >= 0 && id < a.n_experts;
+        meta = (uint32_t(ok ? id : 0) << 16) | (uint32_t(min(pick, 15)) << 12) | uint32_t(row);
+        okmask = __builtin_amdgcn_ballot_w64(ok && j < n);
+    }
+    auto gsl = [&](int j) { return uint32_t(__builtin_amdgcn_readlane(int(meta), j)); };
+    auto dsl = [&](int j) { return uint32_t(__builtin_amdgcn_readlane(int(meta), 32 + j)); };
+    auto dpick = [&](int j) { return int((dsl(j) >> 12) & 15u); };
+    const uint32_t gok = uint32_t(okmask), dok = uint32_t(okmask >> 32);
+    // h word of slot j's first row (pick * ff + row = slot * RG), or -2^30 when the
+    // slot is not this wave's
+    auto hrow = [&](int j) { return j < ng ? (gw + W * j) * RG : -(1 << 30); };
+
+    // Matrices. Single-type instances (regular layers): matrix (e, role) at
+    // slab + e * estride + roff[role], plane offsets shared. Mixed instance: lane
+    // 16 role + i holds pick i's matrix of that role (base, type), from the
+    // layer's slab or the pick's descriptor (a bad id reads expert 0's).
+    uint32_t go1 = 0, go2 = 0, do1 = 0, do2 = 0;
+    if constexpr (!MIX) {
+        plane_offs(single_type<GT>(), uint64_t(ff) * uint64_t(nbx), go1, go2);
+        plane_offs(single_type<DT>(), uint64_t(dim) * uint64_t(nbh), do1, do2);
+    }
+    auto matrix = [&](int e, int role, uint32_t o1, uint32_t o2, int type, int nb) {
+        return MRef{a.slab + uint64_t(e) * a.estride + a.roff[role], o1, o2, type, nb};
+    };
+    uint32_t tb_lo = 0, tb_hi = 0;
+    int tb_ty = 0;
+    if constexpr (MIX) {
+        const int ti = lane & 15, tr = min(lane >> 4, 2);
+        const int id = __shfl(idv, ti < k ? ti : k - 1);
+        const int e = (id >= 0 && id < a.n_experts) ? id : 0;
+        uint64_t base;
+        if (a.slab) {
+            base = uint64_t(a.slab) + uint64_t(e) * a.estride + (tr == 0 ? a.roff[0] : tr == 1 ? a.roff[1] : a.roff[2]);
+            tb_ty = tr == 0 ? a.rtype[0] : tr == 1 ? a.rtype[1] : a.rtype[2];
+        } else {
+            const MatRef& d = a.descs[e].m[tr];
+            base = uint64_t(d.base);
+            tb_ty = d.type;
+        }
+        tb_lo = uint32_t(base);
+        tb_hi = uint32_t(base >> 32);
+    }
+    // pick i's matrix of a role (mixed instance): type from the lane table, planes from the shape
+    auto mref = [&](int pick, int role, int rows, int nb) {
+        const int L = 16 * role + pick;
+        MRef m;
+        m.base = reinterpret_cast<const uint8_t*>((uint64_t(uint32_t(__builtin_amdgcn_readlane(int(tb_hi), L))) << 32) |
+                                                  uint32_t(__builtin_amdgcn_readlane(int(tb_lo), L)));
+        m.type = __builtin_amdgcn_readlane(tb_ty, L);
+        m.nb = nb;
+        plane_offs(m.type, uint64_t(rows) * uint64_t(nb), m.o1, m.o2);
+        return m;
+    };
+    auto mtype = [&](int pick, int role) { return __builtin_amdgcn_readlane(tb_ty, 16 * role + pick); };
+
+    // ---- codebook rows and x first (they need no ids), then the first slots. The
+    // rows come into registers (plain loads: waiting for them does not wait for
+    // the slot loads issued after them).
+    constexpr int NT = NW * 64;
+    constexpr bool HASXXS = (M & 1) != 0 || MIX, HASXS = (M & 2) != 0 || MIX;
+    constexpr bool HAS1 = (M & 4) != 0;
+    constexpr int NX = (4096 + NT - 1) / NT, NS = (1024 + NT - 1) / NT, N1 = (2048 + NT - 1) / NT;
+    uint2 vx[HASXXS ? NX : 1], vs[HASXS ? NS : 1];
+    uint4 v1[HAS1 ? N1 : 1];
+    {
+        const uint2* gx = reinterpret_cast<const uint2*>(reinterpret_cast<const uint8_t*>(a.tables) + kG_XXS);
+        const uint2* gs = reinterpret_cast<const uint2*>(reinterpret_cast<const uint8_t*>(a.tables) + kG_XS);
+        const uint4* g1 = reinterpret_cast<const uint4*>(reinterpret_cast<const uint8_t*>(a.tables) + kTableIQ1X);
+        // chunk c of the XXS/sign table: row c / 16, 16-byte piece c % 16
+        if constexpr (HASXXS)
+#pragma unroll
+            for (int i = 0; i < NX; ++i) vx[i] = gx[min(t + NT * i, 4095) >> 4];
+        if constexpr (HASXS)
+#pragma unroll
+            for (int i = 0; i < NS; ++i) vs[i] = gs[min(t + NT * i, 1023) >> 1];   // chunk c: row c / 2, copies 2(c % 2), +1
+        if constexpr (HAS1)
+#pragma unroll
+            for (int i = 0; i < N1; ++i) v1[i] = g1[min(t + NT * i, 2047)];
+    }
+    constexpr int UX = (16 + NW - 1) / NW;
+    float4 xv[UX];
+#pragma unroll
+    for (int u = 0; u < UX; ++u) {
+        const int b = wv + NW * u;
+        xv[u] = reinterpret_cast<const float4*>(a.x + 256 * (b < nbx ? b : 0))[lane];
+    }
+    const float cw = a.w[lane < k ? lane : k - 1];
+    uint32_t* ctl = a.ctl + 2;   // [0] parity source: launches of this kernel so far, [1] arrivals
+    const uint32_t e_prev = coh_ld32(ctl);
+
+    Raw3 rg[WIN][PG], ru[WIN][PG];
+    auto load_slot = [&]<int j>() {
+        constexpr int b = j % WIN;
+        const uint32_t m = gsl(j);
+        const int row0 = int(m & 0xfffu), e = int(m >> 16);
+#pragma unroll
+        for (int q = 0; q < PG; ++q) {
+            if constexpr (MIX) {
+                const int pk = int((m >> 12) & 15u);
+                load_pair3(rg[b][q], mref(pk, 0, ff, nbx), row0, rG, lG + LG * q);
+                load_pair3(ru[b][q], mref(pk, 1, ff, nbx), row0, rG, lG + LG * q);
+            } else {
+                load_pair_t<GT>(rg[b][q], matrix(e, 0, go1, go2, single_type<GT>(), nbx), row0, rG, lG + LG * q);
+                load_pair_t<GT>(ru[b][q], matrix(e, 1, go1, go2, single_type<GT>(), nbx), row0, rG, lG + LG * q);
+            }
+        }
+    };
+    // Every wave issues the same loads whatever its share (idle slots and passes
+    // re-read valid rows and are discarded), so every wait count is exact.
+    static_for<WIN>([&]<int j>() { load_slot.template operator()<j>(); });
+    mark(0);
+
+    // ---- codebooks (copies, computed sign rows), Q8_K(x): LDS writes, one barrier
+    if constexpr (M == 3) {
+#pragma unroll
+        for (int i = 0; i < NX; ++i) {
+            const int c = t + NT * i;   // chunk c: sign row c / 16, copies 2(c % 16), +1
+            if (c < 4096) {
+                const uint2 r = sign_row(uint32_t(c) >> 4);
+                *reinterpret_cast<uint4*>(lds + LY::SGN + 16 * c) = make_uint4(r.x, r.y, r.x, r.y);
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < NX; ++i)
+            if (t + NT * i < 4096)
+                *reinterpret_cast<uint4*>(lds + LY::XXS + 16 * (t + NT * i)) = make_uint4(vx[i].x, vx[i].y, vx[i].x, vx[i].y);
+    } else if constexpr (MIX) {
+#pragma unroll
+        for (int i = 0; i < NX; ++i) {
+            const int c = t + NT * i;   // chunk c: row c / 16; pieces 0..7 grid copies, 8..15 sign copies
+            if (c < 4096) {
+                const uint2 r = (c & 8) ? sign_row(uint32_t(c) >> 4) : vx[i];
+                *reinterpret_cast<uint4*>(lds + LY::XXS + 16 * c) = make_uint4(r.x, r.y, r.x, r.y);
+            }
+        }
+    }
+    if constexpr (HASXS)
+#pragma unroll
+        for (int i = 0; i < NS; ++i)
+            if (t + NT * i < 1024)
+                *reinterpret_cast<uint4*>(lds + LY::XS + 16 * (t + NT * i)) = make_uint4(vs[i].x, vs[i].y, vs[i].x, vs[i].y);
+    if constexpr (HAS1)
+#pragma unroll
+        for (int i = 0; i < N1; ++i)
+            if (t + NT * i < 2048)
+                *reinterpret_cast<uint4*>(lds + LY::IQ1 + 16 * (t + NT * i)) = make_uint4(v1[i].x, v1[i].y, v1[i].z, v1[i].w);
+    mark(1);
+    {
+        uint4 xb[UX];
+        uint32_t xp[UX];
+        float xd[UX];
+#pragma unroll
+        for (int u = 0; u < UX; ++u)
+            xb[u] = make_uint4(__float_as_uint(xv[u].x), __float_as_uint(xv[u].y), __float_as_uint(xv[u].z),
+                               __float_as_uint(xv[u].w));
+        const bool fin = q8k_blocks<UX>(xb, nbx > wv ? (nbx - wv + NW - 1) / NW : 0, lane, xp, xd);
+        if (!fin && lane == 0) set_err(a.err, kDevErrNonFinite);
+#pragma unroll
+        for (int u = 0; u < UX; ++u) {
+            const int b = wv + NW * u;
+            if (b < nbx) {
+                *reinterpret_cast<uint32_t*>(lds + LY::XQ + qswz(256 * b + 4 * lane)) = xp[u];
+                if (lane == 0) reinterpret_cast<float*>(lds + LY::XQ + 4096)[b] = xd[u];
+            }
+        }
+    }
+    if (wv == 0) {
+        int rank = 0;   // the combine order (engine/strata/warm/runtime.cpp:183-188)
+        for (int j = 0; j < k; ++j) {
+            const int idj = __builtin_amdgcn_readlane(idv, j);
+            rank += (idj < idv) | ((idj == idv) & (j < lane));
+        }
+        if (lane < k) {
+            sm.ids[lane] = idv;
+            sm.w[lane] = cw;
+            sm.order[rank] = lane;
+        }
+    }
+    if (t == 0) sm.parity = (e_prev + 1u) & 1u;
+    lds_barrier();
+    if constexpr (TR) {   // workgroup 0's staged Q8_K(x), as the gate/up rows read it
+        if (blockIdx.x == 0 && a.tq8x)
+            for (int b = wv; b < nbx; b += NW)
+                trace_q8_block(a.tq8x + 292 * b, reinterpret_cast<const float*>(lds + LY::XQ + 4096)[b],
+                               *reinterpret_cast<const uint32_t*>(lds + LY::XQ + qswz(256 * b + 4 * lane)), lane);
+    }
+    const uint32_t parity = __builtin_amdgcn_readfirstlane(sm.parity);   // uniform: keeps buffer bases scalar
+    float* const hcur = a.hbuf + size_t(parity) * kHBufWords;
+    // The unit kernel (xl_unit.hip) shares the launch count: its partial counters
+    // of the other parity are cleared for the next launch, as it does itself.
+    if (a.ucnt && blockIdx.x == 0 && t < 8) coh_st32(a.ucnt + size_t(parity ^ 1u) * 256 + 32 * t, 0u);
+    // Arrival: the last workgroup to arrive advances the launch count at its end.
+    uint32_t arrived = 0;
+    if (t == 0) arrived = __hip_atomic_fetch_add(ctl + 1, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (gw < k && lane == 0) {
+        const int id = sm.ids[gw];
+        if (id < 0 || id >= a.n_experts) set_err(a.err, kDevErrExpertId);
+    }
+    // The other buffer (used by the previous launch) back to the sentinel for the next one.
+    {
+        float* const hnext = a.hbuf + size_t(parity ^ 1u) * kHBufWords;
+        const uint4 s4 = make_uint4(kSentinel, kSentinel, kSentinel, kSentinel);
+        for (int c = int(blockIdx.x) * NW * 64 + t; c < kHBufWords / 4; c += G * NW * 64)
+            reinterpret_cast<uint4*>(hnext)[c] = s4;
+    }
+    mark(2);
+
+    LoLanes lo;
+    {
+        constexpr uint32_t cmask = LY::CP > 0 ? uint32_t(LY::CP - 1) : 0u;
+        const uint32_t cp = (uint32_t(lane) & cmask) * 8u;
+        lo.g = cp | uint32_t(LY::XXS > 0 ? LY::XXS : 0);                              // table base in byte 2
+        lo.s = cp | uint32_t(LY::SGN > 0 ? LY::SGN : 0) | uint32_t(LY::SGN_IN_ROW);
+        lo.x = uint32_t(LY::XS > 0 ? LY::XS : 0) + uint32_t(lane & 3) * 8u;
+        asm volatile("" : "+v"(lo.x));   // opaque: keeps (x & mask) | lo.x one v_and_or_b32
+    }
+
+    Raw3 rd[WIND + 1][PD];
+    auto load_pass = [&]<int j>() {
+        const uint32_t m = dsl(j);
+#pragma unroll
+        for (int q = 0; q < PD; ++q) {
+            if constexpr (MIX)
+                load_pair3(rd[j % (WIND + 1)][q], mref(int((m >> 12) & 15u), 2, dim, nbh), int(m & 0xfffu), rD, lD + LD * q);
+            else
+                load_pair_t<DT>(rd[j % (WIND + 1)][q], matrix(int(m >> 16), 2, do1, do2, single_type<DT>(), nbh),
+                                int(m & 0xfffu), rD, lD + LD * q);
+        }
+    };
+
+    // ---- gate/up
+    {
+        Act<PG> A;
+        load_act<PG>(A, lds, LY::XQ, 4096, lG, LG);
+        constexpr bool NEEDNA = (GT & 1) != 0;
+        uint32_t NA[NEEDNA ? PG : 1][16];   // -q bytewise (q in -127..127, so no overflow)
+        if constexpr (NEEDNA)
+#pragma unroll
+            for (int q = 0; q < PG; ++q)
+#pragma unroll
+                for (int c = 0; c < 16; ++c) NA[q][c] = neg_bytes(A.a[q][c]);
+        float bg = 0.0f, bu = 0.0f;   // lane LG-1-b of each row group: slot b of the batch
+        int hidx = 0;                 // that slot's h word (pick * ff + row)
+        static_for<MG>([&]<int j>() {
+            // The SIMD arbiter favours older waves, so the first NW/2 waves of a
+            // workgroup would finish gate/up well before their SIMD partners (which
+            // then run alone, latency-bound, while the down phase waits for them).
+            // The younger half runs at wave priority 1 for the first two thirds of
+            // its slots, which evens out the finish times.
+            if constexpr (j == 0) {
+                if (wv >= NW / 2) __builtin_amdgcn_s_setprio(1);
+            }
+            if constexpr (j == (2 * MG) / 3) __builtin_amdgcn_s_setprio(0);
+            if constexpr (j >= 1 && j + WIN - 1 < MG) load_slot.template operator()<j + WIN - 1>();
+            if constexpr (j >= MG - WIND) load_pass.template operator()<j - (MG - WIND)>();   // the down stream starts under the last slots
+            int tg = 0, tu = 0;
+            if constexpr (MIX) {
+                const int pk = int((gsl(j) >> 12) & 15u);
+                tg = mtype(pk, 0);
+                tu = mtype(pk, 1);
+            }
+            float fg = 0.0f, fu = 0.0f;
+#pragma unroll
+            for (int q = 0; q < PG; ++q) {
+                const Raw3& G0 = rg[j % WIN][q];
+                const Raw3& U0 = ru[j % WIN][q];
+                const int pp = (lG + LG * q) & 3;
+                Looks Lg, Lu;
+                look_any<GT>(Lg, tg, lds, lo, G0);
+                look_any<GT>(Lu, tu, lds, lo, U0);
+                uint32_t dg, du;
+                const int Ig = sum_any<GT, NEEDNA>(tg, Lg, G0, A.a[q], NA[NEEDNA ? q : 0], pp, dg);
+                const int Iu = sum_any<GT, NEEDNA>(tu, Lu, U0, A.a[q], NA[NEEDNA ? q : 0], pp, du);
+                if constexpr (TR) {   // the row's block integers: a quad holds one block's four pairs
+                    const int bg = quad_isum(Ig), bu = quad_isum(Iu);
+                    if (a.tint && ((gok >> j) & 1u) && (lG & 3) == 0) {
+                        const uint32_t m = gsl(j);
+                        const size_t rec = size_t((m >> 12) & 15u) * (2 * size_t(ff) * nbx + size_t(dim) * nbh);
+                        const size_t o = rec + size_t(int(m & 0xfffu) + rG) * nbx + size_t((lG + LG * q) >> 2);
+                        a.tint[o] = bg;
+                        a.tint[o + size_t(ff) * nbx] = bu;
+                    }
+                }
+                fg = fmaf(__fmul_rn(h2f(dg), A.d[q]), float(Ig), fg);
+                fu = fmaf(__fmul_rn(h2f(du), A.d[q]), float(Iu), fu);
+            }
+            // A bad id read expert 0's rows: its h is published as 0 so that readers
+            // finish. The mask is applied by an opaque multiply: a select would let the
+            // compiler sink each row's whole decode into its own branch, serializing the
+            // gate and up rows.
+            float okf = ((gok >> j) & 1u) ? 1.0f : 0.0f;
+            asm volatile("" : "+v"(okf));
+            const float g = gsum<LG>(fg) * okf, u = gsum<LG>(fu) * okf;
+            const int b = j % kBatch;
+            const bool mine = lG == LG - 1 - b;
+            bg = mine ? g : bg;
+            bu = mine ? u : bu;
+            hidx = mine ? hrow(j) + rG : hidx;
+            if (b == kBatch - 1 || j == MG - 1) {
+                // (g / (1 + exp(-g))) * u with the device expf and an IEEE division, as
+                // q8k_core.hpp:92-95: an approximate exp or reciprocal moves h by an ulp
+                // often enough to flip Q8_K(h) quants (a 1e-4-scale output change each)
+                const float hv = silu_mul3(__fmul_rn(0.125f, bg), __fmul_rn(0.125f, bu), a.lim);
+                const uint32_t hb = __float_as_uint(hv) == kSentinel ? kQNaN : __float_as_uint(hv);
+                if (lG >= LG - 1 - b && hidx >= 0)
+                    __hip_atomic_store(reinterpret_cast<uint32_t*>(hcur) + hidx, hb, __ATOMIC_RELAXED,
+                                       __HIP_MEMORY_SCOPE_AGENT);
+                if constexpr (TR) {
+                    if (a.th && lG >= LG - 1 - b && hidx >= 0) a.th[hidx] = __uint_as_float(hb);
+                }
+            }
+            mark(8 + j);
+        });
+    }
+    mark(3);
+    __builtin_amdgcn_s_setprio(0);
+
+    // ---- down: step j quantizes the h of the picks it needs, then every wave runs pass j
+    float* ys = reinterpret_cast<float*>(lds + LY::Y);
+    const int hq_stride = ff + 64;
+    // picks [pk_lo(j), pk_hi(j)) are first needed at step j
+    auto pk_lo = [&](int j) { return min(k, (NW * j + nq_wg - 1) / nq_wg); };
+    auto pk_hi = [&](int j) { return min(k, (NW * j + NW + nq_wg - 1) / nq_wg); };
+    uint4 hv[2][MQ];   // h loads of steps j and j + 1 (issued two steps ahead)
+    auto h_issue = [&]<int j>() {   // loads of step j's blocks owned by this wave
+        const int b0 = pk_lo(j) * nbh, nb = pk_hi(j) * nbh - b0;
+#pragma unroll
+        for (int m = 0; m < MQ; ++m) {
+            const int bq = wv + NW * m;
+            const int blk = bq < nb ? b0 + bq : 0;   // unused slots re-read block 0
+            const int i = blk / nbh, bb = blk - i * nbh;
+            hv[j & 1][m] = h_load(hcur, uint32_t(i * ff + 256 * bb + 4 * lane));
+        }
+    };
+    h_issue.template operator()<0>();
+    if constexpr (MD > 1) h_issue.template operator()<1>();
+    lds_barrier();   // Q8_K(h) is staged over a region gate/up read: every wave is past gate/up
+    {
+        Act<PD> B;
+        static_for<MD>([&]<int j>() {
+            {   // steps past nsteps stage nothing and compute a discarded pass
+                // wait until this step's blocks are complete (all re-polled together), then
+                // quantize them into LDS
+                const int b0 = pk_lo(j) * nbh, nb = pk_hi(j) * nbh - b0;
+                auto all_ready = [&]() {
+                    bool ok = true;
+#pragma unroll
+                    for (int m = 0; m < MQ; ++m) ok = ok & ((wv + NW * m >= nb) | h_ready(hv[j & 1][m]));
+                    return __all(ok);
+                };
+                uint32_t polls = 0;
+                if (!all_ready()) {   // the common case never enters the retry loop
+                    do {
+                        if (++polls > kPollLimit) {
+                            if (lane == 0) set_err(a.err, kDevErrTimeout);
+                            break;
+                        }
+                        __builtin_amdgcn_s_sleep(2);
+                        h_issue.template operator()<j>();
+                    } while (!all_ready());
+                }
+                if (a.trace && lane == 0 && j < 4) a.trace[size_t(gw) * 32 + 20 + j] = polls;
+                mark(24 + 2 * j);
+                {
+                    uint32_t hp[MQ];
+                    float hd[MQ];
+                    const bool fin = q8k_blocks<MQ>(hv[j & 1], nb > wv ? (nb - wv + NW - 1) / NW : 0, lane, hp, hd);
+                    if (!fin && lane == 0) set_err(a.err, kDevErrNonFinite);
+#pragma unroll
+                    for (int m = 0; m < MQ; ++m) {
+                        const int bq = wv + NW * m;
+                        if (bq < nb) {
+                            const int blk = b0 + bq, i = blk / nbh, bb = blk - i * nbh;
+                            uint8_t* hq = lds + LY::HQ + i * hq_stride;
+                            *reinterpret_cast<uint32_t*>(hq + qswz(256 * bb + 4 * lane)) = hp[m];
+                            if (lane == 0) reinterpret_cast<float*>(hq + ff)[bb] = hd[m];
+                        }
+                    }
+                }
+                if (j < 3) mark(17 + j);
+                lds_barrier();
+                mark(25 + 2 * j);
+                if constexpr (j + 2 < MD) h_issue.template operator()<j + 2>();
+                {
+                    if constexpr (j + WIND < MD) load_pass.template operator()<j + WIND>();
+                    const int i = dpick(j);
+                    if (j == 0 || i != dpick(j > 0 ? j - 1 : 0)) load_act<PD>(B, lds, LY::HQ + i * hq_stride, ff, lD, LD);
+                    const int td = MIX ? mtype(i, 2) : 0;
+                    float f = 0.0f;
+                    Looks La, Lb;   // pair q's lookups in La (q even) or Lb; the next pair's are issued first
+                    look_any<DT>(La, td, lds, lo, rd[j % (WIND + 1)][0]);
+                    static_for<PD>([&]<int q>() {
+                        const Raw3& D0 = rd[j % (WIND + 1)][q];
+                        Looks& Lc = (q & 1) ? Lb : La;
+                        Looks& Ln = (q & 1) ? La : Lb;
+                        if constexpr (q + 1 < PD) look_any<DT>(Ln, td, lds, lo, rd[j % (WIND + 1)][q + 1]);
+                        uint32_t d16;
+                        const int I = sum_any<DT, false>(td, Lc, D0, B.a[q], nullptr, (lD + LD * q) & 3, d16);
+                        if constexpr (TR) {
+                            const int bi = quad_isum(I);
+                            if (a.tint && ((dok >> j) & 1u) && (lD & 3) == 0) {
+                                const uint32_t m = dsl(j);
+                                const size_t rec = size_t((m >> 12) & 15u) * (2 * size_t(ff) * nbx + size_t(dim) * nbh);
+                                a.tint[rec + 2 * size_t(ff) * nbx + size_t(int(m & 0xfffu) + rD) * nbh +
+                                       size_t((lD + LD * q) >> 2)] = bi;
+                            }
+                        }
+                        f = fmaf(__fmul_rn(h2f(d16), B.d[q]), float(I), f);
+                    });
+                    float okf = ((dok >> j) & 1u) ? 0.125f : 0.0f;   // opaque, as in gate/up
+                    asm volatile("" : "+v"(okf));
+                    const float y = __fmul_rn(okf, gsum<LD>(f));
+                    if (j < nd && lD == LD - 1) ys[(wv + NW * j) * RD + rD] = y;
+                }
+                if (j == 0) mark(5);
+            }
+        });
+    }
+    mark(6);
+    lds_barrier();
+    if constexpr (TR) {   // workgroup 0's staged Q8_K(h) of every pick, as its down passes read it
+        if (blockIdx.x == 0 && a.tq8h)
+            for (int blk = wv; blk < k * nbh; blk += NW) {
+                const int i = blk / nbh, bb = blk - i * nbh;
+                const uint8_t* hq = lds + LY::HQ + i * hq_stride;
+                trace_q8_block(a.tq8h + 292 * blk, reinterpret_cast<const float*>(hq + ff)[bb],
+                               *reinterpret_cast<const uint32_t*>(hq + qswz(256 * bb + 4 * lane)), lane);
+            }
+    }
+
+    // ---- fixed-order combine of this workgroup's rows
+    const int nrows = nq_wg * RD;
+    for (int r = t; r < nrows; r += NW * 64) {
+        const int qq = r / RD, rr = r - qq * RD;
+        const int orow = (int(blockIdx.x) + G * qq) * RD + rr;
+        float acc = 0.0f;
+        for (int s2 = 0; s2 < k; ++s2) {
+            const int i = sm.order[s2];
+            acc = fmaf(sm.w[i], ys[(i * nq_wg + qq) * RD + rr], acc);
+        }
+        if (a.shared) acc = __fadd_rn(acc, a.shared[orow]);
+        a.out[orow] = acc;
+    }
+    mark(7);
+    if (t == 0 && arrived == uint32_t(G) - 1u) {   // every workgroup has read the launch count
+        coh_st32(ctl, e_prev + 1u);
+        coh_st32(ctl + 1, 0u);
+    }
+}
+
+template <int NW, int LG, int PG, int LD, int PD, int MG, int MD, int WIN, int WIND, int MQ, int GT, int DT>
+hipError_t launch_stream_t(const Layer3Args& args, int grid, hipStream_t s, hipEvent_t stop) {
+    constexpr int M = (GT == 1 && DT == 2) ? 3 : (GT == 4 && DT == 4) ? 4 : 7;
+    const bool tr = args.tq8x || args.tq8h || args.th || args.tint;
+    constexpr int RG = 64 / LG, RD = 64 / LD;
+    const int W = grid * NW;
+    const int SG = args.k * (args.ff / RG);
+    const int quads = args.dim / RD;
+    const int nq_wg = (quads + grid - 1) / grid;
+    const int P = args.k * nq_wg;
+    const int nbh = args.ff / 256;
+    // most blocks one step needs: the picks first needed by NW consecutive passes,
+    // in workgroups owning quads / grid and quads / grid + 1 row groups
+    int most = 0;
+    for (int nq = quads / grid; nq <= nq_wg; ++nq)
+        for (int j = 0; j * NW < args.k * nq; ++j) {
+            const int lo = std::min(args.k, (NW * j + nq - 1) / nq);
+            const int hi = std::min(args.k, (NW * j + NW + nq - 1) / nq);
+            most = std::max(most, (hi - lo) * nbh);
+        }
+    if ((SG + W - 1) / W > MG || args.n_experts > 65536 || args.dim > 4096 || args.ff > 4096 ||
+        (P + NW - 1) / NW > MD || (most + NW - 1) / NW > MQ || P * RD > kS_YFloats || grid > quads ||
+        args.k * (args.ff + 64) > SLay<M>::HQBytes || args.k * args.ff > kHBufWords || !args.hbuf ||
+        (M != 7 && !args.slab) || (M == 7 && !args.slab && !args.descs))
+        return hipErrorNotSupported;
+    if (tr)
+        hipExtLaunchKernelGGL((stream_kernel<NW, LG, PG, LD, PD, MG, MD, WIN, WIND, MQ, GT, DT, true>), dim3(grid),
+                              dim3(NW * 64), 0, s, nullptr, stop, 0, args);
+    else
+        hipExtLaunchKernelGGL((stream_kernel<NW, LG, PG, LD, PD, MG, MD, WIN, WIND, MQ, GT, DT, false>), dim3(grid),
+                              dim3(NW * 64), 0, s, nullptr, stop, 0, args);
+    return hipGetLastError();
+}
+
+// Instances by shape and pick count for one (GT, DT).
+template <int GT, int DT>
+hipError_t launch_stream_shapes(const Layer3Args& args, int cus, hipStream_t s, hipEvent_t stop) {
+    if (args.k < 1 || args.k > 16 || args.dim > 4096 || args.ff > 4096) return hipErrorNotSupported;
+    int lg, pg, ld, pd;
+    if (!row_shape(args.dim, lg, pg) || !row_shape(args.ff, ld, pd)) return hipErrorNotSupported;
+    const int RD = 64 / ld;
+    const int grid = std::min(cus, args.dim / RD);
+    if (lg == 64 && pg == 1 && ld == 16 && pd == 3) {   // 4096 x 3072: slots and steps sized by the pick count
+        if (args.k <= 2) return launch_stream_t<8, 64, 1, 16, 3, 3, 1, 3, 1, 3, GT, DT>(args, grid, s, stop);
+        if (args.k <= 4) return launch_stream_t<8, 64, 1, 16, 3, 6, 2, 3, 2, 3, GT, DT>(args, grid, s, stop);
+        return launch_stream_t<8, 64, 1, 16, 3, 9, 3, 3, 3, 3, GT, DT>(args, grid, s, stop);
+    }
+    if (lg == 16 && pg == 1 && ld == 8 && pd == 1)    // 1024 x 512
+        return launch_stream_t<8, 16, 1, 8, 1, 6, 2, 3, 1, 2, GT, DT>(args, grid, s, stop);
+    if (lg == 4 && pg == 1 && ld == 4 && pd == 3)     // 256 x 768
+        return launch_stream_t<8, 4, 1, 4, 3, 6, 2, 3, 1, 3, GT, DT>(args, grid, s, stop);
+    return hipErrorNotSupported;
+}
+
+}  // namespace
+}  // namespace xl::dev

@@ -263,9 +263,9 @@ def test_matvec_any_fp16_scale(probe, orc, t):
                                         (1024, 512, (16, 16, 17)), (256, 768, (16, 16, 17)),
                                         (256, 768, (29, 29, 17)), (512, 256, (16, 16, 29)), (256, 256, (17, 17, 17))])
 def test_layer_paths_agree(orc, dim, ff, sig, monkeypatch):
-    # The single-launch kernels (path 1: the streaming kernel where the types
-    # are IQ2_XXS gate/up + IQ2_XS down, else the all-types one; path 3: the
-    # all-types one only), the separate launches (path 0) and the cooperative
+    # The single-launch kernels (path 1: the streaming kernel where one of its
+    # instances fits the shape, else the all-types one; path 3: the all-types
+    # one only), the separate launches (path 0) and the cooperative
     # kernel (path 2) share the row arithmetic per block but sum lanes in their
     # own orders, so they agree to the tolerance, and each is bit-identical run
     # to run; the oracle checks every path.
@@ -303,17 +303,34 @@ def test_layer_paths_agree(orc, dim, ff, sig, monkeypatch):
             lane.close()
 
 
-@pytest.mark.parametrize("dim,ff,k", [(4096, 3072, 6), (4096, 3072, 5), (4096, 3072, 4), (4096, 3072, 3),
-                                      (4096, 3072, 2), (4096, 3072, 1), (1024, 512, 8),
-                                      (1024, 512, 12), (1024, 512, 16), (256, 768, 6), (256, 768, 12)])
-def test_streaming_kernel_pick_counts(orc, dim, ff, k, monkeypatch):
+def kind_types(kind, E, seed=0):
+    """Layer type maps by kind: IQ2_XXS gate/up + IQ2_XS down, IQ1_M only, or a
+    per-expert mix of the three types (every type present)."""
+    if kind == "iq2":
+        return types_map(1, E, 16, 17)
+    if kind == "iq1":
+        return types_map(1, E, 29, 29)
+    t = np.random.default_rng(seed + E).choice([16, 17, 29], size=E)
+    t[:3] = [16, 17, 29]
+    return np.repeat(t.reshape(1, E, 1), 3, axis=-1).astype(np.int32)
+
+
+STREAM_CASES = [(4096, 3072, 6), (4096, 3072, 5), (4096, 3072, 4), (4096, 3072, 3), (4096, 3072, 2),
+                (4096, 3072, 1), (1024, 512, 8), (1024, 512, 12), (1024, 512, 16), (256, 768, 6), (256, 768, 12)]
+STREAM_CASES_OTHER = [(4096, 3072, 6), (4096, 3072, 4), (4096, 3072, 1), (1024, 512, 16), (256, 768, 12)]
+
+
+@pytest.mark.parametrize("kind,dim,ff,k", [("iq2",) + c for c in STREAM_CASES] +
+                         [(kd,) + c for kd in ("iq1", "mixed") for c in STREAM_CASES_OTHER])
+def test_streaming_kernel_pick_counts(orc, kind, dim, ff, k, monkeypatch):
     # XL_LAYER_PATH=4 runs the streaming kernel or fails: pick counts that give
     # one, two or three down steps and steps staging one to eight picks must
-    # match the oracle and repeat bit for bit.
-    step(f"streaming kernel dim={dim} ff={ff} k={k}")
+    # match the oracle and repeat bit for bit, for the IQ2 instance, the IQ1_M
+    # instance and the mixed-type instance (matrices from descriptors).
+    step(f"streaming kernel {kind} dim={dim} ff={ff} k={k}")
     E = 24
     rng = np.random.default_rng(dim + ff + k)
-    types = types_map(1, E, 16, 17)
+    types = kind_types(kind, E)
     monkeypatch.setenv("XL_LAYER_PATH", "4")
     lane = xl.Lane(dim, ff, 1, E, types, max_picks=16)
     try:
@@ -322,8 +339,10 @@ def test_streaming_kernel_pick_counts(orc, dim, ff, k, monkeypatch):
             ids, w = route(rng.standard_normal(E).astype(np.float32), k)
             x = rng.standard_normal(dim).astype(np.float32)
             shared = rng.standard_normal(dim).astype(np.float32) if trial else None
-            rows = [orc.expert((16, 16, 17), *orc.gen_expert((16, 16, 17), 91, 0, int(e), dim, ff), dim, ff, x)
-                    for e in ids]
+            rows = []
+            for e in ids:
+                sig = tuple(int(v) for v in types[0, e])
+                rows.append(orc.expert(sig, *orc.gen_expert(sig, 91, 0, int(e), dim, ff), dim, ff, x))
             want = orc.combine(ids, w, np.stack(rows), shared)
             got = lane.layer_forward(0, ids, w, x, shared)
             again = lane.layer_forward(0, ids, w, x, shared)

@@ -3,8 +3,9 @@
 The north star's exact bars (Q8_K activation bytes and per-block int32
 partials) are checked here on what the hot kernels themselves stage and form,
 through the parity trace (xl_layer_trace_async, xl_grouped_trace_async): the
-streaming kernel (configs 0 and 1), the unit kernel, the all-types kernel with its IQ2, IQ1_M
-and mixed-type instances (configs 2 and 3), and the grouped MFMA kernels
+streaming kernel with its IQ2, IQ1_M and mixed-type instances (configs 0 to
+3), the unit kernel, the all-types kernel with its IQ2, IQ1_M and mixed-type
+instances, and the grouped MFMA kernels
 (config 4). For each launch:
 
 * Q8_K(x) as staged: the 292-byte blocks equal the oracle's quant_block of x
@@ -63,9 +64,15 @@ LAYER_CASES = [
     ("5", 4096, 3072, 12, 3, "iq2", 5),
     ("5", 4096, 3072, 12, 8, "iq2", 5),
     ("1", 1024, 512, 8, 6, "iq2", 1),
+    ("1", 4096, 3072, 12, 6, "iq1", 1),     # config 2: the streaming kernel's IQ1_M instance
+    ("1", 4096, 3072, 12, 6, "mixed", 1),   # config 3: its mixed instance (descriptors)
+    ("4", 4096, 3072, 12, 1, "iq1", 1),
+    ("4", 4096, 3072, 12, 3, "mixed", 1),
+    ("4", 1024, 512, 8, 8, "mixed", 1),
+    ("4", 256, 768, 6, 5, "iq1", 1),
     ("3", 4096, 3072, 12, 6, "iq2", 3),     # all-types kernel, IQ2 instance
-    ("3", 4096, 3072, 12, 6, "iq1", 3),     # config 2: IQ1_M-only instance
-    ("3", 4096, 3072, 12, 6, "mixed", 3),   # config 3: mixed types, descriptors
+    ("3", 4096, 3072, 12, 6, "iq1", 3),     # IQ1_M-only instance
+    ("3", 4096, 3072, 12, 6, "mixed", 3),   # mixed types, descriptors
     ("3", 1024, 512, 8, 5, "mixed", 3),
     ("3", 256, 768, 6, 4, "iq1", 3),
 ]

@@ -144,7 +144,7 @@ __device__ __forceinline__ float silu_mul3(float g, float u, float lim) {
 // The 16-bit loads stay 16-bit until used: widening them where they are loaded
 // would make the load's wave wait for it (and for every load before it).
 struct Raw3 {
-    uint32_t w[5];
+    uint32_t w[7];
     uint16_t h[2];
 };
 // Plane offsets of a matrix of NB blocks (plane_layout in xl_format.hpp).
@@ -211,28 +211,6 @@ __device__ __forceinline__ void load_pair_t(Raw3& r, const MRef& m, int row0, in
     else if constexpr (TM == 2) load_pair(r, kIQ2_XS, m, row0, pair_off(kIQ2_XS, m.nb, rG, p));
     else if constexpr (TM == 4) load_pair(r, kIQ1_M, m, row0, pair_off(kIQ1_M, m.nb, rG, p));
     else load_pair(r, m.type, m, row0, pair_off(m.type, m.nb, rG, p));
-}
-
-// Pair p of row row0 + rG of a matrix of any type, by exactly three loads (an
-// IQ2_XXS pair reads its block scale twice), so that a kernel whose slots differ
-// in type keeps exact wait counts whichever type each slot has.
-__device__ __forceinline__ void load_pair3(Raw3& r, const MRef& m, int row0, int rG, int p) {
-    const PairOff po = pair_off(m.type, m.nb, rG, p);
-    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc((void*)m.base, (short)0, -1, 0x00020000);
-    const uint32_t rb = uint32_t(row0) * uint32_t(m.nb);
-    if (m.type == kIQ1_M) {
-        const v2u32 q = __builtin_amdgcn_raw_buffer_load_b64(rs, po.q, rb * 32, kNT);
-        r.w[2] = __builtin_amdgcn_raw_buffer_load_b32(rs, po.a, m.o1 + rb * 16, kNT);
-        const v2u32 sw = __builtin_amdgcn_raw_buffer_load_b64(rs, po.b, m.o2 + rb * 8, kNT);
-        r.w[0] = q.x; r.w[1] = q.y;
-        r.w[3] = sw.x; r.w[4] = sw.y;
-    } else {
-        const v4u32 q = __builtin_amdgcn_raw_buffer_load_b128(rs, po.q, rb * 64, kNT);
-        r.w[0] = q.x; r.w[1] = q.y; r.w[2] = q.z; r.w[3] = q.w;
-        const bool xs = m.type == kIQ2_XS;
-        r.h[0] = __builtin_amdgcn_raw_buffer_load_b16(rs, po.a, m.o1 + rb * (xs ? 8u : 2u), kNT);
-        r.h[1] = __builtin_amdgcn_raw_buffer_load_b16(rs, xs ? po.b : po.a, xs ? m.o2 + rb * 2 : m.o1 + rb * 2, kNT);
-    }
 }
 
 // 2s+1 from the four scale bits stored in bit 7 of each sign byte.

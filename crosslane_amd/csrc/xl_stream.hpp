@@ -116,32 +116,148 @@ constexpr bool one_type() { return TM == 1 || TM == 2 || TM == 4; }
 struct LoLanes {
     uint32_t g, s, x;
 };
-// Lookups of one pair of type `type` (TM: the matrix's type mask; one bit = known
-// at compile time, else the wave-uniform runtime type picks the decoder).
-template <int TM>
-__device__ __forceinline__ void look_any(Looks& L, int type, const uint8_t* lds, const LoLanes& lo, const Raw3& r) {
-    const int t = one_type<TM>() ? single_type<TM>() : type;
-    if ((TM & 1) && t == kIQ2_XXS) look_xxs_to(L, lds, lo.g, lo.s, r.w);
-    else if ((TM & 2) && t == kIQ2_XS) look_xs_to(L, lds, lo.x, lo.s, r.w);
+
+// Pair loads of the mixed instance: the same three loads whatever the type
+// (no branch: register copies where branches merge, and wait counts made
+// inexact by them, would wait for the loads), their offsets chosen by the
+// wave-uniform type: b128 of code bytes (IQ2: the pair's 16; IQ1_M: its 8
+// index bytes and the next pair's 8), b32 (IQ2_XXS: the aligned word holding
+// its block's fp16 scale; IQ2_XS: the word holding the pair's scale bytes;
+// IQ1_M: its nibble word) and b64 (IQ2_XS: the aligned 4 block scales holding
+// its block's; IQ1_M: the block's scale words; IQ2_XXS: 8 code bytes again,
+// unused). Every read stays inside the matrix: the row groups start at a
+// multiple of 4 blocks and each plane holds a multiple of 4 blocks.
+// The per-(pick, role) constants are packed as (MixLoad):
+//   voffsets  e << s1, (e >> r2) << 2, (e >> r3) << 3 (e: the pair's index in its row group)
+//   soffsets  rb << t1, c2 + (rb << t2), c3 + (rb << t3) (rb: blocks before the row group)
+struct MixLoad {
+    uint32_t code;   // s1 | r2 << 4 | r3 << 8 | t1 << 12 | t2 << 16 | t3 << 20
+    uint32_t c2, c3;
+};
+__device__ __forceinline__ MixLoad mix_load(int type, uint32_t o1, uint32_t o2) {
+    MixLoad L;
+    if (type == kIQ2_XXS) {
+        L.code = 4u | (3u << 4) | (4u << 8) | (6u << 12) | (1u << 16) | (6u << 20);
+        L.c2 = o1; L.c3 = 0;
+    } else if (type == kIQ2_XS) {
+        L.code = 4u | (1u << 4) | (4u << 8) | (6u << 12) | (3u << 16) | (1u << 20);
+        L.c2 = o1; L.c3 = o2;
+    } else {
+        L.code = 3u | (0u << 4) | (2u << 8) | (5u << 12) | (4u << 16) | (3u << 20);
+        L.c2 = o1; L.c3 = o2;
+    }
+    return L;
+}
+__device__ __forceinline__ void load_pair_u(Raw3& r, const uint8_t* base, uint32_t code, uint32_t c2, uint32_t c3,
+                                            uint32_t rb, uint32_t e, uint32_t dq) {
+    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc((void*)base, (short)0, -1, 0x00020000);
+    const uint32_t s1 = code & 15u, r2 = (code >> 4) & 15u, r3 = (code >> 8) & 15u;
+    const uint32_t t1 = (code >> 12) & 15u, t2 = (code >> 16) & 15u, t3 = (code >> 20) & 15u;
+    const uint32_t ee = e + dq;   // (dq: pairs past the lane's first)
+    const v4u32 q = __builtin_amdgcn_raw_buffer_load_b128(rs, ee << s1, rb << t1, kNT);
+    r.w[4] = __builtin_amdgcn_raw_buffer_load_b32(rs, (ee >> r2) << 2, c2 + (rb << t2), kNT);
+    const v2u32 v = __builtin_amdgcn_raw_buffer_load_b64(rs, (ee >> r3) << 3, c3 + (rb << t3), kNT);
+    r.w[0] = q.x; r.w[1] = q.y; r.w[2] = q.z; r.w[3] = q.w;
+    r.w[5] = v.x; r.w[6] = v.y;
+}
+// The fields of a pair loaded by load_pair_u, as the decoders of type T read
+// them: pair p of a row group whose first block is bq mod 4.
+template <int T>
+__device__ __forceinline__ Raw3 mix_view(const Raw3& r, int bq, int p) {
+    Raw3 v = r;
+    const uint32_t blk = uint32_t(bq + (p >> 2));   // the block mod 4 (within its aligned group)
+    if constexpr (T == 1) {
+        v.h[0] = uint16_t(r.w[4] >> ((blk & 1u) << 4));
+    } else if constexpr (T == 2) {
+        v.h[0] = uint16_t(r.w[4] >> (uint32_t(p & 1) << 4));
+        v.h[1] = uint16_t(((blk & 2u) ? r.w[6] : r.w[5]) >> ((blk & 1u) << 4));
+    } else {
+        v.w[2] = r.w[4];
+        v.w[3] = r.w[5]; v.w[4] = r.w[6];
+    }
+    return v;
+}
+
+// Lookups and exact integer of one pair of static type T (1 IQ2_XXS, 2 IQ2_XS,
+// 4 IQ1_M); NA: IQ2_XXS takes its signs on the negated activations na, else
+// on the grid; pp: the pair's place in its block; d16: its fp16 scale.
+template <int T>
+__device__ __forceinline__ void look_t(Looks& L, const uint8_t* lds, const LoLanes& lo, const Raw3& r) {
+    if constexpr (T == 1) look_xxs_to(L, lds, lo.g, lo.s, r.w);
+    else if constexpr (T == 2) look_xs_to(L, lds, lo.x, lo.s, r.w);
     else look_iq1_to(L, lds, r.w);
 }
-// The pair's exact integer against quants a (na: their negations, used by
-// IQ2_XXS when NA; without, its signs go on the grid) and its fp16 scale.
-template <int TM, bool NA>
-__device__ __forceinline__ int sum_any(int type, const Looks& L, const Raw3& r, const uint32_t* a, const uint32_t* na,
-                                       int pp, uint32_t& d16) {
-    const int t = one_type<TM>() ? single_type<TM>() : type;
-    if ((TM & 1) && t == kIQ2_XXS) {
+template <int T, bool NA>
+__device__ __forceinline__ int sum_t(const Looks& L, const Raw3& r, const uint32_t* a, const uint32_t* na, int pp,
+                                     uint32_t& d16) {
+    if constexpr (T == 1) {
         d16 = r.h[0];
         if constexpr (NA) return sum_xxs(L, r.w, a, na);
         else return sum_xxs_g(L, r.w, a);
-    }
-    if ((TM & 2) && t == kIQ2_XS) {
+    } else if constexpr (T == 2) {
         d16 = r.h[1];
         return sum_xs(L, r.h[0], a);
+    } else {
+        d16 = iq1_d16(r.w);
+        return sum_iq1(L, iq1_scw(r.w, pp), a);
     }
-    d16 = iq1_d16(r.w);
-    return sum_iq1(L, iq1_scw(r.w, pp), a);
+}
+// A pair as the decoders of type T read it (V: loaded by load_pair_u; bq, p as mix_view).
+template <int T, bool V>
+__device__ __forceinline__ Raw3 pair_view(const Raw3& r, int bq, int p) {
+    if constexpr (V) return mix_view<T>(r, bq, p);
+    else return r;
+}
+// Gate and up rows of one slot, static types TG_ / TU_: both rows' lookups
+// are issued before either row's arithmetic.
+template <int TG_, int TU_, bool V, int PG, int NQ>
+__device__ __forceinline__ void decode_slot(int (&Ig)[PG], int (&Iu)[PG], uint32_t (&dg)[PG], uint32_t (&du)[PG],
+                                            const Raw3 (&G)[PG], const Raw3 (&U)[PG], const Act<PG>& A,
+                                            const uint32_t (&NA)[NQ][16], const uint8_t* lds, const LoLanes& lo,
+                                            int lG, int LG, int bq) {
+#pragma unroll
+    for (int q = 0; q < PG; ++q) {
+        const int p = lG + LG * q, pp = p & 3;
+        const Raw3 g = pair_view<TG_, V>(G[q], bq, p), u = pair_view<TU_, V>(U[q], bq, p);
+        Looks Lg, Lu;
+        look_t<TG_>(Lg, lds, lo, g);
+        look_t<TU_>(Lu, lds, lo, u);
+        Ig[q] = sum_t<TG_, true>(Lg, g, A.a[q], NA[NQ > 1 ? q : 0], pp, dg[q]);
+        Iu[q] = sum_t<TU_, true>(Lu, u, A.a[q], NA[NQ > 1 ? q : 0], pp, du[q]);
+    }
+}
+// One row of a slot whose gate and up types differ (mixed instance), type t at run time.
+template <int PG, int NQ>
+__device__ __forceinline__ void decode_row(int t, int (&I)[PG], uint32_t (&d)[PG], const Raw3 (&R)[PG],
+                                           const Act<PG>& A, const uint32_t (&NA)[NQ][16], const uint8_t* lds,
+                                           const LoLanes& lo, int lG, int LG, int bq) {
+    auto one = [&]<int T>() {
+#pragma unroll
+        for (int q = 0; q < PG; ++q) {
+            const Raw3 r = pair_view<T, true>(R[q], bq, lG + LG * q);
+            Looks L;
+            look_t<T>(L, lds, lo, r);
+            I[q] = sum_t<T, true>(L, r, A.a[q], NA[NQ > 1 ? q : 0], (lG + LG * q) & 3, d[q]);
+        }
+    };
+    if (t == kIQ2_XXS) one.template operator()<1>();
+    else if (t == kIQ2_XS) one.template operator()<2>();
+    else one.template operator()<4>();
+}
+// A down pass (PD pairs per lane) of static type T: the next pair's lookups are
+// issued before the current pair's arithmetic.
+template <int T, bool V, int PD>
+__device__ __forceinline__ void decode_pass(int (&I)[PD], uint32_t (&d)[PD], const Raw3 (&R)[PD], const Act<PD>& B,
+                                            const uint8_t* lds, const LoLanes& lo, int lD, int LD, int bq) {
+    Looks La, Lb;
+    look_t<T>(La, lds, lo, pair_view<T, V>(R[0], bq, lD));
+    static_for<PD>([&]<int q>() {
+        const Raw3 r = pair_view<T, V>(R[q], bq, lD + LD * q);
+        Looks& Lc = (q & 1) ? Lb : La;
+        Looks& Ln = (q & 1) ? La : Lb;
+        if constexpr (q + 1 < PD) look_t<T>(Ln, lds, lo, pair_view<T, V>(R[q + 1], bq, lD + LD * (q + 1)));
+        I[q] = sum_t<T, false>(Lc, r, B.a[q], nullptr, (lD + LD * q) & 3, d[q]);
+    });
 }
 
 // ---- the kernel ----------------------------------------------------------------------------
@@ -224,6 +340,7 @@ __global__ __launch_bounds__(NW * 64, 1) void stream_kernel(Layer3Args a) {
         return MRef{a.slab + uint64_t(e) * a.estride + a.roff[role], o1, o2, type, nb};
     };
     uint32_t tb_lo = 0, tb_hi = 0;
+    MixLoad tb_ml{};
     int tb_ty = 0;
     if constexpr (MIX) {
         const int ti = lane & 15, tr = min(lane >> 4, 2);
@@ -240,18 +357,33 @@ __global__ __launch_bounds__(NW * 64, 1) void stream_kernel(Layer3Args a) {
         }
         tb_lo = uint32_t(base);
         tb_hi = uint32_t(base >> 32);
+        // plane offsets from the type and the role's shape (gate/up: ff rows of nbx
+        // blocks, down: dim rows of nbh blocks), then the load constants, once here
+        // rather than per slot
+        uint32_t o1, o2;
+        plane_offs(tb_ty, tr < 2 ? uint64_t(ff) * uint64_t(nbx) : uint64_t(dim) * uint64_t(nbh), o1, o2);
+        tb_ml = mix_load(tb_ty, o1, o2);
     }
-    // pick i's matrix of a role (mixed instance): type from the lane table, planes from the shape
-    auto mref = [&](int pick, int role, int rows, int nb) {
+    // pick i's matrix of a role (mixed instance), from the lane table: base and load constants
+    struct MixRef {
+        const uint8_t* base;
+        uint32_t code, c2, c3;
+    };
+    auto mref = [&](int pick, int role) {
         const int L = 16 * role + pick;
-        MRef m;
+        MixRef m;
         m.base = reinterpret_cast<const uint8_t*>((uint64_t(uint32_t(__builtin_amdgcn_readlane(int(tb_hi), L))) << 32) |
                                                   uint32_t(__builtin_amdgcn_readlane(int(tb_lo), L)));
-        m.type = __builtin_amdgcn_readlane(tb_ty, L);
-        m.nb = nb;
-        plane_offs(m.type, uint64_t(rows) * uint64_t(nb), m.o1, m.o2);
+        m.code = uint32_t(__builtin_amdgcn_readlane(int(tb_ml.code), L));
+        m.c2 = uint32_t(__builtin_amdgcn_readlane(int(tb_ml.c2), L));
+        m.c3 = uint32_t(__builtin_amdgcn_readlane(int(tb_ml.c3), L));
         return m;
     };
+    // The lanes' pair indices in their row groups (gate/up; down pass pair 0, the
+    // others LD * q further, which enters the scalar offsets) and the first block
+    // of their row groups mod 4.
+    const uint32_t eg = uint32_t(rG * nbx * 4 + lG), ed = uint32_t(rD * nbh * 4 + lD);
+    const int bqg = (rG * nbx) & 3, bqd = (rD * nbh) & 3;
     auto mtype = [&](int pick, int role) { return __builtin_amdgcn_readlane(tb_ty, 16 * role + pick); };
 
     // ---- codebook rows and x first (they need no ids), then the first slots. The
@@ -298,8 +430,10 @@ __global__ __launch_bounds__(NW * 64, 1) void stream_kernel(Layer3Args a) {
         for (int q = 0; q < PG; ++q) {
             if constexpr (MIX) {
                 const int pk = int((m >> 12) & 15u);
-                load_pair3(rg[b][q], mref(pk, 0, ff, nbx), row0, rG, lG + LG * q);
-                load_pair3(ru[b][q], mref(pk, 1, ff, nbx), row0, rG, lG + LG * q);
+                const uint32_t rb = uint32_t(row0) * uint32_t(nbx);
+                const MixRef mg = mref(pk, 0), mu = mref(pk, 1);
+                load_pair_u(rg[b][q], mg.base, mg.code, mg.c2, mg.c3, rb, eg, uint32_t(LG * q));
+                load_pair_u(ru[b][q], mu.base, mu.code, mu.c2, mu.c3, rb, eg, uint32_t(LG * q));
             } else {
                 load_pair_t<GT>(rg[b][q], matrix(e, 0, go1, go2, single_type<GT>(), nbx), row0, rG, lG + LG * q);
                 load_pair_t<GT>(ru[b][q], matrix(e, 1, go1, go2, single_type<GT>(), nbx), row0, rG, lG + LG * q);
@@ -421,9 +555,11 @@ __global__ __launch_bounds__(NW * 64, 1) void stream_kernel(Layer3Args a) {
         const uint32_t m = dsl(j);
 #pragma unroll
         for (int q = 0; q < PD; ++q) {
-            if constexpr (MIX)
-                load_pair3(rd[j % (WIND + 1)][q], mref(int((m >> 12) & 15u), 2, dim, nbh), int(m & 0xfffu), rD, lD + LD * q);
-            else
+            if constexpr (MIX) {
+                const MixRef md = mref(int((m >> 12) & 15u), 2);
+                load_pair_u(rd[j % (WIND + 1)][q], md.base, md.code, md.c2, md.c3, uint32_t(m & 0xfffu) * uint32_t(nbh),
+                            ed, uint32_t(LD * q));
+            } else
                 load_pair_t<DT>(rd[j % (WIND + 1)][q], matrix(int(m >> 16), 2, do1, do2, single_type<DT>(), nbh),
                                 int(m & 0xfffu), rD, lD + LD * q);
         }
@@ -434,7 +570,7 @@ __global__ __launch_bounds__(NW * 64, 1) void stream_kernel(Layer3Args a) {
         Act<PG> A;
         load_act<PG>(A, lds, LY::XQ, 4096, lG, LG);
         constexpr bool NEEDNA = (GT & 1) != 0;
-        uint32_t NA[NEEDNA ? PG : 1][16];   // -q bytewise (q in -127..127, so no overflow)
+        uint32_t NA[PG][16];   // -q bytewise (q in -127..127, so no overflow); unused without IQ2_XXS
         if constexpr (NEEDNA)
 #pragma unroll
             for (int q = 0; q < PG; ++q)
@@ -460,20 +596,23 @@ __global__ __launch_bounds__(NW * 64, 1) void stream_kernel(Layer3Args a) {
                 tg = mtype(pk, 0);
                 tu = mtype(pk, 1);
             }
+            int Ig[PG], Iu[PG];
+            uint32_t dg[PG], du[PG];
+            if constexpr (!MIX) {
+                decode_slot<GT, GT, false>(Ig, Iu, dg, du, rg[j % WIN], ru[j % WIN], A, NA, lds, lo, lG, LG, 0);
+            } else if (tg == tu) {   // one branch per slot, static types inside
+                if (tg == kIQ2_XXS) decode_slot<1, 1, true>(Ig, Iu, dg, du, rg[j % WIN], ru[j % WIN], A, NA, lds, lo, lG, LG, bqg);
+                else if (tg == kIQ2_XS) decode_slot<2, 2, true>(Ig, Iu, dg, du, rg[j % WIN], ru[j % WIN], A, NA, lds, lo, lG, LG, bqg);
+                else decode_slot<4, 4, true>(Ig, Iu, dg, du, rg[j % WIN], ru[j % WIN], A, NA, lds, lo, lG, LG, bqg);
+            } else {
+                decode_row(tg, Ig, dg, rg[j % WIN], A, NA, lds, lo, lG, LG, bqg);
+                decode_row(tu, Iu, du, ru[j % WIN], A, NA, lds, lo, lG, LG, bqg);
+            }
             float fg = 0.0f, fu = 0.0f;
 #pragma unroll
             for (int q = 0; q < PG; ++q) {
-                const Raw3& G0 = rg[j % WIN][q];
-                const Raw3& U0 = ru[j % WIN][q];
-                const int pp = (lG + LG * q) & 3;
-                Looks Lg, Lu;
-                look_any<GT>(Lg, tg, lds, lo, G0);
-                look_any<GT>(Lu, tu, lds, lo, U0);
-                uint32_t dg, du;
-                const int Ig = sum_any<GT, NEEDNA>(tg, Lg, G0, A.a[q], NA[NEEDNA ? q : 0], pp, dg);
-                const int Iu = sum_any<GT, NEEDNA>(tu, Lu, U0, A.a[q], NA[NEEDNA ? q : 0], pp, du);
                 if constexpr (TR) {   // the row's block integers: a quad holds one block's four pairs
-                    const int bg = quad_isum(Ig), bu = quad_isum(Iu);
+                    const int bg = quad_isum(Ig[q]), bu = quad_isum(Iu[q]);
                     if (a.tint && ((gok >> j) & 1u) && (lG & 3) == 0) {
                         const uint32_t m = gsl(j);
                         const size_t rec = size_t((m >> 12) & 15u) * (2 * size_t(ff) * nbx + size_t(dim) * nbh);
@@ -482,8 +621,8 @@ __global__ __launch_bounds__(NW * 64, 1) void stream_kernel(Layer3Args a) {
                         a.tint[o + size_t(ff) * nbx] = bu;
                     }
                 }
-                fg = fmaf(__fmul_rn(h2f(dg), A.d[q]), float(Ig), fg);
-                fu = fmaf(__fmul_rn(h2f(du), A.d[q]), float(Iu), fu);
+                fg = fmaf(__fmul_rn(h2f(dg[q]), A.d[q]), float(Ig[q]), fg);
+                fu = fmaf(__fmul_rn(h2f(du[q]), A.d[q]), float(Iu[q]), fu);
             }
             // A bad id read expert 0's rows: its h is published as 0 so that readers
             // finish. The mask is applied by an opaque multiply: a select would let the
@@ -587,18 +726,20 @@ __global__ __launch_bounds__(NW * 64, 1) void stream_kernel(Layer3Args a) {
                     const int i = dpick(j);
                     if (j == 0 || i != dpick(j > 0 ? j - 1 : 0)) load_act<PD>(B, lds, LY::HQ + i * hq_stride, ff, lD, LD);
                     const int td = MIX ? mtype(i, 2) : 0;
+                    int I[PD];
+                    uint32_t d16[PD];
+                    if constexpr (!MIX) {
+                        decode_pass<DT, false>(I, d16, rd[j % (WIND + 1)], B, lds, lo, lD, LD, 0);
+                    } else {   // one branch per pass, static type inside
+                        if (td == kIQ2_XXS) decode_pass<1, true>(I, d16, rd[j % (WIND + 1)], B, lds, lo, lD, LD, bqd);
+                        else if (td == kIQ2_XS) decode_pass<2, true>(I, d16, rd[j % (WIND + 1)], B, lds, lo, lD, LD, bqd);
+                        else decode_pass<4, true>(I, d16, rd[j % (WIND + 1)], B, lds, lo, lD, LD, bqd);
+                    }
                     float f = 0.0f;
-                    Looks La, Lb;   // pair q's lookups in La (q even) or Lb; the next pair's are issued first
-                    look_any<DT>(La, td, lds, lo, rd[j % (WIND + 1)][0]);
-                    static_for<PD>([&]<int q>() {
-                        const Raw3& D0 = rd[j % (WIND + 1)][q];
-                        Looks& Lc = (q & 1) ? Lb : La;
-                        Looks& Ln = (q & 1) ? La : Lb;
-                        if constexpr (q + 1 < PD) look_any<DT>(Ln, td, lds, lo, rd[j % (WIND + 1)][q + 1]);
-                        uint32_t d16;
-                        const int I = sum_any<DT, false>(td, Lc, D0, B.a[q], nullptr, (lD + LD * q) & 3, d16);
+#pragma unroll
+                    for (int q = 0; q < PD; ++q) {
                         if constexpr (TR) {
-                            const int bi = quad_isum(I);
+                            const int bi = quad_isum(I[q]);
                             if (a.tint && ((dok >> j) & 1u) && (lD & 3) == 0) {
                                 const uint32_t m = dsl(j);
                                 const size_t rec = size_t((m >> 12) & 15u) * (2 * size_t(ff) * nbx + size_t(dim) * nbh);
@@ -606,8 +747,8 @@ __global__ __launch_bounds__(NW * 64, 1) void stream_kernel(Layer3Args a) {
                                        size_t((lD + LD * q) >> 2)] = bi;
                             }
                         }
-                        f = fmaf(__fmul_rn(h2f(d16), B.d[q]), float(I), f);
-                    });
+                        f = fmaf(__fmul_rn(h2f(d16[q]), B.d[q]), float(I[q]), f);
+                    }
                     float okf = ((dok >> j) & 1u) ? 0.125f : 0.0f;   // opaque, as in gate/up
                     asm volatile("" : "+v"(okf));
                     const float y = __fmul_rn(okf, gsum<LD>(f));

@@ -341,6 +341,7 @@ struct LayerTrace {
     uint8_t* q8h = nullptr;
     float* h = nullptr;
     int32_t* ints = nullptr;
+    float* y = nullptr;   // per-pick (per-pair) rows before the combine
     int kernel = 0;
 };
 
@@ -369,7 +370,7 @@ bool enqueue_layer(xl_context* ctx, int32_t layer, const int32_t* d_ids, const f
             a.trace = ctx->timeline;
             hip_check(hipMemsetAsync(ctx->timeline, 0, size_t(ctx->cus) * 16 * 32 * 8, s), "timeline clear");
         }
-        if (tr) { a.tq8x = tr->q8x; a.tq8h = tr->q8h; a.th = tr->h; a.tint = tr->ints; }
+        if (tr) { a.tq8x = tr->q8x; a.tq8h = tr->q8h; a.th = tr->h; a.tint = tr->ints; a.ty = tr->y; }
         const LayerShape& ls = ctx->layer_shape[size_t(layer)];
         if (ls.regular) {
             a.slab = ctx->slabs[size_t(layer)];
@@ -1049,6 +1050,9 @@ void enqueue_grouped(xl_context* ctx, int32_t layer, int32_t T, int32_t k, const
             if (tr && tr->h)   // the pairs' h as the gate/up kernel wrote it for Q8_K(h)
                 hip_check(hipMemcpyAsync(tr->h, g.h, sizeof(float) * size_t(T) * k * ctx->cfg.ff,
                                          hipMemcpyDeviceToDevice, s), "trace h copy");
+            if (tr && tr->y)   // the pairs' rows as the combine kernel read them
+                hip_check(hipMemcpyAsync(tr->y, g.y, sizeof(float) * size_t(T) * k * dim, hipMemcpyDeviceToDevice, s),
+                          "trace y copy");
             mark("grouped");
             return;
         }
@@ -1235,18 +1239,20 @@ int32_t xl_layer_forward_async(xl_context* ctx, int32_t layer, const int32_t* d_
 
 int32_t xl_layer_trace_async(xl_context* ctx, int32_t layer, const int32_t* d_ids, const float* d_w, int32_t k,
                              const float* d_x, const float* d_shared_or_null, float* d_out, void* d_q8x, void* d_q8h,
-                             float* d_h, int32_t* d_ints, int32_t* kernel_out, void* stream, xl_error* err) {
+                             float* d_h, int32_t* d_ints, float* d_y, int32_t* kernel_out, void* stream,
+                             xl_error* err) {
     return guarded(ctx, err, [&] {
         ready(ctx, true);
         check_layer(ctx, layer);
         need(k >= 1 && k <= ctx->cfg.max_picks, XL_E_ARG, "pick count outside 1..max_picks");
         need(d_ids && d_w && d_x && d_out, XL_E_ARG, "null device pointer");
-        need(d_q8x || d_q8h || d_h || d_ints, XL_E_ARG, "trace: no output requested");
+        need(d_q8x || d_q8h || d_h || d_ints || d_y, XL_E_ARG, "trace: no output requested");
         LayerTrace tr;
         tr.q8x = static_cast<uint8_t*>(d_q8x);
         tr.q8h = static_cast<uint8_t*>(d_q8h);
         tr.h = d_h;
         tr.ints = d_ints;
+        tr.y = d_y;
         hipStream_t s = pick_stream(ctx, stream);
         Ordered ord(ctx, s);
         ord.carried_by_launch(
@@ -1257,21 +1263,36 @@ int32_t xl_layer_trace_async(xl_context* ctx, int32_t layer, const int32_t* d_id
 
 int32_t xl_grouped_trace_async(xl_context* ctx, int32_t layer, int32_t T, int32_t k, const int32_t* d_ids,
                                const float* d_w, const float* d_x, const float* d_shared_or_null, float* d_out,
-                               void* d_q8x, void* d_q8h, float* d_h, int32_t* d_ints, void* stream, xl_error* err) {
+                               void* d_q8x, void* d_q8h, float* d_h, int32_t* d_ints, float* d_y, void* stream,
+                               xl_error* err) {
     return guarded(ctx, err, [&] {
         ready(ctx, true);
         check_layer(ctx, layer);
         check_grouped(ctx, T, k);
         need(d_ids && d_w && d_x && d_out, XL_E_ARG, "null device pointer");
-        need(d_q8x || d_q8h || d_h || d_ints, XL_E_ARG, "trace: no output requested");
+        need(d_q8x || d_q8h || d_h || d_ints || d_y, XL_E_ARG, "trace: no output requested");
         LayerTrace tr;
         tr.q8x = static_cast<uint8_t*>(d_q8x);
         tr.q8h = static_cast<uint8_t*>(d_q8h);
         tr.h = d_h;
         tr.ints = d_ints;
+        tr.y = d_y;
         hipStream_t s = pick_stream(ctx, stream);
         Ordered ord(ctx, s);
         enqueue_grouped(ctx, layer, T, k, d_ids, d_w, d_x, d_shared_or_null, d_out, s, &tr);
+    });
+}
+
+int32_t xl_combine_async(xl_context* ctx, const int32_t* d_ids, const float* d_w, int32_t k, const float* d_rows,
+                         int32_t dim, const float* d_shared_or_null, float* d_out, void* stream, xl_error* err) {
+    return guarded(ctx, err, [&] {
+        ready(ctx, false);
+        need(k >= 1 && k <= 16, XL_E_ARG, "pick count outside 1..16");
+        need(dim >= 1 && dim <= (1 << 24), XL_E_ARG, "dim outside 1..2^24");
+        need(d_ids && d_w && d_rows && d_out, XL_E_ARG, "null device pointer");
+        hipStream_t s = pick_stream(ctx, stream);
+        Ordered ord(ctx, s);
+        hip_check(xl::dev::launch_combine(d_ids, d_w, k, d_rows, dim, d_shared_or_null, d_out, s), "combine");
     });
 }
 

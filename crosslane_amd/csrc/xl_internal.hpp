@@ -102,6 +102,7 @@ struct Layer3Args {
     uint8_t* tq8h;
     float* th;
     int32_t* tint;
+    float* ty;                  // trace: every pick's row before the combine (k x dim, ids order)
     float* part;                // unit kernel: per (pick, h block) unit, dim float partials of the down rows
     uint32_t* ucnt;             // unit kernel: 2 sets (launch parity) of 8 partial counters, 32 words apart (2 x 256 words)
 };

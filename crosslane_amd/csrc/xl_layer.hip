@@ -644,7 +644,11 @@ __global__ __launch_bounds__(NW * 64, 1) void layer3_kernel(Layer3Args a) {
         float acc = 0.0f;
         for (int s2 = 0; s2 < k; ++s2) {
             const int i = order[s2];
-            acc = fmaf(s_w[i], ys[(i * nq_wg + qq) * RD + rr], acc);
+            const float yi = ys[(i * nq_wg + qq) * RD + rr];
+            if constexpr (TR) {
+                if (a.ty) a.ty[size_t(i) * dim + orow] = yi;
+            }
+            acc = fmaf(s_w[i], yi, acc);
         }
         if (a.shared) acc = __fadd_rn(acc, a.shared[orow]);
         a.out[orow] = acc;
@@ -659,7 +663,7 @@ __global__ __launch_bounds__(NW * 64, 1) void layer3_kernel(Layer3Args a) {
 // ---- launcher ------------------------------------------------------------------------------
 template <int NW, int LG, int PG, int LD, int PD, int MG, int MD, int WIN, int WIND, int GUT, int DNT, int DP = 0>
 static hipError_t launch3(const Layer3Args& args, int grid, hipStream_t s, hipEvent_t stop) {
-    const bool tr = args.tq8x || args.tq8h || args.th || args.tint;
+    const bool tr = args.tq8x || args.tq8h || args.th || args.tint || args.ty;
     constexpr int RG = 64 / LG, RD = 64 / LD;
     const int W = grid * NW;
     const int SG = args.k * (args.ff / RG);

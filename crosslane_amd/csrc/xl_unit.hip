@@ -436,6 +436,9 @@ __global__ __launch_bounds__(NW * 64, 1) void unit_kernel(Layer3Args a) {
             float acc = 0.0f;
             for (int s2 = 0; s2 < k; ++s2) {
                 const int i = sm.order[s2];
+                if constexpr (TR) {
+                    if (a.ty) a.ty[size_t(i) * dim + orow] = sm.yv[t][i];
+                }
                 acc = fmaf(sm.w[i], sm.yv[t][i], acc);
             }
             if (a.shared) acc = __fadd_rn(acc, a.shared[orow]);
@@ -458,7 +461,7 @@ hipError_t launch_unit_t(const Layer3Args& args, int grid, hipStream_t s, hipEve
     if (NG < 1 || (grid * NW) % WPU || (U + NG - 1) / NG > MG || args.dim != 16 * WPU || args.k > 16 ||
         args.k * args.ff > kHBufWords || !args.hbuf || !args.slab || !args.part || !args.ucnt || args.n_experts > 65536)
         return hipErrorNotSupported;
-    const bool tr = args.tq8x || args.tq8h || args.th || args.tint;
+    const bool tr = args.tq8x || args.tq8h || args.th || args.tint || args.ty;
     if (tr)
         hipExtLaunchKernelGGL((unit_kernel<NW, LG, MG, WIN, LAG, true>), dim3(grid), dim3(NW * 64), 0, s, nullptr, stop, 0,
                               args);

@@ -24,7 +24,7 @@ import numpy as np
 
 IQ2_XXS, IQ2_XS, IQ1_M = 16, 17, 29
 BLOCK_BYTES = {IQ2_XXS: 66, IQ2_XS: 74, IQ1_M: 56}
-ABI_VERSION = 2
+ABI_VERSION = 3
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "libcrosslane.so")
 
@@ -80,8 +80,10 @@ _SIGNATURES = {
     "xl_expert_trace": (_I32, [_P, _I32, _I32, _f32p, _P, _P, _P, _P, _P, _ErrP]),
     "xl_layer_forward_async": (_I32, [_P, _I32, _P, _P, _I32, _P, _P, _P, _P, _ErrP]),
     "xl_sync": (_I32, [_P, _P, _ErrP]),
-    "xl_layer_trace_async": (_I32, [_P, _I32, _P, _P, _I32, _P, _P, _P, _P, _P, _P, _P, C.POINTER(_I32), _P, _ErrP]),
-    "xl_grouped_trace_async": (_I32, [_P, _I32, _I32, _I32, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _ErrP]),
+    "xl_layer_trace_async": (_I32, [_P, _I32, _P, _P, _I32, _P, _P, _P, _P, _P, _P, _P, _P, C.POINTER(_I32), _P,
+                                    _ErrP]),
+    "xl_grouped_trace_async": (_I32, [_P, _I32, _I32, _I32, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _ErrP]),
+    "xl_combine_async": (_I32, [_P, _P, _P, _I32, _P, _I32, _P, _P, _P, _ErrP]),
     "xl_grouped_forward": (_I32, [_P, _I32, _I32, _I32, _i32p, _f32p, _f32p, _P, _f32p, _ErrP]),
     "xl_grouped_forward_async": (_I32, [_P, _I32, _I32, _I32, _P, _P, _P, _P, _P, _P, _ErrP]),
     "xl_route_async": (_I32, [_P, _P, _I32, _I32, _P, _I32, _I32, C.c_float, _P, _P, _P, _ErrP]),
@@ -346,21 +348,28 @@ class Lane:
                    _ptr(out), None if stream is None else int(stream))
 
     def layer_trace_async(self, layer: int, ids, w, x, out, q8x=None, q8h=None, h=None, ints=None, shared=None,
-                          stream=None) -> int:
+                          stream=None, y=None) -> int:
         """The single-launch layer call with its own Q8_K(x) / Q8_K(h) blocks (uint8
-        tensors of 292-byte blocks), h and block integers written out; returns the
-        kernel that ran (1 streaming, 3 all-types)."""
+        tensors of 292-byte blocks), h, block integers and per-pick rows (y, k x dim,
+        as its combine read them) written out; returns the kernel that ran (1
+        streaming, 3 all-types, 5 unit)."""
         kern = _I32()
         self._call("xl_layer_trace_async", layer, _ptr(ids), _ptr(w), int(ids.numel()), _ptr(x), _ptr(shared),
-                   _ptr(out), _ptr(q8x), _ptr(q8h), _ptr(h), _ptr(ints), C.byref(kern),
+                   _ptr(out), _ptr(q8x), _ptr(q8h), _ptr(h), _ptr(ints), _ptr(y), C.byref(kern),
                    None if stream is None else int(stream))
         return kern.value
 
     def grouped_trace_async(self, layer: int, ids, w, x, out, q8x=None, q8h=None, h=None, ints=None, shared=None,
-                            stream=None) -> None:
+                            stream=None, y=None) -> None:
         T, k = int(ids.shape[0]), int(ids.shape[1])
         self._call("xl_grouped_trace_async", layer, T, k, _ptr(ids), _ptr(w), _ptr(x), _ptr(shared), _ptr(out),
-                   _ptr(q8x), _ptr(q8h), _ptr(h), _ptr(ints), None if stream is None else int(stream))
+                   _ptr(q8x), _ptr(q8h), _ptr(h), _ptr(ints), _ptr(y), None if stream is None else int(stream))
+
+    def combine_async(self, ids, w, rows, out, shared=None, stream=None) -> None:
+        """xl_combine_async: out = fixed-order combine of rows [k, dim] (device tensors)."""
+        k, dim = int(rows.shape[0]), int(rows.shape[1])
+        self._call("xl_combine_async", _ptr(ids), _ptr(w), k, _ptr(rows), dim, _ptr(shared), _ptr(out),
+                   None if stream is None else int(stream))
 
     def grouped_forward_async(self, layer: int, ids, w, x, out, shared=None, stream=None) -> None:
         """ids, w: [T, k] device tensors; x, out (and shared): [T, dim]."""

@@ -33,7 +33,7 @@
 extern "C" {
 #endif
 
-#define XL_ABI_VERSION 2u
+#define XL_ABI_VERSION 3u
 
 enum {
     XL_OK = 0,
@@ -186,19 +186,35 @@ int32_t xl_grouped_forward_async(xl_context* ctx, int32_t layer, int32_t T, int3
  *   ints per pick (ids order): gate ff x dim/256, up ff x dim/256, down
  *        dim x ff/256 int32, each row's exact integer per 256-weight block (as
  *        xl_matvec_async's partials; IQ1_M: 8 * main + delta);
+ *   y    k * dim floats, every pick's row (ids order) as the launch's own
+ *        fixed-order combine read it (so that out can be checked bit for bit
+ *        against the combine of these rows);
  * kernel_out (host, may be null): 1 the streaming kernel ran, 3 the all-types
- * kernel. Any of q8x, q8h, h, ints may be null (not all). XL_E_ARG when the
+ * kernel, 5 the unit kernel. Any of q8x, q8h, h, ints, y may be null (not all).
+ * XL_E_ARG when the
  * layer does not run as a single launch. A diagnostic aid (no counterpart in
  * the reference beyond its probe); it runs the traced kernel instances. */
 int32_t xl_layer_trace_async(xl_context* ctx, int32_t layer, const int32_t* d_ids, const float* d_w, int32_t k,
                              const float* d_x, const float* d_shared_or_null, float* d_out, void* d_q8x, void* d_q8h,
-                             float* d_h, int32_t* d_ints, int32_t* kernel_out, void* stream, xl_error* err);
+                             float* d_h, int32_t* d_ints, float* d_y, int32_t* kernel_out, void* stream,
+                             xl_error* err);
 /* The same for the grouped MFMA path (XL_E_ARG when the layer does not run on
- * it): q8x per token (T x dim/256 blocks), q8h, h and ints per pair (P = T * k,
- * token-major), layouts as above. */
+ * it): q8x per token (T x dim/256 blocks), q8h, h, ints and y per pair (P =
+ * T * k, token-major), layouts as above. */
 int32_t xl_grouped_trace_async(xl_context* ctx, int32_t layer, int32_t T, int32_t k, const int32_t* d_ids,
                                const float* d_w, const float* d_x, const float* d_shared_or_null, float* d_out,
-                               void* d_q8x, void* d_q8h, float* d_h, int32_t* d_ints, void* stream, xl_error* err);
+                               void* d_q8x, void* d_q8h, float* d_h, int32_t* d_ints, float* d_y, void* stream,
+                               xl_error* err);
+
+/* Fixed-order combine of k per-pick rows on the device (engine/strata/warm/
+ * runtime.cpp:183-188; other_combine.hpp:51-73 other_combine): out[c] =
+ * fma(w_i, rows[i][c], .) over the picks in ascending expert id (equal ids in
+ * pick order) from +0, then + shared[c]. d_rows: k x dim floats (ids order);
+ * k in 1..16, dim in 1..2^24; d_shared_or_null may be null. Ordered with the
+ * context's other calls; for rows computed elsewhere (xl_experts_forward, the
+ * per32 rows). */
+int32_t xl_combine_async(xl_context* ctx, const int32_t* d_ids, const float* d_w, int32_t k, const float* d_rows,
+                         int32_t dim, const float* d_shared_or_null, float* d_out, void* stream, xl_error* err);
 
 /* ---- router (device pointers) -----------------------------------------------
  * route.cpp:15-37 (route_cpu) on the device, per token: score =

@@ -31,7 +31,7 @@ def test_exports_every_declared_symbol():
 
 
 def test_abi_version():
-    assert xl.lib().xl_abi_version() == L.ABI_VERSION == 2
+    assert xl.lib().xl_abi_version() == L.ABI_VERSION == 3
 
 
 def test_open_rejects_version_and_size_before_device():

@@ -52,6 +52,23 @@ __device__ __forceinline__ uint32_t neg_bytes(uint32_t x) {
     return (lo & 0x00ff00ffu) | (hi & 0xff00ff00u);
 }
 
+// (x ^ y) + z as one v_xad_u32: inside the unrolled decoders the compiler emits
+// v_xor_b32 and v_add_u32 for it.
+__device__ __forceinline__ uint32_t xad_op(uint32_t x, uint32_t y, uint32_t z) {
+    uint32_t r;
+    asm("v_xad_u32 %0, %1, %2, %3" : "=v"(r) : "v"(x), "v"(y), "v"(z));
+    return r;
+}
+// The grid bytes with the sign mask M applied: (g ^ M) + (M & 0x01010101).
+__device__ __forceinline__ uint32_t signed_grid(uint32_t g, uint32_t m) { return xad_op(g, m, m & 0x01010101u); }
+// The first v_dot4 of a chain, in the VOP3P form with a zero accumulator (the
+// compiler's v_dot4c ties the accumulator to the result and needs a v_mov of 0).
+__device__ __forceinline__ int sdot4_0(uint32_t a, uint32_t b) {
+    int r;
+    asm("v_dot4_i32_i8 %0, %1, %2, 0" : "=v"(r) : "v"(a), "v"(b));
+    return r;
+}
+
 // ---- pair decoders -------------------------------------------------------------------------
 // Codebook rows of one pair: 8 grid rows and 8 sign masks. The decoders are
 // split into lookups and arithmetic so that a slot issues both of its rows'
@@ -82,13 +99,14 @@ __device__ __forceinline__ Looks look_xxs(const uint8_t* lds, uint32_t lo_g, uin
 // (2s+1) * grid * sign * q over the pair (q8k_core.hpp:96-114 regrouped per
 // sub-block; the sign is applied to q).
 __device__ __forceinline__ int sum_xxs(const Looks& L, const uint32_t* w, const uint32_t* a, const uint32_t* na) {
-    int acc[2] = {0, 0};
+    int acc[2];
 #pragma unroll
     for (int s = 0; s < 2; ++s)
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
             const int e = 4 * s + q, k0 = 8 * s + 2 * q;
-            acc[s] = sdot4(L.g[e].x, bfi(L.m[e].x, na[k0], a[k0]), acc[s]);
+            const uint32_t v = bfi(L.m[e].x, na[k0], a[k0]);
+            acc[s] = q == 0 ? sdot4_0(L.g[e].x, v) : sdot4(L.g[e].x, v, acc[s]);
             acc[s] = sdot4(L.g[e].y, bfi(L.m[e].y, na[k0 + 1], a[k0 + 1]), acc[s]);
         }
     return __mul24(acc[0], xxs_sc(w[1])) + __mul24(acc[1], xxs_sc(w[3]));
@@ -113,19 +131,23 @@ __device__ __forceinline__ Looks look_xs(const uint8_t* lds, uint32_t lo_x, uint
     return L;
 }
 __device__ __forceinline__ int sum_xs(const Looks& L, uint32_t sc, const uint32_t* a) {
+    // the four 16-weight scales 2 n + 1, two per word: byte s of t1 from the low
+    // nibble of scale byte s, byte s of t2 from its high nibble (sc < 2^16)
+    const uint32_t t1 = ((sc << 1) & 0x1e1eu) | 0x0101u;
+    const uint32_t t2 = ((sc >> 3) & 0x1e1eu) | 0x0101u;
     int total = 0;
 #pragma unroll
     for (int s = 0; s < 2; ++s) {
-        int lo = 0, hi = 0;
+        int part[2];
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
-            const int e = 4 * s + q;
-            int& acc = q < 2 ? lo : hi;
-            acc = sdot4(xad(L.g[e].x, L.m[e].x, L.m[e].x & 0x01010101u), a[8 * s + 2 * q], acc);
-            acc = sdot4(xad(L.g[e].y, L.m[e].y, L.m[e].y & 0x01010101u), a[8 * s + 2 * q + 1], acc);
+        for (int h = 0; h < 2; ++h) {   // 16 weights: groups 4 s + 2 h and 4 s + 2 h + 1
+            const int e = 4 * s + 2 * h, k0 = 8 * s + 4 * h;
+            int acc = sdot4_0(signed_grid(L.g[e].x, L.m[e].x), a[k0]);
+            acc = sdot4(signed_grid(L.g[e].y, L.m[e].y), a[k0 + 1], acc);
+            acc = sdot4(signed_grid(L.g[e + 1].x, L.m[e + 1].x), a[k0 + 2], acc);
+            part[h] = sdot4(signed_grid(L.g[e + 1].y, L.m[e + 1].y), a[k0 + 3], acc);
         }
-        const uint32_t byte = (sc >> (8 * s)) & 255u;
-        total += __mul24(lo, int(2u * (byte & 15u) + 1u)) + __mul24(hi, int(2u * (byte >> 4) + 1u));
+        total += __mul24(part[0], int((t1 >> (8 * s)) & 255u)) + __mul24(part[1], int((t2 >> (8 * s)) & 255u));
     }
     return total;
 }
@@ -134,14 +156,15 @@ __device__ __forceinline__ int sum_xs(const Looks& L, uint32_t sc, const uint32_
 // activations ((g ^ M) + (M & 0x01010101), no negated activations needed): the
 // same integer as sum_xxs.
 __device__ __forceinline__ int sum_xxs_g(const Looks& L, const uint32_t* w, const uint32_t* a) {
-    int acc[2] = {0, 0};
+    int acc[2];
 #pragma unroll
     for (int s = 0; s < 2; ++s)
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
             const int e = 4 * s + q, k0 = 8 * s + 2 * q;
-            acc[s] = sdot4(xad(L.g[e].x, L.m[e].x, L.m[e].x & 0x01010101u), a[k0], acc[s]);
-            acc[s] = sdot4(xad(L.g[e].y, L.m[e].y, L.m[e].y & 0x01010101u), a[k0 + 1], acc[s]);
+            const uint32_t v = signed_grid(L.g[e].x, L.m[e].x);
+            acc[s] = q == 0 ? sdot4_0(v, a[k0]) : sdot4(v, a[k0], acc[s]);
+            acc[s] = sdot4(signed_grid(L.g[e].y, L.m[e].y), a[k0 + 1], acc[s]);
         }
     return __mul24(acc[0], xxs_sc(w[1])) + __mul24(acc[1], xxs_sc(w[3]));
 }
@@ -176,11 +199,11 @@ __device__ __forceinline__ int sum_iq1(const Looks& L, uint32_t scw, const uint3
     int total = 0;
 #pragma unroll
     for (int s = 0; s < 2; ++s) {
-        int lo = 0, hi = 0;
+        int lo, hi;
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
             int& acc = g < 2 ? lo : hi;
-            acc = sdot4(L.g[4 * s + g].x, a[8 * s + 2 * g], acc);
+            acc = (g & 1) ? sdot4(L.g[4 * s + g].x, a[8 * s + 2 * g], acc) : sdot4_0(L.g[4 * s + g].x, a[8 * s + 2 * g]);
             acc = sdot4(L.g[4 * s + g].y, a[8 * s + 2 * g + 1], acc);
         }
         total += __mul24(lo, int(2u * ((scw >> (6 * s)) & 7u) + 1u)) + __mul24(hi, int(2u * ((scw >> (6 * s + 3)) & 7u) + 1u));
@@ -298,9 +321,12 @@ __device__ __forceinline__ bool q8k_blocks(const uint4 (&hv)[NB], int nvalid, in
 #pragma unroll
         for (int j = 0; j < 4; ++j)   // q + 128 in 1..255, an exact integer: the byte conversion is exact
             p = __builtin_amdgcn_cvt_pk_u8_f32(__fadd_rn(__builtin_rintf(__fmul_rn(is, __uint_as_float(x[m][j]))), 128.0f), j, p);
+        // the readlane stays outside the select: a select over it becomes a branch
+        // (a convergent call is not speculated), which splits the caller's code
+        const float dm = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(dv), m));
         const bool zero = am[m] == 0u;
         packed[m] = zero ? 0u : p ^ 0x80808080u;
-        d[m] = zero ? 0.0f : __int_as_float(__builtin_amdgcn_readlane(__float_as_int(dv), m));
+        d[m] = zero ? 0.0f : dm;
     }
     return fin;
 }

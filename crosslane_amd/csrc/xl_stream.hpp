@@ -393,6 +393,14 @@ __global__ __launch_bounds__(NW * 64, 1) void stream_kernel(Layer3Args a) {
     constexpr bool HASXXS = (M & 1) != 0 || MIX, HASXS = (M & 2) != 0 || MIX;
     constexpr bool HAS1 = (M & 4) != 0;
     constexpr int NX = (4096 + NT - 1) / NT, NS = (1024 + NT - 1) / NT, N1 = (2048 + NT - 1) / NT;
+    // x first: its Q8_K runs while the codebook loads are in flight
+    constexpr int UX = (16 + NW - 1) / NW;
+    float4 xv[UX];
+#pragma unroll
+    for (int u = 0; u < UX; ++u) {
+        const int b = wv + NW * u;
+        xv[u] = reinterpret_cast<const float4*>(a.x + 256 * (b < nbx ? b : 0))[lane];
+    }
     uint2 vx[HASXXS ? NX : 1], vs[HASXS ? NS : 1];
     uint4 v1[HAS1 ? N1 : 1];
     {
@@ -409,13 +417,6 @@ __global__ __launch_bounds__(NW * 64, 1) void stream_kernel(Layer3Args a) {
         if constexpr (HAS1)
 #pragma unroll
             for (int i = 0; i < N1; ++i) v1[i] = g1[min(t + NT * i, 2047)];
-    }
-    constexpr int UX = (16 + NW - 1) / NW;
-    float4 xv[UX];
-#pragma unroll
-    for (int u = 0; u < UX; ++u) {
-        const int b = wv + NW * u;
-        xv[u] = reinterpret_cast<const float4*>(a.x + 256 * (b < nbx ? b : 0))[lane];
     }
     const float cw = a.w[lane < k ? lane : k - 1];
     uint32_t* ctl = a.ctl + 2;   // [0] parity source: launches of this kernel so far, [1] arrivals
@@ -445,7 +446,26 @@ __global__ __launch_bounds__(NW * 64, 1) void stream_kernel(Layer3Args a) {
     static_for<WIN>([&]<int j>() { load_slot.template operator()<j>(); });
     mark(0);
 
-    // ---- codebooks (copies, computed sign rows), Q8_K(x): LDS writes, one barrier
+    // ---- Q8_K(x), then codebooks (copies, computed sign rows): LDS writes, one barrier
+    {
+        uint4 xb[UX];
+        uint32_t xp[UX];
+        float xd[UX];
+#pragma unroll
+        for (int u = 0; u < UX; ++u)
+            xb[u] = make_uint4(__float_as_uint(xv[u].x), __float_as_uint(xv[u].y), __float_as_uint(xv[u].z),
+                               __float_as_uint(xv[u].w));
+        const bool fin = q8k_blocks<UX>(xb, nbx > wv ? (nbx - wv + NW - 1) / NW : 0, lane, xp, xd);
+        if (!fin && lane == 0) set_err(a.err, kDevErrNonFinite);
+#pragma unroll
+        for (int u = 0; u < UX; ++u) {
+            const int b = wv + NW * u;
+            if (b < nbx) {
+                *reinterpret_cast<uint32_t*>(lds + LY::XQ + qswz(256 * b + 4 * lane)) = xp[u];
+                if (lane == 0) reinterpret_cast<float*>(lds + LY::XQ + 4096)[b] = xd[u];
+            }
+        }
+    }
     if constexpr (M == 3) {
 #pragma unroll
         for (int i = 0; i < NX; ++i) {
@@ -480,25 +500,6 @@ __global__ __launch_bounds__(NW * 64, 1) void stream_kernel(Layer3Args a) {
             if (t + NT * i < 2048)
                 *reinterpret_cast<uint4*>(lds + LY::IQ1 + 16 * (t + NT * i)) = make_uint4(v1[i].x, v1[i].y, v1[i].z, v1[i].w);
     mark(1);
-    {
-        uint4 xb[UX];
-        uint32_t xp[UX];
-        float xd[UX];
-#pragma unroll
-        for (int u = 0; u < UX; ++u)
-            xb[u] = make_uint4(__float_as_uint(xv[u].x), __float_as_uint(xv[u].y), __float_as_uint(xv[u].z),
-                               __float_as_uint(xv[u].w));
-        const bool fin = q8k_blocks<UX>(xb, nbx > wv ? (nbx - wv + NW - 1) / NW : 0, lane, xp, xd);
-        if (!fin && lane == 0) set_err(a.err, kDevErrNonFinite);
-#pragma unroll
-        for (int u = 0; u < UX; ++u) {
-            const int b = wv + NW * u;
-            if (b < nbx) {
-                *reinterpret_cast<uint32_t*>(lds + LY::XQ + qswz(256 * b + 4 * lane)) = xp[u];
-                if (lane == 0) reinterpret_cast<float*>(lds + LY::XQ + 4096)[b] = xd[u];
-            }
-        }
-    }
     if (wv == 0) {
         int rank = 0;   // the combine order (engine/strata/warm/runtime.cpp:183-188)
         for (int j = 0; j < k; ++j) {
@@ -674,87 +675,112 @@ __global__ __launch_bounds__(NW * 64, 1) void stream_kernel(Layer3Args a) {
     };
     h_issue.template operator()<0>();
     if constexpr (MD > 1) h_issue.template operator()<1>();
+    // wait until step j's blocks are complete (all re-polled together; the common
+    // case never enters the retry loop)
+    auto h_wait = [&]<int j>() {
+        const int nb = pk_hi(j) * nbh - pk_lo(j) * nbh;
+        auto all_ready = [&]() {
+            bool ok = true;
+#pragma unroll
+            for (int m = 0; m < MQ; ++m) ok = ok & ((wv + NW * m >= nb) | h_ready(hv[j & 1][m]));
+            return __all(ok);
+        };
+        uint32_t polls = 0;
+        if (!all_ready()) {
+            do {
+                if (++polls > kPollLimit) {
+                    if (lane == 0) set_err(a.err, kDevErrTimeout);
+                    break;
+                }
+                __builtin_amdgcn_s_sleep(2);
+                h_issue.template operator()<j>();
+            } while (!all_ready());
+        }
+        if (a.trace && lane == 0 && j < 4) a.trace[size_t(gw) * 32 + 20 + j] = polls;
+    };
+    // Q8_K of step j's blocks owned by this wave (registers), then their LDS stores
+    auto h_quant = [&]<int j>(uint32_t (&hp)[MQ], float (&hd)[MQ]) {
+        const int nb = pk_hi(j) * nbh - pk_lo(j) * nbh;
+        return q8k_blocks<MQ>(hv[j & 1], nb > wv ? (nb - wv + NW - 1) / NW : 0, lane, hp, hd);
+    };
+    auto h_store = [&]<int j>(const uint32_t (&hp)[MQ], const float (&hd)[MQ], bool fin) {
+        const int b0 = pk_lo(j) * nbh, nb = pk_hi(j) * nbh - b0;
+        if (!fin && lane == 0) set_err(a.err, kDevErrNonFinite);
+#pragma unroll
+        for (int m = 0; m < MQ; ++m) {
+            const int bq = wv + NW * m;
+            if (bq < nb) {
+                const int blk = b0 + bq, i = blk / nbh, bb = blk - i * nbh;
+                uint8_t* hq = lds + LY::HQ + i * hq_stride;
+                *reinterpret_cast<uint32_t*>(hq + qswz(256 * bb + 4 * lane)) = hp[m];
+                if (lane == 0) reinterpret_cast<float*>(hq + ff)[bb] = hd[m];
+            }
+        }
+    };
     lds_barrier();   // Q8_K(h) is staged over a region gate/up read: every wave is past gate/up
     {
+        h_wait.template operator()<0>();
+        mark(24);
+        {
+            uint32_t hp[MQ];
+            float hd[MQ];
+            const bool fin = h_quant.template operator()<0>(hp, hd);
+            h_store.template operator()<0>(hp, hd, fin);
+        }
+        mark(17);
+        lds_barrier();
+        mark(25);
+        // Step j runs pass j with the next step's Q8_K(h) in the same straight-line
+        // code (its quantizer's DPP and division chains fill the pass's LDS waits);
+        // the next step's blocks go to LDS after the pass, then one barrier.
         Act<PD> B;
-        static_for<MD>([&]<int j>() {
-            {   // steps past nsteps stage nothing and compute a discarded pass
-                // wait until this step's blocks are complete (all re-polled together), then
-                // quantize them into LDS
-                const int b0 = pk_lo(j) * nbh, nb = pk_hi(j) * nbh - b0;
-                auto all_ready = [&]() {
-                    bool ok = true;
+        static_for<MD>([&]<int j>() {   // steps past nsteps stage nothing and compute a discarded pass
+            if constexpr (j + 2 < MD) h_issue.template operator()<j + 2>();
+            if constexpr (j + WIND < MD) load_pass.template operator()<j + WIND>();
+            if constexpr (j + 1 < MD) {
+                h_wait.template operator()<j + 1>();
+                mark(24 + 2 * (j + 1));
+            }
+            const int i = dpick(j);
+            if (j == 0 || i != dpick(j > 0 ? j - 1 : 0)) load_act<PD>(B, lds, LY::HQ + i * hq_stride, ff, lD, LD);
+            uint32_t hp[MQ];
+            float hd[MQ];
+            bool fin = true;
+            if constexpr (j + 1 < MD) fin = h_quant.template operator()<j + 1>(hp, hd);
+            const int td = MIX ? mtype(i, 2) : 0;
+            int I[PD];
+            uint32_t d16[PD];
+            if constexpr (!MIX) {
+                decode_pass<DT, false>(I, d16, rd[j % (WIND + 1)], B, lds, lo, lD, LD, 0);
+            } else {   // one branch per pass, static type inside
+                if (td == kIQ2_XXS) decode_pass<1, true>(I, d16, rd[j % (WIND + 1)], B, lds, lo, lD, LD, bqd);
+                else if (td == kIQ2_XS) decode_pass<2, true>(I, d16, rd[j % (WIND + 1)], B, lds, lo, lD, LD, bqd);
+                else decode_pass<4, true>(I, d16, rd[j % (WIND + 1)], B, lds, lo, lD, LD, bqd);
+            }
+            float f = 0.0f;
 #pragma unroll
-                    for (int m = 0; m < MQ; ++m) ok = ok & ((wv + NW * m >= nb) | h_ready(hv[j & 1][m]));
-                    return __all(ok);
-                };
-                uint32_t polls = 0;
-                if (!all_ready()) {   // the common case never enters the retry loop
-                    do {
-                        if (++polls > kPollLimit) {
-                            if (lane == 0) set_err(a.err, kDevErrTimeout);
-                            break;
-                        }
-                        __builtin_amdgcn_s_sleep(2);
-                        h_issue.template operator()<j>();
-                    } while (!all_ready());
-                }
-                if (a.trace && lane == 0 && j < 4) a.trace[size_t(gw) * 32 + 20 + j] = polls;
-                mark(24 + 2 * j);
-                {
-                    uint32_t hp[MQ];
-                    float hd[MQ];
-                    const bool fin = q8k_blocks<MQ>(hv[j & 1], nb > wv ? (nb - wv + NW - 1) / NW : 0, lane, hp, hd);
-                    if (!fin && lane == 0) set_err(a.err, kDevErrNonFinite);
-#pragma unroll
-                    for (int m = 0; m < MQ; ++m) {
-                        const int bq = wv + NW * m;
-                        if (bq < nb) {
-                            const int blk = b0 + bq, i = blk / nbh, bb = blk - i * nbh;
-                            uint8_t* hq = lds + LY::HQ + i * hq_stride;
-                            *reinterpret_cast<uint32_t*>(hq + qswz(256 * bb + 4 * lane)) = hp[m];
-                            if (lane == 0) reinterpret_cast<float*>(hq + ff)[bb] = hd[m];
-                        }
+            for (int q = 0; q < PD; ++q) {
+                if constexpr (TR) {
+                    const int bi = quad_isum(I[q]);
+                    if (a.tint && ((dok >> j) & 1u) && (lD & 3) == 0) {
+                        const uint32_t m = dsl(j);
+                        const size_t rec = size_t((m >> 12) & 15u) * (2 * size_t(ff) * nbx + size_t(dim) * nbh);
+                        a.tint[rec + 2 * size_t(ff) * nbx + size_t(int(m & 0xfffu) + rD) * nbh +
+                               size_t((lD + LD * q) >> 2)] = bi;
                     }
                 }
-                if (j < 3) mark(17 + j);
+                f = fmaf(__fmul_rn(h2f(d16[q]), B.d[q]), float(I[q]), f);
+            }
+            float okf = ((dok >> j) & 1u) ? 0.125f : 0.0f;   // opaque, as in gate/up
+            asm volatile("" : "+v"(okf));
+            const float y = __fmul_rn(okf, gsum<LD>(f));
+            if (j < nd && lD == LD - 1) ys[(wv + NW * j) * RD + rD] = y;
+            if (j == 0) mark(5);
+            if constexpr (j + 1 < MD) {
+                h_store.template operator()<j + 1>(hp, hd, fin);
+                if (j + 1 < 3) mark(17 + j + 1);
                 lds_barrier();
-                mark(25 + 2 * j);
-                if constexpr (j + 2 < MD) h_issue.template operator()<j + 2>();
-                {
-                    if constexpr (j + WIND < MD) load_pass.template operator()<j + WIND>();
-                    const int i = dpick(j);
-                    if (j == 0 || i != dpick(j > 0 ? j - 1 : 0)) load_act<PD>(B, lds, LY::HQ + i * hq_stride, ff, lD, LD);
-                    const int td = MIX ? mtype(i, 2) : 0;
-                    int I[PD];
-                    uint32_t d16[PD];
-                    if constexpr (!MIX) {
-                        decode_pass<DT, false>(I, d16, rd[j % (WIND + 1)], B, lds, lo, lD, LD, 0);
-                    } else {   // one branch per pass, static type inside
-                        if (td == kIQ2_XXS) decode_pass<1, true>(I, d16, rd[j % (WIND + 1)], B, lds, lo, lD, LD, bqd);
-                        else if (td == kIQ2_XS) decode_pass<2, true>(I, d16, rd[j % (WIND + 1)], B, lds, lo, lD, LD, bqd);
-                        else decode_pass<4, true>(I, d16, rd[j % (WIND + 1)], B, lds, lo, lD, LD, bqd);
-                    }
-                    float f = 0.0f;
-#pragma unroll
-                    for (int q = 0; q < PD; ++q) {
-                        if constexpr (TR) {
-                            const int bi = quad_isum(I[q]);
-                            if (a.tint && ((dok >> j) & 1u) && (lD & 3) == 0) {
-                                const uint32_t m = dsl(j);
-                                const size_t rec = size_t((m >> 12) & 15u) * (2 * size_t(ff) * nbx + size_t(dim) * nbh);
-                                a.tint[rec + 2 * size_t(ff) * nbx + size_t(int(m & 0xfffu) + rD) * nbh +
-                                       size_t((lD + LD * q) >> 2)] = bi;
-                            }
-                        }
-                        f = fmaf(__fmul_rn(h2f(d16[q]), B.d[q]), float(I[q]), f);
-                    }
-                    float okf = ((dok >> j) & 1u) ? 0.125f : 0.0f;   // opaque, as in gate/up
-                    asm volatile("" : "+v"(okf));
-                    const float y = __fmul_rn(okf, gsum<LD>(f));
-                    if (j < nd && lD == LD - 1) ys[(wv + NW * j) * RD + rD] = y;
-                }
-                if (j == 0) mark(5);
+                mark(25 + 2 * (j + 1));
             }
         });
     }
@@ -839,7 +865,10 @@ hipError_t launch_stream_shapes(const Layer3Args& args, int cus, hipStream_t s, 
     if (lg == 64 && pg == 1 && ld == 16 && pd == 3) {   // 4096 x 3072: slots and steps sized by the pick count
         if (args.k <= 2) return launch_stream_t<8, 64, 1, 16, 3, 3, 1, 3, 1, 3, GT, DT>(args, grid, s, stop);
         if (args.k <= 4) return launch_stream_t<8, 64, 1, 16, 3, 6, 2, 3, 2, 3, GT, DT>(args, grid, s, stop);
-        return launch_stream_t<8, 64, 1, 16, 3, 9, 3, 3, 3, 3, GT, DT>(args, grid, s, stop);
+        // one down pass in flight: its weights load under the last gate/up slot and
+        // each later pass's under the step before it (three passes in flight under
+        // the last three slots: 25.4 us at config 1, one: 24.4 us)
+        return launch_stream_t<8, 64, 1, 16, 3, 9, 3, 3, 1, 3, GT, DT>(args, grid, s, stop);
     }
     if (lg == 16 && pg == 1 && ld == 8 && pd == 1)    // 1024 x 512
         return launch_stream_t<8, 16, 1, 8, 1, 6, 2, 3, 1, 2, GT, DT>(args, grid, s, stop);

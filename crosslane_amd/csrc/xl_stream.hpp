@@ -445,6 +445,25 @@ __global__ __launch_bounds__(NW * 64, 1) void stream_kernel(Layer3Args a) {
     // re-read valid rows and are discarded), so every wait count is exact.
     static_for<WIN>([&]<int j>() { load_slot.template operator()<j>(); });
     mark(0);
+    // Down-phase Q8_K(h) blocks, lane-parallel and kept in one register (the
+    // steps read their lanes back, so no scalar division runs between steps;
+    // computed once the first loads are out):
+    // lane j * MQ + m holds step j's m-th block of this wave as valid << 8 |
+    // pick << 4 | block. Step j quantizes the picks its passes are the first to
+    // need, [ceil(NW j / nq_wg), ceil(NW (j + 1) / nq_wg)) clipped to k; wave wv
+    // owns blocks wv, wv + NW, ... of them.
+    static_assert(MD * MQ <= 64, "Q8_K(h) block table lanes");
+    uint32_t hblk = 0;
+    {
+        const int j = lane / MQ, m = lane - j * MQ;
+        if (j < MD) {
+            const int plo = min(k, (NW * j + nq_wg - 1) / nq_wg), phi = min(k, (NW * j + NW + nq_wg - 1) / nq_wg);
+            const int b0 = plo * nbh, nb = phi * nbh - b0, bq = wv + NW * m;
+            const int blk = bq < nb ? b0 + bq : 0;
+            const int i = blk / nbh;
+            hblk = (uint32_t(bq < nb) << 8) | (uint32_t(i) << 4) | uint32_t(blk - i * nbh);
+        }
+    }
 
     // ---- Q8_K(x), then codebooks (copies, computed sign rows): LDS writes, one barrier
     {
@@ -659,18 +678,17 @@ __global__ __launch_bounds__(NW * 64, 1) void stream_kernel(Layer3Args a) {
     // ---- down: step j quantizes the h of the picks it needs, then every wave runs pass j
     float* ys = reinterpret_cast<float*>(lds + LY::Y);
     const int hq_stride = ff + 64;
-    // picks [pk_lo(j), pk_hi(j)) are first needed at step j
-    auto pk_lo = [&](int j) { return min(k, (NW * j + nq_wg - 1) / nq_wg); };
-    auto pk_hi = [&](int j) { return min(k, (NW * j + NW + nq_wg - 1) / nq_wg); };
+    // step j's m-th Q8_K(h) block of this wave (from the lane table hblk)
+    auto hb_of = [&](int j, int m) { return uint32_t(__builtin_amdgcn_readlane(int(hblk), j * MQ + m)); };
     uint4 hv[2][MQ];   // h loads of steps j and j + 1 (issued two steps ahead)
-    auto h_issue = [&]<int j>() {   // loads of step j's blocks owned by this wave
-        const int b0 = pk_lo(j) * nbh, nb = pk_hi(j) * nbh - b0;
+    // loads of step j's blocks owned by this wave; an unused slot still loads (so
+    // that every wait count is exact), all its lanes the same 16 bytes
+    auto h_issue = [&]<int j>() {
 #pragma unroll
         for (int m = 0; m < MQ; ++m) {
-            const int bq = wv + NW * m;
-            const int blk = bq < nb ? b0 + bq : 0;   // unused slots re-read block 0
-            const int i = blk / nbh, bb = blk - i * nbh;
-            hv[j & 1][m] = h_load(hcur, uint32_t(i * ff + 256 * bb + 4 * lane));
+            const uint32_t b = hb_of(j, m);
+            const uint32_t w = ((b >> 8) & 1u) ? uint32_t(int((b >> 4) & 15u) * ff + 256 * int(b & 15u) + 4 * lane) : 0u;
+            hv[j & 1][m] = h_load(hcur, w);
         }
     };
     h_issue.template operator()<0>();
@@ -678,11 +696,10 @@ __global__ __launch_bounds__(NW * 64, 1) void stream_kernel(Layer3Args a) {
     // wait until step j's blocks are complete (all re-polled together; the common
     // case never enters the retry loop)
     auto h_wait = [&]<int j>() {
-        const int nb = pk_hi(j) * nbh - pk_lo(j) * nbh;
         auto all_ready = [&]() {
             bool ok = true;
 #pragma unroll
-            for (int m = 0; m < MQ; ++m) ok = ok & ((wv + NW * m >= nb) | h_ready(hv[j & 1][m]));
+            for (int m = 0; m < MQ; ++m) ok = ok & (((hb_of(j, m) >> 8) & 1u) == 0u || h_ready(hv[j & 1][m]));
             return __all(ok);
         };
         uint32_t polls = 0;
@@ -700,17 +717,18 @@ __global__ __launch_bounds__(NW * 64, 1) void stream_kernel(Layer3Args a) {
     };
     // Q8_K of step j's blocks owned by this wave (registers), then their LDS stores
     auto h_quant = [&]<int j>(uint32_t (&hp)[MQ], float (&hd)[MQ]) {
-        const int nb = pk_hi(j) * nbh - pk_lo(j) * nbh;
-        return q8k_blocks<MQ>(hv[j & 1], nb > wv ? (nb - wv + NW - 1) / NW : 0, lane, hp, hd);
+        int nvalid = 0;   // the valid blocks are the first ones
+#pragma unroll
+        for (int m = 0; m < MQ; ++m) nvalid += int((hb_of(j, m) >> 8) & 1u);
+        return q8k_blocks<MQ>(hv[j & 1], nvalid, lane, hp, hd);
     };
     auto h_store = [&]<int j>(const uint32_t (&hp)[MQ], const float (&hd)[MQ], bool fin) {
-        const int b0 = pk_lo(j) * nbh, nb = pk_hi(j) * nbh - b0;
         if (!fin && lane == 0) set_err(a.err, kDevErrNonFinite);
 #pragma unroll
         for (int m = 0; m < MQ; ++m) {
-            const int bq = wv + NW * m;
-            if (bq < nb) {
-                const int blk = b0 + bq, i = blk / nbh, bb = blk - i * nbh;
+            const uint32_t b = hb_of(j, m);
+            if ((b >> 8) & 1u) {
+                const int i = int((b >> 4) & 15u), bb = int(b & 15u);
                 uint8_t* hq = lds + LY::HQ + i * hq_stride;
                 *reinterpret_cast<uint32_t*>(hq + qswz(256 * bb + 4 * lane)) = hp[m];
                 if (lane == 0) reinterpret_cast<float*>(hq + ff)[bb] = hd[m];

@@ -753,12 +753,14 @@ __global__ __launch_bounds__(NW * 64, 1) void stream_kernel(Layer3Args a) {
         // the next step's blocks go to LDS after the pass, then one barrier.
         Act<PD> B;
         static_for<MD>([&]<int j>() {   // steps past nsteps stage nothing and compute a discarded pass
-            if constexpr (j + 2 < MD) h_issue.template operator()<j + 2>();
-            if constexpr (j + WIND < MD) load_pass.template operator()<j + WIND>();
+            // the next step's h first (its loads went out a step ago), then the next
+            // pass's weight loads: issued before the check, their texture-unit time
+            // would delay it
             if constexpr (j + 1 < MD) {
                 h_wait.template operator()<j + 1>();
                 mark(24 + 2 * (j + 1));
             }
+            if constexpr (j + WIND < MD) load_pass.template operator()<j + WIND>();
             const int i = dpick(j);
             if (j == 0 || i != dpick(j > 0 ? j - 1 : 0)) load_act<PD>(B, lds, LY::HQ + i * hq_stride, ff, lD, LD);
             uint32_t hp[MQ];
@@ -794,6 +796,8 @@ __global__ __launch_bounds__(NW * 64, 1) void stream_kernel(Layer3Args a) {
             const float y = __fmul_rn(okf, gsum<LD>(f));
             if (j < nd && lD == LD - 1) ys[(wv + NW * j) * RD + rD] = y;
             if (j == 0) mark(5);
+            // the h loads of step j + 2 go out after the pass: later issue, fewer re-polls
+            if constexpr (j + 2 < MD) h_issue.template operator()<j + 2>();
             if constexpr (j + 1 < MD) {
                 h_store.template operator()<j + 1>(hp, hd, fin);
                 if (j + 1 < 3) mark(17 + j + 1);

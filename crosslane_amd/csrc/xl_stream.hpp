@@ -656,7 +656,9 @@ __global__ __launch_bounds__(NW * 64, 1) void stream_kernel(Layer3Args a) {
             bg = mine ? g : bg;
             bu = mine ? u : bu;
             hidx = mine ? hrow(j) + rG : hidx;
-            if (b == kBatch - 1 || j == MG - 1) {
+            // a batch's h goes out at its last slot, or at the wave's last valid slot
+            // (fewer picks than slots: published a slot or two sooner, fewer polls)
+            if (b == kBatch - 1 || j == MG - 1 || j == ng - 1) {
                 // (g / (1 + exp(-g))) * u with the device expf and an IEEE division, as
                 // q8k_core.hpp:92-95: an approximate exp or reciprocal moves h by an ulp
                 // often enough to flip Q8_K(h) quants (a 1e-4-scale output change each)

@@ -893,6 +893,9 @@ hipError_t launch_stream_shapes(const Layer3Args& args, int cus, hipStream_t s, 
     const int RD = 64 / ld;
     const int grid = std::min(cus, args.dim / RD);
     if (lg == 64 && pg == 1 && ld == 16 && pd == 3) {   // 4096 x 3072: slots and steps sized by the pick count
+        // one pick: 3,072 rows over 2,048 waves fill at most two slots per wave (a
+        // third, idle slot would re-read rows for nothing)
+        if (args.k == 1) return launch_stream_t<8, 64, 1, 16, 3, 2, 1, 2, 1, 3, GT, DT>(args, grid, s, stop);
         if (args.k <= 2) return launch_stream_t<8, 64, 1, 16, 3, 3, 1, 3, 1, 3, GT, DT>(args, grid, s, stop);
         if (args.k <= 4) return launch_stream_t<8, 64, 1, 16, 3, 6, 2, 3, 2, 3, GT, DT>(args, grid, s, stop);
         // one down pass in flight: its weights load under the last gate/up slot and

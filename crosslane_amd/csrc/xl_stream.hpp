@@ -295,12 +295,45 @@ __global__ __launch_bounds__(NW * 64, 1) void stream_kernel(Layer3Args a) {
     const int nq_wg = quads > int(blockIdx.x) ? (quads - int(blockIdx.x) + G - 1) / G : 0;
     const int P = k * nq_wg;
     const int nd = P > wv ? min(MD, (P - wv + NW - 1) / NW) : 0;
+    const int idl = a.ids[lane < k ? lane : k - 1];   // unconditional loads keep the wait counts exact
+    // ---- x and the codebook rows: they need no ids, so they go out right after
+    // the ids load (the wait for the ids then leaves them in flight) and before the
+    // slot loads. The rows come into registers (plain loads: waiting for them does
+    // not wait for the slot loads issued after them).
+    constexpr int NT = NW * 64;
+    constexpr bool HASXXS = (M & 1) != 0 || MIX, HASXS = (M & 2) != 0 || MIX;
+    constexpr bool HAS1 = (M & 4) != 0;
+    constexpr int NX = (4096 + NT - 1) / NT, NS = (1024 + NT - 1) / NT, N1 = (2048 + NT - 1) / NT;
+    // x first: its Q8_K runs while the codebook loads are in flight
+    constexpr int UX = (16 + NW - 1) / NW;
+    float4 xv[UX];
+#pragma unroll
+    for (int u = 0; u < UX; ++u) {
+        const int b = wv + NW * u;
+        xv[u] = reinterpret_cast<const float4*>(a.x + 256 * (b < nbx ? b : 0))[lane];
+    }
+    uint2 vx[HASXXS ? NX : 1], vs[HASXS ? NS : 1];
+    uint4 v1[HAS1 ? N1 : 1];
+    {
+        const uint2* gx = reinterpret_cast<const uint2*>(reinterpret_cast<const uint8_t*>(a.tables) + kG_XXS);
+        const uint2* gs = reinterpret_cast<const uint2*>(reinterpret_cast<const uint8_t*>(a.tables) + kG_XS);
+        const uint4* g1 = reinterpret_cast<const uint4*>(reinterpret_cast<const uint8_t*>(a.tables) + kTableIQ1X);
+        // chunk c of the XXS/sign table: row c / 16, 16-byte piece c % 16
+        if constexpr (HASXXS)
+#pragma unroll
+            for (int i = 0; i < NX; ++i) vx[i] = gx[min(t + NT * i, 4095) >> 4];
+        if constexpr (HASXS)
+#pragma unroll
+            for (int i = 0; i < NS; ++i) vs[i] = gs[min(t + NT * i, 1023) >> 1];   // chunk c: row c / 2, copies 2(c % 2), +1
+        if constexpr (HAS1)
+#pragma unroll
+            for (int i = 0; i < N1; ++i) v1[i] = g1[min(t + NT * i, 2047)];
+    }
     // Slot and pass metadata, computed lane-parallel and kept in one register:
     // lane j < 32 holds gate/up slot j, lane 32 + j down pass j, packed as
     // expert << 16 | pick << 12 | first row (bad ids read expert 0 and are
     // masked out). A use reads its lane back (v_readlane), so the scalar
     // registers stay free for the loads' addresses.
-    const int idl = a.ids[lane < k ? lane : k - 1];   // unconditional loads keep the wait counts exact
     const int idv = lane < k ? idl : -1;
     uint32_t meta;
     uint64_t okmask;   // bit j: slot j is this wave's with a valid id; bit 32 + j: pass j likewise
@@ -386,38 +419,7 @@ __global__ __launch_bounds__(NW * 64, 1) void stream_kernel(Layer3Args a) {
     const int bqg = (rG * nbx) & 3, bqd = (rD * nbh) & 3;
     auto mtype = [&](int pick, int role) { return __builtin_amdgcn_readlane(tb_ty, 16 * role + pick); };
 
-    // ---- codebook rows and x first (they need no ids), then the first slots. The
-    // rows come into registers (plain loads: waiting for them does not wait for
-    // the slot loads issued after them).
-    constexpr int NT = NW * 64;
-    constexpr bool HASXXS = (M & 1) != 0 || MIX, HASXS = (M & 2) != 0 || MIX;
-    constexpr bool HAS1 = (M & 4) != 0;
-    constexpr int NX = (4096 + NT - 1) / NT, NS = (1024 + NT - 1) / NT, N1 = (2048 + NT - 1) / NT;
-    // x first: its Q8_K runs while the codebook loads are in flight
-    constexpr int UX = (16 + NW - 1) / NW;
-    float4 xv[UX];
-#pragma unroll
-    for (int u = 0; u < UX; ++u) {
-        const int b = wv + NW * u;
-        xv[u] = reinterpret_cast<const float4*>(a.x + 256 * (b < nbx ? b : 0))[lane];
-    }
-    uint2 vx[HASXXS ? NX : 1], vs[HASXS ? NS : 1];
-    uint4 v1[HAS1 ? N1 : 1];
-    {
-        const uint2* gx = reinterpret_cast<const uint2*>(reinterpret_cast<const uint8_t*>(a.tables) + kG_XXS);
-        const uint2* gs = reinterpret_cast<const uint2*>(reinterpret_cast<const uint8_t*>(a.tables) + kG_XS);
-        const uint4* g1 = reinterpret_cast<const uint4*>(reinterpret_cast<const uint8_t*>(a.tables) + kTableIQ1X);
-        // chunk c of the XXS/sign table: row c / 16, 16-byte piece c % 16
-        if constexpr (HASXXS)
-#pragma unroll
-            for (int i = 0; i < NX; ++i) vx[i] = gx[min(t + NT * i, 4095) >> 4];
-        if constexpr (HASXS)
-#pragma unroll
-            for (int i = 0; i < NS; ++i) vs[i] = gs[min(t + NT * i, 1023) >> 1];   // chunk c: row c / 2, copies 2(c % 2), +1
-        if constexpr (HAS1)
-#pragma unroll
-            for (int i = 0; i < N1; ++i) v1[i] = g1[min(t + NT * i, 2047)];
-    }
+    // ---- the first slots (the codebook rows and x are in flight since the start)
     const float cw = a.w[lane < k ? lane : k - 1];
     uint32_t* ctl = a.ctl + 2;   // [0] parity source: launches of this kernel so far, [1] arrivals
     const uint32_t e_prev = coh_ld32(ctl);

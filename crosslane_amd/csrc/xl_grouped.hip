@@ -104,7 +104,13 @@ __device__ __forceinline__ long pack64(uint32_t lo, uint32_t hi) {
 __device__ __forceinline__ v4i mfma(long a, long b, v4i c) {
     return __builtin_amdgcn_mfma_i32_16x16x32_i8(a, b, c, 0, 0, 0);
 }
-__device__ __forceinline__ int mad24(int a, int b, int c) { return __mul24(a, b) + c; }   // v_mad_i32_i24
+__device__ __forceinline__ int mad24(int a, int b, int c) {   // v_mad_i32_i24
+    // the opaque result keeps the add from merging into a v_add3 (mul + add3 per
+    // pair of terms instead of one mad each)
+    int r = __mul24(a, b) + c;
+    asm volatile("" : "+v"(r));
+    return r;
+}
 // Bytewise negation of grid bytes (all in 1..127, so no byte borrows).
 __device__ __forceinline__ uint64_t neg_grid(uint64_t g) { return ~g + 0x0101010101010101ull; }
 

@@ -56,18 +56,19 @@ constexpr int kTabSgn = 0, kTabXXS = 2048, kTabXS = 4096;
 constexpr int kL_GRID = 0, kL_SGN = 65536, kL_TAB = 131072;
 // Per work item, staged once by the workgroup (each wave would otherwise issue
 // these small loads every block): the 16 pairs' activation block scales
-// [block][pair] (f32), then the item's 128 rows' fp16 block scales [row][block]
-// for each matrix, then (down) the rows' IQ2_XS scale bytes [row][block][8].
+// [block][pair] (f32), then the item's rows' fp16 block scales [row][block]
+// for each matrix (gate/up: NW x 16 rows, down: 128), then (down) the rows'
+// IQ2_XS scale bytes [row][block][8].
 // Blocks per row these regions hold: gate/up rows of dim <= kMaxRowK, down
 // rows of ff <= 4096.
 constexpr int kGuNb = kMaxRowK / 256, kDnNb = 16;
 constexpr int kL_PD = kL_TAB;
-constexpr int kL_RDG = kL_PD + 16 * kGuNb * 4;     // gate/up: 2 planes of 128 rows x kGuNb fp16 scales
-constexpr int kL_GuBytes = kL_RDG + 2 * 128 * kGuNb * 2;
+constexpr int kL_RDG = kL_PD + 16 * kGuNb * 4;     // gate/up: 2 planes of `rows` rows x kGuNb fp16 scales
+constexpr int gu_lds_bytes(int rows) { return kL_RDG + 2 * rows * kGuNb * 2; }
 constexpr int kL_RDD = kL_PD + 16 * kDnNb * 4;     // down: 128 rows x kDnNb fp16 scales, then scale bytes
 constexpr int kL_RS = kL_RDD + 128 * kDnNb * 2;
 constexpr int kL_DnBytes = kL_RS + 128 * kDnNb * 8;
-static_assert(kL_GuBytes <= 160 * 1024 && kL_DnBytes <= 160 * 1024, "LDS budget");
+static_assert(gu_lds_bytes(12 * 16) <= 160 * 1024 && kL_DnBytes <= 160 * 1024, "LDS budget");
 constexpr int kCopiesXXS = 16;   // 256 entries x 256 B: the entry byte lands in address byte 1
 constexpr int kCopiesXS = 8;     // 512 entries x 128 B: the 9-bit entry lands at address bit 7
 
@@ -307,10 +308,10 @@ struct DnOps {
 };
 
 // Stages one item's pair scales (scl: one f32 per (pair row, block), pairs of
-// the task's order slots) and `mats` planes of fp16 row scales (128 rows from
+// the task's order slots) and `mats` planes of fp16 row scales (ROWS rows from
 // row0, nb per row, contiguous in each plane) into LDS, between two barriers.
 // The planes go to LDS at rd, `mstride` bytes apart.
-template <int NT>
+template <int NT, int ROWS>
 __device__ __forceinline__ void stage_item(uint8_t* lds, const GroupArgs& a, const int4& tk, const float* scl, int per_pair,
                                            int nb, const uint8_t* const* planes, int mats, int row0, int t, int rd,
                                            int mstride) {
@@ -320,7 +321,7 @@ __device__ __forceinline__ void stage_item(uint8_t* lds, const GroupArgs& a, con
         const int p = a.order[tk.y + min(pos, tk.z - 1)];
         reinterpret_cast<float*>(lds + kL_PD)[i] = scl[size_t(per_pair ? p : p / a.k) * nb + blk];
     }
-    const int chunks = 128 * nb * 2 / 16;   // 16-byte pieces of one plane's 128 rows
+    const int chunks = ROWS * nb * 2 / 16;   // 16-byte pieces of one plane's rows
     for (int i = t; i < mats * chunks; i += NT) {
         const int m = i / chunks, c = i - m * chunks;
         const uint4 v = reinterpret_cast<const uint4*>(planes[m] + size_t(row0) * nb * 2)[c];
@@ -335,7 +336,7 @@ __device__ __forceinline__ void stage_item(uint8_t* lds, const GroupArgs& a, con
 // TR: also write each pair's block integers (GroupArgs::tint).
 template <int NW, bool TR>
 __global__ __launch_bounds__(NW * 64, 1) void gu_kernel(GroupArgs a) {
-    __shared__ __attribute__((aligned(16))) uint8_t lds[kL_GuBytes];
+    __shared__ __attribute__((aligned(16))) uint8_t lds[gu_lds_bytes(NW * 16)];
     const int t = threadIdx.x, lane = t & 63, wv = t >> 6;
     fill_grid<256, kCopiesXXS>(lds, a.tables + kTabXXS / 8, t, NW * 64);
     fill_signs(lds, a.tables, t, NW * 64);
@@ -363,7 +364,7 @@ __global__ __launch_bounds__(NW * 64, 1) void gu_kernel(GroupArgs a) {
         const MatRef G = mat_at(a.descs, tk.x, 0), U = mat_at(a.descs, tk.x, 1);
         {
             const uint8_t* planes[2] = {G.base + G.off1, U.base + U.off1};
-            stage_item<NW * 64>(lds, a, tk, a.xd, 0, nb, planes, 2, grp * NW * 16, t, kL_RDG, 128 * kGuNb * 2);
+            stage_item<NW * 64, NW * 16>(lds, a, tk, a.xd, 0, nb, planes, 2, grp * NW * 16, t, kL_RDG, NW * 16 * kGuNb * 2);
         }
         const __amdgpu_buffer_rsrc_t rg = rsrc(G.base), ru = rsrc(U.base), rx = rsrc(a.xq);
         const uint32_t vq = uint32_t(row * nb) * 64u;
@@ -394,7 +395,7 @@ __global__ __launch_bounds__(NW * 64, 1) void gu_kernel(GroupArgs a) {
             for (int r = 0; r < 4; ++r) bi[r] = mad24(ls, C[r], bi[r]);
         };
         const uint16_t* sdg = reinterpret_cast<const uint16_t*>(lds + kL_RDG) + (wv * 16 + col) * nb;
-        const uint16_t* sdu = sdg + 128 * kGuNb;
+        const uint16_t* sdu = sdg + NW * 16 * kGuNb;
         int blk_c = 0;   // block the next compute() handles
         auto compute = [&](const GuOps& o) {
             const int b = blk_c++;
@@ -489,6 +490,7 @@ __device__ __forceinline__ void xs_lane(const uint4& w, uint32_t (&u)[4]) {
 // ---------------------------------------------------------------------------
 template <int NW, bool TR>
 __global__ __launch_bounds__(NW * 64, 1) void dn_kernel(GroupArgs a) {
+    static_assert(NW * 16 == 128, "the down staging holds 128 rows");
     __shared__ __attribute__((aligned(16))) uint8_t lds[kL_DnBytes];
     const int t = threadIdx.x, lane = t & 63, wv = t >> 6;
     fill_grid<512, kCopiesXS>(lds, a.tables + kTabXS / 8, t, NW * 64);
@@ -517,7 +519,7 @@ __global__ __launch_bounds__(NW * 64, 1) void dn_kernel(GroupArgs a) {
         {
             const int row0 = grp * NW * 16;
             const uint8_t* planes[1] = {D.base + D.off2};
-            stage_item<NW * 64>(lds, a, tk, a.hd, 1, nb, planes, 1, row0, t, kL_RDD, 0);
+            stage_item<NW * 64, 128>(lds, a, tk, a.hd, 1, nb, planes, 1, row0, t, kL_RDD, 0);
             const int chunks = 128 * nb * 8 / 16;   // the rows' IQ2_XS scale bytes
             for (int i = t; i < chunks; i += NW * 64)
                 *reinterpret_cast<uint4*>(lds + kL_RS + 16 * i) =
@@ -632,24 +634,33 @@ __global__ __launch_bounds__(256) void gcombine_kernel(GroupArgs a) {
 }  // namespace
 
 hipError_t launch_grouped(const GroupArgs& args, int cus, hipStream_t s) {
+    // down: 8 waves per workgroup; gate/up: 12 (3 per SIMD, 192 rows per item)
+    // where ff allows, else 8
     constexpr int NW = 8;
     if (args.T < 1 || args.k < 1 || args.k > 16 || args.n_experts > kGroupMaxExperts || args.dim % (NW * 16) ||
         args.ff % (NW * 16) || args.dim % 256 || args.ff % 256 || args.dim > kGuNb * 256 || args.ff > kDnNb * 256)
         return hipErrorNotSupported;
+    const bool gu12 = args.ff % (12 * 16) == 0;
     const int P = args.T * args.k;
     hipLaunchKernelGGL(bucket_kernel, dim3(1), dim3(1024), 0, s, args);
     const int nbx = args.dim / 256, nbh = args.ff / 256;
     if (args.tq8x || args.tq8h || args.th || args.tint) {   // the parity trace (separate instances)
         hipLaunchKernelGGL((q8k_rows_kernel<ROWS_X, true>), dim3((args.T * nbx + 3) / 4), dim3(256), 0, s, args.x,
                            args.T, nbx, args.xq, args.xd, args.pos, args.k, args.err, args.tq8x);
-        hipLaunchKernelGGL((gu_kernel<NW, true>), dim3(cus), dim3(NW * 64), 0, s, args);
+        if (gu12)
+            hipLaunchKernelGGL((gu_kernel<12, true>), dim3(cus), dim3(12 * 64), 0, s, args);
+        else
+            hipLaunchKernelGGL((gu_kernel<NW, true>), dim3(cus), dim3(NW * 64), 0, s, args);
         hipLaunchKernelGGL((q8k_rows_kernel<ROWS_H, true>), dim3((P * nbh + 3) / 4), dim3(256), 0, s, args.h, P, nbh,
                            args.hq, args.hd, args.pos, args.k, args.err, args.tq8h);
         hipLaunchKernelGGL((dn_kernel<NW, true>), dim3(cus), dim3(NW * 64), 0, s, args);
     } else {
         hipLaunchKernelGGL((q8k_rows_kernel<ROWS_X, false>), dim3((args.T * nbx + 3) / 4), dim3(256), 0, s, args.x,
                            args.T, nbx, args.xq, args.xd, args.pos, args.k, args.err, nullptr);
-        hipLaunchKernelGGL((gu_kernel<NW, false>), dim3(cus), dim3(NW * 64), 0, s, args);
+        if (gu12)
+            hipLaunchKernelGGL((gu_kernel<12, false>), dim3(cus), dim3(12 * 64), 0, s, args);
+        else
+            hipLaunchKernelGGL((gu_kernel<NW, false>), dim3(cus), dim3(NW * 64), 0, s, args);
         hipLaunchKernelGGL((q8k_rows_kernel<ROWS_H, false>), dim3((P * nbh + 3) / 4), dim3(256), 0, s, args.h, P, nbh,
                            args.hq, args.hd, args.pos, args.k, args.err, nullptr);
         hipLaunchKernelGGL((dn_kernel<NW, false>), dim3(cus), dim3(NW * 64), 0, s, args);

@@ -226,24 +226,6 @@ __device__ __forceinline__ void decode_slot(int (&Ig)[PG], int (&Iu)[PG], uint32
         Iu[q] = sum_t<TU_, true>(Lu, u, A.a[q], NA[NQ > 1 ? q : 0], pp, du[q]);
     }
 }
-// One row of a slot whose gate and up types differ (mixed instance), type t at run time.
-template <int PG, int NQ>
-__device__ __forceinline__ void decode_row(int t, int (&I)[PG], uint32_t (&d)[PG], const Raw3 (&R)[PG],
-                                           const Act<PG>& A, const uint32_t (&NA)[NQ][16], const uint8_t* lds,
-                                           const LoLanes& lo, int lG, int LG, int bq) {
-    auto one = [&]<int T>() {
-#pragma unroll
-        for (int q = 0; q < PG; ++q) {
-            const Raw3 r = pair_view<T, true>(R[q], bq, lG + LG * q);
-            Looks L;
-            look_t<T>(L, lds, lo, r);
-            I[q] = sum_t<T, true>(L, r, A.a[q], NA[NQ > 1 ? q : 0], (lG + LG * q) & 3, d[q]);
-        }
-    };
-    if (t == kIQ2_XXS) one.template operator()<1>();
-    else if (t == kIQ2_XS) one.template operator()<2>();
-    else one.template operator()<4>();
-}
 // A down pass (PD pairs per lane) of static type T: the next pair's lookups are
 // issued before the current pair's arithmetic.
 template <int T, bool V, int PD>
@@ -612,23 +594,16 @@ __global__ __launch_bounds__(NW * 64, 1) void stream_kernel(Layer3Args a) {
             if constexpr (j == (2 * MG) / 3) __builtin_amdgcn_s_setprio(0);
             if constexpr (j >= 1 && j + WIN - 1 < MG) load_slot.template operator()<j + WIN - 1>();
             if constexpr (j >= MG - WIND) load_pass.template operator()<j - (MG - WIND)>();   // the down stream starts under the last slots
-            int tg = 0, tu = 0;
-            if constexpr (MIX) {
-                const int pk = int((gsl(j) >> 12) & 15u);
-                tg = mtype(pk, 0);
-                tu = mtype(pk, 1);
-            }
+            // (gate and up share a block type: xl_open rejects a bank where they differ)
+            const int tg = MIX ? mtype(int((gsl(j) >> 12) & 15u), 0) : 0;
             int Ig[PG], Iu[PG];
             uint32_t dg[PG], du[PG];
             if constexpr (!MIX) {
                 decode_slot<GT, GT, false>(Ig, Iu, dg, du, rg[j % WIN], ru[j % WIN], A, NA, lds, lo, lG, LG, 0);
-            } else if (tg == tu) {   // one branch per slot, static types inside
+            } else {   // one branch per slot, static types inside
                 if (tg == kIQ2_XXS) decode_slot<1, 1, true>(Ig, Iu, dg, du, rg[j % WIN], ru[j % WIN], A, NA, lds, lo, lG, LG, bqg);
                 else if (tg == kIQ2_XS) decode_slot<2, 2, true>(Ig, Iu, dg, du, rg[j % WIN], ru[j % WIN], A, NA, lds, lo, lG, LG, bqg);
                 else decode_slot<4, 4, true>(Ig, Iu, dg, du, rg[j % WIN], ru[j % WIN], A, NA, lds, lo, lG, LG, bqg);
-            } else {
-                decode_row(tg, Ig, dg, rg[j % WIN], A, NA, lds, lo, lG, LG, bqg);
-                decode_row(tu, Iu, du, ru[j % WIN], A, NA, lds, lo, lG, LG, bqg);
             }
             float fg = 0.0f, fu = 0.0f;
 #pragma unroll

@@ -18,10 +18,11 @@ steps touch different experts (the bank is ~3.9 GB, far beyond the 256 MB MALL).
      of its pairs, int8 MFMA);
   3  a 40-layer pass per step: 40 x 384 experts whose whole-expert type is
      drawn 17 % IQ2_XS / 19 % IQ2_XXS / 64 % IQ1_M, top-6 per layer, the
-     hidden carried layer to layer through an RMS normalization (torch's
-     rms_norm on the same stream, inside the timed region: the model's RMSNorm
-     stand-in, without which the quadratic SwiGLU overflows f32 within a few
-     layers).
+     hidden carried layer to layer through an RMS normalization (the library's
+     hyper-connection pre + RMS norm, xl_hc_pre_norm_async, with one stream and
+     a unit weight, on the same stream inside the timed region: the model's
+     ffn_norm step, without which the quadratic SwiGLU overflows f32 within a
+     few layers).
 
 Prints one JSON line: value = achieved algorithmic HBM GB/s (selected experts'
 weight bytes + x in + out per layer), plus us_per_layer; the roofline of the
@@ -290,7 +291,6 @@ def main():
     warmup = args.warmup if args.warmup >= 0 else {3: 5, 4: 5}.get(cfg, 100)
 
     import torch
-    import torch.nn.functional as F
     import crosslane_amd as xl
 
     # ---- bank and routes
@@ -364,6 +364,10 @@ def main():
         d_w = torch.from_numpy(w).cuda()
         d_x = torch.from_numpy(x).cuda()
         d_h = torch.zeros((L + 1, DIM), dtype=torch.float32, device="cuda")   # config 3: final hiddens of the passes
+        d_hn = torch.zeros(DIM, dtype=torch.float32, device="cuda")           # config 3: the carried hidden
+        d_mix1 = torch.zeros(8, dtype=torch.float32, device="cuda")
+        d_mix1[0] = 1.0
+        d_ones = torch.ones(DIM, dtype=torch.float32, device="cuda")
         d_y = torch.zeros(DIM, dtype=torch.float32, device="cuda")             # config 3: a layer's raw output
         d_out = torch.zeros((n_r, TOK, DIM) if cfg == 4 else (n_r, DIM), dtype=torch.float32, device="cuda")
         d_logits = torch.from_numpy(logits).cuda() if droute else None
@@ -403,7 +407,9 @@ def main():
             h = d_x[r]
             for l in range(L):
                 lane.layer_forward_async(l, d_ids[r, l], d_w[r, l], h, d_y, stream=sp)
-                h = F.rms_norm(d_y, (DIM,), eps=1e-6)   # RMS-normalized hidden for the next layer, read in place
+                # RMS-normalized hidden for the next layer (one stream, mix 1, unit weight)
+                lane.hc_pre_norm_async(d_y.view(1, 1, DIM), d_mix1, d_ones, d_hn.view(1, DIM), eps=1e-6, stream=sp)
+                h = d_hn
             d_h[r % (L + 1)].copy_(h)   # the pass's final hidden (checked for finiteness after timing)
 
     for i in range(warmup):

@@ -1461,6 +1461,32 @@ int32_t xl_shared_forward_noalloc(xl_context* ctx, int32_t type_gate, const void
     });
 }
 
+int32_t xl_hc_pre_norm_async(xl_context* ctx, const float* d_h, const float* d_mix, const float* d_w_or_null,
+                             int32_t D, int32_t H, int32_t T, float eps, float* d_x, void* stream, xl_error* err) {
+    return guarded(ctx, err, [&] {
+        ready(ctx, false);
+        // hc.cpp:5-7,89-92: geometry, a finite positive epsilon, no null input,
+        // x neither h itself nor overlapping h, mix or w
+        need(d_h && d_mix && d_x, XL_E_ARG, "null device pointer");
+        need(D >= 1 && D <= 32768 && H >= 1 && H <= 4 && T >= 1 && T <= 8192, XL_E_ARG,
+             "hc geometry: D in 1..32768, H in 1..4, T in 1..8192");
+        need(std::isfinite(eps) && eps > 0.0f, XL_E_ARG, "hc epsilon must be finite and positive");
+        const uint64_t xb = uint64_t(T) * D * 4;
+        const auto overlaps = [&](const void* p, uint64_t bytes) {
+            const uintptr_t a = reinterpret_cast<uintptr_t>(d_x), b = reinterpret_cast<uintptr_t>(p);
+            return a <= b ? b - a < xb : a - b < bytes;
+        };
+        need(!overlaps(d_h, uint64_t(T) * H * D * 4) && !overlaps(d_mix, uint64_t(T) * 32) &&
+                 (!d_w_or_null || !overlaps(d_w_or_null, uint64_t(D) * 4)),
+             XL_E_ARG, "hc output overlaps an input");
+        hipStream_t s = pick_stream(ctx, stream);
+        Ordered ord(ctx, s);
+        hip_check(xl::dev::launch_hc_pre_norm(d_h, d_mix, d_w_or_null, D, H, T, eps, d_x, s, ord.stop()),
+                  "hc_pre_norm launch");
+        ord.carried_by_launch(true);   // the launch records the ordering event itself
+    });
+}
+
 int32_t xl_hc_post_async(xl_context* ctx, const float* d_y, const float* d_res, const float* d_post,
                          const float* d_comb, int32_t D, int32_t H, int32_t T, float* d_out, void* stream,
                          xl_error* err) {
@@ -1482,8 +1508,8 @@ int32_t xl_hc_post_async(xl_context* ctx, const float* d_y, const float* d_res, 
              XL_E_ARG, "hc output overlaps an input");
         hipStream_t s = pick_stream(ctx, stream);
         Ordered ord(ctx, s);
-        hip_check(xl::dev::launch_hc_post(d_y, d_res, d_post, d_comb, D, H, T, d_out, s),
-                  "hc_post launch");
+        hip_check(xl::dev::launch_hc_post(d_y, d_res, d_post, d_comb, D, H, T, d_out, s, ord.stop()), "hc_post launch");
+        ord.carried_by_launch(true);   // the launch records the ordering event itself
     });
 }
 

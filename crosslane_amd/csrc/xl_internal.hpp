@@ -216,8 +216,11 @@ hipError_t launch_mv32(const ExpertDesc* descs, const int32_t* ids, const MatRef
 // Hyper-connection post (sycl/hc/core.hpp:81-86) of T tokens, H <= 4 streams
 // of D: out[t][k][e] = post[t][k] * y[t][e] + sum_j comb[t][j * H + k] *
 // res[t][j][e]; out may equal res (in place).
+// stop: recorded as the launch completes (the caller's ordering event)
+hipError_t launch_hc_pre_norm(const float* h, const float* mix, const float* w, int D, int H, int T, float eps,
+                              float* x, hipStream_t s, hipEvent_t stop);
 hipError_t launch_hc_post(const float* y, const float* res, const float* post, const float* comb, int D, int H, int T,
-                          float* out, hipStream_t s);
+                          float* out, hipStream_t s, hipEvent_t stop);
 // h = g / (1 + exp(-g)) * u (lim > 0: g, u clamped first) of rows x k values,
 // quantized per 32 into q, d exactly as launch_quant32 would quantize h.
 hipError_t launch_swiglu_quant32(const float* g, const float* u, int rows, int k, float lim, int8_t* q, float* d,

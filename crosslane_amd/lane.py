@@ -104,6 +104,7 @@ _SIGNATURES = {
                                        _ErrP]),
     "xl_shared_forward_noalloc": (_I32, [_P, _I32, _P, _I32, _P, _I32, _P, _I32, _I32, _P, _P, _P, _ErrP]),
     "xl_hc_post_async": (_I32, [_P, _P, _P, _P, _P, _I32, _I32, _I32, _P, _P, _ErrP]),
+    "xl_hc_pre_norm_async": (_I32, [_P, _P, _P, _P, _I32, _I32, _I32, C.c_float, _P, _P, _ErrP]),
     "xl_profile_begin": (_I32, [_P, _I32, _ErrP]),
     "xl_profile_end": (_I32, [_P, _f32p, _I32, C.POINTER(_I32), C.POINTER(_I32), C.c_char_p, _I32, _ErrP]),
     "xl_profile_timeline": (_I32, [_P, _u64p, _I32, C.POINTER(_I32), _ErrP]),
@@ -448,6 +449,12 @@ class Lane:
         T = int(x.numel()) // self.dim
         self._call("xl_shared_forward_noalloc", int(types[0]), _ptr(gate), int(types[1]), _ptr(up), int(types[2]),
                    _ptr(down), ff, T, _ptr(x), _ptr(out), None if stream is None else int(stream))
+
+    def hc_pre_norm_async(self, h, mix, w, x, eps: float = 1e-6, stream=None) -> None:
+        """h [T, H, D], mix [T, 8], w [D] or None, x [T, D] device tensors."""
+        T, H, D = (int(v) for v in h.shape)
+        self._call("xl_hc_pre_norm_async", _ptr(h), _ptr(mix), _ptr(w), D, H, T, float(eps), _ptr(x),
+                   None if stream is None else int(stream))
 
     def hc_post_async(self, y, res, post, comb, out, stream=None) -> None:
         """y [T, D], res / out [T, H, D], post [T, 8], comb [T, 64] device tensors."""

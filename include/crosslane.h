@@ -310,6 +310,16 @@ int32_t xl_shared_forward_async(xl_context* ctx, int32_t type_gate, const void* 
 int32_t xl_shared_forward_noalloc(xl_context* ctx, int32_t type_gate, const void* d_gate, int32_t type_up,
                                   const void* d_up, int32_t type_down, const void* d_down, int32_t ff, int32_t T,
                                   const float* d_x, float* d_out, void* stream, xl_error* err);
+/* Hyper-connection pre + RMS norm that makes the MoE block's input
+ * (hip_backend.cpp:629 k4::hc_pre_norm with the layer's ffn_norm; sycl/hc/
+ * hc.cpp:89-106, core.hpp:74-80): for T tokens of H <= 4 streams of D,
+ * x[t][e] = sum_j mix[t][j] * h[t][j][e] (j ascending), then, when w is not
+ * null, x[t][e] = x[t][e] * inv * w[e] with inv = 1 / sqrt(S / D + eps) and S
+ * the sum of x^2 in the reference's fixed order (1024 lane sums, 32-lane XOR
+ * trees). h T x H x D, mix T x 8, w D, x T x D; bit-identical to the
+ * reference. x may not overlap h, mix or w; eps finite and positive. */
+int32_t xl_hc_pre_norm_async(xl_context* ctx, const float* d_h, const float* d_mix, const float* d_w_or_null,
+                             int32_t D, int32_t H, int32_t T, float eps, float* d_x, void* stream, xl_error* err);
 /* Hyper-connection post after the MoE block (hip_backend.cpp:777 k4::hc_post;
  * sycl/hc/hc.cpp:107-115, core.hpp:81-86): for T tokens and H <= 4 streams of
  * D, out[t][k][e] = post[t][k] * y[t][e] + sum_j comb[t][j * H + k] *

@@ -70,6 +70,7 @@ class Oracle:
         L.orc_row_bytes32.restype = C.c_int
         L.orc_dequant32.argtypes = [C.c_int, _u8p, C.c_int, np.ctypeslib.ndpointer(np.float64, flags="C_CONTIGUOUS")]
         L.orc_hc_post.argtypes = [_f32p, _f32p, _f32p, _f32p, C.c_int, C.c_int, C.c_int, _f32p]
+        L.orc_hc_pre_norm.argtypes = [_f32p, _f32p, _P, C.c_int, C.c_int, C.c_int, C.c_float, _f32p]
         L.orc_expert32.argtypes = [_i32p, _u8p, _u8p, _u8p, C.c_int, C.c_int, _f32p, _f32p, _P, _P, _P, C.c_float]
         L.orc_gen_key.argtypes = [C.c_uint64, C.c_uint32, C.c_uint32, C.c_uint32]
         L.orc_gen_key.restype = C.c_uint64
@@ -194,6 +195,16 @@ class Oracle:
         self.lib.orc_dequant32(t, np.ascontiguousarray(row, dtype=np.uint8).reshape(-1), kb, out)
         return out
 
+    def hc_pre_norm(self, h, mix, w, eps=1e-6):
+        """sycl/hc/core.hpp:74-80: h [T, H, D], mix [T, 8], w [D] or None -> x [T, D]."""
+        T, H, D = (int(v) for v in np.shape(h))
+        x = np.zeros((T, D), np.float32)
+        wv = None if w is None else np.ascontiguousarray(w, dtype=np.float32).reshape(-1)
+        self.lib.orc_hc_pre_norm(np.ascontiguousarray(h, dtype=np.float32).reshape(-1),
+                                 np.ascontiguousarray(mix, dtype=np.float32).reshape(-1),
+                                 None if wv is None else wv.ctypes.data, D, H, T, float(eps), x.reshape(-1))
+        return x
+
     def hc_post(self, y, res, post, comb, D, H, T):
         """sycl/hc/core.hpp:81-86: y [T, D], res [T, H, D], post [T, 8], comb [T, 64] -> [T, H, D]."""
         out = np.zeros((T, H, D), np.float32)
@@ -267,6 +278,7 @@ class Reference:
         L.ref_table.argtypes = [C.c_int, _u64p]
         L.ref_decode.argtypes = [C.c_int, _u8p, C.c_int, _i32p, _i32p, C.POINTER(C.c_float), _P]
         L.ref_hc_post.argtypes = [_f32p, _f32p, _f32p, _f32p, C.c_int, C.c_int, C.c_int, _f32p]
+        L.ref_hc_pre_norm.argtypes = [_f32p, _f32p, _P, C.c_int, C.c_int, C.c_int, C.c_float, _f32p]
         L.ref_matvec.argtypes = [C.c_int, _u8p, C.c_int, C.c_int, _P, _f32p, C.c_int]
         L.ref_combine.argtypes = [_i32p, _f32p, C.c_int, _f32p, C.c_int, _f32p, _f32p]
         L.ref_route.argtypes = [_f32p, C.c_int, _f32p, C.c_int, C.c_int, C.c_int, C.c_float, _i32p, _f32p]
@@ -316,6 +328,15 @@ class Reference:
         m = np.zeros(2, dtype=np.float32)
         self.lib.ref_decode(t, np.ascontiguousarray(row), kb, q, s, C.byref(d), m.ctypes.data)
         return q, s, d.value, m
+
+    def hc_pre_norm(self, h, mix, w, eps=1e-6):
+        T, H, D = (int(v) for v in np.shape(h))
+        x = np.zeros((T, D), np.float32)
+        wv = None if w is None else np.ascontiguousarray(w, dtype=np.float32).reshape(-1)
+        self.lib.ref_hc_pre_norm(np.ascontiguousarray(h, dtype=np.float32).reshape(-1),
+                                 np.ascontiguousarray(mix, dtype=np.float32).reshape(-1),
+                                 None if wv is None else wv.ctypes.data, D, H, T, float(eps), x.reshape(-1))
+        return x
 
     def hc_post(self, y, res, post, comb, D, H, T):
         out = np.zeros((T, H, D), np.float32)

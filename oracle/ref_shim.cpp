@@ -61,6 +61,10 @@ void ref_decode(int t, const uint8_t* row, int kb, int* q32, int* s2, float* d, 
     s2[0] = s.s[0]; s2[1] = s.s[1]; *d = s.d;
     if (m2) { m2[0] = s.m[0]; m2[1] = s.m[1]; }
 }
+// hc_scalar::pre_norm over T tokens.
+void ref_hc_pre_norm(const float* h, const float* mix, const float* w, int D, int H, int T, float eps, float* x) {
+    for (int t = 0; t < T; ++t) strata::ds4::hc_scalar::pre_norm(h, mix, w, D, H, t, eps, x);
+}
 // hc_scalar::post over T tokens x D values.
 void ref_hc_post(const float* y, const float* res, const float* post, const float* comb, int D, int H, int T, float* out) {
     for (int t = 0; t < T; ++t)

@@ -525,6 +525,45 @@ void orc_hc_post(const float* y, const float* res, const float* post, const floa
         }
 }
 
+/* ---- hyper-connection pre + RMS norm (sycl/hc/core.hpp:74-80 pre_norm,
+ * block_sum core.hpp:9-17; hc.cpp:89-106) -----------------------------------
+ * Per token t: x[e] = sum_j mix[t][j] * h[t][j][e] (j ascending from 0.0f,
+ * separate roundings); 1024 lane sums, lane i over e = i, i + 1024, ... of
+ * x[e] * x[e]; their total by a pairwise XOR tree over each 32 lanes
+ * (offsets 16, 8, 4, 2, 1, lane 0's result), then the same tree over the 32
+ * group totals; with w, x[e] = (x[e] * inv) * w[e], inv = 1 / sqrtf(total / D
+ * + eps). mix: T x 8 floats. */
+static float orc_xor32(const float* p) {
+    float v[32];
+    for (int i = 0; i < 32; ++i) v[i] = p[i];
+    for (int o = 16; o; o >>= 1)
+        for (int i = 0; i < 32; ++i)
+            if (!(i & o)) v[i] += v[i ^ o];
+    return v[0];
+}
+void orc_hc_pre_norm(const float* h, const float* mix, const float* w, int D, int H, int T, float eps, float* x) {
+    for (int t = 0; t < T; ++t) {
+        const float* hh = h + (size_t)t * H * D;
+        const float* mm = mix + (size_t)t * 8;
+        float* xx = x + (size_t)t * D;
+        float lanes[1024], red[32];
+        for (int i = 0; i < 1024; ++i) {
+            float ss = 0.0f;
+            for (int e = i; e < D; e += 1024) {
+                float a = 0.0f;
+                for (int j = 0; j < H; ++j) a += mm[j] * hh[(size_t)j * D + e];
+                xx[e] = a;
+                ss += a * a;
+            }
+            lanes[i] = ss;
+        }
+        if (!w) continue;
+        for (int g = 0; g < 32; ++g) red[g] = orc_xor32(lanes + 32 * g);
+        const float inv = 1.0f / sqrtf(orc_xor32(red) / (float)D + eps);
+        for (int e = 0; e < D; ++e) xx[e] = xx[e] * inv * w[e];
+    }
+}
+
 /* ---- router: route.cpp:15-37 ---------------------------------------------
  * Per token: softplus(l) (l itself above 20), its square root as the score,
  * the score plus the expert's bias as the selection key; k rounds of "first

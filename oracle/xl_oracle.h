@@ -115,6 +115,7 @@ void orc_lane_layer(int k, const int* types, const uint8_t* const* mats, int dim
 
 /* Hyper-connection post (sycl/hc/core.hpp:81-86) of T tokens, H streams of D. */
 void orc_hc_post(const float* y, const float* res, const float* post, const float* comb, int D, int H, int T, float* out);
+void orc_hc_pre_norm(const float* h, const float* mix, const float* w, int D, int H, int T, float eps, float* x);
 
 #ifdef __cplusplus
 }

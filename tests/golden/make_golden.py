@@ -135,6 +135,13 @@ def main():
     hcomb = rng2.random((T, 64)).astype(np.float32)
     out["hc_y"], out["hc_res"], out["hc_post"], out["hc_comb"] = hy, hres, hpost, hcomb
     out["hc_out"] = ref.hc_post(hy, hres, hpost, hcomb, D, H, T)
+    # hyper-connection pre + RMS norm (sycl/hc/core.hpp:74-80): T = 2, H = 4, D = 1500
+    T, H, D = 2, 4, 1500
+    ph = rng2.standard_normal((T, H, D)).astype(np.float32)
+    pmix = rng2.standard_normal((T, 8)).astype(np.float32)
+    pw = rng2.standard_normal(D).astype(np.float32)
+    out["hcpre_h"], out["hcpre_mix"], out["hcpre_w"] = ph, pmix, pw
+    out["hcpre_x"] = ref.hc_pre_norm(ph, pmix, pw, 1e-6)
     np.savez_compressed(OUT, **out)
     print("wrote", OUT, sum(v.nbytes for v in out.values()), "bytes")
 

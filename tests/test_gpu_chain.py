@@ -1,17 +1,24 @@
 """GPU parity of the full 40-layer expert pass: 40 layers
 at d_model 4096, d_ff 3072, each expert's three matrices of one type drawn 17 %
 IQ2_XS / 19 % IQ2_XXS / 64 % IQ1_M, top-6 per layer, the hidden carried layer to
-layer on the device (RMS-normalized layer output, the model's RMSNorm stand-in;
-without it the quadratic SwiGLU overflows f32 within a few layers).
+layer on the device by the library's hyper-connection pre + RMS norm with one
+stream and a unit weight (xl_hc_pre_norm_async: the RMS norm of the layer output
+in the reference's fixed order, sycl/hc/core.hpp:74-80; without a norm the
+quadratic SwiGLU overflows f32 within a few layers).
 
 Bars (north star): every layer's output within max relative error 1e-3 of the
 oracle fed that layer's own device input (the oracle takes the carried hidden
 as the device holds it, as the reference's probe feeds the device's own h,
-warm/expert_check.cpp:86-88); the final hidden within 1e-3 of the oracle's own
-40-layer chain from the same input (the normalization restated in numpy); and
-the whole pass bit-identical run to run (warm/hip_batch_check.cpp:28-110 repeats
-its batches the same way). A small E per layer keeps the oracle's work small;
-the kernels see the full-size matrices.
+warm/expert_check.cpp:86-88); every carried hidden bit-identical to the
+oracle's norm of the device's layer output; and the whole pass bit-identical
+run to run (warm/hip_batch_check.cpp:28-110 repeats its batches the same way).
+Together these pin every step of the pass. The final hidden against the
+oracle's own 40-layer chain from the same input is reported, not asserted: this
+synthetic map amplifies rounding-level differences once a Q8_K rounding flips
+(two oracle chains whose norms differ only in the last bit agree to 2.5e-7
+through layer 31 and differ by 0.3 at layer 40), so an end-to-end bar would
+test the seed, not the kernels. A small E per layer keeps the oracle's work
+small; the kernels see the full-size matrices.
 """
 from __future__ import annotations
 
@@ -45,9 +52,12 @@ def chain_routes():
     return ids, w, x0
 
 
-def rms_norm_np(y, eps=1e-6):
-    y = y.astype(np.float32)
-    return (y / np.sqrt(np.mean(y.astype(np.float64) ** 2) + eps)).astype(np.float32)
+MIX1 = np.eye(1, 8, dtype=np.float32)   # one stream, weight 1: x = y exactly before the norm
+
+
+def carry(orc, y):
+    """The oracle's hyper-connection pre + RMS norm of one layer output (unit weight)."""
+    return orc.hc_pre_norm(y.reshape(1, 1, DIM), MIX1, np.ones(DIM, np.float32))[0]
 
 
 @pytest.fixture(scope="module")
@@ -70,9 +80,10 @@ def run_pass(lane, ids, w, x0):
         hs = torch.zeros((L + 1, DIM), dtype=torch.float32, device="cuda")
         ys = torch.zeros((L, DIM), dtype=torch.float32, device="cuda")
         hs[0].copy_(dev(x0))
+        mix, ones = dev(MIX1), torch.ones(DIM, dtype=torch.float32, device="cuda")
         for l in range(L):
             lane.layer_forward_async(l, d_ids[l], d_w[l], hs[l], ys[l], stream=s.cuda_stream)
-            hs[l + 1].copy_(torch.nn.functional.rms_norm(ys[l], (DIM,), eps=1e-6))
+            lane.hc_pre_norm_async(ys[l].view(1, 1, DIM), mix, ones, hs[l + 1].view(1, DIM), stream=s.cuda_stream)
     lane.sync(s.cuda_stream)
     torch.cuda.synchronize()
     return hs.cpu().numpy(), ys.cpu().numpy()
@@ -102,9 +113,8 @@ def test_chain_40_layers(chain, orc):
         r = max_rel(ys[l], want)
         worst = max(worst, r)
         assert r < TOL, (l, r)
-        e2e = rms_norm_np(orc.combine(ids[l], w[l], np.stack(rows_e2e)))
-    # The oracle's own 40-layer chain from the same x0, the normalization restated
-    # in numpy: the device's final hidden within the same bar.
+        assert np.array_equal(hs[l + 1].view(np.uint32), carry(orc, ys[l]).view(np.uint32)), l
+        e2e = carry(orc, orc.combine(ids[l], w[l], np.stack(rows_e2e)))
+    # The oracle's own 40-layer chain from the same x0 (reported: see the module note)
     r_e2e = max_rel(hs[L], e2e)
     step(f"chain: worst per-layer max_rel {worst:.3e}; end-to-end final hidden max_rel {r_e2e:.3e}")
-    assert r_e2e < TOL, r_e2e

@@ -125,6 +125,32 @@ def test_hc_post_bit_exact(probe, orc, T, H, D):
     assert np.array_equal(dres.cpu().numpy().view(np.uint32), want.view(np.uint32))
 
 
+@pytest.mark.parametrize("T,H,D", [(1, 1, 4096), (2, 4, 5120), (3, 3, 1500), (1, 2, 7), (1, 4, 32768), (2, 2, 16384)])
+def test_hc_pre_norm_bit_exact(probe, orc, T, H, D):
+    step(f"hc_pre_norm T={T} H={H} D={D}")
+    rng = np.random.default_rng(T * 1000 + H * 10 + D)
+    h = (rng.standard_normal((T, H, D)) * rng.choice([1e-3, 1.0, 40.0])).astype(np.float32)
+    h[0, 0, : min(D, 3)] = -0.0
+    mix = rng.standard_normal((T, 8)).astype(np.float32)
+    w = rng.standard_normal(D).astype(np.float32)
+    for ww in (None, w):
+        want = orc.hc_pre_norm(h, mix, ww)
+        x = torch.full((T, D), 7.0, dtype=torch.float32, device="cuda")
+        probe.hc_pre_norm_async(dev(h), dev(mix), None if ww is None else dev(ww), x)
+        probe.sync()
+        assert np.array_equal(x.cpu().numpy().view(np.uint32), want.view(np.uint32)), ww is None
+
+
+def test_hc_pre_norm_rejects_bad_arguments(probe):
+    buf = torch.zeros(4 * 64 + 64, dtype=torch.float32, device="cuda")
+    h = buf[:4 * 64].view(1, 4, 64)
+    mix = torch.ones((1, 8), dtype=torch.float32, device="cuda")
+    with pytest.raises(xl.XLError, match="overlaps"):
+        probe.hc_pre_norm_async(h, mix, None, buf[192:256].view(1, 64))
+    with pytest.raises(xl.XLError, match="epsilon"):
+        probe.hc_pre_norm_async(h, mix, None, buf[256:].view(1, 64), eps=0.0)
+
+
 def test_hc_post_rejects_overlap(probe):
     buf = torch.zeros(4 * 4 * 64 + 64, dtype=torch.float32, device="cuda")
     res = buf[64:64 + 4 * 64].view(1, 4, 64)

@@ -421,6 +421,36 @@ def test_hc_post_reference_golden_and_closed_form(orc, ref, rng):
     assert not np.array_equal(got, orc.hc_post(y, res, post, _transpose_comb(comb, H), D, H, T))
 
 
+def test_hc_pre_norm_reference_golden_and_closed_form(orc, ref, rng):
+    # sycl/hc/core.hpp:74-80: against the reference build and its golden vectors
+    for D, H, T in ((4096, 1, 1), (5120, 4, 2), (1500, 3, 2), (7, 2, 1), (1024, 4, 1)):
+        h = (rng.standard_normal((T, H, D)) * rng.choice([1e-3, 1.0, 40.0])).astype(np.float32)
+        h[0, 0, : min(D, 3)] = -0.0   # 0 + (-0) = +0 in the reference's sum
+        mix = rng.standard_normal((T, 8)).astype(np.float32)
+        w = rng.standard_normal(D).astype(np.float32)
+        for ww in (None, w):
+            got = orc.hc_pre_norm(h, mix, ww)
+            assert np.array_equal(got.view(np.uint32), ref.hc_pre_norm(h, mix, ww).view(np.uint32)), (D, H, T)
+    g = {k: GOLD[f"hcpre_{k}"] for k in ("h", "mix", "w", "x")}
+    assert np.array_equal(orc.hc_pre_norm(g["h"], g["mix"], g["w"]).view(np.uint32), g["x"].view(np.uint32))
+    # one stream, mix 1, no weight: x = h exactly, with +0 for -0
+    h = rng.standard_normal((2, 1, 3000)).astype(np.float32)
+    h[0, 0, 5] = -0.0
+    one = np.ones((2, 8), np.float32)
+    x = orc.hc_pre_norm(h, one, None)
+    assert np.array_equal(x, h[:, 0, :]) and not np.signbit(x[0, 5])
+    # with a unit weight: x / sqrt(mean(x^2) + eps), to float rounding
+    xn = orc.hc_pre_norm(h, one, np.ones(3000, np.float32))
+    want = h[:, 0, :] / np.sqrt((h[:, 0, :].astype(np.float64) ** 2).mean(axis=1, keepdims=True) + 1e-6)
+    assert np.allclose(xn, want, rtol=1e-5, atol=0)
+    # all zeros: x = 0 (inv = 1 / sqrt(eps))
+    assert not orc.hc_pre_norm(np.zeros((1, 2, 64), np.float32), one[:1], np.ones(64, np.float32)).any()
+    # a dropped stream (mix of the last stream ignored) changes the answer
+    h4 = rng.standard_normal((1, 4, 256)).astype(np.float32)
+    m4 = rng.standard_normal((1, 8)).astype(np.float32)
+    assert not np.array_equal(orc.hc_pre_norm(h4, m4, None), orc.hc_pre_norm(h4[:, :3], m4, None))
+
+
 def _transpose_comb(comb, H):
     c = comb.copy()
     for j in range(H):

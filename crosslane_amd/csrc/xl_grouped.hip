@@ -609,24 +609,42 @@ __global__ __launch_bounds__(NW * 64, 1) void dn_kernel(GroupArgs a) {
 // ---------------------------------------------------------------------------
 // Fixed-order combine per token (runtime.cpp:183-188): ascending expert id,
 // out = fma(w, y, out) from +0, then + shared. A bad id contributes nothing.
+// Wave 0 ranks the token's picks once (ascending id, equal ids in pick order:
+// the stable order of an insertion sort) into LDS; every thread then issues
+// its column's loads of all the token's rows before the fma chain.
 // ---------------------------------------------------------------------------
 __global__ __launch_bounds__(256) void gcombine_kernel(GroupArgs a) {
-    const int tok = blockIdx.y, c = blockIdx.x * 256 + threadIdx.x;
-    if (c >= a.dim) return;
-    const int32_t* ids = a.ids + size_t(tok) * a.k;
-    int order[16];
-    int n = 0;
-    for (int i = 0; i < a.k; ++i)
-        if (ids[i] >= 0 && ids[i] < a.n_experts) order[n++] = i;
-    for (int i = 1; i < n; ++i)
-        for (int j = i; j > 0 && ids[order[j]] < ids[order[j - 1]]; --j) {
-            const int s = order[j]; order[j] = order[j - 1]; order[j - 1] = s;
+    __shared__ int s_row[16];     // pair row of rank r
+    __shared__ float s_w[16];
+    __shared__ int s_n;
+    const int tok = blockIdx.y, t = threadIdx.x, k = a.k;
+    if (t < 64) {
+        const int id = t < k ? a.ids[size_t(tok) * k + t] : -1;
+        const bool ok = t < k && id >= 0 && id < a.n_experts;
+        int rank = 0;
+        for (int j = 0; j < k; ++j) {
+            const int idj = __shfl(id, j);
+            const bool okj = idj >= 0 && idj < a.n_experts;
+            rank += int(okj && (idj < id || (idj == id && j < t)));
         }
-    float acc = 0.0f;
-    for (int i = 0; i < n; ++i) {
-        const int p = tok * a.k + order[i];
-        acc = fmaf(a.w[p], a.y[size_t(p) * a.dim + c], acc);
+        if (ok) {
+            s_row[rank] = tok * k + t;
+            s_w[rank] = a.w[size_t(tok) * k + t];
+        }
+        const int n = __popcll(__ballot(ok));
+        if (t == 0) s_n = n;
     }
+    __syncthreads();
+    const int c = blockIdx.x * 256 + t;
+    if (c >= a.dim) return;
+    const int n = s_n;
+    float v[16];
+#pragma unroll
+    for (int r = 0; r < 16; ++r) v[r] = r < n ? a.y[size_t(s_row[r]) * a.dim + c] : 0.0f;
+    float acc = 0.0f;
+#pragma unroll
+    for (int r = 0; r < 16; ++r)
+        if (r < n) acc = fmaf(s_w[r], v[r], acc);
     if (a.shared) acc = __fadd_rn(acc, a.shared[size_t(tok) * a.dim + c]);
     a.out[size_t(tok) * a.dim + c] = acc;
 }

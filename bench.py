@@ -1,7 +1,7 @@
 #!/usr/bin/env python3
 """Routed-expert benchmark on one MI355X.
 
-Default workload: one MoE layer at decode batch 1, d_model
+Default workload (benchmark config 1): one MoE layer at decode batch 1, d_model
 4096, d_ff 3072, 384 resident experts (gate/up IQ2_XXS, down IQ2_XS), top-6 of
 a softmax over seeded N(0,1) router logits with renormalized weights,
 fixed-order combine into a 4096-wide f32 output. A step is one layer call

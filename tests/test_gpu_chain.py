@@ -1,4 +1,4 @@
-"""GPU parity of the full 40-layer expert pass: 40 layers
+"""GPU parity of the full 40-layer expert pass (benchmark config 3): 40 layers
 at d_model 4096, d_ff 3072, each expert's three matrices of one type drawn 17 %
 IQ2_XS / 19 % IQ2_XXS / 64 % IQ1_M, top-6 per layer, the hidden carried layer to
 layer on the device by the library's hyper-connection pre + RMS norm with one

@@ -1,4 +1,4 @@
-"""The grouped path at BASELINE config 4's full size: 512 tokens, each routed
+"""The grouped path at benchmark config 4's full size: 512 tokens, each routed
 top-6 over 384 experts (d_model 4096, d_ff 3072, IQ2_XXS gate/up + IQ2_XS
 down), a max_tokens = 512 workspace, thousands of (token, pick) pairs bucketed
 into hundreds of 16-pair tasks. The MFMA kernels are forced

@@ -1,6 +1,6 @@
 """GPU parity of the HIP path against the CPU oracle, through the C ABI.
 
-Bars: Q8_K bytes and per-block int32 partials bit-exact;
+Bars (the north star): Q8_K bytes and per-block int32 partials bit-exact;
 f32 outputs within max relative error 1e-3 (max-norm, tests.conftest.max_rel);
 runs bit-identical run to run. The hidden-state quantization is compared by
 feeding the device's own SwiGLU output to the oracle quantizer (host and device

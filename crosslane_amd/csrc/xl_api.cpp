@@ -348,6 +348,56 @@ struct LayerTrace {
 // Returns true when the layer ran as one launch carrying `stop` (recorded as it
 // completes); false when it took separate launches, which leave `stop` alone.
 // With `tr`, the layer must run as one launch (XL_E_ARG otherwise).
+// Arguments of the single-launch layer kernels for one layer call.
+xl::Layer3Args layer3_args(xl_context* ctx, int32_t layer, const int32_t* d_ids, const float* d_w, int32_t k,
+                           const float* d_x, const float* d_shared, float* d_out, hipStream_t s, LayerTrace* tr) {
+    const int E = ctx->cfg.n_experts;
+    xl::Layer3Args a{};
+    a.descs = ctx->d_descs + size_t(layer) * E; a.ids = d_ids; a.w = d_w; a.x = d_x; a.shared = d_shared; a.out = d_out;
+    a.k = k; a.n_experts = E; a.dim = ctx->cfg.dim; a.ff = ctx->cfg.ff;
+    a.htag = ctx->htag; a.hqtag = ctx->hqtag; a.hdtag = ctx->hdtag; a.ctl = ctx->ctl; a.err = ctx->err_flag;
+    a.lim = ctx->cfg.swiglu_limit;
+    a.tables = ctx->tables;
+    a.hbuf = ctx->hbuf;
+    a.part = ctx->part;
+    a.ucnt = ctx->ucnt;
+    if (ctx->prof.on && ctx->prof.calls <= ctx->prof.max_calls) {
+        a.trace = ctx->timeline;
+        hip_check(hipMemsetAsync(ctx->timeline, 0, size_t(ctx->cus) * 16 * 32 * 8, s), "timeline clear");
+    }
+    if (tr) { a.tq8x = tr->q8x; a.tq8h = tr->q8h; a.th = tr->h; a.tint = tr->ints; a.ty = tr->y; }
+    const LayerShape& ls = ctx->layer_shape[size_t(layer)];
+    if (ls.regular) {
+        a.slab = ctx->slabs[size_t(layer)];
+        a.estride = ls.estride;
+        for (int r = 0; r < 3; ++r) { a.roff[r] = ls.roff[r]; a.rtype[r] = ls.rtype[r]; }
+    }
+    return a;
+}
+
+// A routed layer call as one streaming launch that routes in its prologue
+// (every wave from the logits): true if launched (it records `stop`), false
+// if this layer or expert count has no such launch, or while stages are
+// profiled (the router then runs as its own stage).
+bool enqueue_layer_routed(xl_context* ctx, int32_t layer, const float* d_logits, const float* d_bias, int32_t k,
+                          float scale, const float* d_x, const float* d_shared, float* d_out, hipStream_t s,
+                          hipEvent_t stop) {
+    if (ctx->cfg.n_experts > xl::kStreamRouteMax || (ctx->path != 1 && ctx->path != 4) || ctx->prof.on) return false;
+    // ids and w are not read when routed; valid buffers all the same
+    xl::Layer3Args a = layer3_args(ctx, layer, ctx->ids, ctx->w, k, d_x, d_shared, d_out, s, nullptr);
+    a.rlogits = d_logits;
+    a.rbias = d_bias;
+    a.rscale = scale;
+    const hipError_t e = xl::dev::launch_stream(a, ctx->gu_mask[size_t(layer)], ctx->dn_mask[size_t(layer)], ctx->cus, s,
+                                                stop);
+    if (e == hipErrorNotSupported) {
+        (void)hipGetLastError();
+        return false;
+    }
+    hip_check(e, "routed streaming layer");
+    return true;
+}
+
 bool enqueue_layer(xl_context* ctx, int32_t layer, const int32_t* d_ids, const float* d_w, int32_t k, const float* d_x,
                    const float* d_shared, float* d_out, hipStream_t s, float* g_dbg = nullptr,
                    float* u_dbg = nullptr, hipEvent_t stop = nullptr, LayerTrace* tr = nullptr) {
@@ -357,26 +407,7 @@ bool enqueue_layer(xl_context* ctx, int32_t layer, const int32_t* d_ids, const f
     Marks mark(ctx, s);
     mark("");
     if ((ctx->path == 1 || ctx->path == 3 || ctx->path == 4 || ctx->path == 5) && !g_dbg && !u_dbg) {
-        xl::Layer3Args a{};
-        a.descs = descs; a.ids = d_ids; a.w = d_w; a.x = d_x; a.shared = d_shared; a.out = d_out;
-        a.k = k; a.n_experts = E; a.dim = dim; a.ff = ff;
-        a.htag = ctx->htag; a.hqtag = ctx->hqtag; a.hdtag = ctx->hdtag; a.ctl = ctx->ctl; a.err = ctx->err_flag;
-        a.lim = ctx->cfg.swiglu_limit;
-        a.tables = ctx->tables;
-        a.hbuf = ctx->hbuf;
-        a.part = ctx->part;
-        a.ucnt = ctx->ucnt;
-        if (ctx->prof.on && ctx->prof.calls <= ctx->prof.max_calls) {
-            a.trace = ctx->timeline;
-            hip_check(hipMemsetAsync(ctx->timeline, 0, size_t(ctx->cus) * 16 * 32 * 8, s), "timeline clear");
-        }
-        if (tr) { a.tq8x = tr->q8x; a.tq8h = tr->q8h; a.th = tr->h; a.tint = tr->ints; a.ty = tr->y; }
-        const LayerShape& ls = ctx->layer_shape[size_t(layer)];
-        if (ls.regular) {
-            a.slab = ctx->slabs[size_t(layer)];
-            a.estride = ls.estride;
-            for (int r = 0; r < 3; ++r) { a.roff[r] = ls.roff[r]; a.rtype[r] = ls.rtype[r]; }
-        }
+        xl::Layer3Args a = layer3_args(ctx, layer, d_ids, d_w, k, d_x, d_shared, d_out, s, tr);
         if (d_out) {
             hipError_t e = hipErrorNotSupported;
             if (ctx->path == 5 && gu_mask == 1 && dn_mask == 2) {
@@ -1145,6 +1176,13 @@ int32_t xl_layer_forward_routed_async(xl_context* ctx, int32_t layer, const floa
         hipStream_t s = pick_stream(ctx, stream);
         Ordered ord(ctx, s);
         const int n = ctx->cfg.n_experts;
+        // one launch that routes in its prologue where the streaming kernel has the
+        // layer, else the router kernel and then the layer
+        if (enqueue_layer_routed(ctx, layer, d_logits, d_bias_or_null, k, scale, d_x, d_shared_or_null, d_out, s,
+                                 ord.stop())) {
+            ord.carried_by_launch(true);
+            return;
+        }
         hip_check(xl::dev::launch_route(d_logits, 1, n, d_bias_or_null, n, k, scale, ctx->ids, ctx->w, ctx->err_flag, s),
                   "route launch");
         ord.carried_by_launch(enqueue_layer(ctx, layer, ctx->ids, ctx->w, k, d_x, d_shared_or_null, d_out, s, nullptr,

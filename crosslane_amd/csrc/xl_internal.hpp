@@ -105,8 +105,15 @@ struct Layer3Args {
     float* ty;                  // trace: every pick's row before the combine (k x dim, ids order)
     float* part;                // unit kernel: per (pick, h block) unit, dim float partials of the down rows
     uint32_t* ucnt;             // unit kernel: 2 sets (launch parity) of 8 partial counters, 32 words apart (2 x 256 words)
+    // Routed in the kernel (streaming kernel; null: ids and w are read): every
+    // wave routes the token from its n_experts <= kStreamRouteMax logits (bias
+    // may be null) as the router kernel does; ids and w are then not read.
+    const float* rlogits;
+    const float* rbias;
+    float rscale;
 };
 constexpr int kHBufWords = 16 * 4096;      // k_max * ff_max
+constexpr int kStreamRouteMax = 512;       // experts a streaming kernel routes itself (8 per lane)
 
 // Arguments of the grouped path (xl_grouped.hip): T tokens with k picks each,
 // P = T * k (token, pick) pairs, pair p = token p / k. Device pointers.

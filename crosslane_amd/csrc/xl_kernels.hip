@@ -17,6 +17,7 @@
 
 #include "xl_format.hpp"
 #include "xl_internal.hpp"
+#include "xl_route.hpp"
 #include "xl_rows.hpp"
 
 namespace xl::dev {
@@ -279,33 +280,11 @@ __global__ __launch_bounds__(256) void combine_kernel(const int32_t* __restrict_
 }
 
 // ---------------------------------------------------------------------------
-// Router (route.cpp:15-37, route_cpu), one workgroup per token: score =
-// sqrt(softplus(l)) (l itself above 20), key = score + bias; k rounds of the
-// first largest key (strict '>' in index order: ties go to the lower index),
-// each round taking the expert out (key -FLT_MAX); the picked scores summed in
-// pick order; weight = score / (sum + 1e-20) * scale. Separate IEEE roundings
-// throughout (no contraction); expf / log1pf are the device library's.
+// Router (route.cpp:15-37, route_cpu), one workgroup per token; its arithmetic
+// is xl_route.hpp's. Scores and keys by all 512 threads (PT experts each,
+// loads first), through LDS to wave 0, which selects: expert e in lane e % 64,
+// slot e / 64.
 // ---------------------------------------------------------------------------
-// Keys as unsigned integers that order as the floats do (-FLT_MAX, the taken
-// mark, above 0, which pads lanes past n).
-__device__ __forceinline__ uint32_t ordered(float f) {
-    const uint32_t u = __float_as_uint(f);
-    return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
-}
-template <bool MAX>
-__device__ __forceinline__ uint32_t wave_ext(uint32_t a) {   // wave max / min by DPP, result in every lane
-    auto f = [](uint32_t x, uint32_t y) { return MAX ? max(x, y) : min(x, y); };
-    const int id = MAX ? 0 : -1;
-    a = f(a, uint32_t(__builtin_amdgcn_update_dpp(int(a), int(a), 0xB1, 0xF, 0xF, false)));   // quad_perm 1,0,3,2
-    a = f(a, uint32_t(__builtin_amdgcn_update_dpp(int(a), int(a), 0x4E, 0xF, 0xF, false)));   // quad_perm 2,3,0,1
-    a = f(a, uint32_t(__builtin_amdgcn_update_dpp(int(a), int(a), 0x141, 0xF, 0xF, false)));  // row_half_mirror
-    a = f(a, uint32_t(__builtin_amdgcn_update_dpp(int(a), int(a), 0x140, 0xF, 0xF, false)));  // row_mirror
-    a = f(a, uint32_t(__builtin_amdgcn_update_dpp(id, int(a), 0x142, 0xA, 0xF, false)));       // row_bcast:15
-    a = f(a, uint32_t(__builtin_amdgcn_update_dpp(id, int(a), 0x143, 0xC, 0xF, false)));       // row_bcast:31
-    return uint32_t(__builtin_amdgcn_readlane(int(a), 63));
-}
-// Scores and keys by all 512 threads (PT experts each, loads first), through
-// LDS to wave 0, which selects: expert e in lane e % 64, slot e / 64.
 template <int NPL>   // n <= 64 * NPL
 __global__ __launch_bounds__(512) void route_kernel(const float* __restrict__ logits, int stride,
                                                     const float* __restrict__ bias, int n, int k, float scale,
@@ -327,15 +306,12 @@ __global__ __launch_bounds__(512) void route_kernel(const float* __restrict__ lo
 #pragma unroll
     for (int j = 0; j < PT; ++j) {
         const int e = tid + 512 * j;
-        const float l = lv[j];
-        const float sp = l > 20.0f ? l : log1pf(expf(l));
-        const float s = sqrtf(sp);
-        const float kk = __fadd_rn(s, bv[j]);
-        const bool in = e < n;
-        fin = fin && (!in || ((fabsf(l) <= 3.402823466e38f) && (fabsf(kk) <= 3.402823466e38f)));
+        float s;
+        uint32_t key;
+        route_score(lv[j], bv[j], e < n, s, key, fin);
         if (e < 64 * NPL) {
-            s_sc[e] = in ? s : 0.0f;
-            s_key[e] = in ? ordered(kk) : 0u;
+            s_sc[e] = s;
+            s_key[e] = key;
         }
     }
     if (__any(!fin) && (tid & 63) == 0) atomicOr(err, kDevErrNonFinite);
@@ -349,26 +325,13 @@ __global__ __launch_bounds__(512) void route_kernel(const float* __restrict__ lo
         sc[j] = s_sc[lane + 64 * j];
         key[j] = s_key[lane + 64 * j];
     }
-    const uint32_t taken = ordered(-3.402823466e38f);
-    float sum = 0.0f, mine = 0.0f;   // lane i < k keeps pick i's score
-    for (int i = 0; i < k; ++i) {
-        uint32_t bk = 0u;
-        int bj = 0;
-#pragma unroll
-        for (int j = 0; j < NPL; ++j)   // this lane's first largest key (strict '>')
-            if (key[j] > bk) { bk = key[j]; bj = j; }
-        const uint32_t top = wave_ext<true>(bk);
-        const int e = int(wave_ext<false>(bk == top ? uint32_t(lane + 64 * bj) : 0xffffffffu));   // lowest index
-        float se = 0.0f;
-#pragma unroll
-        for (int j = 0; j < NPL; ++j)
-            if (lane + 64 * j == e) { se = sc[j]; key[j] = taken; }
-        se = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(se), e & 63));
-        sum = __fadd_rn(sum, se);
-        mine = lane == i ? se : mine;
-        if (lane == 0) ids[size_t(t) * k + i] = e;
+    int id;
+    float wt;
+    route_select<NPL>(sc, key, k, lane, scale, id, wt);
+    if (lane < k) {
+        ids[size_t(t) * k + lane] = id;
+        w[size_t(t) * k + lane] = wt;
     }
-    if (lane < k) w[size_t(t) * k + lane] = __fmul_rn(__fdiv_rn(mine, __fadd_rn(sum, 1e-20f)), scale);
 }
 
 // ---------------------------------------------------------------------------

@@ -53,6 +53,7 @@
 #include "xl_dev.hpp"
 #include "xl_internal.hpp"
 #include "xl_iq2.hpp"
+#include "xl_route.hpp"
 
 namespace xl::dev {
 namespace {
@@ -277,7 +278,19 @@ __global__ __launch_bounds__(NW * 64, 1) void stream_kernel(Layer3Args a) {
     const int nq_wg = quads > int(blockIdx.x) ? (quads - int(blockIdx.x) + G - 1) / G : 0;
     const int P = k * nq_wg;
     const int nd = P > wv ? min(MD, (P - wv + NW - 1) / NW) : 0;
-    const int idl = a.ids[lane < k ? lane : k - 1];   // unconditional loads keep the wait counts exact
+    // Routed in the kernel (a.rlogits): thread t loads expert t's logit and bias
+    // here; the routing runs after the x and codebook loads are out. Else the ids.
+    const bool routed = a.rlogits != nullptr;   // uniform
+    static_assert(NW * 64 >= kStreamRouteMax, "one expert per thread");
+    float rl = 0.0f, rb = 0.0f;
+    int idl = 0;
+    if (routed) {
+        const int e = min(t, a.n_experts - 1);   // clamped, unconditional
+        rl = a.rlogits[e];
+        rb = a.rbias ? a.rbias[e] : 0.0f;
+    } else {
+        idl = a.ids[lane < k ? lane : k - 1];   // unconditional loads keep the wait counts exact
+    }
     // ---- x and the codebook rows: they need no ids, so they go out right after
     // the ids load (the wait for the ids then leaves them in flight) and before the
     // slot loads. The rows come into registers (plain loads: waiting for them does
@@ -316,6 +329,45 @@ __global__ __launch_bounds__(NW * 64, 1) void stream_kernel(Layer3Args a) {
     // expert << 16 | pick << 12 | first row (bad ids read expert 0 and are
     // masked out). A use reads its lane back (v_readlane), so the scalar
     // registers stay free for the loads' addresses.
+    float rw = 0.0f;   // routed: lane i < k's pick weight
+    if (routed) {
+        // Scores and keys by every thread into LDS (the sign-table region, written
+        // only after the second barrier), wave 0 selects (the router kernel's
+        // order: expert e in lane e % 64, slot e / 64) into sm.ids / sm.w, which
+        // every wave then reads (wave 0 later stores the same values there).
+        constexpr int RNPL = kStreamRouteMax / 64;
+        float* const rsc = reinterpret_cast<float*>(lds);
+        uint32_t* const rkey = reinterpret_cast<uint32_t*>(lds + 4 * kStreamRouteMax);
+        bool fin = true;
+        float sc;
+        uint32_t key;
+        route_score(rl, rb, t < a.n_experts, sc, key, fin);
+        if (__any(!fin) && lane == 0) set_err(a.err, kDevErrNonFinite);
+        if (t < kStreamRouteMax) {
+            rsc[t] = sc;
+            rkey[t] = key;
+        }
+        lds_barrier();
+        if (wv == 0) {
+            float scs[RNPL];
+            uint32_t keys[RNPL];
+#pragma unroll
+            for (int j = 0; j < RNPL; ++j) {
+                scs[j] = rsc[lane + 64 * j];
+                keys[j] = rkey[lane + 64 * j];
+            }
+            int id;
+            float wt;
+            route_select<RNPL>(scs, keys, k, lane, a.rscale, id, wt);
+            if (lane < k) {
+                sm.ids[lane] = id;
+                sm.w[lane] = wt;
+            }
+        }
+        lds_barrier();
+        idl = sm.ids[lane < k ? lane : k - 1];
+        rw = sm.w[lane < k ? lane : k - 1];
+    }
     const int idv = lane < k ? idl : -1;
     uint32_t meta;
     uint64_t okmask;   // bit j: slot j is this wave's with a valid id; bit 32 + j: pass j likewise
@@ -402,7 +454,7 @@ __global__ __launch_bounds__(NW * 64, 1) void stream_kernel(Layer3Args a) {
     auto mtype = [&](int pick, int role) { return __builtin_amdgcn_readlane(tb_ty, 16 * role + pick); };
 
     // ---- the first slots (the codebook rows and x are in flight since the start)
-    const float cw = a.w[lane < k ? lane : k - 1];
+    const float cw = routed ? rw : a.w[lane < k ? lane : k - 1];
     uint32_t* ctl = a.ctl + 2;   // [0] parity source: launches of this kernel so far, [1] arrivals
     const uint32_t e_prev = coh_ld32(ctl);
 

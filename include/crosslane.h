@@ -226,8 +226,11 @@ int32_t xl_combine_async(xl_context* ctx, const int32_t* d_ids, const float* d_w
 int32_t xl_route_async(xl_context* ctx, const float* d_logits, int32_t T, int32_t stride, const float* d_bias_or_null,
                        int32_t n, int32_t k, float scale, int32_t* d_ids, float* d_w, void* stream, xl_error* err);
 /* The router over the layer's n_experts logits, then the layer call on its ids
- * and weights, both on `stream` (no host round trip; the route result lives in
- * the context's workspace, so routed calls on one context are stream-ordered). */
+ * and weights, both on `stream` (no host round trip). Where the streaming
+ * kernel has the layer and n_experts <= 512 this is one launch that routes in
+ * its prologue, bit-identical to the router followed by the layer call;
+ * otherwise the route result lives in the context's workspace (routed calls on
+ * one context are stream-ordered). */
 int32_t xl_layer_forward_routed_async(xl_context* ctx, int32_t layer, const float* d_logits, const float* d_bias_or_null,
                                       int32_t k, float scale, const float* d_x, const float* d_shared_or_null,
                                       float* d_out, void* stream, xl_error* err);

@@ -114,3 +114,42 @@ def test_routed_layer_and_grouped(orc):
             assert max_rel(ggot[t], want) < TOL, (t, max_rel(ggot[t], want))
     finally:
         lane.close()
+
+
+@pytest.mark.parametrize("dim,ff,E,k,kind", [(4096, 3072, 384, 6, "iq2"), (4096, 3072, 384, 1, "iq2"),
+                                             (4096, 3072, 64, 6, "iq1"), (1024, 512, 600, 4, "iq2"),
+                                             (1024, 512, 40, 3, "mixed")])
+def test_routed_one_launch_matches_router_then_layer(dim, ff, E, k, kind):
+    # Where the streaming kernel has the layer and E <= 512, the routed call is
+    # one launch that routes in its prologue (every wave from the logits); it
+    # must give the bits of the router kernel followed by the layer call on its
+    # ids and weights (E = 600: the two-launch path itself). Ties included: a
+    # few logits repeat exactly.
+    step(f"routed one launch dim={dim} ff={ff} E={E} k={k} {kind}")
+    rng = np.random.default_rng(E + k)
+    if kind == "mixed":
+        types = np.repeat(rng.choice([16, 17, 29], size=(1, E)).astype(np.int32)[..., None], 3, axis=-1)
+    else:
+        t = (16, 17) if kind == "iq2" else (29, 29)
+        types = types_map(1, E, t[0], t[1])
+    lane = xl.Lane(dim, ff, 1, E, types, max_picks=8)
+    try:
+        lane.generate(seed=33)
+        T = 6
+        lg = (rng.standard_normal((T, E)) * 2).astype(np.float32)
+        lg[:, 5] = lg[:, 3]   # an exact tie of keys (the lower index wins)
+        b = (rng.standard_normal(E) * 0.1).astype(np.float32)
+        x = rng.standard_normal((T, dim)).astype(np.float32)
+        d_lg, d_b, d_x = dev(lg), dev(b), dev(x)
+        one = torch.zeros((T, dim), dtype=torch.float32, device="cuda")
+        two = torch.zeros((T, dim), dtype=torch.float32, device="cuda")
+        ids = torch.zeros((T, k), dtype=torch.int32, device="cuda")
+        w = torch.zeros((T, k), dtype=torch.float32, device="cuda")
+        lane.route_async(d_lg, k, ids, w, scale=1.5, bias=d_b)
+        for t in range(T):
+            lane.layer_forward_routed_async(0, d_lg[t], k, d_x[t], one[t], scale=1.5, bias=d_b)
+            lane.layer_forward_async(0, ids[t], w[t], d_x[t], two[t])
+        lane.sync()
+        assert np.array_equal(one.cpu().numpy().view(np.uint32), two.cpu().numpy().view(np.uint32))
+    finally:
+        lane.close()

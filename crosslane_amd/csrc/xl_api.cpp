@@ -1170,6 +1170,7 @@ int32_t xl_layer_forward_routed_async(xl_context* ctx, int32_t layer, const floa
         ready(ctx, true);
         check_layer(ctx, layer);
         need(k >= 1 && k <= ctx->cfg.max_picks, XL_E_ARG, "pick count outside 1..max_picks");
+        need(k <= ctx->cfg.n_experts, XL_E_ARG, "router: more picks than experts");
         need(ctx->cfg.n_experts <= xl::kRouteMaxExperts, XL_E_ARG, "router: more than 4096 experts");
         need(std::isfinite(scale) && scale >= 0.0f, XL_E_ARG, "route scale must be finite and >= 0");
         need(d_logits && d_x && d_out, XL_E_ARG, "null device pointer");

@@ -19,10 +19,11 @@ steps touch different experts (the bank is ~3.9 GB, far beyond the 256 MB MALL).
   3  a 40-layer pass per step: 40 x 384 experts whose whole-expert type is
      drawn 17 % IQ2_XS / 19 % IQ2_XXS / 64 % IQ1_M, top-6 per layer, the
      hidden carried layer to layer through an RMS normalization (the library's
-     hyper-connection pre + RMS norm, xl_hc_pre_norm_async, with one stream and
-     a unit weight, on the same stream inside the timed region: the model's
-     ffn_norm step, without which the quadratic SwiGLU overflows f32 within a
-     few layers).
+     hyper-connection pre + RMS norm with one stream and a unit weight, inside
+     each next layer's launch, xl_layer_forward_prenorm_async, and after the
+     last layer by xl_hc_pre_norm_async, all inside the timed region: the
+     model's ffn_norm step, without which the quadratic SwiGLU overflows f32
+     within a few layers).
 
 Prints one JSON line: value = achieved algorithmic HBM GB/s (selected experts'
 weight bytes + x in + out per layer), plus us_per_layer; the roofline of the
@@ -368,7 +369,8 @@ def main():
         d_mix1 = torch.zeros(8, dtype=torch.float32, device="cuda")
         d_mix1[0] = 1.0
         d_ones = torch.ones(DIM, dtype=torch.float32, device="cuda")
-        d_y = torch.zeros(DIM, dtype=torch.float32, device="cuda")             # config 3: a layer's raw output
+        d_y = torch.zeros(DIM, dtype=torch.float32, device="cuda")             # config 3: layer outputs, alternating
+        d_y2 = torch.zeros(DIM, dtype=torch.float32, device="cuda")
         d_out = torch.zeros((n_r, TOK, DIM) if cfg == 4 else (n_r, DIM), dtype=torch.float32, device="cuda")
         d_logits = torch.from_numpy(logits).cuda() if droute else None
         d_y32 = torch.zeros((K, DIM), dtype=torch.float32, device="cuda") if args.per32 else None
@@ -404,13 +406,16 @@ def main():
             lane.layer_forward_async(0, d_ids[r, 0], d_w[r, 0], d_x[r], d_out[r], stream=sp)
             return
         with torch.cuda.stream(stream):
-            h = d_x[r]
-            for l in range(L):
-                lane.layer_forward_async(l, d_ids[r, l], d_w[r, l], h, d_y, stream=sp)
-                # RMS-normalized hidden for the next layer (one stream, mix 1, unit weight)
-                lane.hc_pre_norm_async(d_y.view(1, 1, DIM), d_mix1, d_ones, d_hn.view(1, DIM), eps=1e-6, stream=sp)
-                h = d_hn
-            d_h[r % (L + 1)].copy_(h)   # the pass's final hidden (checked for finiteness after timing)
+            # layer l > 0 takes the RMS-normalized output of layer l - 1 (one stream,
+            # mix 1, unit weight) inside its own launch; outputs alternate buffers
+            ys = (d_y, d_y2)
+            lane.layer_forward_async(0, d_ids[r, 0], d_w[r, 0], d_x[r], ys[0], stream=sp)
+            for l in range(1, L):
+                lane.layer_forward_prenorm_async(l, d_ids[r, l], d_w[r, l], ys[(l - 1) & 1].view(1, DIM), d_mix1,
+                                                 d_ones, d_hn, ys[l & 1], eps=1e-6, stream=sp)
+            lane.hc_pre_norm_async(ys[(L - 1) & 1].view(1, 1, DIM), d_mix1, d_ones, d_hn.view(1, DIM), eps=1e-6,
+                                   stream=sp)
+            d_h[r % (L + 1)].copy_(d_hn)   # the pass's final hidden (checked for finiteness after timing)
 
     for i in range(warmup):
         step(i)
@@ -435,7 +440,8 @@ def main():
     # One kernel launch per layer: the layer kernel's average duration is the
     # timed region's event time over the launches (rocprofv3 --kernel-trace of
     # the same command agrees; see profiles/). Config 3's figure also holds the
-    # normalization between layers, so it bounds the kernel from below.
+    # normalization inside the layer launches and the one after the last layer,
+    # so it bounds the kernel from below.
     kernel = {0: "xl::dev::stream_kernel (single-launch layer, IQ2 instance)",
               1: "xl::dev::stream_kernel (single-launch layer, IQ2 instance)",
               2: "xl::dev::stream_kernel (single-launch layer, IQ1_M instance)",

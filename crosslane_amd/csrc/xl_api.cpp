@@ -398,6 +398,30 @@ bool enqueue_layer_routed(xl_context* ctx, int32_t layer, const float* d_logits,
     return true;
 }
 
+// A layer call whose x is the pre-norm of one stream, as one streaming launch
+// that normalizes in its prologue (workgroup 0 writes x to d_x): true if
+// launched (it records `stop`), false if this layer has no such launch, or
+// while stages are profiled.
+bool enqueue_layer_prenorm(xl_context* ctx, int32_t layer, const int32_t* d_ids, const float* d_w, int32_t k,
+                           const float* d_h, const float* d_mix, const float* d_norm_w, float eps, float* d_x,
+                           const float* d_shared, float* d_out, hipStream_t s, hipEvent_t stop) {
+    if ((ctx->path != 1 && ctx->path != 4) || ctx->prof.on) return false;
+    xl::Layer3Args a = layer3_args(ctx, layer, d_ids, d_w, k, d_x, d_shared, d_out, s, nullptr);
+    a.pn_h = d_h;
+    a.pn_mix = d_mix;
+    a.pn_w = d_norm_w;
+    a.pn_x = d_x;
+    a.pn_eps = eps;
+    const hipError_t e = xl::dev::launch_stream(a, ctx->gu_mask[size_t(layer)], ctx->dn_mask[size_t(layer)], ctx->cus, s,
+                                                stop);
+    if (e == hipErrorNotSupported) {
+        (void)hipGetLastError();
+        return false;
+    }
+    hip_check(e, "pre-normed streaming layer");
+    return true;
+}
+
 bool enqueue_layer(xl_context* ctx, int32_t layer, const int32_t* d_ids, const float* d_w, int32_t k, const float* d_x,
                    const float* d_shared, float* d_out, hipStream_t s, float* g_dbg = nullptr,
                    float* u_dbg = nullptr, hipEvent_t stop = nullptr, LayerTrace* tr = nullptr) {
@@ -1273,6 +1297,42 @@ int32_t xl_layer_forward_async(xl_context* ctx, int32_t layer, const int32_t* d_
         Ordered ord(ctx, s);
         ord.carried_by_launch(enqueue_layer(ctx, layer, d_ids, d_w, k, d_x, d_shared_or_null, d_out, s, nullptr, nullptr,
                                             ord.stop()));
+    });
+}
+
+int32_t xl_layer_forward_prenorm_async(xl_context* ctx, int32_t layer, const int32_t* d_ids, const float* d_w,
+                                       int32_t k, const float* d_h, int32_t H, const float* d_mix,
+                                       const float* d_norm_w_or_null, float eps, float* d_x,
+                                       const float* d_shared_or_null, float* d_out, void* stream, xl_error* err) {
+    return guarded(ctx, err, [&] {
+        ready(ctx, true);
+        check_layer(ctx, layer);
+        need(k >= 1 && k <= ctx->cfg.max_picks, XL_E_ARG, "pick count outside 1..max_picks");
+        need(d_ids && d_w && d_h && d_mix && d_x && d_out, XL_E_ARG, "null device pointer");
+        need(H >= 1 && H <= 4, XL_E_ARG, "hc geometry: H in 1..4");
+        need(std::isfinite(eps) && eps > 0.0f, XL_E_ARG, "hc epsilon must be finite and positive");
+        const uint64_t D = uint64_t(ctx->cfg.dim);
+        const auto apart = [](const void* p, uint64_t pb, const void* q, uint64_t qb) {
+            const uintptr_t a = reinterpret_cast<uintptr_t>(p), b = reinterpret_cast<uintptr_t>(q);
+            return a <= b ? b - a >= pb : a - b >= qb;
+        };
+        // x is written while h, mix and the norm weights are read; out is written
+        // while h is read by workgroups that start later
+        need(apart(d_x, D * 4, d_h, uint64_t(H) * D * 4) && apart(d_x, D * 4, d_mix, 32) &&
+                 (!d_norm_w_or_null || apart(d_x, D * 4, d_norm_w_or_null, D * 4)) &&
+                 apart(d_out, D * 4, d_h, uint64_t(H) * D * 4) && apart(d_out, D * 4, d_x, D * 4),
+             XL_E_ARG, "pre-norm layer: x or out overlaps an input");
+        hipStream_t s = pick_stream(ctx, stream);
+        Ordered ord(ctx, s);
+        if (H == 1 && enqueue_layer_prenorm(ctx, layer, d_ids, d_w, k, d_h, d_mix, d_norm_w_or_null, eps, d_x,
+                                            d_shared_or_null, d_out, s, ord.stop())) {
+            ord.carried_by_launch(true);
+            return;
+        }
+        hip_check(xl::dev::launch_hc_pre_norm(d_h, d_mix, d_norm_w_or_null, int(D), H, 1, eps, d_x, s, nullptr),
+                  "hc_pre_norm launch");
+        ord.carried_by_launch(enqueue_layer(ctx, layer, d_ids, d_w, k, d_x, d_shared_or_null, d_out, s, nullptr,
+                                            nullptr, ord.stop()));
     });
 }
 

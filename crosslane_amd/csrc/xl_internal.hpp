@@ -111,6 +111,15 @@ struct Layer3Args {
     const float* rlogits;
     const float* rbias;
     float rscale;
+    // Pre-norm in the kernel (streaming kernel; null: x is read as is): x is the
+    // hyper-connection pre + RMS norm of one token's single stream pn_h (dim
+    // floats), mix weight pn_mix[0], norm weights pn_w (null: the pre values
+    // only), as hc_pre_norm_kernel computes it; workgroup 0 writes it to pn_x.
+    const float* pn_h;
+    const float* pn_mix;
+    const float* pn_w;
+    float* pn_x;
+    float pn_eps;
 };
 constexpr int kHBufWords = 16 * 4096;      // k_max * ff_max
 constexpr int kStreamRouteMax = 512;       // experts a streaming kernel routes itself (8 per lane)

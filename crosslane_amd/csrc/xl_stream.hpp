@@ -63,7 +63,9 @@ namespace {
 // address = index << 8 | the lane's copy offset | table base); XS: IQ2_XS grid
 // (512 rows x 4 copies x 8 B); IQ1: IQ1_M value rows; XQ: Q8_K(x) (dim quants,
 // swizzled, then 16 block scales; gate/up phase); HQ: Q8_K(h) of the picks
-// (down phase, over a region gate/up no longer reads); Y: y staging.
+// (down phase, over a region gate/up no longer reads); Y: y staging; NRM: the
+// in-kernel pre-norm's 32 group sums (prologue only, a region nothing writes
+// before the prologue's last barrier).
 template <int M>
 struct SLay;
 template <>
@@ -73,7 +75,8 @@ struct SLay<3> {   // IQ2_XXS gate/up, IQ2_XS down
     static constexpr int SGN_IN_ROW = 0;                  // byte of the sign copies in a row
     static constexpr int XS = 131072, IQ1 = -1;
     static constexpr int XQ = 147456, HQ = 65536, Y = 147456;   // HQ over the XXS grid, Y over XQ
-    static constexpr int Bytes = 151616;
+    static constexpr int NRM = 151616;                    // pre-norm group sums (32 floats)
+    static constexpr int Bytes = 151616 + 256;
     static constexpr int HQBytes = 65536;
 };
 template <>
@@ -81,6 +84,7 @@ struct SLay<4> {   // IQ1_M only
     static constexpr int CP = 0, SGN = -1, XXS = -1, SGN_IN_ROW = 0, XS = -1;
     static constexpr int IQ1 = 0;
     static constexpr int XQ = 32768, HQ = 32768, Y = 98304;   // HQ over XQ
+    static constexpr int NRM = XQ + 8192;                     // pre-norm partials: past XQ, under HQ
     static constexpr int Bytes = 102400;
     static constexpr int HQBytes = 65536;
 };
@@ -90,6 +94,7 @@ struct SLay<7> {   // any mix: one 256-byte row holds 16 grid copies, then 16 si
     static constexpr int XXS = 65536, SGN = 65536, SGN_IN_ROW = 128;
     static constexpr int IQ1 = 0, XS = 32768, Y = 49152;
     static constexpr int XQ = 131072, HQ = 131072;   // HQ over XQ
+    static constexpr int NRM = XQ + 8192;            // pre-norm partials: past XQ, under HQ
     static constexpr int Bytes = 163584;
     static constexpr int HQBytes = Bytes - HQ;
 };
@@ -106,6 +111,23 @@ struct Smem {
     int order[16];   // picks by ascending expert id (stable: equal ids keep pick order)
     uint32_t parity;
 };
+
+// Lanes 0 and 32's sums of a butterfly over each 32-lane half of the wave, xor
+// offsets 16, 8, 4, 2, 1 (v += v of lane ^ o): the order in which __shfl_xor
+// trees sum, by a row swap and DPP moves instead of LDS permutes. Only the
+// lanes that feed lanes 0 and 32 get their xor partners.
+__device__ __forceinline__ float xor_sum32(float v) {
+    const uint32_t u = __float_as_uint(v);
+    const auto r = __builtin_amdgcn_permlane16_swap(u, u, false, false);   // r[1]: rows 1, 3 in rows 0, 2
+    v = __fadd_rn(v, __uint_as_float(r[1]));
+#define XL_DPP(x, ctrl) __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(x), __float_as_int(x), ctrl, 0xF, 0xF, false))
+    v = __fadd_rn(v, XL_DPP(v, 0x128));   // row_ror:8: lane ^ 8
+    v = __fadd_rn(v, XL_DPP(v, 0x104));   // row_shl:4: lanes 0..3 of a row read lanes 4..7
+    v = __fadd_rn(v, XL_DPP(v, 0x4E));    // quad_perm 2,3,0,1: lane ^ 2
+    v = __fadd_rn(v, XL_DPP(v, 0xB1));    // quad_perm 1,0,3,2: lane ^ 1
+#undef XL_DPP
+    return v;
+}
 
 // Type of a matrix whose mask has one bit.
 template <int TM>
@@ -302,10 +324,31 @@ __global__ __launch_bounds__(NW * 64, 1) void stream_kernel(Layer3Args a) {
     // x first: its Q8_K runs while the codebook loads are in flight
     constexpr int UX = (16 + NW - 1) / NW;
     float4 xv[UX];
+    // Pre-norm in the kernel (a.pn_h, uniform): xv takes the stream's values,
+    // pw the norm weights, pv the values of the two threads of hc_pre_norm_kernel's
+    // 1,024 that this thread stands in for (v = t and t + 512: elements v + 1024 r).
+    // The arithmetic waits until the codebook loads are out.
+    const bool pn = a.pn_h != nullptr;
+    static_assert(NW * 64 == 512, "pre-norm: two of hc_pre_norm_kernel's 1,024 threads per thread");
+    float4 pw[UX];
+    float pv[2][4], pm = 0.0f;
 #pragma unroll
     for (int u = 0; u < UX; ++u) {
         const int b = wv + NW * u;
-        xv[u] = reinterpret_cast<const float4*>(a.x + 256 * (b < nbx ? b : 0))[lane];
+        xv[u] = reinterpret_cast<const float4*>((pn ? a.pn_h : a.x) + 256 * (b < nbx ? b : 0))[lane];
+    }
+    if (pn) {
+        pm = a.pn_mix[0];
+#pragma unroll
+        for (int u = 0; u < UX; ++u) {
+            const int b = wv + NW * u;
+            pw[u] = a.pn_w ? reinterpret_cast<const float4*>(a.pn_w + 256 * (b < nbx ? b : 0))[lane]
+                           : make_float4(1.0f, 1.0f, 1.0f, 1.0f);
+        }
+#pragma unroll
+        for (int s = 0; s < 2; ++s)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) pv[s][r] = a.pn_h[min(t + 512 * s + 1024 * r, dim - 1)];
     }
     uint2 vx[HASXXS ? NX : 1], vs[HASXS ? NS : 1];
     uint4 v1[HAS1 ? N1 : 1];
@@ -499,6 +542,57 @@ __global__ __launch_bounds__(NW * 64, 1) void stream_kernel(Layer3Args a) {
             const int i = blk / nbh;
             hblk = (uint32_t(bq < nb) << 8) | (uint32_t(i) << 4) | uint32_t(blk - i * nbh);
         }
+    }
+
+    // ---- pre-norm (a.pn_h): hc_pre_norm_kernel's arithmetic in its order. Pre
+    // values a = 0 + m h; each of the 1,024 threads' sum of a^2 over its elements
+    // in r order, trees over 32-thread groups (xor offsets 16 .. 1), the same
+    // tree over the 32 group sums, then x = (a * inv) * w, inv = 1 / sqrt(S /
+    // dim + eps).
+    if (pn) {
+        const float m = pm;
+#pragma unroll
+        for (int u = 0; u < UX; ++u) {
+            xv[u].x = __fadd_rn(0.0f, __fmul_rn(m, xv[u].x));
+            xv[u].y = __fadd_rn(0.0f, __fmul_rn(m, xv[u].y));
+            xv[u].z = __fadd_rn(0.0f, __fmul_rn(m, xv[u].z));
+            xv[u].w = __fadd_rn(0.0f, __fmul_rn(m, xv[u].w));
+        }
+        if (a.pn_w) {
+            float* const red = reinterpret_cast<float*>(lds + LY::NRM);
+            float ss[2] = {0.0f, 0.0f};
+#pragma unroll
+            for (int s = 0; s < 2; ++s)
+#pragma unroll
+                for (int r = 0; r < 4; ++r)
+                    if (t + 512 * s + 1024 * r < dim) {
+                        const float av = __fadd_rn(0.0f, __fmul_rn(m, pv[s][r]));
+                        ss[s] = __fadd_rn(ss[s], __fmul_rn(av, av));
+                    }
+#pragma unroll
+            for (int s = 0; s < 2; ++s) {
+                ss[s] = xor_sum32(ss[s]);
+                if ((lane & 31) == 0) red[(t + 512 * s) >> 5] = ss[s];
+            }
+            lds_barrier();
+            // every wave sums the 32 group sums itself (NRM is not written again
+            // before the prologue's last barrier, so no second barrier)
+            const float tot = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(xor_sum32(red[lane & 31])), 0));
+            const float inv = __fdiv_rn(1.0f, sqrtf(__fadd_rn(__fdiv_rn(tot, float(dim)), a.pn_eps)));
+#pragma unroll
+            for (int u = 0; u < UX; ++u) {
+                xv[u].x = __fmul_rn(__fmul_rn(xv[u].x, inv), pw[u].x);
+                xv[u].y = __fmul_rn(__fmul_rn(xv[u].y, inv), pw[u].y);
+                xv[u].z = __fmul_rn(__fmul_rn(xv[u].z, inv), pw[u].z);
+                xv[u].w = __fmul_rn(__fmul_rn(xv[u].w, inv), pw[u].w);
+            }
+        }
+        if (a.pn_x && blockIdx.x == 0)
+#pragma unroll
+            for (int u = 0; u < UX; ++u) {
+                const int b = wv + NW * u;
+                if (b < nbx) reinterpret_cast<float4*>(a.pn_x + 256 * b)[lane] = xv[u];
+            }
     }
 
     // ---- Q8_K(x), then codebooks (copies, computed sign rows): LDS writes, one barrier

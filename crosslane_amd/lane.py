@@ -105,6 +105,8 @@ _SIGNATURES = {
     "xl_shared_forward_noalloc": (_I32, [_P, _I32, _P, _I32, _P, _I32, _P, _I32, _I32, _P, _P, _P, _ErrP]),
     "xl_hc_post_async": (_I32, [_P, _P, _P, _P, _P, _I32, _I32, _I32, _P, _P, _ErrP]),
     "xl_hc_pre_norm_async": (_I32, [_P, _P, _P, _P, _I32, _I32, _I32, C.c_float, _P, _P, _ErrP]),
+    "xl_layer_forward_prenorm_async": (_I32, [_P, _I32, _P, _P, _I32, _P, _I32, _P, _P, C.c_float, _P, _P, _P, _P,
+                                              _ErrP]),
     "xl_profile_begin": (_I32, [_P, _I32, _ErrP]),
     "xl_profile_end": (_I32, [_P, _f32p, _I32, C.POINTER(_I32), C.POINTER(_I32), C.c_char_p, _I32, _ErrP]),
     "xl_profile_timeline": (_I32, [_P, _u64p, _I32, C.POINTER(_I32), _ErrP]),
@@ -347,6 +349,17 @@ class Lane:
     def layer_forward_async(self, layer: int, ids, w, x, out, shared=None, stream=None) -> None:
         self._call("xl_layer_forward_async", layer, _ptr(ids), _ptr(w), int(ids.numel()), _ptr(x), _ptr(shared),
                    _ptr(out), None if stream is None else int(stream))
+
+    def layer_forward_prenorm_async(self, layer: int, ids, w, h, mix, norm_w, x, out, eps: float = 1e-6, shared=None,
+                                    stream=None) -> None:
+        """The layer on x = hc_pre_norm(h, mix, norm_w) of one token: h [H, dim]
+        (or [1, H, dim]), mix [8], norm_w [dim] or None; x [dim] receives the
+        normalized input (one launch when H == 1 and the layer has a streaming
+        instance: the norm runs in its prologue)."""
+        H = int(h.shape[-2]) if h.dim() >= 2 else 1
+        self._call("xl_layer_forward_prenorm_async", layer, _ptr(ids), _ptr(w), int(ids.numel()), _ptr(h), H,
+                   _ptr(mix), _ptr(norm_w), float(eps), _ptr(x), _ptr(shared), _ptr(out),
+                   None if stream is None else int(stream))
 
     def layer_trace_async(self, layer: int, ids, w, x, out, q8x=None, q8h=None, h=None, ints=None, shared=None,
                           stream=None, y=None) -> int:

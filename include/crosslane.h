@@ -323,6 +323,18 @@ int32_t xl_shared_forward_noalloc(xl_context* ctx, int32_t type_gate, const void
  * reference. x may not overlap h, mix or w; eps finite and positive. */
 int32_t xl_hc_pre_norm_async(xl_context* ctx, const float* d_h, const float* d_mix, const float* d_w_or_null,
                              int32_t D, int32_t H, int32_t T, float eps, float* d_x, void* stream, xl_error* err);
+/* The pre-norm and the MoE layer of one token as one call (hip_backend.cpp:629
+ * k4::hc_pre_norm, then the routed-expert layer of :635-711): x =
+ * xl_hc_pre_norm_async(h, mix, norm_w, D = dim, H, T = 1) is written to d_x
+ * and is the layer's input, as xl_layer_forward_async(d_ids, d_w, k, d_x)
+ * takes it; out and x bit-identical to those two calls. With H == 1 and a
+ * layer the streaming kernel runs, one launch: every workgroup normalizes h
+ * in its prologue. h H x dim, mix 8, norm_w dim (null: the pre values only).
+ * x may not overlap h, mix or norm_w; out may not overlap h or x. */
+int32_t xl_layer_forward_prenorm_async(xl_context* ctx, int32_t layer, const int32_t* d_ids, const float* d_w,
+                                       int32_t k, const float* d_h, int32_t H, const float* d_mix,
+                                       const float* d_norm_w_or_null, float eps, float* d_x,
+                                       const float* d_shared_or_null, float* d_out, void* stream, xl_error* err);
 /* Hyper-connection post after the MoE block (hip_backend.cpp:777 k4::hc_post;
  * sycl/hc/hc.cpp:107-115, core.hpp:81-86): for T tokens and H <= 4 streams of
  * D, out[t][k][e] = post[t][k] * y[t][e] + sum_j comb[t][j * H + k] *

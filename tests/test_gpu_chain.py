@@ -118,3 +118,36 @@ def test_chain_40_layers(chain, orc):
     # The oracle's own 40-layer chain from the same x0 (reported: see the module note)
     r_e2e = max_rel(hs[L], e2e)
     step(f"chain: worst per-layer max_rel {worst:.3e}; end-to-end final hidden max_rel {r_e2e:.3e}")
+
+
+def run_pass_prenormed(lane, ids, w, x0):
+    """The same pass with each carry inside the next layer's call
+    (xl_layer_forward_prenorm_async: one launch per layer); the last carry by
+    xl_hc_pre_norm_async. Returns (inputs [L+1, dim], outputs [L, dim])."""
+    s = torch.cuda.Stream()
+    with torch.cuda.stream(s):
+        d_ids, d_w = dev(ids), dev(w)
+        hs = torch.zeros((L + 1, DIM), dtype=torch.float32, device="cuda")
+        ys = torch.zeros((L, DIM), dtype=torch.float32, device="cuda")
+        hs[0].copy_(dev(x0))
+        mix, ones = dev(MIX1), torch.ones(DIM, dtype=torch.float32, device="cuda")
+        lane.layer_forward_async(0, d_ids[0], d_w[0], hs[0], ys[0], stream=s.cuda_stream)
+        for l in range(1, L):
+            lane.layer_forward_prenorm_async(l, d_ids[l], d_w[l], ys[l - 1].view(1, DIM), mix, ones, hs[l], ys[l],
+                                             stream=s.cuda_stream)
+        lane.hc_pre_norm_async(ys[L - 1].view(1, 1, DIM), mix, ones, hs[L].view(1, DIM), stream=s.cuda_stream)
+    lane.sync(s.cuda_stream)
+    torch.cuda.synchronize()
+    return hs.cpu().numpy(), ys.cpu().numpy()
+
+
+def test_chain_prenormed_layers_match(chain):
+    # the carry inside the layer call gives the pass of separate norm launches, bit for bit
+    lane, _ = chain
+    ids, w, x0 = chain_routes()
+    step("chain pass, separate norms")
+    hs, ys = run_pass(lane, ids, w, x0)
+    step("chain pass, norms inside the layer calls")
+    hs2, ys2 = run_pass_prenormed(lane, ids, w, x0)
+    assert np.array_equal(ys.view(np.uint32), ys2.view(np.uint32))
+    assert np.array_equal(hs.view(np.uint32), hs2.view(np.uint32))

@@ -34,6 +34,8 @@
 // LDS once per work item instead of being loaded by every wave.
 #include <hip/hip_runtime.h>
 
+#include <type_traits>
+
 #include "xl_dev.hpp"
 #include "xl_format.hpp"
 #include "xl_internal.hpp"
@@ -613,6 +615,9 @@ __global__ __launch_bounds__(NW * 64, 1) void dn_kernel(GroupArgs a) {
 // the stable order of an insertion sort) into LDS; every thread then issues
 // its column's loads of all the token's rows before the fma chain.
 // ---------------------------------------------------------------------------
+// V values per thread (V = 4: 16-byte loads and stores; out and shared 16-byte
+// aligned), each combined exactly as with V = 1.
+template <int V>
 __global__ __launch_bounds__(256) void gcombine_kernel(GroupArgs a) {
     __shared__ int s_row[16];     // pair row of rank r
     __shared__ float s_w[16];
@@ -635,18 +640,26 @@ __global__ __launch_bounds__(256) void gcombine_kernel(GroupArgs a) {
         if (t == 0) s_n = n;
     }
     __syncthreads();
-    const int c = blockIdx.x * 256 + t;
-    if (c >= a.dim) return;
+    const int c = (blockIdx.x * 256 + t) * V;
+    if (c >= a.dim) return;   // dim is a multiple of 256
     const int n = s_n;
-    float v[16];
+    using VT = std::conditional_t<V == 4, float4, float>;
+    auto lanes = [](VT& x) -> float* { return reinterpret_cast<float*>(&x); };
+    VT v[16];
 #pragma unroll
-    for (int r = 0; r < 16; ++r) v[r] = r < n ? a.y[size_t(s_row[r]) * a.dim + c] : 0.0f;
-    float acc = 0.0f;
+    for (int r = 0; r < 16; ++r) v[r] = r < n ? *reinterpret_cast<const VT*>(a.y + size_t(s_row[r]) * a.dim + c) : VT{};
+    VT acc{};
 #pragma unroll
     for (int r = 0; r < 16; ++r)
-        if (r < n) acc = fmaf(s_w[r], v[r], acc);
-    if (a.shared) acc = __fadd_rn(acc, a.shared[size_t(tok) * a.dim + c]);
-    a.out[size_t(tok) * a.dim + c] = acc;
+        if (r < n)
+#pragma unroll
+            for (int e = 0; e < V; ++e) lanes(acc)[e] = fmaf(s_w[r], lanes(v[r])[e], lanes(acc)[e]);
+    if (a.shared) {
+        VT sh = *reinterpret_cast<const VT*>(a.shared + size_t(tok) * a.dim + c);
+#pragma unroll
+        for (int e = 0; e < V; ++e) lanes(acc)[e] = __fadd_rn(lanes(acc)[e], lanes(sh)[e]);
+    }
+    *reinterpret_cast<VT*>(a.out + size_t(tok) * a.dim + c) = acc;
 }
 
 }  // namespace
@@ -683,7 +696,9 @@ hipError_t launch_grouped(const GroupArgs& args, int cus, hipStream_t s) {
                            args.hq, args.hd, args.pos, args.k, args.err, nullptr);
         hipLaunchKernelGGL((dn_kernel<NW, false>), dim3(cus), dim3(NW * 64), 0, s, args);
     }
-    hipLaunchKernelGGL(gcombine_kernel, dim3((args.dim + 255) / 256, args.T), dim3(256), 0, s, args);
+    const bool al16 = (reinterpret_cast<uintptr_t>(args.out) | reinterpret_cast<uintptr_t>(args.shared)) % 16 == 0;
+    if (al16) hipLaunchKernelGGL(gcombine_kernel<4>, dim3((args.dim / 4 + 255) / 256, args.T), dim3(256), 0, s, args);
+    else hipLaunchKernelGGL(gcombine_kernel<1>, dim3((args.dim + 255) / 256, args.T), dim3(256), 0, s, args);
     return hipGetLastError();
 }
 

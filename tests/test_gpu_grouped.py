@@ -168,3 +168,31 @@ def test_grouped_bad_id_and_limits(monkeypatch):
             ctx0.grouped_forward(0, np.zeros((1, 1), np.int32), np.ones((1, 1), np.float32), np.ones((1, dim), np.float32))
     finally:
         ctx0.close()
+
+
+def test_grouped_unaligned_out_and_shared(monkeypatch):
+    # out and shared 4 bytes off a 16-byte boundary take the one-column combine;
+    # it must equal the four-column combine of aligned buffers bit for bit
+    step("grouped combine: unaligned out / shared")
+    rng = np.random.default_rng(77)
+    E, T, k, dim = 16, 12, 6, 1024
+    monkeypatch.setenv("XL_GROUPED_PATH", "2")
+    lane = xl.Lane(dim, 512, 1, E, types_map(1, E, 16, 17), max_picks=8, max_tokens=64)
+    try:
+        lane.generate(seed=5)
+        ids, w = token_routes(rng, T, E, k)
+        x = rng.standard_normal((T, dim)).astype(np.float32)
+        sh = rng.standard_normal((T, dim)).astype(np.float32)
+        d_ids, d_w, d_x = dev(ids), dev(w), dev(x)
+        a_sh, a_out = dev(sh), torch.zeros((T, dim), dtype=torch.float32, device="cuda")
+        u_sh_buf = torch.zeros(T * dim + 1, dtype=torch.float32, device="cuda")
+        u_out_buf = torch.zeros(T * dim + 1, dtype=torch.float32, device="cuda")
+        u_sh, u_out = u_sh_buf[1:].view(T, dim), u_out_buf[1:].view(T, dim)
+        assert u_sh.data_ptr() % 16 == 4 and u_out.data_ptr() % 16 == 4
+        u_sh.copy_(a_sh)
+        lane.grouped_forward_async(0, d_ids, d_w, d_x, a_out, shared=a_sh)
+        lane.grouped_forward_async(0, d_ids, d_w, d_x, u_out, shared=u_sh)
+        lane.sync()
+        assert np.array_equal(a_out.cpu().numpy().view(np.uint32), u_out.cpu().numpy().view(np.uint32))
+    finally:
+        lane.close()

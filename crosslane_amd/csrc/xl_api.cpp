@@ -165,12 +165,11 @@ struct xl_context {
     xl::ExpertDesc* d_descs = nullptr;
     uint64_t payload = 0, allocated = 0;
     int grid_gu = 0, grid_down = 0;
-    // Layer path: 1 = single launch (default: for IQ2_XXS gate/up + IQ2_XS down
-    // layers the unit kernel of xl_unit.hip, else the streaming kernel of
-    // xl_stream.hip; other layers the all-types kernel of xl_layer.hip), 3 = the
-    // all-types single launch only, 2 = cooperative fused kernel, 0 = separate
-    // launches, 4 = the streaming kernel only, 5 = the unit kernel only (a layer
-    // they cannot run is an error). XL_LAYER_PATH selects; shapes without a
+    // Layer path: 1 = single launch (default: the streaming kernel of
+    // xl_stream.hpp where it has an instance for the layer, else the all-types
+    // kernel of xl_layer.hip, else separate launches), 3 = the all-types single
+    // launch only, 4 = the streaming kernel only (a layer it cannot run is an
+    // error), 0 = separate launches. XL_LAYER_PATH selects; shapes without a
     // single-launch instance use separate launches.
     int path = 1;
     // Grouped path: 1 = the MFMA kernels where the layer's types allow, else one
@@ -178,8 +177,6 @@ struct xl_context {
     // kernels only (a layer they cannot run is an error). XL_GROUPED_PATH selects.
     int gpath = 1;
     float* hbuf = nullptr;      // streaming kernel's h exchange (2 x kHBufWords, sentinel-filled)
-    float* part = nullptr;      // unit kernel's down partials (max_picks * ff/256 units x dim floats)
-    uint32_t* ucnt = nullptr;   // unit kernel's partial counters (2 x 256 words, zeroed at open)
     // grouped path (xl_grouped.hip), sized by max_tokens * max_picks pairs
     struct Group {
         int32_t* ids = nullptr; float* w = nullptr; float* x = nullptr; float* shared = nullptr; float* out = nullptr;
@@ -188,7 +185,6 @@ struct xl_context {
         float* h = nullptr; int8_t* hq = nullptr; float* hd = nullptr; float* y = nullptr;
         uint64_t hq_bytes = 0;
     } grp;
-    uint32_t* sync = nullptr;   // counters of the cooperative fused kernel
     uint64_t* htag = nullptr;   // single-launch handoff buffers (Layer3Args)
     uint64_t* hqtag = nullptr;
     uint64_t* hdtag = nullptr;
@@ -212,6 +208,8 @@ struct xl_context {
     hipEvent_t done = nullptr;
     hipStream_t last_stream = nullptr;
     bool has_last = false;
+    // Layer calls by the way they ran (XL_LAUNCH_*), for xl_debug_launch_counts.
+    int64_t launches[XL_LAUNCH_KINDS] = {};
 };
 
 namespace {
@@ -359,8 +357,6 @@ xl::Layer3Args layer3_args(xl_context* ctx, int32_t layer, const int32_t* d_ids,
     a.lim = ctx->cfg.swiglu_limit;
     a.tables = ctx->tables;
     a.hbuf = ctx->hbuf;
-    a.part = ctx->part;
-    a.ucnt = ctx->ucnt;
     if (ctx->prof.on && ctx->prof.calls <= ctx->prof.max_calls) {
         a.trace = ctx->timeline;
         hip_check(hipMemsetAsync(ctx->timeline, 0, size_t(ctx->cus) * 16 * 32 * 8, s), "timeline clear");
@@ -395,6 +391,7 @@ bool enqueue_layer_routed(xl_context* ctx, int32_t layer, const float* d_logits,
         return false;
     }
     hip_check(e, "routed streaming layer");
+    ++ctx->launches[XL_LAUNCH_ROUTED];
     return true;
 }
 
@@ -419,6 +416,7 @@ bool enqueue_layer_prenorm(xl_context* ctx, int32_t layer, const int32_t* d_ids,
         return false;
     }
     hip_check(e, "pre-normed streaming layer");
+    ++ctx->launches[XL_LAUNCH_PRENORM];
     return true;
 }
 
@@ -430,27 +428,26 @@ bool enqueue_layer(xl_context* ctx, int32_t layer, const int32_t* d_ids, const f
     const int gu_mask = ctx->gu_mask[size_t(layer)], dn_mask = ctx->dn_mask[size_t(layer)];
     Marks mark(ctx, s);
     mark("");
-    if ((ctx->path == 1 || ctx->path == 3 || ctx->path == 4 || ctx->path == 5) && !g_dbg && !u_dbg) {
+    if ((ctx->path == 1 || ctx->path == 3 || ctx->path == 4) && !g_dbg && !u_dbg) {
         xl::Layer3Args a = layer3_args(ctx, layer, d_ids, d_w, k, d_x, d_shared, d_out, s, tr);
         if (d_out) {
             hipError_t e = hipErrorNotSupported;
-            if (ctx->path == 5 && gu_mask == 1 && dn_mask == 2) {
-                e = xl::dev::launch_unit(a, ctx->cus, s, stop);
-                if (e != hipSuccess && e != hipErrorNotSupported) hip_check(e, "unit layer");
-                (void)hipGetLastError();
-                if (tr && e == hipSuccess) tr->kernel = 5;
-            }
-            need(ctx->path != 5 || e == hipSuccess, XL_E_ARG, "XL_LAYER_PATH=5: no unit-kernel instance for this layer");
-            if ((ctx->path == 1 || ctx->path == 4) && e == hipErrorNotSupported) {
+            if (ctx->path == 1 || ctx->path == 4) {
                 e = xl::dev::launch_stream(a, gu_mask, dn_mask, ctx->cus, s, stop);
                 if (e != hipSuccess && e != hipErrorNotSupported) hip_check(e, "streaming layer");
                 (void)hipGetLastError();
-                if (tr && e == hipSuccess) tr->kernel = 1;
+                if (e == hipSuccess) {
+                    ++ctx->launches[XL_LAUNCH_STREAM];
+                    if (tr) tr->kernel = 1;
+                }
             }
             need(ctx->path != 4 || e == hipSuccess, XL_E_ARG, "XL_LAYER_PATH=4: no streaming-kernel instance for this layer");
             if (e == hipErrorNotSupported) {
                 e = xl::dev::launch_layer3(a, gu_mask, dn_mask, ctx->cus, s, stop);
-                if (tr && e == hipSuccess) tr->kernel = 3;
+                if (e == hipSuccess) {
+                    ++ctx->launches[XL_LAUNCH_ALLTYPES];
+                    if (tr) tr->kernel = 3;
+                }
             }
             if (e == hipSuccess) {
                 if (a.trace) ctx->timeline_words = uint64_t(ctx->cus) * 16 * 32;
@@ -462,21 +459,7 @@ bool enqueue_layer(xl_context* ctx, int32_t layer, const int32_t* d_ids, const f
         }
     }
     need(tr == nullptr, XL_E_ARG, "trace: this layer does not run as a single launch (shape, path or output)");
-    if (ctx->path == 2 && !g_dbg && !u_dbg) {
-        xl::LayerArgs a{};
-        a.descs = descs; a.ids = d_ids; a.w = d_w; a.x = d_x; a.shared = d_shared; a.out = d_out;
-        a.k = k; a.n_experts = E; a.dim = dim; a.ff = ff;
-        a.xq = ctx->xq; a.xd = ctx->xd; a.h = ctx->h; a.hq = ctx->hq; a.hd = ctx->hd; a.y = ctx->y;
-        a.sync = ctx->sync; a.err = ctx->err_flag; a.codes = ctx->codes;
-        a.lim = ctx->cfg.swiglu_limit;
-        const hipError_t e = xl::dev::launch_layer_fused(a, gu_mask | dn_mask, ctx->cus, s);
-        if (e == hipSuccess) {
-            mark("layer");
-            return false;
-        }
-        if (e != hipErrorNotSupported) hip_check(e, "fused layer launch");
-        (void)hipGetLastError();   // shape without a fused instance: separate launches below
-    }
+    ++ctx->launches[XL_LAUNCH_SEPARATE];
     hip_check(xl::dev::launch_q8k(d_x, dim / 256, ctx->xq, ctx->xd, nullptr, ctx->err_flag, s), "Q8_K(x) launch");
     mark("q8k_x");
     hip_check(xl::dev::launch_gate_up(descs, d_ids, k, E, dim, ff, ctx->xq, ctx->xd, ctx->codes, ctx->h, g_dbg, u_dbg,
@@ -610,7 +593,6 @@ int32_t xl_open(uint32_t abi_version, const xl_config* cfg, xl_context** out, xl
         std::vector<Part> parts = {
             {reinterpret_cast<void**>(&ctx->codes), code_bytes},
             {reinterpret_cast<void**>(&ctx->err_flag), 256},
-            {reinterpret_cast<void**>(&ctx->sync), uint64_t(xl::kSyncWords) * 4},
             {reinterpret_cast<void**>(&ctx->x), uint64_t(dim) * 4},
             {reinterpret_cast<void**>(&ctx->xq), uint64_t(ctx->act_max)},
             {reinterpret_cast<void**>(&ctx->xd), uint64_t(ctx->act_max / 256) * 4},
@@ -631,8 +613,6 @@ int32_t xl_open(uint32_t abi_version, const xl_config* cfg, xl_context** out, xl
             {reinterpret_cast<void**>(&ctx->hdtag), uint64_t(P) * (ff / 256) * 8},
             {reinterpret_cast<void**>(&ctx->ctl), 256},
             {reinterpret_cast<void**>(&ctx->hbuf), uint64_t(2) * xl::kHBufWords * 4},
-            {reinterpret_cast<void**>(&ctx->part), uint64_t(P) * (ff / 256) * dim * 4},
-            {reinterpret_cast<void**>(&ctx->ucnt), 2 * 256 * 4},
             {reinterpret_cast<void**>(&ctx->tables), uint64_t(xl::kTableBytes)},
             {reinterpret_cast<void**>(&ctx->p32d), (uint64_t(ctx->act_max / 32) + uint64_t(P) * (ff / 32)) * 4},
             {reinterpret_cast<void**>(&ctx->timeline), uint64_t(ctx->cus) * 16 * 32 * 8},
@@ -677,19 +657,18 @@ int32_t xl_open(uint32_t abi_version, const xl_config* cfg, xl_context** out, xl
         for (int i = 0; i < 256 + 512; ++i) (void)expand_codes(codes[size_t(i)], false);   // rejects a corrupt symbol
         hip_check(hipMemcpy(ctx->codes, codes.data(), code_bytes, hipMemcpyHostToDevice), "codebook upload");
         hip_check(hipMemset(ctx->err_flag, 0, 256), "error flag clear");
-        hip_check(hipMemset(ctx->sync, 0, size_t(xl::kSyncWords) * 4), "counter clear");
         hip_check(hipMemset(ctx->htag, 0, size_t(P) * ff * 8), "tag clear");
         hip_check(hipMemset(ctx->hdtag, 0, size_t(P) * (ff / 256) * 8), "tag clear");
         hip_check(hipMemset(ctx->hqtag, 0, size_t(P) * ff * 2), "tag clear");
         hip_check(hipMemset(ctx->ctl, 0, 256), "epoch clear");
-        hip_check(hipMemset(ctx->ucnt, 0, 2 * 256 * 4), "unit counter clear");
         hip_check(hipMemset(ctx->hbuf, 0xff, size_t(2) * xl::kHBufWords * 4), "h exchange fill");
         const std::vector<uint64_t> tab = layer_tables();
         hip_check(hipMemcpy(ctx->tables, tab.data(), tab.size() * 8, hipMemcpyHostToDevice), "table upload");
         void* scratch = nullptr;   // the no-allocation scratch's address on this device, looked up once
         hip_check(xl::dev::noalloc_scratch(cfg->device, &scratch), "no-allocation scratch address");
         ctx->path = env_int("XL_LAYER_PATH", 1);
-        need(ctx->path >= 0 && ctx->path <= 5, XL_E_ARG, "XL_LAYER_PATH must be 0, 1, 2, 3, 4 or 5");
+        need(ctx->path == 0 || ctx->path == 1 || ctx->path == 3 || ctx->path == 4, XL_E_ARG,
+             "XL_LAYER_PATH must be 0, 1, 3 or 4");
         ctx->gpath = env_int("XL_GROUPED_PATH", 1);
         need(ctx->gpath >= 0 && ctx->gpath <= 2, XL_E_ARG, "XL_GROUPED_PATH must be 0, 1 or 2");
         *out = ctx;
@@ -1728,9 +1707,24 @@ int32_t xl_debug_set_launch_count(xl_context* ctx, uint32_t launches, xl_error* 
         // count (its parity); the arrival counters ctl[1], ctl[3] are zero between launches.
         const uint32_t w[4] = {launches, 0u, launches, 0u};
         hip_check(hipMemcpyAsync(ctx->ctl, w, sizeof w, hipMemcpyHostToDevice, s), "launch count upload");
-        // the unit kernel's partial counters of both parities start from zero again
-        hip_check(hipMemsetAsync(ctx->ucnt, 0, 2 * 256 * 4, s), "unit counter clear");
+        // The exchange state back to its state at xl_open, so that any count is
+        // safe: the streaming kernel reads the h buffer of parity (count + 1) & 1
+        // and expects it to hold the sentinel only (each launch refills the other
+        // one), and the all-types kernel's tags of an epoch set back to one already
+        // used would otherwise read as ready.
+        const int P = ctx->cfg.max_picks, ff = ctx->cfg.ff;
+        hip_check(hipMemsetAsync(ctx->hbuf, 0xff, size_t(2) * xl::kHBufWords * 4, s), "h exchange fill");
+        hip_check(hipMemsetAsync(ctx->htag, 0, size_t(P) * ff * 8, s), "tag clear");
+        hip_check(hipMemsetAsync(ctx->hdtag, 0, size_t(P) * (ff / 256) * 8, s), "tag clear");
+        hip_check(hipMemsetAsync(ctx->hqtag, 0, size_t(P) * ff * 2, s), "tag clear");
         hip_check(hipStreamSynchronize(s), "launch count drain");
+    });
+}
+
+int32_t xl_debug_launch_counts(xl_context* ctx, int64_t* counts, int32_t n, xl_error* err) {
+    return guarded(ctx, err, [&] {
+        need(counts != nullptr && n >= 0, XL_E_ARG, "null output");
+        for (int i = 0; i < n; ++i) counts[i] = i < XL_LAUNCH_KINDS ? ctx->launches[i] : 0;
     });
 }
 

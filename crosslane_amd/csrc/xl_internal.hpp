@@ -11,7 +11,7 @@ enum : int {
     kDevErrExpertId = 1,     // an id outside [0, n_experts)
     kDevErrNonFinite = 2,    // non-finite activation seen by a quantizer
     kDevErrType = 4,         // a matrix with an unsupported block type
-    kDevErrTimeout = 8,      // a bounded wait of the fused layer kernel expired
+    kDevErrTimeout = 8,      // a bounded wait of a single-launch layer kernel expired
 };
 
 // One planar matrix (see plane_layout in xl_format.hpp).
@@ -44,28 +44,6 @@ inline bool row_shape(int k, int& lpr, int& ppl) {
     }
 }
 constexpr int kMaxRowK = 5120;   // the longest row any kernel stages
-
-// Arguments of the fused layer kernel (device pointers).
-struct LayerArgs {
-    const ExpertDesc* descs;    // this layer's n_experts descriptors
-    const int32_t* ids;
-    const float* w;
-    const float* x;
-    const float* shared;        // may be null
-    float* out;
-    int k, n_experts, dim, ff;
-    int8_t* xq; float* xd;      // Q8_K(x), split form (qs, d)
-    float* h;                   // k * ff
-    int8_t* hq; float* hd;      // Q8_K(h), split form
-    float* y;                   // k * dim
-    uint32_t* sync;             // kSyncWords zeroed counters; the kernel re-zeroes them on exit
-    int* err;
-    float lim;                  // SwiGLU limit (> 0: g = min(g, lim), u = clamp(u, -lim, lim))
-    const uint16_t* codes;
-    int need;                   // codebooks to expand (filled in by the launcher)
-    int per_g, per_d;           // row slots per wave (filled in by the launcher)
-};
-constexpr int kSyncWords = 256;
 
 // Arguments of the single-launch layer kernel (xl_layer.hip); device pointers.
 struct Layer3Args {
@@ -103,8 +81,6 @@ struct Layer3Args {
     float* th;
     int32_t* tint;
     float* ty;                  // trace: every pick's row before the combine (k x dim, ids order)
-    float* part;                // unit kernel: per (pick, h block) unit, dim float partials of the down rows
-    uint32_t* ucnt;             // unit kernel: 2 sets (launch parity) of 8 partial counters, 32 words apart (2 x 256 words)
     // Routed in the kernel (streaming kernel; null: ids and w are read): every
     // wave routes the token from its n_experts <= kStreamRouteMax logits (bias
     // may be null) as the router kernel does; ids and w are then not read.
@@ -186,15 +162,9 @@ hipError_t launch_stream(const Layer3Args& args, int gu_types, int dn_types, int
                          hipEvent_t stop = nullptr);
 hipError_t launch_stream_iq1(const Layer3Args& args, int cus, hipStream_t s, hipEvent_t stop);
 hipError_t launch_stream_mix(const Layer3Args& args, int cus, hipStream_t s, hipEvent_t stop);
-// Unit layer (xl_unit.hip) for IQ2_XXS gate/up + IQ2_XS down: hipErrorNotSupported
-// when (dim, ff, k) has no instance.
-hipError_t launch_unit(const Layer3Args& args, int cus, hipStream_t s, hipEvent_t stop = nullptr);
 // Grouped path: hipErrorNotSupported unless gate/up are IQ2_XXS, down IQ2_XS and
 // the shapes fit (dim, ff multiples of 128; n_experts <= kGroupMaxExperts).
 hipError_t launch_grouped(const GroupArgs& args, int cus, hipStream_t s);
-// Fused layer: returns hipErrorNotSupported when (dim, ff) has no fused
-// instance or the device cannot hold the cooperative grid.
-hipError_t launch_layer_fused(const LayerArgs& args, int type_mask, int cus, hipStream_t s);
 hipError_t launch_q8k(const float* x, int nblocks, int8_t* qs, float* d, uint8_t* std_out, int* err, hipStream_t s);
 // `codes` is the compact codebook buffer (2-bit symbols, see xl_rows.hpp);
 // `target_wgs` is the workgroup count the row launches aim for.

@@ -1,4 +1,4 @@
-// Row decoding of the streaming layer kernels (xl_stream*.hip, xl_unit.hip),
+// Row decoding of the streaming layer kernels (xl_stream*.hip),
 // gfx950: perm-addressed, bank-interleaved LDS codebook copies, IQ2 sign masks
 // applied to the activations or to the grid, IQ1_M value rows, the Q8_K
 // quantizer of several blocks at once, and the sentinel h exchange words.
@@ -249,12 +249,13 @@ __device__ __forceinline__ bool h_ready(const uint4& v) {
 
 // ---- Q8_K of NB blocks at once ---------------------------------------------------------------
 // Block m is held by the wave as v[m] (lane l owns values 4l..4l+3). Bit-exact
-// with q8k_core.hpp:30-38: mx is the first value of largest magnitude (found
-// as the wave's largest magnitude, then the lowest position holding it), is =
-// -127/mx, q = min(127, nearest(is * v)), d = 1/is; an all-zero block gives
-// d = 0 and q = 0. The two divisions run once for all NB blocks (lane m
-// divides for block m); nearest is v_rndne (exact for |is * v| < 2^22) and
-// the quants are packed as q + 128 bytes by v_cvt_pk_u8_f32 (exact integers).
+// with q8k_core.hpp:30-38 on every finite input: mx is the first value of
+// largest magnitude (found as the wave's largest magnitude, then the lowest
+// position holding it), is = -127/mx, q = min(127, nearest(is * v)), d = 1/is;
+// an all-zero block gives d = 0 and q = 0. The two divisions run once for all
+// NB blocks (lane m divides for block m). nearest is the reference's own
+// (q8k_core.hpp:25-29): the quant byte is the low byte of the bits of
+// is * v + 12582912, and four of them are packed by two v_perm_b32.
 // One DPP max step on every block at once: the NB chains are independent, so
 // each fills the others' DPP wait states. old = 0 is max's identity, which lets
 // the compiler fold the move into v_max_u32_dpp.
@@ -278,8 +279,13 @@ __device__ __forceinline__ void wave_umax_n(uint32_t (&a)[NB], uint32_t (&out)[N
     for (int m = 0; m < NB; ++m) out[m] = uint32_t(__builtin_amdgcn_readlane(int(a[m]), 63));
 }
 // Returns false if a value of blocks 0..nvalid-1 is not finite (the others may hold anything).
-// |is * v| <= 127 (1 + 2^-24)^2 < 127.5 for every v of the block, so nearest(is * v)
-// never exceeds 127 and the reference's min(127, .) never applies.
+// With is finite, |is * v| <= 127 (1 + 2^-24)^2 < 127.5 for every v of the block,
+// so nearest(is * v) lies in -127..127, the reference's min(127, .) never applies
+// and the low byte is q's two's-complement byte. A block whose largest magnitude
+// is below 127 / FLT_MAX (subnormal or tiny) has is = -inf or +inf: is * v is
+// infinite (or NaN for v = 0), nearest gives -2^22 (or 0), the reference's int8
+// cast keeps the low byte 0, and so does the bit pattern of inf + 12582912 (or
+// NaN) here; d = 1/is is then -0 or +0, as the reference's.
 template <int NB>
 __device__ __forceinline__ bool q8k_blocks(const uint4 (&hv)[NB], int nvalid, int lane, uint32_t (&packed)[NB],
                                            float (&d)[NB]) {
@@ -317,15 +323,19 @@ __device__ __forceinline__ bool q8k_blocks(const uint4 (&hv)[NB], int nvalid, in
 #pragma unroll
     for (int m = 0; m < NB; ++m) {
         const float is = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(isv), m));
-        uint32_t p = 0;
+        uint32_t f[4];
 #pragma unroll
-        for (int j = 0; j < 4; ++j)   // q + 128 in 1..255, an exact integer: the byte conversion is exact
-            p = __builtin_amdgcn_cvt_pk_u8_f32(__fadd_rn(__builtin_rintf(__fmul_rn(is, __uint_as_float(x[m][j]))), 128.0f), j, p);
-        // the readlane stays outside the select: a select over it becomes a branch
-        // (a convergent call is not speculated), which splits the caller's code
+        for (int j = 0; j < 4; ++j) f[j] = __float_as_uint(__fadd_rn(__fmul_rn(is, __uint_as_float(x[m][j])), 12582912.0f));
+        // bytes 0, 1 <- low bytes of f0, f1; bytes 2, 3 <- low bytes of f2, f3
+        const uint32_t lo = __builtin_amdgcn_perm(f[1], f[0], 0x0C0C0400u);
+        const uint32_t hi = __builtin_amdgcn_perm(f[3], f[2], 0x04000C0Cu);
+        // an all-zero block: d = 0 and q = 0 as the reference's early return (not
+        // 1/is = -0 and the bytes of NaN products). The readlane stays outside the
+        // select: a select over it becomes a branch (a convergent call is not
+        // speculated), which splits the caller's code
         const float dm = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(dv), m));
         const bool zero = am[m] == 0u;
-        packed[m] = zero ? 0u : p ^ 0x80808080u;
+        packed[m] = zero ? 0u : lo | hi;
         d[m] = zero ? 0.0f : dm;
     }
     return fin;

@@ -1,14 +1,12 @@
 // CDNA4 (gfx950) kernels of the routed-expert lane.
 //
-//   layer_kernel    the whole routed-expert layer in one cooperative launch:
-//                   Q8_K(x), gate/up + SwiGLU of every pick, Q8_K(h), down,
-//                   fixed-order combine (the hot path)
 //   q8k_kernel      Q8_K activation quantization, bit-exact to the reference's
 //                   quant_block (engine/strata/sycl/stage/wiring/q8k_core.hpp:30-38)
 //   matvec_kernel   one IQ matrix x Q8_K vector (+ optional per-block int32
 //                   partials); the parity probe for the row engine
 //   gate_up_kernel, down_kernel, combine_kernel
-//                   the same layer as separate launches (probe / fallback path)
+//                   the layer as separate launches (probe / fallback path; the
+//                   single launches are in xl_stream.hpp and xl_layer.hip)
 //   generate_kernel seeded planar bank fill
 //
 // Build with -ffp-contract=off: the quantizer and the combine rely on separately
@@ -35,30 +33,11 @@ __device__ __forceinline__ int nearest_i(float x) {
     return int(__float_as_uint(v) & 0x007fffffu) - 0x00400000;
 }
 
-// Device-coherent 32-bit accesses for data exchanged between workgroups of one
-// launch (possibly on different XCDs): agent-scope relaxed atomics reach memory
-// past the XCD-private L2, so no cache writeback / invalidate is needed; an
-// s_waitcnt before the counter update orders them.
-__device__ __forceinline__ uint32_t coh_ld(const void* p) {
-    return __hip_atomic_load(reinterpret_cast<const uint32_t*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ void coh_st(void* p, uint32_t v) {
-    __hip_atomic_store(reinterpret_cast<uint32_t*>(p), v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ void coh_stf(float* p, float v) { coh_st(p, __float_as_uint(v)); }
-__device__ __forceinline__ void drain_memory() { __builtin_amdgcn_s_waitcnt(0); }
-
-template <bool COH = false>
 __device__ __forceinline__ void q8k_block(const float* __restrict__ x, int8_t* __restrict__ qs, float* __restrict__ dq,
                                           uint8_t* __restrict__ std_out, int* __restrict__ err, int lane) {
     float v[4];
-    if constexpr (COH) {
-#pragma unroll
-        for (int j = 0; j < 4; ++j) v[j] = __uint_as_float(coh_ld(x + 4 * lane + j));
-    } else {
-        const float4 v4 = reinterpret_cast<const float4*>(x)[lane];
-        v[0] = v4.x; v[1] = v4.y; v[2] = v4.z; v[3] = v4.w;
-    }
+    const float4 v4 = reinterpret_cast<const float4*>(x)[lane];
+    v[0] = v4.x; v[1] = v4.y; v[2] = v4.z; v[3] = v4.w;
     float am = 0.0f, mx = 0.0f;
     int idx = 1 << 30;
     bool finite = true;
@@ -91,13 +70,8 @@ __device__ __forceinline__ void q8k_block(const float* __restrict__ x, int8_t* _
         d = __fdiv_rn(1.0f, is);
     }
     bsum = quad_sum(bsum);
-    if constexpr (COH) {
-        coh_st(qs + 4 * lane, packed);
-        if (lane == 0) coh_stf(dq, d);
-    } else {
-        reinterpret_cast<uint32_t*>(qs)[lane] = packed;
-        if (lane == 0) *dq = d;
-    }
+    reinterpret_cast<uint32_t*>(qs)[lane] = packed;
+    if (lane == 0) *dq = d;
     if (std_out) {
         if (lane == 0) *reinterpret_cast<float*>(std_out) = d;
         reinterpret_cast<uint32_t*>(std_out + 4)[lane] = packed;
@@ -110,7 +84,7 @@ __global__ __launch_bounds__(256) void q8k_kernel(const float* __restrict__ x, i
                                                   int* __restrict__ err) {
     const int b = blockIdx.x * 4 + (threadIdx.x >> 6);
     if (b >= nblocks) return;   // wave-uniform
-    q8k_block<false>(x + size_t(b) * 256, qs + size_t(b) * 256, dq + b, std_out ? std_out + size_t(b) * 292 : nullptr, err,
+    q8k_block(x + size_t(b) * 256, qs + size_t(b) * 256, dq + b, std_out ? std_out + size_t(b) * 292 : nullptr, err,
               threadIdx.x & 63);
 }
 
@@ -246,7 +220,6 @@ __global__ __launch_bounds__(256) void down_kernel(const ExpertDesc* __restrict_
 
 // Fixed-order combine (runtime.cpp:183-188) of one output coordinate: ascending
 // expert id, out = fma(w, y, out) from +0, then + shared.
-template <bool COH = false>
 __device__ __forceinline__ float combine_one(const int32_t* ids, const float* w, int k, const float* y, int dim, int c,
                                              const float* shared) {
     int order[16];
@@ -258,7 +231,7 @@ __device__ __forceinline__ float combine_one(const int32_t* ids, const float* w,
     float acc = 0.0f;
     for (int t = 0; t < k; ++t) {
         const float* p = y + size_t(order[t]) * dim + c;
-        acc = fmaf(w[order[t]], COH ? __uint_as_float(coh_ld(p)) : *p, acc);
+        acc = fmaf(w[order[t]], *p, acc);
     }
     if (shared) acc = __fadd_rn(acc, shared[c]);
     return acc;
@@ -276,7 +249,7 @@ __global__ __launch_bounds__(256) void combine_kernel(const int32_t* __restrict_
                                                       int k, const float* __restrict__ y, int dim,
                                                       const float* __restrict__ shared, float* __restrict__ out) {
     const int c = blockIdx.x * 256 + threadIdx.x;
-    if (c < dim) out[c] = combine_one<false>(ids, w, k, y, dim, c, shared);
+    if (c < dim) out[c] = combine_one(ids, w, k, y, dim, c, shared);
 }
 
 // ---------------------------------------------------------------------------
@@ -331,215 +304,6 @@ __global__ __launch_bounds__(512) void route_kernel(const float* __restrict__ lo
     if (lane < k) {
         ids[size_t(t) * k + lane] = id;
         w[size_t(t) * k + lane] = wt;
-    }
-}
-
-// ---------------------------------------------------------------------------
-// The fused layer kernel.
-//
-// Every wave owns a contiguous range of gate/up row slots (pick-major over
-// k * ff rows) and of down row slots (over k * dim rows). It issues the loads
-// of its first batch of each before anything waits, fills the LDS codebooks,
-// then works through the dependency chain:
-//   x ready    workgroup 0 quantizes x into (xq, xd) and raises sync[kSyncX]
-//   gate/up    rows -> h (f32); each wave adds its row count to sync[kSyncGu + i]
-//   Q8_K(h)    wave q < k*ff/256 quantizes block q once pick i's gate/up rows
-//              are all in, then adds 1 to sync[kSyncHq + i]
-//   down       rows of pick i once all its h blocks are in -> y (f32)
-//   combine    the wave whose row count completes a 64-row chunk (all picks)
-//              combines that chunk into out
-//   exit       the last workgroup zeroes every counter for the next launch
-// Waits only point backwards in this chain and the launch is cooperative (all
-// workgroups resident), so it cannot deadlock; every spin is bounded and raises
-// kDevErrTimeout instead of hanging. Device-scope fences order the data
-// written before a counter add against the reads after the matching wait.
-// ---------------------------------------------------------------------------
-constexpr int kSyncX = 0, kSyncExit = 1, kSyncGu = 2, kSyncHq = 18, kSyncChunk = 34;
-constexpr uint32_t kSpinLimit = 1u << 20;   // polls of ~1 us: about a second, far beyond any legal wait
-
-__device__ __forceinline__ uint32_t ld_relaxed(const uint32_t* p) {
-    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ uint32_t add_relaxed(uint32_t* p, uint32_t v) {
-    return __hip_atomic_fetch_add(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-// Wave-uniform bounded wait for *p >= target. The data it guards is read with
-// coh_ld after the wait, so no cache invalidation is needed.
-__device__ bool wait_geq(const uint32_t* p, uint32_t target, int* err) {
-    uint32_t spins = 0;
-    while (ld_relaxed(p) < target) {
-        __builtin_amdgcn_s_sleep(1);
-        if (++spins > kSpinLimit) {
-            if ((threadIdx.x & 63) == 0) atomicOr(err, kDevErrTimeout);
-            return false;
-        }
-    }
-    return true;
-}
-
-template <int LG, int PG, int UG, int LD, int PD, int UD>
-__global__ __launch_bounds__(256) void layer_kernel(LayerArgs a) {
-    extern __shared__ uint8_t lds[];
-    constexpr int RG = 64 / LG, RD = 64 / LD;
-    const int t = threadIdx.x, lane = t & 63, wv = t >> 6;
-    const int gw = blockIdx.x * 4 + wv;
-    const int grpG = lane / LG, lG = lane % LG, grpD = lane / LD, lD = lane % LD;
-
-    CodeRegs cr;
-    codes_prefetch(cr, a.codes, a.need, t);
-
-    // ---- gate/up slots of this wave; the first batch is loaded now
-    const int sppG = a.ff / RG, SG = a.k * sppG;
-    const int g0 = gw * a.per_g, gn = max(0, min(a.per_g, SG - g0));
-    Raw<PG> rg[UG], ru[UG];
-    auto g_slot = [&](int s, int& i, int& row, const ExpertDesc*& D) -> bool {
-        i = s / sppG;
-        row = (s - i * sppG) * RG + grpG;
-        const int id = a.ids[i];
-        if (id < 0 || id >= a.n_experts) return false;
-        D = a.descs + id;
-        return true;
-    };
-    auto g_load = [&](int first) {
-#pragma unroll
-        for (int u = 0; u < UG; ++u)
-            if (first + u < gn) {
-                int i, row;
-                const ExpertDesc* D;
-                if (g_slot(g0 + first + u, i, row, D)) {
-                    load_raw<LG, PG>(rg[u], D->m[0].type, D->m[0], row, lG);
-                    load_raw<LG, PG>(ru[u], D->m[1].type, D->m[1], row, lG);
-                }
-            }
-    };
-    g_load(0);
-
-    // ---- down slots; the first batch is loaded now
-    const int sppD = a.dim / RD, SD = a.k * sppD;
-    const int d0 = gw * a.per_d, dn = max(0, min(a.per_d, SD - d0));
-    Raw<PD> rd[UD];
-    auto d_slot = [&](int s, int& i, int& row, const ExpertDesc*& D) -> bool {
-        i = s / sppD;
-        row = (s - i * sppD) * RD + grpD;
-        const int id = a.ids[i];
-        if (id < 0 || id >= a.n_experts) return false;
-        D = a.descs + id;
-        return true;
-    };
-    auto d_load = [&](int first) {
-#pragma unroll
-        for (int u = 0; u < UD; ++u)
-            if (first + u < dn) {
-                int i, row;
-                const ExpertDesc* D;
-                if (d_slot(d0 + first + u, i, row, D)) load_raw<LD, PD>(rd[u], D->m[2].type, D->m[2], row, lD);
-            }
-    };
-    d_load(0);
-
-    codes_fill(lds, cr, a.need, t);
-    __syncthreads();
-
-    // ---- Q8_K(x) by workgroup 0
-    if (blockIdx.x == 0) {
-        for (int b = wv; b < a.dim / 256; b += 4)
-            q8k_block<true>(a.x + 256 * b, a.xq + 256 * b, a.xd + b, nullptr, a.err, lane);
-        drain_memory();
-        __syncthreads();
-        if (t == 0) add_relaxed(a.sync + kSyncX, 1);
-    }
-    if (gw < a.k && lane == 0) {   // every bad id is reported once
-        const int id = a.ids[gw];
-        if (id < 0 || id >= a.n_experts) atomicOr(a.err, kDevErrExpertId);
-    }
-
-    // ---- gate/up + SwiGLU
-    if (gn > 0) {
-        wait_geq(a.sync + kSyncX, 1, a.err);
-        Act<PG> A;
-        load_act<LG, PG, true>(A, a.xq, a.xd, lG);
-        for (int first = 0; first < gn; first += UG) {
-            if (first > 0) g_load(first);
-#pragma unroll
-            for (int u = 0; u < UG; ++u)
-                if (first + u < gn) {
-                    int i, row;
-                    const ExpertDesc* D;
-                    if (!g_slot(g0 + first + u, i, row, D)) continue;
-                    const int type = D->m[0].type;
-                    const float g = dot_raw<LG, PG, false>(rg[u], type, row, D->m[0].nb, lG, A, lds, nullptr, true);
-                    const float v = dot_raw<LG, PG, false>(ru[u], type, row, D->m[1].nb, lG, A, lds, nullptr, true);
-                    if (lG == 0) coh_stf(a.h + size_t(i) * a.ff + row, silu_mul(g, v, a.lim));
-                }
-        }
-        // publish rows per pick (a wave's range spans at most a few picks)
-        drain_memory();
-        if (lane == 0) {
-            int s = g0;
-            while (s < g0 + gn) {
-                const int i = s / sppG;
-                const int end = min(g0 + gn, (i + 1) * sppG);
-                add_relaxed(a.sync + kSyncGu + i, uint32_t((end - s) * RG));
-                s = end;
-            }
-        }
-    }
-
-    // ---- Q8_K(h): one block per wave for the first k*ff/256 waves
-    const int hblocks = a.ff / 256;
-    if (gw < a.k * hblocks) {
-        const int i = gw / hblocks, b = gw - i * hblocks;
-        wait_geq(a.sync + kSyncGu + i, uint32_t(a.ff), a.err);
-        const size_t o = size_t(i) * a.ff + 256 * b;
-        q8k_block<true>(a.h + o, a.hq + o, a.hd + size_t(i) * hblocks + b, nullptr, a.err, lane);
-        drain_memory();
-        if (lane == 0) add_relaxed(a.sync + kSyncHq + i, 1);
-    }
-
-    // ---- down
-    if (dn > 0) {
-        Act<PD> B;
-        int cur = -1;
-        for (int first = 0; first < dn; first += UD) {
-            if (first > 0) d_load(first);
-#pragma unroll
-            for (int u = 0; u < UD; ++u)
-                if (first + u < dn) {
-                    int i, row;
-                    const ExpertDesc* D;
-                    if (!d_slot(d0 + first + u, i, row, D)) continue;
-                    if (i != cur) {
-                        wait_geq(a.sync + kSyncHq + i, uint32_t(hblocks), a.err);
-                        load_act<LD, PD, true>(B, a.hq + size_t(i) * a.ff, a.hd + size_t(i) * hblocks, lD);
-                        cur = i;
-                    }
-                    const float v =
-                        dot_raw<LD, PD, false>(rd[u], D->m[2].type, row, D->m[2].nb, lD, B, lds, nullptr, true);
-                    if (lD == 0) coh_stf(a.y + size_t(i) * a.dim + row, v);
-                }
-        }
-        // publish per 64-row chunk; the wave completing a chunk combines it
-        drain_memory();
-        for (int u = 0; u < dn; ++u) {
-            const int s = d0 + u, i = s / sppD, row0 = (s - i * sppD) * RD, c = row0 >> 6;
-            uint32_t old = 0;
-            if (lane == 0) old = add_relaxed(a.sync + kSyncChunk + c, uint32_t(RD));
-            old = __shfl(old, 0);
-            if (old + uint32_t(RD) == uint32_t(a.k * 64)) {
-                const int r = 64 * c + lane;
-                if (a.out) a.out[r] = combine_one<true>(a.ids, a.w, a.k, a.y, a.dim, r, a.shared);
-            }
-        }
-    }
-
-    // ---- exit: the last workgroup zeroes the counters for the next launch
-    __syncthreads();
-    if (t == 0) {
-        const uint32_t old = add_relaxed(a.sync + kSyncExit, 1);
-        if (old == gridDim.x - 1) {   // every other workgroup has finished with the counters
-            const int n = kSyncChunk + a.dim / 64;
-            for (int j = 0; j < n; ++j) __hip_atomic_store(a.sync + j, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        }
     }
 }
 
@@ -718,41 +482,6 @@ hipError_t launch_generate(uint8_t* base, int type, int n, int k, uint64_t seed,
     hipLaunchKernelGGL(generate_kernel, dim3(unsigned(grid)), dim3(256), 0, s, base, type, nblocks, L.off[1], L.off[2],
                        key);
     return hipGetLastError();
-}
-
-// One cooperative launch of the fused layer: the grid is every workgroup the
-// device holds at once (occupancy x CUs), so all of them are resident.
-template <int LG, int PG, int UG, int LD, int PD, int UD>
-static hipError_t fused_launch(const LayerArgs& args, int cus, hipStream_t s) {
-    auto kern = layer_kernel<LG, PG, UG, LD, PD, UD>;
-    const size_t lds = size_t(lds_bytes_for(args.need));
-    int per_cu = 0;
-    hipError_t e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kern, 256, lds);
-    if (e != hipSuccess) return e;
-    if (per_cu < 1) return hipErrorNotSupported;
-    LayerArgs a = args;
-    const int grid = cus * per_cu, waves = grid * 4;
-    const int SG = a.k * (a.ff / (64 / LG)), SD = a.k * (a.dim / (64 / LD));
-    a.per_g = (SG + waves - 1) / waves;
-    a.per_d = (SD + waves - 1) / waves;
-    if (a.k * (a.ff / 256) > waves || a.k < 1 || a.k > 16 || a.dim / 64 + 34 > kSyncWords) return hipErrorNotSupported;
-    void* params[] = {&a};
-    e = hipLaunchCooperativeKernel(reinterpret_cast<const void*>(kern), dim3(grid), dim3(256), params,
-                                   static_cast<unsigned int>(lds), s);
-    return e;
-}
-
-hipError_t launch_layer_fused(const LayerArgs& args, int type_mask, int cus, hipStream_t s) {
-    LayerArgs a = args;
-    a.need = need_of(type_mask);
-    int lg, pg, ld, pd;
-    if (!row_shape(a.dim, lg, pg) || !row_shape(a.ff, ld, pd)) return hipErrorNotSupported;
-    if (lg == 64 && pg == 1 && ld == 16 && pd == 3) return fused_launch<64, 1, 4, 16, 3, 1>(a, cus, s);   // 4096 x 3072
-    if (lg == 4 && pg == 1 && ld == 4 && pd == 1) return fused_launch<4, 1, 4, 4, 1, 2>(a, cus, s);       // 256 x 256
-    if (lg == 8 && pg == 1 && ld == 4 && pd == 1) return fused_launch<8, 1, 4, 4, 1, 2>(a, cus, s);       // 512 x 256
-    if (lg == 4 && pg == 1 && ld == 4 && pd == 3) return fused_launch<4, 1, 4, 4, 3, 2>(a, cus, s);       // 256 x 768
-    if (lg == 16 && pg == 1 && ld == 8 && pd == 1) return fused_launch<16, 1, 4, 8, 1, 2>(a, cus, s);     // 1024 x 512
-    return hipErrorNotSupported;
 }
 
 }  // namespace xl::dev

@@ -671,9 +671,6 @@ __global__ __launch_bounds__(NW * 64, 1) void stream_kernel(Layer3Args a) {
     }
     const uint32_t parity = __builtin_amdgcn_readfirstlane(sm.parity);   // uniform: keeps buffer bases scalar
     float* const hcur = a.hbuf + size_t(parity) * kHBufWords;
-    // The unit kernel (xl_unit.hip) shares the launch count: its partial counters
-    // of the other parity are cleared for the next launch, as it does itself.
-    if (a.ucnt && blockIdx.x == 0 && t < 8) coh_st32(a.ucnt + size_t(parity ^ 1u) * 256 + 32 * t, 0u);
     // Arrival: the last workgroup to arrive advances the launch count at its end.
     uint32_t arrived = 0;
     if (t == 0) arrived = __hip_atomic_fetch_add(ctl + 1, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);

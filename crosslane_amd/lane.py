@@ -111,6 +111,7 @@ _SIGNATURES = {
     "xl_profile_end": (_I32, [_P, _f32p, _I32, C.POINTER(_I32), C.POINTER(_I32), C.c_char_p, _I32, _ErrP]),
     "xl_profile_timeline": (_I32, [_P, _u64p, _I32, C.POINTER(_I32), _ErrP]),
     "xl_debug_set_launch_count": (_I32, [_P, C.c_uint32, _ErrP]),
+    "xl_debug_launch_counts": (_I32, [_P, np.ctypeslib.ndpointer(np.int64, flags="C_CONTIGUOUS"), _I32, _ErrP]),
     "xl_planar_bytes": (C.c_uint64, [_I32, _I32, _I32]),
     "xl_repack": (_I32, [_I32, _I32, _I32, _P, _P]),
     "xl_restore": (_I32, [_I32, _I32, _I32, _P, _P]),
@@ -433,6 +434,15 @@ class Lane:
         """Sets the single-launch kernels' launch counters (epoch / parity) as if
         `launches` launches had run: for testing their wrap at 2^32."""
         self._call("xl_debug_set_launch_count", C.c_uint32(launches & 0xFFFFFFFF))
+
+    LAUNCH_KINDS = ("stream", "alltypes", "separate", "routed", "prenorm")   # XL_LAUNCH_* order
+
+    def launch_counts(self) -> dict:
+        """Layer calls so far by how they ran ({kind: count}, XL_LAUNCH_* kinds):
+        which launch served a call (e.g. a routed call routed inside its launch)."""
+        out = np.zeros(len(self.LAUNCH_KINDS), np.int64)
+        self._call("xl_debug_launch_counts", out, out.size)
+        return dict(zip(self.LAUNCH_KINDS, (int(v) for v in out)))
 
     def quantize_q8k_async(self, x, rows: int, k: int, q8k_out, stream=None) -> None:
         self._call("xl_quantize_q8k_async", _ptr(x), rows, k, _ptr(q8k_out), None if stream is None else int(stream))

@@ -190,7 +190,7 @@ int32_t xl_grouped_forward_async(xl_context* ctx, int32_t layer, int32_t T, int3
  *        fixed-order combine read it (so that out can be checked bit for bit
  *        against the combine of these rows);
  * kernel_out (host, may be null): 1 the streaming kernel ran, 3 the all-types
- * kernel, 5 the unit kernel. Any of q8x, q8h, h, ints, y may be null (not all).
+ * kernel. Any of q8x, q8h, h, ints, y may be null (not all).
  * XL_E_ARG when the
  * layer does not run as a single launch. A diagnostic aid (no counterpart in
  * the reference beyond its probe); it runs the traced kernel instances. */
@@ -370,8 +370,24 @@ int32_t xl_profile_timeline(xl_context* ctx, uint64_t* out, int32_t max_words, i
  * kernel's epoch and the streaming kernel's launch count, whose parity picks
  * its h exchange buffer) to `launches`, as if that many launches had run. A
  * diagnostic aid for testing the counters' wrap at 2^32; it has no
- * counterpart in the reference. */
+ * counterpart in the reference. The exchange buffers are reset as at
+ * xl_open (h words to the sentinel, tags to zero), so that any count, of
+ * either parity and any epoch, leaves the next launch correct. */
 int32_t xl_debug_set_launch_count(xl_context* ctx, uint32_t launches, xl_error* err);
+
+/* Layer calls made on the context so far, by how they ran: counts[i] for
+ * i < n (kinds past XL_LAUNCH_KINDS read 0). A diagnostic aid (no counterpart
+ * in the reference): it shows which launch served a call, e.g. that a routed
+ * or pre-normed call ran as one launch rather than as its two-call fallback. */
+enum {
+    XL_LAUNCH_STREAM = 0,     /* xl_layer_* calls served by the streaming kernel */
+    XL_LAUNCH_ALLTYPES = 1,   /* ... by the all-types single launch */
+    XL_LAUNCH_SEPARATE = 2,   /* ... by separate launches */
+    XL_LAUNCH_ROUTED = 3,     /* routed layer calls that routed inside the streaming launch */
+    XL_LAUNCH_PRENORM = 4,    /* pre-normed layer calls that normalized inside the streaming launch */
+    XL_LAUNCH_KINDS = 5
+};
+int32_t xl_debug_launch_counts(xl_context* ctx, int64_t* counts, int32_t n, xl_error* err);
 
 /* ---- host utilities (no device needed) ------------------------------------ */
 uint64_t xl_planar_bytes(int32_t type, int32_t n, int32_t k);

@@ -12,13 +12,20 @@ as the device holds it, as the reference's probe feeds the device's own h,
 warm/expert_check.cpp:86-88); every carried hidden bit-identical to the
 oracle's norm of the device's layer output; and the whole pass bit-identical
 run to run (warm/hip_batch_check.cpp:28-110 repeats its batches the same way).
-Together these pin every step of the pass. The final hidden against the
-oracle's own 40-layer chain from the same input is reported, not asserted: this
-synthetic map amplifies rounding-level differences once a Q8_K rounding flips
-(two oracle chains whose norms differ only in the last bit agree to 2.5e-7
-through layer 31 and differ by 0.3 at layer 40), so an end-to-end bar would
-test the seed, not the kernels. A small E per layer keeps the oracle's work
-small; the kernels see the full-size matrices.
+Together these pin every step of the pass. The final hidden is also held to
+the oracle's own 40-layer chain from the same input, within max relative error
+1e-3 (the north star's end-to-end bar), at the committed seeds: both sides are
+deterministic, so the figure is a fixed property of the code. Its margin is a
+property of the seed as well: while every Q8_K byte of the pass agrees, the two
+chains differ by float rounding only (~1e-7); a Q8_K rounding flip (an input
+within an ulp of a quantization boundary, ~1 % of layers) is amplified by this
+synthetic random map (two oracle chains whose norms differ only in the last bit
+agree to 2.5e-7 through layer 31 and differ by 0.3 at layer 40).
+
+test_chain_40_layers uses 8 experts per layer (small oracle work, full-size
+matrices); test_chain_full_bank runs the pass over config 3's whole bank, 40 x
+384 experts (~138 GB resident), the oracle regenerating only the 240 picked
+experts.
 """
 from __future__ import annotations
 
@@ -115,9 +122,10 @@ def test_chain_40_layers(chain, orc):
         assert r < TOL, (l, r)
         assert np.array_equal(hs[l + 1].view(np.uint32), carry(orc, ys[l]).view(np.uint32)), l
         e2e = carry(orc, orc.combine(ids[l], w[l], np.stack(rows_e2e)))
-    # The oracle's own 40-layer chain from the same x0 (reported: see the module note)
+    # The oracle's own 40-layer chain from the same x0 (see the module note)
     r_e2e = max_rel(hs[L], e2e)
     step(f"chain: worst per-layer max_rel {worst:.3e}; end-to-end final hidden max_rel {r_e2e:.3e}")
+    assert r_e2e < TOL, r_e2e
 
 
 def run_pass_prenormed(lane, ids, w, x0):
@@ -148,6 +156,53 @@ def test_chain_prenormed_layers_match(chain):
     step("chain pass, separate norms")
     hs, ys = run_pass(lane, ids, w, x0)
     step("chain pass, norms inside the layer calls")
+    before = lane.launch_counts()["prenorm"]
     hs2, ys2 = run_pass_prenormed(lane, ids, w, x0)
+    assert lane.launch_counts()["prenorm"] - before == L - 1   # every carried layer normalized in its launch
     assert np.array_equal(ys.view(np.uint32), ys2.view(np.uint32))
     assert np.array_equal(hs.view(np.uint32), hs2.view(np.uint32))
+
+
+def test_chain_full_bank(orc):
+    # Config 3 at full size: 40 layers x 384 experts, whole-expert types drawn 17 %
+    # IQ2_XS / 19 % IQ2_XXS / 64 % IQ1_M, top-6 of a softmax over N(0,1) logits
+    # per layer, the hidden carried inside each layer's launch (the bench's pass).
+    EF, seed = 384, 0xC3F0
+    rng = np.random.default_rng(seed)
+    t = rng.choice([v for v, _ in MIX], size=(L, EF), p=[p for _, p in MIX]).astype(np.int32)
+    types = np.repeat(t[..., None], 3, axis=-1)
+    ids = np.zeros((L, K), np.int32)
+    w = np.zeros((L, K), np.float32)
+    for l in range(L):
+        ids[l], w[l] = route(rng.standard_normal(EF).astype(np.float32), K)
+    x0 = rng.standard_normal(DIM).astype(np.float32)
+    step(f"full bank: {L} x {EF} experts")
+    lane = xl.Lane(DIM, FF, L, EF, types, max_picks=8)
+    try:
+        lane.generate(seed)
+        step("full bank: pass 1")
+        hs, ys = run_pass_prenormed(lane, ids, w, x0)
+        step("full bank: pass 2")
+        hs2, ys2 = run_pass_prenormed(lane, ids, w, x0)
+        assert np.array_equal(ys.view(np.uint32), ys2.view(np.uint32))
+        assert np.array_equal(hs.view(np.uint32), hs2.view(np.uint32))
+        assert np.all(np.isfinite(hs))
+    finally:
+        lane.close()
+    step("full bank: oracle over the 240 picked experts")
+    worst, e2e = 0.0, x0.copy()
+    for l in range(L):
+        rows_dev, rows_e2e = [], []
+        for e in ids[l]:
+            t3 = tuple(int(v) for v in types[l, e])
+            mats = orc.gen_expert(t3, seed, l, int(e), DIM, FF)
+            rows_dev.append(orc.expert(t3, *mats, DIM, FF, hs[l]))
+            rows_e2e.append(orc.expert(t3, *mats, DIM, FF, e2e))
+        r = max_rel(ys[l], orc.combine(ids[l], w[l], np.stack(rows_dev)))
+        worst = max(worst, r)
+        assert r < TOL, (l, r)
+        assert np.array_equal(hs[l + 1].view(np.uint32), carry(orc, ys[l]).view(np.uint32)), l
+        e2e = carry(orc, orc.combine(ids[l], w[l], np.stack(rows_e2e)))
+    r_e2e = max_rel(hs[L], e2e)
+    step(f"full bank: worst per-layer max_rel {worst:.3e}; end-to-end final hidden max_rel {r_e2e:.3e}")
+    assert r_e2e < TOL, r_e2e

@@ -83,7 +83,6 @@ KERNEL_CASES = [
     ("1", 4096, 3072, 12, 6, "iq1", 1),
     ("1", 4096, 3072, 12, 6, "mixed", 1),
     ("1", 1024, 512, 8, 8, "mixed", 1),
-    ("5", 4096, 3072, 12, 6, "iq2", 5),
     ("3", 4096, 3072, 12, 6, "mixed", 3),
     ("3", 1024, 512, 8, 5, "iq1", 3),
 ]

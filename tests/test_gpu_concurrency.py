@@ -38,7 +38,7 @@ def oracle_layer(orc, sig, ids, w, x):
     return orc.combine(ids, w, np.stack(rows))
 
 
-@pytest.mark.parametrize("path,sig", [("5", (16, 16, 17)), ("4", (16, 16, 17)), ("3", (16, 16, 17)),
+@pytest.mark.parametrize("path,sig", [("4", (16, 16, 17)), ("4", (29, 29, 29)), ("3", (16, 16, 17)),
                                       ("3", (29, 29, 29))])
 def test_two_streams_one_context(orc, monkeypatch, path, sig):
     monkeypatch.setenv("XL_LAYER_PATH", path)
@@ -67,20 +67,26 @@ def test_two_streams_one_context(orc, monkeypatch, path, sig):
         lane.close()
 
 
-@pytest.mark.parametrize("path", ["5", "4", "3"])
-def test_launch_counter_wrap(orc, monkeypatch, path):
+@pytest.mark.parametrize("path", ["4", "3"])
+@pytest.mark.parametrize("start", [0xFFFFFFFD, 0xFFFFFFFE, 1])
+def test_launch_counter_wrap(orc, monkeypatch, path, start):
+    # The counters set to either parity near the wrap, and set back to a count
+    # whose epochs earlier launches already used (start 1 after five launches):
+    # every later launch must still compute its own call, bit for bit.
     monkeypatch.setenv("XL_LAYER_PATH", path)
-    step(f"counter wrap: XL_LAYER_PATH={path}")
+    step(f"counter wrap: XL_LAYER_PATH={path} start={start:#x}")
     sig = (16, 16, 17)
     lane = xl.Lane(DIM, FF, 1, E, types_map(1, E, sig[0], sig[2]), max_picks=8)
     try:
         lane.generate(SEED)
-        ids, w, x = routes(5, SEED + 7)
-        want = [lane.layer_forward(0, ids[i], w[i], x[i]) for i in range(5)]   # counters far from the wrap
-        lane.debug_set_launch_count(0xFFFFFFFD)
-        for i in range(5):   # launch counts 0xFFFFFFFE, 0xFFFFFFFF, then over the wrap
+        ids, w, x = routes(6, SEED + 7)
+        want = [lane.layer_forward(0, ids[i], w[i], x[i]) for i in range(6)]   # counters far from the wrap
+        lane.debug_set_launch_count(start)
+        for i in (5, 4, 3, 2, 1, 0):   # other inputs than the last launches: stale words would show
             got = lane.layer_forward(0, ids[i], w[i], x[i])
             assert np.array_equal(got.view(np.uint32), want[i].view(np.uint32)), i
         assert max_rel(want[4], oracle_layer(orc, sig, ids[4], w[4], x[4])) < TOL
+        counts = lane.launch_counts()
+        assert counts["stream" if path == "4" else "alltypes"] == 12, counts
     finally:
         lane.close()

@@ -206,12 +206,13 @@ def test_host_rejects_bad_routes(layer_lane):
 
 
 @pytest.mark.parametrize("dim,ff,gu,dn,path", [(256, 256, 16, 16, "1"), (1024, 512, 16, 17, "1"),
-                                               (4096, 3072, 16, 17, "1"), (4096, 3072, 16, 17, "5")])
+                                               (4096, 3072, 16, 17, "1"), (4096, 3072, 29, 29, "1"),
+                                               (4096, 3072, 16, 17, "3")])
 def test_device_rejects_bad_id_and_poisons(monkeypatch, dim, ff, gu, dn, path):
     # An out-of-range id reaches the kernels only through the device path; the
     # kernels bounds-check it, skip the pick and raise the error flag (the
-    # second and third cases run the streaming kernel, the last the unit kernel,
-    # whose readers must still finish).
+    # second to fourth cases run the streaming kernel, whose readers must still
+    # finish; the last the all-types kernel).
     monkeypatch.setenv("XL_LAYER_PATH", path)
     step(f"device bad id dim={dim} ff={ff} types=({gu},{dn}) path={path}")
     lane = xl.Lane(dim, ff, 1, 4, types_map(1, 4, gu, dn), max_picks=2)
@@ -278,8 +279,8 @@ def test_layer_paths_agree(orc, dim, ff, sig, monkeypatch):
     else:
         types = types_map(1, E, sig[0], sig[2])
     lanes = {}
-    extra = ("4", "5") if (dim, ff, sig) == (4096, 3072, (16, 16, 17)) else ()
-    for path in ("1", "3", "0", "2") + extra:
+    extra = ("4",) if (dim, ff, sig) == (4096, 3072, (16, 16, 17)) else ()
+    for path in ("1", "3", "0") + extra:
         monkeypatch.setenv("XL_LAYER_PATH", path)
         lanes[path] = xl.Lane(dim, ff, 1, E, types, max_picks=8)
         lanes[path].generate(seed=77)
@@ -343,33 +344,6 @@ def test_streaming_kernel_pick_counts(orc, kind, dim, ff, k, monkeypatch):
             for e in ids:
                 sig = tuple(int(v) for v in types[0, e])
                 rows.append(orc.expert(sig, *orc.gen_expert(sig, 91, 0, int(e), dim, ff), dim, ff, x))
-            want = orc.combine(ids, w, np.stack(rows), shared)
-            got = lane.layer_forward(0, ids, w, x, shared)
-            again = lane.layer_forward(0, ids, w, x, shared)
-            assert np.array_equal(got.view(np.uint32), again.view(np.uint32)), trial
-            assert max_rel(got, want) < TOL, (trial, max_rel(got, want))
-    finally:
-        lane.close()
-
-
-@pytest.mark.parametrize("k", [1, 2, 3, 4, 5, 6, 7, 8])
-def test_unit_kernel_pick_counts(orc, k, monkeypatch):
-    # XL_LAYER_PATH=5 runs the unit kernel or fails: 1 to 8 picks give groups of
-    # 2 to 12 units (some groups one fewer, some none) at 4096 x 3072; each must
-    # match the oracle and repeat bit for bit.
-    dim, ff, E = 4096, 3072, 24
-    step(f"unit kernel k={k}")
-    rng = np.random.default_rng(100 + k)
-    monkeypatch.setenv("XL_LAYER_PATH", "5")
-    lane = xl.Lane(dim, ff, 1, E, types_map(1, E, 16, 17), max_picks=16)
-    try:
-        lane.generate(seed=93)
-        for trial in range(2):
-            ids, w = route(rng.standard_normal(E).astype(np.float32), k)
-            x = rng.standard_normal(dim).astype(np.float32)
-            shared = rng.standard_normal(dim).astype(np.float32) if trial else None
-            rows = [orc.expert((16, 16, 17), *orc.gen_expert((16, 16, 17), 93, 0, int(e), dim, ff), dim, ff, x)
-                    for e in ids]
             want = orc.combine(ids, w, np.stack(rows), shared)
             got = lane.layer_forward(0, ids, w, x, shared)
             again = lane.layer_forward(0, ids, w, x, shared)

@@ -65,6 +65,8 @@ def test_prenorm_layer_matches_norm_then_layer(orc, kind, dim, ff, k):
             want_x = orc.hc_pre_norm(h.reshape(1, 1, dim), mix.reshape(1, 8), nw)[0]
             assert np.array_equal(bits(x1), want_x.view(np.uint32)), trial
             assert np.all(np.isfinite(y1.cpu().numpy()))
+            # the pre-normed call normalized inside its one launch (not the two-call fallback)
+            assert lane.launch_counts()["prenorm"] == trial + 1
     finally:
         lane.close()
 

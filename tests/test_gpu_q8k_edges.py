@@ -1,0 +1,163 @@
+"""The reference's Q8_K edge blocks through every kernel that computes the path.
+
+x is built from the 13 golden blocks written from the reference's own
+quant_block (q8k_core.hpp:25-38; tests/golden: an all-zero block, .5 ties, an
+equal-magnitude tie of opposite signs, one-hot blocks, a subnormal largest
+magnitude, a 2.5e30 block), two crafted blocks whose largest magnitude sits
+just below and just above 127 / FLT_MAX (is = -127/mx overflows to -inf in the
+first, d = 1/is = -0), and one N(0,1) block. It is run through the parity
+trace of the streaming kernel (IQ2, IQ1_M and mixed-type instances, one and
+six picks), the all-types kernel and the grouped MFMA kernels (token rows),
+and the staged Q8_K(x) must equal the golden bytes (and the oracle's, for the
+crafted blocks) byte for byte: the bar the reference's probe applies to its
+working lane's own .q8k bytes (parity/hip_resident_check.cpp:91-127).
+
+The SwiGLU limit 7 (the model's own clamp, q8k_core.hpp:92-95) keeps h finite
+when a 2.5e30 block drives the gate rows to ~1e29; Q8_K(h) and every row's
+block integers are then checked as in test_gpu_trace.py, and the output
+against the oracle chain with the same limit.
+"""
+from __future__ import annotations
+
+import os
+
+import numpy as np
+import pytest
+
+import crosslane_amd as xl
+from tests.conftest import max_rel
+from tests.test_gpu_parity import TOL, dev, route, step
+from tests.test_gpu_trace import check_pick, layer_types, zeros
+
+pytestmark = pytest.mark.gpu
+torch = pytest.importorskip("torch")
+
+SEED = 0x0E09E
+LIM = 7.0
+DIM, FF, E = 4096, 3072, 12
+
+
+def edge_x(shift: int = 0):
+    """(x, expected Q8_K bytes per block): 16 blocks, the golden ones first
+    (rotated by `shift` blocks), bytes from the golden file where it has them."""
+    gold = np.load(os.path.join(os.path.dirname(__file__), "golden", "reference_vectors.npz"))
+    gx, gb = gold["q8k_x"], gold["q8k_bytes"]
+    rng = np.random.default_rng(99)
+    tiny = (rng.standard_normal(256) * 1e-39).astype(np.float32)
+    tiny[17] = 1.0e-38                      # largest magnitude, positive: is = -inf, d = -0
+    edge = (rng.standard_normal(256) * 1e-38).astype(np.float32)
+    edge[200] = -4.0e-37                    # just above 127 / FLT_MAX: is finite, huge
+    blocks = list(gx) + [tiny, edge, rng.standard_normal(256).astype(np.float32)]
+    want = list(gb) + [None, None, None]
+    order = [(i + shift) % 16 for i in range(16)]
+    return np.concatenate([blocks[i] for i in order]).astype(np.float32), [want[i] for i in order]
+
+
+def check_q8x(orc, x, want_gold, q8x, tag):
+    want = orc.quantize(x).view(np.uint8).reshape(16, 292)
+    q8x = q8x.reshape(16, 292)
+    for b in range(16):
+        if want_gold[b] is not None:
+            assert np.array_equal(want[b], want_gold[b]), f"{tag}: oracle vs golden, block {b}"
+        assert np.array_equal(q8x[b], want[b]), f"{tag}: Q8_K(x) block {b}"
+    return want.reshape(-1).view(orc.quantize(x).dtype)
+
+
+def test_crafted_blocks_hit_the_overflow():
+    # the crafted blocks' -127 / mx really overflows (first) and stays finite (second)
+    x, _ = edge_x()
+    with np.errstate(over="ignore"):
+        assert np.isinf(np.float32(-127.0) / np.float32(1.0e-38))
+        assert np.isfinite(np.float32(-127.0) / np.float32(-4.0e-37))
+    assert np.max(np.abs(x[13 * 256:14 * 256])) == np.float32(1.0e-38)
+
+
+LAYER_CASES = [
+    # (XL_LAYER_PATH, layer type map kind, k, expected kernel)
+    ("4", "iq2", 6, 1),     # streaming kernel, IQ2 instance (config 1)
+    ("4", "iq2", 1, 1),     # its one-pick instance (config 0)
+    ("4", "iq1", 6, 1),     # IQ1_M instance (config 2)
+    ("4", "mixed", 6, 1),   # mixed instance (config 3)
+    ("3", "iq2", 6, 3),     # all-types kernel
+    ("3", "iq1", 4, 3),
+    ("3", "mixed", 6, 3),
+]
+
+
+@pytest.mark.parametrize("path,kind,k,kernel", LAYER_CASES)
+def test_layer_kernels_stage_golden_q8k(orc, monkeypatch, path, kind, k, kernel):
+    monkeypatch.setenv("XL_LAYER_PATH", path)
+    step(f"Q8_K edge blocks: layer path={path} {kind} k={k}")
+    types = layer_types(kind, E)
+    lane = xl.Lane(DIM, FF, 1, E, types, max_picks=8, swiglu_limit=LIM)
+    try:
+        lane.generate(SEED)
+        rng = np.random.default_rng(k + len(kind))
+        ids, w = route(rng.standard_normal(E).astype(np.float32), k)
+        x, want_gold = edge_x(shift=k)
+        nbx, nbh = DIM // 256, FF // 256
+        rec = 2 * FF * nbx + DIM * nbh
+        out = zeros(DIM, torch.float32)
+        q8x = zeros(nbx * 292, torch.uint8)
+        q8h = zeros(k * nbh * 292, torch.uint8)
+        h = zeros(k * FF, torch.float32)
+        ints = zeros(k * rec, torch.int32)
+        torch.cuda.synchronize()
+        ran = lane.layer_trace_async(0, dev(ids), dev(w), dev(x), out, q8x, q8h, h, ints)
+        lane.sync()
+        assert ran == kernel
+        want_q8x = check_q8x(orc, x, want_gold, q8x.cpu().numpy(), f"path {path} {kind} k={k}")
+        h, q8h, ints = h.cpu().numpy().reshape(k, FF), q8h.cpu().numpy().reshape(k, -1), ints.cpu().numpy().reshape(k, rec)
+        assert np.all(np.isfinite(h))
+        rows = []
+        for i, e in enumerate(ids):
+            sig = tuple(int(v) for v in types[0, e])
+            mats = orc.gen_expert(sig, SEED, 0, int(e), DIM, FF)
+            check_pick(orc, sig, mats, DIM, FF, want_q8x, h[i], q8h[i], ints[i], f"pick {i} (expert {e}, {sig})")
+            rows.append(orc.expert(sig, *mats, DIM, FF, x, limit=LIM))
+        assert max_rel(out.cpu().numpy(), orc.combine(ids, w, np.stack(rows))) < TOL
+    finally:
+        lane.close()
+
+
+def test_grouped_kernels_stage_golden_q8k(orc, monkeypatch):
+    monkeypatch.setenv("XL_GROUPED_PATH", "2")
+    T, k = 4, 6
+    step(f"Q8_K edge blocks: grouped T={T} k={k}")
+    types = layer_types("iq2", E)
+    lane = xl.Lane(DIM, FF, 1, E, types, max_picks=8, max_tokens=T, swiglu_limit=LIM)
+    try:
+        lane.generate(SEED)
+        rng = np.random.default_rng(5)
+        ids = np.stack([rng.choice(E, k, replace=False) for _ in range(T)]).astype(np.int32)
+        w = (rng.random((T, k)) + 0.1).astype(np.float32)
+        xs = [edge_x(shift=3 * t) for t in range(T)]
+        x = np.stack([v for v, _ in xs])
+        nbx, nbh, P = DIM // 256, FF // 256, T * k
+        rec = 2 * FF * nbx + DIM * nbh
+        out = zeros((T, DIM), torch.float32)
+        q8x = zeros(T * nbx * 292, torch.uint8)
+        q8h = zeros(P * nbh * 292, torch.uint8)
+        h = zeros(P * FF, torch.float32)
+        ints = zeros(P * rec, torch.int32)
+        torch.cuda.synchronize()
+        lane.grouped_trace_async(0, dev(ids), dev(w), dev(x), out, q8x, q8h, h, ints)
+        lane.sync()
+        q8x = q8x.cpu().numpy().reshape(T, -1)
+        h, q8h, ints = h.cpu().numpy().reshape(P, FF), q8h.cpu().numpy().reshape(P, -1), ints.cpu().numpy().reshape(P, rec)
+        got = out.cpu().numpy()
+        mats = {}
+        for t in range(T):
+            want_q8x = check_q8x(orc, x[t], xs[t][1], q8x[t], f"token {t}")
+            rows = []
+            for i, e in enumerate(ids[t]):
+                if int(e) not in mats:
+                    mats[int(e)] = orc.gen_expert((16, 16, 17), SEED, 0, int(e), DIM, FF)
+                p = t * k + i
+                if t < 2:   # two tokens in full, the others by their outputs
+                    check_pick(orc, (16, 16, 17), mats[int(e)], DIM, FF, want_q8x, h[p], q8h[p], ints[p],
+                               f"token {t} pick {i} (expert {e})")
+                rows.append(orc.expert((16, 16, 17), *mats[int(e)], DIM, FF, x[t], limit=LIM))
+            assert max_rel(got[t], orc.combine(ids[t], w[t], np.stack(rows))) < TOL, t
+    finally:
+        lane.close()

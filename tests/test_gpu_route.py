@@ -151,5 +151,10 @@ def test_routed_one_launch_matches_router_then_layer(dim, ff, E, k, kind):
             lane.layer_forward_async(0, ids[t], w[t], d_x[t], two[t])
         lane.sync()
         assert np.array_equal(one.cpu().numpy().view(np.uint32), two.cpu().numpy().view(np.uint32))
+        # the routed calls routed inside their launch where one exists (E <= 512),
+        # so the comparison above is the one launch against the two calls
+        counts = lane.launch_counts()
+        assert counts["routed"] == (T if E <= 512 else 0), counts
+        assert counts["stream"] == (T if E <= 512 else 2 * T), counts
     finally:
         lane.close()

@@ -4,8 +4,8 @@ The north star's exact bars (Q8_K activation bytes and per-block int32
 partials) are checked here on what the hot kernels themselves stage and form,
 through the parity trace (xl_layer_trace_async, xl_grouped_trace_async): the
 streaming kernel with its IQ2, IQ1_M and mixed-type instances (configs 0 to
-3), the unit kernel, the all-types kernel with its IQ2, IQ1_M and mixed-type
-instances, and the grouped MFMA kernels
+3), the all-types kernel with its IQ2, IQ1_M and mixed-type instances, and the
+grouped MFMA kernels
 (config 4). For each launch:
 
 * Q8_K(x) as staged: the 292-byte blocks equal the oracle's quant_block of x
@@ -59,10 +59,6 @@ LAYER_CASES = [
     ("1", 4096, 3072, 12, 6, "iq2", 1),     # config 1: the streaming kernel
     ("1", 4096, 3072, 12, 1, "iq2", 1),     # config 0: one pick (1-2 pick instance)
     ("4", 4096, 3072, 12, 3, "iq2", 1),     # 3-4 pick instance
-    ("5", 4096, 3072, 12, 6, "iq2", 5),     # the unit kernel
-    ("5", 4096, 3072, 12, 1, "iq2", 5),
-    ("5", 4096, 3072, 12, 3, "iq2", 5),
-    ("5", 4096, 3072, 12, 8, "iq2", 5),
     ("1", 1024, 512, 8, 6, "iq2", 1),
     ("1", 4096, 3072, 12, 6, "iq1", 1),     # config 2: the streaming kernel's IQ1_M instance
     ("1", 4096, 3072, 12, 6, "mixed", 1),   # config 3: its mixed instance (descriptors)

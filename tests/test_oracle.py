@@ -64,6 +64,30 @@ def test_q8k_closed_forms(orc):
     assert b["qs"][5] == -127 and b["qs"][9] == 127
 
 
+def test_q8k_overflowing_inverse_scale(orc):
+    # Largest magnitude below 127 / FLT_MAX: is = -127/mx overflows to -inf (mx > 0)
+    # or +inf (mx < 0); nearest(+-inf) = -2^22 and nearest(NaN) = 0 both keep
+    # the int8 byte 0 (q8k_core.hpp:25-29, 34), and d = 1/is = -0 / +0.
+    for mx, dbits in [(1.0e-38, 0x80000000), (-1.0e-38, 0x00000000), (2.0e-39, 0x80000000)]:
+        x = np.zeros(256, np.float32)
+        x[::7] = np.float32(mx) * np.float32(0.25)
+        x[100] = np.float32(mx)
+        b = orc.quantize(x)[0]
+        assert not b["qs"].any() and not b["bsums"].any(), mx
+        assert np.float32(b["d"]).view(np.uint32) == dbits, mx
+    # just above the threshold: is finite, and the block quantizes as usual
+    x = np.zeros(256, np.float32); x[3] = np.float32(4.0e-37); x[4] = np.float32(-2.0e-37)
+    b = orc.quantize(x)[0]
+    assert b["qs"][3] == -127 and b["qs"][4] == 64 and np.isfinite(b["d"]) and b["d"] < 0
+
+
+def test_q8k_overflow_vs_reference(orc, ref, rng):
+    for mx in (1.0e-38, -1.0e-38, 3.0e-39, 3.7e-37, 3.8e-37):
+        x = (rng.standard_normal(256) * abs(mx) * 0.3).astype(np.float32)
+        x[int(rng.integers(256))] = np.float32(mx)
+        assert orc.quantize(x).tobytes() == ref.quantize(x).tobytes(), mx
+
+
 def test_q8k_vs_reference_random(orc, ref, rng):
     for scale in (1e-3, 1.0, 1e3):
         x = (rng.standard_normal(256 * 64) * scale).astype(np.float32)

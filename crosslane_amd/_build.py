@@ -15,8 +15,8 @@ CSRC = os.path.join(PKG, "csrc")
 LIB = os.path.join(PKG, "libcrosslane.so")
 OBJDIR = os.path.join(PKG, "_build")
 SOURCES = ["xl_kernels.hip", "xl_layer.hip", "xl_stream.hip", "xl_stream_iq1.hip", "xl_stream_mix.hip",
-           "xl_grouped.hip", "xl_per32.hip", "xl_hc.hip", "xl_noalloc.hip", "xl_api.cpp"]
-HEADERS = ["xl_format.hpp", "xl_rows.hpp", "xl_internal.hpp", "xl_dev.hpp", "xl_iq2.hpp", "xl_stream.hpp", "xl_codebooks.inc",
+           "xl_grouped.hip", "xl_per32.hip", "xl_hc.hip", "xl_exact.hip", "xl_noalloc.hip", "xl_api.cpp"]
+HEADERS = ["xl_format.hpp", "xl_rows.hpp", "xl_internal.hpp", "xl_dev.hpp", "xl_iq2.hpp", "xl_stream.hpp", "xl_refexp.hpp", "xl_codebooks.inc",
            "exports.map"]
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")

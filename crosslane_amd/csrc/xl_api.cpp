@@ -479,6 +479,26 @@ bool enqueue_layer(xl_context* ctx, int32_t layer, const int32_t* d_ids, const f
     return false;
 }
 
+// The layer in the reference CPU lane's float order (xl_exact.hip): Q8_K(x),
+// gate/up rows + SwiGLU, Q8_K(h), down rows, fixed-order combine; every float
+// as q8k_core.hpp:76-95 computes it. Separate launches on stream s.
+void enqueue_layer_exact(xl_context* ctx, int32_t layer, const int32_t* d_ids, const float* d_w, int32_t k,
+                         const float* d_x, const float* d_shared, float* d_out, hipStream_t s) {
+    const int dim = ctx->cfg.dim, ff = ctx->cfg.ff, E = ctx->cfg.n_experts;
+    const xl::ExpertDesc* descs = ctx->d_descs + size_t(layer) * E;
+    need(dim % 32 == 0 && ff % 32 == 0, XL_E_ARG, "exact rows: dim and ff must be multiples of 32");
+    hip_check(xl::dev::launch_q8k(d_x, dim / 256, ctx->xq, ctx->xd, nullptr, ctx->err_flag, s), "Q8_K(x) launch");
+    hip_check(xl::dev::launch_exact_rows(descs, d_ids, k, E, ff, dim, 0, ctx->xq, ctx->xd, ctx->tables, ctx->h,
+                                         ctx->cfg.swiglu_limit, ctx->err_flag, s),
+              "exact gate/up launch");
+    hip_check(xl::dev::launch_q8k(ctx->h, k * ff / 256, ctx->hq, ctx->hd, nullptr, ctx->err_flag, s), "Q8_K(h) launch");
+    hip_check(xl::dev::launch_exact_rows(descs, d_ids, k, E, dim, ff, 2, ctx->hq, ctx->hd, ctx->tables, ctx->y, 0.0f,
+                                         ctx->err_flag, s),
+              "exact down launch");
+    hip_check(xl::dev::launch_combine(d_ids, d_w, k, ctx->y, dim, d_shared, d_out, s), "combine launch");
+    ++ctx->launches[XL_LAUNCH_EXACT];
+}
+
 // A per32 matrix: planar IQ (xl_format.hpp) or raw dense ggml blocks.
 xl::MatRef per32_matrix(int type, const void* base, int n, int k) {
     need(reinterpret_cast<uintptr_t>(base) % 16 == 0, XL_E_ARG, "matrix not 16-byte aligned");
@@ -1276,6 +1296,20 @@ int32_t xl_layer_forward_async(xl_context* ctx, int32_t layer, const int32_t* d_
         Ordered ord(ctx, s);
         ord.carried_by_launch(enqueue_layer(ctx, layer, d_ids, d_w, k, d_x, d_shared_or_null, d_out, s, nullptr, nullptr,
                                             ord.stop()));
+    });
+}
+
+int32_t xl_layer_forward_exact_async(xl_context* ctx, int32_t layer, const int32_t* d_ids, const float* d_w,
+                                     int32_t k, const float* d_x, const float* d_shared_or_null, float* d_out,
+                                     void* stream, xl_error* err) {
+    return guarded(ctx, err, [&] {
+        ready(ctx, true);
+        check_layer(ctx, layer);
+        need(k >= 1 && k <= ctx->cfg.max_picks, XL_E_ARG, "pick count outside 1..max_picks");
+        need(d_ids && d_w && d_x && d_out, XL_E_ARG, "null device pointer");
+        hipStream_t s = pick_stream(ctx, stream);
+        Ordered ord(ctx, s);
+        enqueue_layer_exact(ctx, layer, d_ids, d_w, k, d_x, d_shared_or_null, d_out, s);
     });
 }
 

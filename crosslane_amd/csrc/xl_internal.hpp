@@ -166,6 +166,12 @@ hipError_t launch_stream_mix(const Layer3Args& args, int cus, hipStream_t s, hip
 // the shapes fit (dim, ff multiples of 128; n_experts <= kGroupMaxExperts).
 hipError_t launch_grouped(const GroupArgs& args, int cus, hipStream_t s);
 hipError_t launch_q8k(const float* x, int nblocks, int8_t* qs, float* d, uint8_t* std_out, int* err, hipStream_t s);
+// Rows in the reference CPU lane's float order (xl_exact.hip): role 0 gives
+// h = SwiGLU(gate . a, up . a) of every pick (out: k x rows), role 2 the down
+// rows against each pick's own activation (aq + pick * kdim; out: k x rows).
+hipError_t launch_exact_rows(const ExpertDesc* descs, const int32_t* ids, int k, int n_experts, int rows, int kdim,
+                             int role, const int8_t* aq, const float* ad, const uint64_t* tables, float* out, float lim,
+                             int* err, hipStream_t s);
 // `codes` is the compact codebook buffer (2-bit symbols, see xl_rows.hpp);
 // `target_wgs` is the workgroup count the row launches aim for.
 hipError_t launch_matvec(const MatRef& m, int n, int k, const int8_t* aq, const float* ad, const uint16_t* codes,

@@ -111,6 +111,7 @@ _SIGNATURES = {
     "xl_profile_end": (_I32, [_P, _f32p, _I32, C.POINTER(_I32), C.POINTER(_I32), C.c_char_p, _I32, _ErrP]),
     "xl_profile_timeline": (_I32, [_P, _u64p, _I32, C.POINTER(_I32), _ErrP]),
     "xl_debug_set_launch_count": (_I32, [_P, C.c_uint32, _ErrP]),
+    "xl_layer_forward_exact_async": (_I32, [_P, _I32, _P, _P, _I32, _P, _P, _P, _P, _ErrP]),
     "xl_debug_launch_counts": (_I32, [_P, np.ctypeslib.ndpointer(np.int64, flags="C_CONTIGUOUS"), _I32, _ErrP]),
     "xl_planar_bytes": (C.c_uint64, [_I32, _I32, _I32]),
     "xl_repack": (_I32, [_I32, _I32, _I32, _P, _P]),
@@ -351,6 +352,12 @@ class Lane:
         self._call("xl_layer_forward_async", layer, _ptr(ids), _ptr(w), int(ids.numel()), _ptr(x), _ptr(shared),
                    _ptr(out), None if stream is None else int(stream))
 
+    def layer_forward_exact_async(self, layer: int, ids, w, x, out, shared=None, stream=None) -> None:
+        """xl_layer_forward_async with every float in the reference CPU lane's
+        order (q8k_core.hpp:76-95): the reference's output bit for bit."""
+        self._call("xl_layer_forward_exact_async", layer, _ptr(ids), _ptr(w), int(ids.numel()), _ptr(x), _ptr(shared),
+                   _ptr(out), None if stream is None else int(stream))
+
     def layer_forward_prenorm_async(self, layer: int, ids, w, h, mix, norm_w, x, out, eps: float = 1e-6, shared=None,
                                     stream=None) -> None:
         """The layer on x = hc_pre_norm(h, mix, norm_w) of one token: h [H, dim]
@@ -435,7 +442,7 @@ class Lane:
         `launches` launches had run: for testing their wrap at 2^32."""
         self._call("xl_debug_set_launch_count", C.c_uint32(launches & 0xFFFFFFFF))
 
-    LAUNCH_KINDS = ("stream", "alltypes", "separate", "routed", "prenorm")   # XL_LAUNCH_* order
+    LAUNCH_KINDS = ("stream", "alltypes", "separate", "routed", "prenorm", "exact")   # XL_LAUNCH_* order
 
     def launch_counts(self) -> dict:
         """Layer calls so far by how they ran ({kind: count}, XL_LAUNCH_* kinds):

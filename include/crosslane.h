@@ -174,6 +174,19 @@ int32_t xl_grouped_forward_async(xl_context* ctx, int32_t layer, int32_t T, int3
                                  const float* d_w, const float* d_x, const float* d_shared_or_null, float* d_out,
                                  void* stream, xl_error* err);
 
+/* The layer call of xl_layer_forward_async with every float computed in the
+ * reference CPU lane's own order: q8k_core.hpp:76-91 (`dot_lane`, `hsum`,
+ * `dot`: one exact integer per AVX2 lane and block, one fmaf chain per lane
+ * over the blocks, the fixed hsum, IQ1_M's main and delta chains apart) and
+ * :92-95 (`swiglu`, whose expf is the host C library's, restated for the
+ * device), then the fixed-order combine of runtime.cpp:183-188. Its output
+ * equals the CPU reference's bit for bit, so that a pass over many layers can
+ * be held to the reference end to end. Separate launches, slower than
+ * xl_layer_forward_async; same contract and device pointers. */
+int32_t xl_layer_forward_exact_async(xl_context* ctx, int32_t layer, const int32_t* d_ids, const float* d_w,
+                                     int32_t k, const float* d_x, const float* d_shared_or_null, float* d_out,
+                                     void* stream, xl_error* err);
+
 /* ---- parity trace (device pointers) -------------------------------------------
  * The layer call's own intermediates, written by the kernel that computes it
  * (the reference's probe dumps its lane's Q8_K bytes the same way,
@@ -385,7 +398,8 @@ enum {
     XL_LAUNCH_SEPARATE = 2,   /* ... by separate launches */
     XL_LAUNCH_ROUTED = 3,     /* routed layer calls that routed inside the streaming launch */
     XL_LAUNCH_PRENORM = 4,    /* pre-normed layer calls that normalized inside the streaming launch */
-    XL_LAUNCH_KINDS = 5
+    XL_LAUNCH_EXACT = 5,      /* xl_layer_forward_exact_async calls */
+    XL_LAUNCH_KINDS = 6
 };
 int32_t xl_debug_launch_counts(xl_context* ctx, int64_t* counts, int32_t n, xl_error* err);
 

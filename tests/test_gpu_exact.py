@@ -1,0 +1,166 @@
+"""The layer in the reference CPU lane's own float order
+(xl_layer_forward_exact_async; xl_exact.hip, xl_refexp.hpp), held to the oracle
+bit for bit: q8k_core.hpp:76-91's eight lane chains and hsum, :92-95's SwiGLU
+with the host C library's expf, runtime.cpp:183-188's combine.
+
+With every float equal, a pass over many layers is equal too, whatever the
+synthetic map does with last-bit differences: the 40-layer pass of benchmark
+config 3 (8 experts per layer, and the whole 40 x 384 bank) ends on the
+oracle's own chain from the same input, bit for bit: the north star's
+end-to-end bar (within 1e-3 of the CPU reference) with no tolerance used.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+import crosslane_amd as xl
+from tests.test_gpu_chain import MIX, MIX1, carry, chain_routes, chain_types
+from tests.test_gpu_parity import dev, route, step
+
+pytestmark = pytest.mark.gpu
+torch = pytest.importorskip("torch")
+
+SEED = 0xE7AC
+
+
+def bits(a):
+    return np.ascontiguousarray(a, dtype=np.float32).view(np.uint32)
+
+
+def kind_types(kind, E):
+    rng = np.random.default_rng(E + len(kind))
+    if kind == "mixed":
+        t = rng.choice([16, 17, 29], size=E)
+        t[:3] = [16, 17, 29]
+        return np.repeat(t.reshape(1, E, 1), 3, axis=-1).astype(np.int32)
+    t3 = {"iq2": (16, 16, 17), "iq1": (29, 29, 29), "xs": (17, 17, 17), "xxs": (16, 16, 16)}[kind]
+    t = np.zeros((1, E, 3), np.int32)
+    t[..., 0], t[..., 1], t[..., 2] = t3
+    return t
+
+
+CASES = [
+    (4096, 3072, "iq2", 6, 0.0), (4096, 3072, "iq2", 1, 0.0), (4096, 3072, "iq1", 6, 0.0),
+    (4096, 3072, "mixed", 6, 7.0), (4096, 3072, "xs", 3, 0.0), (1024, 512, "xxs", 8, 0.0),
+    (1024, 512, "mixed", 5, 7.0), (256, 768, "iq1", 4, 7.0), (5120, 2304, "mixed", 6, 10.0),
+]
+
+
+@pytest.mark.parametrize("dim,ff,kind,k,lim", CASES)
+def test_exact_layer_bit_identical(orc, dim, ff, kind, k, lim):
+    step(f"exact layer dim={dim} ff={ff} {kind} k={k} lim={lim}")
+    E = 12
+    types = kind_types(kind, E)
+    lane = xl.Lane(dim, ff, 1, E, types, max_picks=8, swiglu_limit=lim)
+    try:
+        lane.generate(SEED)
+        rng = np.random.default_rng(dim + k)
+        for trial in range(2):
+            ids, w = route(rng.standard_normal(E).astype(np.float32), k)
+            x = (rng.standard_normal(dim) * (1 + 2 * trial)).astype(np.float32)
+            shared = rng.standard_normal(dim).astype(np.float32) if trial else None
+            out = torch.zeros(dim, dtype=torch.float32, device="cuda")
+            lane.layer_forward_exact_async(0, dev(ids), dev(w), dev(x), out, shared=None if shared is None else dev(shared))
+            lane.sync()
+            rows = []
+            for e in ids:
+                sig = tuple(int(v) for v in types[0, e])
+                rows.append(orc.expert(sig, *orc.gen_expert(sig, SEED, 0, int(e), dim, ff), dim, ff, x, limit=lim))
+            want = orc.combine(ids, w, np.stack(rows), shared)
+            got = out.cpu().numpy()
+            assert np.array_equal(bits(got), bits(want)), (trial, int(np.sum(bits(got) != bits(want))))
+        assert lane.launch_counts()["exact"] == 2
+    finally:
+        lane.close()
+
+
+def exact_pass(lane, ids, w, x0, L, dim):
+    """One pass through L exact layers, the hidden carried by the hyper-connection
+    pre + RMS norm of one stream; returns (inputs [L+1, dim], outputs [L, dim])."""
+    s = torch.cuda.Stream()
+    with torch.cuda.stream(s):
+        d_ids, d_w = dev(ids), dev(w)
+        hs = torch.zeros((L + 1, dim), dtype=torch.float32, device="cuda")
+        ys = torch.zeros((L, dim), dtype=torch.float32, device="cuda")
+        hs[0].copy_(dev(x0))
+        mix, ones = dev(MIX1), torch.ones(dim, dtype=torch.float32, device="cuda")
+        for l in range(L):
+            lane.layer_forward_exact_async(l, d_ids[l], d_w[l], hs[l], ys[l], stream=s.cuda_stream)
+            lane.hc_pre_norm_async(ys[l].view(1, 1, dim), mix, ones, hs[l + 1].view(1, dim), stream=s.cuda_stream)
+    lane.sync(s.cuda_stream)
+    torch.cuda.synchronize()
+    return hs.cpu().numpy(), ys.cpu().numpy()
+
+
+def oracle_chain(orc, types, seed, ids, w, x0, L, dim, ff):
+    """The oracle's own pass from x0: every layer's output and carried hidden."""
+    hs, ys = [x0], []
+    for l in range(L):
+        rows = []
+        for e in ids[l]:
+            t3 = tuple(int(v) for v in types[l, e])
+            rows.append(orc.expert(t3, *orc.gen_expert(t3, seed, l, int(e), dim, ff), dim, ff, hs[-1]))
+        ys.append(orc.combine(ids[l], w[l], np.stack(rows)))
+        hs.append(carry(orc, ys[-1]))
+    return np.stack(hs), np.stack(ys)
+
+
+def check_chain(hs, ys, hw, yw, tag):
+    for l in range(ys.shape[0]):
+        assert np.array_equal(bits(ys[l]), bits(yw[l])), f"{tag}: layer {l} output"
+        assert np.array_equal(bits(hs[l + 1]), bits(hw[l + 1])), f"{tag}: hidden after layer {l}"
+
+
+def test_exact_chain_40_layers(orc):
+    # tests/test_gpu_chain.py's pass (config 3's type mix, 8 experts per layer)
+    from tests.test_gpu_chain import DIM, FF, L, E, SEED as CSEED
+    types = chain_types()
+    ids, w, x0 = chain_routes()
+    step("exact chain: 40 layers x 8 experts")
+    lane = xl.Lane(DIM, FF, L, E, types, max_picks=8)
+    try:
+        lane.generate(CSEED)
+        hs, ys = exact_pass(lane, ids, w, x0, L, DIM)
+        hs2, ys2 = exact_pass(lane, ids, w, x0, L, DIM)
+    finally:
+        lane.close()
+    assert np.array_equal(bits(hs), bits(hs2)) and np.array_equal(bits(ys), bits(ys2))
+    hw, yw = oracle_chain(orc, types, CSEED, ids, w, x0, L, DIM, FF)
+    check_chain(hs, ys, hw, yw, "8 experts per layer")
+
+
+def test_exact_chain_full_bank(orc):
+    # config 3 at full size: 40 layers x 384 experts, top-6 per layer
+    L, EF, K, DIM, FF, seed = 40, 384, 6, 4096, 3072, 0xC3F1
+    rng = np.random.default_rng(seed)
+    t = rng.choice([v for v, _ in MIX], size=(L, EF), p=[p for _, p in MIX]).astype(np.int32)
+    types = np.repeat(t[..., None], 3, axis=-1)
+    ids = np.zeros((L, K), np.int32)
+    w = np.zeros((L, K), np.float32)
+    for l in range(L):
+        ids[l], w[l] = route(rng.standard_normal(EF).astype(np.float32), K)
+    x0 = rng.standard_normal(DIM).astype(np.float32)
+    step(f"exact chain: full bank {L} x {EF}")
+    lane = xl.Lane(DIM, FF, L, EF, types, max_picks=8)
+    try:
+        lane.generate(seed)
+        hs, ys = exact_pass(lane, ids, w, x0, L, DIM)
+    finally:
+        lane.close()
+    step("exact chain: oracle pass over the 240 picked experts")
+    hw, yw = oracle_chain(orc, types, seed, ids, w, x0, L, DIM, FF)
+    check_chain(hs, ys, hw, yw, "40 x 384 bank")
+
+
+def test_exact_rejects_bad_id():
+    lane = xl.Lane(1024, 512, 1, 4, kind_types("iq2", 4), max_picks=2)
+    try:
+        lane.generate(1)
+        out = torch.zeros(1024, dtype=torch.float32, device="cuda")
+        lane.layer_forward_exact_async(0, dev(np.array([1, 9], np.int32)), dev(np.array([0.5, 0.5], np.float32)),
+                                       dev(np.ones(1024, np.float32)), out)
+        with pytest.raises(xl.XLError, match="expert id"):
+            lane.sync()
+    finally:
+        lane.close()

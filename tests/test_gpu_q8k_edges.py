@@ -14,8 +14,17 @@ working lane's own .q8k bytes (parity/hip_resident_check.cpp:91-127).
 
 The SwiGLU limit 7 (the model's own clamp, q8k_core.hpp:92-95) keeps h finite
 when a 2.5e30 block drives the gate rows to ~1e29; Q8_K(h) and every row's
-block integers are then checked as in test_gpu_trace.py, and the output
-against the oracle chain with the same limit.
+block integers are then checked as in test_gpu_trace.py.
+
+The float results are held to a float64 evaluation of the same exact block
+integers (h from the gate/up integers and scales; the output from the down
+integers and the launch's own Q8_K(h) scales), within 1e-3, not to the oracle
+chain: on this input the reference's float order (eight lane chains, IQ1_M's
+main and delta sums apart, q8k_core.hpp:76-91) cancels catastrophically where
+a row's terms of the 2.5e30 block nearly cancel (one seed's gate row comes out
+of the oracle with the wrong sign and ~1e28 too large), so the oracle itself is
+not within 1e-3 of the exact value there. The kernels form each block's
+integer exactly and scale it once, and stay within the bar.
 """
 from __future__ import annotations
 
@@ -51,6 +60,49 @@ def edge_x(shift: int = 0):
     want = list(gb) + [None, None, None]
     order = [(i + shift) % 16 for i in range(16)]
     return np.concatenate([blocks[i] for i in order]).astype(np.float32), [want[i] for i in order]
+
+
+def block_scales(t, mat, rows):
+    """fp16 block scales of an AoS matrix as float64 [rows, blocks] (IQ1_M: the
+    scale split over the top nibbles of the four scale words)."""
+    bb = {16: 66, 17: 74, 29: 56}[t]
+    b = np.ascontiguousarray(mat).reshape(-1).view(np.uint8).reshape(rows, -1, bb)
+    if t != 29:
+        h = b[..., 0:2].copy().view("<u2")[..., 0]
+    else:
+        sc = b[..., 48:56].copy().view("<u2").astype(np.uint32)
+        h = ((sc[..., 0] >> 12) | ((sc[..., 1] >> 8) & 0xF0) | ((sc[..., 2] >> 4) & 0xF00) | (sc[..., 3] & 0xF000))
+        h = h.astype(np.uint16)
+    return h.view(np.float16).astype(np.float64)
+
+
+def exact_h(sig, mats, ints, q8x):
+    """h of one pick in float64 from the exact gate/up block integers."""
+    nbx = DIM // 256
+    dx = q8x["d"].astype(np.float64)
+    gi = ints[:FF * nbx].reshape(FF, nbx).astype(np.float64)
+    ui = ints[FF * nbx:2 * FF * nbx].reshape(FF, nbx).astype(np.float64)
+    g = 0.125 * np.sum(block_scales(sig[0], mats[0], FF) * dx * gi, axis=1)
+    u = 0.125 * np.sum(block_scales(sig[1], mats[1], FF) * dx * ui, axis=1)
+    g = np.minimum(g, LIM)
+    u = np.clip(u, -LIM, LIM)
+    with np.errstate(over="ignore"):
+        return g / (1.0 + np.exp(-g)) * u
+
+
+def exact_y(sig, mats, ints, q8h_bytes):
+    """One pick's output row in float64 from the exact down block integers and
+    the launch's own Q8_K(h) scales."""
+    nbx, nbh = DIM // 256, FF // 256
+    dh = q8h_bytes.reshape(nbh, 292)[:, :4].copy().view(np.float32)[:, 0].astype(np.float64)
+    di = ints[2 * FF * nbx:].reshape(DIM, nbh).astype(np.float64)
+    return 0.125 * np.sum(block_scales(sig[2], mats[2], DIM) * dh * di, axis=1)
+
+
+def check_exact(sig, mats, ints, q8x, h, q8h_bytes, tag):
+    h64 = exact_h(sig, mats, ints, q8x)
+    assert max_rel(h, h64) < TOL, (tag, max_rel(h, h64))
+    return exact_y(sig, mats, ints, q8h_bytes)
 
 
 def check_q8x(orc, x, want_gold, q8x, tag):
@@ -109,13 +161,14 @@ def test_layer_kernels_stage_golden_q8k(orc, monkeypatch, path, kind, k, kernel)
         want_q8x = check_q8x(orc, x, want_gold, q8x.cpu().numpy(), f"path {path} {kind} k={k}")
         h, q8h, ints = h.cpu().numpy().reshape(k, FF), q8h.cpu().numpy().reshape(k, -1), ints.cpu().numpy().reshape(k, rec)
         assert np.all(np.isfinite(h))
-        rows = []
+        y64 = np.zeros(DIM)
         for i, e in enumerate(ids):
             sig = tuple(int(v) for v in types[0, e])
             mats = orc.gen_expert(sig, SEED, 0, int(e), DIM, FF)
-            check_pick(orc, sig, mats, DIM, FF, want_q8x, h[i], q8h[i], ints[i], f"pick {i} (expert {e}, {sig})")
-            rows.append(orc.expert(sig, *mats, DIM, FF, x, limit=LIM))
-        assert max_rel(out.cpu().numpy(), orc.combine(ids, w, np.stack(rows))) < TOL
+            tag = f"pick {i} (expert {e}, {sig})"
+            check_pick(orc, sig, mats, DIM, FF, want_q8x, h[i], q8h[i], ints[i], tag)
+            y64 += float(w[i]) * check_exact(sig, mats, ints[i], want_q8x, h[i], q8h[i], tag)
+        assert max_rel(out.cpu().numpy(), y64) < TOL
     finally:
         lane.close()
 
@@ -147,17 +200,17 @@ def test_grouped_kernels_stage_golden_q8k(orc, monkeypatch):
         h, q8h, ints = h.cpu().numpy().reshape(P, FF), q8h.cpu().numpy().reshape(P, -1), ints.cpu().numpy().reshape(P, rec)
         got = out.cpu().numpy()
         mats = {}
+        sig = (16, 16, 17)
         for t in range(T):
             want_q8x = check_q8x(orc, x[t], xs[t][1], q8x[t], f"token {t}")
-            rows = []
+            y64 = np.zeros(DIM)
             for i, e in enumerate(ids[t]):
                 if int(e) not in mats:
-                    mats[int(e)] = orc.gen_expert((16, 16, 17), SEED, 0, int(e), DIM, FF)
+                    mats[int(e)] = orc.gen_expert(sig, SEED, 0, int(e), DIM, FF)
                 p = t * k + i
-                if t < 2:   # two tokens in full, the others by their outputs
-                    check_pick(orc, (16, 16, 17), mats[int(e)], DIM, FF, want_q8x, h[p], q8h[p], ints[p],
-                               f"token {t} pick {i} (expert {e})")
-                rows.append(orc.expert((16, 16, 17), *mats[int(e)], DIM, FF, x[t], limit=LIM))
-            assert max_rel(got[t], orc.combine(ids[t], w[t], np.stack(rows))) < TOL, t
+                tag = f"token {t} pick {i} (expert {e})"
+                check_pick(orc, sig, mats[int(e)], DIM, FF, want_q8x, h[p], q8h[p], ints[p], tag)
+                y64 += float(w[t, i]) * check_exact(sig, mats[int(e)], ints[p], want_q8x, h[p], q8h[p], tag)
+            assert max_rel(got[t], y64) < TOL, t
     finally:
         lane.close()

@@ -243,8 +243,9 @@ __device__ __forceinline__ uint4 h_load(const float* hb, uint32_t word) {
     const v4u32 v = __builtin_amdgcn_raw_buffer_load_b128(rs, word * 4, 0, 16);   // per-lane offset: voffset
     return make_uint4(v.x, v.y, v.z, v.w);
 }
+// The sentinel is the largest 32-bit value: no word holds it iff their maximum is below it.
 __device__ __forceinline__ bool h_ready(const uint4& v) {
-    return (v.x != kSentinel) & (v.y != kSentinel) & (v.z != kSentinel) & (v.w != kSentinel);
+    return max(max(v.x, v.y), max(v.z, v.w)) != kSentinel;
 }
 
 // ---- Q8_K of NB blocks at once ---------------------------------------------------------------
@@ -307,15 +308,15 @@ __device__ __forceinline__ bool q8k_blocks(const uint4 (&hv)[NB], int nvalid, in
     for (int m = 0; m < NB; ++m) {
         fin = fin & ((m >= nvalid) | (am[m] <= 0x7f7fffffu));
         // mx: the magnitude am[m] with the sign of the block's first value of that
-        // magnitude (the lane's first match by a bit scan, the wave's by a ballot;
-        // integer ops only, no select over the block's words)
-        const uint32_t hm = uint32_t(ab[m][0] == am[m]) | (uint32_t(ab[m][1] == am[m]) << 1) |
-                            (uint32_t(ab[m][2] == am[m]) << 2) | (uint32_t(ab[m][3] == am[m]) << 3);
-        const uint32_t sg = (x[m][0] >> 31) | ((x[m][1] >> 31) << 1) | ((x[m][2] >> 31) << 2) | ((x[m][3] >> 31) << 3);
-        const uint32_t sb = (sg >> __builtin_ctz(hm | 16u)) & 1u;
-        const uint64_t hit = __builtin_amdgcn_ballot_w64(hm != 0u);
+        // magnitude: each lane's first such value (a select chain in reverse
+        // order), then the first lane holding one (a ballot); no branch
+        uint32_t lv = 0u;
+#pragma unroll
+        for (int i = 3; i >= 0; --i) lv = ab[m][i] == am[m] ? x[m][i] : lv;
+        const uint64_t hit = __builtin_amdgcn_ballot_w64((ab[m][0] == am[m]) | (ab[m][1] == am[m]) |
+                                                         (ab[m][2] == am[m]) | (ab[m][3] == am[m]));
         const int first = int(__builtin_ctzll(hit | (uint64_t(1) << 63)));
-        const float mx = __uint_as_float(am[m] | (uint32_t(__builtin_amdgcn_readlane(int(sb), first)) << 31));
+        const float mx = __uint_as_float(am[m] | (uint32_t(__builtin_amdgcn_readlane(int(lv), first)) & 0x80000000u));
         mxv = lane == m ? mx : mxv;
     }
     const float isv = __fdiv_rn(-127.0f, mxv);

@@ -62,6 +62,30 @@ def edge_x(shift: int = 0):
     return np.concatenate([blocks[i] for i in order]).astype(np.float32), [want[i] for i in order]
 
 
+def tie_x():
+    """(x, None bytes): 16 crafted blocks whose largest magnitude M occurs more
+    than once with both signs, in different lanes (4 values per lane) and within
+    one lane, in either order; the first occurrence sets the sign of mx
+    (q8k_core.hpp:33's strict '>' scan). Expected bytes come from the oracle."""
+    rng = np.random.default_rng(7)
+    cases = [((5, 1), (9, -1)), ((5, -1), (9, 1)), ((4, -1), (6, 1)), ((6, 1), (7, -1)), ((6, -1), (7, 1)),
+             ((200, 1), (100, -1)), ((0, 1), (3, -1)), ((0, -1), (1, 1)), ((254, -1), (255, 1)),
+             ((252, -1), (253, 1), (2, 1)), ((128, 1), (64, -1), (65, 1)), ((17, -1), (18, -1), (19, 1))]
+    blocks = []
+    for pos in cases:
+        b = (rng.standard_normal(256) * 0.5).astype(np.float32)
+        for i, sg in pos:
+            b[i] = np.float32(3.0 * sg)
+        blocks.append(b)
+    alt = np.full(256, 2.0, np.float32) * np.where(np.arange(256) % 2, 1, -1).astype(np.float32)
+    blocks.append(alt)                                         # every value a tie, the first negative
+    blocks.append(np.where(np.arange(256) % 3 == 0, -0.0, 0.0).astype(np.float32))   # zero block with -0
+    one = np.zeros(256, np.float32); one[255] = -1.5
+    blocks.append(one)
+    blocks.append(rng.standard_normal(256).astype(np.float32))
+    return np.concatenate(blocks).astype(np.float32), [None] * 16
+
+
 def block_scales(t, mat, rows):
     """fp16 block scales of an AoS matrix as float64 [rows, blocks] (IQ1_M: the
     scale split over the top nibbles of the four scale words)."""
@@ -136,8 +160,9 @@ LAYER_CASES = [
 ]
 
 
+@pytest.mark.parametrize("ties", [False, True])
 @pytest.mark.parametrize("path,kind,k,kernel", LAYER_CASES)
-def test_layer_kernels_stage_golden_q8k(orc, monkeypatch, path, kind, k, kernel):
+def test_layer_kernels_stage_golden_q8k(orc, monkeypatch, path, kind, k, kernel, ties):
     monkeypatch.setenv("XL_LAYER_PATH", path)
     step(f"Q8_K edge blocks: layer path={path} {kind} k={k}")
     types = layer_types(kind, E)
@@ -146,7 +171,7 @@ def test_layer_kernels_stage_golden_q8k(orc, monkeypatch, path, kind, k, kernel)
         lane.generate(SEED)
         rng = np.random.default_rng(k + len(kind))
         ids, w = route(rng.standard_normal(E).astype(np.float32), k)
-        x, want_gold = edge_x(shift=k)
+        x, want_gold = tie_x() if ties else edge_x(shift=k)
         nbx, nbh = DIM // 256, FF // 256
         rec = 2 * FF * nbx + DIM * nbh
         out = zeros(DIM, torch.float32)

@@ -23,7 +23,10 @@ steps touch different experts (the bank is ~3.9 GB, far beyond the 256 MB MALL).
      each next layer's launch, xl_layer_forward_prenorm_async, and after the
      last layer by xl_hc_pre_norm_async, all inside the timed region: the
      model's ffn_norm step, without which the quadratic SwiGLU overflows f32
-     within a few layers).
+     within a few layers);
+  6  config 1 at the real model's expert shape: d_model 5120, d_ff 2304
+     (engine/strata/fixtures/moe/cpu_lane_fixture.cpp:17), the model's SwiGLU
+     limit 10, 384 resident experts, top-6.
 
 Prints one JSON line: value = achieved algorithmic HBM GB/s (selected experts'
 weight bytes + x in + out per layer), plus us_per_layer; the roofline of the
@@ -50,6 +53,7 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 DIM, FF, E, K = 4096, 3072, 384, 6
+REAL_DIM, REAL_FF, REAL_LIM = 5120, 2304, 10.0   # config 6: the DeepSeek expert shape and SwiGLU limit
 GATE_T, DOWN_T = 16, 17
 BYTES = {16: 66, 17: 74, 29: 56}
 W_GU = FF * (DIM // 256) * BYTES[GATE_T]          # 3,244,032 B per gate/up matrix
@@ -265,7 +269,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=0, help="timed steps (default: 2000 layers' worth)")
     ap.add_argument("--warmup", type=int, default=-1)
-    ap.add_argument("--config", type=int, default=1, choices=(0, 1, 2, 3, 4, 5))
+    ap.add_argument("--config", type=int, default=1, choices=(0, 1, 2, 3, 4, 5, 6))
     ap.add_argument("--tokens", type=int, default=512, help="config 4: tokens per grouped call")
     ap.add_argument("--device-route", action="store_true",
                     help="configs 1, 4: route each step on the GPU from N(0,1) logits (route.cpp router: "
@@ -283,6 +287,9 @@ def main():
               "the routed-expert path runs on a single MI355X holding the whole bank", file=sys.stderr)
         sys.exit(2)
     cfg = args.config
+    global DIM, FF
+    if cfg == 6:   # the real expert shape; the rest of config 1's workload unchanged
+        DIM, FF = REAL_DIM, REAL_FF
     if args.per32 and (cfg > 2 or args.device_route):
         print("bench.py: --per32 applies to configs 0-2 without --device-route", file=sys.stderr)
         sys.exit(2)
@@ -301,7 +308,8 @@ def main():
         types = np.zeros((1, E, 3), np.int32)
         t3 = (29, 29, 29) if cfg == 2 else (GATE_T, GATE_T, DOWN_T)
         types[..., 0], types[..., 1], types[..., 2] = t3
-    lane = xl.Lane(DIM, FF, L, E, types, max_picks=8, max_tokens=TOK if cfg == 4 else 0)
+    lane = xl.Lane(DIM, FF, L, E, types, max_picks=8, max_tokens=TOK if cfg == 4 else 0,
+                   swiglu_limit=REAL_LIM if cfg == 6 else 0.0)
     lane.generate(SEED)
     n_r = args.routes
     if cfg == 0:
@@ -447,6 +455,11 @@ def main():
               2: "xl::dev::stream_kernel (single-launch layer, IQ1_M instance)",
               3: "xl::dev::stream_kernel (single-launch layer, mixed-type instance)",
               4: "grouped path (bucket, Q8_K, gu_kernel, Q8_K, dn_kernel, combine: 6 launches per step)"}.get(cfg)
+    if cfg == 6:   # whichever single launch served the calls (xl_debug_launch_counts)
+        counts = lane.launch_counts()
+        kernel = ("xl::dev::stream_kernel (single-launch layer, IQ2 instance, 5120 x 2304)" if counts["stream"]
+                  else "xl::dev::layer3_kernel (all-types single-launch layer)" if counts["alltypes"]
+                  else "separate launches")
     if cfg == 5:
         kernel = ("MoE block: shared FFN (quant32, mv32 gate+up, swiglu32, quant32, mv32 down) + stream_kernel "
                   "+ hc_post_kernel: 7 launches per step")
@@ -474,6 +487,8 @@ def main():
            "fixed-order combine per token",
         5: "config5: MoE block of one token: shared-expert FFN (Q5_K gate/up, Q6_K down, 4096x3072, per32), "
            "config-1 routed layer with the shared row added last, hc_post over 4 streams",
+        6: "config6: config 1 at the real expert shape, d_model 5120, d_ff 2304, SwiGLU limit 10, top-6 of 384 "
+           "resident experts, gate/up IQ2_XXS + down IQ2_XS, fixed-order combine",
     }
     line = {
         "metric": "routed-expert µs/layer (top-6, batch 1) + achieved HBM GB/s vs MI355X peak",

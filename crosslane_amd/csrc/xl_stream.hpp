@@ -75,8 +75,8 @@ struct SLay<3> {   // IQ2_XXS gate/up, IQ2_XS down
     static constexpr int SGN_IN_ROW = 0;                  // byte of the sign copies in a row
     static constexpr int XS = 131072, IQ1 = -1;
     static constexpr int XQ = 147456, HQ = 65536, Y = 147456;   // HQ over the XXS grid, Y over XQ
-    static constexpr int NRM = 151616;                    // pre-norm group sums (32 floats)
-    static constexpr int Bytes = 151616 + 256;
+    static constexpr int NRM = 152704;                    // pre-norm group sums (32 floats), past XQ
+    static constexpr int Bytes = NRM + 256;
     static constexpr int HQBytes = 65536;
 };
 template <>
@@ -99,6 +99,11 @@ struct SLay<7> {   // any mix: one 256-byte row holds 16 grid copies, then 16 si
     static constexpr int HQBytes = Bytes - HQ;
 };
 constexpr int kS_YFloats = 1024;
+// Q8_K(x) in LDS: kMaxRowK quants (swizzled) at XQ, then the block scales.
+constexpr int kXQScl = kMaxRowK;
+// Slot and pass metadata words: expert id << 17 | pick << 13 | first row (13 bits).
+constexpr uint32_t kMetaRow = 0x1fffu;
+constexpr int kMetaPick = 13, kMetaId = 17;
 
 // Global codebooks (layer_tables in xl_api.cpp): IQ2_XXS grid, IQ2_XS grid, IQ1_M value rows.
 constexpr int kG_XXS = 2048, kG_XS = 4096;
@@ -265,6 +270,42 @@ __device__ __forceinline__ void decode_pass(int (&I)[PD], uint32_t (&d)[PD], con
     });
 }
 
+// Instances whose lanes cover more pairs (PG > 2 gate/up pairs, PD > 4 down
+// pairs: the 5120 x 2304 expert) read each pair's activations from LDS as the
+// pair is decoded, since registers for every pair's activations would not fit;
+// the IQ2_XXS signs then go on the grid bytes (no negated activations).
+template <int TG_, int TU_, bool V>
+__device__ __forceinline__ void decode_pair_al(int& Ig, int& Iu, uint32_t& dg, uint32_t& du, float& dx, const Raw3& G,
+                                               const Raw3& U, const uint8_t* lds, int xq, const LoLanes& lo, int p,
+                                               int bq) {
+    Act<1> A;
+    load_act<1>(A, lds, xq, kXQScl, p, 0);
+    const Raw3 g = pair_view<TG_, V>(G, bq, p), u = pair_view<TU_, V>(U, bq, p);
+    Looks Lg, Lu;
+    look_t<TG_>(Lg, lds, lo, g);
+    look_t<TU_>(Lu, lds, lo, u);
+    Ig = sum_t<TG_, false>(Lg, g, A.a[0], nullptr, p & 3, dg);
+    Iu = sum_t<TU_, false>(Lu, u, A.a[0], nullptr, p & 3, du);
+    dx = A.d[0];
+}
+// A down pass of the same kind, one pair at a time (lookahead registers would
+// not fit beside the pass's raw words; hq, hs: the pick's Q8_K(h) in LDS).
+template <int T, bool V, int PD>
+__device__ __forceinline__ void decode_pass_al(int (&I)[PD], uint32_t (&d)[PD], float (&dx)[PD], const Raw3 (&R)[PD],
+                                               const uint8_t* lds, int hq, int hs, const LoLanes& lo, int lD, int LD,
+                                               int bq) {
+    static_for<PD>([&]<int q>() {
+        const int p = lD + LD * q;
+        const Raw3 r = pair_view<T, V>(R[q], bq, p);
+        Looks Lc;
+        Act<1> Ac;
+        look_t<T>(Lc, lds, lo, r);
+        load_act<1>(Ac, lds, hq, hs, p, 0);
+        I[q] = sum_t<T, false>(Lc, r, Ac.a[0], nullptr, p & 3, d[q]);
+        dx[q] = Ac.d[0];
+    });
+}
+
 // ---- the kernel ----------------------------------------------------------------------------
 // LG x PG: lanes per gate/up row and pairs per lane (LG * PG * 64 == dim);
 // LD x PD: the same for down rows (LD * PD * 64 == ff). MG / MD: most gate/up
@@ -322,7 +363,9 @@ __global__ __launch_bounds__(NW * 64, 1) void stream_kernel(Layer3Args a) {
     constexpr bool HAS1 = (M & 4) != 0;
     constexpr int NX = (4096 + NT - 1) / NT, NS = (1024 + NT - 1) / NT, N1 = (2048 + NT - 1) / NT;
     // x first: its Q8_K runs while the codebook loads are in flight
-    constexpr int UX = (16 + NW - 1) / NW;
+    constexpr int NBXM = LG * PG / 4;                       // the instance's Q8_K(x) blocks (dim / 256)
+    constexpr int UX = (NBXM + NW - 1) / NW;
+    constexpr int PNR = (LG * PG * 64 + 1023) / 1024;       // pre-norm elements per hc_pre_norm thread
     float4 xv[UX];
     // Pre-norm in the kernel (a.pn_h, uniform): xv takes the stream's values,
     // pw the norm weights, pv the values of the two threads of hc_pre_norm_kernel's
@@ -331,7 +374,7 @@ __global__ __launch_bounds__(NW * 64, 1) void stream_kernel(Layer3Args a) {
     const bool pn = a.pn_h != nullptr;
     static_assert(NW * 64 == 512, "pre-norm: two of hc_pre_norm_kernel's 1,024 threads per thread");
     float4 pw[UX];
-    float pv[2][4], pm = 0.0f;
+    float pv[2][PNR], pm = 0.0f;
 #pragma unroll
     for (int u = 0; u < UX; ++u) {
         const int b = wv + NW * u;
@@ -348,7 +391,7 @@ __global__ __launch_bounds__(NW * 64, 1) void stream_kernel(Layer3Args a) {
 #pragma unroll
         for (int s = 0; s < 2; ++s)
 #pragma unroll
-            for (int r = 0; r < 4; ++r) pv[s][r] = a.pn_h[min(t + 512 * s + 1024 * r, dim - 1)];
+            for (int r = 0; r < PNR; ++r) pv[s][r] = a.pn_h[min(t + 512 * s + 1024 * r, dim - 1)];
     }
     uint2 vx[HASXXS ? NX : 1], vs[HASXS ? NS : 1];
     uint4 v1[HAS1 ? N1 : 1];
@@ -369,7 +412,7 @@ __global__ __launch_bounds__(NW * 64, 1) void stream_kernel(Layer3Args a) {
     }
     // Slot and pass metadata, computed lane-parallel and kept in one register:
     // lane j < 32 holds gate/up slot j, lane 32 + j down pass j, packed as
-    // expert << 16 | pick << 12 | first row (bad ids read expert 0 and are
+    // expert << 17 | pick << 13 | first row (bad ids read expert 0 and are
     // masked out). A use reads its lane back (v_readlane), so the scalar
     // registers stay free for the loads' addresses.
     float rw = 0.0f;   // routed: lane i < k's pick weight
@@ -426,12 +469,12 @@ __global__ __launch_bounds__(NW * 64, 1) void stream_kernel(Layer3Args a) {
                             : (unit - pick * sppG) * RG;
         const int id = __shfl(idv, min(pick, 15));
         const bool ok = n > 0 && id >= 0 && id < a.n_experts;
-        meta = (uint32_t(ok ? id : 0) << 16) | (uint32_t(min(pick, 15)) << 12) | uint32_t(row);
+        meta = (uint32_t(ok ? id : 0) << kMetaId) | (uint32_t(min(pick, 15)) << kMetaPick) | uint32_t(row);
         okmask = __builtin_amdgcn_ballot_w64(ok && j < n);
     }
     auto gsl = [&](int j) { return uint32_t(__builtin_amdgcn_readlane(int(meta), j)); };
     auto dsl = [&](int j) { return uint32_t(__builtin_amdgcn_readlane(int(meta), 32 + j)); };
-    auto dpick = [&](int j) { return int((dsl(j) >> 12) & 15u); };
+    auto dpick = [&](int j) { return int((dsl(j) >> kMetaPick) & 15u); };
     const uint32_t gok = uint32_t(okmask), dok = uint32_t(okmask >> 32);
     // h word of slot j's first row (pick * ff + row = slot * RG), or -2^30 when the
     // slot is not this wave's
@@ -502,24 +545,23 @@ __global__ __launch_bounds__(NW * 64, 1) void stream_kernel(Layer3Args a) {
     const uint32_t e_prev = coh_ld32(ctl);
 
     Raw3 rg[WIN][PG], ru[WIN][PG];
-    auto load_slot = [&]<int j>() {
+    // pair q of slot j's gate and up rows
+    auto load_slot_pair = [&]<int j, int q>() {
         constexpr int b = j % WIN;
         const uint32_t m = gsl(j);
-        const int row0 = int(m & 0xfffu), e = int(m >> 16);
-#pragma unroll
-        for (int q = 0; q < PG; ++q) {
-            if constexpr (MIX) {
-                const int pk = int((m >> 12) & 15u);
-                const uint32_t rb = uint32_t(row0) * uint32_t(nbx);
-                const MixRef mg = mref(pk, 0), mu = mref(pk, 1);
-                load_pair_u(rg[b][q], mg.base, mg.code, mg.c2, mg.c3, rb, eg, uint32_t(LG * q));
-                load_pair_u(ru[b][q], mu.base, mu.code, mu.c2, mu.c3, rb, eg, uint32_t(LG * q));
-            } else {
-                load_pair_t<GT>(rg[b][q], matrix(e, 0, go1, go2, single_type<GT>(), nbx), row0, rG, lG + LG * q);
-                load_pair_t<GT>(ru[b][q], matrix(e, 1, go1, go2, single_type<GT>(), nbx), row0, rG, lG + LG * q);
-            }
+        const int row0 = int(m & kMetaRow), e = int(m >> kMetaId);
+        if constexpr (MIX) {
+            const int pk = int((m >> kMetaPick) & 15u);
+            const uint32_t rb = uint32_t(row0) * uint32_t(nbx);
+            const MixRef mg = mref(pk, 0), mu = mref(pk, 1);
+            load_pair_u(rg[b][q], mg.base, mg.code, mg.c2, mg.c3, rb, eg, uint32_t(LG * q));
+            load_pair_u(ru[b][q], mu.base, mu.code, mu.c2, mu.c3, rb, eg, uint32_t(LG * q));
+        } else {
+            load_pair_t<GT>(rg[b][q], matrix(e, 0, go1, go2, single_type<GT>(), nbx), row0, rG, lG + LG * q);
+            load_pair_t<GT>(ru[b][q], matrix(e, 1, go1, go2, single_type<GT>(), nbx), row0, rG, lG + LG * q);
         }
     };
+    auto load_slot = [&]<int j>() { static_for<PG>([&]<int q>() { load_slot_pair.template operator()<j, q>(); }); };
     // Every wave issues the same loads whatever its share (idle slots and passes
     // re-read valid rows and are discarded), so every wait count is exact.
     static_for<WIN>([&]<int j>() { load_slot.template operator()<j>(); });
@@ -564,7 +606,7 @@ __global__ __launch_bounds__(NW * 64, 1) void stream_kernel(Layer3Args a) {
 #pragma unroll
             for (int s = 0; s < 2; ++s)
 #pragma unroll
-                for (int r = 0; r < 4; ++r)
+                for (int r = 0; r < PNR; ++r)
                     if (t + 512 * s + 1024 * r < dim) {
                         const float av = __fadd_rn(0.0f, __fmul_rn(m, pv[s][r]));
                         ss[s] = __fadd_rn(ss[s], __fmul_rn(av, av));
@@ -611,7 +653,7 @@ __global__ __launch_bounds__(NW * 64, 1) void stream_kernel(Layer3Args a) {
             const int b = wv + NW * u;
             if (b < nbx) {
                 *reinterpret_cast<uint32_t*>(lds + LY::XQ + qswz(256 * b + 4 * lane)) = xp[u];
-                if (lane == 0) reinterpret_cast<float*>(lds + LY::XQ + 4096)[b] = xd[u];
+                if (lane == 0) reinterpret_cast<float*>(lds + LY::XQ + kXQScl)[b] = xd[u];
             }
         }
     }
@@ -666,7 +708,7 @@ __global__ __launch_bounds__(NW * 64, 1) void stream_kernel(Layer3Args a) {
     if constexpr (TR) {   // workgroup 0's staged Q8_K(x), as the gate/up rows read it
         if (blockIdx.x == 0 && a.tq8x)
             for (int b = wv; b < nbx; b += NW)
-                trace_q8_block(a.tq8x + 292 * b, reinterpret_cast<const float*>(lds + LY::XQ + 4096)[b],
+                trace_q8_block(a.tq8x + 292 * b, reinterpret_cast<const float*>(lds + LY::XQ + kXQScl)[b],
                                *reinterpret_cast<const uint32_t*>(lds + LY::XQ + qswz(256 * b + 4 * lane)), lane);
     }
     const uint32_t parity = __builtin_amdgcn_readfirstlane(sm.parity);   // uniform: keeps buffer bases scalar
@@ -703,21 +745,22 @@ __global__ __launch_bounds__(NW * 64, 1) void stream_kernel(Layer3Args a) {
 #pragma unroll
         for (int q = 0; q < PD; ++q) {
             if constexpr (MIX) {
-                const MixRef md = mref(int((m >> 12) & 15u), 2);
-                load_pair_u(rd[j % (WIND + 1)][q], md.base, md.code, md.c2, md.c3, uint32_t(m & 0xfffu) * uint32_t(nbh),
+                const MixRef md = mref(int((m >> kMetaPick) & 15u), 2);
+                load_pair_u(rd[j % (WIND + 1)][q], md.base, md.code, md.c2, md.c3, uint32_t(m & kMetaRow) * uint32_t(nbh),
                             ed, uint32_t(LD * q));
             } else
-                load_pair_t<DT>(rd[j % (WIND + 1)][q], matrix(int(m >> 16), 2, do1, do2, single_type<DT>(), nbh),
-                                int(m & 0xfffu), rD, lD + LD * q);
+                load_pair_t<DT>(rd[j % (WIND + 1)][q], matrix(int(m >> kMetaId), 2, do1, do2, single_type<DT>(), nbh),
+                                int(m & kMetaRow), rD, lD + LD * q);
         }
     };
 
     // ---- gate/up
     {
-        Act<PG> A;
-        load_act<PG>(A, lds, LY::XQ, 4096, lG, LG);
-        constexpr bool NEEDNA = (GT & 1) != 0;
-        uint32_t NA[PG][16];   // -q bytewise (q in -127..127, so no overflow); unused without IQ2_XXS
+        constexpr bool ALG = PG > 2;   // activations per pair from LDS (decode_pair_al)
+        Act<ALG ? 1 : PG> A;
+        if constexpr (!ALG) load_act<PG>(A, lds, LY::XQ, kXQScl, lG, LG);
+        constexpr bool NEEDNA = (GT & 1) != 0 && !ALG;
+        uint32_t NA[NEEDNA ? PG : 1][16];   // -q bytewise (q in -127..127, so no overflow); unused without IQ2_XXS
         if constexpr (NEEDNA)
 #pragma unroll
             for (int q = 0; q < PG; ++q)
@@ -735,34 +778,57 @@ __global__ __launch_bounds__(NW * 64, 1) void stream_kernel(Layer3Args a) {
                 if (wv >= NW / 2) __builtin_amdgcn_s_setprio(1);
             }
             if constexpr (j == (2 * MG) / 3) __builtin_amdgcn_s_setprio(0);
-            if constexpr (j >= 1 && j + WIN - 1 < MG) load_slot.template operator()<j + WIN - 1>();
-            if constexpr (j >= MG - WIND) load_pass.template operator()<j - (MG - WIND)>();   // the down stream starts under the last slots
+            if constexpr (j >= 1 && j + WIN - 1 < MG && !(ALG && WIN == 1)) load_slot.template operator()<j + WIN - 1>();
+            // the down stream starts under the last slots (ALG instances: after gate/up,
+            // their slots' raw words and per-pair activations fill the registers)
+            if constexpr (!ALG && j >= MG - WIND) load_pass.template operator()<j - (MG - WIND)>();
             // (gate and up share a block type: xl_open rejects a bank where they differ)
-            const int tg = MIX ? mtype(int((gsl(j) >> 12) & 15u), 0) : 0;
+            const int tg = MIX ? mtype(int((gsl(j) >> kMetaPick) & 15u), 0) : 0;
             int Ig[PG], Iu[PG];
             uint32_t dg[PG], du[PG];
-            if constexpr (!MIX) {
-                decode_slot<GT, GT, false>(Ig, Iu, dg, du, rg[j % WIN], ru[j % WIN], A, NA, lds, lo, lG, LG, 0);
-            } else {   // one branch per slot, static types inside
-                if (tg == kIQ2_XXS) decode_slot<1, 1, true>(Ig, Iu, dg, du, rg[j % WIN], ru[j % WIN], A, NA, lds, lo, lG, LG, bqg);
-                else if (tg == kIQ2_XS) decode_slot<2, 2, true>(Ig, Iu, dg, du, rg[j % WIN], ru[j % WIN], A, NA, lds, lo, lG, LG, bqg);
-                else decode_slot<4, 4, true>(Ig, Iu, dg, du, rg[j % WIN], ru[j % WIN], A, NA, lds, lo, lG, LG, bqg);
+            float dxs[PG];
+            if constexpr (ALG) {
+                // (WIN == 1: the next slot's pair q goes into pair q's registers as soon as
+                // pair q is decoded, so one slot's raw words are live at a time)
+                auto pairs = [&]<int T_, bool V_>(int bq) {
+                    static_for<PG>([&]<int q>() {
+                        decode_pair_al<T_, T_, V_>(Ig[q], Iu[q], dg[q], du[q], dxs[q], rg[j % WIN][q], ru[j % WIN][q], lds,
+                                                   LY::XQ, lo, lG + LG * q, bq);
+                        if constexpr (WIN == 1 && j + 1 < MG) load_slot_pair.template operator()<j + 1, q>();
+                    });
+                };
+                if constexpr (!MIX) pairs.template operator()<GT, false>(0);
+                else if (tg == kIQ2_XXS) pairs.template operator()<1, true>(bqg);
+                else if (tg == kIQ2_XS) pairs.template operator()<2, true>(bqg);
+                else pairs.template operator()<4, true>(bqg);
+            } else {
+                if constexpr (!MIX) {
+                    decode_slot<GT, GT, false>(Ig, Iu, dg, du, rg[j % WIN], ru[j % WIN], A, NA, lds, lo, lG, LG, 0);
+                } else {   // one branch per slot, static types inside
+                    if (tg == kIQ2_XXS) decode_slot<1, 1, true>(Ig, Iu, dg, du, rg[j % WIN], ru[j % WIN], A, NA, lds, lo, lG, LG, bqg);
+                    else if (tg == kIQ2_XS) decode_slot<2, 2, true>(Ig, Iu, dg, du, rg[j % WIN], ru[j % WIN], A, NA, lds, lo, lG, LG, bqg);
+                    else decode_slot<4, 4, true>(Ig, Iu, dg, du, rg[j % WIN], ru[j % WIN], A, NA, lds, lo, lG, LG, bqg);
+                }
+#pragma unroll
+                for (int q = 0; q < PG; ++q) dxs[q] = A.d[ALG ? 0 : q];
             }
             float fg = 0.0f, fu = 0.0f;
 #pragma unroll
             for (int q = 0; q < PG; ++q) {
                 if constexpr (TR) {   // the row's block integers: a quad holds one block's four pairs
                     const int bg = quad_isum(Ig[q]), bu = quad_isum(Iu[q]);
+                    // (the lane read stays outside the branch: a spilled meta reloaded
+                    // inside it would leave lane j, inactive there, stale)
+                    const uint32_t m = gsl(j);
                     if (a.tint && ((gok >> j) & 1u) && (lG & 3) == 0) {
-                        const uint32_t m = gsl(j);
-                        const size_t rec = size_t((m >> 12) & 15u) * (2 * size_t(ff) * nbx + size_t(dim) * nbh);
-                        const size_t o = rec + size_t(int(m & 0xfffu) + rG) * nbx + size_t((lG + LG * q) >> 2);
+                        const size_t rec = size_t((m >> kMetaPick) & 15u) * (2 * size_t(ff) * nbx + size_t(dim) * nbh);
+                        const size_t o = rec + size_t(int(m & kMetaRow) + rG) * nbx + size_t((lG + LG * q) >> 2);
                         a.tint[o] = bg;
                         a.tint[o + size_t(ff) * nbx] = bu;
                     }
                 }
-                fg = fmaf(__fmul_rn(h2f(dg[q]), A.d[q]), float(Ig[q]), fg);
-                fu = fmaf(__fmul_rn(h2f(du[q]), A.d[q]), float(Iu[q]), fu);
+                fg = fmaf(__fmul_rn(h2f(dg[q]), dxs[q]), float(Ig[q]), fg);
+                fu = fmaf(__fmul_rn(h2f(du[q]), dxs[q]), float(Iu[q]), fu);
             }
             // A bad id read expert 0's rows: its h is published as 0 so that readers
             // finish. The mask is applied by an opaque multiply: a select would let the
@@ -796,6 +862,7 @@ __global__ __launch_bounds__(NW * 64, 1) void stream_kernel(Layer3Args a) {
     }
     mark(3);
     __builtin_amdgcn_s_setprio(0);
+    if constexpr (PG > 2) static_for<WIND>([&]<int j>() { load_pass.template operator()<j>(); });
 
     // ---- down: step j quantizes the h of the picks it needs, then every wave runs pass j
     float* ys = reinterpret_cast<float*>(lds + LY::Y);
@@ -879,7 +946,8 @@ __global__ __launch_bounds__(NW * 64, 1) void stream_kernel(Layer3Args a) {
         // Step j runs pass j with the next step's Q8_K(h) in the same straight-line
         // code (its quantizer's DPP and division chains fill the pass's LDS waits);
         // the next step's blocks go to LDS after the pass, then one barrier.
-        Act<PD> B;
+        constexpr bool ALD = PD > 4;   // activations per pair from LDS (decode_pass_al)
+        Act<ALD ? 1 : PD> B;
         static_for<MD>([&]<int j>() {   // steps past nsteps stage nothing and compute a discarded pass
             // the next step's h first (its loads went out a step ago), then the next
             // pass's weight loads: issued before the check, their texture-unit time
@@ -890,7 +958,9 @@ __global__ __launch_bounds__(NW * 64, 1) void stream_kernel(Layer3Args a) {
             }
             if constexpr (j + WIND < MD) load_pass.template operator()<j + WIND>();
             const int i = dpick(j);
-            if (j == 0 || i != dpick(j > 0 ? j - 1 : 0)) load_act<PD>(B, lds, LY::HQ + i * hq_stride, ff, lD, LD);
+            if constexpr (!ALD) {
+                if (j == 0 || i != dpick(j > 0 ? j - 1 : 0)) load_act<PD>(B, lds, LY::HQ + i * hq_stride, ff, lD, LD);
+            }
             uint32_t hp[MQ];
             float hd[MQ];
             bool fin = true;
@@ -898,26 +968,40 @@ __global__ __launch_bounds__(NW * 64, 1) void stream_kernel(Layer3Args a) {
             const int td = MIX ? mtype(i, 2) : 0;
             int I[PD];
             uint32_t d16[PD];
-            if constexpr (!MIX) {
-                decode_pass<DT, false>(I, d16, rd[j % (WIND + 1)], B, lds, lo, lD, LD, 0);
-            } else {   // one branch per pass, static type inside
-                if (td == kIQ2_XXS) decode_pass<1, true>(I, d16, rd[j % (WIND + 1)], B, lds, lo, lD, LD, bqd);
-                else if (td == kIQ2_XS) decode_pass<2, true>(I, d16, rd[j % (WIND + 1)], B, lds, lo, lD, LD, bqd);
-                else decode_pass<4, true>(I, d16, rd[j % (WIND + 1)], B, lds, lo, lD, LD, bqd);
+            float dxs[PD];
+            if constexpr (ALD) {
+                const int hq = LY::HQ + i * hq_stride;
+                if constexpr (!MIX) {
+                    decode_pass_al<DT, false>(I, d16, dxs, rd[j % (WIND + 1)], lds, hq, ff, lo, lD, LD, 0);
+                } else {
+                    if (td == kIQ2_XXS) decode_pass_al<1, true>(I, d16, dxs, rd[j % (WIND + 1)], lds, hq, ff, lo, lD, LD, bqd);
+                    else if (td == kIQ2_XS) decode_pass_al<2, true>(I, d16, dxs, rd[j % (WIND + 1)], lds, hq, ff, lo, lD, LD, bqd);
+                    else decode_pass_al<4, true>(I, d16, dxs, rd[j % (WIND + 1)], lds, hq, ff, lo, lD, LD, bqd);
+                }
+            } else {
+                if constexpr (!MIX) {
+                    decode_pass<DT, false>(I, d16, rd[j % (WIND + 1)], B, lds, lo, lD, LD, 0);
+                } else {   // one branch per pass, static type inside
+                    if (td == kIQ2_XXS) decode_pass<1, true>(I, d16, rd[j % (WIND + 1)], B, lds, lo, lD, LD, bqd);
+                    else if (td == kIQ2_XS) decode_pass<2, true>(I, d16, rd[j % (WIND + 1)], B, lds, lo, lD, LD, bqd);
+                    else decode_pass<4, true>(I, d16, rd[j % (WIND + 1)], B, lds, lo, lD, LD, bqd);
+                }
+#pragma unroll
+                for (int q = 0; q < PD; ++q) dxs[q] = B.d[ALD ? 0 : q];
             }
             float f = 0.0f;
 #pragma unroll
             for (int q = 0; q < PD; ++q) {
                 if constexpr (TR) {
                     const int bi = quad_isum(I[q]);
+                    const uint32_t m = dsl(j);   // outside the branch, as in gate/up
                     if (a.tint && ((dok >> j) & 1u) && (lD & 3) == 0) {
-                        const uint32_t m = dsl(j);
-                        const size_t rec = size_t((m >> 12) & 15u) * (2 * size_t(ff) * nbx + size_t(dim) * nbh);
-                        a.tint[rec + 2 * size_t(ff) * nbx + size_t(int(m & 0xfffu) + rD) * nbh +
+                        const size_t rec = size_t((m >> kMetaPick) & 15u) * (2 * size_t(ff) * nbx + size_t(dim) * nbh);
+                        a.tint[rec + 2 * size_t(ff) * nbx + size_t(int(m & kMetaRow) + rD) * nbh +
                                size_t((lD + LD * q) >> 2)] = bi;
                     }
                 }
-                f = fmaf(__fmul_rn(h2f(d16[q]), B.d[q]), float(I[q]), f);
+                f = fmaf(__fmul_rn(h2f(d16[q]), dxs[q]), float(I[q]), f);
             }
             float okf = ((dok >> j) & 1u) ? 0.125f : 0.0f;   // opaque, as in gate/up
             asm volatile("" : "+v"(okf));
@@ -990,7 +1074,7 @@ hipError_t launch_stream_t(const Layer3Args& args, int grid, hipStream_t s, hipE
             const int hi = std::min(args.k, (NW * j + NW + nq - 1) / nq);
             most = std::max(most, (hi - lo) * nbh);
         }
-    if ((SG + W - 1) / W > MG || args.n_experts > 65536 || args.dim > 4096 || args.ff > 4096 ||
+    if ((SG + W - 1) / W > MG || args.n_experts > 32768 || args.dim > kMaxRowK || args.ff > 4096 ||
         (P + NW - 1) / NW > MD || (most + NW - 1) / NW > MQ || P * RD > kS_YFloats || grid > quads ||
         args.k * (args.ff + 64) > SLay<M>::HQBytes || args.k * args.ff > kHBufWords || !args.hbuf ||
         (M != 7 && !args.slab) || (M == 7 && !args.slab && !args.descs))
@@ -1007,7 +1091,7 @@ hipError_t launch_stream_t(const Layer3Args& args, int grid, hipStream_t s, hipE
 // Instances by shape and pick count for one (GT, DT).
 template <int GT, int DT>
 hipError_t launch_stream_shapes(const Layer3Args& args, int cus, hipStream_t s, hipEvent_t stop) {
-    if (args.k < 1 || args.k > 16 || args.dim > 4096 || args.ff > 4096) return hipErrorNotSupported;
+    if (args.k < 1 || args.k > 16 || args.dim > kMaxRowK || args.ff > 4096) return hipErrorNotSupported;
     int lg, pg, ld, pd;
     if (!row_shape(args.dim, lg, pg) || !row_shape(args.ff, ld, pd)) return hipErrorNotSupported;
     const int RD = 64 / ld;
@@ -1022,6 +1106,10 @@ hipError_t launch_stream_shapes(const Layer3Args& args, int cus, hipStream_t s, 
         // each later pass's under the step before it (three passes in flight under
         // the last three slots: 25.4 us at config 1, one: 24.4 us)
         return launch_stream_t<8, 64, 1, 16, 3, 9, 3, 3, 1, 3, GT, DT>(args, grid, s, stop);
+    }
+    if (lg == 16 && pg == 5 && ld == 4 && pd == 9) {   // 5120 x 2304, the DeepSeek expert (cpu_lane_fixture.cpp:17)
+        if (args.k <= 2) return launch_stream_t<8, 16, 5, 4, 9, 1, 1, 1, 1, 7, GT, DT>(args, grid, s, stop);
+        return launch_stream_t<8, 16, 5, 4, 9, 2, 2, 1, 1, 7, GT, DT>(args, grid, s, stop);
     }
     if (lg == 16 && pg == 1 && ld == 8 && pd == 1)    // 1024 x 512
         return launch_stream_t<8, 16, 1, 8, 1, 6, 2, 3, 1, 2, GT, DT>(args, grid, s, stop);

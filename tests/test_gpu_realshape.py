@@ -1,8 +1,9 @@
 """The DeepSeek-V4.1 expert shape, d_model 5120 x d_ff 2304
 (engine/strata/fixtures/moe/cpu_lane_fixture.cpp:17; the reference's own checks
 run K = 2304 / 5120, warm/grouped_check.hpp:89, warm/expert_check.cpp:144), on
-every path: the single-launch all-types kernel (IQ2, IQ1_M and mixed-type
-layers) with its parity trace, the separate launches, the per32 mode, the
+every path: the streaming kernel's 5120 x 2304 instances (IQ2, IQ1_M and
+mixed-type layers, up to 6 picks) and the all-types kernel (more picks, or
+forced) with their parity traces, the separate launches, the per32 mode, the
 grouped MFMA kernels, and a weight pack in the reference's layout loaded
 through xl_bank_load_pack.
 
@@ -28,12 +29,16 @@ torch = pytest.importorskip("torch")
 DIM, FF, SEED = 5120, 2304, 0x5120
 
 
-@pytest.mark.parametrize("kind,k", [("iq2", 6), ("iq1", 6), ("mixed", 8), ("iq2", 1)])
-def test_real_shape_layer(orc, monkeypatch, kind, k):
+@pytest.mark.parametrize("kind,k,path,kernel,lim", [
+    ("iq2", 6, "1", 1, 0.0), ("iq1", 6, "1", 1, 0.0), ("mixed", 6, "1", 1, 10.0), ("iq2", 1, "1", 1, 10.0),
+    ("iq2", 2, "1", 1, 0.0), ("mixed", 3, "1", 1, 0.0), ("mixed", 8, "1", 3, 0.0), ("iq2", 6, "3", 3, 10.0),
+    ("iq1", 6, "3", 3, 0.0)])
+def test_real_shape_layer(orc, monkeypatch, kind, k, path, kernel, lim):
     E = 12
     types = layer_types(kind, E)
-    step(f"real shape {DIM}x{FF} layer {kind} k={k}")
-    lane = xl.Lane(DIM, FF, 1, E, types, max_picks=8)
+    step(f"real shape {DIM}x{FF} layer {kind} k={k} path={path} lim={lim}")
+    monkeypatch.setenv("XL_LAYER_PATH", path)
+    lane = xl.Lane(DIM, FF, 1, E, types, max_picks=8, swiglu_limit=lim)
     try:
         lane.generate(SEED)
         rng = np.random.default_rng(k + len(kind))
@@ -43,7 +48,7 @@ def test_real_shape_layer(orc, monkeypatch, kind, k):
         for e in ids:
             sig = tuple(int(v) for v in types[0, e])
             mats.append(orc.gen_expert(sig, SEED, 0, int(e), DIM, FF))
-            rows.append(orc.expert(sig, *mats[-1], DIM, FF, x))
+            rows.append(orc.expert(sig, *mats[-1], DIM, FF, x, limit=lim))
         want = orc.combine(ids, w, np.stack(rows))
         got = lane.layer_forward(0, ids, w, x)
         assert max_rel(got, want) < TOL, max_rel(got, want)
@@ -55,7 +60,7 @@ def test_real_shape_layer(orc, monkeypatch, kind, k):
         q8x, q8h = zeros(nbx * 292, torch.uint8), zeros(k * nbh * 292, torch.uint8)
         h, ints = zeros(k * FF, torch.float32), zeros(k * rec, torch.int32)
         torch.cuda.synchronize()
-        assert lane.layer_trace_async(0, dev(ids), dev(w), dev(x), out, q8x, q8h, h, ints) == 3
+        assert lane.layer_trace_async(0, dev(ids), dev(w), dev(x), out, q8x, q8h, h, ints) == kernel
         lane.sync()
         want_q8x = orc.quantize(x)
         assert np.array_equal(q8x.cpu().numpy(), want_q8x.view(np.uint8))
@@ -66,7 +71,7 @@ def test_real_shape_layer(orc, monkeypatch, kind, k):
         assert np.array_equal(out.cpu().numpy().view(np.uint32), got.view(np.uint32))
         # separate launches (the fallback) on the same layer
         monkeypatch.setenv("XL_LAYER_PATH", "0")
-        sep = xl.Lane(DIM, FF, 1, E, types, max_picks=8)
+        sep = xl.Lane(DIM, FF, 1, E, types, max_picks=8, swiglu_limit=lim)
         try:
             sep.generate(SEED)
             got0 = sep.layer_forward(0, ids, w, x)

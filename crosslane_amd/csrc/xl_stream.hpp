@@ -98,6 +98,10 @@ struct SLay<7> {   // any mix: one 256-byte row holds 16 grid copies, then 16 si
     static constexpr int Bytes = 163584;
     static constexpr int HQBytes = Bytes - HQ;
 };
+// Down passes over the flattened (pick, row) list of a workgroup's row band
+// (single-type instances whose passes hold more than four pairs per lane).
+template <int M, int PD>
+constexpr bool stream_xp() { return M != 7 && PD > 4; }
 constexpr int kS_YFloats = 1024;
 // Q8_K(x) in LDS: kMaxRowK quants (swizzled) at XQ, then the block scales.
 constexpr int kXQScl = kMaxRowK;
@@ -306,6 +310,51 @@ __device__ __forceinline__ void decode_pass_al(int (&I)[PD], uint32_t (&d)[PD], 
     });
 }
 
+// A down pass's PD pairs (p = lD + LD q) of row `row` of a matrix whose base
+// differs per lane (XP passes hold rows of two picks): global loads from 64-bit
+// lane addresses, the pair offsets immediates.
+template <int TM, int PD, int LD>
+__device__ __forceinline__ void load_pass_v(Raw3 (&R)[PD], const uint8_t* base, uint32_t o1, uint32_t o2, int row,
+                                            int nb, int lD) {
+    static_assert(LD % 4 == 0, "a lane's pairs stay in one block column");
+    const uint64_t rb = uint64_t(uint32_t(row) * uint32_t(nb));   // blocks before the row
+    const int b0 = lD >> 2;                                       // the lane's first block
+    if constexpr (TM == 4) {
+        const uint8_t* pq = base + rb * 32 + 8 * lD;
+        const uint8_t* pa = base + o1 + rb * 16 + 4 * lD;
+        const uint8_t* pb = base + o2 + rb * 8 + 8 * b0;
+#pragma unroll
+        for (int q = 0; q < PD; ++q) {
+            const v2u32 v = __builtin_nontemporal_load(reinterpret_cast<const v2u32*>(pq + 8 * LD * q));
+            const v2u32 sw = __builtin_nontemporal_load(reinterpret_cast<const v2u32*>(pb + 8 * (LD / 4) * q));
+            R[q].w[0] = v.x; R[q].w[1] = v.y;
+            R[q].w[2] = __builtin_nontemporal_load(reinterpret_cast<const uint32_t*>(pa + 4 * LD * q));
+            R[q].w[3] = sw.x; R[q].w[4] = sw.y;
+        }
+    } else {
+        const uint8_t* pq = base + rb * 64 + 16 * lD;
+#pragma unroll
+        for (int q = 0; q < PD; ++q) {
+            const v4u32 v = __builtin_nontemporal_load(reinterpret_cast<const v4u32*>(pq + 16 * LD * q));
+            R[q].w[0] = v.x; R[q].w[1] = v.y; R[q].w[2] = v.z; R[q].w[3] = v.w;
+        }
+        if constexpr (TM == 1) {
+            const uint8_t* pa = base + o1 + rb * 2 + 2 * b0;
+#pragma unroll
+            for (int q = 0; q < PD; ++q)
+                R[q].h[0] = __builtin_nontemporal_load(reinterpret_cast<const uint16_t*>(pa + 2 * (LD / 4) * q));
+        } else {
+            const uint8_t* pa = base + o1 + rb * 8 + 2 * lD;
+            const uint8_t* pb = base + o2 + rb * 2 + 2 * b0;
+#pragma unroll
+            for (int q = 0; q < PD; ++q) {
+                R[q].h[0] = __builtin_nontemporal_load(reinterpret_cast<const uint16_t*>(pa + 2 * LD * q));
+                R[q].h[1] = __builtin_nontemporal_load(reinterpret_cast<const uint16_t*>(pb + 2 * (LD / 4) * q));
+            }
+        }
+    }
+}
+
 // ---- the kernel ----------------------------------------------------------------------------
 // LG x PG: lanes per gate/up row and pairs per lane (LG * PG * 64 == dim);
 // LD x PD: the same for down rows (LD * PD * 64 == ff). MG / MD: most gate/up
@@ -319,6 +368,7 @@ __global__ __launch_bounds__(NW * 64, 1) void stream_kernel(Layer3Args a) {
     static_assert(WIN <= MG && WIND <= MD && WIND <= MG && MG <= 32 && MD <= 32, "prefetch depths, metadata lanes");
     constexpr int M = (GT == 1 && DT == 2) ? 3 : (GT == 4 && DT == 4) ? 4 : 7;
     constexpr bool MIX = M == 7;   // matrices from per-(pick, role) lane tables, types at run time
+    constexpr bool XP = stream_xp<M, PD>();
     using LY = SLay<M>;
     static_assert(MIX || (one_type<GT>() && one_type<DT>()), "single-type instances");
     __shared__ __attribute__((aligned(16))) Smem<M> sm;
@@ -334,12 +384,22 @@ __global__ __launch_bounds__(NW * 64, 1) void stream_kernel(Layer3Args a) {
         if (a.trace && lane == 0) a.trace[size_t(gw) * 32 + n] = __builtin_amdgcn_s_memrealtime();
     };
 
-    // ---- this wave's work: gate/up slots gw + W*j, down passes wv + NW*j (pick-major)
+    // ---- this wave's work: gate/up slots gs + W*j, down passes wv + NW*j (pick-major)
+    // When the slots do not divide evenly over the waves, the slot index runs
+    // wave-major (wave wv of workgroup b starts at gs = wv G + b): every
+    // workgroup then holds the same share to within one slot, instead of some
+    // holding twice the slots of others.
     const int sppG = ff / RG, SG = k * sppG;
-    const int ng = SG > gw ? min(MG, (SG - gw + W - 1) / W) : 0;
+    const int gs = SG % W ? wv * G + int(blockIdx.x) : gw;
+    const int ng = SG > gs ? min(MG, (SG - gs + W - 1) / W) : 0;
+    // Down rows. XP instances: workgroup b owns rows [b R, b R + R) of every pick
+    // (R = dim / G), and pass u's RD row groups run over the flattened (pick, row)
+    // list, so a pass may hold rows of two picks. Else: row quads b, b + G, ...
+    // of each pick, one pick per pass.
     const int quads = dim / RD;
     const int nq_wg = quads > int(blockIdx.x) ? (quads - int(blockIdx.x) + G - 1) / G : 0;
-    const int P = k * nq_wg;
+    const int RW = XP ? dim / G : nq_wg * RD;   // rows of one pick in this workgroup
+    const int P = XP ? (k * RW + RD - 1) / RD : k * nq_wg;
     const int nd = P > wv ? min(MD, (P - wv + NW - 1) / NW) : 0;
     // Routed in the kernel (a.rlogits): thread t loads expert t's logit and bias
     // here; the routing runs after the x and codebook loads are out. Else the ids.
@@ -462,7 +522,7 @@ __global__ __launch_bounds__(NW * 64, 1) void stream_kernel(Layer3Args a) {
         const int j = lane & 31;
         const int n = isd ? nd : ng;
         const int jj = j < n ? j : n > 0 ? n - 1 : 0;   // past the last: repeat a valid row
-        const int unit = isd ? wv + NW * jj : gw + W * jj;
+        const int unit = isd ? wv + NW * jj : gs + W * jj;
         const int per = isd ? nq_wg : sppG;
         const int pick = n > 0 ? unit / per : 0;
         const int row = isd ? (n > 0 ? (int(blockIdx.x) + G * (unit - pick * nq_wg)) * RD : 0)
@@ -475,10 +535,29 @@ __global__ __launch_bounds__(NW * 64, 1) void stream_kernel(Layer3Args a) {
     auto gsl = [&](int j) { return uint32_t(__builtin_amdgcn_readlane(int(meta), j)); };
     auto dsl = [&](int j) { return uint32_t(__builtin_amdgcn_readlane(int(meta), 32 + j)); };
     auto dpick = [&](int j) { return int((dsl(j) >> kMetaPick) & 15u); };
+    // XP: lane group rD's row of pass j (flattened index u = pass * RD + rD over
+    // pick-major (pick, row) of the band), its expert (a bad id reads expert 0's
+    // rows, masked out) and whether it holds one
+    struct XRow {
+        int pick, row, e;
+        bool ok;
+    };
+    const float rw_inv = XP ? 1.0f / float(RW) : 0.0f;   // (u + 0.5) / RW floors exactly for u, RW < 2^10
+    auto xrow = [&](int j) {
+        XRow x;
+        const int u = (wv + NW * j) * RD + rD;
+        const bool in = u < k * RW;
+        x.pick = in ? int((float(u) + 0.5f) * rw_inv) : 0;
+        x.row = int(blockIdx.x) * RW + (in ? u - x.pick * RW : 0);
+        const int id = __shfl(idv, x.pick);
+        x.ok = in && id >= 0 && id < a.n_experts;
+        x.e = x.ok ? id : 0;
+        return x;
+    };
     const uint32_t gok = uint32_t(okmask), dok = uint32_t(okmask >> 32);
     // h word of slot j's first row (pick * ff + row = slot * RG), or -2^30 when the
     // slot is not this wave's
-    auto hrow = [&](int j) { return j < ng ? (gw + W * j) * RG : -(1 << 30); };
+    auto hrow = [&](int j) { return j < ng ? (gs + W * j) * RG : -(1 << 30); };
 
     // Matrices. Single-type instances (regular layers): matrix (e, role) at
     // slab + e * estride + roff[role], plane offsets shared. Mixed instance: lane
@@ -571,14 +650,14 @@ __global__ __launch_bounds__(NW * 64, 1) void stream_kernel(Layer3Args a) {
     // computed once the first loads are out):
     // lane j * MQ + m holds step j's m-th block of this wave as valid << 8 |
     // pick << 4 | block. Step j quantizes the picks its passes are the first to
-    // need, [ceil(NW j / nq_wg), ceil(NW (j + 1) / nq_wg)) clipped to k; wave wv
+    // need, [ceil(NW RD j / RW), ceil(NW RD (j + 1) / RW)) clipped to k; wave wv
     // owns blocks wv, wv + NW, ... of them.
     static_assert(MD * MQ <= 64, "Q8_K(h) block table lanes");
     uint32_t hblk = 0;
     {
         const int j = lane / MQ, m = lane - j * MQ;
         if (j < MD) {
-            const int plo = min(k, (NW * j + nq_wg - 1) / nq_wg), phi = min(k, (NW * j + NW + nq_wg - 1) / nq_wg);
+            const int plo = min(k, (NW * RD * j + RW - 1) / RW), phi = min(k, (NW * RD * (j + 1) + RW - 1) / RW);
             const int b0 = plo * nbh, nb = phi * nbh - b0, bq = wv + NW * m;
             const int blk = bq < nb ? b0 + bq : 0;
             const int i = blk / nbh;
@@ -741,6 +820,12 @@ __global__ __launch_bounds__(NW * 64, 1) void stream_kernel(Layer3Args a) {
 
     Raw3 rd[WIND + 1][PD];
     auto load_pass = [&]<int j>() {
+        if constexpr (XP) {
+            const XRow x = xrow(j);
+            load_pass_v<DT, PD, LD>(rd[j % (WIND + 1)], a.slab + uint64_t(x.e) * a.estride + a.roff[2], do1, do2, x.row,
+                                    nbh, lD);
+            return;
+        }
         const uint32_t m = dsl(j);
 #pragma unroll
         for (int q = 0; q < PD; ++q) {
@@ -957,7 +1042,14 @@ __global__ __launch_bounds__(NW * 64, 1) void stream_kernel(Layer3Args a) {
                 mark(24 + 2 * (j + 1));
             }
             if constexpr (j + WIND < MD) load_pass.template operator()<j + WIND>();
-            const int i = dpick(j);
+            XRow xr{};
+            int i;   // the pass's pick (XP: the lane group's)
+            if constexpr (XP) {
+                xr = xrow(j);
+                i = xr.pick;
+            } else {
+                i = dpick(j);
+            }
             if constexpr (!ALD) {
                 if (j == 0 || i != dpick(j > 0 ? j - 1 : 0)) load_act<PD>(B, lds, LY::HQ + i * hq_stride, ff, lD, LD);
             }
@@ -995,18 +1087,23 @@ __global__ __launch_bounds__(NW * 64, 1) void stream_kernel(Layer3Args a) {
                 if constexpr (TR) {
                     const int bi = quad_isum(I[q]);
                     const uint32_t m = dsl(j);   // outside the branch, as in gate/up
-                    if (a.tint && ((dok >> j) & 1u) && (lD & 3) == 0) {
-                        const size_t rec = size_t((m >> kMetaPick) & 15u) * (2 * size_t(ff) * nbx + size_t(dim) * nbh);
-                        a.tint[rec + 2 * size_t(ff) * nbx + size_t(int(m & kMetaRow) + rD) * nbh +
-                               size_t((lD + LD * q) >> 2)] = bi;
+                    const bool tok = XP ? xr.ok : ((dok >> j) & 1u) != 0;
+                    const int tpick = XP ? xr.pick : int((m >> kMetaPick) & 15u);
+                    const int trow = XP ? xr.row : int(m & kMetaRow) + rD;
+                    if (a.tint && tok && (lD & 3) == 0) {
+                        const size_t rec = size_t(tpick) * (2 * size_t(ff) * nbx + size_t(dim) * nbh);
+                        a.tint[rec + 2 * size_t(ff) * nbx + size_t(trow) * nbh + size_t((lD + LD * q) >> 2)] = bi;
                     }
                 }
                 f = fmaf(__fmul_rn(h2f(d16[q]), dxs[q]), float(I[q]), f);
             }
-            float okf = ((dok >> j) & 1u) ? 0.125f : 0.0f;   // opaque, as in gate/up
+            float okf = (XP ? xr.ok : ((dok >> j) & 1u) != 0) ? 0.125f : 0.0f;   // opaque, as in gate/up
             asm volatile("" : "+v"(okf));
             const float y = __fmul_rn(okf, gsum<LD>(f));
-            if (j < nd && lD == LD - 1) ys[(wv + NW * j) * RD + rD] = y;
+            // ys[u]: pick-major rows of the band, u = pass * RD + rD (passes past nd
+            // have u >= k RW)
+            const int u = (wv + NW * j) * RD + rD;
+            if (u < k * RW && lD == LD - 1) ys[u] = y;
             if (j == 0) mark(5);
             // the h loads of step j + 2 go out after the pass: later issue, fewer re-polls
             if constexpr (j + 2 < MD) h_issue.template operator()<j + 2>();
@@ -1031,14 +1128,13 @@ __global__ __launch_bounds__(NW * 64, 1) void stream_kernel(Layer3Args a) {
     }
 
     // ---- fixed-order combine of this workgroup's rows
-    const int nrows = nq_wg * RD;
-    for (int r = t; r < nrows; r += NW * 64) {
+    for (int r = t; r < RW; r += NW * 64) {
         const int qq = r / RD, rr = r - qq * RD;
-        const int orow = (int(blockIdx.x) + G * qq) * RD + rr;
+        const int orow = XP ? int(blockIdx.x) * RW + r : (int(blockIdx.x) + G * qq) * RD + rr;
         float acc = 0.0f;
         for (int s2 = 0; s2 < k; ++s2) {
             const int i = sm.order[s2];
-            const float yi = ys[(i * nq_wg + qq) * RD + rr];
+            const float yi = ys[i * RW + r];
             if constexpr (TR) {
                 if (a.ty) a.ty[size_t(i) * dim + orow] = yi;
             }
@@ -1061,21 +1157,25 @@ hipError_t launch_stream_t(const Layer3Args& args, int grid, hipStream_t s, hipE
     constexpr int RG = 64 / LG, RD = 64 / LD;
     const int W = grid * NW;
     const int SG = args.k * (args.ff / RG);
+    constexpr bool XP = stream_xp<M, PD>();
     const int quads = args.dim / RD;
     const int nq_wg = (quads + grid - 1) / grid;
-    const int P = args.k * nq_wg;
+    // rows of one pick in a workgroup (XP: its band; else up to nq_wg quads)
+    const int RW = XP ? args.dim / grid : nq_wg * RD;
+    const int P = (args.k * RW + RD - 1) / RD;
     const int nbh = args.ff / 256;
     // most blocks one step needs: the picks first needed by NW consecutive passes,
-    // in workgroups owning quads / grid and quads / grid + 1 row groups
+    // in workgroups owning RW rows of each pick (else quads / grid and quads / grid + 1 quads)
     int most = 0;
-    for (int nq = quads / grid; nq <= nq_wg; ++nq)
-        for (int j = 0; j * NW < args.k * nq; ++j) {
-            const int lo = std::min(args.k, (NW * j + nq - 1) / nq);
-            const int hi = std::min(args.k, (NW * j + NW + nq - 1) / nq);
+    for (int rw = XP ? RW : (quads / grid) * RD; rw <= RW; rw += RD)
+        for (int j = 0; j * NW * RD < args.k * rw; ++j) {
+            const int lo = std::min(args.k, (NW * RD * j + rw - 1) / rw);
+            const int hi = std::min(args.k, (NW * RD * (j + 1) + rw - 1) / rw);
             most = std::max(most, (hi - lo) * nbh);
         }
     if ((SG + W - 1) / W > MG || args.n_experts > 32768 || args.dim > kMaxRowK || args.ff > 4096 ||
-        (P + NW - 1) / NW > MD || (most + NW - 1) / NW > MQ || P * RD > kS_YFloats || grid > quads ||
+        (P + NW - 1) / NW > MD || (most + NW - 1) / NW > MQ || args.k * RW > kS_YFloats || grid > quads ||
+        (XP && args.dim % grid != 0) ||
         args.k * (args.ff + 64) > SLay<M>::HQBytes || args.k * args.ff > kHBufWords || !args.hbuf ||
         (M != 7 && !args.slab) || (M == 7 && !args.slab && !args.descs))
         return hipErrorNotSupported;
@@ -1109,7 +1209,9 @@ hipError_t launch_stream_shapes(const Layer3Args& args, int cus, hipStream_t s, 
     }
     if (lg == 16 && pg == 5 && ld == 4 && pd == 9) {   // 5120 x 2304, the DeepSeek expert (cpu_lane_fixture.cpp:17)
         if (args.k <= 2) return launch_stream_t<8, 16, 5, 4, 9, 1, 1, 1, 1, 7, GT, DT>(args, grid, s, stop);
-        return launch_stream_t<8, 16, 5, 4, 9, 2, 2, 1, 1, 7, GT, DT>(args, grid, s, stop);
+        // single-type layers: up to six picks' 20-row bands fill one pass per wave
+        if constexpr (GT != 7) return launch_stream_t<8, 16, 5, 4, 9, 2, 1, 1, 1, 7, GT, DT>(args, grid, s, stop);
+        else return launch_stream_t<8, 16, 5, 4, 9, 2, 2, 1, 1, 7, GT, DT>(args, grid, s, stop);
     }
     if (lg == 16 && pg == 1 && ld == 8 && pd == 1)    // 1024 x 512
         return launch_stream_t<8, 16, 1, 8, 1, 6, 2, 3, 1, 2, GT, DT>(args, grid, s, stop);

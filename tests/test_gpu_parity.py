@@ -207,7 +207,8 @@ def test_host_rejects_bad_routes(layer_lane):
 
 @pytest.mark.parametrize("dim,ff,gu,dn,path", [(256, 256, 16, 16, "1"), (1024, 512, 16, 17, "1"),
                                                (4096, 3072, 16, 17, "1"), (4096, 3072, 29, 29, "1"),
-                                               (4096, 3072, 16, 17, "3")])
+                                               (4096, 3072, 16, 17, "3"), (5120, 2304, 16, 17, "1"),
+                                               (5120, 2304, 29, 29, "1")])
 def test_device_rejects_bad_id_and_poisons(monkeypatch, dim, ff, gu, dn, path):
     # An out-of-range id reaches the kernels only through the device path; the
     # kernels bounds-check it, skip the pick and raise the error flag (the
@@ -317,8 +318,11 @@ def kind_types(kind, E, seed=0):
 
 
 STREAM_CASES = [(4096, 3072, 6), (4096, 3072, 5), (4096, 3072, 4), (4096, 3072, 3), (4096, 3072, 2),
-                (4096, 3072, 1), (1024, 512, 8), (1024, 512, 12), (1024, 512, 16), (256, 768, 6), (256, 768, 12)]
-STREAM_CASES_OTHER = [(4096, 3072, 6), (4096, 3072, 4), (4096, 3072, 1), (1024, 512, 16), (256, 768, 12)]
+                (4096, 3072, 1), (1024, 512, 8), (1024, 512, 12), (1024, 512, 16), (256, 768, 6), (256, 768, 12),
+                (5120, 2304, 6), (5120, 2304, 5), (5120, 2304, 4), (5120, 2304, 3), (5120, 2304, 2),
+                (5120, 2304, 1)]
+STREAM_CASES_OTHER = [(4096, 3072, 6), (4096, 3072, 4), (4096, 3072, 1), (1024, 512, 16), (256, 768, 12),
+                      (5120, 2304, 6), (5120, 2304, 4), (5120, 2304, 1)]
 
 
 @pytest.mark.parametrize("kind,dim,ff,k", [("iq2",) + c for c in STREAM_CASES] +
@@ -327,7 +331,9 @@ def test_streaming_kernel_pick_counts(orc, kind, dim, ff, k, monkeypatch):
     # XL_LAYER_PATH=4 runs the streaming kernel or fails: pick counts that give
     # one, two or three down steps and steps staging one to eight picks must
     # match the oracle and repeat bit for bit, for the IQ2 instance, the IQ1_M
-    # instance and the mixed-type instance (matrices from descriptors).
+    # instance and the mixed-type instance (matrices from descriptors). At
+    # 5120 x 2304 the single-type instances' down passes cross pick boundaries
+    # (a workgroup's 20-row band of every pick, 16 rows a pass).
     step(f"streaming kernel {kind} dim={dim} ff={ff} k={k}")
     E = 24
     rng = np.random.default_rng(dim + ff + k)

@@ -522,12 +522,15 @@ __global__ __launch_bounds__(NW * 64, 1) void stream_kernel(Layer3Args a) {
         const bool isd = lane >= 32;
         const int j = lane & 31;
         const int n = isd ? nd : ng;
-        const int jj = j < n ? j : n > 0 ? n - 1 : 0;   // past the last: repeat a valid row
+        const int jj = j < n ? j : n > 0 ? n - 1 : 0;   // past the last: a valid row
         const int unit = isd ? wv + NW * jj : gs + W * jj;
         const int per = isd ? nq_wg : sppG;
         const int pick = n > 0 ? unit / per : 0;
+        // An idle gate/up slot (and every slot of a wave with none) reads the first
+        // rows of its pick: in bounds, and the same lines for every idle wave, so
+        // they come from cache instead of re-streaming rows from HBM.
         const int row = isd ? (n > 0 ? (int(blockIdx.x) + G * (unit - pick * nq_wg)) * RD : 0)
-                            : (unit - pick * sppG) * RG;
+                            : (j < n ? (unit - pick * sppG) * RG : 0);
         const int id = __shfl(idv, min(pick, 15));
         const bool ok = n > 0 && id >= 0 && id < a.n_experts;
         meta = (uint32_t(ok ? id : 0) << kMetaId) | (uint32_t(min(pick, 15)) << kMetaPick) | uint32_t(row);

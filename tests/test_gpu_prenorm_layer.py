@@ -19,7 +19,7 @@ pytestmark = pytest.mark.gpu
 torch = pytest.importorskip("torch")
 
 E = 24
-SHAPES = [(4096, 3072, 6), (4096, 3072, 1), (1024, 512, 16), (256, 768, 12)]
+SHAPES = [(4096, 3072, 6), (4096, 3072, 1), (1024, 512, 16), (256, 768, 12), (5120, 2304, 6), (5120, 2304, 2)]
 
 
 def bits(t):

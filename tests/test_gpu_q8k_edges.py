@@ -6,11 +6,12 @@ equal-magnitude tie of opposite signs, one-hot blocks, a subnormal largest
 magnitude, a 2.5e30 block), two crafted blocks whose largest magnitude sits
 just below and just above 127 / FLT_MAX (is = -127/mx overflows to -inf in the
 first, d = 1/is = -0), and one N(0,1) block. It is run through the parity
-trace of the streaming kernel (IQ2, IQ1_M and mixed-type instances, one and
-six picks), the all-types kernel and the grouped MFMA kernels (token rows),
-and the staged Q8_K(x) must equal the golden bytes (and the oracle's, for the
-crafted blocks) byte for byte: the bar the reference's probe applies to its
-working lane's own .q8k bytes (parity/hip_resident_check.cpp:91-127).
+trace of the streaming kernel (IQ2, IQ1_M and mixed-type instances, one to
+six picks, at 4096 x 3072 and at 5120 x 2304, where x takes four more blocks
+of the other set), the all-types kernel and the grouped MFMA kernels (token
+rows), and the staged Q8_K(x) must equal the golden bytes (and the oracle's,
+for the crafted blocks) byte for byte: the bar the reference's probe applies
+to its working lane's own .q8k bytes (parity/hip_resident_check.cpp:91-127).
 
 The SwiGLU limit 7 (the model's own clamp, q8k_core.hpp:92-95) keeps h finite
 when a 2.5e30 block drives the gate rows to ~1e29; Q8_K(h) and every row's
@@ -86,6 +87,18 @@ def tie_x():
     return np.concatenate(blocks).astype(np.float32), [None] * 16
 
 
+def x_for(dim, ties, shift):
+    """(x, expected bytes per block) of dim values: the tie or edge blocks, then
+    (dim above 4096) the first blocks of the other set."""
+    x, want = tie_x() if ties else edge_x(shift=shift)
+    extra = (dim - 4096) // 256
+    if extra > 0:
+        x2, want2 = edge_x(shift=shift) if ties else tie_x()
+        x = np.concatenate([x, x2[:256 * extra]])
+        want = list(want) + list(want2[:extra])
+    return x.astype(np.float32), want
+
+
 def block_scales(t, mat, rows):
     """fp16 block scales of an AoS matrix as float64 [rows, blocks] (IQ1_M: the
     scale split over the top nibbles of the four scale words)."""
@@ -100,8 +113,9 @@ def block_scales(t, mat, rows):
     return h.view(np.float16).astype(np.float64)
 
 
-def exact_h(sig, mats, ints, q8x):
+def exact_h(sig, mats, ints, q8x, dim=DIM, ff=FF):
     """h of one pick in float64 from the exact gate/up block integers."""
+    DIM, FF = dim, ff
     nbx = DIM // 256
     dx = q8x["d"].astype(np.float64)
     gi = ints[:FF * nbx].reshape(FF, nbx).astype(np.float64)
@@ -114,25 +128,27 @@ def exact_h(sig, mats, ints, q8x):
         return g / (1.0 + np.exp(-g)) * u
 
 
-def exact_y(sig, mats, ints, q8h_bytes):
+def exact_y(sig, mats, ints, q8h_bytes, dim=DIM, ff=FF):
     """One pick's output row in float64 from the exact down block integers and
     the launch's own Q8_K(h) scales."""
+    DIM, FF = dim, ff
     nbx, nbh = DIM // 256, FF // 256
     dh = q8h_bytes.reshape(nbh, 292)[:, :4].copy().view(np.float32)[:, 0].astype(np.float64)
     di = ints[2 * FF * nbx:].reshape(DIM, nbh).astype(np.float64)
     return 0.125 * np.sum(block_scales(sig[2], mats[2], DIM) * dh * di, axis=1)
 
 
-def check_exact(sig, mats, ints, q8x, h, q8h_bytes, tag):
-    h64 = exact_h(sig, mats, ints, q8x)
+def check_exact(sig, mats, ints, q8x, h, q8h_bytes, tag, dim=DIM, ff=FF):
+    h64 = exact_h(sig, mats, ints, q8x, dim, ff)
     assert max_rel(h, h64) < TOL, (tag, max_rel(h, h64))
-    return exact_y(sig, mats, ints, q8h_bytes)
+    return exact_y(sig, mats, ints, q8h_bytes, dim, ff)
 
 
 def check_q8x(orc, x, want_gold, q8x, tag):
-    want = orc.quantize(x).view(np.uint8).reshape(16, 292)
-    q8x = q8x.reshape(16, 292)
-    for b in range(16):
+    nb = x.size // 256
+    want = orc.quantize(x).view(np.uint8).reshape(nb, 292)
+    q8x = q8x.reshape(nb, 292)
+    for b in range(nb):
         if want_gold[b] is not None:
             assert np.array_equal(want[b], want_gold[b]), f"{tag}: oracle vs golden, block {b}"
         assert np.array_equal(q8x[b], want[b]), f"{tag}: Q8_K(x) block {b}"
@@ -149,29 +165,36 @@ def test_crafted_blocks_hit_the_overflow():
 
 
 LAYER_CASES = [
-    # (XL_LAYER_PATH, layer type map kind, k, expected kernel)
-    ("4", "iq2", 6, 1),     # streaming kernel, IQ2 instance (config 1)
-    ("4", "iq2", 1, 1),     # its one-pick instance (config 0)
-    ("4", "iq1", 6, 1),     # IQ1_M instance (config 2)
-    ("4", "mixed", 6, 1),   # mixed instance (config 3)
-    ("3", "iq2", 6, 3),     # all-types kernel
-    ("3", "iq1", 4, 3),
-    ("3", "mixed", 6, 3),
+    # (XL_LAYER_PATH, layer type map kind, k, expected kernel, dim)
+    ("4", "iq2", 6, 1, 4096),     # streaming kernel, IQ2 instance (config 1)
+    ("4", "iq2", 1, 1, 4096),     # its one-pick instance (config 0)
+    ("4", "iq1", 6, 1, 4096),     # IQ1_M instance (config 2)
+    ("4", "mixed", 6, 1, 4096),   # mixed instance (config 3)
+    ("3", "iq2", 6, 3, 4096),     # all-types kernel
+    ("3", "iq1", 4, 3, 4096),
+    ("3", "mixed", 6, 3, 4096),
+    # 5120 x 2304 (config 6): 20-row bands, one down step up to six picks
+    ("4", "iq2", 6, 1, 5120),     # config 6
+    ("4", "iq2", 2, 1, 5120),
+    ("4", "iq1", 6, 1, 5120),
+    ("4", "mixed", 2, 1, 5120),
+    ("4", "mixed", 6, 1, 5120),   # two steps, quantized as at 4096
 ]
 
 
 @pytest.mark.parametrize("ties", [False, True])
-@pytest.mark.parametrize("path,kind,k,kernel", LAYER_CASES)
-def test_layer_kernels_stage_golden_q8k(orc, monkeypatch, path, kind, k, kernel, ties):
+@pytest.mark.parametrize("path,kind,k,kernel,dim", LAYER_CASES)
+def test_layer_kernels_stage_golden_q8k(orc, monkeypatch, path, kind, k, kernel, dim, ties):
     monkeypatch.setenv("XL_LAYER_PATH", path)
-    step(f"Q8_K edge blocks: layer path={path} {kind} k={k}")
+    step(f"Q8_K edge blocks: layer path={path} {kind} k={k} dim={dim} ties={ties}")
+    DIM, FF = dim, {4096: 3072, 5120: 2304}[dim]
     types = layer_types(kind, E)
     lane = xl.Lane(DIM, FF, 1, E, types, max_picks=8, swiglu_limit=LIM)
     try:
         lane.generate(SEED)
         rng = np.random.default_rng(k + len(kind))
         ids, w = route(rng.standard_normal(E).astype(np.float32), k)
-        x, want_gold = tie_x() if ties else edge_x(shift=k)
+        x, want_gold = x_for(DIM, ties, k)
         nbx, nbh = DIM // 256, FF // 256
         rec = 2 * FF * nbx + DIM * nbh
         out = zeros(DIM, torch.float32)
@@ -192,7 +215,7 @@ def test_layer_kernels_stage_golden_q8k(orc, monkeypatch, path, kind, k, kernel,
             mats = orc.gen_expert(sig, SEED, 0, int(e), DIM, FF)
             tag = f"pick {i} (expert {e}, {sig})"
             check_pick(orc, sig, mats, DIM, FF, want_q8x, h[i], q8h[i], ints[i], tag)
-            y64 += float(w[i]) * check_exact(sig, mats, ints[i], want_q8x, h[i], q8h[i], tag)
+            y64 += float(w[i]) * check_exact(sig, mats, ints[i], want_q8x, h[i], q8h[i], tag, DIM, FF)
         assert max_rel(out.cpu().numpy(), y64) < TOL
     finally:
         lane.close()

@@ -445,6 +445,30 @@ def main():
     us_layer = us_step / L   # config 4: one grouped call of TOK tokens
     gbs = bytes_per_step / (us_step * 1e-6) / 1e9
 
+    # The spread, after the timed region: 20 batches of up to 25 further steps
+    # (fresh routes as before), each batch between two events of its own,
+    # enqueued behind a device-side sleep so that they run back to back rather
+    # than at the host's enqueue pace (an event pair around every single step
+    # would add its packets' cost to each step: +4.7 us at config 1)
+    per_b = max(1, min(25, steps // 20))
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(20)]
+    with torch.cuda.stream(stream):
+        torch.cuda._sleep(int(5e7))   # ~25 ms at the shader clock: longer than enqueueing the batches
+    i = warmup + steps
+    for ea, eb in evs:
+        ea.record(stream)
+        for _ in range(per_b):
+            step(i)
+            i += 1
+        eb.record(stream)
+    torch.cuda.synchronize()
+    lane.sync(sp)
+    per = np.array([ea.elapsed_time(eb) * 1e3 / (per_b * L) for ea, eb in evs])
+    dist = {"median": round(float(np.median(per)), 3), "p10": round(float(np.percentile(per, 10)), 3),
+            "p90": round(float(np.percentile(per, 90)), 3), "batches": len(evs), "steps_per_batch": per_b,
+            "how": "us per layer: mean of each batch of steps run back to back after the timed region, "
+                   "each batch between its own events"}
+
     # One kernel launch per layer: the layer kernel's average duration is the
     # timed region's event time over the launches (rocprofv3 --kernel-trace of
     # the same command agrees; see profiles/). Config 3's figure also holds the
@@ -494,6 +518,7 @@ def main():
         "metric": "routed-expert µs/layer (top-6, batch 1) + achieved HBM GB/s vs MI355X peak",
         "value": round(gbs, 2), "unit": "GB/s", "n_gpus": 1, "steps": steps, "warmup": warmup,
         "ms_per_step": round(ms / steps, 6), "us_per_layer": round(us_layer, 3),
+        "us_per_layer_dist": dist,
         "hbm_frac": round(gbs / HBM_PEAK_GBS, 4),
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "int8",
         "data": "synthetic (seeded IQ blocks generated on device, N(0,1) activations and router logits)",

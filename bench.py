@@ -194,6 +194,7 @@ def cpu_baseline(budget_s: float = 12.0, pool: int = 48, config: int = 1, max_th
     else:
         ptypes = [(GATE_T, GATE_T, DOWN_T)] * pool
     k = 1 if config == 0 else K
+    lim = REAL_LIM if config == 6 else 0.0   # the SwiGLU limit the GPU layer uses
     mats = [orc.gen_expert(ptypes[e], SEED, 0, e, DIM, FF) for e in range(pool)]   # not timed
     draws = [(rng.choice(pool, size=k, replace=False).astype(np.int32), rng.random(k).astype(np.float32),
               rng.standard_normal(DIM).astype(np.float32)) for _ in range(64)]
@@ -204,7 +205,8 @@ def cpu_baseline(budget_s: float = 12.0, pool: int = 48, config: int = 1, max_th
         times, phases, nbytes = [], np.zeros(5, np.float64), 0
         for i in range(2):
             ids, w, x = draws[i]
-            orc.lane_layer([ptypes[e] for e in ids], [mats[e] for e in ids], ids, w, x, DIM, FF, threads=n_threads)
+            orc.lane_layer([ptypes[e] for e in ids], [mats[e] for e in ids], ids, w, x, DIM, FF, threads=n_threads,
+                           limit=lim)
         t_end = time.perf_counter() + seconds
         i = 0
         while len(times) < min_reps or time.perf_counter() < t_end:
@@ -212,7 +214,7 @@ def cpu_baseline(budget_s: float = 12.0, pool: int = 48, config: int = 1, max_th
             i += 1
             t0 = time.perf_counter()
             orc.lane_layer([ptypes[e] for e in ids], [mats[e] for e in ids], ids, w, x, DIM, FF, threads=n_threads,
-                           phases=phases)
+                           limit=lim, phases=phases)
             times.append(time.perf_counter() - t0)
             nbytes += sum(expert_bytes(ptypes[e]) for e in ids) + 2 * DIM * 4
         t = np.array(times)
@@ -236,7 +238,7 @@ def cpu_baseline(budget_s: float = 12.0, pool: int = 48, config: int = 1, max_th
         while n_l < 2 or time.perf_counter() < t_end:
             ids, w, x = draws[n_l % len(draws)]
             t0 = time.perf_counter()
-            rows = np.stack([ref.expert(ptypes[e], *mats[e], DIM, FF, x, threads=share) for e in ids])
+            rows = np.stack([ref.expert(ptypes[e], *mats[e], DIM, FF, x, threads=share, limit=lim) for e in ids])
             ref.combine(ids, w, rows, np.zeros(DIM, np.float32))
             t_all += time.perf_counter() - t0
             nb += sum(expert_bytes(ptypes[e]) for e in ids) + 2 * DIM * 4

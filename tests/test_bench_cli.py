@@ -1,7 +1,8 @@
 """bench.py without a GPU: the one-GPU refusal, the synthetic route
 generators' invariants, and the algorithmic bytes the JSON line's `value`
-divides by (SURVEY.md's constants for config 1, the same formula at the real
-expert shape for config 6)."""
+divides by (config 1: 6 experts of IQ2_XXS gate/up 3,072 x 4,096 at 66 B and
+IQ2_XS down 4,096 x 3,072 at 74 B per 256 weights, plus x in and y out; the
+same formula at the real expert shape for config 6)."""
 from __future__ import annotations
 
 import os

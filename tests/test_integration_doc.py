@@ -1,7 +1,8 @@
-"""The reference-side adapter of INTEGRATION.md keeps compiling against the
-interface it implements (engine/strata/warm/runtime.hpp:10-16, WarmRedirect)
-and this repository's C ABI (include/crosslane.h), and every entry point the
-document names exists in the header. CPU only; the compile check is skipped
+"""The reference-side C++ adapter in the repository's integration guide (its
+first cpp block) keeps compiling against the interface it implements
+(engine/strata/warm/runtime.hpp:10-16, WarmRedirect) and this repository's C
+ABI (include/crosslane.h), and every entry point the guide names exists in the
+header. CPU only; the compile check is skipped
 where the reference tree is absent (the GPU box)."""
 from __future__ import annotations
 

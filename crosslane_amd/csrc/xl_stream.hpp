@@ -662,8 +662,8 @@ __global__ __launch_bounds__(NW * 64, 1) void stream_kernel(Layer3Args a) {
     // Group sync (4096-row instances, four row quads per pick and workgroup): a
     // step's passes then cover two picks, waves 0-3 one and waves 4-7 the other;
     // each group of four quantizes its own pick's Q8_K(h) blocks (nbh / 4 each)
-    // and the steps after the first wait for their group only (an LDS arrival
-    // count) instead of the whole workgroup (config 3: 26.95 -> 26.4 us).
+    // and every step waits for its group only (an LDS arrival count) instead of
+    // the whole workgroup (config 3: 26.95 -> 26.2 us).
     const bool gsync = !XP && NW == 8 && nq_wg == 4 && nbh % nq_wg == 0 && nbh / nq_wg <= MQ && MD <= 4;
     {
         const int j = lane / MQ, m = lane - j * MQ;
@@ -1034,6 +1034,20 @@ __global__ __launch_bounds__(NW * 64, 1) void stream_kernel(Layer3Args a) {
             }
         }
     };
+    // Group sync: count this wave in at gcnt[c] (after its LDS stores, in order)
+    // and wait until the group's four waves are in; bounded like every wait.
+    auto group_wait = [&](int c) {
+        uint32_t* const p = &sm.gcnt[c];
+        if (lane == 0) __hip_atomic_fetch_add(p, 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
+        uint32_t spins = 0;
+        while (__hip_atomic_load(p, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) < 4u) {
+            if (++spins > (1u << 20)) {
+                if (lane == 0) set_err(a.err, kDevErrTimeout);
+                break;
+            }
+            __builtin_amdgcn_s_sleep(1);
+        }
+    };
     lds_barrier();   // Q8_K(h) is staged over a region gate/up read: every wave is past gate/up
     if constexpr (H0LATE) h_issue.template operator()<0>();
     {
@@ -1046,7 +1060,11 @@ __global__ __launch_bounds__(NW * 64, 1) void stream_kernel(Layer3Args a) {
             h_store.template operator()<0>(hp, hd, fin);
         }
         mark(17);
-        lds_barrier();
+        if (gsync) {
+            group_wait(6 + wv / 4);   // the group has stored step 0's blocks
+        } else {
+            lds_barrier();
+        }
         mark(25);
         // Step j runs pass j with the next step's Q8_K(h) in the same straight-line
         // code (its quantizer's DPP and division chains fill the pass's LDS waits);
@@ -1130,17 +1148,8 @@ __global__ __launch_bounds__(NW * 64, 1) void stream_kernel(Layer3Args a) {
             if constexpr (j + 1 < MD) {
                 h_store.template operator()<j + 1>(hp, hd, fin);
                 if (j + 1 < 3) mark(17 + j + 1);
-                if (gsync) {   // the group's four waves have stored the next step's blocks
-                    uint32_t* const c = &sm.gcnt[2 * j + wv / 4];
-                    if (lane == 0) __hip_atomic_fetch_add(c, 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
-                    uint32_t spins = 0;
-                    while (__hip_atomic_load(c, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) < 4u) {
-                        if (++spins > (1u << 20)) {
-                            if (lane == 0) set_err(a.err, kDevErrTimeout);
-                            break;
-                        }
-                        __builtin_amdgcn_s_sleep(1);
-                    }
+                if (gsync) {
+                    group_wait(2 * j + wv / 4);   // the group has stored the next step's blocks
                 } else {
                     lds_barrier();
                 }

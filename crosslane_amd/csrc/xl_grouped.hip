@@ -59,18 +59,18 @@ constexpr int kL_GRID = 0, kL_SGN = 65536, kL_TAB = 131072;
 // Per work item, staged once by the workgroup (each wave would otherwise issue
 // these small loads every block): the 16 pairs' activation block scales
 // [block][pair] (f32), then the item's rows' fp16 block scales [row][block]
-// for each matrix (gate/up: NW x 16 rows, down: 128), then (down) the rows'
-// IQ2_XS scale bytes [row][block][8].
+// for each matrix (NW x 16 rows), then (down) the rows' IQ2_XS scale bytes
+// [row][block][8].
 // Blocks per row these regions hold: gate/up rows of dim <= kMaxRowK, down
 // rows of ff <= 4096.
 constexpr int kGuNb = kMaxRowK / 256, kDnNb = 16;
 constexpr int kL_PD = kL_TAB;
 constexpr int kL_RDG = kL_PD + 16 * kGuNb * 4;     // gate/up: 2 planes of `rows` rows x kGuNb fp16 scales
 constexpr int gu_lds_bytes(int rows) { return kL_RDG + 2 * rows * kGuNb * 2; }
-constexpr int kL_RDD = kL_PD + 16 * kDnNb * 4;     // down: 128 rows x kDnNb fp16 scales, then scale bytes
-constexpr int kL_RS = kL_RDD + 128 * kDnNb * 2;
-constexpr int kL_DnBytes = kL_RS + 128 * kDnNb * 8;
-static_assert(gu_lds_bytes(12 * 16) <= 160 * 1024 && kL_DnBytes <= 160 * 1024, "LDS budget");
+constexpr int kL_RDD = kL_PD + 16 * kDnNb * 4;     // down: `rows` rows x kDnNb fp16 scales, then scale bytes
+constexpr int dn_rs(int rows) { return kL_RDD + rows * kDnNb * 2; }
+constexpr int dn_lds_bytes(int rows) { return dn_rs(rows) + rows * kDnNb * 8; }
+static_assert(gu_lds_bytes(12 * 16) <= 160 * 1024 && dn_lds_bytes(12 * 16) <= 160 * 1024, "LDS budget");
 constexpr int kCopiesXXS = 16;   // 256 entries x 256 B: the entry byte lands in address byte 1
 constexpr int kCopiesXS = 8;     // 512 entries x 128 B: the 9-bit entry lands at address bit 7
 
@@ -287,9 +287,10 @@ __device__ __forceinline__ uint32_t gather4(uint32_t x) {
 // bytes 16 g .. + 15 of row col's block (sub-blocks 2g and 2g + 1: grid bytes,
 // then aux bytes = 7 sign bits | scale bit k in byte k). Afterwards u[j] holds
 // {grid, aux} bytes of entry e4 of sub-blocks 2j (bytes 0, 1) and 2j + 1 (bytes
-// 2, 3), and s holds the 4-bit scale of sub-block c at bits 4c .. 4c + 3.
+// 2, 3), and byte j of ls[c & 1] holds sub-block c = 2j + (c & 1)'s factor
+// 2 s + 1 (s its 4-bit scale).
 struct XxsLane {
-    uint32_t u[4], s;
+    uint32_t u[4], ls[2];
 };
 __device__ __forceinline__ XxsLane xxs_lane(const uint4& w, int e4) {
     const uint32_t p01 = perm(w.y, w.x, 0x05010400u), p01b = perm(w.y, w.x, 0x07030602u);
@@ -302,7 +303,9 @@ __device__ __forceinline__ XxsLane xxs_lane(const uint4& w, int e4) {
     xpose4(r.u);
     const uint32_t sa = __builtin_amdgcn_udot4((w.y >> 7) & 0x01010101u, 0x08040201u, 0u, false);
     const uint32_t sb = __builtin_amdgcn_udot4((w.w >> 7) & 0x01010101u, 0x08040201u, 0u, false);
-    r.s = gather4((sa | (sb << 4)) << (8 * e4));
+    const uint32_t s = gather4((sa | (sb << 4)) << (8 * e4));   // sub-block c's scale at bits 4c .. 4c + 3
+    r.ls[0] = ((s << 1) & 0x1E1E1E1Eu) | 0x01010101u;
+    r.ls[1] = ((s >> 3) & 0x1E1E1E1Eu) | 0x01010101u;
     return r;
 }
 struct DnOps {
@@ -310,20 +313,20 @@ struct DnOps {
 };
 
 // Stages one item's pair scales (scl: one f32 per (pair row, block), pairs of
-// the task's order slots) and `mats` planes of fp16 row scales (ROWS rows from
-// row0, nb per row, contiguous in each plane) into LDS, between two barriers.
+// the task's order slots) and `mats` planes of fp16 row scales (rows rows from
+// row0, nb per row, contiguous in each plane) into LDS, after a barrier.
 // The planes go to LDS at rd, `mstride` bytes apart.
-template <int NT, int ROWS>
+template <int NT>
 __device__ __forceinline__ void stage_item(uint8_t* lds, const GroupArgs& a, const int4& tk, const float* scl, int per_pair,
-                                           int nb, const uint8_t* const* planes, int mats, int row0, int t, int rd,
-                                           int mstride) {
+                                           int nb, const uint8_t* const* planes, int mats, int row0, int rows, int t,
+                                           int rd, int mstride) {
     __syncthreads();   // every wave is done with the previous item's staging
     for (int i = t; i < 16 * nb; i += NT) {
         const int pos = i & 15, blk = i >> 4;
         const int p = a.order[tk.y + min(pos, tk.z - 1)];
         reinterpret_cast<float*>(lds + kL_PD)[i] = scl[size_t(per_pair ? p : p / a.k) * nb + blk];
     }
-    const int chunks = ROWS * nb * 2 / 16;   // 16-byte pieces of one plane's rows
+    const int chunks = rows * nb * 2 / 16;   // 16-byte pieces of one plane's rows
     for (int i = t; i < mats * chunks; i += NT) {
         const int m = i / chunks, c = i - m * chunks;
         const uint4 v = reinterpret_cast<const uint4*>(planes[m] + size_t(row0) * nb * 2)[c];
@@ -366,7 +369,8 @@ __global__ __launch_bounds__(NW * 64, 1) void gu_kernel(GroupArgs a) {
         const MatRef G = mat_at(a.descs, tk.x, 0), U = mat_at(a.descs, tk.x, 1);
         {
             const uint8_t* planes[2] = {G.base + G.off1, U.base + U.off1};
-            stage_item<NW * 64, NW * 16>(lds, a, tk, a.xd, 0, nb, planes, 2, grp * NW * 16, t, kL_RDG, NW * 16 * kGuNb * 2);
+            stage_item<NW * 64>(lds, a, tk, a.xd, 0, nb, planes, 2, grp * NW * 16, NW * 16, t, kL_RDG,
+                                NW * 16 * kGuNb * 2);
         }
         const __amdgpu_buffer_rsrc_t rg = rsrc(G.base), ru = rsrc(U.base), rx = rsrc(a.xq);
         const uint32_t vq = uint32_t(row * nb) * 64u;
@@ -390,9 +394,11 @@ __global__ __launch_bounds__(NW * 64, 1) void gu_kernel(GroupArgs a) {
             L.m = *reinterpret_cast<const uint2*>(lds + perm(w, lo_s, 0x0C020000u | ((5u + h) << 8)));
             return L;
         };
-        auto use = [&](const Look& L, const XxsLane& X, int c, long A, int (&bi)[4]) {
-            const v4i C = mfma(A, pack64(bfi(L.m.x, L.g.z, L.g.x), bfi(L.m.y, L.g.w, L.g.y)), v4i{0, 0, 0, 0});
-            const int ls = int(__builtin_amdgcn_ubfe(X.s, 4 * c, 4) * 2u + 1u);
+        auto prod = [&](const Look& L, long A) {
+            return mfma(A, pack64(bfi(L.m.x, L.g.z, L.g.x), bfi(L.m.y, L.g.w, L.g.y)), v4i{0, 0, 0, 0});
+        };
+        auto scale = [&](const v4i& C, const XxsLane& X, int c, int (&bi)[4]) {
+            const int ls = int(__builtin_amdgcn_ubfe(X.ls[c & 1], 8 * (c >> 1), 8));
 #pragma unroll
             for (int r = 0; r < 4; ++r) bi[r] = mad24(ls, C[r], bi[r]);
         };
@@ -412,13 +418,20 @@ __global__ __launch_bounds__(NW * 64, 1) void gu_kernel(GroupArgs a) {
             Look L[8];
 #pragma unroll
             for (int c = 0; c < 8; ++c) L[c] = look(XG, c);
+            // step i < 8: gate sub-block i, else up sub-block i - 8; each step's
+            // MFMA is issued before the previous step's multiply-adds read theirs
+            v4i C[16];
 #pragma unroll
-            for (int c = 0; c < 8; ++c) {
-                use(L[c], XG, c, A[c], big);
-                L[c] = look(XU, c);
+            for (int i = 0; i <= 16; ++i) {
+                if (i < 8) {
+                    C[i] = prod(L[i], A[i]);
+                    L[i] = look(XU, i);
+                } else if (i < 16) {
+                    C[i] = prod(L[i - 8], A[i - 8]);
+                }
+                if (i > 8) scale(C[i - 1], XU, i - 9, biu);
+                else if (i > 0) scale(C[i - 1], XG, i - 1, big);
             }
-#pragma unroll
-            for (int c = 0; c < 8; ++c) use(L[c], XU, c, A[c], biu);
             if constexpr (TR) {   // pair po[r]'s block integers of this lane's row
                 const size_t rec = 2 * size_t(a.ff) * nb + size_t(a.dim) * (a.ff / 256);
 #pragma unroll
@@ -485,22 +498,26 @@ __device__ __forceinline__ void xs_lane(const uint4& w, uint32_t (&u)[4]) {
 }
 
 // ---------------------------------------------------------------------------
-// down. Work item = (task, group of NW * 16 output rows). IQ2_XS keeps a scale
+// down. Work item = (task, group of NW * 16 output rows; the last group of a
+// task holds what is left of dim, whole waves of 16 rows, and the waves past
+// it only join the item's barriers). IQ2_XS keeps a scale
 // nibble per 16 weights (entries 0, 1 of a sub-block: ls1; entries 2, 3: ls2):
 // per sub-block one MFMA over all 32 weights (C) and one with entries 2, 3 of B
 // zeroed (C1), then ls1 C1 + ls2 (C - C1) as ls2 C + (ls1 - ls2) C1, exactly.
 // ---------------------------------------------------------------------------
 template <int NW, bool TR>
 __global__ __launch_bounds__(NW * 64, 1) void dn_kernel(GroupArgs a) {
-    static_assert(NW * 16 == 128, "the down staging holds 128 rows");
-    __shared__ __attribute__((aligned(16))) uint8_t lds[kL_DnBytes];
+    constexpr int R = NW * 16;   // rows per item
+    constexpr int kL_RS = dn_rs(R);
+    static_assert(dn_lds_bytes(R) <= 160 * 1024, "LDS budget");
+    __shared__ __attribute__((aligned(16))) uint8_t lds[dn_lds_bytes(R)];
     const int t = threadIdx.x, lane = t & 63, wv = t >> 6;
     fill_grid<512, kCopiesXS>(lds, a.tables + kTabXS / 8, t, NW * 64);
     fill_signs(lds, a.tables, t, NW * 64);
     __syncthreads();
 
     const int col = lane & 15, e4 = lane >> 4;
-    const int nb = a.ff / 256, groups = a.dim / (NW * 16);
+    const int nb = a.ff / 256, groups = (a.dim + R - 1) / R;
     const int items = uni(*a.n_tasks) * groups;
     const uint32_t lo_x = uint32_t(lane & (kCopiesXS - 1)) << 4;        // kL_GRID = 0
     const uint32_t lo_s = (uint32_t(lane & 31) << 3) | (1u << 16);      // kL_SGN = 1 << 16
@@ -509,7 +526,8 @@ __global__ __launch_bounds__(NW * 64, 1) void dn_kernel(GroupArgs a) {
     for (int item = blockIdx.x; item < items; item += gridDim.x) {
         const int task = item / groups, grp = item - task * groups;
         const int4 tk = task_at(a.tasks, task);
-        const int row = grp * NW * 16 + wv * 16 + col;
+        const int row0 = grp * R, rows = min(R, a.dim - row0);   // rows: a multiple of 16
+        const int row = row0 + wv * 16 + col;
         const uint32_t va = uint32_t(slot_off(tk.y, nb, 0, 0, e4) + 16 * col);   // as in gu_kernel
         int po[4];
 #pragma unroll
@@ -519,10 +537,9 @@ __global__ __launch_bounds__(NW * 64, 1) void dn_kernel(GroupArgs a) {
         }
         const MatRef D = mat_at(a.descs, tk.x, 2);
         {
-            const int row0 = grp * NW * 16;
             const uint8_t* planes[1] = {D.base + D.off2};
-            stage_item<NW * 64, 128>(lds, a, tk, a.hd, 1, nb, planes, 1, row0, t, kL_RDD, 0);
-            const int chunks = 128 * nb * 8 / 16;   // the rows' IQ2_XS scale bytes
+            stage_item<NW * 64>(lds, a, tk, a.hd, 1, nb, planes, 1, row0, rows, t, kL_RDD, 0);
+            const int chunks = rows * nb * 8 / 16;   // the rows' IQ2_XS scale bytes
             for (int i = t; i < chunks; i += NW * 64)
                 *reinterpret_cast<uint4*>(lds + kL_RS + 16 * i) =
                     reinterpret_cast<const uint4*>(D.base + D.off1 + size_t(row0) * nb * 8)[i];
@@ -541,6 +558,17 @@ __global__ __launch_bounds__(NW * 64, 1) void dn_kernel(GroupArgs a) {
         auto compute = [&](const DnOps& o) {
             const int b = blk_c++;
             const uint2 sc = *reinterpret_cast<const uint2*>(lds + kL_RS + 8 * (rl * nb + b));
+            // Scale byte c holds nibbles lo (entries 0, 1) and hi (entries 2, 3):
+            // ls2 = 2 hi + 1 and ls1 - ls2 = 2 (lo - hi) as byte c & 3 of l2[c >> 2]
+            // and (signed) of dl[c >> 2]; 128 + 2 lo - 2 hi never borrows.
+            uint32_t l2[2], dl[2];
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                const uint32_t w = h ? sc.y : sc.x;
+                const uint32_t hi2 = (w >> 3) & 0x1E1E1E1Eu, lo2 = (w << 1) & 0x1E1E1E1Eu;
+                l2[h] = hi2 | 0x01010101u;
+                dl[h] = ((lo2 | 0x80808080u) - hi2) ^ 0x80808080u;
+            }
             int bi[4] = {0, 0, 0, 0};
             uint32_t u[4];
             xs_lane(o.q, u);
@@ -552,17 +580,25 @@ __global__ __launch_bounds__(NW * 64, 1) void dn_kernel(GroupArgs a) {
                 g[c] = *reinterpret_cast<const uint4*>(lds + ((code & 0xff80u) | lo_x));
                 m[c] = *reinterpret_cast<const uint2*>(lds + perm(w, lo_s, (c & 1) ? 0x0C020600u : 0x0C020400u));
             }
+            // sub-block c's two MFMAs are issued before sub-block c - 1's scale
+            // multiply-adds read their results (no wait states between them)
+            v4i C[8], C1[8];
 #pragma unroll
-            for (int c = 0; c < 8; ++c) {
-                const uint32_t* av = reinterpret_cast<const uint32_t*>(o.a) + 2 * c;
-                const long A = pack64(av[0], av[1]);
-                const uint32_t blo = bfi(m[c].x, g[c].z, g[c].x), bhi = bfi(m[c].y, g[c].w, g[c].y);
-                const v4i C = mfma(A, pack64(blo, bhi), v4i{0, 0, 0, 0});
-                const v4i C1 = mfma(A, pack64(blo & mk, bhi & mk), v4i{0, 0, 0, 0});
-                const uint32_t sb = ((c < 4 ? sc.x : sc.y) >> (8 * (c & 3))) & 0xffu;
-                const int ls1 = int(((sb & 15u) << 1) | 1u), ls2 = int(((sb >> 3) & 30u) | 1u);
+            for (int c = 0; c <= 8; ++c) {
+                if (c < 8) {
+                    const uint32_t* av = reinterpret_cast<const uint32_t*>(o.a) + 2 * c;
+                    const long A = pack64(av[0], av[1]);
+                    const uint32_t blo = bfi(m[c].x, g[c].z, g[c].x), bhi = bfi(m[c].y, g[c].w, g[c].y);
+                    C[c] = mfma(A, pack64(blo, bhi), v4i{0, 0, 0, 0});
+                    C1[c] = mfma(A, pack64(blo & mk, bhi & mk), v4i{0, 0, 0, 0});
+                }
+                if (c > 0) {
+                    const int p = c - 1;
+                    const int ls2 = int(__builtin_amdgcn_ubfe(l2[p >> 2], 8 * (p & 3), 8));
+                    const int dls = __builtin_amdgcn_sbfe(int(dl[p >> 2]), 8 * (p & 3), 8);
 #pragma unroll
-                for (int r = 0; r < 4; ++r) bi[r] = mad24(ls2, C[r], mad24(ls1 - ls2, C1[r], bi[r]));
+                    for (int r = 0; r < 4; ++r) bi[r] = mad24(ls2, C[p][r], mad24(dls, C1[p][r], bi[r]));
+                }
             }
             if constexpr (TR) {
                 const int nbx = a.dim / 256;
@@ -580,6 +616,7 @@ __global__ __launch_bounds__(NW * 64, 1) void dn_kernel(GroupArgs a) {
         };
         DnOps s0, s1;
         __syncthreads();   // the item's scales are staged
+        if (wv * 16 >= rows) continue;   // wave-uniform: no rows of this wave in the last group
         load(s0, 0);
         uint32_t t0 = touch(min(1, nb - 1)), t2 = touch(min(3, nb - 1));
         for (int b = 0; b < nb; b += 4) {
@@ -665,9 +702,9 @@ __global__ __launch_bounds__(256) void gcombine_kernel(GroupArgs a) {
 }  // namespace
 
 hipError_t launch_grouped(const GroupArgs& args, int cus, hipStream_t s) {
-    // down: 8 waves per workgroup; gate/up: 12 (3 per SIMD, 192 rows per item)
-    // where ff allows, else 8
-    constexpr int NW = 8;
+    // gate/up: 12 waves per workgroup (3 per SIMD, 192 rows per item) where ff
+    // allows, else 8; down: 12 (its last group of a task ragged)
+    constexpr int NW = 8, NWD = 12;
     if (args.T < 1 || args.k < 1 || args.k > 16 || args.n_experts > kGroupMaxExperts || args.dim % (NW * 16) ||
         args.ff % (NW * 16) || args.dim % 256 || args.ff % 256 || args.dim > kGuNb * 256 || args.ff > kDnNb * 256)
         return hipErrorNotSupported;
@@ -684,7 +721,7 @@ hipError_t launch_grouped(const GroupArgs& args, int cus, hipStream_t s) {
             hipLaunchKernelGGL((gu_kernel<NW, true>), dim3(cus), dim3(NW * 64), 0, s, args);
         hipLaunchKernelGGL((q8k_rows_kernel<ROWS_H, true>), dim3((P * nbh + 3) / 4), dim3(256), 0, s, args.h, P, nbh,
                            args.hq, args.hd, args.pos, args.k, args.err, args.tq8h);
-        hipLaunchKernelGGL((dn_kernel<NW, true>), dim3(cus), dim3(NW * 64), 0, s, args);
+        hipLaunchKernelGGL((dn_kernel<NWD, true>), dim3(cus), dim3(NWD * 64), 0, s, args);
     } else {
         hipLaunchKernelGGL((q8k_rows_kernel<ROWS_X, false>), dim3((args.T * nbx + 3) / 4), dim3(256), 0, s, args.x,
                            args.T, nbx, args.xq, args.xd, args.pos, args.k, args.err, nullptr);
@@ -694,7 +731,7 @@ hipError_t launch_grouped(const GroupArgs& args, int cus, hipStream_t s) {
             hipLaunchKernelGGL((gu_kernel<NW, false>), dim3(cus), dim3(NW * 64), 0, s, args);
         hipLaunchKernelGGL((q8k_rows_kernel<ROWS_H, false>), dim3((P * nbh + 3) / 4), dim3(256), 0, s, args.h, P, nbh,
                            args.hq, args.hd, args.pos, args.k, args.err, nullptr);
-        hipLaunchKernelGGL((dn_kernel<NW, false>), dim3(cus), dim3(NW * 64), 0, s, args);
+        hipLaunchKernelGGL((dn_kernel<NWD, false>), dim3(cus), dim3(NWD * 64), 0, s, args);
     }
     const bool al16 = (reinterpret_cast<uintptr_t>(args.out) | reinterpret_cast<uintptr_t>(args.shared)) % 16 == 0;
     if (al16) hipLaunchKernelGGL(gcombine_kernel<4>, dim3((args.dim / 4 + 255) / 256, args.T), dim3(256), 0, s, args);

@@ -193,8 +193,14 @@ __global__ __launch_bounds__(1024) void bucket_kernel(GroupArgs a) {
 // 2i + 1) of slot s sits at ((4 b + i) * 4 + e) * 256 + 16 s, so that four lanes
 // of consecutive slots read 64 contiguous bytes.
 // ---------------------------------------------------------------------------
+// The j-th pair of a task (slot 16 i + j) sits at tile position 4 (j % 4) + j / 4
+// (M index of the MFMAs; the map is its own inverse): the lane holding M rows
+// 4 e + r, r = 0..3, gets pairs 4 r + e, so a task of n pairs has results only
+// in the lanes' first ceil(n / 4) output registers.
+__device__ __forceinline__ int tile_pos(int j) { return ((j & 3) << 2) | (j >> 2); }
 __device__ __forceinline__ size_t slot_off(int slot, int nb, int blk, int piece, int chunk) {
-    return size_t(slot >> 4) * size_t(nb) * 4096 + size_t(((4 * blk + piece) * 4 + chunk) * 256 + 16 * (slot & 15));
+    return size_t(slot >> 4) * size_t(nb) * 4096 +
+           size_t(((4 * blk + piece) * 4 + chunk) * 256 + 16 * tile_pos(slot & 15));
 }
 enum { ROWS_X = 0, ROWS_H = 1 };
 // trace (null outside the parity trace): the row's blocks also as 292-byte Q8_K
@@ -322,8 +328,8 @@ __device__ __forceinline__ void stage_item(uint8_t* lds, const GroupArgs& a, con
                                            int rd, int mstride) {
     __syncthreads();   // every wave is done with the previous item's staging
     for (int i = t; i < 16 * nb; i += NT) {
-        const int pos = i & 15, blk = i >> 4;
-        const int p = a.order[tk.y + min(pos, tk.z - 1)];
+        const int pos = i & 15, blk = i >> 4;   // tile position pos holds the task's pair tile_pos(pos)
+        const int p = a.order[tk.y + min(tile_pos(pos), tk.z - 1)];
         reinterpret_cast<float*>(lds + kL_PD)[i] = scl[size_t(per_pair ? p : p / a.k) * nb + blk];
     }
     const int chunks = rows * nb * 2 / 16;   // 16-byte pieces of one plane's rows
@@ -360,11 +366,11 @@ __global__ __launch_bounds__(NW * 64, 1) void gu_kernel(GroupArgs a) {
         // A operand: slot col of the task (past its pairs: unused slot memory, whose
         // outputs are discarded), the lane's chunk e4, block 0
         const uint32_t va = uint32_t(slot_off(tk.y, nb, 0, 0, e4) + 16 * col);
-        int po[4];
+        int po[4];   // the pairs of the lane's four outputs (tile positions 4 e4 + r)
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-            const int pos = 4 * e4 + r;
-            po[r] = pos < tk.z ? a.order[tk.y + pos] : -1;
+            const int j = 4 * r + e4;
+            po[r] = j < tk.z ? a.order[tk.y + j] : -1;
         }
         const MatRef G = mat_at(a.descs, tk.x, 0), U = mat_at(a.descs, tk.x, 1);
         {
@@ -381,107 +387,113 @@ __global__ __launch_bounds__(NW * 64, 1) void gu_kernel(GroupArgs a) {
             for (int i = 0; i < 4; ++i) o.a[i] = ld128(rx, va + 4096u * blk + 1024u * i);
         };
         auto touch = [&](int blk) { return ld32(rg, vq + 64u * blk) ^ ld32(ru, vq + 64u * blk); };
-        float accg[4] = {0.0f, 0.0f, 0.0f, 0.0f}, accu[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-        // Sub-block c of a matrix: its grid entry (g, -g) and sign mask from LDS,
-        // then B = signed entry, one MFMA, the row's (2s + 1) on the four outputs.
-        // All eight gate lookups are issued first; each up lookup is issued as a
-        // gate one is consumed, so about seven are in flight throughout.
-        struct Look { uint4 g; uint2 m; };
-        auto look = [&](const XxsLane& X, int c) {   // grid byte -> address byte 1, then the aux byte
-            const uint32_t w = X.u[c >> 1], h = uint32_t(c & 1) * 2u;
-            Look L;
-            L.g = *reinterpret_cast<const uint4*>(lds + perm(w, lo_g, 0x0C020000u | ((4u + h) << 8)));
-            L.m = *reinterpret_cast<const uint2*>(lds + perm(w, lo_s, 0x0C020000u | ((5u + h) << 8)));
-            return L;
-        };
-        auto prod = [&](const Look& L, long A) {
-            return mfma(A, pack64(bfi(L.m.x, L.g.z, L.g.x), bfi(L.m.y, L.g.w, L.g.y)), v4i{0, 0, 0, 0});
-        };
-        auto scale = [&](const v4i& C, const XxsLane& X, int c, int (&bi)[4]) {
-            const int ls = int(__builtin_amdgcn_ubfe(X.ls[c & 1], 8 * (c >> 1), 8));
+        // RR: output registers that can hold a pair (2 for tasks of at most 8 pairs, else 4)
+        auto run = [&]<int RR>() {
+            float accg[4] = {0.0f, 0.0f, 0.0f, 0.0f}, accu[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+            // Sub-block c of a matrix: its grid entry (g, -g) and sign mask from LDS,
+            // then B = signed entry, one MFMA, the row's (2s + 1) on the RR outputs.
+            // All eight gate lookups are issued first; each up lookup is issued as a
+            // gate one is consumed, so about seven are in flight throughout.
+            struct Look { uint4 g; uint2 m; };
+            auto look = [&](const XxsLane& X, int c) {   // grid byte -> address byte 1, then the aux byte
+                const uint32_t w = X.u[c >> 1], h = uint32_t(c & 1) * 2u;
+                Look L;
+                L.g = *reinterpret_cast<const uint4*>(lds + perm(w, lo_g, 0x0C020000u | ((4u + h) << 8)));
+                L.m = *reinterpret_cast<const uint2*>(lds + perm(w, lo_s, 0x0C020000u | ((5u + h) << 8)));
+                return L;
+            };
+            auto prod = [&](const Look& L, long A) {
+                return mfma(A, pack64(bfi(L.m.x, L.g.z, L.g.x), bfi(L.m.y, L.g.w, L.g.y)), v4i{0, 0, 0, 0});
+            };
+            auto scale = [&](const v4i& C, const XxsLane& X, int c, int (&bi)[4]) {
+                const int ls = int(__builtin_amdgcn_ubfe(X.ls[c & 1], 8 * (c >> 1), 8));
 #pragma unroll
-            for (int r = 0; r < 4; ++r) bi[r] = mad24(ls, C[r], bi[r]);
-        };
-        const uint16_t* sdg = reinterpret_cast<const uint16_t*>(lds + kL_RDG) + (wv * 16 + col) * nb;
-        const uint16_t* sdu = sdg + NW * 16 * kGuNb;
-        int blk_c = 0;   // block the next compute() handles
-        auto compute = [&](const GuOps& o) {
-            const int b = blk_c++;
-            int big[4] = {0, 0, 0, 0}, biu[4] = {0, 0, 0, 0};
-            long A[8];
+                for (int r = 0; r < RR; ++r) bi[r] = mad24(ls, C[r], bi[r]);
+            };
+            const uint16_t* sdg = reinterpret_cast<const uint16_t*>(lds + kL_RDG) + (wv * 16 + col) * nb;
+            const uint16_t* sdu = sdg + NW * 16 * kGuNb;
+            int blk_c = 0;   // block the next compute() handles
+            auto compute = [&](const GuOps& o) {
+                const int b = blk_c++;
+                int big[4] = {0, 0, 0, 0}, biu[4] = {0, 0, 0, 0};
+                long A[8];
 #pragma unroll
-            for (int c = 0; c < 8; ++c) {
-                const uint32_t* av = reinterpret_cast<const uint32_t*>(o.a) + 2 * c;
-                A[c] = pack64(av[0], av[1]);
-            }
-            const XxsLane XG = xxs_lane(o.g, e4), XU = xxs_lane(o.u, e4);
-            Look L[8];
-#pragma unroll
-            for (int c = 0; c < 8; ++c) L[c] = look(XG, c);
-            // step i < 8: gate sub-block i, else up sub-block i - 8; each step's
-            // MFMA is issued before the previous step's multiply-adds read theirs
-            v4i C[16];
-#pragma unroll
-            for (int i = 0; i <= 16; ++i) {
-                if (i < 8) {
-                    C[i] = prod(L[i], A[i]);
-                    L[i] = look(XU, i);
-                } else if (i < 16) {
-                    C[i] = prod(L[i - 8], A[i - 8]);
+                for (int c = 0; c < 8; ++c) {
+                    const uint32_t* av = reinterpret_cast<const uint32_t*>(o.a) + 2 * c;
+                    A[c] = pack64(av[0], av[1]);
                 }
-                if (i > 8) scale(C[i - 1], XU, i - 9, biu);
-                else if (i > 0) scale(C[i - 1], XG, i - 1, big);
-            }
-            if constexpr (TR) {   // pair po[r]'s block integers of this lane's row
-                const size_t rec = 2 * size_t(a.ff) * nb + size_t(a.dim) * (a.ff / 256);
+                const XxsLane XG = xxs_lane(o.g, e4), XU = xxs_lane(o.u, e4);
+                Look L[8];
 #pragma unroll
-                for (int r = 0; r < 4; ++r)
-                    if (a.tint && po[r] >= 0) {
-                        const size_t o = size_t(po[r]) * rec + size_t(row) * nb + size_t(b);
-                        a.tint[o] = big[r];
-                        a.tint[o + size_t(a.ff) * nb] = biu[r];
+                for (int c = 0; c < 8; ++c) L[c] = look(XG, c);
+                // step i < 8: gate sub-block i, else up sub-block i - 8; each step's
+                // MFMA is issued before the previous step's multiply-adds read theirs
+                v4i C[16];
+#pragma unroll
+                for (int i = 0; i <= 16; ++i) {
+                    if (i < 8) {
+                        C[i] = prod(L[i], A[i]);
+                        L[i] = look(XU, i);
+                    } else if (i < 16) {
+                        C[i] = prod(L[i - 8], A[i - 8]);
                     }
-            }
-            const float dgf = h2f(sdg[b]), duf = h2f(sdu[b]);
-            const float4 xd4 = *reinterpret_cast<const float4*>(lds + kL_PD + 64 * b + 16 * e4);
-            const float xd[4] = {xd4.x, xd4.y, xd4.z, xd4.w};
+                    if (i > 8) scale(C[i - 1], XU, i - 9, biu);
+                    else if (i > 0) scale(C[i - 1], XG, i - 1, big);
+                }
+                if constexpr (TR) {   // pair po[r]'s block integers of this lane's row
+                    const size_t rec = 2 * size_t(a.ff) * nb + size_t(a.dim) * (a.ff / 256);
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                accg[r] = fmaf(__fmul_rn(dgf, xd[r]), float(big[r]), accg[r]);
-                accu[r] = fmaf(__fmul_rn(duf, xd[r]), float(biu[r]), accu[r]);
+                    for (int r = 0; r < RR; ++r)
+                        if (a.tint && po[r] >= 0) {
+                            const size_t o = size_t(po[r]) * rec + size_t(row) * nb + size_t(b);
+                            a.tint[o] = big[r];
+                            a.tint[o + size_t(a.ff) * nb] = biu[r];
+                        }
+                }
+                const float dgf = h2f(sdg[b]), duf = h2f(sdu[b]);
+                const float4 xd4 = *reinterpret_cast<const float4*>(lds + kL_PD + 64 * b + 16 * e4);
+                const float xd[4] = {xd4.x, xd4.y, xd4.z, xd4.w};
+#pragma unroll
+                for (int r = 0; r < RR; ++r) {
+                    accg[r] = fmaf(__fmul_rn(dgf, xd[r]), float(big[r]), accg[r]);
+                    accu[r] = fmaf(__fmul_rn(duf, xd[r]), float(biu[r]), accu[r]);
+                }
+            };
+            // Two operand sets alternate over a 4-step unrolled loop (no register
+            // copies, so no wait ever covers a load issued in the same step); line
+            // touches four blocks ahead in four fixed registers.
+            // A row's blocks 2j and 2j + 1 share a 128-byte line: one touch per line.
+            GuOps s0, s1;
+            load(s0, 0);
+            uint32_t t0 = touch(min(1, nb - 1)), t2 = touch(min(3, nb - 1));
+            for (int b = 0; b < nb; b += 4) {
+                load(s1, min(b + 1, nb - 1));
+                sink(sunk, t0);
+                t0 = touch(min(b + 5, nb - 1));
+                __builtin_amdgcn_sched_barrier(0);   // the loads stay ahead of the compute
+                compute(s0);
+                load(s0, min(b + 2, nb - 1));
+                __builtin_amdgcn_sched_barrier(0);
+                if (b + 1 < nb) compute(s1);
+                load(s1, min(b + 3, nb - 1));
+                sink(sunk, t2);
+                t2 = touch(min(b + 7, nb - 1));
+                __builtin_amdgcn_sched_barrier(0);
+                if (b + 2 < nb) compute(s0);
+                load(s0, min(b + 4, nb - 1));
+                __builtin_amdgcn_sched_barrier(0);
+                if (b + 3 < nb) compute(s1);
             }
+            sink(sunk, t0 ^ t2);
+#pragma unroll
+            for (int r = 0; r < RR; ++r)
+                if (po[r] >= 0)
+                    a.h[size_t(po[r]) * a.ff + row] =
+                        silu_mul3(__fmul_rn(0.125f, accg[r]), __fmul_rn(0.125f, accu[r]), a.lim);
         };
-        // Two operand sets alternate over a 4-step unrolled loop (no register
-        // copies, so no wait ever covers a load issued in the same step); line
-        // touches four blocks ahead in four fixed registers.
-        // A row's blocks 2j and 2j + 1 share a 128-byte line: one touch per line.
-        GuOps s0, s1;
         __syncthreads();   // the item's scales are staged
-        load(s0, 0);
-        uint32_t t0 = touch(min(1, nb - 1)), t2 = touch(min(3, nb - 1));
-        for (int b = 0; b < nb; b += 4) {
-            load(s1, min(b + 1, nb - 1));
-            sink(sunk, t0);
-            t0 = touch(min(b + 5, nb - 1));
-            __builtin_amdgcn_sched_barrier(0);   // the loads stay ahead of the compute
-            compute(s0);
-            load(s0, min(b + 2, nb - 1));
-            __builtin_amdgcn_sched_barrier(0);
-            if (b + 1 < nb) compute(s1);
-            load(s1, min(b + 3, nb - 1));
-            sink(sunk, t2);
-            t2 = touch(min(b + 7, nb - 1));
-            __builtin_amdgcn_sched_barrier(0);
-            if (b + 2 < nb) compute(s0);
-            load(s0, min(b + 4, nb - 1));
-            __builtin_amdgcn_sched_barrier(0);
-            if (b + 3 < nb) compute(s1);
-        }
-        sink(sunk, t0 ^ t2);
-#pragma unroll
-        for (int r = 0; r < 4; ++r)
-            if (po[r] >= 0)
-                a.h[size_t(po[r]) * a.ff + row] = silu_mul3(__fmul_rn(0.125f, accg[r]), __fmul_rn(0.125f, accu[r]), a.lim);
+        if (tk.z <= 8) run.template operator()<2>();
+        else run.template operator()<4>();
     }
     if (sunk == 0x9e3779b9u && lane == 64) a.h[0] = 0.0f;   // never true (lane < 64): keeps the touches
 }
@@ -529,11 +541,11 @@ __global__ __launch_bounds__(NW * 64, 1) void dn_kernel(GroupArgs a) {
         const int row0 = grp * R, rows = min(R, a.dim - row0);   // rows: a multiple of 16
         const int row = row0 + wv * 16 + col;
         const uint32_t va = uint32_t(slot_off(tk.y, nb, 0, 0, e4) + 16 * col);   // as in gu_kernel
-        int po[4];
+        int po[4];   // the pairs of the lane's four outputs (tile positions 4 e4 + r)
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-            const int pos = 4 * e4 + r;
-            po[r] = pos < tk.z ? a.order[tk.y + pos] : -1;
+            const int j = 4 * r + e4;
+            po[r] = j < tk.z ? a.order[tk.y + j] : -1;
         }
         const MatRef D = mat_at(a.descs, tk.x, 2);
         {
@@ -552,95 +564,101 @@ __global__ __launch_bounds__(NW * 64, 1) void dn_kernel(GroupArgs a) {
             for (int i = 0; i < 4; ++i) o.a[i] = ld128(rh, va + 4096u * blk + 1024u * i);
         };
         auto touch = [&](int blk) { return ld32(rd, vq + 64u * blk); };
-        float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-        const int rl = wv * 16 + col;   // the lane's row within the item
-        int blk_c = 0;                   // block the next compute() handles
-        auto compute = [&](const DnOps& o) {
-            const int b = blk_c++;
-            const uint2 sc = *reinterpret_cast<const uint2*>(lds + kL_RS + 8 * (rl * nb + b));
-            // Scale byte c holds nibbles lo (entries 0, 1) and hi (entries 2, 3):
-            // ls2 = 2 hi + 1 and ls1 - ls2 = 2 (lo - hi) as byte c & 3 of l2[c >> 2]
-            // and (signed) of dl[c >> 2]; 128 + 2 lo - 2 hi never borrows.
-            uint32_t l2[2], dl[2];
+        // RR: output registers that can hold a pair (ceil(pairs / 4), rounded up to 2, 3 or 4)
+        auto run = [&]<int RR>() {
+            float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+            const int rl = wv * 16 + col;   // the lane's row within the item
+            int blk_c = 0;                   // block the next compute() handles
+            auto compute = [&](const DnOps& o) {
+                const int b = blk_c++;
+                const uint2 sc = *reinterpret_cast<const uint2*>(lds + kL_RS + 8 * (rl * nb + b));
+                // Scale byte c holds nibbles lo (entries 0, 1) and hi (entries 2, 3):
+                // ls2 = 2 hi + 1 and ls1 - ls2 = 2 (lo - hi) as byte c & 3 of l2[c >> 2]
+                // and (signed) of dl[c >> 2]; 128 + 2 lo - 2 hi never borrows.
+                uint32_t l2[2], dl[2];
 #pragma unroll
-            for (int h = 0; h < 2; ++h) {
-                const uint32_t w = h ? sc.y : sc.x;
-                const uint32_t hi2 = (w >> 3) & 0x1E1E1E1Eu, lo2 = (w << 1) & 0x1E1E1E1Eu;
-                l2[h] = hi2 | 0x01010101u;
-                dl[h] = ((lo2 | 0x80808080u) - hi2) ^ 0x80808080u;
-            }
-            int bi[4] = {0, 0, 0, 0};
-            uint32_t u[4];
-            xs_lane(o.q, u);
-            uint4 g[8];
-            uint2 m[8];
-#pragma unroll
-            for (int c = 0; c < 8; ++c) {   // all eight lookups in flight before the first use
-                const uint32_t w = u[c >> 1], code = (c & 1) ? w >> 16 : w;
-                g[c] = *reinterpret_cast<const uint4*>(lds + ((code & 0xff80u) | lo_x));
-                m[c] = *reinterpret_cast<const uint2*>(lds + perm(w, lo_s, (c & 1) ? 0x0C020600u : 0x0C020400u));
-            }
-            // sub-block c's two MFMAs are issued before sub-block c - 1's scale
-            // multiply-adds read their results (no wait states between them)
-            v4i C[8], C1[8];
-#pragma unroll
-            for (int c = 0; c <= 8; ++c) {
-                if (c < 8) {
-                    const uint32_t* av = reinterpret_cast<const uint32_t*>(o.a) + 2 * c;
-                    const long A = pack64(av[0], av[1]);
-                    const uint32_t blo = bfi(m[c].x, g[c].z, g[c].x), bhi = bfi(m[c].y, g[c].w, g[c].y);
-                    C[c] = mfma(A, pack64(blo, bhi), v4i{0, 0, 0, 0});
-                    C1[c] = mfma(A, pack64(blo & mk, bhi & mk), v4i{0, 0, 0, 0});
+                for (int h = 0; h < 2; ++h) {
+                    const uint32_t w = h ? sc.y : sc.x;
+                    const uint32_t hi2 = (w >> 3) & 0x1E1E1E1Eu, lo2 = (w << 1) & 0x1E1E1E1Eu;
+                    l2[h] = hi2 | 0x01010101u;
+                    dl[h] = ((lo2 | 0x80808080u) - hi2) ^ 0x80808080u;
                 }
-                if (c > 0) {
-                    const int p = c - 1;
-                    const int ls2 = int(__builtin_amdgcn_ubfe(l2[p >> 2], 8 * (p & 3), 8));
-                    const int dls = __builtin_amdgcn_sbfe(int(dl[p >> 2]), 8 * (p & 3), 8);
+                int bi[4] = {0, 0, 0, 0};
+                uint32_t u[4];
+                xs_lane(o.q, u);
+                uint4 g[8];
+                uint2 m[8];
 #pragma unroll
-                    for (int r = 0; r < 4; ++r) bi[r] = mad24(ls2, C[p][r], mad24(dls, C1[p][r], bi[r]));
+                for (int c = 0; c < 8; ++c) {   // all eight lookups in flight before the first use
+                    const uint32_t w = u[c >> 1], code = (c & 1) ? w >> 16 : w;
+                    g[c] = *reinterpret_cast<const uint4*>(lds + ((code & 0xff80u) | lo_x));
+                    m[c] = *reinterpret_cast<const uint2*>(lds + perm(w, lo_s, (c & 1) ? 0x0C020600u : 0x0C020400u));
                 }
-            }
-            if constexpr (TR) {
-                const int nbx = a.dim / 256;
-                const size_t rec = 2 * size_t(a.ff) * nbx + size_t(a.dim) * nb;
+                // sub-block c's two MFMAs are issued before sub-block c - 1's scale
+                // multiply-adds read their results (no wait states between them)
+                v4i C[8], C1[8];
 #pragma unroll
-                for (int r = 0; r < 4; ++r)
-                    if (a.tint && po[r] >= 0)
-                        a.tint[size_t(po[r]) * rec + 2 * size_t(a.ff) * nbx + size_t(row) * nb + size_t(b)] = bi[r];
-            }
-            const float ddf = h2f(reinterpret_cast<const uint16_t*>(lds + kL_RDD)[rl * nb + b]);
-            const float4 hd4 = *reinterpret_cast<const float4*>(lds + kL_PD + 64 * b + 16 * e4);
-            const float hd[4] = {hd4.x, hd4.y, hd4.z, hd4.w};
+                for (int c = 0; c <= 8; ++c) {
+                    if (c < 8) {
+                        const uint32_t* av = reinterpret_cast<const uint32_t*>(o.a) + 2 * c;
+                        const long A = pack64(av[0], av[1]);
+                        const uint32_t blo = bfi(m[c].x, g[c].z, g[c].x), bhi = bfi(m[c].y, g[c].w, g[c].y);
+                        C[c] = mfma(A, pack64(blo, bhi), v4i{0, 0, 0, 0});
+                        C1[c] = mfma(A, pack64(blo & mk, bhi & mk), v4i{0, 0, 0, 0});
+                    }
+                    if (c > 0) {
+                        const int p = c - 1;
+                        const int ls2 = int(__builtin_amdgcn_ubfe(l2[p >> 2], 8 * (p & 3), 8));
+                        const int dls = __builtin_amdgcn_sbfe(int(dl[p >> 2]), 8 * (p & 3), 8);
 #pragma unroll
-            for (int r = 0; r < 4; ++r) acc[r] = fmaf(__fmul_rn(ddf, hd[r]), float(bi[r]), acc[r]);
+                        for (int r = 0; r < RR; ++r) bi[r] = mad24(ls2, C[p][r], mad24(dls, C1[p][r], bi[r]));
+                    }
+                }
+                if constexpr (TR) {
+                    const int nbx = a.dim / 256;
+                    const size_t rec = 2 * size_t(a.ff) * nbx + size_t(a.dim) * nb;
+#pragma unroll
+                    for (int r = 0; r < RR; ++r)
+                        if (a.tint && po[r] >= 0)
+                            a.tint[size_t(po[r]) * rec + 2 * size_t(a.ff) * nbx + size_t(row) * nb + size_t(b)] = bi[r];
+                }
+                const float ddf = h2f(reinterpret_cast<const uint16_t*>(lds + kL_RDD)[rl * nb + b]);
+                const float4 hd4 = *reinterpret_cast<const float4*>(lds + kL_PD + 64 * b + 16 * e4);
+                const float hd[4] = {hd4.x, hd4.y, hd4.z, hd4.w};
+#pragma unroll
+                for (int r = 0; r < RR; ++r) acc[r] = fmaf(__fmul_rn(ddf, hd[r]), float(bi[r]), acc[r]);
+            };
+            DnOps s0, s1;
+            load(s0, 0);
+            uint32_t t0 = touch(min(1, nb - 1)), t2 = touch(min(3, nb - 1));
+            for (int b = 0; b < nb; b += 4) {
+                load(s1, min(b + 1, nb - 1));
+                sink(sunk, t0);
+                t0 = touch(min(b + 5, nb - 1));
+                __builtin_amdgcn_sched_barrier(0);   // the loads stay ahead of the compute
+                compute(s0);
+                load(s0, min(b + 2, nb - 1));
+                __builtin_amdgcn_sched_barrier(0);
+                if (b + 1 < nb) compute(s1);
+                load(s1, min(b + 3, nb - 1));
+                sink(sunk, t2);
+                t2 = touch(min(b + 7, nb - 1));
+                __builtin_amdgcn_sched_barrier(0);
+                if (b + 2 < nb) compute(s0);
+                load(s0, min(b + 4, nb - 1));
+                __builtin_amdgcn_sched_barrier(0);
+                if (b + 3 < nb) compute(s1);
+            }
+            sink(sunk, t0 ^ t2);
+#pragma unroll
+            for (int r = 0; r < RR; ++r)
+                if (po[r] >= 0) a.y[size_t(po[r]) * a.dim + row] = __fmul_rn(0.125f, acc[r]);
         };
-        DnOps s0, s1;
         __syncthreads();   // the item's scales are staged
         if (wv * 16 >= rows) continue;   // wave-uniform: no rows of this wave in the last group
-        load(s0, 0);
-        uint32_t t0 = touch(min(1, nb - 1)), t2 = touch(min(3, nb - 1));
-        for (int b = 0; b < nb; b += 4) {
-            load(s1, min(b + 1, nb - 1));
-            sink(sunk, t0);
-            t0 = touch(min(b + 5, nb - 1));
-            __builtin_amdgcn_sched_barrier(0);   // the loads stay ahead of the compute
-            compute(s0);
-            load(s0, min(b + 2, nb - 1));
-            __builtin_amdgcn_sched_barrier(0);
-            if (b + 1 < nb) compute(s1);
-            load(s1, min(b + 3, nb - 1));
-            sink(sunk, t2);
-            t2 = touch(min(b + 7, nb - 1));
-            __builtin_amdgcn_sched_barrier(0);
-            if (b + 2 < nb) compute(s0);
-            load(s0, min(b + 4, nb - 1));
-            __builtin_amdgcn_sched_barrier(0);
-            if (b + 3 < nb) compute(s1);
-        }
-        sink(sunk, t0 ^ t2);
-#pragma unroll
-        for (int r = 0; r < 4; ++r)
-            if (po[r] >= 0) a.y[size_t(po[r]) * a.dim + row] = __fmul_rn(0.125f, acc[r]);
+        if (tk.z <= 8) run.template operator()<2>();
+        else if (tk.z <= 12) run.template operator()<3>();
+        else run.template operator()<4>();
     }
     if (sunk == 0x9e3779b9u && lane == 64) a.y[0] = 0.0f;   // never true (lane < 64): keeps the touches
 }

@@ -405,11 +405,10 @@ def main():
         if cfg == 4:
             lane.grouped_forward_async(0, d_ids[r], d_w[r], d_x[r], d_out[r], stream=sp)
             return
-        if cfg == 5:   # shared FFN -> routed layer (+ shared row) -> hc_post, one stream
+        if cfg == 5:   # shared FFN -> routed layer (+ shared row) with hc_post in its launch, one stream
             lane.shared_forward_async(SHARED_T, *d_mats, FF, d_x[r], d_sh, d_work, stream=sp)
-            lane.layer_forward_async(0, d_ids[r, 0], d_w[r, 0], d_x[r], d_out[r], shared=d_sh, stream=sp)
-            lane.hc_post_async(d_out[r].view(1, DIM), d_res[r:r + 1], d_post[r:r + 1], d_comb[r:r + 1], d_h2,
-                               stream=sp)
+            lane.layer_forward_post_async(0, d_ids[r, 0], d_w[r, 0], d_x[r], d_out[r], d_res[r:r + 1], d_post[r],
+                                          d_comb[r], d_h2, shared=d_sh, stream=sp)
             return
         if args.per32:
             lane.layer_forward_per32_async(0, d_ids[r, 0], d_x[r], d_y32, w=d_w[r, 0], out=d_out[r], stream=sp)
@@ -500,8 +499,8 @@ def main():
                   else "xl::dev::layer3_kernel (all-types single-launch layer)" if counts["alltypes"]
                   else "separate launches")
     if cfg == 5:
-        kernel = ("MoE block: shared FFN (quant32, mv32 gate+up, swiglu32, quant32, mv32 down) + stream_kernel "
-                  "+ hc_post_kernel: 7 launches per step")
+        kernel = ("MoE block: shared FFN (quant32, mv32 gate+up, swiglu_quant32, mv32 down) + stream_kernel "
+                  "with hc_post in its combine: 5 launches per step")
     if args.per32:
         kernel = "per32 chain (quant32, mv32 gate+up, swiglu32, quant32, mv32 down, combine: 6 launches per step)"
     traffic = measured_traffic() if cfg == 1 and not args.per32 else None

@@ -420,6 +420,30 @@ bool enqueue_layer_prenorm(xl_context* ctx, int32_t layer, const int32_t* d_ids,
     return true;
 }
 
+// A layer call followed by hc_post of its output, as one streaming launch
+// whose combine applies hc_post to its rows: true if launched (it records
+// `stop`), false if this layer has no such launch, or while stages are profiled.
+bool enqueue_layer_post(xl_context* ctx, int32_t layer, const int32_t* d_ids, const float* d_w, int32_t k,
+                        const float* d_x, const float* d_shared, float* d_out, const float* d_res, const float* d_post,
+                        const float* d_comb, int32_t H, float* d_post_out, hipStream_t s, hipEvent_t stop) {
+    if ((ctx->path != 1 && ctx->path != 4) || ctx->prof.on) return false;
+    xl::Layer3Args a = layer3_args(ctx, layer, d_ids, d_w, k, d_x, d_shared, d_out, s, nullptr);
+    a.po_res = d_res;
+    a.po_post = d_post;
+    a.po_comb = d_comb;
+    a.po_out = d_post_out;
+    a.po_H = H;
+    const hipError_t e = xl::dev::launch_stream(a, ctx->gu_mask[size_t(layer)], ctx->dn_mask[size_t(layer)], ctx->cus, s,
+                                                stop);
+    if (e == hipErrorNotSupported) {
+        (void)hipGetLastError();
+        return false;
+    }
+    hip_check(e, "streaming layer with hc_post");
+    ++ctx->launches[XL_LAUNCH_POST];
+    return true;
+}
+
 bool enqueue_layer(xl_context* ctx, int32_t layer, const int32_t* d_ids, const float* d_w, int32_t k, const float* d_x,
                    const float* d_shared, float* d_out, hipStream_t s, float* g_dbg = nullptr,
                    float* u_dbg = nullptr, hipEvent_t stop = nullptr, LayerTrace* tr = nullptr) {
@@ -1346,6 +1370,45 @@ int32_t xl_layer_forward_prenorm_async(xl_context* ctx, int32_t layer, const int
                   "hc_pre_norm launch");
         ord.carried_by_launch(enqueue_layer(ctx, layer, d_ids, d_w, k, d_x, d_shared_or_null, d_out, s, nullptr,
                                             nullptr, ord.stop()));
+    });
+}
+
+int32_t xl_layer_forward_post_async(xl_context* ctx, int32_t layer, const int32_t* d_ids, const float* d_w,
+                                    int32_t k, const float* d_x, const float* d_shared_or_null, float* d_out,
+                                    const float* d_res, const float* d_post, const float* d_comb, int32_t H,
+                                    float* d_post_out, void* stream, xl_error* err) {
+    return guarded(ctx, err, [&] {
+        ready(ctx, true);
+        check_layer(ctx, layer);
+        need(k >= 1 && k <= ctx->cfg.max_picks, XL_E_ARG, "pick count outside 1..max_picks");
+        need(d_ids && d_w && d_x && d_out && d_res && d_post && d_comb && d_post_out, XL_E_ARG, "null device pointer");
+        need(H >= 1 && H <= 4, XL_E_ARG, "hc geometry: H in 1..4");
+        const uint64_t D = uint64_t(ctx->cfg.dim), ob = uint64_t(H) * D * 4;
+        const auto apart = [](const void* p, uint64_t pb, const void* q, uint64_t qb) {
+            const uintptr_t a = reinterpret_cast<uintptr_t>(p), b = reinterpret_cast<uintptr_t>(q);
+            return a <= b ? b - a >= pb : a - b >= qb;
+        };
+        // post_out: res itself (in place) or apart from every input and from out; out
+        // apart from what hc_post reads (other workgroups read those columns later)
+        need(d_post_out == d_res || apart(d_post_out, ob, d_res, ob), XL_E_ARG, "hc output overlaps the residual streams");
+        need(apart(d_post_out, ob, d_out, D * 4) && apart(d_post_out, ob, d_x, D * 4) &&
+                 (!d_shared_or_null || apart(d_post_out, ob, d_shared_or_null, D * 4)) &&
+                 apart(d_post_out, ob, d_post, 32) && apart(d_post_out, ob, d_comb, 256) &&
+                 apart(d_post_out, ob, d_ids, uint64_t(k) * 4) && apart(d_post_out, ob, d_w, uint64_t(k) * 4),
+             XL_E_ARG, "hc output overlaps an input");
+        need(apart(d_out, D * 4, d_res, ob) && apart(d_out, D * 4, d_post, 32) && apart(d_out, D * 4, d_comb, 256),
+             XL_E_ARG, "layer output overlaps an hc_post input");
+        hipStream_t s = pick_stream(ctx, stream);
+        Ordered ord(ctx, s);
+        if (enqueue_layer_post(ctx, layer, d_ids, d_w, k, d_x, d_shared_or_null, d_out, d_res, d_post, d_comb, H,
+                               d_post_out, s, ord.stop())) {
+            ord.carried_by_launch(true);
+            return;
+        }
+        enqueue_layer(ctx, layer, d_ids, d_w, k, d_x, d_shared_or_null, d_out, s);
+        hip_check(xl::dev::launch_hc_post(d_out, d_res, d_post, d_comb, int(D), H, 1, d_post_out, s, ord.stop()),
+                  "hc_post launch");
+        ord.carried_by_launch(true);
     });
 }
 

@@ -96,6 +96,15 @@ struct Layer3Args {
     const float* pn_w;
     float* pn_x;
     float pn_eps;
+    // Hyper-connection post in the kernel (streaming kernel; null: none): each
+    // output row e of the layer also gives po_out[j][e] = po_post[j] * out[e] +
+    // sum_i po_comb[i * po_H + j] * po_res[i][e], as hc_post_kernel computes it
+    // for one token (po_res and po_out po_H x dim; po_out may be po_res).
+    const float* po_res;
+    const float* po_post;
+    const float* po_comb;
+    float* po_out;
+    int po_H;
 };
 constexpr int kHBufWords = 16 * 4096;      // k_max * ff_max
 constexpr int kStreamRouteMax = 512;       // experts a streaming kernel routes itself (8 per lane)

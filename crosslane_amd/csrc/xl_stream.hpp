@@ -1184,6 +1184,22 @@ __global__ __launch_bounds__(NW * 64, 1) void stream_kernel(Layer3Args a) {
         }
         if (a.shared) acc = __fadd_rn(acc, a.shared[orow]);
         a.out[orow] = acc;
+        if (a.po_out) {   // hc_post of this column, in hc_post_kernel's order (every load first)
+            const int H = a.po_H;
+            float r[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) r[i] = i < H ? a.po_res[size_t(i) * dim + orow] : 0.0f;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                if (j < H) {
+                    float v = __fmul_rn(a.po_post[j], acc);
+#pragma unroll
+                    for (int i = 0; i < 4; ++i)
+                        if (i < H) v = __fadd_rn(v, __fmul_rn(a.po_comb[i * H + j], r[i]));
+                    a.po_out[size_t(j) * dim + orow] = v;
+                }
+            }
+        }
     }
     mark(7);
     if (t == 0 && arrived == uint32_t(G) - 1u) {   // every workgroup has read the launch count

@@ -107,6 +107,7 @@ _SIGNATURES = {
     "xl_hc_pre_norm_async": (_I32, [_P, _P, _P, _P, _I32, _I32, _I32, C.c_float, _P, _P, _ErrP]),
     "xl_layer_forward_prenorm_async": (_I32, [_P, _I32, _P, _P, _I32, _P, _I32, _P, _P, C.c_float, _P, _P, _P, _P,
                                               _ErrP]),
+    "xl_layer_forward_post_async": (_I32, [_P, _I32, _P, _P, _I32, _P, _P, _P, _P, _P, _P, _I32, _P, _P, _ErrP]),
     "xl_profile_begin": (_I32, [_P, _I32, _ErrP]),
     "xl_profile_end": (_I32, [_P, _f32p, _I32, C.POINTER(_I32), C.POINTER(_I32), C.c_char_p, _I32, _ErrP]),
     "xl_profile_timeline": (_I32, [_P, _u64p, _I32, C.POINTER(_I32), _ErrP]),
@@ -369,6 +370,17 @@ class Lane:
                    _ptr(mix), _ptr(norm_w), float(eps), _ptr(x), _ptr(shared), _ptr(out),
                    None if stream is None else int(stream))
 
+    def layer_forward_post_async(self, layer: int, ids, w, x, out, res, post, comb, post_out, shared=None,
+                                 stream=None) -> None:
+        """The layer (out [dim], with shared added last) and hc_post of its output
+        for one token: res and post_out [H, dim] (or [1, H, dim]; post_out may be
+        res), post [8], comb [64]. One launch when the layer has a streaming
+        instance: each workgroup applies hc_post to the rows it combines."""
+        H = int(res.shape[-2]) if res.dim() >= 2 else 1
+        self._call("xl_layer_forward_post_async", layer, _ptr(ids), _ptr(w), int(ids.numel()), _ptr(x), _ptr(shared),
+                   _ptr(out), _ptr(res), _ptr(post), _ptr(comb), H, _ptr(post_out),
+                   None if stream is None else int(stream))
+
     def layer_trace_async(self, layer: int, ids, w, x, out, q8x=None, q8h=None, h=None, ints=None, shared=None,
                           stream=None, y=None) -> int:
         """The single-launch layer call with its own Q8_K(x) / Q8_K(h) blocks (uint8
@@ -442,7 +454,7 @@ class Lane:
         `launches` launches had run: for testing their wrap at 2^32."""
         self._call("xl_debug_set_launch_count", C.c_uint32(launches & 0xFFFFFFFF))
 
-    LAUNCH_KINDS = ("stream", "alltypes", "separate", "routed", "prenorm", "exact")   # XL_LAUNCH_* order
+    LAUNCH_KINDS = ("stream", "alltypes", "separate", "routed", "prenorm", "exact", "post")   # XL_LAUNCH_* order
 
     def launch_counts(self) -> dict:
         """Layer calls so far by how they ran ({kind: count}, XL_LAUNCH_* kinds):

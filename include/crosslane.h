@@ -357,6 +357,18 @@ int32_t xl_layer_forward_prenorm_async(xl_context* ctx, int32_t layer, const int
 int32_t xl_hc_post_async(xl_context* ctx, const float* d_y, const float* d_res, const float* d_post,
                          const float* d_comb, int32_t D, int32_t H, int32_t T, float* d_out, void* stream,
                          xl_error* err);
+/* The MoE layer of one token and the hyper-connection post after it as one
+ * call (the routed-expert layer of hip_backend.cpp:635-711, then :777
+ * k4::hc_post): xl_layer_forward_async(d_ids, d_w, k, d_x, d_shared) writes
+ * d_out, and xl_hc_post_async(y = d_out, res, post, comb, D = dim, H, T = 1)
+ * writes d_post_out; both bit-identical to those two calls. With a layer the
+ * streaming kernel runs, one launch: each workgroup applies hc_post to the
+ * output rows it combines. res and post_out H x dim, post 8, comb 64;
+ * post_out may be res (in place) and overlaps nothing else. */
+int32_t xl_layer_forward_post_async(xl_context* ctx, int32_t layer, const int32_t* d_ids, const float* d_w,
+                                    int32_t k, const float* d_x, const float* d_shared_or_null, float* d_out,
+                                    const float* d_res, const float* d_post, const float* d_comb, int32_t H,
+                                    float* d_post_out, void* stream, xl_error* err);
 
 /* ---- stage profiling --------------------------------------------------------
  * Between xl_profile_begin and xl_profile_end, the first max_calls layer calls
@@ -399,7 +411,8 @@ enum {
     XL_LAUNCH_ROUTED = 3,     /* routed layer calls that routed inside the streaming launch */
     XL_LAUNCH_PRENORM = 4,    /* pre-normed layer calls that normalized inside the streaming launch */
     XL_LAUNCH_EXACT = 5,      /* xl_layer_forward_exact_async calls */
-    XL_LAUNCH_KINDS = 6
+    XL_LAUNCH_POST = 6,       /* layer + hc_post calls that applied hc_post inside the streaming launch */
+    XL_LAUNCH_KINDS = 7
 };
 int32_t xl_debug_launch_counts(xl_context* ctx, int64_t* counts, int32_t n, xl_error* err);
 

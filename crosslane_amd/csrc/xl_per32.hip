@@ -54,6 +54,21 @@ __device__ __forceinline__ void ld32b_a2(const uint8_t* p, uint32_t* w) {
 #pragma unroll
     for (int j = 0; j < 8; ++j) w[j] = uint32_t(h[2 * j]) | (uint32_t(h[2 * j + 1]) << 16);
 }
+// 32 bytes at a 2-byte-aligned address as eight words, from the nine aligned
+// words that cover them (the last read only when p is not 4-byte aligned) and
+// a byte shift: for runs whose covering words stay inside their block (the
+// Q6_K rows' low and high bits end at least 16 bytes before the block's end).
+__device__ __forceinline__ void ld32b_a2w(const uint8_t* p, uint32_t* w) {
+    const uintptr_t a = reinterpret_cast<uintptr_t>(p);
+    const uint32_t* q = reinterpret_cast<const uint32_t*>(a & ~uintptr_t(3));
+    const uint32_t sh = uint32_t(a & 2u);   // bytes: 0 or 2
+    uint32_t d[9];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) d[j] = q[j];
+    d[8] = sh ? q[8] : 0u;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) w[j] = __builtin_amdgcn_alignbyte(d[j + 1], d[j], sh);
+}
 // 32 bytes at a 16-byte-aligned address (the Q4_K / Q5_K planes).
 __device__ __forceinline__ void ld32b_a16(const uint8_t* p, uint32_t* w) {
     const uint4 lo = reinterpret_cast<const uint4*>(p)[0], hi = reinterpret_cast<const uint4*>(p)[1];
@@ -80,8 +95,8 @@ __device__ __forceinline__ Sub32 sub32_dense(const MatRef& m, int row, int kb, c
         const uint8_t* b = m.base + (size_t(row) * m.nb + (kb >> 3)) * 210;
         const int h = ib >> 2, quarter = ib & 3;
         uint32_t hi[8];
-        ld32b_a2(b + 64 * h + ((quarter & 1) ? 32 : 0), v);
-        ld32b_a2(b + 128 + 32 * h, hi);
+        ld32b_a2w(b + 64 * h + ((quarter & 1) ? 32 : 0), v);   // ends by byte 128 of 210
+        ld32b_a2w(b + 128 + 32 * h, hi);                         // ends by byte 192
         const uint32_t sc = ld16(b + 192 + 8 * h + 2 * quarter);
         r.s0 = int(int8_t(sc & 255u));
         r.s1 = int(int8_t(sc >> 8));
@@ -99,7 +114,8 @@ __device__ __forceinline__ Sub32 sub32_dense(const MatRef& m, int row, int kb, c
     }
     // Q4_K / Q5_K
     const uint8_t* b = m.base + (size_t(row) * m.nb + (kb >> 3)) * (m.type == kQ5_K ? 176 : 144);
-    const uint32_t dd = ld32(b), s03 = ld32(b + 4), s47 = ld32(b + 8), s8b = ld32(b + 12);
+    const uint4 hd = *reinterpret_cast<const uint4*>(b);   // d, dmin, 12 scale bytes (blocks of 144 / 176 B: 16-byte aligned)
+    const uint32_t dd = hd.x, s03 = hd.y, s47 = hd.z, s8b = hd.w;
     const auto sbyte = [&](int i) -> uint32_t {
         const uint32_t w = i < 4 ? s03 : i < 8 ? s47 : s8b;
         return (w >> (8 * (i & 3))) & 255u;
@@ -250,7 +266,11 @@ __device__ __forceinline__ float row_acc(MatRef m, int row, int l, int nk, const
 // q_stride (k int8), d + pick * d_stride (k / 32 scales); output y + pick *
 // y_stride. ids == nullptr: the matrices single0 (z = 0) and single1 (z = 1)
 // for every pick. stage: the launch has IQ matrices (their codebooks go to LDS).
+// FAM: the block types the launch's matrices have (0 the IQ types, 1 the dense
+// ones, 2 any), so that each family's decoder gets the registers it needs
+// (the dense decoder's wider loads would cost the IQ rows occupancy).
 constexpr int kTabBytes = 24576;   // layer_tables: sign masks, IQ2_XXS, IQ2_XS, IQ1 grids
+template <int FAM>
 __global__ __launch_bounds__(256) void mv32_kernel(const ExpertDesc* __restrict__ descs, const int32_t* __restrict__ ids,
                                                    MatRef single0, MatRef single1, int picks, int n_experts, int role0,
                                                    int n, int k, const int8_t* __restrict__ q, size_t q_stride,
@@ -280,14 +300,29 @@ __global__ __launch_bounds__(256) void mv32_kernel(const ExpertDesc* __restrict_
         const float* dp = d + pick * d_stride;
         const int rr = row < n ? row : n - 1;   // rows past the end compute row n - 1 and store nothing
         float acc = 0.0f;
-        switch (m.type) {   // uniform per workgroup
-        case kIQ2_XXS: acc = row_acc<kIQ2_XXS>(m, rr, l, k / 32, qp, dp, stab); break;
-        case kIQ2_XS: acc = row_acc<kIQ2_XS>(m, rr, l, k / 32, qp, dp, stab); break;
-        case kIQ1_M: acc = row_acc<kIQ1_M>(m, rr, l, k / 32, qp, dp, stab); break;
-        case kQ8_0: acc = row_acc<kQ8_0>(m, rr, l, k / 32, qp, dp, stab); break;
-        case kQ4_K: acc = row_acc<kQ4_K>(m, rr, l, k / 32, qp, dp, stab); break;
-        case kQ5_K: acc = row_acc<kQ5_K>(m, rr, l, k / 32, qp, dp, stab); break;
-        default: acc = row_acc<kQ6_K>(m, rr, l, k / 32, qp, dp, stab); break;
+        if constexpr (FAM == 0) {
+            switch (m.type) {   // uniform per workgroup
+            case kIQ2_XXS: acc = row_acc<kIQ2_XXS>(m, rr, l, k / 32, qp, dp, stab); break;
+            case kIQ2_XS: acc = row_acc<kIQ2_XS>(m, rr, l, k / 32, qp, dp, stab); break;
+            default: acc = row_acc<kIQ1_M>(m, rr, l, k / 32, qp, dp, stab); break;
+            }
+        } else if constexpr (FAM == 1) {
+            switch (m.type) {
+            case kQ8_0: acc = row_acc<kQ8_0>(m, rr, l, k / 32, qp, dp, stab); break;
+            case kQ4_K: acc = row_acc<kQ4_K>(m, rr, l, k / 32, qp, dp, stab); break;
+            case kQ5_K: acc = row_acc<kQ5_K>(m, rr, l, k / 32, qp, dp, stab); break;
+            default: acc = row_acc<kQ6_K>(m, rr, l, k / 32, qp, dp, stab); break;
+            }
+        } else {
+            switch (m.type) {
+            case kIQ2_XXS: acc = row_acc<kIQ2_XXS>(m, rr, l, k / 32, qp, dp, stab); break;
+            case kIQ2_XS: acc = row_acc<kIQ2_XS>(m, rr, l, k / 32, qp, dp, stab); break;
+            case kIQ1_M: acc = row_acc<kIQ1_M>(m, rr, l, k / 32, qp, dp, stab); break;
+            case kQ8_0: acc = row_acc<kQ8_0>(m, rr, l, k / 32, qp, dp, stab); break;
+            case kQ4_K: acc = row_acc<kQ4_K>(m, rr, l, k / 32, qp, dp, stab); break;
+            case kQ5_K: acc = row_acc<kQ5_K>(m, rr, l, k / 32, qp, dp, stab); break;
+            default: acc = row_acc<kQ6_K>(m, rr, l, k / 32, qp, dp, stab); break;
+            }
         }
 #pragma unroll
         for (int o = 16; o > 0; o >>= 1) acc = __fadd_rn(acc, __shfl_xor(acc, o, 32));
@@ -330,8 +365,15 @@ hipError_t launch_mv32(const ExpertDesc* descs, const int32_t* ids, const MatRef
     const int stage = ids || !dense_type(single0.type) || (roles > 1 && !dense_type(single1.type));
     const int total = picks * ((n + 7) / 8);
     const int G = stage ? (total < 512 ? total : 512) : total;   // staging workgroups take several row groups
-    hipLaunchKernelGGL(mv32_kernel, dim3(G, 1, roles), dim3(256), 0, s, descs, ids, single0, single1, picks,
-                       n_experts, role0, n, k, q, q_stride, d, d_stride, y0, y1, y_stride, tables, stage, err);
+    // bank matrices (ids) are IQ types; single ones are whatever they are
+    const bool dense0 = !ids && dense_type(single0.type), dense1 = roles > 1 ? !ids && dense_type(single1.type) : dense0;
+    const auto go = [&](auto kernel) {
+        hipLaunchKernelGGL(kernel, dim3(G, 1, roles), dim3(256), 0, s, descs, ids, single0, single1, picks, n_experts,
+                           role0, n, k, q, q_stride, d, d_stride, y0, y1, y_stride, tables, stage, err);
+    };
+    if (dense0 != dense1) go(mv32_kernel<2>);
+    else if (dense0) go(mv32_kernel<1>);
+    else go(mv32_kernel<0>);
     return hipGetLastError();
 }
 

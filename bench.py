@@ -363,9 +363,9 @@ def main():
     else:
         step_bytes = np.array([sum(expert_bytes(types[l, e]) for l in range(L) for e in ids[r, l]) + L * 2 * DIM * 4
                                for r in range(n_r)], np.float64)
-    if cfg == 5:   # + shared matrices, the shared row out and in, hc_post's y, res, post, comb, out
+    if cfg == 5:   # + shared matrices, hc_post's res in and post streams out, post and comb
         step_bytes += (dense_bytes(SHARED_T[0], FF, DIM) + dense_bytes(SHARED_T[1], FF, DIM)
-                       + dense_bytes(SHARED_T[2], DIM, FF) + 2 * DIM * 4 + DIM * 4 + 2 * HC_H * DIM * 4 + 72 * 4)
+                       + dense_bytes(SHARED_T[2], DIM, FF) + 2 * HC_H * DIM * 4 + 72 * 4)
     bytes_per_step = float(step_bytes[used].mean())
 
     # A dedicated (non-default) stream: the library launches on it and the
@@ -389,8 +389,7 @@ def main():
         if blk:
             d_mats = [torch.from_numpy(m).cuda() for m in blk["mats"]]
             d_res, d_post, d_comb = (torch.from_numpy(blk[key]).cuda() for key in ("res", "post", "comb"))
-            d_sh = torch.zeros((1, DIM), dtype=torch.float32, device="cuda")
-            d_h2 = torch.zeros((HC_H, DIM), dtype=torch.float32, device="cuda").view(1, HC_H, DIM)
+            d_h2 = torch.zeros((HC_H, DIM), dtype=torch.float32, device="cuda")
             d_work = torch.empty(xl.shared_work_bytes(DIM, FF, 1), dtype=torch.uint8, device="cuda")
     torch.cuda.synchronize()
 
@@ -405,10 +404,9 @@ def main():
         if cfg == 4:
             lane.grouped_forward_async(0, d_ids[r], d_w[r], d_x[r], d_out[r], stream=sp)
             return
-        if cfg == 5:   # shared FFN -> routed layer (+ shared row) with hc_post in its launch, one stream
-            lane.shared_forward_async(SHARED_T, *d_mats, FF, d_x[r], d_sh, d_work, stream=sp)
-            lane.layer_forward_post_async(0, d_ids[r, 0], d_w[r, 0], d_x[r], d_out[r], d_res[r:r + 1], d_post[r],
-                                          d_comb[r], d_h2, shared=d_sh, stream=sp)
+        if cfg == 5:   # the MoE block: routed layer, shared FFN added last, hc_post of the sum (one call)
+            lane.moe_block_async(0, d_ids[r, 0], d_w[r, 0], d_x[r], SHARED_T, *d_mats, FF, d_work, d_res[r],
+                                 d_post[r], d_comb[r], d_out[r], d_h2, stream=sp)
             return
         if args.per32:
             lane.layer_forward_per32_async(0, d_ids[r, 0], d_x[r], d_y32, w=d_w[r, 0], out=d_out[r], stream=sp)
@@ -500,8 +498,9 @@ def main():
                   else "xl::dev::layer3_kernel (all-types single-launch layer)" if counts["alltypes"]
                   else "separate launches")
     if cfg == 5:
-        kernel = ("MoE block: shared FFN (quant32, mv32 gate+up, swiglu_quant32, mv32 down) + stream_kernel "
-                  "with hc_post in its combine: 5 launches per step")
+        kernel = ("MoE block (xl_moe_block_async): stream_kernel (routed layer; x quantized per 32 in its "
+                  "prologue), mv32 shared gate+up, swiglu_quant32, mv32 shared down (+ the routed row, hc_post in "
+                  "its epilogue): 4 launches per step")
     if args.per32:
         kernel = "per32 chain (quant32, mv32 gate+up, swiglu32, quant32, mv32 down, combine: 6 launches per step)"
     traffic = measured_traffic() if cfg == 1 and not args.per32 else None

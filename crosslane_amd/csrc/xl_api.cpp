@@ -1636,6 +1636,86 @@ int32_t xl_shared_forward_noalloc(xl_context* ctx, int32_t type_gate, const void
     });
 }
 
+int32_t xl_moe_block_async(xl_context* ctx, int32_t layer, const int32_t* d_ids, const float* d_w, int32_t k,
+                           const float* d_x, int32_t type_gate, const void* d_gate, int32_t type_up, const void* d_up,
+                           int32_t type_down, const void* d_down, int32_t ff, void* d_work, uint64_t work_bytes,
+                           const float* d_res, const float* d_post, const float* d_comb, int32_t H, float* d_out,
+                           float* d_post_out, void* stream, xl_error* err) {
+    return guarded(ctx, err, [&] {
+        ready(ctx, true);
+        check_layer(ctx, layer);
+        need(k >= 1 && k <= ctx->cfg.max_picks, XL_E_ARG, "pick count outside 1..max_picks");
+        check_shared(ctx, type_gate, d_gate, type_up, d_up, type_down, d_down, ff, 1, d_x, d_out);
+        need(d_ids && d_w && d_res && d_post && d_comb && d_post_out && d_work, XL_E_ARG, "null device pointer");
+        need(H >= 1 && H <= 4, XL_E_ARG, "hc geometry: H in 1..4");
+        const int dim = ctx->cfg.dim;
+        const SharedWork w = shared_work(dim, ff, 1);
+        need(work_bytes >= w.bytes, XL_E_ARG, "workspace smaller than xl_shared_work_bytes(dim, ff, 1)");
+        need(reinterpret_cast<uintptr_t>(d_work) % 256 == 0, XL_E_ARG, "workspace not 256-byte aligned");
+        const uint64_t D = uint64_t(dim), ob = uint64_t(H) * D * 4;
+        const auto apart = [](const void* p, uint64_t pb, const void* q, uint64_t qb) {
+            const uintptr_t a = reinterpret_cast<uintptr_t>(p), b = reinterpret_cast<uintptr_t>(q);
+            return a <= b ? b - a >= pb : a - b >= qb;
+        };
+        // the workspace, out and post_out each apart from everything the block reads or
+        // writes (post_out may be res itself)
+        const std::pair<const void*, uint64_t> ins[] = {{d_x, D * 4}, {d_ids, uint64_t(k) * 4}, {d_w, uint64_t(k) * 4},
+                                                        {d_post, 32}, {d_comb, 256}, {d_res, ob}};
+        for (const auto& [p, b] : ins) {
+            need(apart(d_work, w.bytes, p, b), XL_E_ARG, "workspace overlaps an input");
+            need(apart(d_out, D * 4, p, b), XL_E_ARG, "block output overlaps an input");
+            need(p == d_res || apart(d_post_out, ob, p, b), XL_E_ARG, "hc output overlaps an input");
+        }
+        need(d_post_out == d_res || apart(d_post_out, ob, d_res, ob), XL_E_ARG, "hc output overlaps the residual streams");
+        need(apart(d_work, w.bytes, d_out, D * 4) && apart(d_work, w.bytes, d_post_out, ob) &&
+                 apart(d_out, D * 4, d_post_out, ob),
+             XL_E_ARG, "workspace, block output and hc output overlap");
+        uint8_t* base = static_cast<uint8_t*>(d_work);
+        float* g = reinterpret_cast<float*>(base + w.g);
+        float* u = reinterpret_cast<float*>(base + w.u);
+        int8_t* xq = reinterpret_cast<int8_t*>(base + w.xq);
+        int8_t* hq = reinterpret_cast<int8_t*>(base + w.hq);
+        float* xd = reinterpret_cast<float*>(base + w.xd);
+        float* hd = reinterpret_cast<float*>(base + w.hd);
+        hipStream_t s = pick_stream(ctx, stream);
+        Ordered ord(ctx, s);
+        // the routed layer (no shared row): out = its fixed-order combine; the
+        // streaming launch also writes x per 32
+        bool fused = false;
+        if ((ctx->path == 1 || ctx->path == 4) && !ctx->prof.on) {
+            xl::Layer3Args a = layer3_args(ctx, layer, d_ids, d_w, k, d_x, nullptr, d_out, s, nullptr);
+            a.p32_q = xq;
+            a.p32_d = xd;
+            const hipError_t e = xl::dev::launch_stream(a, ctx->gu_mask[size_t(layer)], ctx->dn_mask[size_t(layer)],
+                                                        ctx->cus, s, nullptr);
+            if (e == hipSuccess) {
+                fused = true;
+                ++ctx->launches[XL_LAUNCH_BLOCK];
+            } else if (e != hipErrorNotSupported) {
+                hip_check(e, "streaming layer with quant32(x)");
+            }
+            (void)hipGetLastError();
+        }
+        if (!fused) {
+            hip_check(xl::dev::launch_quant32(d_x, 1, dim, xq, xd, ctx->err_flag, s), "quant32(x) launch");
+            enqueue_layer(ctx, layer, d_ids, d_w, k, d_x, nullptr, d_out, s);
+        }
+        // the shared expert: gate/up rows, SwiGLU + quant32(h), then its down rows
+        // added to the routed output (out = routed + shared) and hc_post of the sum
+        const xl::MatRef mg = per32_matrix(type_gate, d_gate, ff, dim), mu = per32_matrix(type_up, d_up, ff, dim);
+        const xl::MatRef md = per32_matrix(type_down, d_down, dim, ff);
+        hip_check(xl::dev::launch_mv32(nullptr, nullptr, mg, mu, 1, 0, 0, 2, ff, dim, xq, size_t(dim), xd,
+                                       size_t(dim / 32), g, u, size_t(ff), ctx->tables, ctx->err_flag, s),
+                  "shared gate/up launch");
+        hip_check(xl::dev::launch_swiglu_quant32(g, u, 1, ff, ctx->cfg.swiglu_limit, hq, hd, s),
+                  "shared SwiGLU + quant32(h) launch");
+        const xl::dev::Mv32Post ep{d_out, d_res, d_post, d_comb, d_post_out, H};
+        hip_check(xl::dev::launch_mv32(nullptr, nullptr, md, md, 1, 0, 0, 1, dim, ff, hq, size_t(ff), hd,
+                                       size_t(ff / 32), d_out, nullptr, size_t(dim), ctx->tables, ctx->err_flag, s, &ep),
+                  "shared down + hc_post launch");
+    });
+}
+
 int32_t xl_hc_pre_norm_async(xl_context* ctx, const float* d_h, const float* d_mix, const float* d_w_or_null,
                              int32_t D, int32_t H, int32_t T, float eps, float* d_x, void* stream, xl_error* err) {
     return guarded(ctx, err, [&] {

@@ -105,6 +105,11 @@ struct Layer3Args {
     const float* po_comb;
     float* po_out;
     int po_H;
+    // x quantized per 32 as quant32_kernel does (streaming kernel; null: not
+    // written): dim int8 quants in x order and dim / 32 scales, for a per32
+    // shared-expert FFN that runs after the layer.
+    int8_t* p32_q;
+    float* p32_d;
 };
 constexpr int kHBufWords = 16 * 4096;      // k_max * ff_max
 constexpr int kStreamRouteMax = 512;       // experts a streaming kernel routes itself (8 per lane)
@@ -210,10 +215,23 @@ hipError_t launch_quant32(const float* x, int rows, int k, int8_t* q, float* d, 
 // y_r[pick * y_stride + row] from q + pick * q_stride (16-byte aligned) and
 // d + pick * d_stride. Matrices: planar IQ types or raw dense blocks (Q8_0,
 // Q4_K, Q5_K, Q6_K, base 16-byte aligned).
+// Epilogue of a one-pick, one-role row launch (the MoE block's shared down
+// rows): y[row] = add[row] + the row's value (the layer combine's order,
+// routed + shared), then, if res is set, the hyper-connection post of that
+// column as hc_post_kernel computes it for one token: out[j][row] = post[j] *
+// y[row] + sum_i comb[i * H + j] * res[i][row] (out H x n, may equal res).
+struct Mv32Post {
+    const float* add;
+    const float* res;
+    const float* post;
+    const float* comb;
+    float* out;
+    int H;
+};
 hipError_t launch_mv32(const ExpertDesc* descs, const int32_t* ids, const MatRef& single0, const MatRef& single1,
                        int picks, int n_experts, int role0, int roles, int n, int k, const int8_t* q, size_t q_stride,
                        const float* d, size_t d_stride, float* y0, float* y1, size_t y_stride,
-                       const uint64_t* tables, int* err, hipStream_t s);
+                       const uint64_t* tables, int* err, hipStream_t s, const Mv32Post* epi = nullptr);
 // Hyper-connection post (sycl/hc/core.hpp:81-86) of T tokens, H <= 4 streams
 // of D: out[t][k][e] = post[t][k] * y[t][e] + sum_j comb[t][j * H + k] *
 // res[t][j][e]; out may equal res (in place).

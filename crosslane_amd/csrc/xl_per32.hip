@@ -276,7 +276,8 @@ __global__ __launch_bounds__(256) void mv32_kernel(const ExpertDesc* __restrict_
                                                    int n, int k, const int8_t* __restrict__ q, size_t q_stride,
                                                    const float* __restrict__ d, size_t d_stride, float* __restrict__ y0,
                                                    float* __restrict__ y1, size_t y_stride,
-                                                   const uint64_t* __restrict__ tab, int stage, int* __restrict__ err) {
+                                                   const uint64_t* __restrict__ tab, int stage, int* __restrict__ err,
+                                                   Mv32Post ep) {
     __shared__ __attribute__((aligned(16))) uint64_t stab[kTabBytes / 8];
     if (stage) {
         for (int c = threadIdx.x; c < kTabBytes / 16; c += 256)
@@ -326,7 +327,27 @@ __global__ __launch_bounds__(256) void mv32_kernel(const ExpertDesc* __restrict_
         }
 #pragma unroll
         for (int o = 16; o > 0; o >>= 1) acc = __fadd_rn(acc, __shfl_xor(acc, o, 32));
-        if (row < n && l == 0) y[pick * y_stride + row] = __fadd_rn(acc, 0.0f);
+        if (row < n && l == 0) {
+            float v = __fadd_rn(acc, 0.0f);
+            if (ep.add) v = __fadd_rn(ep.add[row], v);   // one pick: the routed output, then + this row
+            y[pick * y_stride + row] = v;
+            if (ep.res) {   // hc_post of this column, in hc_post_kernel's order (every load first)
+                const int H = ep.H;
+                float r[4];
+#pragma unroll
+                for (int i = 0; i < 4; ++i) r[i] = i < H ? ep.res[size_t(i) * n + row] : 0.0f;
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    if (j < H) {
+                        float o = __fmul_rn(ep.post[j], v);
+#pragma unroll
+                        for (int i = 0; i < 4; ++i)
+                            if (i < H) o = __fadd_rn(o, __fmul_rn(ep.comb[i * H + j], r[i]));
+                        ep.out[size_t(j) * n + row] = o;
+                    }
+                }
+            }
+        }
     }
 }
 
@@ -359,8 +380,11 @@ hipError_t launch_quant32(const float* x, int rows, int k, int8_t* q, float* d, 
 hipError_t launch_mv32(const ExpertDesc* descs, const int32_t* ids, const MatRef& single0, const MatRef& single1,
                        int picks, int n_experts, int role0, int roles, int n, int k, const int8_t* q, size_t q_stride,
                        const float* d, size_t d_stride, float* y0, float* y1, size_t y_stride,
-                       const uint64_t* tables, int* err, hipStream_t s) {
+                       const uint64_t* tables, int* err, hipStream_t s, const Mv32Post* epi) {
     if (picks < 1 || roles < 1 || roles > 2 || n < 1 || k < 256 || k % 256) return hipErrorInvalidValue;
+    const Mv32Post ep = epi ? *epi : Mv32Post{};
+    if ((ep.add || ep.res) && (picks != 1 || roles != 1 || (ep.res && (ep.H < 1 || ep.H > 4 || !ep.out))))
+        return hipErrorInvalidValue;
     // Bank matrices (ids) may be any IQ type; a single pair of dense matrices needs no codebook.
     const int stage = ids || !dense_type(single0.type) || (roles > 1 && !dense_type(single1.type));
     const int total = picks * ((n + 7) / 8);
@@ -369,7 +393,7 @@ hipError_t launch_mv32(const ExpertDesc* descs, const int32_t* ids, const MatRef
     const bool dense0 = !ids && dense_type(single0.type), dense1 = roles > 1 ? !ids && dense_type(single1.type) : dense0;
     const auto go = [&](auto kernel) {
         hipLaunchKernelGGL(kernel, dim3(G, 1, roles), dim3(256), 0, s, descs, ids, single0, single1, picks, n_experts,
-                           role0, n, k, q, q_stride, d, d_stride, y0, y1, y_stride, tables, stage, err);
+                           role0, n, k, q, q_stride, d, d_stride, y0, y1, y_stride, tables, stage, err, ep);
     };
     if (dense0 != dense1) go(mv32_kernel<2>);
     else if (dense0) go(mv32_kernel<1>);

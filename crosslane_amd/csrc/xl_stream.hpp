@@ -753,6 +753,33 @@ __global__ __launch_bounds__(NW * 64, 1) void stream_kernel(Layer3Args a) {
                 if (lane == 0) reinterpret_cast<float*>(lds + LY::XQ + kXQScl)[b] = xd[u];
             }
         }
+        // x per 32 (a.p32_q): workgroup g quantizes the 32-value chunks g, g + G, ...,
+        // each by the wave holding its block (lanes 8 c .. 8 c + 7 of block c / 8), as
+        // quant32_kernel: d = max|x| / 127, q = round-half-even(x / d), zero chunk zero.
+        // (A non-finite x is flagged by the Q8_K(x) above.)
+        if (a.p32_q) {
+#pragma unroll
+            for (int u = 0; u < UX; ++u) {
+                const int b = wv + NW * u;
+                for (int c = int(blockIdx.x); c < 8 * nbx; c += G) {   // uniform
+                    if ((c >> 3) != b) continue;
+                    const float v[4] = {xv[u].x, xv[u].y, xv[u].z, xv[u].w};
+                    float am = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
+                    am = fmaxf(am, dppf<0xB1>(am));    // quad_perm [1,0,3,2]
+                    am = fmaxf(am, dppf<0x4E>(am));    // quad_perm [2,3,0,1]
+                    am = fmaxf(am, dppf<0x141>(am));   // row_half_mirror: the 8-lane chunk's two quads
+                    const float sc = __fdiv_rn(am, 127.0f);
+                    uint32_t qw = 0;
+#pragma unroll
+                    for (int i = 0; i < 4; ++i)
+                        qw |= uint32_t(uint8_t(int8_t(am > 0.0f ? __float2int_rn(__fdiv_rn(v[i], sc)) : 0))) << (8 * i);
+                    if ((lane >> 3) == (c & 7)) {
+                        reinterpret_cast<uint32_t*>(a.p32_q)[64 * b + lane] = qw;
+                        if ((lane & 7) == 0) a.p32_d[c] = sc;
+                    }
+                }
+            }
+        }
     }
     if constexpr (M == 3) {
 #pragma unroll

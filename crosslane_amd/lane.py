@@ -108,6 +108,8 @@ _SIGNATURES = {
     "xl_layer_forward_prenorm_async": (_I32, [_P, _I32, _P, _P, _I32, _P, _I32, _P, _P, C.c_float, _P, _P, _P, _P,
                                               _ErrP]),
     "xl_layer_forward_post_async": (_I32, [_P, _I32, _P, _P, _I32, _P, _P, _P, _P, _P, _P, _I32, _P, _P, _ErrP]),
+    "xl_moe_block_async": (_I32, [_P, _I32, _P, _P, _I32, _P, _I32, _P, _I32, _P, _I32, _P, _I32, _P, C.c_uint64,
+                                  _P, _P, _P, _I32, _P, _P, _P, _ErrP]),
     "xl_profile_begin": (_I32, [_P, _I32, _ErrP]),
     "xl_profile_end": (_I32, [_P, _f32p, _I32, C.POINTER(_I32), C.POINTER(_I32), C.c_char_p, _I32, _ErrP]),
     "xl_profile_timeline": (_I32, [_P, _u64p, _I32, C.POINTER(_I32), _ErrP]),
@@ -381,6 +383,19 @@ class Lane:
                    _ptr(out), _ptr(res), _ptr(post), _ptr(comb), H, _ptr(post_out),
                    None if stream is None else int(stream))
 
+    def moe_block_async(self, layer: int, ids, w, x, types, gate, up, down, ff: int, work, res, post, comb, out,
+                        post_out, stream=None) -> None:
+        """The MoE block of one token: the routed layer, the shared-expert FFN
+        (types, gate, up, down, ff as shared_forward_async) added last, and
+        hc_post of the sum: out [dim], res and post_out [H, dim] (post_out may be
+        res), post [8], comb [64]; work >= shared_work_bytes(dim, ff, 1). The same
+        bits as shared_forward_async then layer_forward_post_async with that row."""
+        H = int(res.shape[-2]) if res.dim() >= 2 else 1
+        self._call("xl_moe_block_async", layer, _ptr(ids), _ptr(w), int(ids.numel()), _ptr(x), int(types[0]),
+                   _ptr(gate), int(types[1]), _ptr(up), int(types[2]), _ptr(down), ff, _ptr(work),
+                   int(work.numel() * work.element_size()), _ptr(res), _ptr(post), _ptr(comb), H, _ptr(out),
+                   _ptr(post_out), None if stream is None else int(stream))
+
     def layer_trace_async(self, layer: int, ids, w, x, out, q8x=None, q8h=None, h=None, ints=None, shared=None,
                           stream=None, y=None) -> int:
         """The single-launch layer call with its own Q8_K(x) / Q8_K(h) blocks (uint8
@@ -454,7 +469,7 @@ class Lane:
         `launches` launches had run: for testing their wrap at 2^32."""
         self._call("xl_debug_set_launch_count", C.c_uint32(launches & 0xFFFFFFFF))
 
-    LAUNCH_KINDS = ("stream", "alltypes", "separate", "routed", "prenorm", "exact", "post")   # XL_LAUNCH_* order
+    LAUNCH_KINDS = ("stream", "alltypes", "separate", "routed", "prenorm", "exact", "post", "block")   # XL_LAUNCH_* order
 
     def launch_counts(self) -> dict:
         """Layer calls so far by how they ran ({kind: count}, XL_LAUNCH_* kinds):

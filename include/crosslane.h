@@ -369,6 +369,23 @@ int32_t xl_layer_forward_post_async(xl_context* ctx, int32_t layer, const int32_
                                     int32_t k, const float* d_x, const float* d_shared_or_null, float* d_out,
                                     const float* d_res, const float* d_post, const float* d_comb, int32_t H,
                                     float* d_post_out, void* stream, xl_error* err);
+/* The MoE block of one token as one call (hip_backend.cpp:635-711 with the
+ * shared expert of :664-666 added last, then :777 k4::hc_post): d_out and
+ * d_post_out bit-identical to xl_shared_forward_async(gate, up, down, ff,
+ * T = 1, d_x) into a row s, then xl_layer_forward_post_async(d_ids, d_w, k,
+ * d_x, s, d_out, res, post, comb, H, d_post_out). The routed layer runs first
+ * and writes d_out; with a layer the streaming kernel runs, that launch also
+ * quantizes x per 32 for the shared FFN (no quant32 launch); the shared down
+ * rows then add themselves to d_out and apply hc_post in their epilogue.
+ * Workspace: xl_shared_work_bytes(dim, ff, 1) bytes, 256-byte aligned,
+ * overlapping nothing else. res and post_out H x dim, post 8, comb 64;
+ * post_out may be res (in place) and overlaps nothing else; out overlaps no
+ * input. */
+int32_t xl_moe_block_async(xl_context* ctx, int32_t layer, const int32_t* d_ids, const float* d_w, int32_t k,
+                           const float* d_x, int32_t type_gate, const void* d_gate, int32_t type_up, const void* d_up,
+                           int32_t type_down, const void* d_down, int32_t ff, void* d_work, uint64_t work_bytes,
+                           const float* d_res, const float* d_post, const float* d_comb, int32_t H, float* d_out,
+                           float* d_post_out, void* stream, xl_error* err);
 
 /* ---- stage profiling --------------------------------------------------------
  * Between xl_profile_begin and xl_profile_end, the first max_calls layer calls
@@ -412,7 +429,8 @@ enum {
     XL_LAUNCH_PRENORM = 4,    /* pre-normed layer calls that normalized inside the streaming launch */
     XL_LAUNCH_EXACT = 5,      /* xl_layer_forward_exact_async calls */
     XL_LAUNCH_POST = 6,       /* layer + hc_post calls that applied hc_post inside the streaming launch */
-    XL_LAUNCH_KINDS = 7
+    XL_LAUNCH_BLOCK = 7,      /* xl_moe_block_async calls whose streaming launch quantized x for the shared FFN */
+    XL_LAUNCH_KINDS = 8
 };
 int32_t xl_debug_launch_counts(xl_context* ctx, int64_t* counts, int32_t n, xl_error* err);
 

@@ -270,7 +270,9 @@ __device__ __forceinline__ float row_acc(MatRef m, int row, int l, int nk, const
 // ones, 2 any), so that each family's decoder gets the registers it needs
 // (the dense decoder's wider loads would cost the IQ rows occupancy).
 constexpr int kTabBytes = 24576;   // layer_tables: sign masks, IQ2_XXS, IQ2_XS, IQ1 grids
-template <int FAM>
+// EPI: the launch has an epilogue (Mv32Post: the MoE block's shared down rows);
+// only those instances carry its code, so the others keep their registers.
+template <int FAM, bool EPI>
 __global__ __launch_bounds__(256) void mv32_kernel(const ExpertDesc* __restrict__ descs, const int32_t* __restrict__ ids,
                                                    MatRef single0, MatRef single1, int picks, int n_experts, int role0,
                                                    int n, int k, const int8_t* __restrict__ q, size_t q_stride,
@@ -329,9 +331,11 @@ __global__ __launch_bounds__(256) void mv32_kernel(const ExpertDesc* __restrict_
         for (int o = 16; o > 0; o >>= 1) acc = __fadd_rn(acc, __shfl_xor(acc, o, 32));
         if (row < n && l == 0) {
             float v = __fadd_rn(acc, 0.0f);
-            if (ep.add) v = __fadd_rn(ep.add[row], v);   // one pick: the routed output, then + this row
+            if constexpr (EPI) {
+                if (ep.add) v = __fadd_rn(ep.add[row], v);   // one pick: the routed output, then + this row
+            }
             y[pick * y_stride + row] = v;
-            if (ep.res) {   // hc_post of this column, in hc_post_kernel's order (every load first)
+            if (EPI && ep.res) {   // hc_post of this column, in hc_post_kernel's order (every load first)
                 const int H = ep.H;
                 float r[4];
 #pragma unroll
@@ -395,9 +399,10 @@ hipError_t launch_mv32(const ExpertDesc* descs, const int32_t* ids, const MatRef
         hipLaunchKernelGGL(kernel, dim3(G, 1, roles), dim3(256), 0, s, descs, ids, single0, single1, picks, n_experts,
                            role0, n, k, q, q_stride, d, d_stride, y0, y1, y_stride, tables, stage, err, ep);
     };
-    if (dense0 != dense1) go(mv32_kernel<2>);
-    else if (dense0) go(mv32_kernel<1>);
-    else go(mv32_kernel<0>);
+    const bool epi_on = ep.add || ep.res;
+    if (dense0 != dense1) epi_on ? go(mv32_kernel<2, true>) : go(mv32_kernel<2, false>);
+    else if (dense0) epi_on ? go(mv32_kernel<1, true>) : go(mv32_kernel<1, false>);
+    else epi_on ? go(mv32_kernel<0, true>) : go(mv32_kernel<0, false>);
     return hipGetLastError();
 }
 

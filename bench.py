@@ -502,7 +502,8 @@ def main():
                   "prologue), mv32 shared gate+up, swiglu_quant32, mv32 shared down (+ the routed row, hc_post in "
                   "its epilogue): 4 launches per step")
     if args.per32:
-        kernel = "per32 chain (quant32, mv32 gate+up, swiglu32, quant32, mv32 down, combine: 6 launches per step)"
+        kernel = ("per32 chain (quant32, mv32 gate+up, swiglu_quant32, mv32 down with the fixed-order combine in its "
+                  "epilogue: 4 launches per step)")
     traffic = measured_traffic() if cfg == 1 and not args.per32 else None
 
     cpu = None

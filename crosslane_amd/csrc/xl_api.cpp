@@ -582,14 +582,14 @@ void enqueue_per32(xl_context* ctx, int32_t layer, const int32_t* d_ids, const f
     hip_check(xl::dev::launch_swiglu_quant32(ctx->g, ctx->u, k, ff, ctx->cfg.swiglu_limit, ctx->hq, hd, s),
               "SwiGLU + quant32(h) launch");
     mark("swiglu_quant32");
+    // the fixed-order combine (runtime.cpp:183-188) in the down launch's epilogue
+    // when out is given: each workgroup holds every pick's value of its rows
+    const xl::dev::Mv32Comb cb{d_w, d_shared, d_out};
     hip_check(xl::dev::launch_mv32(descs, d_ids, none, none, k, E, 2, 1, dim, ff, ctx->hq, size_t(ff), hd, size_t(ff / 32),
-                                   d_y, nullptr, size_t(dim), ctx->tables, ctx->err_flag, s),
+                                   d_y, nullptr, size_t(dim), ctx->tables, ctx->err_flag, s, nullptr,
+                                   d_out ? &cb : nullptr),
               "per32 down launch");
-    mark("down32");
-    if (d_out) {
-        hip_check(xl::dev::launch_combine(d_ids, d_w, k, d_y, dim, d_shared, d_out, s), "combine launch");
-        mark("combine");
-    }
+    mark(d_out ? "down32_combine" : "down32");
 }
 
 }  // namespace

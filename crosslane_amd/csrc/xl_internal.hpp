@@ -228,10 +228,20 @@ struct Mv32Post {
     float* out;
     int H;
 };
+// The per32 layer's fixed-order combine in a bank row launch (ids, one role,
+// picks <= 16): out[row] = fma(w, y, .) over the picks by ascending expert id
+// (equal ids in pick order) from +0, then + shared[row] when shared is set;
+// y is written as well.
+struct Mv32Comb {
+    const float* w;
+    const float* shared;
+    float* out;
+};
 hipError_t launch_mv32(const ExpertDesc* descs, const int32_t* ids, const MatRef& single0, const MatRef& single1,
                        int picks, int n_experts, int role0, int roles, int n, int k, const int8_t* q, size_t q_stride,
                        const float* d, size_t d_stride, float* y0, float* y1, size_t y_stride,
-                       const uint64_t* tables, int* err, hipStream_t s, const Mv32Post* epi = nullptr);
+                       const uint64_t* tables, int* err, hipStream_t s, const Mv32Post* epi = nullptr,
+                       const Mv32Comb* comb = nullptr);
 // Hyper-connection post (sycl/hc/core.hpp:81-86) of T tokens, H <= 4 streams
 // of D: out[t][k][e] = post[t][k] * y[t][e] + sum_j comb[t][j * H + k] *
 // res[t][j][e]; out may equal res (in place).

@@ -270,26 +270,40 @@ __device__ __forceinline__ float row_acc(MatRef m, int row, int l, int nk, const
 // ones, 2 any), so that each family's decoder gets the registers it needs
 // (the dense decoder's wider loads would cost the IQ rows occupancy).
 constexpr int kTabBytes = 24576;   // layer_tables: sign masks, IQ2_XXS, IQ2_XS, IQ1 grids
-// EPI: the launch has an epilogue (Mv32Post: the MoE block's shared down rows);
-// only those instances carry its code, so the others keep their registers.
-template <int FAM, bool EPI>
+// EPI: the launch's epilogue, 0 none, 1 Mv32Post (the MoE block's shared down
+// rows), 2 Mv32Comb (the per32 layer's combine: workgroup g takes row group g
+// of every pick, the picks in the combine's order); only those instances carry
+// its code, so the others keep their registers.
+template <int FAM, int EPI>
 __global__ __launch_bounds__(256) void mv32_kernel(const ExpertDesc* __restrict__ descs, const int32_t* __restrict__ ids,
                                                    MatRef single0, MatRef single1, int picks, int n_experts, int role0,
                                                    int n, int k, const int8_t* __restrict__ q, size_t q_stride,
                                                    const float* __restrict__ d, size_t d_stride, float* __restrict__ y0,
                                                    float* __restrict__ y1, size_t y_stride,
                                                    const uint64_t* __restrict__ tab, int stage, int* __restrict__ err,
-                                                   Mv32Post ep) {
+                                                   Mv32Post ep, Mv32Comb cb) {
     __shared__ __attribute__((aligned(16))) uint64_t stab[kTabBytes / 8];
+    __shared__ int s_order[16];
     if (stage) {
         for (int c = threadIdx.x; c < kTabBytes / 16; c += 256)
             reinterpret_cast<uint4*>(stab)[c] = reinterpret_cast<const uint4*>(tab)[c];
-        __syncthreads();
     }
+    if constexpr (EPI == 2) {
+        if (threadIdx.x == 0) {   // combine_one's order: ascending expert id, equal ids in pick order
+            for (int i = 0; i < picks; ++i) {
+                int j = i;
+                for (; j > 0 && ids[s_order[j - 1]] > ids[i]; --j) s_order[j] = s_order[j - 1];
+                s_order[j] = i;
+            }
+        }
+    }
+    if (stage || EPI == 2) __syncthreads();
     float* y = blockIdx.z ? y1 : y0;
     const int l = threadIdx.x & 31, rgp = (n + 7) / 8, total = picks * rgp;
+    float cacc = 0.0f;   // EPI 2, lane 0 of each row: fma(w, y, .) over the picks so far, from +0
     for (int w = blockIdx.x; w < total; w += gridDim.x) {
-        const int pick = w / rgp, row = (w - pick * rgp) * 8 + (threadIdx.x >> 5);
+        const int slot = w / rgp, row = (w - slot * rgp) * 8 + (threadIdx.x >> 5);
+        const int pick = EPI == 2 ? s_order[slot] : slot;
         MatRef m = blockIdx.z ? single1 : single0;
         if (ids) {
             const int id = ids[pick];
@@ -331,11 +345,12 @@ __global__ __launch_bounds__(256) void mv32_kernel(const ExpertDesc* __restrict_
         for (int o = 16; o > 0; o >>= 1) acc = __fadd_rn(acc, __shfl_xor(acc, o, 32));
         if (row < n && l == 0) {
             float v = __fadd_rn(acc, 0.0f);
-            if constexpr (EPI) {
+            if constexpr (EPI == 1) {
                 if (ep.add) v = __fadd_rn(ep.add[row], v);   // one pick: the routed output, then + this row
             }
             y[pick * y_stride + row] = v;
-            if (EPI && ep.res) {   // hc_post of this column, in hc_post_kernel's order (every load first)
+            if constexpr (EPI == 2) cacc = fmaf(cb.w[pick], v, cacc);
+            if (EPI == 1 && ep.res) {   // hc_post of this column, in hc_post_kernel's order (every load first)
                 const int H = ep.H;
                 float r[4];
 #pragma unroll
@@ -352,6 +367,10 @@ __global__ __launch_bounds__(256) void mv32_kernel(const ExpertDesc* __restrict_
                 }
             }
         }
+    }
+    if constexpr (EPI == 2) {   // combine_one: then + shared
+        const int row = int(blockIdx.x) * 8 + int(threadIdx.x >> 5);
+        if (row < n && l == 0) cb.out[row] = cb.shared ? __fadd_rn(cacc, cb.shared[row]) : cacc;
     }
 }
 
@@ -384,25 +403,31 @@ hipError_t launch_quant32(const float* x, int rows, int k, int8_t* q, float* d, 
 hipError_t launch_mv32(const ExpertDesc* descs, const int32_t* ids, const MatRef& single0, const MatRef& single1,
                        int picks, int n_experts, int role0, int roles, int n, int k, const int8_t* q, size_t q_stride,
                        const float* d, size_t d_stride, float* y0, float* y1, size_t y_stride,
-                       const uint64_t* tables, int* err, hipStream_t s, const Mv32Post* epi) {
+                       const uint64_t* tables, int* err, hipStream_t s, const Mv32Post* epi,
+                       const Mv32Comb* comb) {
     if (picks < 1 || roles < 1 || roles > 2 || n < 1 || k < 256 || k % 256) return hipErrorInvalidValue;
     const Mv32Post ep = epi ? *epi : Mv32Post{};
     if ((ep.add || ep.res) && (picks != 1 || roles != 1 || (ep.res && (ep.H < 1 || ep.H > 4 || !ep.out))))
         return hipErrorInvalidValue;
+    const Mv32Comb cb = comb ? *comb : Mv32Comb{};
+    if (cb.out && (!ids || roles != 1 || picks > 16 || !cb.w || ep.add || ep.res)) return hipErrorInvalidValue;
     // Bank matrices (ids) may be any IQ type; a single pair of dense matrices needs no codebook.
     const int stage = ids || !dense_type(single0.type) || (roles > 1 && !dense_type(single1.type));
     const int total = picks * ((n + 7) / 8);
-    const int G = stage ? (total < 512 ? total : 512) : total;   // staging workgroups take several row groups
+    // staging workgroups take several row groups; the combine takes one row group
+    // per workgroup, every pick of it
+    const int G = cb.out ? (n + 7) / 8 : stage ? (total < 512 ? total : 512) : total;
     // bank matrices (ids) are IQ types; single ones are whatever they are
     const bool dense0 = !ids && dense_type(single0.type), dense1 = roles > 1 ? !ids && dense_type(single1.type) : dense0;
     const auto go = [&](auto kernel) {
         hipLaunchKernelGGL(kernel, dim3(G, 1, roles), dim3(256), 0, s, descs, ids, single0, single1, picks, n_experts,
-                           role0, n, k, q, q_stride, d, d_stride, y0, y1, y_stride, tables, stage, err, ep);
+                           role0, n, k, q, q_stride, d, d_stride, y0, y1, y_stride, tables, stage, err, ep, cb);
     };
     const bool epi_on = ep.add || ep.res;
-    if (dense0 != dense1) epi_on ? go(mv32_kernel<2, true>) : go(mv32_kernel<2, false>);
-    else if (dense0) epi_on ? go(mv32_kernel<1, true>) : go(mv32_kernel<1, false>);
-    else epi_on ? go(mv32_kernel<0, true>) : go(mv32_kernel<0, false>);
+    if (cb.out) go(mv32_kernel<0, 2>);   // bank matrices: the IQ family
+    else if (dense0 != dense1) epi_on ? go(mv32_kernel<2, 1>) : go(mv32_kernel<2, 0>);
+    else if (dense0) epi_on ? go(mv32_kernel<1, 1>) : go(mv32_kernel<1, 0>);
+    else epi_on ? go(mv32_kernel<0, 1>) : go(mv32_kernel<0, 0>);
     return hipGetLastError();
 }
 

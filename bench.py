@@ -81,6 +81,15 @@ def dense_bytes(t, n, k) -> int:
     return n * (k // DENSE_VALUES[t]) * DENSE_BYTES[t]
 
 
+def block_extra_bytes() -> int:
+    """Config 5: what the MoE block reads and writes beyond the routed layer's
+    bytes: the shared expert's gate and up (FF x DIM) and down (DIM x FF) in
+    SHARED_T, hc_post's residual streams in and post streams out (HC_H x DIM
+    floats each), post (8) and comb (64)."""
+    return (dense_bytes(SHARED_T[0], FF, DIM) + dense_bytes(SHARED_T[1], FF, DIM)
+            + dense_bytes(SHARED_T[2], DIM, FF) + 2 * HC_H * DIM * 4 + 72 * 4)
+
+
 def dense_matrix(t, n, k, rng):
     """Uniform random ggml blocks of a dense format with finite fp16 scales in [1e-3, 1e-2)."""
     nb = n * (k // DENSE_VALUES[t])
@@ -363,9 +372,8 @@ def main():
     else:
         step_bytes = np.array([sum(expert_bytes(types[l, e]) for l in range(L) for e in ids[r, l]) + L * 2 * DIM * 4
                                for r in range(n_r)], np.float64)
-    if cfg == 5:   # + shared matrices, hc_post's res in and post streams out, post and comb
-        step_bytes += (dense_bytes(SHARED_T[0], FF, DIM) + dense_bytes(SHARED_T[1], FF, DIM)
-                       + dense_bytes(SHARED_T[2], DIM, FF) + 2 * HC_H * DIM * 4 + 72 * 4)
+    if cfg == 5:
+        step_bytes += block_extra_bytes()
     bytes_per_step = float(step_bytes[used].mean())
 
     # A dedicated (non-default) stream: the library launches on it and the

@@ -2,7 +2,8 @@
 generators' invariants, and the algorithmic bytes the JSON line's `value`
 divides by (config 1: 6 experts of IQ2_XXS gate/up 3,072 x 4,096 at 66 B and
 IQ2_XS down 4,096 x 3,072 at 74 B per 256 weights, plus x in and y out; the
-same formula at the real expert shape for config 6)."""
+same formula at the real expert shape for config 6; config 5 adds the shared
+expert's Q5_K gate/up and Q6_K down and hc_post's streams)."""
 from __future__ import annotations
 
 import os
@@ -55,3 +56,13 @@ def test_algorithmic_bytes():
         assert bench.expert_bytes((16, 16, 17)) * bench.K + 2 * bench.DIM * 4 == 56_995_840
     finally:
         bench.DIM, bench.FF = saved
+
+
+def test_block_extra_bytes():
+    # Q5_K: 176 B per 256 values, Q6_K: 210 B; gate and up 3,072 x 4,096, down 4,096 x 3,072
+    assert bench.SHARED_T == (13, 13, 14)
+    assert bench.dense_bytes(13, 3072, 4096) == 3072 * 16 * 176 == 8_650_752
+    assert bench.dense_bytes(14, 4096, 3072) == 4096 * 12 * 210 == 10_321_920
+    extra = 2 * 8_650_752 + 10_321_920 + 2 * 4 * 4096 * 4 + 72 * 4
+    assert bench.block_extra_bytes() == extra == 27_754_784
+    assert bench.LAYER_BYTES + extra == 88_539_424   # + the routed layer's: config 5's algorithmic bytes per step

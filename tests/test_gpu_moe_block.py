@@ -7,7 +7,8 @@ xl_layer_forward_post_async with that row: the shared FFN's x quantization
 moves into the streaming launch and the final sum and hc_post into the shared
 down rows' epilogue, but every value is the same operation on the same
 operands. With a layer the streaming kernel does not run (4096 x 3072 at eight
-picks) the block takes its separate-launch route, with the same bits.
+picks) the block takes its separate-launch route, with the same bits. The
+block captured in a HIP graph replays on new inputs with the eager call's bits.
 """
 from __future__ import annotations
 
@@ -101,5 +102,66 @@ def test_moe_block_rejects_bad_arguments():
             lane.moe_block_async(0, d_ids, d_w, x, st, g, u, dn, sff, work, res, post, comb, buf[:dim],
                                  buf[dim // 2:dim // 2 + H * dim].view(H, dim))
         assert lane.launch_counts()["block"] == 0
+    finally:
+        lane.close()
+
+
+def test_moe_block_captured_in_a_graph_replays():
+    """The block's four launches captured in a HIP graph: each replay on new
+    inputs (copied into the captured buffers) equals the eager call on the same
+    inputs bit for bit, with eager calls and synchronizations between replays."""
+    dim, ff, sff, st, k, H = 4096, 3072, 3072, (13, 13, 14), 6, 4
+    step("MoE block: graph capture and replays")
+    rng = np.random.default_rng(77)
+    lane = xl.Lane(dim, ff, 1, E, kind_types("iq2", E), max_picks=8)
+    try:
+        lane.generate(seed=71)
+        g = dev(dense_matrix(st[0], sff, dim, 72))
+        u = dev(dense_matrix(st[1], sff, dim, 73))
+        dn = dev(dense_matrix(st[2], dim, sff, 74))
+        work = torch.empty(xl.shared_work_bytes(dim, sff, 1), dtype=torch.uint8, device="cuda")
+        s = torch.cuda.Stream()
+        with torch.cuda.stream(s):
+            c_ids = torch.zeros(k, dtype=torch.int32, device="cuda")
+            c_w = torch.zeros(k, dtype=torch.float32, device="cuda")
+            c_x = torch.zeros(dim, dtype=torch.float32, device="cuda")
+            c_res = torch.zeros((H, dim), dtype=torch.float32, device="cuda")
+            c_post = torch.zeros(8, dtype=torch.float32, device="cuda")
+            c_comb = torch.zeros(64, dtype=torch.float32, device="cuda")
+            g_out, e_out = torch.zeros(dim, device="cuda"), torch.zeros(dim, device="cuda")
+            g_p, e_p = torch.zeros((H, dim), device="cuda"), torch.zeros((H, dim), device="cuda")
+
+        def load_inputs():
+            ids, w = route(rng.standard_normal(E).astype(np.float32), k)
+            with torch.cuda.stream(s):
+                c_ids.copy_(dev(ids)); c_w.copy_(dev(w))
+                c_x.copy_(dev((rng.standard_normal(dim) * 2.0).astype(np.float32)))
+                c_res.copy_(dev(rng.standard_normal((H, dim)).astype(np.float32)))
+                c_post.copy_(dev((rng.random(8) * 2).astype(np.float32)))
+                c_comb.copy_(dev(rng.random(64).astype(np.float32)))
+
+        def block(out, p):
+            lane.moe_block_async(0, c_ids, c_w, c_x, st, g, u, dn, sff, work, c_res, c_post, c_comb, out, p,
+                                 stream=s.cuda_stream)
+
+        load_inputs()
+        with torch.cuda.stream(s):
+            for _ in range(3):   # eager calls on the capture stream first
+                block(e_out, e_p)
+        s.synchronize()
+        lane.sync(s.cuda_stream)
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=s):
+            block(g_out, g_p)
+        for rep in range(5):
+            load_inputs()
+            with torch.cuda.stream(s):
+                graph.replay()
+                block(e_out, e_p)   # the same inputs eagerly, after the replay
+            s.synchronize()
+            lane.sync(s.cuda_stream)
+            assert np.array_equal(bits(g_out), bits(e_out)), rep
+            assert np.array_equal(bits(g_p), bits(e_p)), rep
+            assert np.all(np.isfinite(g_out.cpu().numpy()))
     finally:
         lane.close()

@@ -312,6 +312,12 @@ void drain(xl_context* ctx, hipStream_t s) {
     }
 }
 
+// Whether byte ranges [p, p + pb) and [q, q + qb) are disjoint.
+bool apart(const void* p, uint64_t pb, const void* q, uint64_t qb) {
+    const uintptr_t a = reinterpret_cast<uintptr_t>(p), b = reinterpret_cast<uintptr_t>(q);
+    return a <= b ? b - a >= pb : a - b >= qb;
+}
+
 void check_ids(const xl_context* ctx, const int32_t* ids, int32_t k) {
     need(ids != nullptr, XL_E_ARG, "null ids");
     need(k >= 1 && k <= ctx->cfg.max_picks, XL_E_ARG, "pick count outside 1..max_picks");
@@ -1349,10 +1355,6 @@ int32_t xl_layer_forward_prenorm_async(xl_context* ctx, int32_t layer, const int
         need(H >= 1 && H <= 4, XL_E_ARG, "hc geometry: H in 1..4");
         need(std::isfinite(eps) && eps > 0.0f, XL_E_ARG, "hc epsilon must be finite and positive");
         const uint64_t D = uint64_t(ctx->cfg.dim);
-        const auto apart = [](const void* p, uint64_t pb, const void* q, uint64_t qb) {
-            const uintptr_t a = reinterpret_cast<uintptr_t>(p), b = reinterpret_cast<uintptr_t>(q);
-            return a <= b ? b - a >= pb : a - b >= qb;
-        };
         // x is written while h, mix and the norm weights are read; out is written
         // while h is read by workgroups that start later
         need(apart(d_x, D * 4, d_h, uint64_t(H) * D * 4) && apart(d_x, D * 4, d_mix, 32) &&
@@ -1384,10 +1386,6 @@ int32_t xl_layer_forward_post_async(xl_context* ctx, int32_t layer, const int32_
         need(d_ids && d_w && d_x && d_out && d_res && d_post && d_comb && d_post_out, XL_E_ARG, "null device pointer");
         need(H >= 1 && H <= 4, XL_E_ARG, "hc geometry: H in 1..4");
         const uint64_t D = uint64_t(ctx->cfg.dim), ob = uint64_t(H) * D * 4;
-        const auto apart = [](const void* p, uint64_t pb, const void* q, uint64_t qb) {
-            const uintptr_t a = reinterpret_cast<uintptr_t>(p), b = reinterpret_cast<uintptr_t>(q);
-            return a <= b ? b - a >= pb : a - b >= qb;
-        };
         // post_out: res itself (in place) or apart from every input and from out; out
         // apart from what hc_post reads (other workgroups read those columns later)
         need(d_post_out == d_res || apart(d_post_out, ob, d_res, ob), XL_E_ARG, "hc output overlaps the residual streams");
@@ -1653,10 +1651,6 @@ int32_t xl_moe_block_async(xl_context* ctx, int32_t layer, const int32_t* d_ids,
         need(work_bytes >= w.bytes, XL_E_ARG, "workspace smaller than xl_shared_work_bytes(dim, ff, 1)");
         need(reinterpret_cast<uintptr_t>(d_work) % 256 == 0, XL_E_ARG, "workspace not 256-byte aligned");
         const uint64_t D = uint64_t(dim), ob = uint64_t(H) * D * 4;
-        const auto apart = [](const void* p, uint64_t pb, const void* q, uint64_t qb) {
-            const uintptr_t a = reinterpret_cast<uintptr_t>(p), b = reinterpret_cast<uintptr_t>(q);
-            return a <= b ? b - a >= pb : a - b >= qb;
-        };
         // the workspace, out and post_out each apart from everything the block reads or
         // writes (post_out may be res itself)
         const std::pair<const void*, uint64_t> ins[] = {{d_x, D * 4}, {d_ids, uint64_t(k) * 4}, {d_w, uint64_t(k) * 4},

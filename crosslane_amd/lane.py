@@ -219,7 +219,17 @@ def pack_types(pack_dir: str, first_layer: int, n_layers: int, n_experts: int) -
 
 # ---- the lane ------------------------------------------------------------------
 class Lane:
-    """One context: a resident bank of n_layers x n_experts experts on one GPU."""
+    """One context: a resident bank of n_layers x n_experts experts on one GPU.
+
+    The *_async calls enqueue on `stream` (a raw HIP stream handle), by default
+    on the context's own non-blocking stream. Tensors passed to them must stay
+    alive until that stream has run the call (`sync(stream)`): PyTorch's caching
+    allocator hands a freed tensor's memory to the next allocation on its own
+    current stream at once, so a temporary such as `torch.tensor(...).cuda()`
+    passed inline and followed by another allocation before the sync can be
+    overwritten while the kernel reads it. Passing
+    `stream=torch.cuda.current_stream().cuda_stream` orders the call with
+    PyTorch's own work and allocations on that stream."""
 
     def __init__(self, dim: int, ff: int, n_layers: int, n_experts: int, types: np.ndarray,
                  max_picks: int = 8, max_tokens: int = 0, device: int = 0, swiglu_limit: float = 0.0):
@@ -401,7 +411,7 @@ class Lane:
         """The single-launch layer call with its own Q8_K(x) / Q8_K(h) blocks (uint8
         tensors of 292-byte blocks), h, block integers and per-pick rows (y, k x dim,
         as its combine read them) written out; returns the kernel that ran (1
-        streaming, 3 all-types, 5 unit)."""
+        streaming, 3 all-types)."""
         kern = _I32()
         self._call("xl_layer_trace_async", layer, _ptr(ids), _ptr(w), int(ids.numel()), _ptr(x), _ptr(shared),
                    _ptr(out), _ptr(q8x), _ptr(q8h), _ptr(h), _ptr(ints), _ptr(y), C.byref(kern),

@@ -150,9 +150,13 @@ int32_t xl_expert_trace(xl_context* ctx, int32_t layer, int32_t expert, const fl
                         void* q8h, float* y, xl_error* err);
 
 /* ---- device-resident calls (device pointers, ordered on `stream`; a null
- * stream means the context stream). Results are valid after the stream
- * drains; xl_sync drains and reports kernel error flags. ids are checked on
- * the device: a bad id sets the flag and that pick contributes nothing. */
+ * stream means the context stream, created non-blocking: it does not wait
+ * for work on the legacy default stream). Results are valid after the stream
+ * drains; xl_sync drains and reports kernel error flags. Every buffer passed
+ * must stay allocated and unwritten by other streams until then: a caching
+ * allocator (PyTorch's) that reuses a freed input's memory for work on its own
+ * stream races with the call. ids are checked on the device: a bad id sets the flag and
+ * that pick contributes nothing. */
 int32_t xl_layer_forward_async(xl_context* ctx, int32_t layer, const int32_t* d_ids, const float* d_w, int32_t k,
                                const float* d_x, const float* d_shared_or_null, float* d_out, void* stream,
                                xl_error* err);
